@@ -1,0 +1,132 @@
+/* libkrafla_hip.so: the MI355X (gfx950) device layer of the Krafla token loop.
+ *
+ * Plain C ABI: device pointers, sizes and the reference's own types
+ * (krafla_types.h). Three groups of entry points:
+ *
+ *   1. runtime   device guard, HBM allocation, copies, one stream, graphs
+ *   2. fused ops the decode/prefill step as fused HIP kernels on the library
+ *                stream, each computing exactly the float operations of the
+ *                reference's scalar path (kernels/scalar/k_scalar.c) in its
+ *                order, so results are bit-identical
+ *   3. op table  the reference's kernel and ops ABI under its own names
+ *                (krafla_optable.h), for the ISA=hip binding
+ *
+ * Ops return void, as the reference's kernels do (docs/kernels.md:50); a
+ * launch or device error is kept as a sticky status that krh_sync() and
+ * krh_status() report, with the message in krh_last_error().
+ */
+#ifndef KRAFLA_HIP_H
+#define KRAFLA_HIP_H
+#include "krafla_types.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* A quantized matrix resident in HBM, in the .mlb layout (row-major, one row
+ * per output; Q4 byte j of a block = elements j and j+16, docs/file-format.md
+ * :121-131). Scales [rows][cols/32] are f32, or f16 when d16 is set (the
+ * file's own width; widened exactly on the fly). */
+typedef struct {
+    const void *q;
+    const void *d;
+    int rows, cols;
+    int type;   /* ML_Q8_0 or ML_Q4_0 */
+    int d16;
+} krh_mat;
+
+typedef struct krh_graph krh_graph;
+
+/* ---- 1. runtime ---- */
+
+/* Selects device 0 and checks it is gfx950: ML_E_ISA otherwise (the hip
+ * counterpart of ml_isa_check, core/isa_check.h:8-9). Idempotent. */
+ml_status krh_init(void);
+const char *krh_device_arch(void);
+/* ML_OK, or the first error since the last krh_clear_error() */
+ml_status krh_status(void);
+const char *krh_last_error(void);
+void krh_clear_error(void);
+void *krh_alloc(size_t bytes);          /* HBM, 256-byte aligned; NULL on failure */
+void krh_free(void *p);
+void *krh_host_alloc(size_t bytes);     /* pinned host memory */
+void krh_host_free(void *p);
+ml_status krh_copy_h2d(void *dst, const void *src, size_t bytes);   /* synchronous */
+ml_status krh_copy_d2h(void *dst, const void *src, size_t bytes);   /* synchronous */
+void krh_copy_d2d_async(void *dst, const void *src, size_t bytes);  /* on the library stream */
+ml_status krh_sync(void);               /* waits for the library stream */
+/* Stream capture into a graph: every op issued between begin and end is
+ * recorded, not run; krh_graph_launch replays them. */
+ml_status krh_graph_begin(void);
+ml_status krh_graph_end(krh_graph **g);
+ml_status krh_graph_launch(const krh_graph *g);
+void krh_graph_free(krh_graph *g);
+/* Events on the library stream, for timing: milliseconds between two marks */
+typedef struct krh_timer krh_timer;
+krh_timer *krh_timer_new(void);
+void krh_timer_mark(krh_timer *t, int which);   /* which = 0 (start) or 1 (stop) */
+float krh_timer_ms(krh_timer *t);               /* synchronizes on the stop mark */
+void krh_timer_free(krh_timer *t);
+
+/* ---- 2. fused ops (device pointers; `pos` and `tok` point to device ints so a
+ *         captured step replays without new arguments) ---- */
+
+/* x[0..cols) = row *tok of emb, dequantized (core/quant_ref.c:4-19),
+ * times embed_scale when it is not 1 (model/transformer.c:226-230) */
+void krh_embed(float *x, const krh_mat *emb, const int *tok, float embed_scale);
+
+/* o = rmsnorm(x) * w (k_scalar.c:59-64), quantized to Q8_0 blocks into q, d
+ * (k_scalar.c:39-57); xb (nullable) receives the float o. ntok rows of n. */
+void krh_rmsnorm_q8(int8_t *q, float *d, float *xb, const float *x, const float *w, int n, float eps, int ntok);
+
+/* Q8_0 quantize of ntok rows of n floats (k_scalar.c:39-57) */
+void krh_quantize_q8(int8_t *q, float *d, const float *x, int n, int ntok);
+
+/* y = W x (k_scalar.c:4-37); accumulate != 0: y += W x, the residual add of
+ * model/transformer.c:240-243 */
+void krh_matvec(float *y, const krh_mat *W, const int8_t *xq, const float *xd, int accumulate);
+
+/* The attention projections of one layer at position *pos
+ * (model/transformer.c:270-281): q = wq x, k = wk x, v = wv x, plus the
+ * biases when non-NULL, then RoPE on q and k with the tables' row *pos;
+ * k and v go to row *pos of this layer's F32 cache (kc, vc: [max_seq][kv_dim]). */
+void krh_matvec_qkv(float *q, float *kc, float *vc, const krh_mat *wq, const krh_mat *wk, const krh_mat *wv,
+                    const float *bq, const float *bk, const float *bv, const int8_t *xq, const float *xd,
+                    const float *rope_cos, const float *rope_sin, int head_dim, const int *pos);
+
+/* h = silu(w1 x) * (w3 x) (k_scalar.c:96-98), quantized to Q8_0 into hq, hd
+ * (model/transformer.c:291-294); hb (nullable) receives the float h.
+ * Needs rows % 32 == 0. */
+void krh_matvec_swiglu_q8(int8_t *hq, float *hd, float *hb, const krh_mat *w1, const krh_mat *w3,
+                          const int8_t *xq, const float *xd);
+
+/* Causal GQA attention of one position *pos over this layer's F32 cache
+ * (ops/ops.c:169-225): ao [n_heads * head_dim]; aq, ad (nullable) receive its
+ * Q8_0 quantization. att: n_heads * max_seq floats of scratch. */
+void krh_attention(float *ao, int8_t *aq, float *ad, float *att, const float *q, const float *kc, const float *vc,
+                   int n_heads, int n_kv_heads, int head_dim, int max_seq, int window, float scale, const int *pos);
+
+/* Greedy pick (model/sampler.c:57-61, ties to the lowest id): *tok = argmax;
+ * then, when non-NULL, log[*pos + 1] = *tok and *pos += 1. */
+void krh_argmax(int *tok, const float *logits, int n, int *pos, int *log);
+
+/* tok = prompt[*pos] (the prompt resident on the device) */
+void krh_take_token(int *tok, const int *prompt, const int *pos);
+/* *pos += 1 */
+void krh_advance(int *pos);
+
+/* ---- self-checks for tests ---- */
+/* y[i] = op(a[i], b[i]) as the kernels compute it: expf(a), sqrtf(a), a / b,
+ * or rmsnorm's 1 / sqrtf(a / b + 1e-5) */
+enum { KRH_MATH_EXPF = 0, KRH_MATH_SQRT = 1, KRH_MATH_DIV = 2, KRH_MATH_RMS_INV = 3 };
+void krh_math_batch(int op, float *y, const float *a, const float *b, size_t n);
+/* y[i] = f16 -> f32 of h[i] */
+void krh_h2f_batch(float *y, const uint16_t *h, size_t n);
+/* s[r*nb+b]: int32 block dots of rows [0, rows) (the exact integer part of
+ * the matvec) */
+void krh_block_dots(int32_t *s, const krh_mat *W, const int8_t *xq);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,598 @@
+// Decode-step kernels for gfx950 (one token at a time, batch 1).
+//
+// Matvec (k_matvec): HBM-streaming, no MFMA. A workgroup owns R output rows
+// (of up to three matrices that share the input, or the w1/w3 row pairs of
+// SwiGLU). Its 256 threads walk the rows' 32-element blocks in memory order,
+// so each wave reads one contiguous span per step (2 x 16-byte loads per
+// lane for Q8, one for Q4), and form the exact int32 block dot with v_dot4
+// against the Q8_0 activation staged in LDS. The per-block term
+// ((float)s * wd) * xd is computed in parallel into LDS; one lane per row then
+// adds the terms in block order, which is the reference's float order
+// (kernels/scalar/k_scalar.c:13, :34). Fused epilogues: plain store,
+// residual add, QKV bias + RoPE + KV-cache write, SwiGLU + Q8_0 quantize.
+#include "kr_internal.h"
+#include "kr_numerics.h"
+
+namespace {
+
+struct KMat {
+    const uint8_t *q;
+    const void *d;
+    int rows, cols, type, d16;
+};
+
+KMat to_kmat(const krh_mat *m) {
+    KMat k = { (const uint8_t *)m->q, m->d, m->rows, m->cols, m->type, m->d16 };
+    return k;
+}
+
+enum { EPI_STORE = 0, EPI_ADD = 1, EPI_QKV = 2, EPI_SWIGLU = 3 };
+
+struct MvArgs {
+    KMat m[3];
+    int tile0[4];        // first workgroup of matrix i; tile0[nmat] = grid size
+    int nmat;
+    const int8_t *xq;
+    const float *xd;
+    int K;
+    float *y[3];
+    const float *bias[3];
+    const float *rope_cos, *rope_sin;
+    int head_dim, ld_cache;
+    const int *pos;
+    int8_t *oq;
+    float *od;
+};
+
+constexpr int MV_THREADS = 256;
+
+template <typename T> __device__ __forceinline__ T pick3(int i, T a, T b, T c) { return i == 0 ? a : (i == 1 ? b : c); }
+
+// Exact int32 dot of one weight block with the activation block in LDS.
+template <int QT>
+__device__ __forceinline__ int block_dot(const int4 w0, const int4 w1, const int8_t *xb) {
+    const int4 xa = *(const int4 *)xb, xc = *(const int4 *)(xb + 16);
+    int s = 0;
+    if (QT == ML_Q8_0) {
+        s = kr_dot4(w0.x, xa.x, s); s = kr_dot4(w0.y, xa.y, s);
+        s = kr_dot4(w0.z, xa.z, s); s = kr_dot4(w0.w, xa.w, s);
+        s = kr_dot4(w1.x, xc.x, s); s = kr_dot4(w1.y, xc.y, s);
+        s = kr_dot4(w1.z, xc.z, s); s = kr_dot4(w1.w, xc.w, s);
+    } else {
+        // byte j holds element j (low nibble) and j+16 (high); nibble n is
+        // weight n-8, so the dot is sum(n x) - 8 sum(x), all exact in int32
+        const unsigned M = 0x0F0F0F0Fu;
+        s = kr_dot4((int)((unsigned)w0.x & M), xa.x, s); s = kr_dot4((int)((unsigned)w0.y & M), xa.y, s);
+        s = kr_dot4((int)((unsigned)w0.z & M), xa.z, s); s = kr_dot4((int)((unsigned)w0.w & M), xa.w, s);
+        s = kr_dot4((int)(((unsigned)w0.x >> 4) & M), xc.x, s); s = kr_dot4((int)(((unsigned)w0.y >> 4) & M), xc.y, s);
+        s = kr_dot4((int)(((unsigned)w0.z >> 4) & M), xc.z, s); s = kr_dot4((int)(((unsigned)w0.w >> 4) & M), xc.w, s);
+        const int one = 0x01010101;
+        int sx = 0;
+        sx = kr_dot4(one, xa.x, sx); sx = kr_dot4(one, xa.y, sx); sx = kr_dot4(one, xa.z, sx); sx = kr_dot4(one, xa.w, sx);
+        sx = kr_dot4(one, xc.x, sx); sx = kr_dot4(one, xc.y, sx); sx = kr_dot4(one, xc.z, sx); sx = kr_dot4(one, xc.w, sx);
+        s -= 8 * sx;
+    }
+    return s;
+}
+
+// Phase 1: the per-block terms of local rows [0, nloc) into t2[lr * stride + b].
+// Local rows below `split` come from A (rows row0..), the rest from B.
+template <int QT, int D16>
+__device__ __forceinline__ void mv_terms(const KMat &A, const KMat &B, int split, int row0, int nloc, int nb,
+                                         int stride, const int8_t *xs, const float *xds, float *t2) {
+    const int tid = threadIdx.x;
+    const int sr = MV_THREADS / nb, sb = MV_THREADS % nb;
+    int lr = tid / nb, b = tid - (tid / nb) * nb;
+    constexpr int U = 4;
+    while (lr < nloc) {
+        int lrs[U], bs[U];
+        int4 w0[U], w1[U];
+        float wd[U];
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            lrs[u] = lr;
+            bs[u] = b;
+            if (lr < nloc) {
+                const bool second = lr >= split;
+                const uint8_t *q = second ? B.q : A.q;
+                const void *d = second ? B.d : A.d;
+                const size_t blk = (size_t)(row0 + (second ? lr - split : lr)) * nb + b;
+                if (QT == ML_Q8_0) {
+                    const int4 *p = (const int4 *)(q + blk * 32);
+                    w0[u] = p[0];
+                    w1[u] = p[1];
+                } else {
+                    w0[u] = *(const int4 *)(q + blk * 16);
+                    w1[u] = make_int4(0, 0, 0, 0);
+                }
+                wd[u] = D16 ? kr_h2f(((const uint16_t *)d)[blk]) : ((const float *)d)[blk];
+            }
+            b += sb;
+            lr += sr;
+            if (b >= nb) { b -= nb; lr++; }
+        }
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            if (lrs[u] < nloc) {
+                const int bb = bs[u];
+                const int s = block_dot<QT>(w0[u], w1[u], xs + bb * 32);
+                const float t = kr_fmul((float)s, wd[u]);
+                t2[lrs[u] * stride + bb] = kr_fmul(t, xds[bb]);
+            }
+        }
+    }
+}
+
+template <int EPI, int R>
+__global__ void __launch_bounds__(MV_THREADS) k_matvec(const MvArgs a) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    const int K = a.K, nb = K / KR_QK, tid = threadIdx.x;
+    int mi = 0;
+    if (EPI != EPI_SWIGLU)
+        while (mi + 1 < a.nmat && (int)blockIdx.x >= a.tile0[mi + 1]) mi++;
+    const KMat W = pick3(mi, a.m[0], a.m[1], a.m[2]);
+    const KMat W2 = a.m[1];
+    const int row0 = ((int)blockIdx.x - a.tile0[mi]) * R;
+    const int nr = min(R, W.rows - row0);
+    const int nloc = EPI == EPI_SWIGLU ? 2 * R : nr;
+    const int split = EPI == EPI_SWIGLU ? R : nloc;
+    const int stride = nb | 1;   // odd: the chain lanes read distinct banks
+    int8_t *xs = (int8_t *)smem;
+    float *xds = (float *)(smem + K);
+    float *t2 = xds + nb;
+    float *sums = t2 + (EPI == EPI_SWIGLU ? 2 * R : R) * stride;
+
+    for (int i = tid; i < K / 16; i += MV_THREADS) ((int4 *)xs)[i] = ((const int4 *)a.xq)[i];
+    for (int i = tid; i < nb; i += MV_THREADS) xds[i] = a.xd[i];
+    __syncthreads();
+
+    if (W.type == ML_Q8_0) {
+        if (W.d16) mv_terms<ML_Q8_0, 1>(W, W2, split, row0, nloc, nb, stride, xs, xds, t2);
+        else mv_terms<ML_Q8_0, 0>(W, W2, split, row0, nloc, nb, stride, xs, xds, t2);
+    } else {
+        if (W.d16) mv_terms<ML_Q4_0, 1>(W, W2, split, row0, nloc, nb, stride, xs, xds, t2);
+        else mv_terms<ML_Q4_0, 0>(W, W2, split, row0, nloc, nb, stride, xs, xds, t2);
+    }
+    __syncthreads();
+
+    // Phase 2: one lane per row adds its terms in block order (k_scalar.c:13)
+    if (tid < nloc) {
+        const float *p = t2 + tid * stride;
+        float s = 0.0f;
+#pragma unroll 8
+        for (int b = 0; b < nb; b++) s = kr_fadd(s, p[b]);
+        sums[tid] = s;
+    }
+    __syncthreads();
+
+    if (EPI == EPI_STORE) {
+        if (tid < nr) pick3(mi, a.y[0], a.y[1], a.y[2])[row0 + tid] = sums[tid];
+    } else if (EPI == EPI_ADD) {
+        if (tid < nr) {
+            float *y = pick3(mi, a.y[0], a.y[1], a.y[2]) + row0 + tid;
+            *y = kr_fadd(*y, sums[tid]);
+        }
+    } else if (EPI == EPI_QKV) {
+        // bias (model/transformer.c:276-277), then RoPE on q and k
+        // (k_scalar.c:79-94: pairs 2i, 2i+1 of each head, unfused)
+        const float *bias = pick3(mi, a.bias[0], a.bias[1], a.bias[2]);
+        float v = 0.0f;
+        if (tid < nr) {
+            v = sums[tid];
+            if (bias) v = kr_fadd(v, bias[row0 + tid]);
+        }
+        __syncthreads();
+        if (tid < nr) sums[tid] = v;
+        __syncthreads();
+        if (tid < nr) {
+            const int row = row0 + tid, pos = *a.pos;
+            float o = v;
+            if (mi < 2) {
+                const int hd = a.head_dim, j = row % hd, h2 = hd >> 1;
+                const float c = a.rope_cos[(size_t)pos * h2 + (j >> 1)], s = a.rope_sin[(size_t)pos * h2 + (j >> 1)];
+                const float pa = sums[tid & ~1], pb = sums[tid | 1];
+                o = (j & 1) == 0 ? kr_fsub(kr_fmul(pa, c), kr_fmul(pb, s))
+                                 : kr_fadd(kr_fmul(pa, s), kr_fmul(pb, c));
+            }
+            if (mi == 0) a.y[0][row] = o;
+            else pick3(mi, a.y[0], a.y[1], a.y[2])[(size_t)pos * a.ld_cache + row] = o;
+        }
+    } else if (EPI == EPI_SWIGLU) {
+        // g = g / (1 + expf(-g)) * u (k_scalar.c:96-98), then Q8_0 of the
+        // 32-row block (k_scalar.c:39-57)
+        if (tid < R) {
+            const float h1 = sums[tid], h3 = sums[R + tid];
+            const float g = kr_fmul(kr_fdiv(h1, kr_fadd(1.0f, kr_expf(-h1))), h3);
+            if (a.y[0]) a.y[0][row0 + tid] = g;
+            int8_t q;
+            float d;
+            kr_quant_block32(g, &q, &d);
+            a.oq[row0 + tid] = q;
+            if (tid == 0) a.od[row0 / KR_QK] = d;
+        }
+    }
+}
+
+template <int EPI, int R>
+void launch_mv(const MvArgs &a, int grid) {
+    const int nb = a.K / KR_QK;
+    const int nloc = EPI == EPI_SWIGLU ? 2 * R : R;
+    const size_t lds = (size_t)a.K + 4u * nb + 4u * (size_t)nloc * (nb | 1) + 4u * nloc;
+    if (a.K % KR_QK || lds > 65536 || grid <= 0) {
+        kr_fail(ML_E_SHAPE, "matvec shape", hipSuccess);
+        return;
+    }
+    hipLaunchKernelGGL((k_matvec<EPI, R>), dim3(grid), dim3(MV_THREADS), lds, kr_stream(), a);
+    kr_check_launch("matvec");
+}
+
+constexpr int MV_R = 16;
+constexpr int SW_R = 32;
+
+// ---- rmsnorm + quantize, quantize ----
+
+// One workgroup per token: lane 0 sums x_i * x_i in index order
+// (k_scalar.c:61), then every lane forms (x * inv) * w and the half-waves
+// quantize their 32-element blocks.
+__global__ void __launch_bounds__(256) k_rmsnorm_q8(int8_t *q, float *d, float *xb, const float *x, const float *w,
+                                                    int n, float eps, int norm) {
+    const size_t t = blockIdx.x;
+    x += t * n;
+    q += t * n;
+    d += t * (n / KR_QK);
+    if (xb) xb += t * n;
+    __shared__ float s_inv;
+    if (norm) {
+        if (threadIdx.x == 0) {
+            float ss = 0.0f;
+            int i = 0;
+            if ((n & 3) == 0 && ((uintptr_t)x & 15) == 0) {
+#pragma unroll 4
+                for (; i < n; i += 4) {
+                    const float4 v = *(const float4 *)(x + i);
+                    ss = kr_fadd(ss, kr_fmul(v.x, v.x));
+                    ss = kr_fadd(ss, kr_fmul(v.y, v.y));
+                    ss = kr_fadd(ss, kr_fmul(v.z, v.z));
+                    ss = kr_fadd(ss, kr_fmul(v.w, v.w));
+                }
+            }
+            for (; i < n; i++) ss = kr_fadd(ss, kr_fmul(x[i], x[i]));
+            s_inv = kr_fdiv(1.0f, kr_fsqrt(kr_fadd(kr_fdiv(ss, (float)n), eps)));
+        }
+        __syncthreads();
+    }
+    const float inv = norm ? s_inv : 1.0f;
+    for (int base = 0; base < n; base += 256) {
+        const int i = base + threadIdx.x;
+        if (i < n) {   // n % 32 == 0: a half-wave is all in or all out
+            const float o = norm ? kr_fmul(kr_fmul(x[i], inv), w[i]) : x[i];
+            if (xb) xb[i] = o;
+            int8_t qq;
+            float dd;
+            kr_quant_block32(o, &qq, &dd);
+            q[i] = qq;
+            if ((i & 31) == 0) d[i >> 5] = dd;
+        }
+    }
+}
+
+// ---- embedding ----
+
+__global__ void k_embed(float *x, const KMat e, const int *tok, float scale) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= e.cols) return;
+    const int nb = e.cols / KR_QK, row = *tok, b = i / KR_QK, j = i % KR_QK;
+    const float d = kr_scale(e.d, (size_t)row * nb + b, e.d16);
+    int v;
+    if (e.type == ML_Q8_0) {
+        v = ((const int8_t *)e.q)[(size_t)row * e.cols + i];
+    } else {
+        const uint8_t p = e.q[((size_t)row * nb + b) * 16 + (j & 15)];
+        v = (j < 16 ? (p & 0xF) : (p >> 4)) - 8;
+    }
+    float o = kr_fmul((float)v, d);
+    if (scale != 1.0f) o = kr_fmul(o, scale);
+    x[i] = o;
+}
+
+// ---- attention (F32 cache) ----
+
+// Scores of one KV head's query heads for 64 positions: lane = position,
+// s = (sum_i q_i k_i in index order) * scale (k_scalar.c:111-117).
+__global__ void __launch_bounds__(64) k_attn_scores(float *att, const float *q, const float *kc, int group, int hd,
+                                                    int kv_dim, int max_seq, int window, float scale, const int *pos_p) {
+    extern __shared__ float qs[];
+    const int pos = *pos_p, first = window && pos >= window ? pos + 1 - window : 0, n = pos + 1 - first;
+    const int g = blockIdx.x, t0 = blockIdx.y * 64;
+    if (t0 >= n) return;
+    for (int i = threadIdx.x; i < group * hd; i += 64) qs[i] = q[(size_t)g * group * hd + i];
+    __syncthreads();
+    const int t = t0 + threadIdx.x;
+    if (t >= n) return;
+    const float2 *k = (const float2 *)(kc + (size_t)(first + t) * kv_dim + (size_t)g * hd);
+    for (int h0 = 0; h0 < group; h0 += 4) {
+        const int nh = min(4, group - h0);
+        float acc[4] = { 0.0f, 0.0f, 0.0f, 0.0f };
+        for (int i = 0; i < hd / 2; i++) {
+            const float2 kv = k[i];
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+                if (j < nh) {
+                    acc[j] = kr_fadd(acc[j], kr_fmul(qs[(h0 + j) * hd + 2 * i], kv.x));
+                    acc[j] = kr_fadd(acc[j], kr_fmul(qs[(h0 + j) * hd + 2 * i + 1], kv.y));
+                }
+        }
+        for (int j = 0; j < nh; j++) att[(size_t)(g * group + h0 + j) * max_seq + t] = kr_fmul(acc[j], scale);
+    }
+}
+
+// Softmax of one head's scores in place (k_scalar.c:66-77): max, expf,
+// the sum in position order by one lane, then x * (1 / sum).
+__global__ void __launch_bounds__(256) k_attn_softmax(float *att, int max_seq, int window, const int *pos_p) {
+    const int pos = *pos_p, first = window && pos >= window ? pos + 1 - window : 0, n = pos + 1 - first;
+    float *a = att + (size_t)blockIdx.x * max_seq;
+    __shared__ float red[4];
+    __shared__ float s_inv;
+    float m = -INFINITY;
+    for (int t = threadIdx.x; t < n; t += 256) m = fmaxf(m, a[t]);
+    for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+    __syncthreads();
+    const float mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    if (mx == -INFINITY) {
+        for (int t = threadIdx.x; t < n; t += 256) a[t] = kr_fdiv(1.0f, (float)n);
+        return;
+    }
+    for (int t = threadIdx.x; t < n; t += 256) a[t] = kr_expf(kr_fsub(a[t], mx));
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float sum = 0.0f;
+#pragma unroll 8
+        for (int t = 0; t < n; t++) sum = kr_fadd(sum, a[t]);
+        s_inv = kr_fdiv(1.0f, sum);
+    }
+    __syncthreads();
+    const float inv = s_inv;
+    for (int t = threadIdx.x; t < n; t += 256) a[t] = kr_fmul(a[t], inv);
+}
+
+// Output of one (query head, dim) per lane: o = 0, then o += a_t * v_t,i in
+// position order (k_scalar.c:119-122); the 32-lane halves then quantize
+// their block of the output (q_dim % 32 == 0).
+__global__ void __launch_bounds__(64) k_attn_mix(float *ao, int8_t *aq, float *ad, const float *att, const float *vc,
+                                                 int q_dim, int group, int hd, int kv_dim, int max_seq, int window,
+                                                 const int *pos_p) {
+    const int pos = *pos_p, first = window && pos >= window ? pos + 1 - window : 0, n = pos + 1 - first;
+    const int slot = blockIdx.x * 64 + threadIdx.x;
+    if (slot >= q_dim) return;   // whole half-waves (q_dim % 32 == 0)
+    const int h = slot / hd, i = slot - h * hd, kvh = h / group;
+    const float *a = att + (size_t)h * max_seq;
+    const float *v = vc + (size_t)first * kv_dim + (size_t)kvh * hd + i;
+    float o = 0.0f;
+#pragma unroll 8
+    for (int t = 0; t < n; t++) o = kr_fadd(o, kr_fmul(a[t], v[(size_t)t * kv_dim]));
+    ao[slot] = o;
+    if (aq) {
+        int8_t q;
+        float d;
+        kr_quant_block32(o, &q, &d);
+        aq[slot] = q;
+        if ((slot & 31) == 0) ad[slot >> 5] = d;
+    }
+}
+
+// ---- greedy pick ----
+
+// First index of the maximum (model/sampler.c:57-61): NaN entries never win,
+// and a NaN at index 0 keeps 0, as the sequential loop does.
+__global__ void __launch_bounds__(1024) k_argmax(int *tok, const float *v, int n, int *pos, int *log) {
+    __shared__ float sv[16];
+    __shared__ int si[16];
+    float bv = -INFINITY;
+    int bi = INT_MAX;
+    for (int i = threadIdx.x; i < n; i += 1024) {
+        const float x = v[i];
+        if (x > bv || (bi == INT_MAX && x == bv)) { bv = x; bi = i; }
+    }
+    for (int o = 32; o >= 1; o >>= 1) {
+        const float ov = __shfl_xor(bv, o);
+        const int oi = __shfl_xor(bi, o);
+        if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+    }
+    const int w = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) { sv[w] = bv; si[w] = bi; }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int k = 1; k < 16; k++)
+            if (sv[k] > bv || (sv[k] == bv && si[k] < bi)) { bv = sv[k]; bi = si[k]; }
+        if (bi == INT_MAX || v[0] != v[0]) bi = 0;
+        *tok = bi;
+        if (pos) {
+            const int p = *pos + 1;
+            if (log) log[p] = bi;
+            *pos = p;
+        }
+    }
+}
+
+__global__ void k_take_token(int *tok, const int *prompt, const int *pos) { *tok = prompt[*pos]; }
+__global__ void k_advance(int *pos) { *pos += 1; }
+
+__global__ void k_math_batch(int op, float *y, const float *a, const float *b, size_t n) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    switch (op) {
+    case KRH_MATH_EXPF: y[i] = kr_expf(a[i]); break;
+    case KRH_MATH_SQRT: y[i] = kr_fsqrt(a[i]); break;
+    case KRH_MATH_DIV: y[i] = kr_fdiv(a[i], b[i]); break;
+    case KRH_MATH_RMS_INV: y[i] = kr_fdiv(1.0f, kr_fsqrt(kr_fadd(kr_fdiv(a[i], b[i]), 1e-5f))); break;
+    default: y[i] = 0.0f;
+    }
+}
+__global__ void k_h2f_batch(float *y, const uint16_t *h, size_t n) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) y[i] = kr_h2f(h[i]);
+}
+__global__ void k_block_dots(int32_t *out, const KMat W, const int8_t *xq) {
+    const int nb = W.cols / KR_QK;
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (size_t)W.rows * nb) return;
+    const int b = (int)(i % nb);
+    int4 w0, w1 = make_int4(0, 0, 0, 0);
+    int s;
+    __align__(16) int8_t xb[32];
+    for (int j = 0; j < 32; j++) xb[j] = xq[b * 32 + j];
+    if (W.type == ML_Q8_0) {
+        w0 = ((const int4 *)(W.q + i * 32))[0];
+        w1 = ((const int4 *)(W.q + i * 32))[1];
+        s = block_dot<ML_Q8_0>(w0, w1, xb);
+    } else {
+        w0 = *(const int4 *)(W.q + i * 16);
+        s = block_dot<ML_Q4_0>(w0, w1, xb);
+    }
+    out[i] = s;
+}
+
+}  // namespace
+
+// ---- C ABI ----
+
+extern "C" void krh_embed(float *x, const krh_mat *emb, const int *tok, float embed_scale) {
+    hipLaunchKernelGGL(k_embed, dim3((emb->cols + 255) / 256), dim3(256), 0, kr_stream(), x, to_kmat(emb), tok,
+                       embed_scale);
+    kr_check_launch("embed");
+}
+
+extern "C" void krh_rmsnorm_q8(int8_t *q, float *d, float *xb, const float *x, const float *w, int n, float eps,
+                               int ntok) {
+    if (n % KR_QK || ntok <= 0) { kr_fail(ML_E_SHAPE, "rmsnorm shape", hipSuccess); return; }
+    hipLaunchKernelGGL(k_rmsnorm_q8, dim3(ntok), dim3(256), 0, kr_stream(), q, d, xb, x, w, n, eps, 1);
+    kr_check_launch("rmsnorm_q8");
+}
+
+extern "C" void krh_quantize_q8(int8_t *q, float *d, const float *x, int n, int ntok) {
+    if (n % KR_QK || ntok <= 0) { kr_fail(ML_E_SHAPE, "quantize shape", hipSuccess); return; }
+    hipLaunchKernelGGL(k_rmsnorm_q8, dim3(ntok), dim3(256), 0, kr_stream(), q, d, (float *)nullptr, x,
+                       (const float *)nullptr, n, 0.0f, 0);
+    kr_check_launch("quantize_q8");
+}
+
+extern "C" void krh_matvec(float *y, const krh_mat *W, const int8_t *xq, const float *xd, int accumulate) {
+    MvArgs a = {};
+    a.m[0] = to_kmat(W);
+    a.nmat = 1;
+    a.tile0[0] = 0;
+    a.tile0[1] = (W->rows + MV_R - 1) / MV_R;
+    a.xq = xq;
+    a.xd = xd;
+    a.K = W->cols;
+    a.y[0] = y;
+    if (accumulate) launch_mv<EPI_ADD, MV_R>(a, a.tile0[1]);
+    else launch_mv<EPI_STORE, MV_R>(a, a.tile0[1]);
+}
+
+extern "C" void krh_matvec_qkv(float *q, float *kc, float *vc, const krh_mat *wq, const krh_mat *wk,
+                               const krh_mat *wv, const float *bq, const float *bk, const float *bv, const int8_t *xq,
+                               const float *xd, const float *rope_cos, const float *rope_sin, int head_dim,
+                               const int *pos) {
+    if (wq->cols != wk->cols || wq->cols != wv->cols || wk->rows != wv->rows || head_dim % 2 || wq->rows % 2 ||
+        wk->rows % 2) {
+        kr_fail(ML_E_SHAPE, "qkv shapes", hipSuccess);
+        return;
+    }
+    MvArgs a = {};
+    a.m[0] = to_kmat(wq);
+    a.m[1] = to_kmat(wk);
+    a.m[2] = to_kmat(wv);
+    a.nmat = 3;
+    a.tile0[0] = 0;
+    a.tile0[1] = (wq->rows + MV_R - 1) / MV_R;
+    a.tile0[2] = a.tile0[1] + (wk->rows + MV_R - 1) / MV_R;
+    a.tile0[3] = a.tile0[2] + (wv->rows + MV_R - 1) / MV_R;
+    a.xq = xq;
+    a.xd = xd;
+    a.K = wq->cols;
+    a.y[0] = q;
+    a.y[1] = kc;
+    a.y[2] = vc;
+    a.bias[0] = bq;
+    a.bias[1] = bk;
+    a.bias[2] = bv;
+    a.rope_cos = rope_cos;
+    a.rope_sin = rope_sin;
+    a.head_dim = head_dim;
+    a.ld_cache = wk->rows;
+    a.pos = pos;
+    launch_mv<EPI_QKV, MV_R>(a, a.tile0[3]);
+}
+
+extern "C" void krh_matvec_swiglu_q8(int8_t *hq, float *hd, float *hb, const krh_mat *w1, const krh_mat *w3,
+                                     const int8_t *xq, const float *xd) {
+    if (w1->rows != w3->rows || w1->cols != w3->cols || w1->type != w3->type || w1->d16 != w3->d16 ||
+        w1->rows % SW_R) {
+        kr_fail(ML_E_SHAPE, "swiglu shapes", hipSuccess);
+        return;
+    }
+    MvArgs a = {};
+    a.m[0] = to_kmat(w1);
+    a.m[1] = to_kmat(w3);
+    a.nmat = 1;
+    a.tile0[0] = 0;
+    a.tile0[1] = w1->rows / SW_R;
+    a.xq = xq;
+    a.xd = xd;
+    a.K = w1->cols;
+    a.y[0] = hb;
+    a.oq = hq;
+    a.od = hd;
+    launch_mv<EPI_SWIGLU, SW_R>(a, a.tile0[1]);
+}
+
+extern "C" void krh_attention(float *ao, int8_t *aq, float *ad, float *att, const float *q, const float *kc,
+                              const float *vc, int n_heads, int n_kv_heads, int head_dim, int max_seq, int window,
+                              float scale, const int *pos) {
+    if (n_kv_heads <= 0 || n_heads % n_kv_heads || head_dim % 2 || (n_heads * head_dim) % KR_QK) {
+        kr_fail(ML_E_SHAPE, "attention shape", hipSuccess);
+        return;
+    }
+    const int group = n_heads / n_kv_heads, kv_dim = n_kv_heads * head_dim, q_dim = n_heads * head_dim;
+    hipLaunchKernelGGL(k_attn_scores, dim3(n_kv_heads, (max_seq + 63) / 64), dim3(64),
+                       sizeof(float) * group * head_dim, kr_stream(), att, q, kc, group, head_dim, kv_dim, max_seq,
+                       window, scale, pos);
+    hipLaunchKernelGGL(k_attn_softmax, dim3(n_heads), dim3(256), 0, kr_stream(), att, max_seq, window, pos);
+    hipLaunchKernelGGL(k_attn_mix, dim3((q_dim + 63) / 64), dim3(64), 0, kr_stream(), ao, aq, ad, att, vc, q_dim,
+                       group, head_dim, kv_dim, max_seq, window, pos);
+    kr_check_launch("attention");
+}
+
+extern "C" void krh_argmax(int *tok, const float *logits, int n, int *pos, int *log) {
+    hipLaunchKernelGGL(k_argmax, dim3(1), dim3(1024), 0, kr_stream(), tok, logits, n, pos, log);
+    kr_check_launch("argmax");
+}
+
+extern "C" void krh_take_token(int *tok, const int *prompt, const int *pos) {
+    hipLaunchKernelGGL(k_take_token, dim3(1), dim3(1), 0, kr_stream(), tok, prompt, pos);
+    kr_check_launch("take_token");
+}
+
+extern "C" void krh_advance(int *pos) {
+    hipLaunchKernelGGL(k_advance, dim3(1), dim3(1), 0, kr_stream(), pos);
+    kr_check_launch("advance");
+}
+
+extern "C" void krh_math_batch(int op, float *y, const float *a, const float *b, size_t n) {
+    hipLaunchKernelGGL(k_math_batch, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, kr_stream(), op, y, a, b, n);
+    kr_check_launch("math_batch");
+}
+
+extern "C" void krh_h2f_batch(float *y, const uint16_t *h, size_t n) {
+    hipLaunchKernelGGL(k_h2f_batch, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, kr_stream(), y, h, n);
+    kr_check_launch("h2f_batch");
+}
+
+extern "C" void krh_block_dots(int32_t *s, const krh_mat *W, const int8_t *xq) {
+    const size_t n = (size_t)W->rows * (W->cols / KR_QK);
+    hipLaunchKernelGGL(k_block_dots, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, kr_stream(), s, to_kmat(W),
+                       xq);
+    kr_check_launch("block_dots");
+}

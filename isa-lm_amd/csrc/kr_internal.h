@@ -1,0 +1,10 @@
+// Internal declarations shared by the library's translation units.
+#pragma once
+#include <hip/hip_runtime.h>
+#include "../../include/krafla_hip.h"
+
+hipStream_t kr_stream(void);
+// records the first error (sticky) with a message
+void kr_fail(ml_status st, const char *what, hipError_t e);
+// records a launch error, if any
+void kr_check_launch(const char *what);

@@ -1,0 +1,106 @@
+// Device numerics shared by every kernel. Every float operation whose
+// rounding the scalar reference fixes goes through the helpers below: one
+// IEEE operation each, rounded to nearest even. Contraction into fused
+// multiply-adds is switched off for every file that includes this header
+// (and on the command line), and division and square root are the correctly
+// rounded ones (-fhip-fp32-correctly-rounded-divide-sqrt; checked against the
+// host exhaustively for sqrt). HIP's __fsqrt_rn is not used: in this ROCm it
+// is the approximate native square root.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <stdint.h>
+
+#pragma clang fp contract(off)
+
+__device__ __forceinline__ float kr_fadd(float a, float b) { return a + b; }
+__device__ __forceinline__ float kr_fsub(float a, float b) { return a - b; }
+__device__ __forceinline__ float kr_fmul(float a, float b) { return a * b; }
+__device__ __forceinline__ float kr_fdiv(float a, float b) { return a / b; }
+__device__ __forceinline__ float kr_fsqrt(float a) { return __builtin_sqrtf(a); }
+
+#define KR_QK 32
+#define KR_QUANT_TINY 1e-30f
+
+// 2^(i/32) as doubles, minus (i << 47): the table of the C library's expf
+// (ARM optimized-routines exp2f_data.c); each entry is the correctly rounded
+// double of 2^(i/32) with the exponent bits of i/32 taken out.
+__constant__ uint64_t kr_exp2_tab[32] = {
+    0x3ff0000000000000ULL, 0x3fefd9b0d3158574ULL, 0x3fefb5586cf9890fULL, 0x3fef9301d0125b51ULL,
+    0x3fef72b83c7d517bULL, 0x3fef54873168b9aaULL, 0x3fef387a6e756238ULL, 0x3fef1e9df51fdee1ULL,
+    0x3fef06fe0a31b715ULL, 0x3feef1a7373aa9cbULL, 0x3feedea64c123422ULL, 0x3feece086061892dULL,
+    0x3feebfdad5362a27ULL, 0x3feeb42b569d4f82ULL, 0x3feeab07dd485429ULL, 0x3feea47eb03a5585ULL,
+    0x3feea09e667f3bcdULL, 0x3fee9f75e8ec5f74ULL, 0x3feea11473eb0187ULL, 0x3feea589994cce13ULL,
+    0x3feeace5422aa0dbULL, 0x3feeb737b0cdc5e5ULL, 0x3feec49182a3f090ULL, 0x3feed503b23e255dULL,
+    0x3feee89f995ad3adULL, 0x3feeff76f2fb5e47ULL, 0x3fef199bdd85529cULL, 0x3fef3720dcef9069ULL,
+    0x3fef5818dcfba487ULL, 0x3fef7c97337b9b5fULL, 0x3fefa4afa2a490daULL, 0x3fefd0765b6e4540ULL,
+};
+
+// expf with the C library's results, bit for bit: the reference's softmax and
+// SiLU call glibc's expf (kernels/scalar/k_scalar.c:74, :97), whose x86-64 FMA
+// build evaluates x*32/ln2 = k + r with two fused multiply-adds and
+// 2^(k/32) * (1 + c2 r + (c0 r + c1) r^2) in double.
+__device__ __forceinline__ float kr_expf(float x) {
+    const uint32_t ux = __float_as_uint(x);
+    const uint32_t top = (ux >> 20) & 0x7ff;
+    if (top >= 0x42bu) {                       // |x| >= 88, inf or NaN
+        if (ux == 0xff800000u) return 0.0f;
+        if (top >= 0x7f8u) return x + x;
+        if (x > 0x1.62e42ep6f) return __uint_as_float(0x7f800000u);
+        if (x < -0x1.9fe368p6f) return 0.0f;
+    }
+    const double inv_ln2_n = 0x1.71547652b82fep+0 * 32, shift = 0x1.8p+52;
+    const double c0 = 0x1.c6af84b912394p-5 / 32 / 32 / 32, c1 = 0x1.ebfce50fac4f3p-3 / 32 / 32,
+                 c2 = 0x1.62e42ff0c52d6p-1 / 32;
+    const double xd = (double)x;
+    double kd = __builtin_fma(inv_ln2_n, xd, shift);
+    const uint64_t ki = (uint64_t)__double_as_longlong(kd);
+    kd = kd - shift;
+    const double r = __builtin_fma(inv_ln2_n, xd, -kd);
+    const double s = __longlong_as_double((long long)(kr_exp2_tab[ki & 31] + (ki << 47)));
+    const double p = __builtin_fma(c0, r, c1);
+    const double r2 = r * r;
+    double y = __builtin_fma(c2, r, 1.0);
+    y = __builtin_fma(p, r2, y);
+    return (float)(y * s);
+}
+
+// IEEE binary16 -> float32; exact for every input (subnormals included).
+__device__ __forceinline__ float kr_h2f(uint16_t h) { return __half2float(__ushort_as_half(h)); }
+
+__device__ __forceinline__ float kr_scale(const void *d, size_t i, int d16) {
+    return d16 ? kr_h2f(((const uint16_t *)d)[i]) : ((const float *)d)[i];
+}
+
+// One element of the Q8_0 rule (docs/file-format.md:133-144,
+// kernels/scalar/k_scalar.c:52-54): trunc(x * id + copysign(0.5, x)),
+// multiply then add, clamped to +-127.
+__device__ __forceinline__ int kr_q8_elem(float x, float id) {
+    float v = truncf(kr_fadd(kr_fmul(x, id), copysignf(0.5f, x)));
+    v = fminf(fmaxf(v, -127.0f), 127.0f);
+    return (int)v;
+}
+
+// Max over the 32 lanes of a half-wave (lanes 0-31 or 32-63). fmaxf is
+// exact, so the order of the reduction does not matter.
+__device__ __forceinline__ float kr_max32(float v) {
+#pragma unroll
+    for (int m = 16; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, 32));
+    return v;
+}
+
+// Quantizes the 32 values held by the 32 lanes of a half-wave (lane j holds
+// element j of the block) into q (this lane's element) and the block scale.
+__device__ __forceinline__ void kr_quant_block32(float x, int8_t *q, float *d) {
+    const float amax = kr_max32(fabsf(x));
+    if (amax < KR_QUANT_TINY) {
+        *q = 0;
+        *d = 0.0f;
+        return;
+    }
+    const float id = kr_fdiv(127.0f, amax);
+    *d = kr_fdiv(amax, 127.0f);
+    *q = (int8_t)kr_q8_elem(x, id);
+}
+
+__device__ __forceinline__ int kr_dot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }

@@ -1,0 +1,431 @@
+/* The token loop on the device: model upload, decoding state, and
+ * ml_forward / ml_prefill / ml_run's greedy loop as sequences of fused HIP
+ * ops, each sequence captured once into a graph and replayed per token.
+ *
+ * One decode step (model/transformer.c:257-306), per layer:
+ *   rmsnorm+quantize(attn_norm) -> q,k,v matvec + bias + RoPE + cache write
+ *   -> attention (+ quantize of its output) -> x += wo.ao
+ *   -> rmsnorm+quantize(ffn_norm) -> silu(w1.x) * (w3.x) + quantize
+ *   -> x += w2.h
+ * then rmsnorm+quantize(final_norm) -> logits = wcls.x. Every op reads the
+ * token and position from device memory, so the captured step replays for
+ * any position without new arguments. */
+#include <math.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+#include <sys/mman.h>
+#include <time.h>
+#include "kr_host.h"
+
+static char g_err[512];
+
+ml_status kr_seterr(ml_status s, const char *fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof g_err, fmt, ap);
+    va_end(ap);
+    return s;
+}
+
+const char *kr_error(void) { return g_err; }
+
+/* core/ml.c:21-33 */
+const char *kr_status_str(ml_status s) {
+    switch (s) {
+    case ML_OK: return "ok";
+    case ML_E_IO: return "i/o error";
+    case ML_E_FORMAT: return "bad file format";
+    case ML_E_SHAPE: return "bad tensor shape";
+    case ML_E_NOMEM: return "out of memory";
+    case ML_E_ISA: return "no gfx950 device";
+    }
+    return "unknown";
+}
+
+double kr_now(void) {
+    struct timespec t;
+    clock_gettime(CLOCK_MONOTONIC, &t);
+    return (double)t.tv_sec + 1e-9 * (double)t.tv_nsec;
+}
+
+/* ---- upload ---- */
+
+#define RUP(n) (((size_t)(n) + 255) & ~(size_t)255)
+
+static size_t mat_bytes(const ml_qtensor *W, int f16) {
+    const size_t n = (size_t)W->rows * W->cols;
+    return RUP(W->type == ML_Q4_0 ? n / 2 : n) + RUP(n / QK * (f16 ? 2 : 4));
+}
+
+typedef struct { uint8_t *base; size_t off; ml_status st; } placer;
+
+static void *place(placer *p, const void *src, size_t n) {
+    void *dst = p->base + p->off;
+    p->off += RUP(n);
+    if (p->st == ML_OK && n && krh_copy_h2d(dst, src, n) != ML_OK) p->st = kr_seterr(ML_E_IO, "%s", krh_last_error());
+    return dst;
+}
+
+static krh_mat place_mat(placer *p, const ml_qtensor *W, int f16) {
+    const size_t n = (size_t)W->rows * W->cols;
+    krh_mat d;
+    d.rows = W->rows;
+    d.cols = W->cols;
+    d.type = W->type;
+    d.d16 = f16;
+    d.q = place(p, W->q, W->type == ML_Q4_0 ? n / 2 : n);
+    d.d = place(p, f16 ? (const void *)W->dh : (const void *)W->d, n / QK * (f16 ? 2 : 4));
+    return d;
+}
+
+ml_status kr_model_upload(kr_model *m) {
+    if (m->dev) return ML_OK;
+    ml_status st = krh_init();
+    if (st != ML_OK) return kr_seterr(st, "%s", krh_last_error());
+    const ml_config *c = &m->cfg;
+    const int f16 = c->scale_f16;
+    const size_t fd = sizeof(float) * (size_t)c->dim;
+    size_t total = mat_bytes(&m->tok_emb, f16) + RUP(fd);
+    if (!m->shared) total += mat_bytes(&m->wcls, f16);
+    for (int l = 0; l < c->n_layers; l++) {
+        const ml_layer *L = &m->layers[l];
+        const ml_qtensor *ws[7] = { &L->wq, &L->wk, &L->wv, &L->wo, &L->w1, &L->w2, &L->w3 };
+        for (int k = 0; k < 7; k++) total += mat_bytes(ws[k], f16);
+        total += 2 * RUP(fd);
+        if (L->bq) total += RUP(sizeof(float) * c->q_dim) + 2 * RUP(sizeof(float) * c->kv_dim);
+    }
+    m->dev = krh_alloc(total);
+    if (!m->dev) return kr_seterr(ML_E_NOMEM, "cannot allocate %zu bytes of HBM for the weights", total);
+    m->dev_bytes = total;
+    m->d_layers = calloc((size_t)c->n_layers, sizeof *m->d_layers);
+    if (!m->d_layers) return ML_E_NOMEM;
+    placer p = { m->dev, 0, ML_OK };
+    m->d_tok_emb = place_mat(&p, &m->tok_emb, f16);
+    for (int l = 0; l < c->n_layers; l++) {
+        const ml_layer *L = &m->layers[l];
+        struct kr_dev_layer *D = &m->d_layers[l];
+        D->attn_norm = place(&p, L->attn_norm, fd);
+        D->ffn_norm = place(&p, L->ffn_norm, fd);
+        D->wq = place_mat(&p, &L->wq, f16);
+        D->wk = place_mat(&p, &L->wk, f16);
+        D->wv = place_mat(&p, &L->wv, f16);
+        D->wo = place_mat(&p, &L->wo, f16);
+        D->w1 = place_mat(&p, &L->w1, f16);
+        D->w2 = place_mat(&p, &L->w2, f16);
+        D->w3 = place_mat(&p, &L->w3, f16);
+        if (L->bq) {
+            D->bq = place(&p, L->bq, sizeof(float) * c->q_dim);
+            D->bk = place(&p, L->bk, sizeof(float) * c->kv_dim);
+            D->bv = place(&p, L->bv, sizeof(float) * c->kv_dim);
+        }
+    }
+    m->d_final_norm = place(&p, m->final_norm, fd);
+    m->d_wcls = m->shared ? m->d_tok_emb : place_mat(&p, &m->wcls, f16);
+    return p.st;
+}
+
+size_t kr_model_device_bytes(const kr_model *m) { return m->dev_bytes; }
+
+const krh_mat *kr_model_device_mat(const kr_model *m, int layer, const char *name) {
+    if (!m->dev) return NULL;
+    if (!strcmp(name, "tok_emb")) return &m->d_tok_emb;
+    if (!strcmp(name, "wcls")) return &m->d_wcls;
+    if (layer < 0 || layer >= m->cfg.n_layers) return NULL;
+    const struct kr_dev_layer *D = &m->d_layers[layer];
+    static const char *const names[] = { "wq", "wk", "wv", "wo", "w1", "w2", "w3" };
+    const krh_mat *mats[] = { &D->wq, &D->wk, &D->wv, &D->wo, &D->w1, &D->w2, &D->w3 };
+    for (int i = 0; i < 7; i++)
+        if (!strcmp(names[i], name)) return mats[i];
+    return NULL;
+}
+
+const float *kr_model_device_vec(const kr_model *m, int layer, const char *name) {
+    if (!m->dev) return NULL;
+    if (!strcmp(name, "final_norm")) return m->d_final_norm;
+    if (layer < 0 || layer >= m->cfg.n_layers) return NULL;
+    const struct kr_dev_layer *D = &m->d_layers[layer];
+    if (!strcmp(name, "attn_norm")) return D->attn_norm;
+    if (!strcmp(name, "ffn_norm")) return D->ffn_norm;
+    if (!strcmp(name, "bq")) return D->bq;
+    if (!strcmp(name, "bk")) return D->bk;
+    if (!strcmp(name, "bv")) return D->bv;
+    return NULL;
+}
+
+void kr_model_free(kr_model *m) {
+    if (!m) return;
+    krh_free(m->dev);
+    free(m->d_layers);
+    free(m->layers);
+    if (m->map) munmap(m->map, m->size);
+    free(m);
+}
+
+/* ---- state ---- */
+
+struct kr_state {
+    kr_model *m;
+    /* device buffers */
+    float *x, *q, *ao, *att, *logits, *kcache, *vcache, *rope_cos, *rope_sin, *rope_cos_l, *rope_sin_l;
+    int8_t *qa_dim, *qa_q, *qa_hid;
+    float *qd_dim, *qd_q, *qd_hid;
+    int *tok, *pos, *prompt, *log;
+    void *mem;
+    float *h_logits;          /* pinned */
+    int *h_ints;              /* pinned: tok, pos */
+    krh_graph *g_logits, *g_greedy, *g_prefill;
+    int batch;
+};
+
+/* model/transformer.c:16-38: inverse frequency of rotary pair i */
+static double rope_inv_freq(const ml_config *c, int i) {
+    const double inv = pow((double)c->rope_theta, -2.0 * i / c->head_dim);
+    if (c->rope_type == ML_ROPE_LINEAR) return inv / c->rope_factor;
+    if (c->rope_type == ML_ROPE_YARN) {
+        const double hd = c->head_dim, orig = c->rope_orig_max_seq, lb = 2.0 * log((double)c->rope_theta);
+        const double pi2 = 2.0 * 3.14159265358979323846;
+        double lo = floor(hd * log(orig / ((double)c->rope_low_freq_factor * pi2)) / lb);
+        double hi = ceil(hd * log(orig / ((double)c->rope_high_freq_factor * pi2)) / lb);
+        lo = lo < 0.0 ? 0.0 : lo;
+        hi = hi > hd - 1.0 ? hd - 1.0 : hi;
+        if (lo == hi) hi += 0.001;
+        double ramp = (i - lo) / (hi - lo);
+        ramp = ramp < 0.0 ? 0.0 : (ramp > 1.0 ? 1.0 : ramp);
+        return inv / c->rope_factor * ramp + inv * (1.0 - ramp);
+    }
+    if (c->rope_type != ML_ROPE_LLAMA3) return inv;
+    const double f = c->rope_factor, lo = c->rope_low_freq_factor, hi = c->rope_high_freq_factor;
+    const double orig = c->rope_orig_max_seq, wavelen = 2.0 * 3.14159265358979323846 / inv;
+    if (wavelen < orig / hi) return inv;
+    if (wavelen > orig / lo) return inv / f;
+    const double smooth = (orig / wavelen - lo) / (hi - lo);
+    return (1.0 - smooth) * inv / f + smooth * inv;
+}
+
+/* The tables in double on the host, then rounded to float, exactly as
+ * model/transformer.c:147-162 builds them. */
+static void rope_tables(const ml_config *c, float *cs, float *sn, float *cs_l, float *sn_l) {
+    const int h2 = c->head_dim / 2;
+    const double af = c->rope_type == ML_ROPE_YARN ? c->rope_attn_factor : 1.0;
+    for (int i = 0; i < h2; i++) {
+        const double freq = rope_inv_freq(c, i);
+        const double lfreq = cs_l ? pow((double)c->rope_local_theta, -2.0 * i / c->head_dim) : 0.0;
+        for (int p = 0; p < c->max_seq; p++) {
+            const double ang = p * freq;
+            cs[(size_t)p * h2 + i] = (float)(cos(ang) * af);
+            sn[(size_t)p * h2 + i] = (float)(sin(ang) * af);
+            if (cs_l) {
+                cs_l[(size_t)p * h2 + i] = (float)cos(p * lfreq);
+                sn_l[(size_t)p * h2 + i] = (float)sin(p * lfreq);
+            }
+        }
+    }
+}
+
+/* ml_forward's ops for the token in s->tok at position s->pos; cls: run the
+ * final norm and the classifier too */
+static void issue_step(kr_state *s, int cls) {
+    const kr_model *m = s->m;
+    const ml_config *c = &m->cfg;
+    const size_t lkv = (size_t)c->max_seq * c->kv_dim;
+    krh_embed(s->x, &m->d_tok_emb, s->tok, c->embed_scale);
+    for (int l = 0; l < c->n_layers; l++) {
+        const struct kr_dev_layer *D = &m->d_layers[l];
+        const ml_layer *L = &m->layers[l];
+        float *kc = s->kcache + (size_t)l * lkv, *vc = s->vcache + (size_t)l * lkv;
+        const float *cs = L->local_rope ? s->rope_cos_l : s->rope_cos, *sn = L->local_rope ? s->rope_sin_l : s->rope_sin;
+        krh_rmsnorm_q8(s->qa_dim, s->qd_dim, NULL, s->x, D->attn_norm, c->dim, c->norm_eps, 1);
+        krh_matvec_qkv(s->q, kc, vc, &D->wq, &D->wk, &D->wv, D->bq, D->bk, D->bv, s->qa_dim, s->qd_dim, cs, sn,
+                       c->head_dim, s->pos);
+        krh_attention(s->ao, s->qa_q, s->qd_q, s->att, s->q, kc, vc, c->n_heads, c->n_kv_heads, c->head_dim,
+                      c->max_seq, L->window, c->attn_scale, s->pos);
+        krh_matvec(s->x, &D->wo, s->qa_q, s->qd_q, 1);
+        krh_rmsnorm_q8(s->qa_dim, s->qd_dim, NULL, s->x, D->ffn_norm, c->dim, c->norm_eps, 1);
+        krh_matvec_swiglu_q8(s->qa_hid, s->qd_hid, NULL, &D->w1, &D->w3, s->qa_dim, s->qd_dim);
+        krh_matvec(s->x, &D->w2, s->qa_hid, s->qd_hid, 1);
+    }
+    if (!cls) return;
+    krh_rmsnorm_q8(s->qa_dim, s->qd_dim, NULL, s->x, m->d_final_norm, c->dim, c->norm_eps, 1);
+    krh_matvec(s->logits, &m->d_wcls, s->qa_dim, s->qd_dim, 0);
+}
+
+static ml_status capture(kr_state *s, krh_graph **g, int kind) {
+    ml_status st = krh_graph_begin();
+    if (st != ML_OK) return kr_seterr(st, "%s", krh_last_error());
+    if (kind == 2) krh_take_token(s->tok, s->prompt, s->pos);
+    issue_step(s, kind != 2);
+    if (kind == 1) krh_argmax(s->tok, s->logits, s->m->cfg.vocab, s->pos, s->log);
+    if (kind == 2) krh_advance(s->pos);
+    st = krh_graph_end(g);
+    return st == ML_OK ? ML_OK : kr_seterr(st, "%s", krh_last_error());
+}
+
+ml_status kr_state_new(kr_state **out, kr_model *m, int kv_type) {
+    *out = NULL;
+    const ml_config *c = &m->cfg;
+    if (kv_type != ML_F32) return kr_seterr(ML_E_SHAPE, "only the F32 KV cache is supported");
+    if (c->qk_norm || c->post_norms || c->act != ML_ACT_SILU || c->attn_softcap > 0.0f || c->final_softcap > 0.0f)
+        return kr_seterr(ML_E_SHAPE, "model uses q/k norm, post-norms, GELU or soft-capping: not supported");
+    ml_status st = kr_model_upload(m);
+    if (st != ML_OK) return st;
+    kr_state *s = calloc(1, sizeof *s);
+    if (!s) return ML_E_NOMEM;
+    s->m = m;
+    const size_t f = sizeof(float), kv = (size_t)c->n_layers * c->max_seq * c->kv_dim;
+    const size_t half = (size_t)c->max_seq * (c->head_dim / 2);
+    const int local = c->rope_local_theta > 0.0f;
+    struct { void **p; size_t n; } parts[] = {
+        { (void **)&s->x, f * c->dim }, { (void **)&s->q, f * c->q_dim }, { (void **)&s->ao, f * c->q_dim },
+        { (void **)&s->att, f * (size_t)c->n_heads * c->max_seq }, { (void **)&s->logits, f * c->vocab },
+        { (void **)&s->kcache, f * kv }, { (void **)&s->vcache, f * kv },
+        { (void **)&s->rope_cos, f * half }, { (void **)&s->rope_sin, f * half },
+        { (void **)&s->rope_cos_l, local ? f * half : 0 }, { (void **)&s->rope_sin_l, local ? f * half : 0 },
+        { (void **)&s->qa_dim, (size_t)c->dim }, { (void **)&s->qd_dim, f * c->dim / QK },
+        { (void **)&s->qa_q, (size_t)c->q_dim }, { (void **)&s->qd_q, f * c->q_dim / QK },
+        { (void **)&s->qa_hid, (size_t)c->hidden_dim }, { (void **)&s->qd_hid, f * c->hidden_dim / QK },
+        { (void **)&s->tok, sizeof(int) }, { (void **)&s->pos, sizeof(int) },
+        { (void **)&s->prompt, sizeof(int) * ((size_t)c->max_seq + 1) },
+        { (void **)&s->log, sizeof(int) * ((size_t)c->max_seq + 2) },
+    };
+    const int np = (int)(sizeof parts / sizeof parts[0]);
+    size_t total = 0;
+    for (int i = 0; i < np; i++) total += RUP(parts[i].n);
+    s->mem = krh_alloc(total);
+    s->h_logits = krh_host_alloc(f * c->vocab);
+    s->h_ints = krh_host_alloc(sizeof(int) * 4);
+    if (!s->mem || !s->h_logits || !s->h_ints) {
+        kr_state_free(s);
+        return kr_seterr(ML_E_NOMEM, "cannot allocate the decoding state (%zu bytes of HBM)", total);
+    }
+    size_t off = 0;
+    for (int i = 0; i < np; i++) {
+        *parts[i].p = parts[i].n ? (uint8_t *)s->mem + off : NULL;
+        off += RUP(parts[i].n);
+    }
+    float *cs = malloc(f * half), *sn = malloc(f * half);
+    float *csl = local ? malloc(f * half) : NULL, *snl = local ? malloc(f * half) : NULL;
+    if (!cs || !sn || (local && (!csl || !snl))) {
+        free(cs); free(sn); free(csl); free(snl);
+        kr_state_free(s);
+        return ML_E_NOMEM;
+    }
+    rope_tables(c, cs, sn, csl, snl);
+    st = krh_copy_h2d(s->rope_cos, cs, f * half);
+    if (st == ML_OK) st = krh_copy_h2d(s->rope_sin, sn, f * half);
+    if (st == ML_OK && local) st = krh_copy_h2d(s->rope_cos_l, csl, f * half);
+    if (st == ML_OK && local) st = krh_copy_h2d(s->rope_sin_l, snl, f * half);
+    free(cs); free(sn); free(csl); free(snl);
+    if (st == ML_OK) st = capture(s, &s->g_logits, 0);
+    if (st == ML_OK) st = capture(s, &s->g_greedy, 1);
+    if (st == ML_OK) st = capture(s, &s->g_prefill, 2);
+    if (st != ML_OK) {
+        kr_state_free(s);
+        return kr_seterr(st, "%s", krh_last_error());
+    }
+    *out = s;
+    return ML_OK;
+}
+
+void kr_state_free(kr_state *s) {
+    if (!s) return;
+    krh_graph_free(s->g_logits);
+    krh_graph_free(s->g_greedy);
+    krh_graph_free(s->g_prefill);
+    krh_free(s->mem);
+    krh_host_free(s->h_logits);
+    krh_host_free(s->h_ints);
+    free(s);
+}
+
+void kr_state_set_batch(kr_state *s, int batch) { s->batch = batch; }
+const float *kr_state_x_device(const kr_state *s) { return s->x; }
+
+const void *kr_state_buffer(const kr_state *s, const char *name) {
+    static const char *const names[] = { "x", "q", "ao", "att", "logits", "kcache", "vcache", "rope_cos",
+                                         "rope_sin", "qa_dim", "qd_dim", "qa_q", "qd_q", "qa_hid", "qd_hid" };
+    const void *ptrs[] = { s->x, s->q, s->ao, s->att, s->logits, s->kcache, s->vcache, s->rope_cos,
+                           s->rope_sin, s->qa_dim, s->qd_dim, s->qa_q, s->qd_q, s->qa_hid, s->qd_hid };
+    for (size_t i = 0; i < sizeof names / sizeof names[0]; i++)
+        if (!strcmp(names[i], name)) return ptrs[i];
+    return NULL;
+}
+
+static ml_status set_ints(kr_state *s, int tok, int pos) {
+    s->h_ints[0] = tok;
+    s->h_ints[1] = pos;
+    ml_status st = krh_copy_h2d(s->tok, &s->h_ints[0], sizeof(int));
+    if (st == ML_OK) st = krh_copy_h2d(s->pos, &s->h_ints[1], sizeof(int));
+    return st;
+}
+
+static ml_status dev_status(void) {
+    const ml_status st = krh_sync();
+    return st == ML_OK ? ML_OK : kr_seterr(st, "%s", krh_last_error());
+}
+
+ml_status kr_forward(kr_state *s, int token, int pos, float *logits) {
+    const ml_config *c = &s->m->cfg;
+    if (pos < 0 || pos >= c->max_seq || token < 0 || token >= c->vocab) return ML_E_SHAPE;
+    ml_status st = set_ints(s, token, pos);
+    if (st == ML_OK) st = krh_graph_launch(s->g_logits);
+    if (st == ML_OK && logits) st = krh_copy_d2h(logits, s->logits, sizeof(float) * c->vocab);
+    return st == ML_OK ? dev_status() : st;
+}
+
+/* Batched prefill computes every per-token op in ml_forward's order
+ * (model/transformer.c:381-384); here each prompt token replays the step. */
+ml_status kr_prefill(kr_state *s, const int *tokens, int n, int pos0, float *logits) {
+    const ml_config *c = &s->m->cfg;
+    if (n < 0 || pos0 < 0 || pos0 + n > c->max_seq) return ML_E_SHAPE;
+    for (int i = 0; i < n; i++)
+        if (tokens[i] < 0 || tokens[i] >= c->vocab) return ML_E_SHAPE;
+    if (logits) {
+        for (int i = 0; i < n; i++) {
+            const ml_status st = kr_forward(s, tokens[i], pos0 + i, logits + (size_t)i * c->vocab);
+            if (st != ML_OK) return st;
+        }
+        return ML_OK;
+    }
+    if (n == 0) return ML_OK;
+    ml_status st = krh_copy_h2d(s->prompt + pos0, tokens, sizeof(int) * (size_t)n);
+    if (st == ML_OK) st = set_ints(s, 0, pos0);
+    for (int i = 0; st == ML_OK && i < n; i++) st = krh_graph_launch(s->g_prefill);
+    return st == ML_OK ? dev_status() : st;
+}
+
+int kr_generate(kr_state *s, const int *prompt, int np, int steps, int *out, double *prefill_s, double *decode_s) {
+    const ml_config *c = &s->m->cfg;
+    if (np < 1 || np > c->max_seq || steps < 1) return -1;
+    if (steps > c->max_seq) steps = c->max_seq;
+    int n = 0, pos = 0, token = prompt[0];
+    const int npre = np - 1 < steps - 1 ? np - 1 : steps - 1;
+    double t0 = kr_now();
+    if (npre > 0) {
+        if (kr_prefill(s, prompt, npre, 0, NULL) != ML_OK) return -1;
+        for (pos = 0; pos < npre; pos++) out[n++] = prompt[pos + 1];
+        token = prompt[npre];
+    }
+    const double t1 = kr_now();
+    if (prefill_s) *prefill_s = t1 - t0;
+    /* positions where ml_run takes the next id from the prompt (only when
+     * the prompt is longer than steps) run one at a time */
+    while (pos < steps && pos + 1 < np) {
+        if (kr_forward(s, token, pos, NULL) != ML_OK) return -1;
+        token = prompt[pos + 1];
+        out[n++] = token;
+        pos++;
+    }
+    if (pos < steps) {
+        const int first = pos;
+        if (set_ints(s, token, pos) != ML_OK) return -1;
+        for (; pos < steps; pos++)
+            if (krh_graph_launch(s->g_greedy) != ML_OK) return -1;
+        if (dev_status() != ML_OK) return -1;
+        if (krh_copy_d2h(out + n, s->log + first + 1, sizeof(int) * (size_t)(steps - first)) != ML_OK) return -1;
+        n += steps - first;
+    }
+    if (decode_s) *decode_s = kr_now() - t1;
+    return n;
+}

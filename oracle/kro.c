@@ -1,0 +1,463 @@
+/* ORACLE — test infrastructure only. Scalar restatement of the reference's
+ * kernels (kernels/scalar/k_scalar.c), attention order (ops/ops.c) and forward
+ * pass (model/transformer.c). Compiled with -ffp-contract=off like the
+ * reference's scalar build, so every float operation rounds where the
+ * reference's does. */
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+#include "kro.h"
+
+/* core/ml.c:39-53 */
+uint16_t kro_f32_to_f16(float f) {
+    uint32_t x;
+    memcpy(&x, &f, 4);
+    const uint16_t sign = (uint16_t)((x >> 16) & 0x8000);
+    x &= 0x7fffffff;
+    if (x > 0x7f800000) return sign | 0x7e00;
+    if (x >= 0x477ff000) return sign | 0x7c00;
+    if (x < 0x38800000) {
+        float a;
+        memcpy(&a, &x, 4);
+        return sign | (uint16_t)lrintf(a * 16777216.0f);
+    }
+    x += 0xfff + ((x >> 13) & 1);
+    return sign | (uint16_t)((x >> 13) - (112u << 10));
+}
+
+/* core/ml.c:55-62 */
+float kro_f16_to_f32(uint16_t h) {
+    const uint32_t sign = (uint32_t)(h & 0x8000) << 16, e = (h >> 10) & 0x1f, m = h & 0x3ff;
+    if (e == 0) return (sign ? -1.0f : 1.0f) * (float)m * (1.0f / 16777216.0f);
+    const uint32_t x = sign | (e == 31 ? 0x7f800000u | (m << 13) : ((e + 112u) << 23) | (m << 13));
+    float f;
+    memcpy(&f, &x, 4);
+    return f;
+}
+
+/* k_scalar.c:4-17: per row, int32 block dot, then sum += (float)s * wd * xd
+ * in block order */
+void kro_matvec_q8(float *y, const ml_qtensor *W, const ml_qact *x, int r0, int r1) {
+    const int nb = W->cols / QK;
+    for (int r = r0; r < r1; r++) {
+        const int8_t *wq = W->q + (size_t)r * W->cols;
+        const float *wd = W->d + (size_t)r * nb;
+        float sum = 0.0f;
+        for (int b = 0; b < nb; b++) {
+            int32_t s = 0;
+            for (int j = 0; j < QK; j++) s += wq[b * QK + j] * x->q[b * QK + j];
+            const float t = (float)s * wd[b];
+            sum = sum + t * x->d[b];
+        }
+        y[r] = sum;
+    }
+}
+
+/* k_scalar.c:19-37: byte j of a block holds elements j (low) and j+16 (high) */
+void kro_matvec_q4(float *y, const ml_qtensor *W, const ml_qact *x, int r0, int r1) {
+    const int nb = W->cols / QK;
+    for (int r = r0; r < r1; r++) {
+        const uint8_t *wq = (const uint8_t *)W->q + (size_t)r * nb * (QK / 2);
+        const float *wd = W->d + (size_t)r * nb;
+        float sum = 0.0f;
+        for (int b = 0; b < nb; b++) {
+            const uint8_t *p = wq + b * (QK / 2);
+            const int8_t *xq = x->q + b * QK;
+            int32_t s = 0;
+            for (int j = 0; j < QK / 2; j++) {
+                s += ((p[j] & 0xF) - 8) * xq[j];
+                s += ((p[j] >> 4) - 8) * xq[j + QK / 2];
+            }
+            const float t = (float)s * wd[b];
+            sum = sum + t * x->d[b];
+        }
+        y[r] = sum;
+    }
+}
+
+void kro_block_dots(int32_t *s, const ml_qtensor *W, const ml_qact *x, int r0, int r1) {
+    const int nb = W->cols / QK;
+    for (int r = r0; r < r1; r++)
+        for (int b = 0; b < nb; b++) {
+            int32_t acc = 0;
+            if (W->type == ML_Q8_0) {
+                const int8_t *wq = W->q + (size_t)r * W->cols + b * QK;
+                for (int j = 0; j < QK; j++) acc += wq[j] * x->q[b * QK + j];
+            } else {
+                const uint8_t *p = (const uint8_t *)W->q + ((size_t)r * nb + b) * (QK / 2);
+                for (int j = 0; j < QK / 2; j++)
+                    acc += ((p[j] & 0xF) - 8) * x->q[b * QK + j] + ((p[j] >> 4) - 8) * x->q[b * QK + j + QK / 2];
+            }
+            s[(size_t)(r - r0) * nb + b] = acc;
+        }
+}
+
+/* k_scalar.c:39-57 and the rule in docs/file-format.md:133-144 */
+void kro_quantize_q8(ml_qact *out, const float *x, int k) {
+    for (int b = 0; b < k / QK; b++) {
+        const float *xb = x + b * QK;
+        float amax = 0.0f;
+        for (int j = 0; j < QK; j++) amax = fmaxf(amax, fabsf(xb[j]));
+        if (amax < ML_QUANT_TINY) {
+            out->d[b] = 0.0f;
+            for (int j = 0; j < QK; j++) out->q[b * QK + j] = 0;
+            continue;
+        }
+        const float id = 127.0f / amax;
+        out->d[b] = amax / 127.0f;
+        for (int j = 0; j < QK; j++) {
+            const float m = xb[j] * id;
+            float v = truncf(m + copysignf(0.5f, xb[j]));
+            v = fminf(fmaxf(v, -127.0f), 127.0f);
+            out->q[b * QK + j] = (int8_t)v;
+        }
+    }
+}
+
+/* k_scalar.c:59-64: sequential sum of squares, then (x * inv) * w */
+void kro_rmsnorm(float *o, const float *x, const float *w, int n, float eps) {
+    float ss = 0.0f;
+    for (int i = 0; i < n; i++) ss = ss + x[i] * x[i];
+    const float inv = 1.0f / sqrtf(ss / (float)n + eps);
+    for (int i = 0; i < n; i++) o[i] = x[i] * inv * w[i];
+}
+
+/* k_scalar.c:66-77 */
+void kro_softmax(float *x, int n) {
+    float mx = x[0];
+    for (int i = 1; i < n; i++) mx = fmaxf(mx, x[i]);
+    if (mx == -INFINITY) {
+        for (int i = 0; i < n; i++) x[i] = 1.0f / (float)n;
+        return;
+    }
+    float sum = 0.0f;
+    for (int i = 0; i < n; i++) { x[i] = kro_expf(x[i] - mx); sum = sum + x[i]; }
+    const float inv = 1.0f / sum;
+    for (int i = 0; i < n; i++) x[i] *= inv;
+}
+
+/* k_scalar.c:79-94: interleaved pairs (2i, 2i+1) of every head */
+static void rope_heads(float *v, const float *c, const float *s, int hd, int nh) {
+    for (int h = 0; h < nh; h++) {
+        float *p = v + h * hd;
+        for (int i = 0; i < hd / 2; i++) {
+            const float a = p[2 * i], b = p[2 * i + 1];
+            p[2 * i] = a * c[i] - b * s[i];
+            p[2 * i + 1] = a * s[i] + b * c[i];
+        }
+    }
+}
+
+void kro_rope(float *q, float *k, const float *cos_t, const float *sin_t, int head_dim, int n_heads, int n_kv_heads) {
+    rope_heads(q, cos_t, sin_t, head_dim, n_heads);
+    rope_heads(k, cos_t, sin_t, head_dim, n_kv_heads);
+}
+
+/* k_scalar.c:96-98: g / (1 + expf(-g)) * u */
+void kro_silu_mul(float *g, const float *u, int n) {
+    for (int i = 0; i < n; i++) g[i] = g[i] / (1.0f + kro_expf(-g[i])) * u[i];
+}
+
+/* k_scalar.c:107-109 */
+void kro_add(float *y, const float *x, int n) {
+    for (int i = 0; i < n; i++) y[i] += x[i];
+}
+
+/* k_scalar.c:111-117 */
+void kro_dot_f32(float *s, const float *q, const float *k, size_t ldk, int rows, int n, float scale) {
+    for (int t = 0; t < rows; t++, k += ldk) {
+        float acc = 0.0f;
+        for (int i = 0; i < n; i++) acc = acc + q[i] * k[i];
+        s[t] = acc * scale;
+    }
+}
+
+/* k_scalar.c:119-122 */
+void kro_axpy_f32(float *y, const float *a, const float *x, size_t ldx, int rows, int n) {
+    for (int t = 0; t < rows; t++, x += ldx)
+        for (int i = 0; i < n; i++) y[i] = y[i] + a[t] * x[i];
+}
+
+/* core/quant_ref.c:4-19 */
+void kro_dequant_row(float *out, const ml_qtensor *W, int row) {
+    const int nb = W->cols / QK;
+    const float *d = W->d + (size_t)row * nb;
+    if (W->type == ML_Q8_0) {
+        const int8_t *q = W->q + (size_t)row * W->cols;
+        for (int i = 0; i < W->cols; i++) out[i] = q[i] * d[i / QK];
+        return;
+    }
+    const uint8_t *q = (const uint8_t *)W->q + (size_t)row * nb * (QK / 2);
+    for (int b = 0; b < nb; b++)
+        for (int j = 0; j < QK / 2; j++) {
+            const uint8_t v = q[b * (QK / 2) + j];
+            out[b * QK + j] = ((v & 0xF) - 8) * d[b];
+            out[b * QK + j + QK / 2] = ((v >> 4) - 8) * d[b];
+        }
+}
+
+/* core/quant_ref.c:21-38 (the amax/7 rule) */
+void kro_quantize_row_q4(int8_t *q, float *d, const float *x, int k) {
+    for (int b = 0; b < k / QK; b++) {
+        const float *xb = x + b * QK;
+        float amax = 0.0f;
+        for (int j = 0; j < QK; j++) amax = fmaxf(amax, fabsf(xb[j]));
+        if (amax < ML_QUANT_TINY) amax = 0.0f;
+        const float id = amax != 0.0f ? 7.0f / amax : 0.0f;
+        d[b] = amax / 7.0f;
+        uint8_t nib[QK];
+        for (int j = 0; j < QK; j++) {
+            const float m = xb[j] * id;
+            float v = truncf(m + copysignf(0.5f, xb[j]));
+            v = fminf(fmaxf(v, -8.0f), 7.0f);
+            nib[j] = (uint8_t)((int)v + 8);
+        }
+        for (int j = 0; j < QK / 2; j++) q[b * (QK / 2) + j] = (int8_t)(nib[j] | (nib[j + QK / 2] << 4));
+    }
+}
+
+/* model/sampler.c:57-61: first index of the maximum */
+int kro_argmax(const float *v, int n) {
+    int best = 0;
+    for (int i = 1; i < n; i++) if (v[i] > v[best]) best = i;
+    return best;
+}
+
+/* ops/ops.c:169-200 (attend) for the F32 cache, one query head at a time:
+ * the 64-position blocks and head grouping of the reference leave each head's
+ * operation order as written here (scores per position, softmax over the
+ * positions attended, then the V rows added in position order). */
+void kro_attention(float *out, const float *q, const ml_kv_layer *kv, float *att, const ml_config *cfg, int pos) {
+    const int hd = cfg->head_dim, group = cfg->n_heads / cfg->n_kv_heads;
+    const int first = kv->window && pos >= kv->window ? pos + 1 - kv->window : 0;
+    const int n = pos + 1 - first;
+    const size_t ld = (size_t)cfg->kv_dim;
+    for (int h = 0; h < cfg->n_heads; h++) {
+        const size_t off = (size_t)(h / group) * hd + (size_t)first * ld;
+        kro_dot_f32(att, q + (size_t)h * hd, kv->k + off, ld, n, hd, cfg->attn_scale);
+        kro_softmax(att, n);
+        float *o = out + (size_t)h * hd;
+        for (int i = 0; i < hd; i++) o[i] = 0.0f;
+        kro_axpy_f32(o, att, kv->v + off, ld, n, hd);
+    }
+}
+
+/* ---- model ---- */
+
+struct kro_model_data;   /* kro_mlb.c */
+int kro_mlb_open(kro_model **m, const char *path);
+void kro_mlb_close(kro_model *m);
+const ml_config *kro_mlb_config(const kro_model *m);
+const ml_qtensor *kro_mlb_tok_emb(const kro_model *m);
+const ml_qtensor *kro_mlb_wcls(const kro_model *m);
+const float *kro_mlb_final_norm(const kro_model *m);
+const ml_layer *kro_mlb_layer(const kro_model *m, int l);
+
+int kro_model_open(kro_model **m, const char *path) { return kro_mlb_open(m, path); }
+void kro_model_close(kro_model *m) { kro_mlb_close(m); }
+const ml_config *kro_model_config(const kro_model *m) { return kro_mlb_config(m); }
+
+struct kro_state {
+    const kro_model *m;
+    float *x, *xb, *xb2, *hb, *hb2, *q, *ao, *att, *logits;
+    float *kcache, *vcache;
+    float *rope_cos, *rope_sin, *rope_cos_local, *rope_sin_local;
+    ml_qact qa_dim, qa_hidden, qa_q;
+};
+
+/* model/transformer.c:16-38 */
+static double rope_inv_freq(const ml_config *c, int i) {
+    const double inv = pow((double)c->rope_theta, -2.0 * i / c->head_dim);
+    if (c->rope_type == ML_ROPE_LINEAR) return inv / c->rope_factor;
+    if (c->rope_type == ML_ROPE_YARN) {
+        const double hd = c->head_dim, orig = c->rope_orig_max_seq, lb = 2.0 * log((double)c->rope_theta);
+        const double pi2 = 2.0 * 3.14159265358979323846;
+        double lo = floor(hd * log(orig / ((double)c->rope_low_freq_factor * pi2)) / lb);
+        double hi = ceil(hd * log(orig / ((double)c->rope_high_freq_factor * pi2)) / lb);
+        if (lo < 0.0) lo = 0.0;
+        if (hi > hd - 1.0) hi = hd - 1.0;
+        if (lo == hi) hi += 0.001;
+        double ramp = (i - lo) / (hi - lo);
+        ramp = ramp < 0.0 ? 0.0 : (ramp > 1.0 ? 1.0 : ramp);
+        return inv / c->rope_factor * ramp + inv * (1.0 - ramp);
+    }
+    if (c->rope_type != ML_ROPE_LLAMA3) return inv;
+    const double f = c->rope_factor, lo = c->rope_low_freq_factor, hi = c->rope_high_freq_factor;
+    const double orig = c->rope_orig_max_seq, wavelen = 2.0 * 3.14159265358979323846 / inv;
+    if (wavelen < orig / hi) return inv;
+    if (wavelen > orig / lo) return inv / f;
+    const double smooth = (orig / wavelen - lo) / (hi - lo);
+    return (1.0 - smooth) * inv / f + smooth * inv;
+}
+
+int kro_state_new(kro_state **out, const kro_model *m) {
+    const ml_config *c = kro_mlb_config(m);
+    if (c->act != ML_ACT_SILU || c->attn_softcap > 0.0f || c->final_softcap > 0.0f) return ML_E_SHAPE;
+    kro_state *s = calloc(1, sizeof *s);
+    if (!s) return ML_E_NOMEM;
+    s->m = m;
+    const size_t f = sizeof(float), kv = (size_t)c->n_layers * c->max_seq * c->kv_dim;
+    const size_t half = (size_t)c->max_seq * (c->head_dim / 2);
+    s->x = calloc(c->dim, f); s->xb = calloc(c->dim, f); s->xb2 = calloc(c->dim, f);
+    s->hb = calloc(c->hidden_dim, f); s->hb2 = calloc(c->hidden_dim, f);
+    s->q = calloc(c->q_dim, f); s->ao = calloc(c->q_dim, f);
+    s->att = calloc(c->max_seq, f); s->logits = calloc(c->vocab, f);
+    s->kcache = calloc(kv, f); s->vcache = calloc(kv, f);
+    s->rope_cos = calloc(half, f); s->rope_sin = calloc(half, f);
+    s->qa_dim = (ml_qact){ malloc(c->dim), malloc(f * c->dim / QK), c->dim };
+    s->qa_hidden = (ml_qact){ malloc(c->hidden_dim), malloc(f * c->hidden_dim / QK), c->hidden_dim };
+    s->qa_q = (ml_qact){ malloc(c->q_dim), malloc(f * c->q_dim / QK), c->q_dim };
+    if (c->rope_local_theta > 0.0f) { s->rope_cos_local = calloc(half, f); s->rope_sin_local = calloc(half, f); }
+    if (!s->kcache || !s->vcache || !s->rope_sin || !s->qa_q.d || (c->rope_local_theta > 0.0f && !s->rope_sin_local)) {
+        kro_state_free(s);
+        return ML_E_NOMEM;
+    }
+    /* model/transformer.c:147-162 */
+    const int h2 = c->head_dim / 2;
+    const double af = c->rope_type == ML_ROPE_YARN ? c->rope_attn_factor : 1.0;
+    for (int i = 0; i < h2; i++) {
+        const double freq = rope_inv_freq(c, i);
+        const double lfreq = s->rope_cos_local ? pow((double)c->rope_local_theta, -2.0 * i / c->head_dim) : 0.0;
+        for (int p = 0; p < c->max_seq; p++) {
+            const double ang = p * freq;
+            s->rope_cos[(size_t)p * h2 + i] = (float)(cos(ang) * af);
+            s->rope_sin[(size_t)p * h2 + i] = (float)(sin(ang) * af);
+            if (s->rope_cos_local) {
+                s->rope_cos_local[(size_t)p * h2 + i] = (float)cos(p * lfreq);
+                s->rope_sin_local[(size_t)p * h2 + i] = (float)sin(p * lfreq);
+            }
+        }
+    }
+    *out = s;
+    return ML_OK;
+}
+
+void kro_state_free(kro_state *s) {
+    if (!s) return;
+    free(s->x); free(s->xb); free(s->xb2); free(s->hb); free(s->hb2); free(s->q); free(s->ao);
+    free(s->att); free(s->logits); free(s->kcache); free(s->vcache);
+    free(s->rope_cos); free(s->rope_sin); free(s->rope_cos_local); free(s->rope_sin_local);
+    free(s->qa_dim.q); free(s->qa_dim.d); free(s->qa_hidden.q); free(s->qa_hidden.d);
+    free(s->qa_q.q); free(s->qa_q.d);
+    free(s);
+}
+
+static void matvec(float *y, const ml_qtensor *W, const ml_qact *x) {
+    if (W->type == ML_Q8_0) kro_matvec_q8(y, W, x, 0, W->rows);
+    else kro_matvec_q4(y, W, x, 0, W->rows);
+}
+
+/* model/transformer.c:240-243 */
+static void residual_add(const ml_config *c, float *x, float *y, const float *post_norm) {
+    if (post_norm) kro_rmsnorm(y, y, post_norm, c->dim, c->norm_eps);
+    kro_add(x, y, c->dim);
+}
+
+/* model/transformer.c:246-248 */
+static void heads_norm(float *x, const float *w, int n, const ml_config *c) {
+    for (int h = 0; h < n; h++) kro_rmsnorm(x + (size_t)h * c->head_dim, x + (size_t)h * c->head_dim, w, c->head_dim, c->norm_eps);
+}
+
+/* model/transformer.c:257-306 with the F32 cache; `cls` = run the classifier */
+static void forward(kro_state *s, int token, int pos, int cls) {
+    const kro_model *m = s->m;
+    const ml_config *c = kro_mlb_config(m);
+    kro_dequant_row(s->x, kro_mlb_tok_emb(m), token);
+    if (c->embed_scale != 1.0f)
+        for (int i = 0; i < c->dim; i++) s->x[i] *= c->embed_scale;
+    for (int l = 0; l < c->n_layers; l++) {
+        const ml_layer *L = kro_mlb_layer(m, l);
+        const size_t row = (size_t)l * c->max_seq;
+        float *k = s->kcache + (row + pos) * c->kv_dim, *v = s->vcache + (row + pos) * c->kv_dim;
+        const size_t ro = (size_t)pos * (c->head_dim / 2);
+        const float *cs = (L->local_rope ? s->rope_cos_local : s->rope_cos) + ro;
+        const float *sn = (L->local_rope ? s->rope_sin_local : s->rope_sin) + ro;
+        kro_rmsnorm(s->xb, s->x, L->attn_norm, c->dim, c->norm_eps);
+        kro_quantize_q8(&s->qa_dim, s->xb, c->dim);
+        matvec(s->q, &L->wq, &s->qa_dim);
+        matvec(k, &L->wk, &s->qa_dim);
+        matvec(v, &L->wv, &s->qa_dim);
+        if (L->bq) { kro_add(s->q, L->bq, c->q_dim); kro_add(k, L->bk, c->kv_dim); kro_add(v, L->bv, c->kv_dim); }
+        if (L->q_norm) { heads_norm(s->q, L->q_norm, c->n_heads, c); heads_norm(k, L->k_norm, c->n_kv_heads, c); }
+        kro_rope(s->q, k, cs, sn, c->head_dim, c->n_heads, c->n_kv_heads);
+        const ml_kv_layer kv = { s->kcache + row * c->kv_dim, s->vcache + row * c->kv_dim, NULL, NULL, NULL, NULL,
+                                 L->window, NULL, NULL };
+        kro_attention(s->ao, s->q, &kv, s->att, c, pos);
+        kro_quantize_q8(&s->qa_q, s->ao, c->q_dim);
+        matvec(s->xb2, &L->wo, &s->qa_q);
+        residual_add(c, s->x, s->xb2, L->post_attn_norm);
+        kro_rmsnorm(s->xb, s->x, L->ffn_norm, c->dim, c->norm_eps);
+        kro_quantize_q8(&s->qa_dim, s->xb, c->dim);
+        matvec(s->hb, &L->w1, &s->qa_dim);
+        matvec(s->hb2, &L->w3, &s->qa_dim);
+        kro_silu_mul(s->hb, s->hb2, c->hidden_dim);
+        kro_quantize_q8(&s->qa_hidden, s->hb, c->hidden_dim);
+        matvec(s->xb2, &L->w2, &s->qa_hidden);
+        residual_add(c, s->x, s->xb2, L->post_ffn_norm);
+    }
+    if (!cls) return;
+    kro_rmsnorm(s->xb, s->x, kro_mlb_final_norm(m), c->dim, c->norm_eps);
+    kro_quantize_q8(&s->qa_dim, s->xb, c->dim);
+    matvec(s->logits, kro_mlb_wcls(m), &s->qa_dim);
+}
+
+int kro_forward(kro_state *s, int token, int pos, float *out) {
+    const ml_config *c = kro_mlb_config(s->m);
+    if (pos < 0 || pos >= c->max_seq || token < 0 || token >= c->vocab) return ML_E_SHAPE;
+    forward(s, token, pos, 1);
+    if (out) memcpy(out, s->logits, sizeof(float) * c->vocab);
+    return ML_OK;
+}
+
+/* Batched prefill computes every per-token operation in ml_forward's order
+ * (model/transformer.c:381-384), so it is token-by-token forward here. */
+int kro_prefill(kro_state *s, const int *tokens, int n, int pos0, float *logits) {
+    const ml_config *c = kro_mlb_config(s->m);
+    if (n < 0 || pos0 < 0 || pos0 + n > c->max_seq) return ML_E_SHAPE;
+    for (int i = 0; i < n; i++)
+        if (tokens[i] < 0 || tokens[i] >= c->vocab) return ML_E_SHAPE;
+    for (int i = 0; i < n; i++) {
+        forward(s, tokens[i], pos0 + i, logits != NULL);
+        if (logits) memcpy(logits + (size_t)i * c->vocab, s->logits, sizeof(float) * c->vocab);
+    }
+    return ML_OK;
+}
+
+/* app/ml_run.c:369-404 with -T 0 (greedy) and no --eos */
+int kro_generate(kro_state *s, const int *prompt, int np, int steps, int *out) {
+    const ml_config *c = kro_mlb_config(s->m);
+    if (np < 1 || np > c->max_seq) return -1;
+    if (steps > c->max_seq) steps = c->max_seq;
+    int token = prompt[0], pos = 0, n = 0;
+    const int npre = np - 1 < steps - 1 ? np - 1 : steps - 1;
+    if (npre > 0) {
+        if (kro_prefill(s, prompt, npre, 0, NULL) != ML_OK) return -1;
+        for (pos = 0; pos < npre; pos++) out[n++] = prompt[pos + 1];
+        token = prompt[npre];
+    }
+    while (pos < steps) {
+        forward(s, token, pos, 1);
+        const int next = pos + 1 >= np ? kro_argmax(s->logits, c->vocab) : prompt[pos + 1];
+        pos++;
+        out[n++] = next;
+        token = next;
+    }
+    return n;
+}
+
+const float *kro_state_x(const kro_state *s) { return s->x; }
+const float *kro_state_kcache(const kro_state *s, int layer) {
+    const ml_config *c = kro_mlb_config(s->m);
+    return s->kcache + (size_t)layer * c->max_seq * c->kv_dim;
+}
+
+const float *kro_state_buffer(const kro_state *s, const char *name) {
+    if (!strcmp(name, "x")) return s->x;
+    if (!strcmp(name, "q")) return s->q;
+    if (!strcmp(name, "ao")) return s->ao;
+    if (!strcmp(name, "kcache")) return s->kcache;
+    if (!strcmp(name, "vcache")) return s->vcache;
+    if (!strcmp(name, "rope_cos")) return s->rope_cos;
+    if (!strcmp(name, "rope_sin")) return s->rope_sin;
+    return NULL;
+}

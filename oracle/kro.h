@@ -1,0 +1,84 @@
+/* ORACLE — test infrastructure only. A plain-C restatement of the reference's
+ * scalar token loop, used by tests/ as the checker of the HIP path and by
+ * bench.py's cpu_baseline leg. Nothing in the product links or calls it.
+ *
+ * Every function follows the reference's scalar build in float operation
+ * order (it is compiled with -ffp-contract=off, as the reference is,
+ * Makefile:18-22), so its results are the reference's bit for bit. Each
+ * definition cites the reference file:line it restates.
+ *
+ * Pinning (what checks each part; see tests/test_oracle.py):
+ *   kro_expf             exhaustively equal to the host libm expf (all 2^32
+ *                        inputs) -- the reference calls glibc's expf
+ *   kernels              bit-equal to oracle/_ref/libkrafla_ref_scalar.so on
+ *                        seeded inputs, plus the reference's known answers
+ *                        (tests/test_quant.c:47-70, tests/test_sampler.c:33-40)
+ *                        and closed forms (unit-scale matvec = exact int sum)
+ *   kro_forward/prefill  logits bit-equal to oracle/_ref/scalar/ml_run
+ *                        --dump-logits on generated .mlb models
+ */
+#ifndef KRO_H
+#define KRO_H
+#include "../include/krafla_types.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+float kro_expf(float x);
+/* counts inputs in [lo, hi) (as uint32 bit patterns) where kro_expf differs
+ * from the C library's expf; threads > 1 splits the range */
+uint64_t kro_expf_mismatches(uint64_t lo, uint64_t hi, int threads);
+/* counts i < n where got[i] differs in bits from expf(x[i]) of the C library */
+uint64_t kro_expf_check(const float *x, const float *got, size_t n);
+
+/* the same over got[i] = device expf of the input with bits lo + i */
+uint64_t kro_expf_check_range(uint64_t lo, const float *got, size_t n, int threads);
+
+uint16_t kro_f32_to_f16(float f);
+float kro_f16_to_f32(uint16_t h);
+
+/* kernels: same signatures and semantics as kernels/scalar/k_scalar.h:7-24 */
+void kro_matvec_q8(float *y, const ml_qtensor *W, const ml_qact *x, int r0, int r1);
+void kro_matvec_q4(float *y, const ml_qtensor *W, const ml_qact *x, int r0, int r1);
+void kro_quantize_q8(ml_qact *out, const float *x, int k);
+void kro_rmsnorm(float *o, const float *x, const float *w, int n, float eps);
+void kro_softmax(float *x, int n);
+void kro_rope(float *q, float *k, const float *cos_t, const float *sin_t, int head_dim, int n_heads, int n_kv_heads);
+void kro_silu_mul(float *g, const float *u, int n);
+void kro_add(float *y, const float *x, int n);
+void kro_dot_f32(float *s, const float *q, const float *k, size_t ldk, int rows, int n, float scale);
+void kro_axpy_f32(float *y, const float *a, const float *x, size_t ldx, int rows, int n);
+void kro_dequant_row(float *out, const ml_qtensor *W, int row);
+void kro_quantize_row_q4(int8_t *q, float *d, const float *x, int k);
+/* int32 block dot products s[r*nb + b] of rows [r0, r1) (exact) */
+void kro_block_dots(int32_t *s, const ml_qtensor *W, const ml_qact *x, int r0, int r1);
+int kro_argmax(const float *v, int n);
+/* F32-KV attention for one position (ops/ops.c:169-225 order) */
+void kro_attention(float *out, const float *q, const ml_kv_layer *kv, float *att, const ml_config *cfg, int pos);
+
+/* whole model */
+typedef struct kro_model kro_model;
+typedef struct kro_state kro_state;
+int kro_model_open(kro_model **m, const char *path);
+const ml_config *kro_model_config(const kro_model *m);
+void kro_model_close(kro_model *m);
+int kro_state_new(kro_state **s, const kro_model *m);
+void kro_state_free(kro_state *s);
+/* logits of token at pos into out[vocab] (model/transformer.c:257-306) */
+int kro_forward(kro_state *s, int token, int pos, float *out);
+/* n tokens from pos0; logits [n][vocab] if non-NULL (model/transformer.c:427-438) */
+int kro_prefill(kro_state *s, const int *tokens, int n, int pos0, float *logits);
+/* greedy loop as ml_run does it (app/ml_run.c:373-404): prompt of np ids,
+ * run to `steps` positions; out receives the ids ml_run prints */
+int kro_generate(kro_state *s, const int *prompt, int np, int steps, int *out);
+/* the residual stream x after the last kro_forward */
+const float *kro_state_x(const kro_state *s);
+const float *kro_state_kcache(const kro_state *s, int layer);
+/* internal buffer by name ("x", "q", "ao", "kcache", "vcache", "rope_cos", "rope_sin") */
+const float *kro_state_buffer(const kro_state *s, const char *name);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

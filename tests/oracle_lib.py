@@ -1,0 +1,150 @@
+"""ctypes access to the checkers: the oracle's C restatement
+(oracle/_build/liboracle.so) and the reference's own scalar build
+(oracle/_ref/libkrafla_ref_scalar.so, oracle/_ref/<isa>/ml_run). Test
+infrastructure only."""
+import ctypes as C
+import os
+import subprocess
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+ORACLE_SO = os.path.join(ROOT, "oracle", "_build", "liboracle.so")
+REF_DIR = os.path.join(ROOT, "oracle", "_ref")
+REF_SO = os.path.join(REF_DIR, "libkrafla_ref_scalar.so")
+
+import krafla as K  # noqa: E402  (tests/conftest.py puts the package on sys.path)
+
+_P = C.c_void_p
+
+
+def _lib(path):
+    if not os.path.exists(path):
+        raise RuntimeError("%s missing: run __graft_entry__.build()" % path)
+    return C.CDLL(path)
+
+
+oracle = _lib(ORACLE_SO)
+ref = _lib(REF_SO) if os.path.exists(REF_SO) else None
+
+KERNELS = {
+    "matvec_q8": [_P, _P, _P, C.c_int, C.c_int], "matvec_q4": [_P, _P, _P, C.c_int, C.c_int],
+    "quantize_q8": [_P, _P, C.c_int], "rmsnorm": [_P, _P, _P, C.c_int, C.c_float],
+    "softmax": [_P, C.c_int], "rope": [_P, _P, _P, _P, C.c_int, C.c_int, C.c_int],
+    "silu_mul": [_P, _P, C.c_int], "add": [_P, _P, C.c_int],
+    "dot_f32": [_P, _P, _P, C.c_size_t, C.c_int, C.c_int, C.c_float],
+    "axpy_f32": [_P, _P, _P, C.c_size_t, C.c_int, C.c_int],
+}
+for name, args in KERNELS.items():
+    getattr(oracle, "kro_" + name).argtypes = args
+    if ref is not None:
+        getattr(ref, "ml_k_%s_scalar" % name).argtypes = args
+oracle.kro_expf.restype = C.c_float
+oracle.kro_expf.argtypes = [C.c_float]
+oracle.kro_expf_mismatches.restype = C.c_uint64
+oracle.kro_expf_mismatches.argtypes = [C.c_uint64, C.c_uint64, C.c_int]
+oracle.kro_expf_check.restype = C.c_uint64
+oracle.kro_expf_check.argtypes = [_P, _P, C.c_size_t]
+oracle.kro_expf_check_range.restype = C.c_uint64
+oracle.kro_expf_check_range.argtypes = [C.c_uint64, _P, C.c_size_t, C.c_int]
+oracle.kro_f16_to_f32.restype = C.c_float
+oracle.kro_f16_to_f32.argtypes = [C.c_uint16]
+oracle.kro_dequant_row.argtypes = [_P, _P, C.c_int]
+oracle.kro_quantize_row_q4.argtypes = [_P, _P, _P, C.c_int]
+oracle.kro_block_dots.argtypes = [_P, _P, _P, C.c_int, C.c_int]
+oracle.kro_argmax.restype = C.c_int
+oracle.kro_argmax.argtypes = [_P, C.c_int]
+oracle.kro_attention.argtypes = [_P, _P, _P, _P, _P, C.c_int]
+oracle.kro_model_open.argtypes = [C.POINTER(_P), C.c_char_p]
+oracle.kro_model_config.restype = C.POINTER(K.MlConfig)
+oracle.kro_model_config.argtypes = [_P]
+oracle.kro_model_close.argtypes = [_P]
+oracle.kro_state_new.argtypes = [C.POINTER(_P), _P]
+oracle.kro_state_free.argtypes = [_P]
+oracle.kro_forward.argtypes = [_P, C.c_int, C.c_int, _P]
+oracle.kro_prefill.argtypes = [_P, _P, C.c_int, C.c_int, _P]
+oracle.kro_generate.argtypes = [_P, _P, C.c_int, C.c_int, _P]
+oracle.kro_state_buffer.restype = C.POINTER(C.c_float)
+oracle.kro_state_buffer.argtypes = [_P, C.c_char_p]
+oracle.kro_state_x.restype = C.POINTER(C.c_float)
+oracle.kro_state_x.argtypes = [_P]
+if ref is not None:
+    ref.ml_dequant_row.argtypes = [_P, _P, C.c_int]
+    ref.ml_quantize_row_q4.argtypes = [_P, _P, _P, C.c_int]
+
+
+class KvLayer(C.Structure):
+    """ops/ops.h:16-22"""
+    _fields_ = [("k", _P), ("v", _P), ("kq", _P), ("vq", _P), ("kd", _P), ("vd", _P), ("window", C.c_int),
+                ("kh", _P), ("vh", _P)]
+
+
+def qtensor(q, d, rows, cols, typ):
+    """an ml_qtensor over numpy arrays q (int8/uint8) and d (float32)"""
+    return K.MlQTensor(q.ctypes.data, d.ctypes.data, rows, cols, typ, None, None, None, 0)
+
+
+def qact(q, d):
+    return K.MlQAct(q.ctypes.data, d.ctypes.data, len(q))
+
+
+def quantize(x):
+    """Q8_0 of x with the oracle (int8 quants, f32 scales)"""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    q = np.zeros(len(x), dtype=np.int8)
+    d = np.zeros(len(x) // 32, dtype=np.float32)
+    a = qact(q, d)
+    oracle.kro_quantize_q8(C.byref(a), x.ctypes.data, len(x))
+    return q, d
+
+
+class OracleModel:
+    def __init__(self, path):
+        self.m = _P()
+        st = oracle.kro_model_open(C.byref(self.m), path.encode())
+        assert st == 0, "oracle cannot open %s (%d)" % (path, st)
+        self.cfg = oracle.kro_model_config(self.m).contents
+        self.s = _P()
+        assert oracle.kro_state_new(C.byref(self.s), self.m) == 0
+
+    def forward(self, tok, pos):
+        out = np.empty(self.cfg.vocab, dtype=np.float32)
+        assert oracle.kro_forward(self.s, tok, pos, out.ctypes.data) == 0
+        return out
+
+    def prefill(self, toks, pos0, logits=False):
+        t = np.ascontiguousarray(toks, dtype=np.int32)
+        out = np.empty((len(t), self.cfg.vocab), dtype=np.float32) if logits else None
+        assert oracle.kro_prefill(self.s, t.ctypes.data, len(t), pos0,
+                                  out.ctypes.data if out is not None else None) == 0
+        return out
+
+    def generate(self, prompt, steps):
+        p = np.ascontiguousarray(prompt, dtype=np.int32)
+        out = np.zeros(steps + len(p) + 2, dtype=np.int32)
+        n = oracle.kro_generate(self.s, p.ctypes.data, len(p), steps, out.ctypes.data)
+        assert n >= 0
+        return out[:n].copy()
+
+    def buffer(self, name, count):
+        p = oracle.kro_state_buffer(self.s, name.encode())
+        return np.ctypeslib.as_array(p, shape=(count,)).copy()
+
+    def close(self):
+        oracle.kro_state_free(self.s)
+        oracle.kro_model_close(self.m)
+
+
+def ref_ml_run(model, tokens, steps, threads=1, dump=None, isa="scalar", timeout=600):
+    """the reference's own ml_run (built from its sources into oracle/_ref):
+    greedy ids it prints, or the logits it dumps; with its stderr"""
+    exe = os.path.join(REF_DIR, isa, "ml_run")
+    cmd = [exe, model, "--tokens", ",".join(str(int(t)) for t in tokens), "-n", str(steps), "-T", "0",
+           "-t", str(threads)]
+    if dump:
+        cmd += ["--dump-logits", dump]
+    r = subprocess.run(cmd, capture_output=True, text=True, timeout=timeout)
+    if r.returncode != 0:
+        raise RuntimeError("ml_run failed (%d): %s" % (r.returncode, r.stderr))
+    ids = np.array([int(v) for v in r.stdout.split()], dtype=np.int32)
+    return ids, r.stderr

@@ -1,0 +1,332 @@
+"""Parity of each fused HIP kernel with the oracle, bit for bit, through the
+C ABI of libkrafla_hip.so. Needs a gfx950 device."""
+import ctypes as C
+import os
+
+import numpy as np
+import pytest
+
+import krafla as K
+import oracle_lib as O
+from oracle_lib import oracle
+
+pytestmark = pytest.mark.gpu
+RNG = np.random.default_rng(42)
+
+
+@pytest.fixture(scope="module", autouse=True)
+def device():
+    K.init_device()
+    yield
+    K.hip.krh_sync()
+
+
+def bits(a):
+    return np.ascontiguousarray(a, dtype=np.float32).view(np.uint32)
+
+
+def f32(a):
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def ok():
+    st = K.hip.krh_sync()
+    assert st == 0, K.hip.krh_last_error().decode()
+
+
+class Dev:
+    """device copies of numpy arrays, freed together"""
+
+    def __init__(self):
+        self.bufs = []
+
+    def put(self, a):
+        b = K.DevBuf.of(a)
+        self.bufs.append(b)
+        return b
+
+    def zeros(self, nbytes):
+        return self.put(np.zeros(nbytes, dtype=np.uint8))
+
+    def free(self):
+        for b in self.bufs:
+            b.free()
+
+
+@pytest.fixture
+def dev():
+    d = Dev()
+    yield d
+    d.free()
+
+
+def test_expf_exhaustive(dev):
+    """the device expf equals the host C library's on every float32 input"""
+    n = 1 << 26
+    xb, yb = dev.zeros(4 * n), dev.zeros(4 * n)
+    bad = 0
+    threads = min(16, os.cpu_count() or 1)
+    for lo in range(0, 1 << 32, n):
+        x = np.arange(lo, lo + n, dtype=np.uint64).astype(np.uint32).view(np.float32)
+        K.check(K.hip.krh_copy_h2d(xb.ptr, x.ctypes.data, x.nbytes))
+        K.hip.krh_math_batch(K.MATH_EXPF, yb.ptr, xb.ptr, None, n)
+        y = yb.get(np.float32, n)
+        bad += oracle.kro_expf_check_range(lo, y.ctypes.data, n, threads)
+    assert bad == 0
+
+
+def test_sqrt_exhaustive(dev):
+    """the device square root equals the host's (IEEE, correctly rounded) on
+    every non-negative float32 input"""
+    n = 1 << 26
+    xb, yb = dev.zeros(4 * n), dev.zeros(4 * n)
+    for lo in range(0, 1 << 31, n):
+        x = np.arange(lo, lo + n, dtype=np.uint64).astype(np.uint32).view(np.float32)
+        K.check(K.hip.krh_copy_h2d(xb.ptr, x.ctypes.data, x.nbytes))
+        K.hip.krh_math_batch(K.MATH_SQRT, yb.ptr, xb.ptr, None, n)
+        y = yb.get(np.float32, n)
+        want = np.sqrt(x)
+        fin = ~np.isnan(want)
+        assert np.array_equal(bits(y[fin]), bits(want[fin])), lo
+
+
+def test_division_and_rms_inverse(dev):
+    """a / b and rmsnorm's 1 / sqrtf(ss / n + eps) against numpy float32
+    (IEEE round to nearest even), on random and hard operands"""
+    n = 1 << 24
+    a = RNG.integers(0, 0x7f800000, n, dtype=np.uint32).view(np.float32)
+    b = RNG.integers(0x00800000, 0x7f800000, n, dtype=np.uint32).view(np.float32)
+    a[:4096] = np.float32(1.0)
+    b[:4096] = np.arange(1, 4097, dtype=np.float32)
+    ab, bb, yb = dev.put(a), dev.put(b), dev.zeros(4 * n)
+    K.hip.krh_math_batch(K.MATH_DIV, yb.ptr, ab.ptr, bb.ptr, n)
+    with np.errstate(all="ignore"):
+        want = (a / b).astype(np.float32)
+    assert np.array_equal(bits(yb.get(np.float32, n)), bits(want))
+    ss = f32(np.abs(RNG.normal(0, 1, n)) * RNG.choice([1e-3, 1.0, 100.0, 1e4], n))
+    dn = f32(RNG.choice([48.0, 64.0, 128.0, 288.0, 896.0, 2048.0, 4096.0], n))
+    sb, nb = dev.put(ss), dev.put(dn)
+    K.hip.krh_math_batch(K.MATH_RMS_INV, yb.ptr, sb.ptr, nb.ptr, n)
+    want = (np.float32(1.0) / np.sqrt((ss / dn).astype(np.float32) + np.float32(1e-5))).astype(np.float32)
+    assert np.array_equal(bits(yb.get(np.float32, n)), bits(want))
+
+
+def test_h2f_all(dev):
+    h = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    hb, yb = dev.put(h), dev.zeros(4 * 65536)
+    K.hip.krh_h2f_batch(yb.ptr, hb.ptr, 65536)
+    y = yb.get(np.float32, 65536)
+    want = h.view(np.float16).astype(np.float32)
+    fin = np.isfinite(want)
+    assert np.array_equal(bits(y[fin]), bits(want[fin]))
+    assert np.all(np.isnan(y[np.isnan(want)]))
+
+
+@pytest.mark.parametrize("n,ntok", [(32, 1), (4096, 1), (14336, 1), (288, 5)])
+def test_quantize(dev, n, ntok):
+    x = f32(RNG.normal(0, 1, n * ntok) * RNG.choice([1e-3, 1.0, 1e3], n * ntok))
+    x[:32] = 0.0
+    if n >= 96:
+        x[32:64] = [1e-37 if i % 2 else -2e-37 for i in range(32)]
+        x[64:96] = 0.0
+        x[64:70] = [127.0, 0.5, -0.5, 1.5, 2.5, -2.5]
+    xb, qb, db = dev.put(x), dev.zeros(n * ntok), dev.zeros(4 * n * ntok // 32)
+    K.hip.krh_quantize_q8(qb.ptr, db.ptr, xb.ptr, n, ntok)
+    ok()
+    q0, d0 = O.quantize(x)
+    assert np.array_equal(qb.get(np.int8, n * ntok), q0)
+    assert np.array_equal(bits(db.get(np.float32, n * ntok // 32)), bits(d0))
+
+
+def rand_mat(rows, cols, typ, d16):
+    if typ == K.ML_Q8_0:
+        q = RNG.integers(-127, 128, rows * cols).astype(np.int8)
+    else:
+        q = RNG.integers(0, 256, rows * cols // 2).astype(np.uint8)
+    dh = np.abs(RNG.normal(0, 0.01, rows * cols // 32)).astype(np.float16)
+    d = dh.astype(np.float32) if d16 else f32(np.abs(RNG.normal(0, 0.01, rows * cols // 32)))
+    return q, d, dh
+
+
+def dmat(dev, q, d, dh, rows, cols, typ, d16):
+    qb = dev.put(q)
+    db = dev.put(dh if d16 else d)
+    return K.KrhMat(qb.ptr, db.ptr, rows, cols, typ, d16)
+
+
+def oracle_matvec(q, d, rows, cols, typ, xq, xd):
+    W = O.qtensor(q, d, rows, cols, typ)
+    y = np.zeros(rows, dtype=np.float32)
+    fn = oracle.kro_matvec_q8 if typ == K.ML_Q8_0 else oracle.kro_matvec_q4
+    fn(y.ctypes.data, C.byref(W), C.byref(O.qact(xq, xd)), 0, rows)
+    return y
+
+
+@pytest.mark.parametrize("typ", [K.ML_Q8_0, K.ML_Q4_0])
+def test_block_dots_exact(dev, typ):
+    rows, cols = 37, 4096
+    q, d, dh = rand_mat(rows, cols, typ, 0)
+    xq, xd = O.quantize(f32(RNG.normal(0, 1, cols)))
+    W = dmat(dev, q, d, dh, rows, cols, typ, 0)
+    sb = dev.zeros(4 * rows * cols // 32)
+    K.hip.krh_block_dots(sb.ptr, C.byref(W), dev.put(xq).ptr)
+    ok()
+    want = np.zeros(rows * cols // 32, dtype=np.int32)
+    oracle.kro_block_dots(want.ctypes.data, C.byref(O.qtensor(q, d, rows, cols, typ)), C.byref(O.qact(xq, xd)), 0,
+                          rows)
+    assert np.array_equal(sb.get(np.int32, rows * cols // 32), want)
+
+
+MV_SHAPES = [(1, 32), (3, 96), (16, 256), (17, 288), (64, 768), (288, 768), (4096, 4096), (896, 4864),
+             (14336, 4096), (4096, 14336)]
+
+
+@pytest.mark.parametrize("typ", [K.ML_Q8_0, K.ML_Q4_0])
+@pytest.mark.parametrize("d16", [0, 1])
+@pytest.mark.parametrize("rows,cols", MV_SHAPES)
+def test_matvec(dev, typ, d16, rows, cols):
+    q, d, dh = rand_mat(rows, cols, typ, d16)
+    xq, xd = O.quantize(f32(RNG.normal(0, 1, cols)))
+    W = dmat(dev, q, d, dh, rows, cols, typ, d16)
+    yb = dev.zeros(4 * rows)
+    K.hip.krh_matvec(yb.ptr, C.byref(W), dev.put(xq).ptr, dev.put(xd).ptr, 0)
+    ok()
+    want = oracle_matvec(q, d, rows, cols, typ, xq, xd)
+    assert np.array_equal(bits(yb.get(np.float32, rows)), bits(want))
+
+
+def test_matvec_accumulate(dev):
+    rows, cols = 288, 768
+    q, d, dh = rand_mat(rows, cols, K.ML_Q8_0, 0)
+    xq, xd = O.quantize(f32(RNG.normal(0, 1, cols)))
+    y0 = f32(RNG.normal(0, 1, rows))
+    W = dmat(dev, q, d, dh, rows, cols, K.ML_Q8_0, 0)
+    yb = dev.put(y0)
+    K.hip.krh_matvec(yb.ptr, C.byref(W), dev.put(xq).ptr, dev.put(xd).ptr, 1)
+    ok()
+    want = (y0 + oracle_matvec(q, d, rows, cols, K.ML_Q8_0, xq, xd)).astype(np.float32)
+    assert np.array_equal(bits(yb.get(np.float32, rows)), bits(want))
+
+
+@pytest.mark.parametrize("n,ntok", [(288, 1), (4096, 1), (896, 3)])
+def test_rmsnorm_q8(dev, n, ntok):
+    x = f32(RNG.normal(0, 2, n * ntok))
+    w = f32(RNG.normal(1, 0.1, n))
+    qb, db, ob = dev.zeros(n * ntok), dev.zeros(4 * n * ntok // 32), dev.zeros(4 * n * ntok)
+    K.hip.krh_rmsnorm_q8(qb.ptr, db.ptr, ob.ptr, dev.put(x).ptr, dev.put(w).ptr, n, 1e-5, ntok)
+    ok()
+    for t in range(ntok):
+        o = np.zeros(n, np.float32)
+        xt = f32(x[t * n:(t + 1) * n])
+        oracle.kro_rmsnorm(o.ctypes.data, xt.ctypes.data, w.ctypes.data, n, C.c_float(1e-5))
+        q0, d0 = O.quantize(o)
+        assert np.array_equal(bits(ob.get(np.float32, n * ntok)[t * n:(t + 1) * n]), bits(o))
+        assert np.array_equal(qb.get(np.int8, n * ntok)[t * n:(t + 1) * n], q0)
+        assert np.array_equal(bits(db.get(np.float32, n * ntok // 32)[t * n // 32:(t + 1) * n // 32]), bits(d0))
+
+
+@pytest.mark.parametrize("dim,nh,nkv,hd,typ,bias", [(288, 6, 6, 48, K.ML_Q8_0, 0), (896, 14, 2, 64, K.ML_Q4_0, 1),
+                                                     (4096, 32, 8, 128, K.ML_Q8_0, 0)])
+def test_qkv_bias_rope_cache(dev, dim, nh, nkv, hd, typ, bias):
+    qd, kvd, max_seq, pos = nh * hd, nkv * hd, 40, 23
+    mats = [rand_mat(r, dim, typ, 1) for r in (qd, kvd, kvd)]
+    Ws = [dmat(dev, q, d, dh, r, dim, typ, 1) for (q, d, dh), r in zip(mats, (qd, kvd, kvd))]
+    biases = [f32(RNG.normal(0, 0.02, r)) for r in (qd, kvd, kvd)]
+    cs, sn = f32(RNG.uniform(-1, 1, max_seq * hd // 2)), f32(RNG.uniform(-1, 1, max_seq * hd // 2))
+    xq, xd = O.quantize(f32(RNG.normal(0, 1, dim)))
+    qb, kc, vc = dev.zeros(4 * qd), dev.zeros(4 * max_seq * kvd), dev.zeros(4 * max_seq * kvd)
+    bb = [dev.put(b) if bias else None for b in biases]
+    posb = dev.put(np.array([pos], np.int32))
+    K.hip.krh_matvec_qkv(qb.ptr, kc.ptr, vc.ptr, C.byref(Ws[0]), C.byref(Ws[1]), C.byref(Ws[2]),
+                         *[b.ptr if b else None for b in bb], dev.put(xq).ptr, dev.put(xd).ptr,
+                         dev.put(cs).ptr, dev.put(sn).ptr, hd, posb.ptr)
+    ok()
+    outs = []
+    for (q, d, dh), r, b in zip(mats, (qd, kvd, kvd), biases):
+        y = oracle_matvec(q, d, r, dim, typ, xq, xd)
+        if bias:
+            oracle.kro_add(y.ctypes.data, b.ctypes.data, r)
+        outs.append(y)
+    c0 = f32(cs[pos * hd // 2:(pos + 1) * hd // 2])
+    s0 = f32(sn[pos * hd // 2:(pos + 1) * hd // 2])
+    oracle.kro_rope(outs[0].ctypes.data, outs[1].ctypes.data, c0.ctypes.data, s0.ctypes.data, hd, nh, nkv)
+    assert np.array_equal(bits(qb.get(np.float32, qd)), bits(outs[0]))
+    assert np.array_equal(bits(kc.get(np.float32, max_seq * kvd)[pos * kvd:(pos + 1) * kvd]), bits(outs[1]))
+    assert np.array_equal(bits(vc.get(np.float32, max_seq * kvd)[pos * kvd:(pos + 1) * kvd]), bits(outs[2]))
+
+
+@pytest.mark.parametrize("rows,cols,typ", [(768, 288, K.ML_Q8_0), (4864, 896, K.ML_Q4_0), (14336, 4096, K.ML_Q8_0)])
+def test_swiglu_q8(dev, rows, cols, typ):
+    (q1, d1, h1), (q3, d3, h3) = rand_mat(rows, cols, typ, 1), rand_mat(rows, cols, typ, 1)
+    W1, W3 = dmat(dev, q1, d1, h1, rows, cols, typ, 1), dmat(dev, q3, d3, h3, rows, cols, typ, 1)
+    xq, xd = O.quantize(f32(RNG.normal(0, 1, cols) * 30))
+    hq, hdb, hb = dev.zeros(rows), dev.zeros(4 * rows // 32), dev.zeros(4 * rows)
+    K.hip.krh_matvec_swiglu_q8(hq.ptr, hdb.ptr, hb.ptr, C.byref(W1), C.byref(W3), dev.put(xq).ptr, dev.put(xd).ptr)
+    ok()
+    g = oracle_matvec(q1, d1, rows, cols, typ, xq, xd)
+    u = oracle_matvec(q3, d3, rows, cols, typ, xq, xd)
+    oracle.kro_silu_mul(g.ctypes.data, u.ctypes.data, rows)
+    q0, d0 = O.quantize(g)
+    assert np.array_equal(bits(hb.get(np.float32, rows)), bits(g))
+    assert np.array_equal(hq.get(np.int8, rows), q0)
+    assert np.array_equal(bits(hdb.get(np.float32, rows // 32)), bits(d0))
+
+
+@pytest.mark.parametrize("nh,nkv,hd,pos,window", [(6, 6, 48, 0, 0), (6, 6, 48, 200, 0), (14, 2, 64, 511, 0),
+                                                  (32, 8, 128, 2303, 0), (32, 8, 64, 4000, 0), (8, 2, 64, 100, 7)])
+def test_attention(dev, nh, nkv, hd, pos, window):
+    max_seq = max(256, pos + 1)
+    kvd, qd = nkv * hd, nh * hd
+    q = f32(RNG.normal(0, 1, qd))
+    kc = f32(RNG.normal(0, 1, max_seq * kvd))
+    vc = f32(RNG.normal(0, 1, max_seq * kvd))
+    scale = np.float32(1.0) / np.sqrt(np.float32(hd))
+    ao, aq, ad, att = dev.zeros(4 * qd), dev.zeros(qd), dev.zeros(4 * qd // 32), dev.zeros(4 * nh * max_seq)
+    posb = dev.put(np.array([pos], np.int32))
+    K.hip.krh_attention(ao.ptr, aq.ptr, ad.ptr, att.ptr, dev.put(q).ptr, dev.put(kc).ptr, dev.put(vc).ptr, nh, nkv,
+                        hd, max_seq, window, float(scale), posb.ptr)
+    ok()
+    cfg = K.MlConfig(n_heads=nh, n_kv_heads=nkv, head_dim=hd, kv_dim=kvd, q_dim=qd, max_seq=max_seq,
+                     attn_scale=float(scale))
+    kvl = O.KvLayer(kc.ctypes.data, vc.ctypes.data, None, None, None, None, window, None, None)
+    out = np.zeros(qd, np.float32)
+    scratch = np.zeros(max_seq, np.float32)
+    oracle.kro_attention(out.ctypes.data, q.ctypes.data, C.byref(kvl), scratch.ctypes.data, C.byref(cfg), pos)
+    assert np.array_equal(bits(ao.get(np.float32, qd)), bits(out))
+    q0, d0 = O.quantize(out)
+    assert np.array_equal(aq.get(np.int8, qd), q0)
+    assert np.array_equal(bits(ad.get(np.float32, qd // 32)), bits(d0))
+
+
+@pytest.mark.parametrize("case", ["ties", "neg_inf", "random", "nan0"])
+def test_argmax(dev, case):
+    n = 151936
+    v = f32(RNG.normal(0, 1, n))
+    if case == "ties":
+        v[:] = 0
+        v[40000] = v[9] = v[150000] = 3.0
+    elif case == "neg_inf":
+        v[:] = -np.inf
+    elif case == "nan0":
+        v[0] = np.nan
+    tb, pb, lb = dev.zeros(4), dev.put(np.array([5], np.int32)), dev.zeros(4 * 16)
+    K.hip.krh_argmax(tb.ptr, dev.put(v).ptr, n, pb.ptr, lb.ptr)
+    ok()
+    want = oracle.kro_argmax(v.ctypes.data, n)
+    assert tb.get(np.int32, 1)[0] == want
+    assert pb.get(np.int32, 1)[0] == 6 and lb.get(np.int32, 16)[6] == want
+
+
+@pytest.mark.parametrize("typ,d16,scale", [(K.ML_Q8_0, 0, 1.0), (K.ML_Q4_0, 1, 1.0), (K.ML_Q8_0, 1, 8.0)])
+def test_embed(dev, typ, d16, scale):
+    rows, cols = 50, 896
+    q, d, dh = rand_mat(rows, cols, typ, d16)
+    E = dmat(dev, q, d, dh, rows, cols, typ, d16)
+    xb = dev.zeros(4 * cols)
+    K.hip.krh_embed(xb.ptr, C.byref(E), dev.put(np.array([33], np.int32)).ptr, scale)
+    ok()
+    want = np.zeros(cols, np.float32)
+    oracle.kro_dequant_row(want.ctypes.data, C.byref(O.qtensor(q, d, rows, cols, typ)), 33)
+    if scale != 1.0:
+        want = (want * np.float32(scale)).astype(np.float32)
+    assert np.array_equal(bits(xb.get(np.float32, cols)), bits(want))

@@ -1,0 +1,83 @@
+"""End-to-end parity of the device token loop with the reference: logits bit
+for bit against the reference's scalar ml_run --dump-logits, and greedy ids
+against its printed ids, on generated .mlb models. Needs a gfx950 device."""
+import os
+
+import numpy as np
+import pytest
+
+import krafla as K
+import oracle_lib as O
+
+pytestmark = pytest.mark.gpu
+
+SMALL = {
+    "c1_q8": dict(K.CONFIGS["stories15m_q8"]),
+    "c1_q8_std01": dict(K.CONFIGS["stories15m_q8"], std=0.1, seed=11),
+    "qwen_like_q4mix": dict(K.CONFIGS["qwen05b_mixed"], dim=128, n_layers=3, n_heads=4, n_kv_heads=2,
+                            hidden_dim=256, vocab=512, max_seq=96, std=0.1),
+    "llama3_rope_gqa_q4": dict(K.CONFIGS["llama1b_mixed"], dim=256, n_layers=2, n_heads=8, n_kv_heads=2,
+                               hidden_dim=512, vocab=1000, max_seq=200, std=0.1, rope_orig_max_seq=64),
+    "q8_f16_untied": dict(K.CONFIGS["llama8b_q8"], dim=256, n_layers=2, n_heads=4, n_kv_heads=1, hidden_dim=384,
+                          vocab=700, max_seq=160, std=0.1),
+}
+
+
+@pytest.fixture(scope="module", autouse=True)
+def device():
+    K.init_device()
+
+
+def bits(a):
+    return np.ascontiguousarray(a, dtype=np.float32).view(np.uint32)
+
+
+@pytest.mark.parametrize("name", sorted(SMALL))
+def test_logits_match_reference(name, workdir):
+    path = os.path.join(workdir, name + ".mlb")
+    K.gen_mlb(path, **SMALL[name])
+    m = K.Model(path)
+    s = K.State(m)
+    V = m.cfg.vocab
+    toks = [int(t) for t in np.random.default_rng(5).integers(1, V, 12)]
+    dump = path + ".logits"
+    O.ref_ml_run(path, toks, len(toks), dump=dump)
+    want = np.fromfile(dump, dtype=np.float32).reshape(len(toks), V)
+    got = np.empty((len(toks), V), dtype=np.float32)
+    s.prefill(toks, 0, logits=got)
+    assert np.array_equal(bits(got), bits(want))
+    s.close()
+    m.close()
+
+
+@pytest.mark.parametrize("name", sorted(SMALL))
+def test_greedy_ids_match_reference(name, workdir):
+    path = os.path.join(workdir, name + ".mlb")
+    if not os.path.exists(path):
+        K.gen_mlb(path, **SMALL[name])
+    m = K.Model(path)
+    s = K.State(m)
+    prompt = [int(t) for t in np.random.default_rng(6).integers(1, m.cfg.vocab, 8)]
+    steps = min(m.cfg.max_seq, 8 + 128)
+    want, _ = O.ref_ml_run(path, prompt, steps)
+    got, _, _ = s.generate(prompt, steps)
+    assert np.array_equal(got, want)
+    s.close()
+    m.close()
+
+
+def test_stories15m_shape_128_greedy(workdir):
+    """the tiny-Llama workload: 8-token prompt, 128 greedy tokens (ml_run -n 135)"""
+    path = os.path.join(workdir, "stories15m_q8.mlb")
+    K.gen_mlb(path, **K.CONFIGS["stories15m_q8"])
+    m = K.Model(path)
+    s = K.State(m)
+    prompt = [int(t) for t in np.random.default_rng(1).integers(1, 32000, 8)]
+    want, _ = O.ref_ml_run(path, prompt, 135)
+    got, _, _ = s.generate(prompt, 135)
+    assert len(got) == 135 and np.array_equal(got, want)
+    # decoding again from a fresh prefill gives the same ids (state reuse)
+    got2, _, _ = s.generate(prompt, 135)
+    assert np.array_equal(got2, want)
+    s.close()
+    m.close()

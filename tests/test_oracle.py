@@ -1,0 +1,301 @@
+"""Pins the oracle (oracle/kro*.c) before anything is checked against it:
+against the reference's own scalar build compiled from its sources
+(oracle/_ref), the reference's known-answer tests, the host C library, and
+closed forms. CPU only."""
+import ctypes as C
+import os
+
+import numpy as np
+import pytest
+
+import krafla as K
+import oracle_lib as O
+from oracle_lib import oracle, ref
+
+needs_ref = pytest.mark.skipif(ref is None, reason="oracle/_ref not built (needs /root/reference at build time)")
+RNG = np.random.default_rng(1234)
+
+
+def f32(a):
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def bits(a):
+    return np.ascontiguousarray(a, dtype=np.float32).view(np.uint32)
+
+
+# ---- expf: the reference calls the C library's expf ----
+
+def test_expf_exhaustive_vs_libm():
+    # every float32 input; the restated algorithm must equal the host libm
+    assert oracle.kro_expf_mismatches(0, 1 << 32, os.cpu_count() or 8) == 0
+
+
+def test_expf_specials():
+    for x, want in [(0.0, 1.0), (-np.inf, 0.0), (np.inf, np.inf), (89.0, np.inf), (-104.0, 0.0), (1.0, np.e)]:
+        got = oracle.kro_expf(x)
+        assert got == np.float32(want) or abs(got - want) <= 1e-6 * abs(want)
+    assert np.isnan(oracle.kro_expf(float("nan")))
+
+
+# ---- quantize_q8: known answers (tests/test_quant.c:28-70) and the rule ----
+
+def test_quantize_ties_kat():
+    x = np.zeros(32, dtype=np.float32)
+    x[:6] = [127.0, 0.5, -0.5, 1.5, 2.5, -2.5]
+    q, d = O.quantize(x)
+    assert d[0] == 1.0
+    assert q[1:6].tolist() == [1, -1, 2, 3, -3]
+
+
+def test_quantize_clamp_zero_tiny_kat():
+    x = f32(RNG.uniform(-1, 1, 96))
+    x[3], x[9] = -5.0, 4.999
+    x[32:64] = 0.0
+    x[64:96] = [0.0 if i % 3 == 0 else (1e-37 if i % 3 == 1 else -2e-37) for i in range(32)]
+    q, d = O.quantize(x)
+    assert q[3] == -127 and q.min() >= -127 and q.max() <= 127
+    assert d[1] == 0.0 and not q[32:64].any()
+    assert d[2] == 0.0 and not q[64:96].any()
+
+
+def test_quantize_roundtrip_bound():
+    x = f32(RNG.uniform(-3, 3, 256))
+    q, d = O.quantize(x)
+    err = np.abs(x - q * np.repeat(d, 32))
+    assert np.all(err <= np.repeat(d, 32) / 2 + 1e-7)
+
+
+def test_quantize_closed_form():
+    # numpy float32 arithmetic of the rule, element by element
+    x = f32(RNG.normal(0, 2, 4096))
+    q, d = O.quantize(x)
+    xb = x.reshape(-1, 32)
+    amax = np.abs(xb).max(axis=1)
+    id_ = (np.float32(127.0) / amax).astype(np.float32)
+    v = np.trunc((xb * id_[:, None]).astype(np.float32) + np.copysign(np.float32(0.5), xb)).astype(np.float32)
+    assert np.array_equal(np.clip(v, -127, 127).astype(np.int8).ravel(), q)
+    assert np.array_equal(bits(amax / np.float32(127.0)), bits(d))
+
+
+@needs_ref
+@pytest.mark.parametrize("k", [32, 4096])
+def test_quantize_matches_reference(k):
+    for scale in [1e-3, 1.0, 1e3]:
+        x = f32(RNG.normal(0, scale, k))
+        x[:32] = 0.0 if k > 32 else x[:32]
+        q0, d0 = O.quantize(x)
+        q1 = np.zeros(k, dtype=np.int8)
+        d1 = np.zeros(k // 32, dtype=np.float32)
+        a = O.qact(q1, d1)
+        ref.ml_k_quantize_q8_scalar(C.byref(a), x.ctypes.data, k)
+        assert np.array_equal(q0, q1) and np.array_equal(bits(d0), bits(d1))
+
+
+# ---- matvec: exact int dots (closed form) and the reference's float order ----
+
+def rand_mat(rows, cols, typ, rng=RNG):
+    if typ == K.ML_Q8_0:
+        q = rng.integers(-127, 128, rows * cols).astype(np.int8)
+    else:
+        q = rng.integers(0, 256, rows * cols // 2).astype(np.uint8)
+    d = f32(np.abs(rng.normal(0, 0.01, rows * cols // 32)))
+    return q, d
+
+
+def rand_act(k, rng=RNG):
+    return O.quantize(f32(rng.normal(0, 1, k)))
+
+
+def int_dots(q, typ, rows, cols, xq):
+    nb = cols // 32
+    if typ == K.ML_Q8_0:
+        w = q.astype(np.int64).reshape(rows, nb, 32)
+    else:
+        p = q.reshape(rows, nb, 16)
+        w = np.concatenate([(p & 15).astype(np.int64) - 8, (p >> 4).astype(np.int64) - 8], axis=2)
+    return (w * xq.astype(np.int64).reshape(1, nb, 32)).sum(axis=2)
+
+
+@pytest.mark.parametrize("typ", [K.ML_Q8_0, K.ML_Q4_0])
+def test_block_dots_brute_force(typ):
+    rows, cols = 7, 256
+    q, d = rand_mat(rows, cols, typ)
+    xq, xd = rand_act(cols)
+    W = O.qtensor(q, d, rows, cols, typ)
+    s = np.zeros(rows * cols // 32, dtype=np.int32)
+    oracle.kro_block_dots(s.ctypes.data, C.byref(W), C.byref(O.qact(xq, xd)), 0, rows)
+    assert np.array_equal(s.reshape(rows, -1), int_dots(q, typ, rows, cols, xq))
+
+
+@pytest.mark.parametrize("typ", [K.ML_Q8_0, K.ML_Q4_0])
+def test_matvec_unit_scales_exact(typ):
+    # with unit scales the result is the exact integer sum (tests/test_kernels.c:103)
+    rows, cols = 5, 96
+    q, _ = rand_mat(rows, cols, typ)
+    d = np.ones(rows * cols // 32, dtype=np.float32)
+    xq, _ = rand_act(cols)
+    xd = np.ones(cols // 32, dtype=np.float32)
+    W = O.qtensor(q, d, rows, cols, typ)
+    y = np.zeros(rows, dtype=np.float32)
+    fn = oracle.kro_matvec_q8 if typ == K.ML_Q8_0 else oracle.kro_matvec_q4
+    fn(y.ctypes.data, C.byref(W), C.byref(O.qact(xq, xd)), 0, rows)
+    assert np.array_equal(y, int_dots(q, typ, rows, cols, xq).sum(axis=1).astype(np.float32))
+
+
+def test_matvec_order_closed_form():
+    # sum += ((float)s * wd) * xd in block order, evaluated in numpy float32
+    rows, cols = 3, 8288
+    q, d = rand_mat(rows, cols, K.ML_Q8_0)
+    xq, xd = rand_act(cols)
+    W = O.qtensor(q, d, rows, cols, K.ML_Q8_0)
+    y = np.zeros(rows, dtype=np.float32)
+    oracle.kro_matvec_q8(y.ctypes.data, C.byref(W), C.byref(O.qact(xq, xd)), 0, rows)
+    s = int_dots(q, K.ML_Q8_0, rows, cols, xq).astype(np.float32)
+    t = (s * d.reshape(rows, -1)).astype(np.float32) * xd[None, :]
+    want = np.zeros(rows, dtype=np.float32)
+    for b in range(cols // 32):
+        want = (want + t[:, b]).astype(np.float32)
+    assert np.array_equal(bits(y), bits(want))
+    # a transposed or reordered sum would differ: check the test can tell
+    assert not np.array_equal(bits(t.sum(axis=1, dtype=np.float32)), bits(want)) or rows == 0
+
+
+@needs_ref
+@pytest.mark.parametrize("typ", [K.ML_Q8_0, K.ML_Q4_0])
+@pytest.mark.parametrize("rows,cols", [(1, 32), (3, 96), (64, 256), (7, 8288), (17, 4096)])
+def test_matvec_matches_reference(typ, rows, cols):
+    q, d = rand_mat(rows, cols, typ)
+    xq, xd = rand_act(cols)
+    W = O.qtensor(q, d, rows, cols, typ)
+    x = O.qact(xq, xd)
+    y0 = np.full(rows + 2, 12345.0, dtype=np.float32)
+    y1 = y0.copy()
+    name = "matvec_q8" if typ == K.ML_Q8_0 else "matvec_q4"
+    getattr(oracle, "kro_" + name)(y0.ctypes.data, C.byref(W), C.byref(x), 1, rows)
+    getattr(ref, "ml_k_%s_scalar" % name)(y1.ctypes.data, C.byref(W), C.byref(x), 1, rows)
+    assert np.array_equal(bits(y0), bits(y1))
+    assert y0[0] == 12345.0 and y0[rows] == 12345.0  # rows outside [r0, r1) untouched
+
+
+# ---- float kernels vs the reference's scalar kernels ----
+
+@needs_ref
+@pytest.mark.parametrize("n", [32, 288, 4096])
+def test_rmsnorm_softmax_silu_add_match_reference(n):
+    x, w, u = f32(RNG.normal(0, 1, n)), f32(RNG.normal(1, 0.1, n)), f32(RNG.normal(0, 1, n))
+    for fn_o, fn_r, args in [
+        ("kro_rmsnorm", "ml_k_rmsnorm_scalar", lambda o: (o.ctypes.data, x.ctypes.data, w.ctypes.data, n, 1e-5)),
+    ]:
+        o0, o1 = np.zeros(n, np.float32), np.zeros(n, np.float32)
+        getattr(oracle, fn_o)(*args(o0))
+        getattr(ref, fn_r)(*args(o1))
+        assert np.array_equal(bits(o0), bits(o1))
+    s0, s1 = f32(RNG.normal(0, 3, n)), None
+    s1 = s0.copy()
+    oracle.kro_softmax(s0.ctypes.data, n)
+    ref.ml_k_softmax_scalar(s1.ctypes.data, n)
+    assert np.array_equal(bits(s0), bits(s1))
+    g0 = f32(RNG.normal(0, 4, n))
+    g1 = g0.copy()
+    oracle.kro_silu_mul(g0.ctypes.data, u.ctypes.data, n)
+    ref.ml_k_silu_mul_scalar(g1.ctypes.data, u.ctypes.data, n)
+    assert np.array_equal(bits(g0), bits(g1))
+    a0 = x.copy()
+    a1 = x.copy()
+    oracle.kro_add(a0.ctypes.data, u.ctypes.data, n)
+    ref.ml_k_add_scalar(a1.ctypes.data, u.ctypes.data, n)
+    assert np.array_equal(bits(a0), bits(a1))
+
+
+@needs_ref
+def test_rope_dot_axpy_match_reference():
+    hd, nh, nkv = 64, 4, 2
+    q0, k0 = f32(RNG.normal(0, 1, hd * nh)), f32(RNG.normal(0, 1, hd * nkv))
+    cs, sn = f32(RNG.uniform(-1, 1, hd // 2)), f32(RNG.uniform(-1, 1, hd // 2))
+    q1, k1 = q0.copy(), k0.copy()
+    oracle.kro_rope(q0.ctypes.data, k0.ctypes.data, cs.ctypes.data, sn.ctypes.data, hd, nh, nkv)
+    ref.ml_k_rope_scalar(q1.ctypes.data, k1.ctypes.data, cs.ctypes.data, sn.ctypes.data, hd, nh, nkv)
+    assert np.array_equal(bits(q0), bits(q1)) and np.array_equal(bits(k0), bits(k1))
+    rows, ld = 37, 96
+    kk = f32(RNG.normal(0, 1, rows * ld))
+    s0, s1 = np.zeros(rows, np.float32), np.zeros(rows, np.float32)
+    oracle.kro_dot_f32(s0.ctypes.data, q1.ctypes.data, kk.ctypes.data, ld, rows, hd, 0.125)
+    ref.ml_k_dot_f32_scalar(s1.ctypes.data, q1.ctypes.data, kk.ctypes.data, ld, rows, hd, 0.125)
+    assert np.array_equal(bits(s0), bits(s1))
+    y0 = f32(RNG.normal(0, 1, hd))
+    y1 = y0.copy()
+    oracle.kro_axpy_f32(y0.ctypes.data, s0.ctypes.data, kk.ctypes.data, ld, rows, hd)
+    ref.ml_k_axpy_f32_scalar(y1.ctypes.data, s0.ctypes.data, kk.ctypes.data, ld, rows, hd)
+    assert np.array_equal(bits(y0), bits(y1))
+
+
+@needs_ref
+@pytest.mark.parametrize("typ", [K.ML_Q8_0, K.ML_Q4_0])
+def test_dequant_and_q4_rule_match_reference(typ):
+    q, d = rand_mat(4, 128, typ)
+    W = O.qtensor(q, d, 4, 128, typ)
+    o0, o1 = np.zeros(128, np.float32), np.zeros(128, np.float32)
+    oracle.kro_dequant_row(o0.ctypes.data, C.byref(W), 2)
+    ref.ml_dequant_row(o1.ctypes.data, C.byref(W), 2)
+    assert np.array_equal(bits(o0), bits(o1))
+    x = f32(RNG.normal(0, 1, 128))
+    x[32:64] = 0
+    qa, da = np.zeros(64, np.uint8), np.zeros(4, np.float32)
+    qb, db = qa.copy(), da.copy()
+    oracle.kro_quantize_row_q4(qa.ctypes.data, da.ctypes.data, x.ctypes.data, 128)
+    ref.ml_quantize_row_q4(qb.ctypes.data, db.ctypes.data, x.ctypes.data, 128)
+    assert np.array_equal(qa, qb) and np.array_equal(bits(da), bits(db))
+
+
+def test_argmax_ties_lowest():
+    # tests/test_sampler.c:33-40
+    v = np.zeros(64, np.float32)
+    v[40] = v[9] = 3.0
+    assert oracle.kro_argmax(v.ctypes.data, 64) == 9
+    v = np.full(8, -np.inf, np.float32)
+    assert oracle.kro_argmax(v.ctypes.data, 8) == 0
+
+
+def test_f16_widening_closed_form():
+    h = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    want = h.view(np.float16).astype(np.float32)
+    got = np.array([oracle.kro_f16_to_f32(int(v)) for v in h[::97]], dtype=np.float32)
+    w = want[::97]
+    finite = np.isfinite(w)
+    assert np.array_equal(bits(got[finite]), bits(w[finite]))
+
+
+# ---- whole model: the oracle's forward vs the reference's ml_run ----
+
+SMALL = {
+    "c1_q8": dict(K.CONFIGS["stories15m_q8"]),
+    "c1_q8_std01": dict(K.CONFIGS["stories15m_q8"], std=0.1, seed=11),
+    "qwen_like_q4mix": dict(K.CONFIGS["qwen05b_mixed"], dim=128, n_layers=3, n_heads=4, n_kv_heads=2,
+                            hidden_dim=256, vocab=512, max_seq=96, std=0.1),
+    "llama3_rope_gqa_q4": dict(K.CONFIGS["llama1b_mixed"], dim=256, n_layers=2, n_heads=8, n_kv_heads=2,
+                               hidden_dim=512, vocab=1000, max_seq=200, std=0.1, rope_orig_max_seq=64),
+    "q8_f16_untied": dict(K.CONFIGS["llama8b_q8"], dim=256, n_layers=2, n_heads=4, n_kv_heads=1, hidden_dim=384,
+                          vocab=700, max_seq=160, std=0.1),
+}
+
+
+@needs_ref
+@pytest.mark.parametrize("name", sorted(SMALL))
+def test_forward_matches_reference(name, workdir):
+    path = os.path.join(workdir, name + ".mlb")
+    K.gen_mlb(path, **SMALL[name])
+    om = O.OracleModel(path)
+    V = om.cfg.vocab
+    toks = [int(t) for t in np.random.default_rng(5).integers(1, V, 12)]
+    dump = path + ".logits"
+    O.ref_ml_run(path, toks, len(toks), dump=dump)
+    want = np.fromfile(dump, dtype=np.float32).reshape(len(toks), V)
+    got = om.prefill(toks, 0, logits=True)
+    assert np.array_equal(bits(got), bits(want))
+    om.close()
+    om = O.OracleModel(path)
+    steps = min(om.cfg.max_seq, 60)
+    ids_ref, _ = O.ref_ml_run(path, toks[:5], steps)
+    assert np.array_equal(om.generate(toks[:5], steps), ids_ref)
+    om.close()
