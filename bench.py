@@ -1,0 +1,291 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X token loop on one GPU.
+
+Workload (default): the Llama-3-8B-shaped model -- dim 4096, 32 layers,
+32 query / 8 KV heads, head_dim 128, FFN 14336 SwiGLU, vocab 128256,
+RoPE theta 5e5, every matrix Q8_0 in 32-blocks with f16 scales (8.53 GB),
+random-init N(0, 0.02) from seed 5 -- run the way the reference's ml_run
+runs a prompt (app/ml_run.c:369-404): a 2048-token random prompt
+(ids uniform in [1, vocab)) of which 2047 tokens are prefilled, then
+greedy decode, batch 1. A step is one decode token (one ml_forward plus the
+greedy pick); `value` is decode tokens per second over --steps tokens at
+positions 2047, 2048, ..., with the model and KV cache resident in HBM.
+
+Also reported on the same line:
+  prefill_tok_s   prompt tokens per second of the 2047-token prefill
+  roofline        the dominant decode kernel (the fused w1/w3 SwiGLU matvec,
+                  54% of the weight bytes of a layer): algorithmic bytes per
+                  launch (weights + f16 scales of w1 and w3) over its average
+                  launch duration, timed with HIP events on the library
+                  stream, rotating through all 32 layers so the weights come
+                  from HBM and not from the 256 MB Infinity Cache
+  matvec          the isolated Q4_0/Q8_0 matvec microbench (4096x4096 and
+                  14336x4096, f16 scales, activation quantize_q8(N(0,1))):
+                  GB/s over 1000 launches, cache-resident (one matrix) and
+                  HBM-rotating (copies totalling more than 1 GB)
+  cpu_baseline    the reference's best CPU build (avx512vnni, else avx2,
+                  THREADS=pthread, built from its sources into oracle/_ref)
+                  running ml_run on the same .mlb file on this host's cores,
+                  on a bounded sample: an 8-token prompt and 16 greedy
+                  decode tokens
+"""
+import argparse
+import ctypes as C
+import json
+import os
+import re
+import shutil
+import subprocess
+import sys
+import tempfile
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "isa-lm_amd"))
+
+METRIC = "decode tok/s (bs=1) + prefill tok/s on 1 MI355X; matvec HBM GB/s vs peak"
+HBM_PEAK_GBS = 8000.0
+REF_DIR = os.path.join(ROOT, "oracle", "_ref")
+
+WORKLOADS = {
+    "llama8b_q8": ("llama3-8b-shape Q8_0 (f16 scales, 8.53 GB): 2048-token random prompt prefill, "
+                   "then greedy decode, batch 1", 2048),
+    "llama1b_mixed": ("llama3.2-1b-shape Q4_0 with Q8_0 v/o/down (f16 scales): 4000-token random prompt "
+                      "prefill, then greedy decode over the 4096 KV cache, batch 1", 4000),
+    "qwen05b_mixed": ("qwen2.5-0.5b-shape Q4_0 with Q8_0 v/o/down, tied, QKV bias: 512-token random prompt "
+                      "prefill, then greedy decode, batch 1", 512),
+    "stories15m_q8": ("llama2.c-15M-shape Q8_0 (f32 scales): 8-token random prompt, then greedy decode, "
+                      "batch 1", 8),
+}
+
+
+def log(msg):
+    print("[bench] " + msg, file=sys.stderr, flush=True)
+
+
+def scratch_dir(nbytes):
+    for d in ("/dev/shm", tempfile.gettempdir()):
+        try:
+            if shutil.disk_usage(d).free > 2 * nbytes + (1 << 30):
+                return tempfile.mkdtemp(prefix="krbench_", dir=d)
+        except OSError:
+            pass
+    return tempfile.mkdtemp(prefix="krbench_")
+
+
+def mat_bytes(W):
+    n = W.rows * W.cols
+    return (n if W.type == 1 else n // 2) + (n // 32) * (2 if W.d16 else 4)
+
+
+def time_swiglu(K, model, state, reps):
+    """average duration (ms) of the fused w1/w3 matvec over all layers, and
+    its algorithmic bytes per launch"""
+    cfg = model.cfg
+    xq = K.host.kr_state_buffer(state.ptr, b"qa_dim")
+    xd = K.host.kr_state_buffer(state.ptr, b"qd_dim")
+    hq = K.host.kr_state_buffer(state.ptr, b"qa_hid")
+    hd = K.host.kr_state_buffer(state.ptr, b"qd_hid")
+    t = K.hip.krh_timer_new()
+    total, n, nbytes = 0.0, 0, None
+    for _ in range(reps):
+        for l in range(cfg.n_layers):
+            w1 = K.host.kr_model_device_mat(model.ptr, l, b"w1")
+            w3 = K.host.kr_model_device_mat(model.ptr, l, b"w3")
+            nbytes = mat_bytes(w1.contents) + mat_bytes(w3.contents)
+            K.hip.krh_timer_mark(t, 0)
+            K.hip.krh_matvec_swiglu_q8(hq, hd, None, w1, w3, xq, xd)
+            K.hip.krh_timer_mark(t, 1)
+            total += K.hip.krh_timer_ms(t)
+            n += 1
+    K.hip.krh_timer_free(t)
+    K.check(K.hip.krh_sync(), "swiglu timing")
+    return total / n, nbytes
+
+
+def matvec_microbench(K, iters=1000):
+    """GB/s of the plain matvec on the isolated shapes, resident and rotating"""
+    out = []
+    x = np.empty(4096, dtype=np.float32)
+    K.host.kr_gen_normal(x.ctypes.data, 4096, 9)
+    xb = K.DevBuf.of(x)
+    xq, xdb = K.DevBuf(4096), K.DevBuf(4 * 128)
+    K.hip.krh_quantize_q8(xq.ptr, xdb.ptr, xb.ptr, 4096, 1)
+    t = K.hip.krh_timer_new()
+    for typ, tname in ((2, "q4"), (1, "q8")):
+        for rows in (4096, 14336):
+            cols = 4096
+            nq = rows * cols if typ == 1 else rows * cols // 2
+            nd = rows * cols // 32
+            nbytes = nq + 2 * nd
+            q = np.empty(nq, dtype=np.uint8)
+            d = np.empty(nd, dtype=np.uint16)
+            K.host.kr_gen_matrix(q.ctypes.data, d.ctypes.data, rows, cols, typ, 11 + rows + typ, 16)
+            copies = max(1, -(-(1 << 30) // nbytes))
+            bufs = []
+            for _ in range(copies):
+                bufs.append((K.DevBuf.of(q), K.DevBuf.of(d)))
+            yb = K.DevBuf(4 * rows)
+            mats = [K.KrhMat(bq.ptr, bd.ptr, rows, cols, typ, 1) for bq, bd in bufs]
+            res = {}
+            for mode, seq in (("resident", [mats[0]] * iters), ("rotating", [mats[i % copies] for i in range(iters)])):
+                for w in seq[:10]:
+                    K.hip.krh_matvec(yb.ptr, C.byref(w), xq.ptr, xdb.ptr, 0)
+                K.hip.krh_timer_mark(t, 0)
+                for w in seq:
+                    K.hip.krh_matvec(yb.ptr, C.byref(w), xq.ptr, xdb.ptr, 0)
+                K.hip.krh_timer_mark(t, 1)
+                ms = K.hip.krh_timer_ms(t)
+                res[mode] = round(nbytes * iters / (ms * 1e-3) / 1e9, 1)
+            K.check(K.hip.krh_sync(), "matvec microbench")
+            out.append({"shape": "%s %dx%d f16" % (tname, rows, cols), "bytes": nbytes,
+                        "gbs_resident": res["resident"], "gbs_hbm_rotating": res["rotating"],
+                        "frac_hbm_rotating": round(res["rotating"] / HBM_PEAK_GBS, 3)})
+            for bq, bd in bufs:
+                bq.free()
+                bd.free()
+            yb.free()
+    K.hip.krh_timer_free(t)
+    for b in (xb, xq, xdb):
+        b.free()
+    return out
+
+
+def cpu_baseline(path, prompt, decode):
+    """the reference's ml_run on the same model file, on this host's cores"""
+    cores = min(64, len(os.sched_getaffinity(0)))
+    n = len(prompt) - 1 + decode
+    for isa in ("avx512vnni", "avx2"):
+        exe = os.path.join(REF_DIR, isa, "ml_run")
+        if not os.path.exists(exe):
+            continue
+        cmd = [exe, path, "--tokens", ",".join(str(int(t)) for t in prompt), "-n", str(n), "-T", "0",
+               "-t", str(cores)]
+        r = subprocess.run(cmd, capture_output=True, text=True, timeout=600)
+        if r.returncode == 3:   # the reference's ISA guard: this CPU lacks the ISA
+            continue
+        if r.returncode != 0:
+            return {"value": None, "error": "ml_run %s exited %d: %s" % (isa, r.returncode, r.stderr[-300:])}
+        pm = re.search(r"prefill: (\d+) tokens in ([\d.]+) ms", r.stderr)
+        qm = re.search(r"positions: (\d+), tok/s: ([\d.]+)", r.stderr)
+        P, M = int(pm.group(1)), float(pm.group(2))
+        pos, X = int(qm.group(1)), float(qm.group(2))
+        dec = (pos - P) / (pos / X - M / 1000.0)
+        cpu = ""
+        try:
+            with open("/proc/cpuinfo") as f:
+                cpu = next((l.split(":", 1)[1].strip() for l in f if l.startswith("model name")), "")
+        except OSError:
+            pass
+        return {"value": round(dec, 3), "unit": "tok/s", "cores": cores, "kind": "reference",
+                "build": "ISA=%s THREADS=pthread" % isa, "cpu": cpu,
+                "sample": "ml_run on the same .mlb: %d-token prompt (%d prefilled), %d greedy decode tokens "
+                          "at positions %d..%d; decode tok/s = (positions - prefilled) / (positions / tok/s - "
+                          "prefill s)" % (len(prompt), P, pos - P, P, pos - 1),
+                "prefill_tok_s": round(P / (M / 1000.0), 2) if M > 0 else None}
+    return {"value": None, "error": "no reference CPU build in oracle/_ref (build() needs the reference sources)"}
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=256, help="timed decode tokens")
+    ap.add_argument("--warmup", type=int, default=16, help="untimed decode tokens before the timed run")
+    ap.add_argument("--workload", default="llama8b_q8", choices=sorted(WORKLOADS))
+    ap.add_argument("--prompt", type=int, default=None, help="prompt tokens (default: the workload's)")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-matvec", action="store_true")
+    ap.add_argument("--roofline-reps", type=int, default=3)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (the decode step would shard "
+              "by output rows; see the design notes). Run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+
+    import krafla as K
+    K.init_device()
+    desc, P = WORKLOADS[args.workload]
+    if args.prompt:
+        P = args.prompt
+    spec = dict(K.CONFIGS[args.workload], device=1)
+    V = spec["vocab"]
+    if P - 1 + max(args.steps, args.warmup) > spec["max_seq"]:
+        sys.exit("prompt + steps exceed max_seq %d" % spec["max_seq"])
+    est = 9 << 30 if args.workload == "llama8b_q8" else 2 << 30
+    tmp = scratch_dir(est)
+    path = os.path.join(tmp, args.workload + ".mlb")
+    try:
+        t0 = time.time()
+        K.gen_mlb(path, **spec)
+        log("generated %s (%.2f GB) in %.1f s" % (path, os.path.getsize(path) / 1e9, time.time() - t0))
+        t0 = time.time()
+        model = K.Model(path)
+        state = K.State(model)
+        dev_bytes = K.host.kr_model_device_bytes(model.ptr)
+        log("uploaded %.2f GB to HBM in %.1f s" % (dev_bytes / 1e9, time.time() - t0))
+        prompt = np.random.default_rng(2048).integers(1, V, P).astype(np.int32)
+
+        ids_w, pre_w, _ = state.generate(prompt, P - 1 + args.warmup)
+        log("warmup: prefill %d tokens %.3f s, %d decode tokens" % (P - 1, pre_w, args.warmup))
+        ids, pre_s, dec_s = state.generate(prompt, P - 1 + args.steps)
+        n = min(len(ids_w), len(ids))
+        deterministic = bool(np.array_equal(ids[:n], ids_w[:n]))
+        tok_s = args.steps / dec_s
+        prefill_tok_s = (P - 1) / pre_s if P > 1 else None
+        log("timed: %d decode tokens in %.3f s (%.2f tok/s), prefill %.1f tok/s, ids deterministic: %s"
+            % (args.steps, dec_s, tok_s, prefill_tok_s or 0.0, deterministic))
+
+        ms, nbytes = time_swiglu(K, model, state, args.roofline_reps)
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        log("swiglu matvec: %.1f us per launch, %.1f GB/s" % (ms * 1e3, gbs))
+        cfg = model.cfg
+        per_tok = 0
+        for l in range(cfg.n_layers):
+            for w in (b"wq", b"wk", b"wv", b"wo", b"w1", b"w2", b"w3"):
+                per_tok += mat_bytes(K.host.kr_model_device_mat(model.ptr, l, w).contents)
+        per_tok += mat_bytes(K.host.kr_model_device_mat(model.ptr, 0, b"wcls").contents)
+        # F32 KV cache: keys and values of positions 0..p read, row p written,
+        # at the mean position of the timed tokens
+        p_mean = P - 1 + (args.steps - 1) / 2.0
+        kv_tok = int(2 * cfg.n_layers * (p_mean + 2) * cfg.kv_dim * 4)
+        mv = None if args.no_matvec else matvec_microbench(K)
+        if mv:
+            for r in mv:
+                log("matvec %s: %.1f GB/s resident, %.1f GB/s rotating" % (r["shape"], r["gbs_resident"],
+                                                                           r["gbs_hbm_rotating"]))
+        cpu = None
+        if not args.no_cpu_baseline:
+            t0 = time.time()
+            cpu = cpu_baseline(path, prompt[:8], 16)
+            log("cpu baseline (%.1f s): %s" % (time.time() - t0, json.dumps(cpu)))
+        state.close()
+        model.close()
+    finally:
+        shutil.rmtree(tmp, ignore_errors=True)
+
+    line = {
+        "metric": METRIC, "value": round(tok_s, 3), "unit": "tok/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(1e3 * dec_s / args.steps, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "int8", "data": "synthetic",
+        "config": {"workload": desc, "prompt_tokens": P, "prefilled_tokens": P - 1, "decode_tokens": args.steps,
+                   "first_decode_position": P - 1, "weight_bytes_per_token": per_tok,
+                   "kv_bytes_per_token": kv_tok,
+                   "decode_roofline_tok_s": round(HBM_PEAK_GBS * 1e9 / (per_tok + kv_tok), 1),
+                   "parallelism": "single GPU"},
+        "prefill_tok_s": round(prefill_tok_s, 2) if prefill_tok_s else None,
+        "decode_frac_of_hbm_roofline": round(tok_s * (per_tok + kv_tok) / (HBM_PEAK_GBS * 1e9), 4),
+        "deterministic_ids": deterministic,
+        "roofline": {"bound": "hbm", "kernel": "k_matvec<EPI_SWIGLU> (w1|w3 + SiLU*up + quantize_q8)",
+                     "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "bytes_per_launch": nbytes, "avg_launch_us": round(ms * 1e3, 2)},
+        "matvec": mv,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

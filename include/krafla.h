@@ -77,6 +77,7 @@ typedef struct {
     float std;             /* weight and embedding std (0.02) */
     uint64_t seed;
     int threads;
+    int device;            /* draw the matrices on the GPU (krh_gen_blocks) */
 } kr_gen_spec;
 /* Writes an .mlb: matrices and embedding N(0, std^2), norms 1 + 0.01 N,
  * biases 0.02 N, quantized by the format's rules (docs/file-format.md:133-159). */

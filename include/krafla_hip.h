@@ -115,6 +115,13 @@ void krh_take_token(int *tok, const int *prompt, const int *pos);
 /* *pos += 1 */
 void krh_advance(int *pos);
 
+/* ---- synthetic data ---- */
+/* Random quantized matrix [rows][cols] on the device: normals of the host
+ * generator's stream `key` (include/krafla.h, kr_gen_mlb) times std,
+ * quantized per 32-block by the .mlb writer rules; q: rows*cols (Q8) or
+ * rows*cols/2 bytes, d: rows*cols/32 scales, f16 when f16 != 0. */
+void krh_gen_blocks(void *q, void *d, uint64_t key, int rows, int cols, int type, int f16, float std);
+
 /* ---- self-checks for tests ---- */
 /* y[i] = op(a[i], b[i]) as the kernels compute it: expf(a), sqrtf(a), a / b,
  * or rmsnorm's 1 / sqrtf(a / b + 1e-5) */

@@ -231,39 +231,52 @@ constexpr int SW_R = 32;
 
 // ---- rmsnorm + quantize, quantize ----
 
-// One workgroup per token: lane 0 sums x_i * x_i in index order
-// (k_scalar.c:61), then every lane forms (x * inv) * w and the half-waves
-// quantize their 32-element blocks.
-__global__ void __launch_bounds__(256) k_rmsnorm_q8(int8_t *q, float *d, float *xb, const float *x, const float *w,
-                                                    int n, float eps, int norm) {
+// One workgroup per token. The squares x_i * x_i are formed in parallel into
+// LDS (each one rounded product, as in the scalar loop), then lane 0 adds them
+// in index order (k_scalar.c:61) from LDS, RN_CHUNK floats at a time; then
+// every lane forms (x * inv) * w and the half-waves quantize their 32-element
+// blocks (k_scalar.c:39-57). n % 32 == 0; x rows 16-byte aligned.
+constexpr int RN_THREADS = 256, RN_CHUNK = 8192;
+
+__global__ void __launch_bounds__(RN_THREADS) k_rmsnorm_q8(int8_t *q, float *d, float *xb, const float *x,
+                                                           const float *w, int n, float eps, int norm) {
     const size_t t = blockIdx.x;
+    const int tid = threadIdx.x;
     x += t * n;
     q += t * n;
     d += t * (n / KR_QK);
     if (xb) xb += t * n;
+    __shared__ __align__(16) float sq[RN_CHUNK];
     __shared__ float s_inv;
     if (norm) {
-        if (threadIdx.x == 0) {
-            float ss = 0.0f;
-            int i = 0;
-            if ((n & 3) == 0 && ((uintptr_t)x & 15) == 0) {
-#pragma unroll 4
-                for (; i < n; i += 4) {
-                    const float4 v = *(const float4 *)(x + i);
-                    ss = kr_fadd(ss, kr_fmul(v.x, v.x));
-                    ss = kr_fadd(ss, kr_fmul(v.y, v.y));
-                    ss = kr_fadd(ss, kr_fmul(v.z, v.z));
-                    ss = kr_fadd(ss, kr_fmul(v.w, v.w));
+        float ss = 0.0f;   // lane 0's running sum
+        for (int c0 = 0; c0 < n; c0 += RN_CHUNK) {
+            const int cn = min(RN_CHUNK, n - c0);
+            for (int i = 4 * tid; i < cn; i += 4 * RN_THREADS) {
+                const float4 v = *(const float4 *)(x + c0 + i);
+                *(float4 *)(sq + i) = make_float4(kr_fmul(v.x, v.x), kr_fmul(v.y, v.y), kr_fmul(v.z, v.z),
+                                                  kr_fmul(v.w, v.w));
+            }
+            __syncthreads();
+            if (tid == 0) {
+                const float4 *p = (const float4 *)sq;
+#pragma unroll 16
+                for (int i = 0; i < cn / 4; i++) {
+                    const float4 v = p[i];
+                    ss = kr_fadd(ss, v.x);
+                    ss = kr_fadd(ss, v.y);
+                    ss = kr_fadd(ss, v.z);
+                    ss = kr_fadd(ss, v.w);
                 }
             }
-            for (; i < n; i++) ss = kr_fadd(ss, kr_fmul(x[i], x[i]));
-            s_inv = kr_fdiv(1.0f, kr_fsqrt(kr_fadd(kr_fdiv(ss, (float)n), eps)));
+            __syncthreads();
         }
+        if (tid == 0) s_inv = kr_fdiv(1.0f, kr_fsqrt(kr_fadd(kr_fdiv(ss, (float)n), eps)));
         __syncthreads();
     }
     const float inv = norm ? s_inv : 1.0f;
-    for (int base = 0; base < n; base += 256) {
-        const int i = base + threadIdx.x;
+    for (int base = 0; base < n; base += RN_THREADS) {
+        const int i = base + tid;
         if (i < n) {   // n % 32 == 0: a half-wave is all in or all out
             const float o = norm ? kr_fmul(kr_fmul(x[i], inv), w[i]) : x[i];
             if (xb) xb[i] = o;
@@ -296,89 +309,191 @@ __global__ void k_embed(float *x, const KMat e, const int *tok, float scale) {
 }
 
 // ---- attention (F32 cache) ----
+//
+// Per layer and position (ops/ops.c:124-155): for query head h (KV head
+// h / group), s_t = (sum_i q_i k_t,i in index order) * scale
+// (k_scalar.c:111-117), softmax over t (k_scalar.c:66-77: max, expf(x - max),
+// the sum in position order, then x * (1 / sum)), and out_i = 0,
+// out_i += a_t v_t,i in position order (k_scalar.c:119-122). The ordered
+// chains run from LDS; the loads feeding them are wide and parallel.
 
-// Scores of one KV head's query heads for 64 positions: lane = position,
-// s = (sum_i q_i k_i in index order) * scale (k_scalar.c:111-117).
-__global__ void __launch_bounds__(64) k_attn_scores(float *att, const float *q, const float *kc, int group, int hd,
-                                                    int kv_dim, int max_seq, int window, float scale, const int *pos_p) {
-    extern __shared__ float qs[];
-    const int pos = *pos_p, first = window && pos >= window ? pos + 1 - window : 0, n = pos + 1 - first;
-    const int g = blockIdx.x, t0 = blockIdx.y * 64;
+constexpr int AT_T = 64;          // positions per score tile
+constexpr int AT_THREADS = 256;
+
+__device__ __forceinline__ void attn_range(const int *pos_p, int window, int *first, int *n) {
+    const int pos = *pos_p;
+    *first = window && pos >= window ? pos + 1 - window : 0;
+    *n = pos + 1 - *first;
+}
+
+// Scores of one KV head's query heads for AT_T positions. The K tile is staged
+// in LDS (row stride hd + 1: the lanes of a wave read distinct banks); thread
+// (t, j) computes heads j, j + 4, ... of the group for position t.
+__global__ void __launch_bounds__(AT_THREADS) k_attn_scores(float *att, const float *q, const float *kc, int group,
+                                                            int hd, int kv_dim, int max_seq, int window, float scale,
+                                                            const int *pos_p) {
+    extern __shared__ __align__(16) float at_smem[];
+    int first, n;
+    attn_range(pos_p, window, &first, &n);
+    const int g = blockIdx.x, t0 = blockIdx.y * AT_T, tid = threadIdx.x;
     if (t0 >= n) return;
-    for (int i = threadIdx.x; i < group * hd; i += 64) qs[i] = q[(size_t)g * group * hd + i];
+    const int nt = min(AT_T, n - t0), ks = hd + 1;
+    float *qs = at_smem, *kt = at_smem + group * hd;
+    for (int i = tid; i < group * hd; i += AT_THREADS) qs[i] = q[(size_t)g * group * hd + i];
+    const int h4 = hd / 4;
+    for (int e = tid; e < nt * h4; e += AT_THREADS) {
+        const int r = e / h4, c = e - r * h4;
+        const float4 v = *(const float4 *)(kc + (size_t)(first + t0 + r) * kv_dim + (size_t)g * hd + 4 * c);
+        float *dst = kt + r * ks + 4 * c;
+        dst[0] = v.x; dst[1] = v.y; dst[2] = v.z; dst[3] = v.w;
+    }
     __syncthreads();
-    const int t = t0 + threadIdx.x;
-    if (t >= n) return;
-    const float2 *k = (const float2 *)(kc + (size_t)(first + t) * kv_dim + (size_t)g * hd);
-    for (int h0 = 0; h0 < group; h0 += 4) {
-        const int nh = min(4, group - h0);
-        float acc[4] = { 0.0f, 0.0f, 0.0f, 0.0f };
-        for (int i = 0; i < hd / 2; i++) {
-            const float2 kv = k[i];
-#pragma unroll
-            for (int j = 0; j < 4; j++)
-                if (j < nh) {
-                    acc[j] = kr_fadd(acc[j], kr_fmul(qs[(h0 + j) * hd + 2 * i], kv.x));
-                    acc[j] = kr_fadd(acc[j], kr_fmul(qs[(h0 + j) * hd + 2 * i + 1], kv.y));
-                }
-        }
-        for (int j = 0; j < nh; j++) att[(size_t)(g * group + h0 + j) * max_seq + t] = kr_fmul(acc[j], scale);
+    const int t = tid % AT_T;
+    if (t >= nt) return;
+    const float *kr = kt + t * ks;
+    for (int j = tid / AT_T; j < group; j += AT_THREADS / AT_T) {
+        const float *qh = qs + j * hd;
+        float acc = 0.0f;
+#pragma unroll 8
+        for (int i = 0; i < hd; i++) acc = kr_fadd(acc, kr_fmul(qh[i], kr[i]));
+        att[(size_t)(g * group + j) * max_seq + t0 + t] = kr_fmul(acc, scale);
     }
 }
 
-// Softmax of one head's scores in place (k_scalar.c:66-77): max, expf,
-// the sum in position order by one lane, then x * (1 / sum).
-__global__ void __launch_bounds__(256) k_attn_softmax(float *att, int max_seq, int window, const int *pos_p) {
-    const int pos = *pos_p, first = window && pos >= window ? pos + 1 - window : 0, n = pos + 1 - first;
-    float *a = att + (size_t)blockIdx.x * max_seq;
-    __shared__ float red[4];
+// Softmax of one head's n scores in place, AT_CHUNK at a time through LDS.
+constexpr int AT_CHUNK = 8192;
+__global__ void __launch_bounds__(AT_THREADS) k_attn_softmax(float *att, int max_seq, int window, const int *pos_p) {
+    __shared__ __align__(16) float es[AT_CHUNK];
+    __shared__ float red[AT_THREADS / 64];
     __shared__ float s_inv;
+    int first, n;
+    attn_range(pos_p, window, &first, &n);
+    float *a = att + (size_t)blockIdx.x * max_seq;
+    const int tid = threadIdx.x;
     float m = -INFINITY;
-    for (int t = threadIdx.x; t < n; t += 256) m = fmaxf(m, a[t]);
+    for (int t = tid; t < n; t += AT_THREADS) m = fmaxf(m, a[t]);
     for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+    if ((tid & 63) == 0) red[tid >> 6] = m;
     __syncthreads();
-    const float mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-    if (mx == -INFINITY) {
-        for (int t = threadIdx.x; t < n; t += 256) a[t] = kr_fdiv(1.0f, (float)n);
+    float mx = red[0];
+    for (int k = 1; k < AT_THREADS / 64; k++) mx = fmaxf(mx, red[k]);
+    if (mx == -INFINITY) {   // every score -inf: the scalar loop's 1/n
+        for (int t = tid; t < n; t += AT_THREADS) a[t] = kr_fdiv(1.0f, (float)n);
         return;
     }
-    for (int t = threadIdx.x; t < n; t += 256) a[t] = kr_expf(kr_fsub(a[t], mx));
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        float sum = 0.0f;
-#pragma unroll 8
-        for (int t = 0; t < n; t++) sum = kr_fadd(sum, a[t]);
-        s_inv = kr_fdiv(1.0f, sum);
+    float sum = 0.0f;   // lane 0's running sum
+    for (int c0 = 0; c0 < n; c0 += AT_CHUNK) {
+        const int cn = min(AT_CHUNK, n - c0);
+        for (int t = tid; t < cn; t += AT_THREADS) {
+            const float e = kr_expf(kr_fsub(a[c0 + t], mx));
+            es[t] = e;
+            a[c0 + t] = e;
+        }
+        __syncthreads();
+        if (tid == 0) {
+            int t = 0;
+            const float4 *p = (const float4 *)es;
+#pragma unroll 16
+            for (; t + 4 <= cn; t += 4) {
+                const float4 v = p[t >> 2];
+                sum = kr_fadd(sum, v.x);
+                sum = kr_fadd(sum, v.y);
+                sum = kr_fadd(sum, v.z);
+                sum = kr_fadd(sum, v.w);
+            }
+            for (; t < cn; t++) sum = kr_fadd(sum, es[t]);
+        }
+        __syncthreads();
     }
+    if (tid == 0) s_inv = kr_fdiv(1.0f, sum);
     __syncthreads();
     const float inv = s_inv;
-    for (int t = threadIdx.x; t < n; t += 256) a[t] = kr_fmul(a[t], inv);
+    for (int t = tid; t < n; t += AT_THREADS) a[t] = kr_fmul(a[t], inv);
 }
 
-// Output of one (query head, dim) per lane: o = 0, then o += a_t * v_t,i in
-// position order (k_scalar.c:119-122); the 32-lane halves then quantize
-// their block of the output (q_dim % 32 == 0).
-__global__ void __launch_bounds__(64) k_attn_mix(float *ao, int8_t *aq, float *ad, const float *att, const float *vc,
-                                                 int q_dim, int group, int hd, int kv_dim, int max_seq, int window,
-                                                 const int *pos_p) {
-    const int pos = *pos_p, first = window && pos >= window ? pos + 1 - window : 0, n = pos + 1 - first;
-    const int slot = blockIdx.x * 64 + threadIdx.x;
-    if (slot >= q_dim) return;   // whole half-waves (q_dim % 32 == 0)
-    const int h = slot / hd, i = slot - h * hd, kvh = h / group;
-    const float *a = att + (size_t)h * max_seq;
-    const float *v = vc + (size_t)first * kv_dim + (size_t)kvh * hd + i;
+// out for one KV head's query heads and DW of their dims, one wave per
+// workgroup: lane = (head j of the group, dim d), DW = 64 / (group rounded up
+// to a power of two). Tiles of MX_TILE floats of V (MX_TILE / DW positions)
+// and the heads' weights for those positions are loaded MX_DEPTH tiles ahead
+// into registers, then passed through LDS; each lane runs its ordered chain
+// o += a_t * v_t,d (k_scalar.c:119-122). ao is written as floats (its
+// quantization happens where it is consumed).
+constexpr int MX_TILE = 1024;
+
+template <int DW>
+__global__ void __launch_bounds__(64) k_attn_mix(float *ao, const float *att, const float *vc, int group, int hd,
+                                                 int kv_dim, int max_seq, int window, const int *pos_p) {
+    constexpr int TP = MX_TILE / DW;         // positions per tile
+    constexpr int NV = MX_TILE / 4 / 64;     // float4 of V per lane per tile
+    constexpr int GP = 64 / DW;              // head slots per wave
+    constexpr int NA = (GP * TP + 255) / 256;   // float4 of weights per lane per tile
+    constexpr int MX_DEPTH = NA > 4 ? 2 : 6;    // tiles in flight
+    __shared__ __align__(16) float vt[2][MX_TILE];
+    __shared__ __align__(16) float aw[2][GP * TP];
+    int first, n;
+    attn_range(pos_p, window, &first, &n);
+    const int g = blockIdx.x, c0 = blockIdx.y * DW, lane = threadIdx.x;
+    const int j = lane / DW, d = lane % DW;
+    const float *vbase = vc + (size_t)first * kv_dim + (size_t)g * hd + c0;
+    const float *abase = att + (size_t)g * group * max_seq;
+    const int ntiles = (n + TP - 1) / TP;
+    const int cw = min(DW, hd - c0);         // valid dims of the chunk (multiple of 4)
+
+    float4 rv[MX_DEPTH][NV], ra[MX_DEPTH][NA];
+    auto load = [&](int tile, float4 *v, float4 *a) {
+        const int t0 = tile * TP;
+#pragma unroll
+        for (int k = 0; k < NV; k++) {
+            const int e = (k * 64 + lane) * 4, r = e / DW, c = e % DW;
+            v[k] = t0 + r < n && c < cw ? *(const float4 *)(vbase + (size_t)(t0 + r) * kv_dim + c)
+                                        : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        }
+#pragma unroll
+        for (int k = 0; k < NA; k++) {
+            const int e = (k * 64 + lane) * 4, jj = e / TP, r = e % TP;   // TP % 4 == 0
+            float4 x = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            if (jj < group && e < GP * TP) {
+                const float *src = abase + (size_t)jj * max_seq + t0 + r;
+                if (t0 + r + 3 < n) x = make_float4(src[0], src[1], src[2], src[3]);
+                else {
+                    if (t0 + r < n) x.x = src[0];
+                    if (t0 + r + 1 < n) x.y = src[1];
+                    if (t0 + r + 2 < n) x.z = src[2];
+                }
+            }
+            a[k] = x;
+        }
+    };
+#pragma unroll
+    for (int s = 0; s < MX_DEPTH; s++)
+        if (s < ntiles) load(s, rv[s], ra[s]);
     float o = 0.0f;
-#pragma unroll 8
-    for (int t = 0; t < n; t++) o = kr_fadd(o, kr_fmul(a[t], v[(size_t)t * kv_dim]));
-    ao[slot] = o;
-    if (aq) {
-        int8_t q;
-        float d;
-        kr_quant_block32(o, &q, &d);
-        aq[slot] = q;
-        if ((slot & 31) == 0) ad[slot >> 5] = d;
+    for (int k0 = 0; k0 < ntiles; k0 += MX_DEPTH) {
+#pragma unroll
+        for (int s = 0; s < MX_DEPTH; s++) {
+            const int tile = k0 + s;
+            if (tile >= ntiles) break;
+            float *V = vt[s & 1], *A = aw[s & 1];
+#pragma unroll
+            for (int k = 0; k < NV; k++) *(float4 *)(V + (k * 64 + lane) * 4) = rv[s][k];
+#pragma unroll
+            for (int k = 0; k < NA; k++) {
+                const int e = (k * 64 + lane) * 4;
+                if (e < GP * TP) *(float4 *)(A + e) = ra[s][k];
+            }
+            if (tile + MX_DEPTH < ntiles) load(tile + MX_DEPTH, rv[s], ra[s]);
+            __syncthreads();
+            const int nt = min(TP, n - tile * TP);
+            const float *ap = A + j * TP, *vp = V + d;
+            if (nt == TP) {
+#pragma unroll 16
+                for (int r = 0; r < TP; r++) o = kr_fadd(o, kr_fmul(ap[r], vp[r * DW]));
+            } else {
+                for (int r = 0; r < nt; r++) o = kr_fadd(o, kr_fmul(ap[r], vp[r * DW]));
+            }
+        }
     }
+    if (j < group && d < cw) ao[(size_t)(g * group + j) * hd + c0 + d] = o;
 }
 
 // ---- greedy pick ----
@@ -551,18 +666,28 @@ extern "C" void krh_matvec_swiglu_q8(int8_t *hq, float *hd, float *hb, const krh
 extern "C" void krh_attention(float *ao, int8_t *aq, float *ad, float *att, const float *q, const float *kc,
                               const float *vc, int n_heads, int n_kv_heads, int head_dim, int max_seq, int window,
                               float scale, const int *pos) {
-    if (n_kv_heads <= 0 || n_heads % n_kv_heads || head_dim % 2 || (n_heads * head_dim) % KR_QK) {
+    if (n_kv_heads <= 0 || n_heads % n_kv_heads || head_dim % 4 || (n_heads * head_dim) % KR_QK ||
+        n_heads / n_kv_heads > 16 || head_dim > 1024) {
         kr_fail(ML_E_SHAPE, "attention shape", hipSuccess);
         return;
     }
     const int group = n_heads / n_kv_heads, kv_dim = n_kv_heads * head_dim, q_dim = n_heads * head_dim;
-    hipLaunchKernelGGL(k_attn_scores, dim3(n_kv_heads, (max_seq + 63) / 64), dim3(64),
-                       sizeof(float) * group * head_dim, kr_stream(), att, q, kc, group, head_dim, kv_dim, max_seq,
-                       window, scale, pos);
-    hipLaunchKernelGGL(k_attn_softmax, dim3(n_heads), dim3(256), 0, kr_stream(), att, max_seq, window, pos);
-    hipLaunchKernelGGL(k_attn_mix, dim3((q_dim + 63) / 64), dim3(64), 0, kr_stream(), ao, aq, ad, att, vc, q_dim,
-                       group, head_dim, kv_dim, max_seq, window, pos);
+    const size_t lds = sizeof(float) * ((size_t)group * head_dim + (size_t)AT_T * (head_dim + 1));
+    hipLaunchKernelGGL(k_attn_scores, dim3(n_kv_heads, (max_seq + AT_T - 1) / AT_T), dim3(AT_THREADS), lds,
+                       kr_stream(), att, q, kc, group, head_dim, kv_dim, max_seq, window, scale, pos);
+    hipLaunchKernelGGL(k_attn_softmax, dim3(n_heads), dim3(AT_THREADS), 0, kr_stream(), att, max_seq, window, pos);
+    const int gp = group <= 1 ? 1 : group <= 2 ? 2 : group <= 4 ? 4 : group <= 8 ? 8 : 16;
+    const int dw = 64 / gp;
+    const dim3 grid(n_kv_heads, (head_dim + dw - 1) / dw);
+    switch (dw) {
+    case 64: hipLaunchKernelGGL(k_attn_mix<64>, grid, dim3(64), 0, kr_stream(), ao, att, vc, group, head_dim, kv_dim, max_seq, window, pos); break;
+    case 32: hipLaunchKernelGGL(k_attn_mix<32>, grid, dim3(64), 0, kr_stream(), ao, att, vc, group, head_dim, kv_dim, max_seq, window, pos); break;
+    case 16: hipLaunchKernelGGL(k_attn_mix<16>, grid, dim3(64), 0, kr_stream(), ao, att, vc, group, head_dim, kv_dim, max_seq, window, pos); break;
+    case 8: hipLaunchKernelGGL(k_attn_mix<8>, grid, dim3(64), 0, kr_stream(), ao, att, vc, group, head_dim, kv_dim, max_seq, window, pos); break;
+    default: hipLaunchKernelGGL(k_attn_mix<4>, grid, dim3(64), 0, kr_stream(), ao, att, vc, group, head_dim, kv_dim, max_seq, window, pos); break;
+    }
     kr_check_launch("attention");
+    if (aq) krh_quantize_q8(aq, ad, ao, q_dim, 1);
 }
 
 extern "C" void krh_argmax(int *tok, const float *logits, int n, int *pos, int *log) {

@@ -133,7 +133,7 @@ static void run_jobs(mat_job *proto, int threads, void *(*fn)(void *)) {
     for (int i = 0; i < threads; i++) pthread_join(th[i], NULL);
 }
 
-typedef struct { FILE *f; size_t off; int ok; } writer;
+typedef struct { FILE *f; size_t off; int ok; uint8_t *dev; } writer;
 
 static void put(writer *w, const void *p, size_t n) {
     static const uint8_t zero[ML_ALIGN] = { 0 };
@@ -144,12 +144,19 @@ static void put(writer *w, const void *p, size_t n) {
     w->off += pad;
 }
 
+/* threads < 0: draw on the device (krh_gen_blocks) into w->dev */
 static void put_mat(writer *w, uint64_t key, int rows, int cols, int type, int f16, float std, int threads) {
     const size_t n = (size_t)rows * cols, nq = type == ML_Q8_0 ? n : n / 2, nd = n / QK * (f16 ? 2 : 4);
     uint8_t *q = malloc(nq), *d = malloc(nd);
     if (!q || !d) { w->ok = 0; free(q); free(d); return; }
-    mat_job j = { key, rows, cols, type, f16, std, q, d, 0, rows };
-    run_jobs(&j, threads, mat_rows);
+    if (threads < 0) {
+        uint8_t *dq = w->dev, *dd = w->dev + ((nq + 255) & ~(size_t)255);
+        krh_gen_blocks(dq, dd, key, rows, cols, type, f16, std);
+        if (krh_copy_d2h(q, dq, nq) != ML_OK || krh_copy_d2h(d, dd, nd) != ML_OK) w->ok = 0;
+    } else {
+        mat_job j = { key, rows, cols, type, f16, std, q, d, 0, rows };
+        run_jobs(&j, threads, mat_rows);
+    }
     put(w, q, nq);
     put(w, d, nd);
     free(q);
@@ -189,11 +196,26 @@ ml_status kr_gen_mlb(const char *path, const kr_gen_spec *sp) {
     int shared;
     ml_status st = kr_parse_header(&c, &shared, h);
     if (st != ML_OK) return kr_seterr(st, "generator: invalid model shape");
+    uint8_t *dev = NULL;
+    if (sp->device) {
+        /* room for the largest matrix: quants then scales */
+        size_t big = 0;
+        const size_t dims[4][2] = { { (size_t)c.vocab, (size_t)c.dim }, { (size_t)c.q_dim, (size_t)c.dim },
+                                    { (size_t)c.hidden_dim, (size_t)c.dim }, { (size_t)c.dim, (size_t)c.q_dim } };
+        for (int i = 0; i < 4; i++) {
+            const size_t n = dims[i][0] * dims[i][1], b = ((n + 255) & ~(size_t)255) + n / QK * 4;
+            big = b > big ? b : big;
+        }
+        st = krh_init();
+        if (st != ML_OK) return kr_seterr(st, "%s", krh_last_error());
+        dev = krh_alloc(big);
+        if (!dev) return kr_seterr(ML_E_NOMEM, "generator: cannot allocate %zu bytes of HBM", big);
+    }
     FILE *f = fopen(path, "wb");
-    if (!f) return kr_seterr(ML_E_IO, "cannot write %s", path);
-    writer w = { f, 0, 1 };
+    if (!f) { krh_free(dev); return kr_seterr(ML_E_IO, "cannot write %s", path); }
+    writer w = { f, 0, 1, dev };
     put(&w, h, sizeof h);
-    const int f16 = sp->scale_f16, th = sp->threads;
+    const int f16 = sp->scale_f16, th = sp->device ? -1 : sp->threads;
     const float sd = sp->std > 0.0f ? sp->std : 0.02f;
     uint64_t s = 0;
 #define WT(bits) (c.wtype == ML_Q8_0 || (c.q8_mask & (bits)) ? ML_Q8_0 : ML_Q4_0)
@@ -218,6 +240,7 @@ ml_status kr_gen_mlb(const char *path, const kr_gen_spec *sp) {
     if (!shared) put_mat(&w, stream_key(sp->seed, s++), c.vocab, c.dim, WT(ML_Q8M_CLS), f16, sd, th);
 #undef WT
     if (fclose(f) != 0) w.ok = 0;
+    krh_free(dev);
     return w.ok ? ML_OK : kr_seterr(ML_E_IO, "write failed: %s", path);
 }
 

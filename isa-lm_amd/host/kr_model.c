@@ -177,6 +177,7 @@ struct kr_state {
     int *h_ints;              /* pinned: tok, pos */
     krh_graph *g_logits, *g_greedy, *g_prefill;
     int batch;
+    int eager;                /* issue ops directly instead of replaying graphs */
 };
 
 /* model/transformer.c:16-38: inverse frequency of rotary pair i */
@@ -251,15 +252,36 @@ static void issue_step(kr_state *s, int cls) {
     krh_matvec(s->logits, &m->d_wcls, s->qa_dim, s->qd_dim, 0);
 }
 
+enum { STEP_LOGITS = 0, STEP_GREEDY = 1, STEP_PREFILL = 2 };
+
+/* The ops of one replayed step: STEP_LOGITS (ml_forward), STEP_GREEDY
+ * (ml_forward + the greedy pick, appended to the id log), STEP_PREFILL (the
+ * next prompt token into the cache, no classifier). */
+static void issue(kr_state *s, int kind) {
+    if (kind == STEP_PREFILL) krh_take_token(s->tok, s->prompt, s->pos);
+    issue_step(s, kind != STEP_PREFILL);
+    if (kind == STEP_GREEDY) krh_argmax(s->tok, s->logits, s->m->cfg.vocab, s->pos, s->log);
+    if (kind == STEP_PREFILL) krh_advance(s->pos);
+}
+
 static ml_status capture(kr_state *s, krh_graph **g, int kind) {
     ml_status st = krh_graph_begin();
     if (st != ML_OK) return kr_seterr(st, "%s", krh_last_error());
-    if (kind == 2) krh_take_token(s->tok, s->prompt, s->pos);
-    issue_step(s, kind != 2);
-    if (kind == 1) krh_argmax(s->tok, s->logits, s->m->cfg.vocab, s->pos, s->log);
-    if (kind == 2) krh_advance(s->pos);
+    issue(s, kind);
     st = krh_graph_end(g);
     return st == ML_OK ? ML_OK : kr_seterr(st, "%s", krh_last_error());
+}
+
+/* Runs a step: replays its graph, or issues its ops one by one when the
+ * state is eager (KRAFLA_EAGER=1 in the environment: for profilers that
+ * trace kernel dispatches, and for debugging) */
+static ml_status run_step(kr_state *s, int kind) {
+    if (s->eager) {
+        issue(s, kind);
+        return krh_status();
+    }
+    const krh_graph *g = kind == STEP_LOGITS ? s->g_logits : kind == STEP_GREEDY ? s->g_greedy : s->g_prefill;
+    return krh_graph_launch(g);
 }
 
 ml_status kr_state_new(kr_state **out, kr_model *m, int kv_type) {
@@ -317,9 +339,11 @@ ml_status kr_state_new(kr_state **out, kr_model *m, int kv_type) {
     if (st == ML_OK && local) st = krh_copy_h2d(s->rope_cos_l, csl, f * half);
     if (st == ML_OK && local) st = krh_copy_h2d(s->rope_sin_l, snl, f * half);
     free(cs); free(sn); free(csl); free(snl);
-    if (st == ML_OK) st = capture(s, &s->g_logits, 0);
-    if (st == ML_OK) st = capture(s, &s->g_greedy, 1);
-    if (st == ML_OK) st = capture(s, &s->g_prefill, 2);
+    const char *ev = getenv("KRAFLA_EAGER");
+    s->eager = ev && ev[0] == '1';
+    if (st == ML_OK && !s->eager) st = capture(s, &s->g_logits, STEP_LOGITS);
+    if (st == ML_OK && !s->eager) st = capture(s, &s->g_greedy, STEP_GREEDY);
+    if (st == ML_OK && !s->eager) st = capture(s, &s->g_prefill, STEP_PREFILL);
     if (st != ML_OK) {
         kr_state_free(s);
         return kr_seterr(st, "%s", krh_last_error());
@@ -369,7 +393,7 @@ ml_status kr_forward(kr_state *s, int token, int pos, float *logits) {
     const ml_config *c = &s->m->cfg;
     if (pos < 0 || pos >= c->max_seq || token < 0 || token >= c->vocab) return ML_E_SHAPE;
     ml_status st = set_ints(s, token, pos);
-    if (st == ML_OK) st = krh_graph_launch(s->g_logits);
+    if (st == ML_OK) st = run_step(s, STEP_LOGITS);
     if (st == ML_OK && logits) st = krh_copy_d2h(logits, s->logits, sizeof(float) * c->vocab);
     return st == ML_OK ? dev_status() : st;
 }
@@ -391,7 +415,7 @@ ml_status kr_prefill(kr_state *s, const int *tokens, int n, int pos0, float *log
     if (n == 0) return ML_OK;
     ml_status st = krh_copy_h2d(s->prompt + pos0, tokens, sizeof(int) * (size_t)n);
     if (st == ML_OK) st = set_ints(s, 0, pos0);
-    for (int i = 0; st == ML_OK && i < n; i++) st = krh_graph_launch(s->g_prefill);
+    for (int i = 0; st == ML_OK && i < n; i++) st = run_step(s, STEP_PREFILL);
     return st == ML_OK ? dev_status() : st;
 }
 
@@ -421,7 +445,7 @@ int kr_generate(kr_state *s, const int *prompt, int np, int steps, int *out, dou
         const int first = pos;
         if (set_ints(s, token, pos) != ML_OK) return -1;
         for (; pos < steps; pos++)
-            if (krh_graph_launch(s->g_greedy) != ML_OK) return -1;
+            if (run_step(s, STEP_GREEDY) != ML_OK) return -1;
         if (dev_status() != ML_OK) return -1;
         if (krh_copy_d2h(out + n, s->log + first + 1, sizeof(int) * (size_t)(steps - first)) != ML_OK) return -1;
         n += steps - first;

@@ -52,7 +52,7 @@ class GenSpec(C.Structure):
         ("rope_theta", C.c_float), ("norm_eps", C.c_float), ("wtype", C.c_int), ("q8_mask", C.c_uint),
         ("shared", C.c_int), ("qkv_bias", C.c_int), ("scale_f16", C.c_int), ("rope_type", C.c_int),
         ("rope_factor", C.c_float), ("rope_low_freq_factor", C.c_float), ("rope_high_freq_factor", C.c_float),
-        ("rope_orig_max_seq", C.c_int), ("std", C.c_float), ("seed", C.c_uint64), ("threads", C.c_int)]
+        ("rope_orig_max_seq", C.c_int), ("std", C.c_float), ("seed", C.c_uint64), ("threads", C.c_int), ("device", C.c_int)]
 
 
 # The workloads, by name. Shapes and quantization as the benchmark configs
@@ -63,7 +63,7 @@ class GenSpec(C.Structure):
 def _spec(**kw):
     base = dict(rope_theta=1e4, norm_eps=1e-5, wtype=ML_Q8_0, q8_mask=0, shared=0, qkv_bias=0, scale_f16=0,
                 rope_type=ML_ROPE_NONE, rope_factor=0.0, rope_low_freq_factor=0.0, rope_high_freq_factor=0.0,
-                rope_orig_max_seq=0, std=0.02, seed=1, threads=8)
+                rope_orig_max_seq=0, std=0.02, seed=1, threads=8, device=0)
     base.update(kw)
     return base
 
@@ -117,6 +117,7 @@ for name, res, args in [
     ("krh_take_token", None, [_P, _P, _P]), ("krh_advance", None, [_P]),
     ("krh_math_batch", None, [C.c_int, _P, _P, _P, C.c_size_t]), ("krh_h2f_batch", None, [_P, _P, C.c_size_t]),
     ("krh_block_dots", None, [_P, C.POINTER(KrhMat), _P]),
+    ("krh_gen_blocks", None, [_P, _P, C.c_uint64, C.c_int, C.c_int, C.c_int, C.c_int, C.c_float]),
 ]:
     f = getattr(hip, name)
     f.restype = res
