@@ -86,8 +86,7 @@ def time_swiglu(K, model, state, reps):
     cfg = model.cfg
     xq = K.host.kr_state_buffer(state.ptr, b"qa_dim")
     xd = K.host.kr_state_buffer(state.ptr, b"qd_dim")
-    hq = K.host.kr_state_buffer(state.ptr, b"qa_hid")
-    hd = K.host.kr_state_buffer(state.ptr, b"qd_hid")
+    hb = K.host.kr_state_buffer(state.ptr, b"hb")
     t = K.hip.krh_timer_new()
     total, n, nbytes = 0.0, 0, None
     for _ in range(reps):
@@ -96,7 +95,7 @@ def time_swiglu(K, model, state, reps):
             w3 = K.host.kr_model_device_mat(model.ptr, l, b"w3")
             nbytes = mat_bytes(w1.contents) + mat_bytes(w3.contents)
             K.hip.krh_timer_mark(t, 0)
-            K.hip.krh_matvec_swiglu_q8(hq, hd, None, w1, w3, xq, xd)
+            K.hip.krh_matvec_swiglu(hb, w1, w3, xq, xd)
             K.hip.krh_timer_mark(t, 1)
             total += K.hip.krh_timer_ms(t)
             n += 1
@@ -277,7 +276,7 @@ def main():
         "prefill_tok_s": round(prefill_tok_s, 2) if prefill_tok_s else None,
         "decode_frac_of_hbm_roofline": round(tok_s * (per_tok + kv_tok) / (HBM_PEAK_GBS * 1e9), 4),
         "deterministic_ids": deterministic,
-        "roofline": {"bound": "hbm", "kernel": "k_matvec<EPI_SWIGLU> (w1|w3 + SiLU*up + quantize_q8)",
+        "roofline": {"bound": "hbm", "kernel": "k_matvec<EPI_SWIGLU> (w1|w3 rows + SiLU(w1 x) * (w3 x))",
                      "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
                      "bytes_per_launch": nbytes, "avg_launch_us": round(ms * 1e3, 2)},

@@ -55,11 +55,13 @@ ml_status kr_prefill(kr_state *s, const int *tokens, int n, int pos0, float *log
 int kr_generate(kr_state *s, const int *prompt, int np, int steps, int *out, double *prefill_s, double *decode_s);
 /* device address of the residual stream x (dim floats), for tests */
 const float *kr_state_x_device(const kr_state *s);
-/* device address of an internal buffer by name ("x", "q", "ao", "att",
+/* device address of an internal buffer by name ("x", "q", "ao", "hb", "att",
  * "logits", "kcache", "vcache", "rope_cos", "rope_sin", "qa_dim", "qd_dim",
  * "qa_q", "qd_q", "qa_hid", "qd_hid"), or NULL; for tests */
 const void *kr_state_buffer(const kr_state *s, const char *name);
-/* prefill step size: 0 = per-token graph replay (default) */
+/* tokens per batched prefill step (ml_state.batch, model/transformer.h:37):
+ * 1 = token by token (replays of the decode step), 0 = the default (2048,
+ * at most max_seq) */
 void kr_state_set_batch(kr_state *s, int batch);
 
 /* ---- seeded synthetic models ---- */

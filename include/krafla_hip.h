@@ -81,10 +81,18 @@ void krh_rmsnorm_q8(int8_t *q, float *d, float *xb, const float *x, const float 
 
 /* Q8_0 quantize of ntok rows of n floats (k_scalar.c:39-57) */
 void krh_quantize_q8(int8_t *q, float *d, const float *x, int n, int ntok);
+/* the same two with the scales transposed: d[b * dld + t] (dld >= ntok), the
+ * layout krh_matmul reads */
+void krh_rmsnorm_q8_t(int8_t *q, float *d, int dld, float *xb, const float *x, const float *w, int n, float eps,
+                      int ntok);
+void krh_quantize_q8_t(int8_t *q, float *d, int dld, const float *x, int n, int ntok);
 
 /* y = W x (k_scalar.c:4-37); accumulate != 0: y += W x, the residual add of
  * model/transformer.c:240-243 */
 void krh_matvec(float *y, const krh_mat *W, const int8_t *xq, const float *xd, int accumulate);
+/* the same with a float input x[W->cols], quantized to Q8_0 first
+ * (k_scalar.c:39-57) inside the launch */
+void krh_matvec_f(float *y, const krh_mat *W, const float *x, int accumulate);
 
 /* The attention projections of one layer at position *pos
  * (model/transformer.c:270-281): q = wq x, k = wk x, v = wv x, plus the
@@ -94,17 +102,41 @@ void krh_matvec_qkv(float *q, float *kc, float *vc, const krh_mat *wq, const krh
                     const float *bq, const float *bk, const float *bv, const int8_t *xq, const float *xd,
                     const float *rope_cos, const float *rope_sin, int head_dim, const int *pos);
 
-/* h = silu(w1 x) * (w3 x) (k_scalar.c:96-98), quantized to Q8_0 into hq, hd
- * (model/transformer.c:291-294); hb (nullable) receives the float h.
- * Needs rows % 32 == 0. */
-void krh_matvec_swiglu_q8(int8_t *hq, float *hd, float *hb, const krh_mat *w1, const krh_mat *w3,
-                          const int8_t *xq, const float *xd);
+/* h = silu(w1 x) * (w3 x) (k_scalar.c:96-98; model/transformer.c:291-293) */
+void krh_matvec_swiglu(float *h, const krh_mat *w1, const krh_mat *w3, const int8_t *xq, const float *xd);
 
 /* Causal GQA attention of one position *pos over this layer's F32 cache
  * (ops/ops.c:169-225): ao [n_heads * head_dim]; aq, ad (nullable) receive its
- * Q8_0 quantization. att: n_heads * max_seq floats of scratch. */
+ * Q8_0 quantization. att: n_heads * max_seq floats of scratch. head_dim % 4
+ * == 0, at most 16 query heads per KV head. */
 void krh_attention(float *ao, int8_t *aq, float *ad, float *att, const float *q, const float *kc, const float *vc,
                    int n_heads, int n_kv_heads, int head_dim, int max_seq, int window, float scale, const int *pos);
+
+/* ---- batched prompt prefill (model/transformer.c:385-425) ---- */
+
+/* Y[t * ldy + r] (+)= W x_t for the T tokens of xq [T][W->cols] with
+ * transposed scales xdT[b * ldx + t] (ml_matmul, ops/ops.c:75-79): int8 MFMA
+ * per 32-block, each token's float order the matvec's. ldx is a multiple of
+ * 128 and >= T; xq must be readable for ldx rows. */
+void krh_matmul(float *Y, int ldy, const krh_mat *W, const int8_t *xq, const float *xdT, int ldx, int T,
+                int accumulate);
+/* the three attention projections of T tokens at positions pos0.. with bias
+ * and RoPE: q [T][q_dim], k and v into cache rows pos0 + t
+ * (model/transformer.c:400-402, :335-344) */
+void krh_matmul_qkv(float *q, float *kc, float *vc, const krh_mat *wq, const krh_mat *wk, const krh_mat *wv,
+                    const float *bq, const float *bk, const float *bv, const int8_t *xq, const float *xdT, int ldx,
+                    int T, const float *rope_cos, const float *rope_sin, int head_dim, int pos0);
+/* causal attention of ntok tokens at positions *pos0 + t (ml_attention_batch,
+ * ops/ops.c:216-238): ao, q [ntok][q_dim], att [ntok][n_heads][max_seq];
+ * last_pos = *pos0 + ntok - 1 (sizes the launch) */
+void krh_attention_batch(float *ao, float *att, const float *q, const float *kc, const float *vc, int n_heads,
+                         int n_kv_heads, int head_dim, int max_seq, int window, float scale, const int *pos0, int ntok,
+                         int last_pos);
+/* h = silu(g) * u per token (k_scalar.c:96-98), quantized to Q8_0 with
+ * transposed scales dT[b * ldd + t] */
+void krh_silu_quant(int8_t *q, float *dT, int ldd, const float *g, const float *u, int n, int ntok);
+/* x[t][0..cols) = row tok[t] of emb, dequantized, for ntok tokens */
+void krh_embed_batch(float *x, const krh_mat *emb, const int *tok, int ntok, float embed_scale);
 
 /* Greedy pick (model/sampler.c:57-61, ties to the lowest id): *tok = argmax;
  * then, when non-NULL, log[*pos + 1] = *tok and *pos += 1. */
@@ -121,6 +153,11 @@ void krh_advance(int *pos);
  * quantized per 32-block by the .mlb writer rules; q: rows*cols (Q8) or
  * rows*cols/2 bytes, d: rows*cols/32 scales, f16 when f16 != 0. */
 void krh_gen_blocks(void *q, void *d, uint64_t key, int rows, int cols, int type, int f16, float std);
+
+/* ---- tuning ---- */
+/* KRH_TUNE_MV_ROWS: rows per matvec workgroup (0 = the built-in choice) */
+enum { KRH_TUNE_MV_ROWS = 1 };
+void krh_tune(int key, int value);
 
 /* ---- self-checks for tests ---- */
 /* y[i] = op(a[i], b[i]) as the kernels compute it: expf(a), sqrtf(a), a / b,

@@ -32,19 +32,20 @@ struct MvArgs {
     KMat m[3];
     int tile0[4];        // first workgroup of matrix i; tile0[nmat] = grid size
     int nmat;
-    const int8_t *xq;
+    int R;               // output rows per workgroup
+    const int8_t *xq;    // Q8_0 activation, or NULL: quantize xf in the prologue
     const float *xd;
+    const float *xf;
     int K;
     float *y[3];
     const float *bias[3];
     const float *rope_cos, *rope_sin;
     int head_dim, ld_cache;
     const int *pos;
-    int8_t *oq;
-    float *od;
 };
 
 constexpr int MV_THREADS = 256;
+constexpr int MV_NPT = 16;   // weight blocks per thread, all loaded up front
 
 template <typename T> __device__ __forceinline__ T pick3(int i, T a, T b, T c) { return i == 0 ? a : (i == 1 ? b : c); }
 
@@ -75,58 +76,54 @@ __device__ __forceinline__ int block_dot(const int4 w0, const int4 w1, const int
     return s;
 }
 
-// Phase 1: the per-block terms of local rows [0, nloc) into t2[lr * stride + b].
-// Local rows below `split` come from A (rows row0..), the rest from B.
-template <int QT, int D16>
-__device__ __forceinline__ void mv_terms(const KMat &A, const KMat &B, int split, int row0, int nloc, int nb,
-                                         int stride, const int8_t *xs, const float *xds, float *t2) {
-    const int tid = threadIdx.x;
-    const int sr = MV_THREADS / nb, sb = MV_THREADS % nb;
-    int lr = tid / nb, b = tid - (tid / nb) * nb;
-    constexpr int U = 4;
-    while (lr < nloc) {
-        int lrs[U], bs[U];
-        int4 w0[U], w1[U];
-        float wd[U];
+// Q8_0 of K floats into LDS (k_scalar.c:39-57): each thread takes 4
+// consecutive values, 8 threads a 32-block; the block max is exact in any
+// order. K % 32 == 0, x 16-byte aligned.
+__device__ __forceinline__ void quantize_to_lds(const float *x, int K, int8_t *xs, float *xds) {
+    constexpr int B = 4;   // float4 loads in flight per thread
+    for (int base = 0; base < K; base += 4 * B * MV_THREADS) {
+        float4 vs[B];
 #pragma unroll
-        for (int u = 0; u < U; u++) {
-            lrs[u] = lr;
-            bs[u] = b;
-            if (lr < nloc) {
-                const bool second = lr >= split;
-                const uint8_t *q = second ? B.q : A.q;
-                const void *d = second ? B.d : A.d;
-                const size_t blk = (size_t)(row0 + (second ? lr - split : lr)) * nb + b;
-                if (QT == ML_Q8_0) {
-                    const int4 *p = (const int4 *)(q + blk * 32);
-                    w0[u] = p[0];
-                    w1[u] = p[1];
-                } else {
-                    w0[u] = *(const int4 *)(q + blk * 16);
-                    w1[u] = make_int4(0, 0, 0, 0);
-                }
-                wd[u] = D16 ? kr_h2f(((const uint16_t *)d)[blk]) : ((const float *)d)[blk];
-            }
-            b += sb;
-            lr += sr;
-            if (b >= nb) { b -= nb; lr++; }
+        for (int k = 0; k < B; k++) {
+            const int i = base + 4 * (k * MV_THREADS + threadIdx.x);
+            if (i < K) vs[k] = *(const float4 *)(x + i);
         }
 #pragma unroll
-        for (int u = 0; u < U; u++) {
-            if (lrs[u] < nloc) {
-                const int bb = bs[u];
-                const int s = block_dot<QT>(w0[u], w1[u], xs + bb * 32);
-                const float t = kr_fmul((float)s, wd[u]);
-                t2[lrs[u] * stride + bb] = kr_fmul(t, xds[bb]);
+        for (int k = 0; k < B; k++) {
+        const int i = base + 4 * (k * MV_THREADS + threadIdx.x);   // K % 32 == 0: 8-lane groups all in or all out
+        if (i < K) {
+            const float4 v = vs[k];
+            float m = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+            m = fmaxf(m, __shfl_xor(m, 1, 8));
+            m = fmaxf(m, __shfl_xor(m, 2, 8));
+            m = fmaxf(m, __shfl_xor(m, 4, 8));
+            int packed = 0;
+            float dd = 0.0f;
+            if (!(m < KR_QUANT_TINY)) {
+                const float id = kr_fdiv(127.0f, m);
+                dd = kr_fdiv(m, 127.0f);
+                packed = (kr_q8_elem(v.x, id) & 0xff) | (kr_q8_elem(v.y, id) & 0xff) << 8 |
+                         (kr_q8_elem(v.z, id) & 0xff) << 16 | (int)((unsigned)kr_q8_elem(v.w, id) << 24);
             }
+            *(int *)(xs + i) = packed;
+            if ((i & 31) == 0) xds[i >> 5] = dd;
+        }
         }
     }
 }
 
-template <int EPI, int R>
+// y rows [row0, row0 + R) of up to three matrices sharing the activation
+// (QKV), or the w1 and w3 rows [row0, row0 + R) (SwiGLU). Phase 1: every
+// thread issues the loads of its MV_NPT weight blocks (consecutive threads on
+// consecutive blocks: each wave reads one contiguous span), then the
+// activation is staged (or quantized) into LDS while they are in flight, then
+// the exact int32 block dots and their terms ((float)s * wd) * xd go to LDS.
+// Phase 2: one lane per row adds its terms in block order
+// (kernels/scalar/k_scalar.c:13, :34). Then the epilogue.
+template <int EPI, int QT, int D16>
 __global__ void __launch_bounds__(MV_THREADS) k_matvec(const MvArgs a) {
     extern __shared__ __align__(16) unsigned char smem[];
-    const int K = a.K, nb = K / KR_QK, tid = threadIdx.x;
+    const int K = a.K, nb = K / KR_QK, tid = threadIdx.x, R = a.R;
     int mi = 0;
     if (EPI != EPI_SWIGLU)
         while (mi + 1 < a.nmat && (int)blockIdx.x >= a.tile0[mi + 1]) mi++;
@@ -134,28 +131,66 @@ __global__ void __launch_bounds__(MV_THREADS) k_matvec(const MvArgs a) {
     const KMat W2 = a.m[1];
     const int row0 = ((int)blockIdx.x - a.tile0[mi]) * R;
     const int nr = min(R, W.rows - row0);
-    const int nloc = EPI == EPI_SWIGLU ? 2 * R : nr;
-    const int split = EPI == EPI_SWIGLU ? R : nloc;
+    const int nloc = EPI == EPI_SWIGLU ? 2 * nr : nr;   // local rows: SwiGLU's w3 rows follow its w1 rows
     const int stride = nb | 1;   // odd: the chain lanes read distinct banks
     int8_t *xs = (int8_t *)smem;
     float *xds = (float *)(smem + K);
     float *t2 = xds + nb;
     float *sums = t2 + (EPI == EPI_SWIGLU ? 2 * R : R) * stride;
+    const int nblk = nloc * nb;
 
-    for (int i = tid; i < K / 16; i += MV_THREADS) ((int4 *)xs)[i] = ((const int4 *)a.xq)[i];
-    for (int i = tid; i < nb; i += MV_THREADS) xds[i] = a.xd[i];
-    __syncthreads();
-
-    if (W.type == ML_Q8_0) {
-        if (W.d16) mv_terms<ML_Q8_0, 1>(W, W2, split, row0, nloc, nb, stride, xs, xds, t2);
-        else mv_terms<ML_Q8_0, 0>(W, W2, split, row0, nloc, nb, stride, xs, xds, t2);
+    int4 w0[MV_NPT], w1[MV_NPT];
+    uint32_t wd[MV_NPT];   // raw scale bits: widened after every load is in flight
+    {
+        int lr = tid / nb, b = tid - (tid / nb) * nb;
+        const int sr = MV_THREADS / nb, sb = MV_THREADS - sr * nb;
+        // every slot loads (slots past the workgroup's blocks re-read its
+        // first block and are not used), so no load waits on a branch
+#pragma unroll
+        for (int k = 0; k < MV_NPT; k++) {
+            const bool in = tid + k * MV_THREADS < nblk;
+            const bool second = EPI == EPI_SWIGLU && in && lr >= nr;
+            const uint8_t *q = second ? W2.q : W.q;
+            const void *d = second ? W2.d : W.d;
+            const size_t blk = in ? (size_t)(row0 + (second ? lr - nr : lr)) * nb + b : (size_t)row0 * nb;
+            if (QT == ML_Q8_0) {
+                const int4 *p = (const int4 *)(q + blk * 32);
+                w0[k] = p[0];
+                w1[k] = p[1];
+            } else {
+                w0[k] = *(const int4 *)(q + blk * 16);
+                w1[k] = make_int4(0, 0, 0, 0);
+            }
+            wd[k] = D16 ? (uint32_t)((const uint16_t *)d)[blk] : ((const uint32_t *)d)[blk];
+            b += sb;
+            lr += sr;
+            if (b >= nb) { b -= nb; lr++; }
+        }
+    }
+    if (a.xq) {
+        for (int i = tid; i < K / 16; i += MV_THREADS) ((int4 *)xs)[i] = ((const int4 *)a.xq)[i];
+        for (int i = tid; i < nb; i += MV_THREADS) xds[i] = a.xd[i];
     } else {
-        if (W.d16) mv_terms<ML_Q4_0, 1>(W, W2, split, row0, nloc, nb, stride, xs, xds, t2);
-        else mv_terms<ML_Q4_0, 0>(W, W2, split, row0, nloc, nb, stride, xs, xds, t2);
+        quantize_to_lds(a.xf, K, xs, xds);
+    }
+    __syncthreads();
+    {
+        int lr = tid / nb, b = tid - (tid / nb) * nb;
+        const int sr = MV_THREADS / nb, sb = MV_THREADS - sr * nb;
+#pragma unroll
+        for (int k = 0; k < MV_NPT; k++) {
+            if (tid + k * MV_THREADS < nblk) {
+                const int s = block_dot<QT>(w0[k], w1[k], xs + b * 32);
+                const float sc = D16 ? kr_h2f((uint16_t)wd[k]) : __uint_as_float(wd[k]);
+                t2[lr * stride + b] = kr_fmul(kr_fmul((float)s, sc), xds[b]);
+            }
+            b += sb;
+            lr += sr;
+            if (b >= nb) { b -= nb; lr++; }
+        }
     }
     __syncthreads();
 
-    // Phase 2: one lane per row adds its terms in block order (k_scalar.c:13)
     if (tid < nloc) {
         const float *p = t2 + tid * stride;
         float s = 0.0f;
@@ -198,94 +233,172 @@ __global__ void __launch_bounds__(MV_THREADS) k_matvec(const MvArgs a) {
             else pick3(mi, a.y[0], a.y[1], a.y[2])[(size_t)pos * a.ld_cache + row] = o;
         }
     } else if (EPI == EPI_SWIGLU) {
-        // g = g / (1 + expf(-g)) * u (k_scalar.c:96-98), then Q8_0 of the
-        // 32-row block (k_scalar.c:39-57)
-        if (tid < R) {
-            const float h1 = sums[tid], h3 = sums[R + tid];
-            const float g = kr_fmul(kr_fdiv(h1, kr_fadd(1.0f, kr_expf(-h1))), h3);
-            if (a.y[0]) a.y[0][row0 + tid] = g;
-            int8_t q;
-            float d;
-            kr_quant_block32(g, &q, &d);
-            a.oq[row0 + tid] = q;
-            if (tid == 0) a.od[row0 / KR_QK] = d;
+        // g = g / (1 + expf(-g)) * u (k_scalar.c:96-98)
+        if (tid < nr) {
+            const float h1 = sums[tid], h3 = sums[nr + tid];
+            a.y[0][row0 + tid] = kr_fmul(kr_fdiv(h1, kr_fadd(1.0f, kr_expf(-h1))), h3);
         }
     }
 }
 
-template <int EPI, int R>
-void launch_mv(const MvArgs &a, int grid) {
+// Rows per workgroup: as many as MV_NPT blocks per thread allow (at most
+// cap, even for the RoPE pairs), halved down to 8 while the launch would have
+// fewer workgroups than compute units (measured on the 8B shapes: wo 4096x4096
+// is fastest at 16, w2 4096x14336 at 8 or more, the classifier at 32).
+int g_mv_rows_override = 0;   // krh_tune(KRH_TUNE_MV_ROWS, R): fixed rows per workgroup
+
+int mv_rows(int K, int total_rows, int local_per_row, int cap) {
+    const int nb = K / KR_QK;
+    if (g_mv_rows_override > 0) {
+        int R = g_mv_rows_override;
+        while (R > 1 && R * local_per_row * nb > MV_NPT * MV_THREADS) R /= 2;
+        return R;
+    }
+    int R = MV_NPT * MV_THREADS / (nb * local_per_row);
+    if (R > cap) R = cap;
+    while (R > 8 && total_rows / R < 256) R /= 2;
+    if (R > 1) R &= ~1;
+    return R < 1 ? 1 : R;
+}
+
+template <int EPI>
+void launch_mv(MvArgs &a, const KMat &W) {
     const int nb = a.K / KR_QK;
-    const int nloc = EPI == EPI_SWIGLU ? 2 * R : R;
+    const int nloc = EPI == EPI_SWIGLU ? 2 * a.R : a.R;
     const size_t lds = (size_t)a.K + 4u * nb + 4u * (size_t)nloc * (nb | 1) + 4u * nloc;
-    if (a.K % KR_QK || lds > 65536 || grid <= 0) {
+    const int grid = a.tile0[a.nmat];
+    if (a.K % KR_QK || lds > 64 * 1024 || grid <= 0 || nloc > MV_THREADS || nloc * nb > MV_NPT * MV_THREADS ||
+        (!a.xq && !a.xf)) {
         kr_fail(ML_E_SHAPE, "matvec shape", hipSuccess);
         return;
     }
-    hipLaunchKernelGGL((k_matvec<EPI, R>), dim3(grid), dim3(MV_THREADS), lds, kr_stream(), a);
+    auto go = [&](auto kern) {
+        hipLaunchKernelGGL(kern, dim3(grid), dim3(MV_THREADS), lds, kr_stream(), a);
+    };
+    if (W.type == ML_Q8_0) {
+        if (W.d16) go(k_matvec<EPI, ML_Q8_0, 1>); else go(k_matvec<EPI, ML_Q8_0, 0>);
+    } else {
+        if (W.d16) go(k_matvec<EPI, ML_Q4_0, 1>); else go(k_matvec<EPI, ML_Q4_0, 0>);
+    }
     kr_check_launch("matvec");
 }
 
-constexpr int MV_R = 16;
-constexpr int SW_R = 32;
-
 // ---- rmsnorm + quantize, quantize ----
 
-// One workgroup per token. The squares x_i * x_i are formed in parallel into
-// LDS (each one rounded product, as in the scalar loop), then lane 0 adds them
-// in index order (k_scalar.c:61) from LDS, RN_CHUNK floats at a time; then
-// every lane forms (x * inv) * w and the half-waves quantize their 32-element
-// blocks (k_scalar.c:39-57). n % 32 == 0; x rows 16-byte aligned.
-constexpr int RN_THREADS = 256, RN_CHUNK = 8192;
+// One workgroup per token; each thread keeps its float4 slices of x and w in
+// registers (n <= RN_MAX). The squares x_i * x_i (each one rounded product,
+// as in the scalar loop) go to LDS and lane 0 adds them in index order
+// (k_scalar.c:61); then every thread forms (x * inv) * w for its values and
+// 8-thread groups quantize their 32-element blocks (k_scalar.c:39-57).
+// n % 32 == 0; rows 16-byte aligned.
+constexpr int RN_THREADS = 256, RN_V4 = 16, RN_MAX = RN_THREADS * RN_V4 * 4;
 
-__global__ void __launch_bounds__(RN_THREADS) k_rmsnorm_q8(int8_t *q, float *d, float *xb, const float *x,
+// 0 + v[0] + v[1] + ... + v[n-1] in index order (one lane), n % 32 == 0, v in
+// LDS: reads are batched 8 float4 at a time so the adds do not wait on each.
+__device__ __forceinline__ float kr_chain_lds(const float *v, int n) {
+    const float4 *p = (const float4 *)v;
+    float s = 0.0f;
+    for (int i = 0; i < n / 4; i += 8) {
+        float4 r[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++) r[k] = p[i + k];
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            s = kr_fadd(s, r[k].x);
+            s = kr_fadd(s, r[k].y);
+            s = kr_fadd(s, r[k].z);
+            s = kr_fadd(s, r[k].w);
+        }
+    }
+    return s;
+}
+
+__global__ void __launch_bounds__(RN_THREADS) k_rmsnorm_q8(int8_t *q, float *d, int dld, float *xb, const float *x,
                                                            const float *w, int n, float eps, int norm) {
     const size_t t = blockIdx.x;
     const int tid = threadIdx.x;
     x += t * n;
     q += t * n;
-    d += t * (n / KR_QK);
+    // scales [t][n / 32], or transposed [n / 32][dld] when dld > 0
+    const size_t dstep = dld > 0 ? (size_t)dld : 1;
+    d += dld > 0 ? t : t * (n / KR_QK);
     if (xb) xb += t * n;
-    __shared__ __align__(16) float sq[RN_CHUNK];
+    extern __shared__ __align__(16) float sq[];   // n floats when norm
     __shared__ float s_inv;
-    if (norm) {
-        float ss = 0.0f;   // lane 0's running sum
-        for (int c0 = 0; c0 < n; c0 += RN_CHUNK) {
-            const int cn = min(RN_CHUNK, n - c0);
-            for (int i = 4 * tid; i < cn; i += 4 * RN_THREADS) {
-                const float4 v = *(const float4 *)(x + c0 + i);
-                *(float4 *)(sq + i) = make_float4(kr_fmul(v.x, v.x), kr_fmul(v.y, v.y), kr_fmul(v.z, v.z),
-                                                  kr_fmul(v.w, v.w));
-            }
-            __syncthreads();
-            if (tid == 0) {
-                const float4 *p = (const float4 *)sq;
-#pragma unroll 16
-                for (int i = 0; i < cn / 4; i++) {
-                    const float4 v = p[i];
-                    ss = kr_fadd(ss, v.x);
-                    ss = kr_fadd(ss, v.y);
-                    ss = kr_fadd(ss, v.z);
-                    ss = kr_fadd(ss, v.w);
-                }
-            }
-            __syncthreads();
+    float4 xv[RN_V4], wv[RN_V4];
+#pragma unroll
+    for (int k = 0; k < RN_V4; k++) {
+        const int i = (k * RN_THREADS + tid) * 4;
+        if (i < n) {
+            xv[k] = *(const float4 *)(x + i);
+            if (norm) wv[k] = *(const float4 *)(w + i);
         }
-        if (tid == 0) s_inv = kr_fdiv(1.0f, kr_fsqrt(kr_fadd(kr_fdiv(ss, (float)n), eps)));
-        __syncthreads();
     }
-    const float inv = norm ? s_inv : 1.0f;
-    for (int base = 0; base < n; base += RN_THREADS) {
-        const int i = base + tid;
-        if (i < n) {   // n % 32 == 0: a half-wave is all in or all out
-            const float o = norm ? kr_fmul(kr_fmul(x[i], inv), w[i]) : x[i];
-            if (xb) xb[i] = o;
-            int8_t qq;
-            float dd;
-            kr_quant_block32(o, &qq, &dd);
-            q[i] = qq;
-            if ((i & 31) == 0) d[i >> 5] = dd;
+    float inv = 1.0f;
+    if (norm) {
+#pragma unroll
+        for (int k = 0; k < RN_V4; k++) {
+            const int i = (k * RN_THREADS + tid) * 4;
+            if (i < n)
+                *(float4 *)(sq + i) = make_float4(kr_fmul(xv[k].x, xv[k].x), kr_fmul(xv[k].y, xv[k].y),
+                                                  kr_fmul(xv[k].z, xv[k].z), kr_fmul(xv[k].w, xv[k].w));
         }
+        __syncthreads();
+        if (tid == 0) s_inv = kr_fdiv(1.0f, kr_fsqrt(kr_fadd(kr_fdiv(kr_chain_lds(sq, n), (float)n), eps)));
+        __syncthreads();
+        inv = s_inv;
+    }
+#pragma unroll
+    for (int k = 0; k < RN_V4; k++) {
+        const int i = (k * RN_THREADS + tid) * 4;
+        if (i < n) {   // n % 32 == 0: 8-thread groups are all in or all out
+            float4 o = xv[k];
+            if (norm)
+                o = make_float4(kr_fmul(kr_fmul(o.x, inv), wv[k].x), kr_fmul(kr_fmul(o.y, inv), wv[k].y),
+                                kr_fmul(kr_fmul(o.z, inv), wv[k].z), kr_fmul(kr_fmul(o.w, inv), wv[k].w));
+            if (xb) *(float4 *)(xb + i) = o;
+            float m = fmaxf(fmaxf(fabsf(o.x), fabsf(o.y)), fmaxf(fabsf(o.z), fabsf(o.w)));
+            m = fmaxf(m, __shfl_xor(m, 1, 8));
+            m = fmaxf(m, __shfl_xor(m, 2, 8));
+            m = fmaxf(m, __shfl_xor(m, 4, 8));
+            int packed = 0;
+            float dd = 0.0f;
+            if (!(m < KR_QUANT_TINY)) {
+                const float id = kr_fdiv(127.0f, m);
+                dd = kr_fdiv(m, 127.0f);
+                packed = (kr_q8_elem(o.x, id) & 0xff) | (kr_q8_elem(o.y, id) & 0xff) << 8 |
+                         (kr_q8_elem(o.z, id) & 0xff) << 16 | (int)((unsigned)kr_q8_elem(o.w, id) << 24);
+            }
+            *(int *)(q + i) = packed;
+            if ((i & 31) == 0) d[(size_t)(i >> 5) * dstep] = dd;
+        }
+    }
+}
+
+// Q8_0 of ntok rows of n floats, QZ_CHUNK values per workgroup: thread t
+// takes 4 consecutive values, 8 threads a 32-block (k_scalar.c:39-57).
+constexpr int QZ_CHUNK = 1024;
+__global__ void __launch_bounds__(256) k_quantize_q8(int8_t *q, float *d, int dld, const float *x, int n) {
+    const size_t row = blockIdx.y;
+    const int i = blockIdx.x * QZ_CHUNK + 4 * threadIdx.x;
+    if (i >= n) return;   // n % 32 == 0: 8-thread groups are all in or all out
+    const float4 v = *(const float4 *)(x + row * n + i);
+    float m = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+    m = fmaxf(m, __shfl_xor(m, 1, 8));
+    m = fmaxf(m, __shfl_xor(m, 2, 8));
+    m = fmaxf(m, __shfl_xor(m, 4, 8));
+    int packed = 0;
+    float dd = 0.0f;
+    if (!(m < KR_QUANT_TINY)) {
+        const float id = kr_fdiv(127.0f, m);
+        dd = kr_fdiv(m, 127.0f);
+        packed = (kr_q8_elem(v.x, id) & 0xff) | (kr_q8_elem(v.y, id) & 0xff) << 8 |
+                 (kr_q8_elem(v.z, id) & 0xff) << 16 | (int)((unsigned)kr_q8_elem(v.w, id) << 24);
+    }
+    *(int *)(q + row * n + i) = packed;
+    if ((i & 31) == 0) {
+        if (dld > 0) d[(size_t)(i >> 5) * dld + row] = dd;
+        else d[row * (n / KR_QK) + (i >> 5)] = dd;
     }
 }
 
@@ -320,8 +433,9 @@ __global__ void k_embed(float *x, const KMat e, const int *tok, float scale) {
 constexpr int AT_T = 64;          // positions per score tile
 constexpr int AT_THREADS = 256;
 
+// positions attended by token blockIdx.z of the launch, at position *pos_p + blockIdx.z
 __device__ __forceinline__ void attn_range(const int *pos_p, int window, int *first, int *n) {
-    const int pos = *pos_p;
+    const int pos = *pos_p + (int)blockIdx.z;
     *first = window && pos >= window ? pos + 1 - window : 0;
     *n = pos + 1 - *first;
 }
@@ -335,6 +449,8 @@ __global__ void __launch_bounds__(AT_THREADS) k_attn_scores(float *att, const fl
     extern __shared__ __align__(16) float at_smem[];
     int first, n;
     attn_range(pos_p, window, &first, &n);
+    att += (size_t)blockIdx.z * gridDim.x * group * max_seq;   // token z: [n_heads][max_seq]
+    q += (size_t)blockIdx.z * gridDim.x * group * hd;
     const int g = blockIdx.x, t0 = blockIdx.y * AT_T, tid = threadIdx.x;
     if (t0 >= n) return;
     const int nt = min(AT_T, n - t0), ks = hd + 1;
@@ -368,7 +484,7 @@ __global__ void __launch_bounds__(AT_THREADS) k_attn_softmax(float *att, int max
     __shared__ float s_inv;
     int first, n;
     attn_range(pos_p, window, &first, &n);
-    float *a = att + (size_t)blockIdx.x * max_seq;
+    float *a = att + ((size_t)blockIdx.z * gridDim.x + blockIdx.x) * max_seq;
     const int tid = threadIdx.x;
     float m = -INFINITY;
     for (int t = tid; t < n; t += AT_THREADS) m = fmaxf(m, a[t]);
@@ -435,7 +551,9 @@ __global__ void __launch_bounds__(64) k_attn_mix(float *ao, const float *att, co
     const int g = blockIdx.x, c0 = blockIdx.y * DW, lane = threadIdx.x;
     const int j = lane / DW, d = lane % DW;
     const float *vbase = vc + (size_t)first * kv_dim + (size_t)g * hd + c0;
-    const float *abase = att + (size_t)g * group * max_seq;
+    const size_t q_dim = (size_t)gridDim.x * group * hd;
+    const float *abase = att + ((size_t)blockIdx.z * gridDim.x * group + (size_t)g * group) * max_seq;
+    ao += blockIdx.z * q_dim;
     const int ntiles = (n + TP - 1) / TP;
     const int cw = min(DW, hd - c0);         // valid dims of the chunk (multiple of 4)
 
@@ -580,30 +698,61 @@ extern "C" void krh_embed(float *x, const krh_mat *emb, const int *tok, float em
 
 extern "C" void krh_rmsnorm_q8(int8_t *q, float *d, float *xb, const float *x, const float *w, int n, float eps,
                                int ntok) {
-    if (n % KR_QK || ntok <= 0) { kr_fail(ML_E_SHAPE, "rmsnorm shape", hipSuccess); return; }
-    hipLaunchKernelGGL(k_rmsnorm_q8, dim3(ntok), dim3(256), 0, kr_stream(), q, d, xb, x, w, n, eps, 1);
+    krh_rmsnorm_q8_t(q, d, 0, xb, x, w, n, eps, ntok);
+}
+
+extern "C" void krh_rmsnorm_q8_t(int8_t *q, float *d, int dld, float *xb, const float *x, const float *w, int n,
+                                 float eps, int ntok) {
+    if (n % KR_QK || n > RN_MAX || ntok <= 0 || (dld > 0 && dld < ntok)) {
+        kr_fail(ML_E_SHAPE, "rmsnorm shape", hipSuccess);
+        return;
+    }
+    hipLaunchKernelGGL(k_rmsnorm_q8, dim3(ntok), dim3(RN_THREADS), sizeof(float) * (size_t)n, kr_stream(), q, d, dld,
+                       xb, x, w, n, eps, 1);
     kr_check_launch("rmsnorm_q8");
 }
 
 extern "C" void krh_quantize_q8(int8_t *q, float *d, const float *x, int n, int ntok) {
-    if (n % KR_QK || ntok <= 0) { kr_fail(ML_E_SHAPE, "quantize shape", hipSuccess); return; }
-    hipLaunchKernelGGL(k_rmsnorm_q8, dim3(ntok), dim3(256), 0, kr_stream(), q, d, (float *)nullptr, x,
-                       (const float *)nullptr, n, 0.0f, 0);
+    krh_quantize_q8_t(q, d, 0, x, n, ntok);
+}
+
+extern "C" void krh_quantize_q8_t(int8_t *q, float *d, int dld, const float *x, int n, int ntok) {
+    if (n % KR_QK || n <= 0 || ntok <= 0 || (dld > 0 && dld < ntok)) {
+        kr_fail(ML_E_SHAPE, "quantize shape", hipSuccess);
+        return;
+    }
+    hipLaunchKernelGGL(k_quantize_q8, dim3((n + QZ_CHUNK - 1) / QZ_CHUNK, ntok), dim3(256), 0, kr_stream(), q, d, dld,
+                       x, n);
     kr_check_launch("quantize_q8");
 }
 
-extern "C" void krh_matvec(float *y, const krh_mat *W, const int8_t *xq, const float *xd, int accumulate) {
+static void mv_plain(float *y, const krh_mat *W, const int8_t *xq, const float *xd, const float *xf,
+                     int accumulate) {
     MvArgs a = {};
     a.m[0] = to_kmat(W);
     a.nmat = 1;
+    a.R = mv_rows(W->cols, W->rows, 1, 64);
     a.tile0[0] = 0;
-    a.tile0[1] = (W->rows + MV_R - 1) / MV_R;
+    a.tile0[1] = (W->rows + a.R - 1) / a.R;
     a.xq = xq;
     a.xd = xd;
+    a.xf = xf;
     a.K = W->cols;
     a.y[0] = y;
-    if (accumulate) launch_mv<EPI_ADD, MV_R>(a, a.tile0[1]);
-    else launch_mv<EPI_STORE, MV_R>(a, a.tile0[1]);
+    if (accumulate) launch_mv<EPI_ADD>(a, a.m[0]);
+    else launch_mv<EPI_STORE>(a, a.m[0]);
+}
+
+extern "C" void krh_tune(int key, int value) {
+    if (key == KRH_TUNE_MV_ROWS) g_mv_rows_override = value;
+}
+
+extern "C" void krh_matvec(float *y, const krh_mat *W, const int8_t *xq, const float *xd, int accumulate) {
+    mv_plain(y, W, xq, xd, nullptr, accumulate);
+}
+
+extern "C" void krh_matvec_f(float *y, const krh_mat *W, const float *x, int accumulate) {
+    mv_plain(y, W, nullptr, nullptr, x, accumulate);
 }
 
 extern "C" void krh_matvec_qkv(float *q, float *kc, float *vc, const krh_mat *wq, const krh_mat *wk,
@@ -611,7 +760,7 @@ extern "C" void krh_matvec_qkv(float *q, float *kc, float *vc, const krh_mat *wq
                                const float *xd, const float *rope_cos, const float *rope_sin, int head_dim,
                                const int *pos) {
     if (wq->cols != wk->cols || wq->cols != wv->cols || wk->rows != wv->rows || head_dim % 2 || wq->rows % 2 ||
-        wk->rows % 2) {
+        wk->rows % 2 || wq->type != wk->type || wq->d16 != wk->d16 || wv->d16 != wq->d16) {
         kr_fail(ML_E_SHAPE, "qkv shapes", hipSuccess);
         return;
     }
@@ -620,10 +769,11 @@ extern "C" void krh_matvec_qkv(float *q, float *kc, float *vc, const krh_mat *wq
     a.m[1] = to_kmat(wk);
     a.m[2] = to_kmat(wv);
     a.nmat = 3;
+    a.R = mv_rows(wq->cols, wq->rows + 2 * wk->rows, 1, 64);
     a.tile0[0] = 0;
-    a.tile0[1] = (wq->rows + MV_R - 1) / MV_R;
-    a.tile0[2] = a.tile0[1] + (wk->rows + MV_R - 1) / MV_R;
-    a.tile0[3] = a.tile0[2] + (wv->rows + MV_R - 1) / MV_R;
+    a.tile0[1] = (wq->rows + a.R - 1) / a.R;
+    a.tile0[2] = a.tile0[1] + (wk->rows + a.R - 1) / a.R;
+    a.tile0[3] = a.tile0[2] + (wv->rows + a.R - 1) / a.R;
     a.xq = xq;
     a.xd = xd;
     a.K = wq->cols;
@@ -638,13 +788,25 @@ extern "C" void krh_matvec_qkv(float *q, float *kc, float *vc, const krh_mat *wq
     a.head_dim = head_dim;
     a.ld_cache = wk->rows;
     a.pos = pos;
-    launch_mv<EPI_QKV, MV_R>(a, a.tile0[3]);
+    // wq, wk and wv may differ in type (Q4 models keep wv in Q8): one launch
+    // per type run
+    if (wv->type == wq->type) {
+        launch_mv<EPI_QKV>(a, a.m[0]);
+        return;
+    }
+    MvArgs b = a;
+    b.nmat = 2;   // q and k
+    launch_mv<EPI_QKV>(b, b.m[0]);
+    MvArgs c = a;   // v alone, as matrix 2 of the same epilogue
+    c.tile0[0] = c.tile0[1] = c.tile0[2] = 0;
+    c.tile0[3] = (wv->rows + a.R - 1) / a.R;
+    c.m[0] = c.m[1] = c.m[2];
+    c.nmat = 3;
+    launch_mv<EPI_QKV>(c, c.m[2]);
 }
 
-extern "C" void krh_matvec_swiglu_q8(int8_t *hq, float *hd, float *hb, const krh_mat *w1, const krh_mat *w3,
-                                     const int8_t *xq, const float *xd) {
-    if (w1->rows != w3->rows || w1->cols != w3->cols || w1->type != w3->type || w1->d16 != w3->d16 ||
-        w1->rows % SW_R) {
+extern "C" void krh_matvec_swiglu(float *h, const krh_mat *w1, const krh_mat *w3, const int8_t *xq, const float *xd) {
+    if (w1->rows != w3->rows || w1->cols != w3->cols || w1->type != w3->type || w1->d16 != w3->d16) {
         kr_fail(ML_E_SHAPE, "swiglu shapes", hipSuccess);
         return;
     }
@@ -652,20 +814,19 @@ extern "C" void krh_matvec_swiglu_q8(int8_t *hq, float *hd, float *hb, const krh
     a.m[0] = to_kmat(w1);
     a.m[1] = to_kmat(w3);
     a.nmat = 1;
+    a.R = mv_rows(w1->cols, w1->rows, 2, 64);
     a.tile0[0] = 0;
-    a.tile0[1] = w1->rows / SW_R;
+    a.tile0[1] = (w1->rows + a.R - 1) / a.R;
     a.xq = xq;
     a.xd = xd;
     a.K = w1->cols;
-    a.y[0] = hb;
-    a.oq = hq;
-    a.od = hd;
-    launch_mv<EPI_SWIGLU, SW_R>(a, a.tile0[1]);
+    a.y[0] = h;
+    launch_mv<EPI_SWIGLU>(a, a.m[0]);
 }
 
-extern "C" void krh_attention(float *ao, int8_t *aq, float *ad, float *att, const float *q, const float *kc,
-                              const float *vc, int n_heads, int n_kv_heads, int head_dim, int max_seq, int window,
-                              float scale, const int *pos) {
+static void attention(float *ao, float *att, const float *q, const float *kc, const float *vc, int n_heads,
+                      int n_kv_heads, int head_dim, int max_seq, int window, float scale, const int *pos, int ntok,
+                      int max_pos) {
     if (n_kv_heads <= 0 || n_heads % n_kv_heads || head_dim % 4 || (n_heads * head_dim) % KR_QK ||
         n_heads / n_kv_heads > 16 || head_dim > 1024) {
         kr_fail(ML_E_SHAPE, "attention shape", hipSuccess);
@@ -673,12 +834,13 @@ extern "C" void krh_attention(float *ao, int8_t *aq, float *ad, float *att, cons
     }
     const int group = n_heads / n_kv_heads, kv_dim = n_kv_heads * head_dim, q_dim = n_heads * head_dim;
     const size_t lds = sizeof(float) * ((size_t)group * head_dim + (size_t)AT_T * (head_dim + 1));
-    hipLaunchKernelGGL(k_attn_scores, dim3(n_kv_heads, (max_seq + AT_T - 1) / AT_T), dim3(AT_THREADS), lds,
+    hipLaunchKernelGGL(k_attn_scores, dim3(n_kv_heads, (max_pos + AT_T) / AT_T, ntok), dim3(AT_THREADS), lds,
                        kr_stream(), att, q, kc, group, head_dim, kv_dim, max_seq, window, scale, pos);
-    hipLaunchKernelGGL(k_attn_softmax, dim3(n_heads), dim3(AT_THREADS), 0, kr_stream(), att, max_seq, window, pos);
+    hipLaunchKernelGGL(k_attn_softmax, dim3(n_heads, 1, ntok), dim3(AT_THREADS), 0, kr_stream(), att, max_seq, window,
+                       pos);
     const int gp = group <= 1 ? 1 : group <= 2 ? 2 : group <= 4 ? 4 : group <= 8 ? 8 : 16;
     const int dw = 64 / gp;
-    const dim3 grid(n_kv_heads, (head_dim + dw - 1) / dw);
+    const dim3 grid(n_kv_heads, (head_dim + dw - 1) / dw, ntok);
     switch (dw) {
     case 64: hipLaunchKernelGGL(k_attn_mix<64>, grid, dim3(64), 0, kr_stream(), ao, att, vc, group, head_dim, kv_dim, max_seq, window, pos); break;
     case 32: hipLaunchKernelGGL(k_attn_mix<32>, grid, dim3(64), 0, kr_stream(), ao, att, vc, group, head_dim, kv_dim, max_seq, window, pos); break;
@@ -687,7 +849,23 @@ extern "C" void krh_attention(float *ao, int8_t *aq, float *ad, float *att, cons
     default: hipLaunchKernelGGL(k_attn_mix<4>, grid, dim3(64), 0, kr_stream(), ao, att, vc, group, head_dim, kv_dim, max_seq, window, pos); break;
     }
     kr_check_launch("attention");
-    if (aq) krh_quantize_q8(aq, ad, ao, q_dim, 1);
+}
+
+extern "C" void krh_attention(float *ao, int8_t *aq, float *ad, float *att, const float *q, const float *kc,
+                              const float *vc, int n_heads, int n_kv_heads, int head_dim, int max_seq, int window,
+                              float scale, const int *pos) {
+    attention(ao, att, q, kc, vc, n_heads, n_kv_heads, head_dim, max_seq, window, scale, pos, 1, max_seq - 1);
+    if (aq) krh_quantize_q8(aq, ad, ao, n_heads * head_dim, 1);
+}
+
+extern "C" void krh_attention_batch(float *ao, float *att, const float *q, const float *kc, const float *vc,
+                                    int n_heads, int n_kv_heads, int head_dim, int max_seq, int window, float scale,
+                                    const int *pos0, int ntok, int last_pos) {
+    if (ntok <= 0 || last_pos >= max_seq) {
+        kr_fail(ML_E_SHAPE, "attention batch shape", hipSuccess);
+        return;
+    }
+    attention(ao, att, q, kc, vc, n_heads, n_kv_heads, head_dim, max_seq, window, scale, pos0, ntok, last_pos);
 }
 
 extern "C" void krh_argmax(int *tok, const float *logits, int n, int *pos, int *log) {

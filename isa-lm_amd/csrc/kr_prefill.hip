@@ -1,0 +1,346 @@
+// Batched prompt prefill on gfx950: the matrix products as int8 MFMA.
+//
+// Y[t][r] = sum over blocks b, in block order, of ((float)S * wd[r][b]) * xd[t][b]
+// where S = the exact int32 dot of block b of weight row r with block b of
+// token t's Q8_0 activation: the scalar kernel's float order for every token
+// (kernels/scalar/k_scalar.c:4-37, ops/ops.c:51-73), so each token's result is
+// bit-identical to the decode matvec's (model/transformer.c:381-384).
+//
+// One v_mfma_i32_32x32x32_i8 computes S for a 32-token x 32-row tile and one
+// block (K = 32 = one Q8_0 block). Operand lanes (checked on the device):
+// lane l supplies A[l % 32][16 (l / 32) .. +15] and B[16 (l / 32) .. +15][l % 32];
+// result register r of lane l is C[8 (r / 4) + 4 (l / 32) + r % 4][l % 32].
+// A = the tokens' activations, B = the weight rows, so each lane holds one
+// weight row (one scale per block) and 16 tokens, whose scales are read from
+// the transposed activation scales xdT[b][t]. The per-block rescale and the
+// ordered accumulation are 4 unfused VALU operations per output and block,
+// which bound the kernel, not the MFMA.
+#include "kr_internal.h"
+#include "kr_numerics.h"
+
+namespace {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+
+struct MMat {
+    const uint8_t *q;
+    const void *d;
+    int rows, cols, type, d16;
+};
+
+enum { MM_STORE = 0, MM_ADD = 1, MM_QKV = 2 };
+
+struct MmArgs {
+    MMat w[3];
+    int tile0[4];        // first workgroup of matrix i; tile0[nmat] = grid size
+    int nmat;
+    const int8_t *xq;    // [T][K] (rows up to the padded token count readable)
+    const float *xdT;    // [K / 32][ldx] activation scales, transposed
+    int ldx;             // token stride of xdT: T rounded up to MM_TT
+    int T, K;
+    float *y[3];         // y[i][t * ldy[i] + r]
+    int ldy[3];
+    const float *bias[3];
+    const float *rope_cos, *rope_sin;
+    int head_dim, pos0;
+};
+
+constexpr int MM_TR = 128;   // weight rows per workgroup
+constexpr int MM_TT = 128;   // tokens per workgroup
+
+// 16 signed quant bytes of half h (elements 16h .. 16h+15) of a weight block
+template <int QT>
+__device__ __forceinline__ v4i weight_frag(const uint8_t *blk, int h) {
+    if (QT == ML_Q8_0) {
+        const int4 v = *(const int4 *)(blk + 16 * h);
+        return v4i{ v.x, v.y, v.z, v.w };
+    }
+    // byte p of a Q4 block holds element p (low nibble) and p + 16 (high);
+    // nibble n is weight n - 8: (n | 0x80) - 8 never borrows across bytes,
+    // and ^ 0x80 then leaves n - 8 as a signed byte
+    const int4 v = *(const int4 *)blk;
+    const unsigned sh = 4u * (unsigned)h, M = 0x0F0F0F0Fu;
+    v4i r;
+    r.x = (int)((((((unsigned)v.x >> sh) & M) | 0x80808080u) - 0x08080808u) ^ 0x80808080u);
+    r.y = (int)((((((unsigned)v.y >> sh) & M) | 0x80808080u) - 0x08080808u) ^ 0x80808080u);
+    r.z = (int)((((((unsigned)v.z >> sh) & M) | 0x80808080u) - 0x08080808u) ^ 0x80808080u);
+    r.w = (int)((((((unsigned)v.w >> sh) & M) | 0x80808080u) - 0x08080808u) ^ 0x80808080u);
+    return r;
+}
+
+// A wave computes MM_NG row groups x 1 token group of 32 (MM_NG MFMA tiles
+// per block); the workgroup's 4 waves take 4 token groups of the same rows.
+constexpr int MM_NG = 4;
+
+struct Frag {
+    v4i xa;              // the wave's 32 tokens
+    v4i wb[MM_NG];       // row groups
+    uint32_t wd[MM_NG];  // raw scale bits of the lane's row in each row group
+    float4 xd[4];        // token scales: quad q -> tokens 8q + 4(l/32) + 0..3
+};
+
+template <int QT, int D16>
+__device__ __forceinline__ void mm_load(Frag &f, const MmArgs &a, const MMat &W, int b, int rowl, int tokl, int lane) {
+    const int nb = a.K / KR_QK, hf = lane >> 5, ln = lane & 31;
+    {
+        const int t = tokl + ln;   // readable: the caller pads the activations to ldx rows
+        const int4 v = *(const int4 *)(a.xq + (size_t)t * a.K + (size_t)b * 32 + 16 * hf);
+        f.xa = v4i{ v.x, v.y, v.z, v.w };
+        const float *xs = a.xdT + (size_t)b * a.ldx + tokl + 4 * hf;
+#pragma unroll
+        for (int q = 0; q < 4; q++) f.xd[q] = *(const float4 *)(xs + 8 * q);
+    }
+#pragma unroll
+    for (int g = 0; g < MM_NG; g++) {
+        int r = rowl + 32 * g + ln;
+        r = r < W.rows ? r : W.rows - 1;   // rows past the end re-read the last row (not stored)
+        const size_t blk = (size_t)r * nb + b;
+        f.wb[g] = weight_frag<QT>(W.q + blk * (QT == ML_Q8_0 ? 32 : 16), hf);
+        f.wd[g] = D16 ? (uint32_t)((const uint16_t *)W.d)[blk] : ((const uint32_t *)W.d)[blk];
+    }
+}
+
+// The MFMA of row group g + 1 is issued before the rescale of group g, so
+// its latency runs under that VALU work.
+template <int D16>
+__device__ __forceinline__ void mm_step(float (&acc)[MM_NG][16], const Frag &f) {
+    v16i s = __builtin_amdgcn_mfma_i32_32x32x32_i8(f.xa, f.wb[0], v16i{}, 0, 0, 0);
+#pragma unroll
+    for (int g = 0; g < MM_NG; g++) {
+        v16i sn;
+        if (g + 1 < MM_NG) sn = __builtin_amdgcn_mfma_i32_32x32x32_i8(f.xa, f.wb[g + 1], v16i{}, 0, 0, 0);
+        const float wd = D16 ? kr_h2f((uint16_t)f.wd[g]) : __uint_as_float(f.wd[g]);
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            const float4 xq = f.xd[r >> 2];
+            const float xd = (r & 3) == 0 ? xq.x : (r & 3) == 1 ? xq.y : (r & 3) == 2 ? xq.z : xq.w;
+            acc[g][r] = kr_fadd(acc[g][r], kr_fmul(kr_fmul((float)s[r], wd), xd));
+        }
+        if (g + 1 < MM_NG) s = sn;
+    }
+}
+
+// Workgroup = 4 waves over a 128-row x 128-token tile; wave w takes all 128
+// rows (4 row groups) and tokens 32 w .. 32 w + 31.
+template <int EPI, int QT, int D16>
+__global__ void __launch_bounds__(256, 2) k_matmul(const MmArgs a) {
+    int mi = 0;
+    while (mi + 1 < a.nmat && (int)blockIdx.x >= a.tile0[mi + 1]) mi++;
+    const MMat W = mi == 0 ? a.w[0] : (mi == 1 ? a.w[1] : a.w[2]);
+    const int ntt = (a.T + MM_TT - 1) / MM_TT;
+    const int local = (int)blockIdx.x - a.tile0[mi];
+    const int rt = local / ntt, tt = local - rt * ntt;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int rowl = rt * MM_TR, tokl = tt * MM_TT + 32 * wave;
+    const int nb = a.K / KR_QK;
+
+    float acc[MM_NG][16];
+#pragma unroll
+    for (int g = 0; g < MM_NG; g++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) acc[g][r] = 0.0f;
+
+    Frag f0, f1;
+    mm_load<QT, D16>(f0, a, W, 0, rowl, tokl, lane);
+    if (nb > 1) mm_load<QT, D16>(f1, a, W, 1, rowl, tokl, lane);
+    for (int b = 0; b < nb; b += 2) {
+        mm_step<D16>(acc, f0);
+        if (b + 2 < nb) mm_load<QT, D16>(f0, a, W, b + 2, rowl, tokl, lane);
+        if (b + 1 < nb) {
+            mm_step<D16>(acc, f1);
+            if (b + 3 < nb) mm_load<QT, D16>(f1, a, W, b + 3, rowl, tokl, lane);
+        }
+    }
+
+    // epilogue: lane = one row (32 g + lane % 32), tokens 8 (r / 4) + 4 (lane / 32) + r % 4
+    float *Y = mi == 0 ? a.y[0] : (mi == 1 ? a.y[1] : a.y[2]);
+    const int ldy = mi == 0 ? a.ldy[0] : (mi == 1 ? a.ldy[1] : a.ldy[2]);
+    const float *bias = mi == 0 ? a.bias[0] : (mi == 1 ? a.bias[1] : a.bias[2]);
+#pragma unroll
+    for (int g = 0; g < MM_NG; g++) {
+        const int row = rowl + 32 * g + (lane & 31);
+        const bool rin = row < W.rows;
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            const int t = tokl + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+            float v = acc[g][r];
+            if (EPI == MM_QKV) {
+                // bias (model/transformer.c:276-277), then RoPE on q and k
+                // (k_scalar.c:79-94): rows 2i, 2i+1 sit in lanes 2i, 2i+1
+                if (bias && rin) v = kr_fadd(v, bias[row]);
+                const float o = __shfl_xor(v, 1);
+                if (mi < 2) {
+                    const int hd = a.head_dim, j = row % hd, h2 = hd >> 1;
+                    const int pos = a.pos0 + (t < a.T ? t : 0);
+                    const float c = a.rope_cos[(size_t)pos * h2 + (j >> 1)];
+                    const float sn = a.rope_sin[(size_t)pos * h2 + (j >> 1)];
+                    v = (j & 1) == 0 ? kr_fsub(kr_fmul(v, c), kr_fmul(o, sn)) : kr_fadd(kr_fmul(o, sn), kr_fmul(v, c));
+                }
+            }
+            if (rin && t < a.T) {
+                float *p = Y + (size_t)t * ldy + row;
+                if (EPI == MM_ADD) *p = kr_fadd(*p, v);
+                else *p = v;
+            }
+        }
+    }
+}
+
+template <int EPI>
+void launch_mm(const MmArgs &a, const MMat &W) {
+    const int grid = a.tile0[a.nmat];
+    if (a.K % KR_QK || a.T <= 0 || grid <= 0 || a.ldx % MM_TT || a.T > a.ldx) {
+        kr_fail(ML_E_SHAPE, "matmul shape", hipSuccess);
+        return;
+    }
+    auto go = [&](auto kern) { hipLaunchKernelGGL(kern, dim3(grid), dim3(256), 0, kr_stream(), a); };
+    if (W.type == ML_Q8_0) {
+        if (W.d16) go(k_matmul<EPI, ML_Q8_0, 1>); else go(k_matmul<EPI, ML_Q8_0, 0>);
+    } else {
+        if (W.d16) go(k_matmul<EPI, ML_Q4_0, 1>); else go(k_matmul<EPI, ML_Q4_0, 0>);
+    }
+    kr_check_launch("matmul");
+}
+
+MMat to_mmat(const krh_mat *m) {
+    MMat k = { (const uint8_t *)m->q, m->d, m->rows, m->cols, m->type, m->d16 };
+    return k;
+}
+
+int row_tiles(int rows) { return (rows + MM_TR - 1) / MM_TR; }
+
+// ---- per-token work of a batched step ----
+
+// h = silu(g) * u (k_scalar.c:96-98) for ntok rows of n, then Q8_0 of h
+// into q [t][n] and the transposed scales dT[b * ldd + t].
+__global__ void __launch_bounds__(256) k_silu_quant(int8_t *q, float *dT, int ldd, const float *g, const float *u,
+                                                    int n) {
+    const size_t t = blockIdx.y;
+    const int i = blockIdx.x * 1024 + 4 * threadIdx.x;
+    if (i >= n) return;   // n % 32 == 0
+    const float4 gv = *(const float4 *)(g + t * n + i), uv = *(const float4 *)(u + t * n + i);
+    float4 v;
+    v.x = kr_fmul(kr_fdiv(gv.x, kr_fadd(1.0f, kr_expf(-gv.x))), uv.x);
+    v.y = kr_fmul(kr_fdiv(gv.y, kr_fadd(1.0f, kr_expf(-gv.y))), uv.y);
+    v.z = kr_fmul(kr_fdiv(gv.z, kr_fadd(1.0f, kr_expf(-gv.z))), uv.z);
+    v.w = kr_fmul(kr_fdiv(gv.w, kr_fadd(1.0f, kr_expf(-gv.w))), uv.w);
+    float m = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+    m = fmaxf(m, __shfl_xor(m, 1, 8));
+    m = fmaxf(m, __shfl_xor(m, 2, 8));
+    m = fmaxf(m, __shfl_xor(m, 4, 8));
+    int packed = 0;
+    float dd = 0.0f;
+    if (!(m < KR_QUANT_TINY)) {
+        const float id = kr_fdiv(127.0f, m);
+        dd = kr_fdiv(m, 127.0f);
+        packed = (kr_q8_elem(v.x, id) & 0xff) | (kr_q8_elem(v.y, id) & 0xff) << 8 |
+                 (kr_q8_elem(v.z, id) & 0xff) << 16 | (int)((unsigned)kr_q8_elem(v.w, id) << 24);
+    }
+    *(int *)(q + t * n + i) = packed;
+    if ((i & 31) == 0) dT[(size_t)(i >> 5) * ldd + t] = dd;
+}
+
+__global__ void k_embed_batch(float *x, const MMat e, const int *tok, float scale) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x, t = blockIdx.y;
+    if (i >= e.cols) return;
+    const int nb = e.cols / KR_QK, row = tok[t], b = i / KR_QK, j = i % KR_QK;
+    const float d = kr_scale(e.d, (size_t)row * nb + b, e.d16);
+    int v;
+    if (e.type == ML_Q8_0) {
+        v = ((const int8_t *)e.q)[(size_t)row * e.cols + i];
+    } else {
+        const uint8_t p = e.q[((size_t)row * nb + b) * 16 + (j & 15)];
+        v = (j < 16 ? (p & 0xF) : (p >> 4)) - 8;
+    }
+    float o = kr_fmul((float)v, d);
+    if (scale != 1.0f) o = kr_fmul(o, scale);
+    x[(size_t)t * e.cols + i] = o;
+}
+
+}  // namespace
+
+// ---- C ABI ----
+
+extern "C" void krh_matmul(float *Y, int ldy, const krh_mat *W, const int8_t *xq, const float *xdT, int ldx, int T,
+                           int accumulate) {
+    MmArgs a = {};
+    a.w[0] = to_mmat(W);
+    a.nmat = 1;
+    a.tile0[0] = 0;
+    a.tile0[1] = row_tiles(W->rows) * ((T + MM_TT - 1) / MM_TT);
+    a.xq = xq;
+    a.xdT = xdT;
+    a.ldx = ldx;
+    a.T = T;
+    a.K = W->cols;
+    a.y[0] = Y;
+    a.ldy[0] = ldy;
+    if (accumulate) launch_mm<MM_ADD>(a, a.w[0]);
+    else launch_mm<MM_STORE>(a, a.w[0]);
+}
+
+extern "C" void krh_matmul_qkv(float *q, float *kc, float *vc, const krh_mat *wq, const krh_mat *wk,
+                               const krh_mat *wv, const float *bq, const float *bk, const float *bv, const int8_t *xq,
+                               const float *xdT, int ldx, int T, const float *rope_cos, const float *rope_sin,
+                               int head_dim, int pos0) {
+    if (wq->cols != wk->cols || wq->cols != wv->cols || wk->rows != wv->rows || head_dim % 2 || wq->type != wk->type ||
+        wq->d16 != wk->d16 || wv->d16 != wq->d16) {
+        kr_fail(ML_E_SHAPE, "matmul qkv shapes", hipSuccess);
+        return;
+    }
+    const int ntt = (T + MM_TT - 1) / MM_TT;
+    MmArgs a = {};
+    a.w[0] = to_mmat(wq);
+    a.w[1] = to_mmat(wk);
+    a.w[2] = to_mmat(wv);
+    a.xq = xq;
+    a.xdT = xdT;
+    a.ldx = ldx;
+    a.T = T;
+    a.K = wq->cols;
+    // q rows [t][q_dim]; k and v straight into the cache rows pos0 + t
+    a.y[0] = q;
+    a.ldy[0] = wq->rows;
+    a.y[1] = kc + (size_t)pos0 * wk->rows;
+    a.ldy[1] = wk->rows;
+    a.y[2] = vc + (size_t)pos0 * wv->rows;
+    a.ldy[2] = wv->rows;
+    a.bias[0] = bq;
+    a.bias[1] = bk;
+    a.bias[2] = bv;
+    a.rope_cos = rope_cos;
+    a.rope_sin = rope_sin;
+    a.head_dim = head_dim;
+    a.pos0 = pos0;
+    a.tile0[0] = 0;
+    a.tile0[1] = row_tiles(wq->rows) * ntt;
+    a.tile0[2] = a.tile0[1] + row_tiles(wk->rows) * ntt;
+    a.tile0[3] = a.tile0[2] + row_tiles(wv->rows) * ntt;
+    if (wv->type == wq->type) {
+        a.nmat = 3;
+        launch_mm<MM_QKV>(a, a.w[0]);
+        return;
+    }
+    MmArgs b = a;   // q and k
+    b.nmat = 2;
+    launch_mm<MM_QKV>(b, b.w[0]);
+    MmArgs c = a;   // v alone, as matrix 2 of the same epilogue
+    c.tile0[0] = c.tile0[1] = c.tile0[2] = 0;
+    c.tile0[3] = row_tiles(wv->rows) * ntt;
+    c.w[0] = c.w[1] = c.w[2];
+    c.nmat = 3;
+    launch_mm<MM_QKV>(c, c.w[2]);
+}
+
+extern "C" void krh_silu_quant(int8_t *q, float *dT, int ldd, const float *g, const float *u, int n, int ntok) {
+    if (n % KR_QK || ntok <= 0) { kr_fail(ML_E_SHAPE, "silu_quant shape", hipSuccess); return; }
+    hipLaunchKernelGGL(k_silu_quant, dim3((n + 1023) / 1024, ntok), dim3(256), 0, kr_stream(), q, dT, ldd, g, u, n);
+    kr_check_launch("silu_quant");
+}
+
+extern "C" void krh_embed_batch(float *x, const krh_mat *emb, const int *tok, int ntok, float embed_scale) {
+    hipLaunchKernelGGL(k_embed_batch, dim3((emb->cols + 255) / 256, ntok), dim3(256), 0, kr_stream(), x, to_mmat(emb),
+                       tok, embed_scale);
+    kr_check_launch("embed_batch");
+}

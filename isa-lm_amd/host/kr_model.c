@@ -168,7 +168,7 @@ void kr_model_free(kr_model *m) {
 struct kr_state {
     kr_model *m;
     /* device buffers */
-    float *x, *q, *ao, *att, *logits, *kcache, *vcache, *rope_cos, *rope_sin, *rope_cos_l, *rope_sin_l;
+    float *x, *q, *ao, *hb, *att, *logits, *kcache, *vcache, *rope_cos, *rope_sin, *rope_cos_l, *rope_sin_l;
     int8_t *qa_dim, *qa_q, *qa_hid;
     float *qd_dim, *qd_q, *qd_hid;
     int *tok, *pos, *prompt, *log;
@@ -176,9 +176,18 @@ struct kr_state {
     float *h_logits;          /* pinned */
     int *h_ints;              /* pinned: tok, pos */
     krh_graph *g_logits, *g_greedy, *g_prefill;
-    int batch;
+    int batch;                /* tokens per batched prefill step; 1: token by token */
     int eager;                /* issue ops directly instead of replaying graphs */
+    /* batched prefill buffers (allocated on first use): [ldx] token rows */
+    void *bmem;
+    int ldx;                  /* capacity, a multiple of 128 */
+    float *bx, *bq, *bao, *bh1, *bh3, *batt, *blog, *bxd;
+    int8_t *bxq;
 };
+
+/* tokens per batched prefill step by default (the attention scratch is
+ * [step][n_heads][max_seq] floats) */
+#define KR_PREFILL_STEP 2048
 
 /* model/transformer.c:16-38: inverse frequency of rotary pair i */
 static double rope_inv_freq(const ml_config *c, int i) {
@@ -240,11 +249,12 @@ static void issue_step(kr_state *s, int cls) {
         krh_rmsnorm_q8(s->qa_dim, s->qd_dim, NULL, s->x, D->attn_norm, c->dim, c->norm_eps, 1);
         krh_matvec_qkv(s->q, kc, vc, &D->wq, &D->wk, &D->wv, D->bq, D->bk, D->bv, s->qa_dim, s->qd_dim, cs, sn,
                        c->head_dim, s->pos);
-        krh_attention(s->ao, s->qa_q, s->qd_q, s->att, s->q, kc, vc, c->n_heads, c->n_kv_heads, c->head_dim,
+        krh_attention(s->ao, NULL, NULL, s->att, s->q, kc, vc, c->n_heads, c->n_kv_heads, c->head_dim,
                       c->max_seq, L->window, c->attn_scale, s->pos);
-        krh_matvec(s->x, &D->wo, s->qa_q, s->qd_q, 1);
+        krh_matvec_f(s->x, &D->wo, s->ao, 1);
         krh_rmsnorm_q8(s->qa_dim, s->qd_dim, NULL, s->x, D->ffn_norm, c->dim, c->norm_eps, 1);
-        krh_matvec_swiglu_q8(s->qa_hid, s->qd_hid, NULL, &D->w1, &D->w3, s->qa_dim, s->qd_dim);
+        krh_matvec_swiglu(s->hb, &D->w1, &D->w3, s->qa_dim, s->qd_dim);
+        krh_quantize_q8(s->qa_hid, s->qd_hid, s->hb, c->hidden_dim, 1);
         krh_matvec(s->x, &D->w2, s->qa_hid, s->qd_hid, 1);
     }
     if (!cls) return;
@@ -300,6 +310,7 @@ ml_status kr_state_new(kr_state **out, kr_model *m, int kv_type) {
     const int local = c->rope_local_theta > 0.0f;
     struct { void **p; size_t n; } parts[] = {
         { (void **)&s->x, f * c->dim }, { (void **)&s->q, f * c->q_dim }, { (void **)&s->ao, f * c->q_dim },
+        { (void **)&s->hb, f * c->hidden_dim },
         { (void **)&s->att, f * (size_t)c->n_heads * c->max_seq }, { (void **)&s->logits, f * c->vocab },
         { (void **)&s->kcache, f * kv }, { (void **)&s->vcache, f * kv },
         { (void **)&s->rope_cos, f * half }, { (void **)&s->rope_sin, f * half },
@@ -339,6 +350,7 @@ ml_status kr_state_new(kr_state **out, kr_model *m, int kv_type) {
     if (st == ML_OK && local) st = krh_copy_h2d(s->rope_cos_l, csl, f * half);
     if (st == ML_OK && local) st = krh_copy_h2d(s->rope_sin_l, snl, f * half);
     free(cs); free(sn); free(csl); free(snl);
+    s->batch = c->max_seq < KR_PREFILL_STEP ? c->max_seq : KR_PREFILL_STEP;
     const char *ev = getenv("KRAFLA_EAGER");
     s->eager = ev && ev[0] == '1';
     if (st == ML_OK && !s->eager) st = capture(s, &s->g_logits, STEP_LOGITS);
@@ -354,6 +366,7 @@ ml_status kr_state_new(kr_state **out, kr_model *m, int kv_type) {
 
 void kr_state_free(kr_state *s) {
     if (!s) return;
+    krh_free(s->bmem);
     krh_graph_free(s->g_logits);
     krh_graph_free(s->g_greedy);
     krh_graph_free(s->g_prefill);
@@ -363,13 +376,21 @@ void kr_state_free(kr_state *s) {
     free(s);
 }
 
-void kr_state_set_batch(kr_state *s, int batch) { s->batch = batch; }
+void kr_state_set_batch(kr_state *s, int batch) {
+    if (batch < 1) batch = KR_PREFILL_STEP;
+    if (batch > s->m->cfg.max_seq) batch = s->m->cfg.max_seq;
+    if (batch != s->batch && s->bmem) {   /* re-sized on next use */
+        krh_free(s->bmem);
+        s->bmem = NULL;
+    }
+    s->batch = batch;
+}
 const float *kr_state_x_device(const kr_state *s) { return s->x; }
 
 const void *kr_state_buffer(const kr_state *s, const char *name) {
-    static const char *const names[] = { "x", "q", "ao", "att", "logits", "kcache", "vcache", "rope_cos",
+    static const char *const names[] = { "x", "q", "ao", "hb", "att", "logits", "kcache", "vcache", "rope_cos",
                                          "rope_sin", "qa_dim", "qd_dim", "qa_q", "qd_q", "qa_hid", "qd_hid" };
-    const void *ptrs[] = { s->x, s->q, s->ao, s->att, s->logits, s->kcache, s->vcache, s->rope_cos,
+    const void *ptrs[] = { s->x, s->q, s->ao, s->hb, s->att, s->logits, s->kcache, s->vcache, s->rope_cos,
                            s->rope_sin, s->qa_dim, s->qd_dim, s->qa_q, s->qd_q, s->qa_hid, s->qd_hid };
     for (size_t i = 0; i < sizeof names / sizeof names[0]; i++)
         if (!strcmp(names[i], name)) return ptrs[i];
@@ -398,13 +419,93 @@ ml_status kr_forward(kr_state *s, int token, int pos, float *logits) {
     return st == ML_OK ? dev_status() : st;
 }
 
-/* Batched prefill computes every per-token op in ml_forward's order
- * (model/transformer.c:381-384); here each prompt token replays the step. */
+static ml_status batch_buffers(kr_state *s, int with_logits) {
+    const ml_config *c = &s->m->cfg;
+    const int ldx = (s->batch + 127) / 128 * 128;
+    if (s->bmem && (!with_logits || s->blog)) return ML_OK;
+    krh_free(s->bmem);
+    s->bmem = NULL;
+    s->blog = NULL;
+    const size_t f = sizeof(float), L = (size_t)ldx;
+    const int wide = c->hidden_dim > c->q_dim ? (c->hidden_dim > c->dim ? c->hidden_dim : c->dim)
+                                              : (c->q_dim > c->dim ? c->q_dim : c->dim);
+    struct { void **p; size_t n; } parts[] = {
+        { (void **)&s->bx, f * L * c->dim }, { (void **)&s->bq, f * L * c->q_dim },
+        { (void **)&s->bao, f * L * c->q_dim }, { (void **)&s->bh1, f * L * c->hidden_dim },
+        { (void **)&s->bh3, f * L * c->hidden_dim }, { (void **)&s->batt, f * L * c->n_heads * (size_t)c->max_seq },
+        { (void **)&s->bxq, L * wide }, { (void **)&s->bxd, f * L * (wide / QK) },
+        { (void **)&s->blog, with_logits ? f * L * c->vocab : 0 },
+    };
+    size_t total = 0;
+    for (size_t i = 0; i < sizeof parts / sizeof parts[0]; i++) total += RUP(parts[i].n);
+    s->bmem = krh_alloc(total);
+    if (!s->bmem) return kr_seterr(ML_E_NOMEM, "cannot allocate %zu bytes of HBM for batched prefill", total);
+    size_t off = 0;
+    for (size_t i = 0; i < sizeof parts / sizeof parts[0]; i++) {
+        *parts[i].p = parts[i].n ? (uint8_t *)s->bmem + off : NULL;
+        off += RUP(parts[i].n);
+    }
+    s->ldx = ldx;
+    return ML_OK;
+}
+
+/* One batched step (model/transformer.c:385-425): T tokens at positions
+ * p0.. through every layer with the matrix products shared by the tokens;
+ * every per-token operation is ml_forward's, so the cache and the logits are
+ * those of token-by-token decoding, bit for bit. */
+static ml_status prefill_step(kr_state *s, const int *tokens, int T, int p0, float *logits) {
+    const kr_model *m = s->m;
+    const ml_config *c = &m->cfg;
+    const size_t lkv = (size_t)c->max_seq * c->kv_dim;
+    const int ldx = s->ldx;
+    ml_status st = krh_copy_h2d(s->prompt, tokens, sizeof(int) * (size_t)T);
+    if (st == ML_OK) st = set_ints(s, 0, p0);
+    if (st != ML_OK) return kr_seterr(st, "%s", krh_last_error());
+    krh_embed_batch(s->bx, &m->d_tok_emb, s->prompt, T, c->embed_scale);
+    for (int l = 0; l < c->n_layers; l++) {
+        const struct kr_dev_layer *D = &m->d_layers[l];
+        const ml_layer *L = &m->layers[l];
+        float *kc = s->kcache + (size_t)l * lkv, *vc = s->vcache + (size_t)l * lkv;
+        const float *cs = L->local_rope ? s->rope_cos_l : s->rope_cos, *sn = L->local_rope ? s->rope_sin_l : s->rope_sin;
+        krh_rmsnorm_q8_t(s->bxq, s->bxd, ldx, NULL, s->bx, D->attn_norm, c->dim, c->norm_eps, T);
+        krh_matmul_qkv(s->bq, kc, vc, &D->wq, &D->wk, &D->wv, D->bq, D->bk, D->bv, s->bxq, s->bxd, ldx, T, cs, sn,
+                       c->head_dim, p0);
+        krh_attention_batch(s->bao, s->batt, s->bq, kc, vc, c->n_heads, c->n_kv_heads, c->head_dim, c->max_seq,
+                            L->window, c->attn_scale, s->pos, T, p0 + T - 1);
+        krh_quantize_q8_t(s->bxq, s->bxd, ldx, s->bao, c->q_dim, T);
+        krh_matmul(s->bx, c->dim, &D->wo, s->bxq, s->bxd, ldx, T, 1);
+        krh_rmsnorm_q8_t(s->bxq, s->bxd, ldx, NULL, s->bx, D->ffn_norm, c->dim, c->norm_eps, T);
+        krh_matmul(s->bh1, c->hidden_dim, &D->w1, s->bxq, s->bxd, ldx, T, 0);
+        krh_matmul(s->bh3, c->hidden_dim, &D->w3, s->bxq, s->bxd, ldx, T, 0);
+        krh_silu_quant(s->bxq, s->bxd, ldx, s->bh1, s->bh3, c->hidden_dim, T);
+        krh_matmul(s->bx, c->dim, &D->w2, s->bxq, s->bxd, ldx, T, 1);
+    }
+    if (logits) {
+        krh_rmsnorm_q8_t(s->bxq, s->bxd, ldx, NULL, s->bx, m->d_final_norm, c->dim, c->norm_eps, T);
+        krh_matmul(s->blog, c->vocab, &m->d_wcls, s->bxq, s->bxd, ldx, T, 0);
+        st = krh_copy_d2h(logits, s->blog, sizeof(float) * (size_t)T * c->vocab);
+        if (st != ML_OK) return kr_seterr(st, "%s", krh_last_error());
+    }
+    return krh_status() == ML_OK ? ML_OK : kr_seterr(krh_status(), "%s", krh_last_error());
+}
+
+/* ml_prefill (model/transformer.c:427-438): n tokens at positions pos0.. in
+ * batched steps of s->batch tokens; with batch 1, each token replays the
+ * captured decode step instead. Every per-token op is ml_forward's, so the
+ * results are the same either way (model/transformer.c:381-384). */
 ml_status kr_prefill(kr_state *s, const int *tokens, int n, int pos0, float *logits) {
     const ml_config *c = &s->m->cfg;
     if (n < 0 || pos0 < 0 || pos0 + n > c->max_seq) return ML_E_SHAPE;
     for (int i = 0; i < n; i++)
         if (tokens[i] < 0 || tokens[i] >= c->vocab) return ML_E_SHAPE;
+    if (s->batch > 1 && n > 1) {
+        ml_status st = batch_buffers(s, logits != NULL);
+        for (int i = 0; st == ML_OK && i < n; i += s->batch) {
+            const int T = n - i < s->batch ? n - i : s->batch;
+            st = prefill_step(s, tokens + i, T, pos0 + i, logits ? logits + (size_t)i * c->vocab : NULL);
+        }
+        return st == ML_OK ? dev_status() : st;
+    }
     if (logits) {
         for (int i = 0; i < n; i++) {
             const ml_status st = kr_forward(s, tokens[i], pos0 + i, logits + (size_t)i * c->vocab);

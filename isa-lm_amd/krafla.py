@@ -110,13 +110,24 @@ for name, res, args in [
     ("krh_matvec", None, [_P, C.POINTER(KrhMat), _P, _P, C.c_int]),
     ("krh_matvec_qkv", None, [_P, _P, _P, C.POINTER(KrhMat), C.POINTER(KrhMat), C.POINTER(KrhMat), _P, _P, _P,
                               _P, _P, _P, _P, C.c_int, _P]),
-    ("krh_matvec_swiglu_q8", None, [_P, _P, _P, C.POINTER(KrhMat), C.POINTER(KrhMat), _P, _P]),
+    ("krh_matvec_f", None, [_P, C.POINTER(KrhMat), _P, C.c_int]),
+    ("krh_matvec_swiglu", None, [_P, C.POINTER(KrhMat), C.POINTER(KrhMat), _P, _P]),
     ("krh_attention", None, [_P, _P, _P, _P, _P, _P, _P, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_float,
                              _P]),
     ("krh_argmax", None, [_P, _P, C.c_int, _P, _P]),
+    ("krh_rmsnorm_q8_t", None, [_P, _P, C.c_int, _P, _P, _P, C.c_int, C.c_float, C.c_int]),
+    ("krh_quantize_q8_t", None, [_P, _P, C.c_int, _P, C.c_int, C.c_int]),
+    ("krh_matmul", None, [_P, C.c_int, C.POINTER(KrhMat), _P, _P, C.c_int, C.c_int, C.c_int]),
+    ("krh_matmul_qkv", None, [_P, _P, _P, C.POINTER(KrhMat), C.POINTER(KrhMat), C.POINTER(KrhMat), _P, _P, _P,
+                              _P, _P, C.c_int, C.c_int, _P, _P, C.c_int, C.c_int]),
+    ("krh_attention_batch", None, [_P, _P, _P, _P, _P, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_float,
+                                   _P, C.c_int, C.c_int]),
+    ("krh_silu_quant", None, [_P, _P, C.c_int, _P, _P, C.c_int, C.c_int]),
+    ("krh_embed_batch", None, [_P, C.POINTER(KrhMat), _P, C.c_int, C.c_float]),
     ("krh_take_token", None, [_P, _P, _P]), ("krh_advance", None, [_P]),
     ("krh_math_batch", None, [C.c_int, _P, _P, _P, C.c_size_t]), ("krh_h2f_batch", None, [_P, _P, C.c_size_t]),
     ("krh_block_dots", None, [_P, C.POINTER(KrhMat), _P]),
+    ("krh_tune", None, [C.c_int, C.c_int]),
     ("krh_gen_blocks", None, [_P, _P, C.c_uint64, C.c_int, C.c_int, C.c_int, C.c_int, C.c_float]),
 ]:
     f = getattr(hip, name)
@@ -193,6 +204,9 @@ class State:
     def forward(self, token, pos, out):
         """out: a float32 numpy array of vocab entries"""
         check(host.kr_forward(self.ptr, token, pos, out.ctypes.data), "forward")
+
+    def set_batch(self, batch):
+        host.kr_state_set_batch(self.ptr, batch)
 
     def prefill(self, tokens, pos0, logits=None):
         import numpy as np

@@ -225,12 +225,16 @@ def test_rmsnorm_q8(dev, n, ntok):
         assert np.array_equal(bits(db.get(np.float32, n * ntok // 32)[t * n // 32:(t + 1) * n // 32]), bits(d0))
 
 
-@pytest.mark.parametrize("dim,nh,nkv,hd,typ,bias", [(288, 6, 6, 48, K.ML_Q8_0, 0), (896, 14, 2, 64, K.ML_Q4_0, 1),
-                                                     (4096, 32, 8, 128, K.ML_Q8_0, 0)])
-def test_qkv_bias_rope_cache(dev, dim, nh, nkv, hd, typ, bias):
+@pytest.mark.parametrize("dim,nh,nkv,hd,typ,vtyp,bias", [(288, 6, 6, 48, K.ML_Q8_0, K.ML_Q8_0, 0),
+                                                          (896, 14, 2, 64, K.ML_Q4_0, K.ML_Q8_0, 1),
+                                                          (896, 14, 2, 64, K.ML_Q4_0, K.ML_Q4_0, 1),
+                                                          (2048, 32, 8, 64, K.ML_Q4_0, K.ML_Q8_0, 0),
+                                                          (4096, 32, 8, 128, K.ML_Q8_0, K.ML_Q8_0, 0)])
+def test_qkv_bias_rope_cache(dev, dim, nh, nkv, hd, typ, vtyp, bias):
     qd, kvd, max_seq, pos = nh * hd, nkv * hd, 40, 23
-    mats = [rand_mat(r, dim, typ, 1) for r in (qd, kvd, kvd)]
-    Ws = [dmat(dev, q, d, dh, r, dim, typ, 1) for (q, d, dh), r in zip(mats, (qd, kvd, kvd))]
+    typs = (typ, typ, vtyp)
+    mats = [rand_mat(r, dim, t, 1) for r, t in zip((qd, kvd, kvd), typs)]
+    Ws = [dmat(dev, q, d, dh, r, dim, t, 1) for (q, d, dh), r, t in zip(mats, (qd, kvd, kvd), typs)]
     biases = [f32(RNG.normal(0, 0.02, r)) for r in (qd, kvd, kvd)]
     cs, sn = f32(RNG.uniform(-1, 1, max_seq * hd // 2)), f32(RNG.uniform(-1, 1, max_seq * hd // 2))
     xq, xd = O.quantize(f32(RNG.normal(0, 1, dim)))
@@ -242,8 +246,8 @@ def test_qkv_bias_rope_cache(dev, dim, nh, nkv, hd, typ, bias):
                          dev.put(cs).ptr, dev.put(sn).ptr, hd, posb.ptr)
     ok()
     outs = []
-    for (q, d, dh), r, b in zip(mats, (qd, kvd, kvd), biases):
-        y = oracle_matvec(q, d, r, dim, typ, xq, xd)
+    for (q, d, dh), r, b, t in zip(mats, (qd, kvd, kvd), biases, typs):
+        y = oracle_matvec(q, d, r, dim, t, xq, xd)
         if bias:
             oracle.kro_add(y.ctypes.data, b.ctypes.data, r)
         outs.append(y)
@@ -255,21 +259,37 @@ def test_qkv_bias_rope_cache(dev, dim, nh, nkv, hd, typ, bias):
     assert np.array_equal(bits(vc.get(np.float32, max_seq * kvd)[pos * kvd:(pos + 1) * kvd]), bits(outs[2]))
 
 
-@pytest.mark.parametrize("rows,cols,typ", [(768, 288, K.ML_Q8_0), (4864, 896, K.ML_Q4_0), (14336, 4096, K.ML_Q8_0)])
-def test_swiglu_q8(dev, rows, cols, typ):
+@pytest.mark.parametrize("rows,cols,typ", [(768, 288, K.ML_Q8_0), (4864, 896, K.ML_Q4_0), (14336, 4096, K.ML_Q8_0),
+                                           (8192, 2048, K.ML_Q4_0), (40, 96, K.ML_Q8_0)])
+def test_swiglu(dev, rows, cols, typ):
     (q1, d1, h1), (q3, d3, h3) = rand_mat(rows, cols, typ, 1), rand_mat(rows, cols, typ, 1)
     W1, W3 = dmat(dev, q1, d1, h1, rows, cols, typ, 1), dmat(dev, q3, d3, h3, rows, cols, typ, 1)
     xq, xd = O.quantize(f32(RNG.normal(0, 1, cols) * 30))
-    hq, hdb, hb = dev.zeros(rows), dev.zeros(4 * rows // 32), dev.zeros(4 * rows)
-    K.hip.krh_matvec_swiglu_q8(hq.ptr, hdb.ptr, hb.ptr, C.byref(W1), C.byref(W3), dev.put(xq).ptr, dev.put(xd).ptr)
+    hb = dev.zeros(4 * rows)
+    K.hip.krh_matvec_swiglu(hb.ptr, C.byref(W1), C.byref(W3), dev.put(xq).ptr, dev.put(xd).ptr)
     ok()
     g = oracle_matvec(q1, d1, rows, cols, typ, xq, xd)
     u = oracle_matvec(q3, d3, rows, cols, typ, xq, xd)
     oracle.kro_silu_mul(g.ctypes.data, u.ctypes.data, rows)
-    q0, d0 = O.quantize(g)
     assert np.array_equal(bits(hb.get(np.float32, rows)), bits(g))
-    assert np.array_equal(hq.get(np.int8, rows), q0)
-    assert np.array_equal(bits(hdb.get(np.float32, rows // 32)), bits(d0))
+
+
+@pytest.mark.parametrize("typ,d16", [(K.ML_Q8_0, 1), (K.ML_Q4_0, 0)])
+@pytest.mark.parametrize("rows,cols", [(4096, 14336), (4096, 4096), (896, 4864), (288, 768), (5, 64)])
+def test_matvec_float_input(dev, typ, d16, rows, cols):
+    """y += W quantize_q8(x): the input quantized inside the launch, as
+    transformer.c quantizes hb and ao before w2 and wo"""
+    q, d, dh = rand_mat(rows, cols, typ, d16)
+    x = f32(RNG.normal(0, 1, cols) * RNG.choice([1e-3, 1.0, 50.0], cols))
+    x[:32] = 0.0
+    y0 = f32(RNG.normal(0, 1, rows))
+    W = dmat(dev, q, d, dh, rows, cols, typ, d16)
+    yb = dev.put(y0)
+    K.hip.krh_matvec_f(yb.ptr, C.byref(W), dev.put(x).ptr, 1)
+    ok()
+    xq, xd = O.quantize(x)
+    want = (y0 + oracle_matvec(q, d, rows, cols, typ, xq, xd)).astype(np.float32)
+    assert np.array_equal(bits(yb.get(np.float32, rows)), bits(want))
 
 
 @pytest.mark.parametrize("nh,nkv,hd,pos,window", [(6, 6, 48, 0, 0), (6, 6, 48, 200, 0), (14, 2, 64, 511, 0),
@@ -330,3 +350,121 @@ def test_embed(dev, typ, d16, scale):
     if scale != 1.0:
         want = (want * np.float32(scale)).astype(np.float32)
     assert np.array_equal(bits(xb.get(np.float32, cols)), bits(want))
+
+
+# ---- batched prefill ----
+
+def transposed_scales(dq, T, nb, ldx):
+    """[T][nb] scales -> [nb][ldx] (the layout krh_matmul reads)"""
+    out = np.zeros((nb, ldx), np.float32)
+    out[:, :T] = dq.reshape(T, nb).T
+    return out
+
+
+@pytest.mark.parametrize("typ,d16", [(K.ML_Q8_0, 1), (K.ML_Q4_0, 1), (K.ML_Q8_0, 0), (K.ML_Q4_0, 0)])
+@pytest.mark.parametrize("rows,cols,T", [(100, 64, 37), (256, 288, 130), (896, 4864, 5), (4096, 4096, 129),
+                                         (1024, 14336, 64), (33, 32, 1)])
+def test_matmul(dev, typ, d16, rows, cols, T):
+    """int8-MFMA matmul: every token's row equals the matvec's, bit for bit
+    (the reference's matmul column == matvec rule, tests/test_kernels.c:146-189)"""
+    q, d, dh = rand_mat(rows, cols, typ, d16)
+    X = f32(RNG.normal(0, 1, (T, cols)) * RNG.choice([1e-2, 1.0, 30.0], (T, 1)))
+    ldx = (T + 127) // 128 * 128
+    xq = np.zeros((ldx, cols), np.int8)
+    xd = np.zeros((T, cols // 32), np.float32)
+    for t in range(T):
+        xq[t], xd[t] = O.quantize(X[t])
+    W = dmat(dev, q, d, dh, rows, cols, typ, d16)
+    y0 = f32(RNG.normal(0, 1, (T, rows)))
+    for acc in (0, 1):
+        yb = dev.put(y0)
+        K.hip.krh_matmul(yb.ptr, rows, C.byref(W), dev.put(xq).ptr,
+                         dev.put(transposed_scales(xd, T, cols // 32, ldx)).ptr, ldx, T, acc)
+        ok()
+        got = yb.get(np.float32, T * rows).reshape(T, rows)
+        for t in range(T):
+            want = oracle_matvec(q, d, rows, cols, typ, xq[t], xd[t])
+            if acc:
+                want = (y0[t] + want).astype(np.float32)
+            assert np.array_equal(bits(got[t]), bits(want)), (t, acc)
+
+
+@pytest.mark.parametrize("dim,nh,nkv,hd,typ,vtyp,bias", [(288, 6, 6, 48, K.ML_Q8_0, K.ML_Q8_0, 0),
+                                                          (896, 14, 2, 64, K.ML_Q4_0, K.ML_Q8_0, 1),
+                                                          (4096, 32, 8, 128, K.ML_Q8_0, K.ML_Q8_0, 0)])
+def test_matmul_qkv_matches_decode(dev, dim, nh, nkv, hd, typ, vtyp, bias):
+    """the batched projections (bias, RoPE, cache rows) equal the decode
+    step's for every token"""
+    qd, kvd, max_seq, pos0, T = nh * hd, nkv * hd, 300, 17, 140
+    typs = (typ, typ, vtyp)
+    mats = [rand_mat(r, dim, t, 1) for r, t in zip((qd, kvd, kvd), typs)]
+    Ws = [dmat(dev, q, d, dh, r, dim, t, 1) for (q, d, dh), r, t in zip(mats, (qd, kvd, kvd), typs)]
+    bb = [dev.put(f32(RNG.normal(0, 0.02, r))) if bias else None for r in (qd, kvd, kvd)]
+    cs, sn = dev.put(f32(RNG.uniform(-1, 1, max_seq * hd // 2))), dev.put(f32(RNG.uniform(-1, 1, max_seq * hd // 2)))
+    ldx = (T + 127) // 128 * 128
+    xq = np.zeros((ldx, dim), np.int8)
+    xd = np.zeros((T, dim // 32), np.float32)
+    for t in range(T):
+        xq[t], xd[t] = O.quantize(f32(RNG.normal(0, 1, dim)))
+    qb, kc, vc = dev.zeros(4 * T * qd), dev.zeros(4 * max_seq * kvd), dev.zeros(4 * max_seq * kvd)
+    K.hip.krh_matmul_qkv(qb.ptr, kc.ptr, vc.ptr, C.byref(Ws[0]), C.byref(Ws[1]), C.byref(Ws[2]),
+                         *[b.ptr if b else None for b in bb], dev.put(xq).ptr,
+                         dev.put(transposed_scales(xd, T, dim // 32, ldx)).ptr, ldx, T, cs.ptr, sn.ptr, hd, pos0)
+    ok()
+    got_q = qb.get(np.float32, T * qd).reshape(T, qd)
+    got_k = kc.get(np.float32, max_seq * kvd).reshape(max_seq, kvd)
+    got_v = vc.get(np.float32, max_seq * kvd).reshape(max_seq, kvd)
+    q1, k1, v1 = dev.zeros(4 * qd), dev.zeros(4 * max_seq * kvd), dev.zeros(4 * max_seq * kvd)
+    for t in range(0, T, 13):
+        posb = dev.put(np.array([pos0 + t], np.int32))
+        K.hip.krh_matvec_qkv(q1.ptr, k1.ptr, v1.ptr, C.byref(Ws[0]), C.byref(Ws[1]), C.byref(Ws[2]),
+                             *[b.ptr if b else None for b in bb], dev.put(xq[t]).ptr, dev.put(xd[t]).ptr,
+                             cs.ptr, sn.ptr, hd, posb.ptr)
+        ok()
+        p = pos0 + t
+        assert np.array_equal(bits(got_q[t]), bits(q1.get(np.float32, qd)))
+        assert np.array_equal(bits(got_k[p]), bits(k1.get(np.float32, max_seq * kvd)[p * kvd:(p + 1) * kvd]))
+        assert np.array_equal(bits(got_v[p]), bits(v1.get(np.float32, max_seq * kvd)[p * kvd:(p + 1) * kvd]))
+
+
+@pytest.mark.parametrize("nh,nkv,hd,pos0,T,window", [(6, 6, 48, 0, 40, 0), (32, 8, 128, 100, 70, 0),
+                                                     (14, 2, 64, 3, 200, 0), (8, 2, 64, 10, 50, 7)])
+def test_attention_batch_matches_decode(dev, nh, nkv, hd, pos0, T, window):
+    max_seq = 512
+    kvd, qd = nkv * hd, nh * hd
+    Q = f32(RNG.normal(0, 1, (T, qd)))
+    kc = f32(RNG.normal(0, 1, max_seq * kvd))
+    vc = f32(RNG.normal(0, 1, max_seq * kvd))
+    scale = float(np.float32(1.0) / np.sqrt(np.float32(hd)))
+    kb, vb = dev.put(kc), dev.put(vc)
+    ao, att = dev.zeros(4 * T * qd), dev.zeros(4 * T * nh * max_seq)
+    K.hip.krh_attention_batch(ao.ptr, att.ptr, dev.put(Q).ptr, kb.ptr, vb.ptr, nh, nkv, hd, max_seq, window, scale,
+                              dev.put(np.array([pos0], np.int32)).ptr, T, pos0 + T - 1)
+    ok()
+    got = ao.get(np.float32, T * qd).reshape(T, qd)
+    cfg = K.MlConfig(n_heads=nh, n_kv_heads=nkv, head_dim=hd, kv_dim=kvd, q_dim=qd, max_seq=max_seq,
+                     attn_scale=scale)
+    kvl = O.KvLayer(kc.ctypes.data, vc.ctypes.data, None, None, None, None, window, None, None)
+    scratch = np.zeros(max_seq, np.float32)
+    for t in range(T):
+        out = np.zeros(qd, np.float32)
+        qt = f32(Q[t])
+        oracle.kro_attention(out.ctypes.data, qt.ctypes.data, C.byref(kvl), scratch.ctypes.data, C.byref(cfg),
+                             pos0 + t)
+        assert np.array_equal(bits(got[t]), bits(out)), t
+
+
+def test_silu_quant(dev):
+    n, T = 4864, 9
+    g, u = f32(RNG.normal(0, 3, (T, n))), f32(RNG.normal(0, 1, (T, n)))
+    ldx = 128
+    qb, db = dev.zeros(T * n), dev.zeros(4 * (n // 32) * ldx)
+    K.hip.krh_silu_quant(qb.ptr, db.ptr, ldx, dev.put(g).ptr, dev.put(u).ptr, n, T)
+    ok()
+    q = qb.get(np.int8, T * n).reshape(T, n)
+    d = db.get(np.float32, (n // 32) * ldx).reshape(n // 32, ldx)
+    for t in range(T):
+        h = f32(g[t])
+        oracle.kro_silu_mul(h.ctypes.data, f32(u[t]).ctypes.data, n)
+        q0, d0 = O.quantize(h)
+        assert np.array_equal(q[t], q0) and np.array_equal(bits(d[:, t]), bits(d0))

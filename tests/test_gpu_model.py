@@ -50,6 +50,29 @@ def test_logits_match_reference(name, workdir):
     m.close()
 
 
+@pytest.mark.parametrize("batch", [1, 5])
+@pytest.mark.parametrize("name", ["qwen_like_q4mix", "llama3_rope_gqa_q4", "c1_q8"])
+def test_prefill_paths_match_reference(name, batch, workdir):
+    """token-by-token (batch 1) and chunked batched prefill give the
+    reference's logits too (model/transformer.c:381-384)"""
+    path = os.path.join(workdir, name + ".mlb")
+    if not os.path.exists(path):
+        K.gen_mlb(path, **SMALL[name])
+    m = K.Model(path)
+    s = K.State(m)
+    s.set_batch(batch)
+    V = m.cfg.vocab
+    toks = [int(t) for t in np.random.default_rng(5).integers(1, V, 12)]
+    dump = path + ".logits"
+    O.ref_ml_run(path, toks, len(toks), dump=dump)
+    want = np.fromfile(dump, dtype=np.float32).reshape(len(toks), V)
+    got = np.empty((len(toks), V), dtype=np.float32)
+    s.prefill(toks, 0, logits=got)
+    assert np.array_equal(bits(got), bits(want))
+    s.close()
+    m.close()
+
+
 @pytest.mark.parametrize("name", sorted(SMALL))
 def test_greedy_ids_match_reference(name, workdir):
     path = os.path.join(workdir, name + ".mlb")
