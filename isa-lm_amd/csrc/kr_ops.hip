@@ -1,0 +1,218 @@
+// The reference's unfused kernels as device ops, one launch each, for the
+// op-table binding (ml_k_<op>_hip under config/ml_config.h): every kernel in
+// the scalar kernel's float order (kernels/scalar/k_scalar.c), so an
+// unchanged model/transformer.c gets the scalar build's bits.
+#include "kr_internal.h"
+#include "kr_numerics.h"
+
+namespace {
+
+constexpr int OP_T = 256;
+
+// o = (x * inv) * w, inv = 1 / sqrtf(ss / n + eps), ss = sum x_i * x_i in
+// index order (k_scalar.c:59-64). One workgroup; the squares go to LDS and
+// lane 0 adds them; o may alias x (each thread reads its values before the
+// barrier that precedes every write).
+__global__ void __launch_bounds__(OP_T) k_rmsnorm(float *o, const float *x, const float *w, int n, float eps) {
+    extern __shared__ float sq[];
+    __shared__ float s_inv;
+    const int tid = threadIdx.x;
+    for (int i = tid; i < n; i += OP_T) sq[i] = kr_fmul(x[i], x[i]);
+    __syncthreads();
+    if (tid == 0) {
+        float ss = 0.0f;
+        for (int i = 0; i < n; i++) ss = kr_fadd(ss, sq[i]);
+        s_inv = kr_fdiv(1.0f, kr_fsqrt(kr_fadd(kr_fdiv(ss, (float)n), eps)));
+    }
+    __syncthreads();
+    const float inv = s_inv;
+    for (int i = tid; i < n; i += OP_T) o[i] = kr_fmul(kr_fmul(x[i], inv), w[i]);
+}
+
+__global__ void k_add(float *y, const float *x, int n) {   // k_scalar.c:107-109
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) y[i] = kr_fadd(y[i], x[i]);
+}
+
+// pairs (2i, 2i+1) of every head of q (nh heads) and k (nkv heads):
+// (a c - b s, a s + b c) (k_scalar.c:79-94)
+__global__ void k_rope(float *q, float *k, const float *c, const float *s, int hd, int nh, int nkv) {
+    const int p = blockIdx.x * blockDim.x + threadIdx.x, h2 = hd / 2;
+    if (p >= (nh + nkv) * h2) return;
+    float *v = p < nh * h2 ? q + (size_t)(p / h2) * hd : k + (size_t)(p / h2 - nh) * hd;
+    const int i = p % h2;
+    const float a = v[2 * i], b = v[2 * i + 1];
+    v[2 * i] = kr_fsub(kr_fmul(a, c[i]), kr_fmul(b, s[i]));
+    v[2 * i + 1] = kr_fadd(kr_fmul(a, s[i]), kr_fmul(b, c[i]));
+}
+
+__global__ void k_silu_mul(float *g, const float *u, int n) {   // k_scalar.c:96-98
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) g[i] = kr_fmul(kr_fdiv(g[i], kr_fadd(1.0f, kr_expf(-g[i]))), u[i]);
+}
+
+// k_scalar.c:100-105 with the device library's tanhf (its bits are not the C
+// library's: parity of this op is not pinned)
+__global__ void k_gelu_mul(float *g, const float *u, int n) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const float x = g[i];
+    const float c = kr_fmul(kr_fmul(kr_fmul(0.044715f, x), x), x);
+    const float t = tanhf(kr_fmul(0.7978845608f, kr_fadd(x, c)));
+    g[i] = kr_fmul(kr_fmul(kr_fmul(0.5f, x), kr_fadd(1.0f, t)), u[i]);
+}
+
+// k_scalar.c:66-77: max, expf(x - max), the sum in index order, x * (1/sum);
+// all -inf: 1/n
+__global__ void __launch_bounds__(OP_T) k_softmax(float *x, int n) {
+    __shared__ float red[OP_T / 64];
+    __shared__ float s_inv;
+    const int tid = threadIdx.x;
+    float m = -INFINITY;
+    for (int i = tid; i < n; i += OP_T) m = fmaxf(m, x[i]);
+    for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+    if ((tid & 63) == 0) red[tid >> 6] = m;
+    __syncthreads();
+    float mx = red[0];
+    for (int k = 1; k < OP_T / 64; k++) mx = fmaxf(mx, red[k]);
+    if (mx == -INFINITY) {
+        for (int i = tid; i < n; i += OP_T) x[i] = kr_fdiv(1.0f, (float)n);
+        return;
+    }
+    for (int i = tid; i < n; i += OP_T) x[i] = kr_expf(kr_fsub(x[i], mx));
+    __syncthreads();
+    if (tid == 0) {
+        float sum = 0.0f;
+        for (int i = 0; i < n; i++) sum = kr_fadd(sum, x[i]);
+        s_inv = kr_fdiv(1.0f, sum);
+    }
+    __syncthreads();
+    for (int i = tid; i < n; i += OP_T) x[i] = kr_fmul(x[i], s_inv);
+}
+
+// s[t] = (sum_i q_i k_t,i in index order) * scale (k_scalar.c:111-117)
+__global__ void k_dot_rows(float *s, const float *q, const float *k, size_t ldk, int rows, int n, float scale) {
+    const int t = blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= rows) return;
+    const float *kt = k + (size_t)t * ldk;
+    float acc = 0.0f;
+    for (int i = 0; i < n; i++) acc = kr_fadd(acc, kr_fmul(q[i], kt[i]));
+    s[t] = kr_fmul(acc, scale);
+}
+
+// y[i] += a[t] * x_t,i for t in order (k_scalar.c:119-122)
+__global__ void k_axpy_rows(float *y, const float *a, const float *x, size_t ldx, int rows, int n) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    float o = y[i];
+    for (int t = 0; t < rows; t++) o = kr_fadd(o, kr_fmul(a[t], x[(size_t)t * ldx + i]));
+    y[i] = o;
+}
+
+// one scale over n values (ops/ops.c:81-96): the quantize_q8 rule
+__global__ void __launch_bounds__(OP_T) k_quantize_row(int8_t *q, float *d, const float *x, int n) {
+    __shared__ float red[OP_T / 64];
+    const int tid = threadIdx.x;
+    float m = 0.0f;
+    for (int i = tid; i < n; i += OP_T) m = fmaxf(m, fabsf(x[i]));
+    for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+    if ((tid & 63) == 0) red[tid >> 6] = m;
+    __syncthreads();
+    float amax = red[0];
+    for (int k = 1; k < OP_T / 64; k++) amax = fmaxf(amax, red[k]);
+    if (amax < KR_QUANT_TINY) {
+        if (tid == 0) *d = 0.0f;
+        for (int i = tid; i < n; i += OP_T) q[i] = 0;
+        return;
+    }
+    const float id = kr_fdiv(127.0f, amax);
+    if (tid == 0) *d = kr_fdiv(amax, 127.0f);
+    for (int i = tid; i < n; i += OP_T) q[i] = (int8_t)kr_q8_elem(x[i], id);
+}
+
+// x = cap * tanhf(x / cap) (ops/ops.c:98-101; tanhf: parity not pinned)
+__global__ void k_softcap(float *x, size_t ld, int rows, int n, float cap) {
+    const size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (e >= (size_t)rows * n) return;
+    float *p = x + (e / n) * ld + e % n;
+    *p = kr_fmul(cap, tanhf(kr_fdiv(*p, cap)));
+}
+
+__global__ void k_set_int(int *dst, int v) { *dst = v; }
+
+// dT[b * ldx + t] = d[t * nb + b]
+__global__ void k_transpose(float *dT, int ldx, const float *d, int n, int nb) {
+    const size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (e >= (size_t)n * nb) return;
+    const int t = (int)(e / nb), b = (int)(e % nb);
+    dT[(size_t)b * ldx + t] = d[e];
+}
+
+unsigned blocks(size_t n) { return (unsigned)((n + OP_T - 1) / OP_T); }
+
+}  // namespace
+
+extern "C" void krh_rmsnorm(float *o, const float *x, const float *w, int n, float eps) {
+    if (n <= 0 || n > 16384) { kr_fail(ML_E_SHAPE, "rmsnorm size", hipSuccess); return; }
+    hipLaunchKernelGGL(k_rmsnorm, dim3(1), dim3(OP_T), sizeof(float) * (size_t)n, kr_stream(), o, x, w, n, eps);
+    kr_check_launch("rmsnorm");
+}
+extern "C" void krh_add(float *y, const float *x, int n) {
+    if (n <= 0) return;
+    hipLaunchKernelGGL(k_add, dim3(blocks(n)), dim3(OP_T), 0, kr_stream(), y, x, n);
+    kr_check_launch("add");
+}
+extern "C" void krh_rope(float *q, float *k, const float *cos_t, const float *sin_t, int head_dim, int n_heads,
+                         int n_kv_heads) {
+    const size_t n = (size_t)(n_heads + n_kv_heads) * (head_dim / 2);
+    if (n == 0) return;
+    hipLaunchKernelGGL(k_rope, dim3(blocks(n)), dim3(OP_T), 0, kr_stream(), q, k, cos_t, sin_t, head_dim, n_heads,
+                       n_kv_heads);
+    kr_check_launch("rope");
+}
+extern "C" void krh_silu_mul(float *g, const float *u, int n) {
+    if (n <= 0) return;
+    hipLaunchKernelGGL(k_silu_mul, dim3(blocks(n)), dim3(OP_T), 0, kr_stream(), g, u, n);
+    kr_check_launch("silu_mul");
+}
+extern "C" void krh_gelu_mul(float *g, const float *u, int n) {
+    if (n <= 0) return;
+    hipLaunchKernelGGL(k_gelu_mul, dim3(blocks(n)), dim3(OP_T), 0, kr_stream(), g, u, n);
+    kr_check_launch("gelu_mul");
+}
+extern "C" void krh_softmax(float *x, int n) {
+    if (n <= 0) return;
+    hipLaunchKernelGGL(k_softmax, dim3(1), dim3(OP_T), 0, kr_stream(), x, n);
+    kr_check_launch("softmax");
+}
+extern "C" void krh_dot_rows(float *s, const float *q, const float *k, size_t ldk, int rows, int n, float scale) {
+    if (rows <= 0) return;
+    hipLaunchKernelGGL(k_dot_rows, dim3(blocks(rows)), dim3(OP_T), 0, kr_stream(), s, q, k, ldk, rows, n, scale);
+    kr_check_launch("dot_rows");
+}
+extern "C" void krh_axpy_rows(float *y, const float *a, const float *x, size_t ldx, int rows, int n) {
+    if (n <= 0) return;
+    hipLaunchKernelGGL(k_axpy_rows, dim3(blocks(n)), dim3(OP_T), 0, kr_stream(), y, a, x, ldx, rows, n);
+    kr_check_launch("axpy_rows");
+}
+extern "C" void krh_quantize_row(int8_t *q, float *d, const float *x, int n) {
+    if (n <= 0) return;
+    hipLaunchKernelGGL(k_quantize_row, dim3(1), dim3(OP_T), 0, kr_stream(), q, d, x, n);
+    kr_check_launch("quantize_row");
+}
+extern "C" void krh_softcap_rows(float *x, size_t ld, int rows, int n, float cap) {
+    const size_t e = (size_t)rows * n;
+    if (e == 0) return;
+    hipLaunchKernelGGL(k_softcap, dim3(blocks(e)), dim3(OP_T), 0, kr_stream(), x, ld, rows, n, cap);
+    kr_check_launch("softcap");
+}
+extern "C" void krh_set_int(int *dst, int value) {
+    hipLaunchKernelGGL(k_set_int, dim3(1), dim3(1), 0, kr_stream(), dst, value);
+    kr_check_launch("set_int");
+}
+extern "C" void krh_transpose_scales(float *dT, int ldx, const float *d, int n, int nb) {
+    const size_t e = (size_t)n * nb;
+    if (e == 0) return;
+    hipLaunchKernelGGL(k_transpose, dim3(blocks(e)), dim3(OP_T), 0, kr_stream(), dT, ldx, d, n, nb);
+    kr_check_launch("transpose_scales");
+}

@@ -1,0 +1,525 @@
+/* ISA=hip: the modules an ISA=hip build of Krafla owns, over the MI355X
+ * backend (libkrafla_hip.so), so that the reference's model/transformer.c,
+ * model/mlb.c, model/sampler.c and app/ml_run.c run unchanged:
+ *
+ *   core/arena.c       ml_arena_*: pinned host memory plus an HBM twin
+ *   core/threads.c     ml_pool_*: one worker (the stream orders the work);
+ *                      creating the pool (the last step of ml_state_init,
+ *                      model/transformer.c:163) uploads the arenas, after the
+ *                      host has written the RoPE tables into them
+ *   model/pack_model.c ml_model_pack*: uploads the mapped model file
+ *   core/quant_ref.c   ml_dequant_row (device gather into the arena),
+ *                      ml_quantize_row_q4 (host)
+ *   core/isa_check.c   ml_isa_check: a gfx950 device or ML_E_ISA (exit 3)
+ *   ops/ops.c          ml_matvec, ml_matmul (int8 MFMA), ml_attention(_batch),
+ *                      ml_quantize_row, ml_softcap_rows
+ *   kernels/hip        ml_k_<op>_hip, bound by config/ml_config.h
+ *
+ * Pointer contract (the reference code passes host addresses): an address
+ * inside a registered range (an arena, a model file) stands for its HBM copy;
+ * any other buffer is staged to the device for the call and copied back.
+ * The host reads activations only as logits: the classifier's matvec copies
+ * them back and synchronizes, which is also where device errors surface.
+ * Supported: the F32 KV cache, models without embed_scale != 1, no --imatrix
+ * (those paths write or read arena memory on the host). */
+#include <math.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+#include "config/ml_config.h"
+#include "core/arena.h"
+#include "core/isa_check.h"
+#include "core/quant_ref.h"
+#include "core/threads.h"
+#include "model/pack_model.h"
+#include "ops/ops.h"
+#define KRAFLA_TYPES_H   /* the types come from the reference's core/ml.h */
+#include "krafla_hip.h"
+
+/* ---- address ranges with an HBM copy ---- */
+
+typedef struct {
+    const uint8_t *h;
+    size_t n;
+    uint8_t *d;
+    int uploaded;
+} kh_range;
+
+#define KH_RANGES 64
+static kh_range g_rg[KH_RANGES];
+static int g_nrg;
+static int *g_ints;                 /* device ints: [0] position, [1] token row */
+static float *g_dT, *g_batt;        /* matmul scales, batched attention scratch */
+static size_t g_dT_n, g_batt_n;
+static const void *g_cls_q;         /* the classifier's quants (ml_model_pack) */
+static int g_reported;
+
+static int ready(void) {
+    if (krh_init() != ML_OK) return 0;
+    if (!g_ints) g_ints = krh_alloc(2 * sizeof(int));
+    return g_ints != NULL;
+}
+
+static uint8_t *dev_addr(const void *p, size_t n) {
+    const uint8_t *b = p;
+    for (int i = 0; i < g_nrg; i++) {
+        const kh_range *r = &g_rg[i];
+        if (b >= r->h && n <= r->n && (size_t)(b - r->h) <= r->n - n) return r->d + (b - r->h);
+    }
+    return NULL;
+}
+
+static void drop_range(const void *h) {
+    for (int i = 0; i < g_nrg; i++)
+        if (g_rg[i].h == h) {
+            g_rg[i] = g_rg[--g_nrg];
+            return;
+        }
+}
+
+static int add_range(const void *h, size_t n, uint8_t *d, int uploaded) {
+    drop_range(h);
+    if (g_nrg == KH_RANGES) return 0;
+    g_rg[g_nrg++] = (kh_range){ h, n, d, uploaded };
+    return 1;
+}
+
+static void *grow(void *p, size_t *have, size_t need) {
+    if (need <= *have) return p;
+    krh_sync();
+    krh_free(p);
+    p = krh_alloc(need);
+    *have = p ? need : 0;
+    return p;
+}
+
+/* ---- one call's arguments ---- */
+
+typedef struct {
+    void *h;
+    uint8_t *d;
+    size_t n;
+    int out;
+} kh_buf;
+
+typedef struct {
+    kh_buf st[16], mir[8];   /* staged buffers; arena outputs */
+    int nst, nmir, staged, fail;
+} kh_call;
+
+/* The device address of caller buffer h of n bytes for one call: its HBM
+ * copy, or a staged copy (filled when `in`, copied back when `out`). */
+static void *arg(kh_call *c, const void *h, size_t n, int in, int out) {
+    if (!h || !n || c->fail) return (void *)h;
+    uint8_t *d = dev_addr(h, n);
+    if (d) {
+        if (out && c->nmir < 8) c->mir[c->nmir++] = (kh_buf){ (void *)h, d, n, 1 };
+        return d;
+    }
+    if (c->nst == 16 || !(d = krh_alloc(n)) || (in && krh_copy_h2d(d, h, n) != ML_OK)) {
+        krh_free(d);
+        c->fail = 1;
+        return NULL;
+    }
+    c->st[c->nst++] = (kh_buf){ (void *)h, d, n, out };
+    c->staged = 1;
+    return d;
+}
+
+/* Copies staged outputs back (and, when weights were staged, outputs that
+ * live in the arena too: their host copy is what a host reader sees) */
+static void done(kh_call *c) {
+    for (int i = 0; i < c->nst; i++)
+        if (c->st[i].out) krh_copy_d2h(c->st[i].h, c->st[i].d, c->st[i].n);
+    if (c->staged)
+        for (int i = 0; i < c->nmir; i++) krh_copy_d2h(c->mir[i].h, c->mir[i].d, c->mir[i].n);
+    if (c->nst) krh_sync();
+    for (int i = 0; i < c->nst; i++) krh_free(c->st[i].d);
+}
+
+/* rows [r0, r1) of W as a device matrix (the file's f16 scales when it has them) */
+static void mat_of(kh_call *c, const ml_qtensor *W, int r0, int r1, krh_mat *m) {
+    const size_t nb = (size_t)W->cols / QK, rowq = W->type == ML_Q8_0 ? (size_t)W->cols : (size_t)W->cols / 2;
+    const size_t nr = (size_t)(r1 - r0);
+    m->rows = r1 - r0;
+    m->cols = W->cols;
+    m->type = W->type;
+    m->q = arg(c, (const uint8_t *)W->q + (size_t)r0 * rowq, nr * rowq, 1, 0);
+    if (W->dh) {
+        m->d16 = 1;
+        m->d = arg(c, W->dh + (size_t)r0 * nb, nr * nb * 2, 1, 0);
+    } else {
+        m->d16 = 0;
+        m->d = arg(c, W->d + (size_t)r0 * nb, nr * nb * 4, 1, 0);
+    }
+}
+
+static void fail_call(const char *what) {
+    if (!g_reported) fprintf(stderr, "error: hip backend: %s\n", what);
+    g_reported = 1;
+}
+
+ml_status ml_hip_status(void) { return krh_status(); }
+const char *ml_hip_last_error(void) { return krh_last_error(); }
+
+/* ---- core/isa_check.c ---- */
+
+const char *ml_isa_build_name(void) { return ML_ISA_NAME; }
+
+ml_status ml_isa_check(const char **missing) {
+    if (ready()) return ML_OK;
+    *missing = "an AMD Instinct MI355X (gfx950) GPU";
+    return ML_E_ISA;
+}
+
+/* ---- core/arena.c: the same bump allocator (core/arena.c:3-26) over
+ * pinned host memory, with an HBM twin registered for translation ---- */
+
+ml_status ml_arena_init(ml_arena *a, size_t cap) {
+    a->base = NULL;
+    a->cap = a->off = 0;
+    if (cap > (size_t)-1 - ML_ALIGN || !ready()) return cap > (size_t)-1 - ML_ALIGN ? ML_E_NOMEM : ML_E_ISA;
+    cap = (cap + ML_ALIGN - 1) & ~(size_t)(ML_ALIGN - 1);
+    uint8_t *h = krh_host_alloc(cap), *d = krh_alloc(cap);
+    if (!h || !d || !add_range(h, cap, d, 0)) {
+        krh_host_free(h);
+        krh_free(d);
+        return ML_E_NOMEM;
+    }
+    a->base = h;
+    a->cap = cap;
+    return ML_OK;
+}
+
+void *ml_arena_alloc(ml_arena *a, size_t n) {
+    const size_t need = (n + ML_ALIGN - 1) & ~(size_t)(ML_ALIGN - 1);
+    if (need > a->cap - a->off) return NULL;
+    void *p = a->base + a->off;
+    a->off += need;
+    return p;
+}
+
+void ml_arena_free(ml_arena *a) {
+    if (a->base) {
+        krh_sync();
+        uint8_t *d = dev_addr(a->base, 1);
+        drop_range(a->base);
+        krh_free(d);
+        krh_host_free(a->base);
+    }
+    a->base = NULL;
+    a->cap = a->off = 0;
+}
+
+/* ---- core/threads.c: one worker ---- */
+
+struct ml_pool { int n; };
+
+ml_status ml_pool_create(ml_pool **p, int n) {
+    (void)n;
+    *p = NULL;
+    if (!ready()) return ML_E_ISA;
+    for (int i = 0; i < g_nrg; i++)   /* the arenas, as the host has filled them */
+        if (!g_rg[i].uploaded) {
+            if (krh_copy_h2d(g_rg[i].d, g_rg[i].h, g_rg[i].n) != ML_OK) return ML_E_IO;
+            g_rg[i].uploaded = 1;
+        }
+    *p = malloc(sizeof **p);
+    if (!*p) return ML_E_NOMEM;
+    (*p)->n = 1;
+    return ML_OK;
+}
+
+void ml_pool_run(ml_pool *p, ml_task_fn fn, void *ctx) { (void)p; fn(ctx, 0, 1); }
+int ml_pool_size(const ml_pool *p) { (void)p; return 1; }
+int ml_pool_threads(int n) { (void)n; return 1; }
+void ml_pool_destroy(ml_pool *p) { free(p); }
+
+/* ---- model/pack_model.c: the model file to HBM, once ---- */
+
+ml_status ml_model_pack(ml_model *m, ml_pool *pool) {
+    (void)pool;
+    if (!ready()) return ML_E_ISA;
+    const uint8_t *h = m->file.data;
+    const size_t n = m->file.size;
+    uint8_t *d = dev_addr(h, n);
+    if (!d) {
+        d = krh_alloc(n);
+        if (!d) return ML_E_NOMEM;
+        if (krh_copy_h2d(d, h, n) != ML_OK || !add_range(h, n, d, 1)) {
+            krh_free(d);
+            return ML_E_IO;
+        }
+    } else if (krh_copy_h2d(d, h, n) != ML_OK) {   /* the same address may be a new file */
+        return ML_E_IO;
+    }
+    g_cls_q = m->wcls.q;
+    return ML_OK;
+}
+
+ml_status ml_model_pack_cached(ml_model *m, ml_pool *pool, const char *path, const char **how) {
+    (void)path;
+    *how = "none";
+    return ml_model_pack(m, pool);
+}
+
+int ml_pack_group(void) { return 0; }
+
+/* ---- core/quant_ref.c ---- */
+
+void ml_dequant_row(float *out, const ml_qtensor *W, int row) {
+    if (dev_addr(out, sizeof(float) * (size_t)W->cols) && ready()) {   /* the embedding of ml_forward */
+        kh_call c = { 0 };
+        krh_mat m;
+        mat_of(&c, W, row, row + 1, &m);
+        float *o = arg(&c, out, sizeof(float) * (size_t)W->cols, 0, 1);
+        if (!c.fail) {
+            krh_set_int(g_ints + 1, 0);
+            krh_embed(o, &m, g_ints + 1, 1.0f);
+        }
+        done(&c);
+        return;
+    }
+    /* a host buffer: the scalar rule (core/quant_ref.c:4-19) */
+    const int nb = W->cols / QK;
+    const float *d = W->d + (size_t)row * nb;
+    if (W->type == ML_Q8_0) {
+        const int8_t *q = W->q + (size_t)row * W->cols;
+        for (int i = 0; i < W->cols; i++) out[i] = q[i] * d[i / QK];
+        return;
+    }
+    const uint8_t *q = (const uint8_t *)W->q + (size_t)row * nb * (QK / 2);
+    for (int b = 0; b < nb; b++)
+        for (int j = 0; j < QK / 2; j++) {
+            const uint8_t v = q[b * (QK / 2) + j];
+            out[b * QK + j] = ((v & 0xF) - 8) * d[b];
+            out[b * QK + j + QK / 2] = ((v >> 4) - 8) * d[b];
+        }
+}
+
+/* host only (load-time and tools), the amax / 7 rule (core/quant_ref.c:21-38) */
+void ml_quantize_row_q4(int8_t *q, float *d, const float *x, int k) {
+    for (int b = 0; b < k / QK; b++) {
+        const float *xb = x + b * QK;
+        float amax = 0.0f;
+        for (int j = 0; j < QK; j++) amax = fmaxf(amax, fabsf(xb[j]));
+        if (amax < ML_QUANT_TINY) amax = 0.0f;
+        const float id = amax != 0.0f ? 7.0f / amax : 0.0f;
+        d[b] = amax / 7.0f;
+        uint8_t nib[QK];
+        for (int j = 0; j < QK; j++) {
+            float v = truncf(xb[j] * id + copysignf(0.5f, xb[j]));
+            v = fminf(fmaxf(v, -8.0f), 7.0f);
+            nib[j] = (uint8_t)((int)v + 8);
+        }
+        for (int j = 0; j < QK / 2; j++) q[b * (QK / 2) + j] = (int8_t)(nib[j] | (nib[j + QK / 2] << 4));
+    }
+}
+
+/* ---- kernels/hip ---- */
+
+#define F(n) (sizeof(float) * (size_t)(n))
+
+static void matvec_rows(float *y, const ml_qtensor *W, const ml_qact *x, int r0, int r1) {
+    if (r0 >= r1 || !ready()) return;
+    kh_call c = { 0 };
+    krh_mat m;
+    mat_of(&c, W, r0, r1, &m);
+    const int8_t *xq = arg(&c, x->q, (size_t)W->cols, 1, 0);
+    const float *xd = arg(&c, x->d, F(W->cols / QK), 1, 0);
+    float *yd = arg(&c, y + r0, F(r1 - r0), 0, 1);
+    if (!c.fail) krh_matvec(yd, &m, xq, xd, 0);
+    if (W->q == g_cls_q && !c.staged && yd && yd != (void *)(y + r0)) {
+        /* the logits: the host reads them next (app/ml_run.c:388-392) */
+        if (krh_copy_d2h(y + r0, yd, F(r1 - r0)) != ML_OK || krh_status() != ML_OK) {
+            fail_call(krh_last_error());
+            for (int r = r0; r < r1; r++) y[r] = NAN;
+        }
+    }
+    done(&c);
+    if (c.fail) fail_call("cannot stage a buffer");
+}
+
+void ml_k_matvec_q8_hip(float *y, const ml_qtensor *W, const ml_qact *x, int r0, int r1) { matvec_rows(y, W, x, r0, r1); }
+void ml_k_matvec_q4_hip(float *y, const ml_qtensor *W, const ml_qact *x, int r0, int r1) { matvec_rows(y, W, x, r0, r1); }
+
+void ml_k_quantize_q8_hip(ml_qact *out, const float *x, int k) {
+    if (!ready()) return;
+    kh_call c = { 0 };
+    const float *xd = arg(&c, x, F(k), 1, 0);
+    int8_t *q = arg(&c, out->q, (size_t)k, 0, 1);
+    float *d = arg(&c, out->d, F(k / QK), 0, 1);
+    if (!c.fail) krh_quantize_q8(q, d, xd, k, 1);
+    done(&c);
+}
+
+void ml_k_rmsnorm_hip(float *o, const float *x, const float *w, int n, float eps) {
+    if (!ready()) return;
+    kh_call c = { 0 };
+    const float *xd = arg(&c, x, F(n), 1, 0), *wd = arg(&c, w, F(n), 1, 0);
+    float *od = arg(&c, o, F(n), 0, 1);
+    if (!c.fail) krh_rmsnorm(od, xd, wd, n, eps);
+    done(&c);
+}
+
+void ml_k_softmax_hip(float *x, int n) {
+    if (!ready()) return;
+    kh_call c = { 0 };
+    float *xd = arg(&c, x, F(n), 1, 1);
+    if (!c.fail) krh_softmax(xd, n);
+    done(&c);
+}
+
+void ml_k_rope_hip(float *q, float *k, const float *cos_t, const float *sin_t, int head_dim, int n_heads,
+                   int n_kv_heads) {
+    if (!ready()) return;
+    kh_call c = { 0 };
+    float *qd = arg(&c, q, F(n_heads * head_dim), 1, 1), *kd = arg(&c, k, F(n_kv_heads * head_dim), 1, 1);
+    const float *cd = arg(&c, cos_t, F(head_dim / 2), 1, 0), *sd = arg(&c, sin_t, F(head_dim / 2), 1, 0);
+    if (!c.fail) krh_rope(qd, kd, cd, sd, head_dim, n_heads, n_kv_heads);
+    done(&c);
+}
+
+static void pair_op(void (*op)(float *, const float *, int), float *g, const float *u, int n) {
+    if (!ready()) return;
+    kh_call c = { 0 };
+    float *gd = arg(&c, g, F(n), 1, 1);
+    const float *ud = arg(&c, u, F(n), 1, 0);
+    if (!c.fail) op(gd, ud, n);
+    done(&c);
+}
+
+void ml_k_silu_mul_hip(float *g, const float *u, int n) { pair_op(krh_silu_mul, g, u, n); }
+void ml_k_gelu_mul_hip(float *g, const float *u, int n) { pair_op(krh_gelu_mul, g, u, n); }
+void ml_k_add_hip(float *y, const float *x, int n) { pair_op(krh_add, y, x, n); }
+
+void ml_k_dot_f32_hip(float *s, const float *q, const float *k, size_t ldk, int rows, int n, float scale) {
+    if (rows <= 0 || !ready()) return;
+    kh_call c = { 0 };
+    float *sd = arg(&c, s, F(rows), 0, 1);
+    const float *qd = arg(&c, q, F(n), 1, 0), *kd = arg(&c, k, F((size_t)(rows - 1) * ldk + n), 1, 0);
+    if (!c.fail) krh_dot_rows(sd, qd, kd, ldk, rows, n, scale);
+    done(&c);
+}
+
+void ml_k_axpy_f32_hip(float *y, const float *a, const float *x, size_t ldx, int rows, int n) {
+    if (rows <= 0 || !ready()) return;
+    kh_call c = { 0 };
+    float *yd = arg(&c, y, F(n), 1, 1);
+    const float *ad = arg(&c, a, F(rows), 1, 0), *xd = arg(&c, x, F((size_t)(rows - 1) * ldx + n), 1, 0);
+    if (!c.fail) krh_axpy_rows(yd, ad, xd, ldx, rows, n);
+    done(&c);
+}
+
+/* ---- ops/ops.c ---- */
+
+void ml_matvec(ml_pool *pool, float *y, const ml_qtensor *W, const ml_qact *x) {
+    (void)pool;
+    matvec_rows(y, W, x, 0, W->rows);
+}
+
+/* Y[t * ldy + r] = W x_t (ops/ops.c:51-79): the MFMA matmul over the batch,
+ * each token's row the matvec's bit for bit */
+void ml_matmul(ml_pool *pool, float *Y, int ldy, const ml_qtensor *W, const ml_qbatch *X) {
+    (void)pool;
+    const int n = X->n, k = X->k, nb = k / QK, ldx = (n + 127) / 128 * 128;
+    if (n <= 0 || !ready()) return;
+    g_dT = grow(g_dT, &g_dT_n, F((size_t)nb * ldx));
+    kh_call c = { 0 };
+    krh_mat m;
+    mat_of(&c, W, 0, W->rows, &m);
+    /* the activations must be readable for ldx rows: arena batches hold
+     * ML_BATCH_MAX rows; anything shorter is staged padded */
+    const int8_t *xq = (const int8_t *)dev_addr(X->q, (size_t)ldx * k);
+    if (!xq) {
+        int8_t *pad = krh_alloc((size_t)ldx * k);
+        const int8_t *src = arg(&c, X->q, (size_t)n * k, 1, 0);
+        if (pad && src) krh_copy_d2d_async(pad, src, (size_t)n * k);
+        if (pad && c.nst < 16) c.st[c.nst++] = (kh_buf){ NULL, (uint8_t *)pad, 0, 0 };
+        else c.fail = 1;
+        xq = pad;
+    }
+    const float *xd = arg(&c, X->d, F((size_t)n * nb), 1, 0);
+    /* in and out: rows of Y are ldy apart and the gaps are the caller's */
+    float *yd = arg(&c, Y, F((size_t)(n - 1) * ldy + W->rows), 1, 1);
+    if (!c.fail && g_dT) {
+        krh_transpose_scales(g_dT, ldx, xd, n, nb);
+        krh_matmul(yd, ldy, &m, xq, g_dT, ldx, n, 0);
+    }
+    done(&c);
+    if (c.fail || !g_dT) fail_call("cannot stage a buffer");
+}
+
+void ml_quantize_row(int8_t *q, float *d, const float *x, int n) {
+    if (!ready()) return;
+    kh_call c = { 0 };
+    const float *xd = arg(&c, x, F(n), 1, 0);
+    int8_t *qd = arg(&c, q, (size_t)n, 0, 1);
+    float *dd = arg(&c, d, F(1), 0, 1);
+    if (!c.fail) krh_quantize_row(qd, dd, xd, n);
+    done(&c);
+}
+
+void ml_softcap_rows(float *x, size_t ld, int rows, int n, float cap) {
+    if (rows <= 0 || !ready()) return;
+    kh_call c = { 0 };
+    const size_t bytes = F((size_t)(rows - 1) * ld + n);
+    float *xd = arg(&c, x, bytes, 1, 1);
+    if (!c.fail) krh_softcap_rows(xd, ld, rows, n, cap);
+    /* soft-capped logits in the arena are read on the host next */
+    if (!c.staged && xd && xd != x) krh_copy_d2h(x, xd, bytes);
+    done(&c);
+}
+
+int ml_attention_batch_heads(const ml_config *cfg, int nthreads) {
+    (void)nthreads;
+    return cfg->n_heads / cfg->n_kv_heads;
+}
+
+static int attn_supported(const ml_kv_layer *kv, const ml_config *cfg) {
+    if (!kv->k || !kv->v) {
+        fail_call("the F16 and Q8 KV caches are not built (use --kv f32)");
+        return 0;
+    }
+    if (cfg->attn_softcap > 0.0f) {
+        fail_call("attention soft-capping is not built");
+        return 0;
+    }
+    return ready();
+}
+
+void ml_attention(ml_pool *pool, float *out, const float *q, const ml_kv_layer *kv, float *att_scratch, int8_t *qq,
+                  float *qd, const ml_config *cfg, int pos) {
+    (void)pool; (void)qq; (void)qd;
+    if (!attn_supported(kv, cfg)) return;
+    const size_t cache = F((size_t)cfg->max_seq * cfg->kv_dim);
+    kh_call c = { 0 };
+    float *o = arg(&c, out, F(cfg->q_dim), 0, 1);
+    const float *qv = arg(&c, q, F(cfg->q_dim), 1, 0);
+    float *att = arg(&c, att_scratch, F((size_t)cfg->n_heads * cfg->max_seq), 0, 0);
+    const float *kc = arg(&c, kv->k, cache, 1, 0), *vc = arg(&c, kv->v, cache, 1, 0);
+    if (!c.fail) {
+        krh_set_int(g_ints, pos);
+        krh_attention(o, NULL, NULL, att, qv, kc, vc, cfg->n_heads, cfg->n_kv_heads, cfg->head_dim, cfg->max_seq,
+                      kv->window, cfg->attn_scale, g_ints);
+    }
+    done(&c);
+}
+
+void ml_attention_batch(ml_pool *pool, float *out, const float *q, const ml_kv_layer *kv, float *att_scratch,
+                        int8_t *qq, float *qd, const ml_config *cfg, int pos0, int n) {
+    (void)pool; (void)qq; (void)qd; (void)att_scratch;
+    if (n <= 0 || !attn_supported(kv, cfg)) return;
+    const size_t cache = F((size_t)cfg->max_seq * cfg->kv_dim);
+    g_batt = grow(g_batt, &g_batt_n, F((size_t)n * cfg->n_heads * cfg->max_seq));
+    kh_call c = { 0 };
+    float *o = arg(&c, out, F((size_t)n * cfg->q_dim), 0, 1);
+    const float *qv = arg(&c, q, F((size_t)n * cfg->q_dim), 1, 0);
+    const float *kc = arg(&c, kv->k, cache, 1, 0), *vc = arg(&c, kv->v, cache, 1, 0);
+    if (!c.fail && g_batt) {
+        krh_set_int(g_ints, pos0);
+        krh_attention_batch(o, g_batt, qv, kc, vc, cfg->n_heads, cfg->n_kv_heads, cfg->head_dim, cfg->max_seq,
+                            kv->window, cfg->attn_scale, g_ints, n, pos0 + n - 1);
+    }
+    done(&c);
+}

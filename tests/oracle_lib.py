@@ -135,12 +135,13 @@ class OracleModel:
         oracle.kro_model_close(self.m)
 
 
-def ref_ml_run(model, tokens, steps, threads=1, dump=None, isa="scalar", timeout=600):
-    """the reference's own ml_run (built from its sources into oracle/_ref):
-    greedy ids it prints, or the logits it dumps; with its stderr"""
+def ref_ml_run(model, tokens, steps, threads=1, dump=None, isa="scalar", timeout=600, extra=()):
+    """the reference's own ml_run (built from its sources into oracle/_ref;
+    isa "hip": over this repository's op-table binding): greedy ids it
+    prints, or the logits it dumps; with its stderr"""
     exe = os.path.join(REF_DIR, isa, "ml_run")
     cmd = [exe, model, "--tokens", ",".join(str(int(t)) for t in tokens), "-n", str(steps), "-T", "0",
-           "-t", str(threads)]
+           "-t", str(threads)] + list(extra)
     if dump:
         cmd += ["--dump-logits", dump]
     r = subprocess.run(cmd, capture_output=True, text=True, timeout=timeout)

@@ -1,0 +1,67 @@
+"""The drop-in check of the ISA=hip op-table binding: the reference's own
+app/ml_run.c and model/transformer.c, unchanged, built over
+isa-lm_amd/optable and libkrafla_hip.so (oracle/Makefile `hip`), against the
+reference's scalar build on the same .mlb files and token ids: the same
+printed ids and the same --dump-logits bytes. Needs a gfx950 device."""
+import os
+
+import numpy as np
+import pytest
+
+import krafla as K
+import oracle_lib as O
+
+pytestmark = [pytest.mark.gpu,
+              pytest.mark.skipif(not os.path.exists(os.path.join(O.REF_DIR, "hip", "ml_run")),
+                                 reason="oracle/_ref/hip not built (needs the reference sources at build time)")]
+
+MODELS = {
+    "c1_q8": dict(K.CONFIGS["stories15m_q8"]),
+    "qwen_like_q4mix": dict(K.CONFIGS["qwen05b_mixed"], dim=128, n_layers=3, n_heads=4, n_kv_heads=2,
+                            hidden_dim=256, vocab=512, max_seq=160, std=0.1),
+    "llama3_rope_gqa_q4": dict(K.CONFIGS["llama1b_mixed"], dim=256, n_layers=2, n_heads=8, n_kv_heads=2,
+                               hidden_dim=512, vocab=1000, max_seq=200, std=0.1, rope_orig_max_seq=64),
+    "q8_f16_untied": dict(K.CONFIGS["llama8b_q8"], dim=256, n_layers=2, n_heads=4, n_kv_heads=1, hidden_dim=384,
+                          vocab=700, max_seq=160, std=0.1),
+}
+
+
+def model(name, workdir):
+    path = os.path.join(workdir, "ot_" + name + ".mlb")
+    if not os.path.exists(path):
+        K.gen_mlb(path, **MODELS[name])
+    return path
+
+
+@pytest.mark.parametrize("name", sorted(MODELS))
+def test_ml_run_greedy_ids(name, workdir):
+    path = model(name, workdir)
+    V = MODELS[name]["vocab"]
+    prompt = [int(t) for t in np.random.default_rng(3).integers(1, V, 8)]
+    steps = min(MODELS[name]["max_seq"], 8 + 128)
+    want, _ = O.ref_ml_run(path, prompt, steps)
+    got, err = O.ref_ml_run(path, prompt, steps, isa="hip")
+    assert "isa: hip" in err
+    assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("batch", [None, 1])
+@pytest.mark.parametrize("name", sorted(MODELS))
+def test_ml_run_dump_logits(name, batch, workdir):
+    path = model(name, workdir)
+    V = MODELS[name]["vocab"]
+    toks = [int(t) for t in np.random.default_rng(4).integers(1, V, 20)]
+    a, b = path + ".scalar.logits", path + ".hip.logits"
+    O.ref_ml_run(path, toks, len(toks), dump=a)
+    O.ref_ml_run(path, toks, len(toks), dump=b, isa="hip", extra=["--batch", str(batch)] if batch else [])
+    x, y = np.fromfile(a, dtype=np.uint8), np.fromfile(b, dtype=np.uint8)
+    assert x.size == len(toks) * V * 4 and np.array_equal(x, y)
+
+
+def test_ml_bench_kernel_table():
+    """ml_bench (no model) runs its kernel table on the hip kernels, staged
+    from host buffers"""
+    import subprocess
+    r = subprocess.run([os.path.join(O.REF_DIR, "hip", "ml_bench")], capture_output=True, text=True, timeout=600)
+    assert r.returncode == 0, r.stderr
+    assert "ISA: hip" in r.stdout and "matvec_q8 -> ml_k_matvec_q8_hip" in r.stdout

@@ -299,3 +299,18 @@ def test_forward_matches_reference(name, workdir):
     ids_ref, _ = O.ref_ml_run(path, toks[:5], steps)
     assert np.array_equal(om.generate(toks[:5], steps), ids_ref)
     om.close()
+
+
+def test_hip_ml_run_guard_without_gpu(workdir):
+    """the ISA=hip build keeps the reference's guard contract
+    (app/main_guard.c:8-15): without a gfx950 device it exits 3"""
+    exe = os.path.join(O.REF_DIR, "hip", "ml_run")
+    if not os.path.exists(exe):
+        pytest.skip("oracle/_ref/hip not built")
+    if K.hip.krh_init() == K.ML_OK:
+        pytest.skip("a gfx950 device is present")
+    import subprocess
+    path = os.path.join(workdir, "guard.mlb")
+    K.gen_mlb(path, **dict(K.CONFIGS["stories15m_q8"], n_layers=1, vocab=64, max_seq=16))
+    r = subprocess.run([exe, path, "--tokens", "1,2", "-n", "3"], capture_output=True, text=True, timeout=60)
+    assert r.returncode == 3 and "ISA=hip" in r.stderr
