@@ -81,8 +81,9 @@ def mat_bytes(W):
 
 
 def time_swiglu(K, model, state, reps):
-    """average duration (ms) of the fused w1/w3 matvec over all layers, and
-    its algorithmic bytes per launch"""
+    """average duration (ms) of the decode step's SwiGLU launch -- w1|w3
+    matvec on the normalized, quantized input, SiLU(w1 x) * (w3 x) -- over
+    all layers, and its algorithmic bytes per launch"""
     cfg = model.cfg
     xq = K.host.kr_state_buffer(state.ptr, b"qa_dim")
     xd = K.host.kr_state_buffer(state.ptr, b"qd_dim")
@@ -276,7 +277,7 @@ def main():
         "prefill_tok_s": round(prefill_tok_s, 2) if prefill_tok_s else None,
         "decode_frac_of_hbm_roofline": round(tok_s * (per_tok + kv_tok) / (HBM_PEAK_GBS * 1e9), 4),
         "deterministic_ids": deterministic,
-        "roofline": {"bound": "hbm", "kernel": "k_matvec<EPI_SWIGLU> (w1|w3 rows + SiLU(w1 x) * (w3 x))",
+        "roofline": {"bound": "hbm", "kernel": "k_matvec<EPI_SWIGLU> (w1|w3 rows, SiLU(w1 x) * (w3 x))",
                      "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
                      "bytes_per_launch": nbytes, "avg_launch_us": round(ms * 1e3, 2)},

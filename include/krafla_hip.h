@@ -93,6 +93,10 @@ void krh_matvec(float *y, const krh_mat *W, const int8_t *xq, const float *xd, i
 /* the same with a float input x[W->cols], quantized to Q8_0 first
  * (k_scalar.c:39-57) inside the launch */
 void krh_matvec_f(float *y, const krh_mat *W, const float *x, int accumulate);
+/* the same with x normalized first: y (+)= W q8(rmsnorm(x) * nw)
+ * (model/transformer.c:299-303, k_scalar.c:59-64) -- every workgroup runs the
+ * norm's ordered sum itself while its weight loads are in flight */
+void krh_rmsnorm_matvec(float *y, const krh_mat *W, const float *x, const float *nw, float eps, int accumulate);
 
 /* The attention projections of one layer at position *pos
  * (model/transformer.c:270-281): q = wq x, k = wk x, v = wv x, plus the
@@ -104,6 +108,15 @@ void krh_matvec_qkv(float *q, float *kc, float *vc, const krh_mat *wq, const krh
 
 /* h = silu(w1 x) * (w3 x) (k_scalar.c:96-98; model/transformer.c:291-293) */
 void krh_matvec_swiglu(float *h, const krh_mat *w1, const krh_mat *w3, const int8_t *xq, const float *xd);
+
+/* krh_matvec_qkv and krh_matvec_swiglu with their input normalized first
+ * (the attention and FFN norms, model/transformer.c:270-271, :288-289): x is
+ * the residual stream, nw the norm weight */
+void krh_rmsnorm_matvec_qkv(float *q, float *kc, float *vc, const krh_mat *wq, const krh_mat *wk, const krh_mat *wv,
+                            const float *bq, const float *bk, const float *bv, const float *x, const float *nw,
+                            float eps, const float *rope_cos, const float *rope_sin, int head_dim, const int *pos);
+void krh_rmsnorm_matvec_swiglu(float *h, const krh_mat *w1, const krh_mat *w3, const float *x, const float *nw,
+                               float eps);
 
 /* Causal GQA attention of one position *pos over this layer's F32 cache
  * (ops/ops.c:169-225): ao [n_heads * head_dim]; aq, ad (nullable) receive its

@@ -10,6 +10,8 @@
 // adds the terms in block order, which is the reference's float order
 // (kernels/scalar/k_scalar.c:13, :34). Fused epilogues: plain store,
 // residual add, QKV bias + RoPE + KV-cache write, SwiGLU + Q8_0 quantize.
+#include <type_traits>
+
 #include "kr_internal.h"
 #include "kr_numerics.h"
 
@@ -32,10 +34,13 @@ struct MvArgs {
     KMat m[3];
     int tile0[4];        // first workgroup of matrix i; tile0[nmat] = grid size
     int nmat;
-    int R;               // output rows per workgroup
-    const int8_t *xq;    // Q8_0 activation, or NULL: quantize xf in the prologue
-    const float *xd;
+    int R;               // output rows per tile
+    int nbc;             // blocks per chunk (set by launch_mv)
+    const int8_t *xq;    // Q8_0 activation; or NULL: quantize xf in the prologue,
+    const float *xd;     // after rmsnorm with weight nw when nw is set
     const float *xf;
+    const float *nw;
+    float eps;
     int K;
     float *y[3];
     const float *bias[3];
@@ -45,7 +50,10 @@ struct MvArgs {
 };
 
 constexpr int MV_THREADS = 256;
-constexpr int MV_NPT = 16;   // weight blocks per thread, all loaded up front
+constexpr int MV_NPT = 4;   // weight blocks per thread per work item
+constexpr int MV_DEPTH = 2;    // work items in flight per workgroup (the one in use included): a wave that
+                               // issues more loads than the memory pipeline holds stalls at issue
+constexpr int MV_XQ_MAX = 16384;   // activations up to this length are staged from registers
 
 template <typename T> __device__ __forceinline__ T pick3(int i, T a, T b, T c) { return i == 0 ? a : (i == 1 ? b : c); }
 
@@ -76,23 +84,51 @@ __device__ __forceinline__ int block_dot(const int4 w0, const int4 w1, const int
     return s;
 }
 
+// 0 + v[0] + v[1] + ... + v[n-1] in index order (one lane), n % 32 == 0, v in
+// LDS: reads are batched 8 float4 at a time so the adds do not wait on each.
+__device__ __forceinline__ float kr_chain_lds(const float *v, int n) {
+    const float4 *p = (const float4 *)v;
+    float s = 0.0f;
+    for (int i = 0; i < n / 4; i += 8) {
+        float4 r[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++) r[k] = p[i + k];
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            s = kr_fadd(s, r[k].x);
+            s = kr_fadd(s, r[k].y);
+            s = kr_fadd(s, r[k].z);
+            s = kr_fadd(s, r[k].w);
+        }
+    }
+    return s;
+}
+
 // Q8_0 of K floats into LDS (k_scalar.c:39-57): each thread takes 4
 // consecutive values, 8 threads a 32-block; the block max is exact in any
 // order. K % 32 == 0, x 16-byte aligned.
-__device__ __forceinline__ void quantize_to_lds(const float *x, int K, int8_t *xs, float *xds) {
+// With w: the rmsnorm output (x * inv) * w (k_scalar.c:63) is quantized.
+__device__ __forceinline__ void quantize_to_lds(const float *x, int K, int8_t *xs, float *xds,
+                                                const float *w = nullptr, float inv = 1.0f) {
     constexpr int B = 4;   // float4 loads in flight per thread
     for (int base = 0; base < K; base += 4 * B * MV_THREADS) {
-        float4 vs[B];
+        float4 vs[B], ws[B];
 #pragma unroll
         for (int k = 0; k < B; k++) {
             const int i = base + 4 * (k * MV_THREADS + threadIdx.x);
-            if (i < K) vs[k] = *(const float4 *)(x + i);
+            if (i < K) {
+                vs[k] = *(const float4 *)(x + i);
+                if (w) ws[k] = *(const float4 *)(w + i);
+            }
         }
 #pragma unroll
         for (int k = 0; k < B; k++) {
         const int i = base + 4 * (k * MV_THREADS + threadIdx.x);   // K % 32 == 0: 8-lane groups all in or all out
         if (i < K) {
-            const float4 v = vs[k];
+            float4 v = vs[k];
+            if (w)
+                v = make_float4(kr_fmul(kr_fmul(v.x, inv), ws[k].x), kr_fmul(kr_fmul(v.y, inv), ws[k].y),
+                                kr_fmul(kr_fmul(v.z, inv), ws[k].z), kr_fmul(kr_fmul(v.w, inv), ws[k].w));
             float m = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
             m = fmaxf(m, __shfl_xor(m, 1, 8));
             m = fmaxf(m, __shfl_xor(m, 2, 8));
@@ -112,162 +148,292 @@ __device__ __forceinline__ void quantize_to_lds(const float *x, int K, int8_t *x
     }
 }
 
-// y rows [row0, row0 + R) of up to three matrices sharing the activation
-// (QKV), or the w1 and w3 rows [row0, row0 + R) (SwiGLU). Phase 1: every
-// thread issues the loads of its MV_NPT weight blocks (consecutive threads on
-// consecutive blocks: each wave reads one contiguous span), then the
-// activation is staged (or quantized) into LDS while they are in flight, then
-// the exact int32 block dots and their terms ((float)s * wd) * xd go to LDS.
-// Phase 2: one lane per row adds its terms in block order
-// (kernels/scalar/k_scalar.c:13, :34). Then the epilogue.
-template <int EPI, int QT, int D16>
-__global__ void __launch_bounds__(MV_THREADS) k_matvec(const MvArgs a) {
-    extern __shared__ __align__(16) unsigned char smem[];
-    const int K = a.K, nb = K / KR_QK, tid = threadIdx.x, R = a.R;
-    int mi = 0;
+// Loads of one work item (row tile, block chunk): slot k of thread tid is
+// local block tid + k * MV_THREADS of the item, blocks fastest, so each wave
+// reads contiguous spans (a Q8_0 block as two 16-byte loads, a Q4_0 block as
+// one). Every slot loads (slots past the item re-read its first block and are
+// not used), so no load waits on a branch.
+struct MvSlots {
+    int4 w0[MV_NPT], w1[MV_NPT];
+    uint32_t wd[MV_NPT];   // raw scale bits: widened at use, after every load is in flight
+};
+
+// Where a work item lies: matrix mi, first row, rows, local rows (SwiGLU's w3
+// rows follow its w1 rows), first block and block count of the chunk.
+struct MvItem {
+    int mi, row0, nr, nloc, c0, nbc;
+};
+
+template <int EPI>
+__device__ __forceinline__ MvItem mv_item(const MvArgs &a, int tile, int chunk, int nb) {
+    MvItem it;
+    it.mi = 0;
     if (EPI != EPI_SWIGLU)
-        while (mi + 1 < a.nmat && (int)blockIdx.x >= a.tile0[mi + 1]) mi++;
-    const KMat W = pick3(mi, a.m[0], a.m[1], a.m[2]);
+        while (it.mi + 1 < a.nmat && tile >= a.tile0[it.mi + 1]) it.mi++;
+    const int rows = pick3(it.mi, a.m[0].rows, a.m[1].rows, a.m[2].rows);
+    it.row0 = (tile - a.tile0[it.mi]) * a.R;
+    it.nr = min(a.R, rows - it.row0);
+    it.nloc = EPI == EPI_SWIGLU ? 2 * it.nr : it.nr;
+    it.c0 = chunk * a.nbc;
+    it.nbc = min(a.nbc, nb - it.c0);
+    return it;
+}
+
+template <int EPI, int QT, int D16>
+__device__ __forceinline__ void mv_load(MvSlots &S, const MvArgs &a, const MvItem &it, int nb) {
+    const KMat W = pick3(it.mi, a.m[0], a.m[1], a.m[2]);
     const KMat W2 = a.m[1];
-    const int row0 = ((int)blockIdx.x - a.tile0[mi]) * R;
-    const int nr = min(R, W.rows - row0);
-    const int nloc = EPI == EPI_SWIGLU ? 2 * nr : nr;   // local rows: SwiGLU's w3 rows follow its w1 rows
-    const int stride = nb | 1;   // odd: the chain lanes read distinct banks
+    const int tid = threadIdx.x, n = it.nloc * it.nbc;
+    int lr = tid / it.nbc, b = tid - lr * it.nbc;
+    const int sr = MV_THREADS / it.nbc, sb = MV_THREADS - sr * it.nbc;
+#pragma unroll
+    for (int k = 0; k < MV_NPT; k++) {
+        const bool in = tid + k * MV_THREADS < n;
+        const bool second = EPI == EPI_SWIGLU && in && lr >= it.nr;
+        const uint8_t *q = second ? W2.q : W.q;
+        const void *d = second ? W2.d : W.d;
+        const size_t blk = in ? (size_t)(it.row0 + (second ? lr - it.nr : lr)) * nb + it.c0 + b
+                              : (size_t)it.row0 * nb + it.c0;
+        if (QT == ML_Q8_0) {
+            const int4 *p = (const int4 *)(q + blk * 32);
+            S.w0[k] = p[0];
+            S.w1[k] = p[1];
+        } else {
+            S.w0[k] = *(const int4 *)(q + blk * 16);
+            S.w1[k] = make_int4(0, 0, 0, 0);
+        }
+        S.wd[k] = D16 ? (uint32_t)((const uint16_t *)d)[blk] : ((const uint32_t *)d)[blk];
+        b += sb;
+        lr += sr;
+        if (b >= it.nbc) { b -= it.nbc; lr++; }
+    }
+}
+
+// y rows [row0, row0 + R) of up to three matrices sharing the activation
+// (QKV), or the w1 and w3 rows [row0, row0 + R) (SwiGLU). A workgroup walks
+// work items (its row tiles blockIdx.x, + gridDim.x, ..., each split into
+// chunks of nbc blocks), and issues the loads of item i + 1 before it uses
+// item i's: the weight stream never stops for the dots or the ordered sums.
+// Per item: the exact int32 block dots and their terms ((float)s * wd) * xd
+// go to one half of a double LDS buffer; after a barrier, one lane per row
+// continues its row's ordered sum over the chunk's terms, in block order
+// (kernels/scalar/k_scalar.c:13, :34), while the other waves go on to the
+// next item's dots. On a tile's last chunk the sums go through the epilogue.
+// Before the first item's dots the activation is staged into LDS (while the
+// first loads are in flight): copied, quantized, or normalized first
+// (rmsnorm's ordered sum by one lane, k_scalar.c:59-64) and quantized.
+template <int EPI, int QT, int D16>
+__global__ void __launch_bounds__(MV_THREADS, 2) k_matvec(const MvArgs a) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    const int K = a.K, nb = K / KR_QK, tid = threadIdx.x, ntiles = a.tile0[a.nmat];
+    const int maxloc = EPI == EPI_SWIGLU ? 2 * a.R : a.R;
+    const int ts = a.nbc + 4;   // term row stride: 16-byte rows, 4-bank shift between rows
     int8_t *xs = (int8_t *)smem;
     float *xds = (float *)(smem + K);
-    float *t2 = xds + nb;
-    float *sums = t2 + (EPI == EPI_SWIGLU ? 2 * R : R) * stride;
-    const int nblk = nloc * nb;
+    float *t2 = xds + nb;                    // [2][maxloc][ts]
+    float *sums = t2 + 2 * maxloc * ts;      // [maxloc]
+    float *sq = sums + maxloc;               // K floats, rmsnorm prologue only
+    __shared__ float s_inv;
+    if ((int)blockIdx.x >= ntiles) return;
+    const int nch = (nb + a.nbc - 1) / a.nbc;
 
-    int4 w0[MV_NPT], w1[MV_NPT];
-    uint32_t wd[MV_NPT];   // raw scale bits: widened after every load is in flight
-    {
-        int lr = tid / nb, b = tid - (tid / nb) * nb;
-        const int sr = MV_THREADS / nb, sb = MV_THREADS - sr * nb;
-        // every slot loads (slots past the workgroup's blocks re-read its
-        // first block and are not used), so no load waits on a branch
+    // items are loaded MV_DEPTH - 1 ahead of the one whose dots run: S[P]
+    // holds item P of every MV_DEPTH; (ltile, lchunk) is the next item to load
+    int tile = blockIdx.x, chunk = 0, ltile = blockIdx.x, lchunk = 0;
+    auto next_item = [&](int &t, int &c) {
+        if (++c == nch) { c = 0; t += gridDim.x; }
+    };
+    auto load_item = [&](MvSlots &dst, MvItem &it) {
+        // past the last item: reload the last tile's chunk (not used)
+        it = mv_item<EPI>(a, min(ltile, ntiles - 1), ltile < ntiles ? lchunk : 0, nb);
+        mv_load<EPI, QT, D16>(dst, a, it, nb);
+        next_item(ltile, lchunk);
+    };
+    MvSlots S[MV_DEPTH];
+    MvItem I[MV_DEPTH];
+    if (a.xq && K <= MV_XQ_MAX) {
+        // a quantized activation: its loads go out before the weight loads,
+        // so storing it to LDS waits on it alone
+        int4 xv[MV_XQ_MAX / 16 / MV_THREADS];
+        float xdv[MV_XQ_MAX / 32 / MV_THREADS];
 #pragma unroll
-        for (int k = 0; k < MV_NPT; k++) {
-            const bool in = tid + k * MV_THREADS < nblk;
-            const bool second = EPI == EPI_SWIGLU && in && lr >= nr;
-            const uint8_t *q = second ? W2.q : W.q;
-            const void *d = second ? W2.d : W.d;
-            const size_t blk = in ? (size_t)(row0 + (second ? lr - nr : lr)) * nb + b : (size_t)row0 * nb;
-            if (QT == ML_Q8_0) {
-                const int4 *p = (const int4 *)(q + blk * 32);
-                w0[k] = p[0];
-                w1[k] = p[1];
-            } else {
-                w0[k] = *(const int4 *)(q + blk * 16);
-                w1[k] = make_int4(0, 0, 0, 0);
-            }
-            wd[k] = D16 ? (uint32_t)((const uint16_t *)d)[blk] : ((const uint32_t *)d)[blk];
-            b += sb;
-            lr += sr;
-            if (b >= nb) { b -= nb; lr++; }
-        }
+        for (int k = 0; k < MV_XQ_MAX / 16 / MV_THREADS; k++)
+            xv[k] = ((const int4 *)a.xq)[min(tid + k * MV_THREADS, K / 16 - 1)];
+#pragma unroll
+        for (int k = 0; k < MV_XQ_MAX / 32 / MV_THREADS; k++) xdv[k] = a.xd[min(tid + k * MV_THREADS, nb - 1)];
+#pragma unroll
+        for (int d = 0; d < MV_DEPTH - 1; d++) load_item(S[d], I[d]);
+#pragma unroll
+        for (int k = 0; k < MV_XQ_MAX / 16 / MV_THREADS; k++)
+            if (tid + k * MV_THREADS < K / 16) ((int4 *)xs)[tid + k * MV_THREADS] = xv[k];
+#pragma unroll
+        for (int k = 0; k < MV_XQ_MAX / 32 / MV_THREADS; k++)
+            if (tid + k * MV_THREADS < nb) xds[tid + k * MV_THREADS] = xdv[k];
+    } else {
+#pragma unroll
+        for (int d = 0; d < MV_DEPTH - 1; d++) load_item(S[d], I[d]);
     }
+
     if (a.xq) {
-        for (int i = tid; i < K / 16; i += MV_THREADS) ((int4 *)xs)[i] = ((const int4 *)a.xq)[i];
-        for (int i = tid; i < nb; i += MV_THREADS) xds[i] = a.xd[i];
+        if (K > MV_XQ_MAX) {
+            for (int i = tid; i < K / 16; i += MV_THREADS) ((int4 *)xs)[i] = ((const int4 *)a.xq)[i];
+            for (int i = tid; i < nb; i += MV_THREADS) xds[i] = a.xd[i];
+        }
+    } else if (a.nw) {
+        for (int i = 4 * tid; i < K; i += 4 * MV_THREADS) {
+            const float4 v = *(const float4 *)(a.xf + i);
+            *(float4 *)(sq + i) = make_float4(kr_fmul(v.x, v.x), kr_fmul(v.y, v.y), kr_fmul(v.z, v.z),
+                                              kr_fmul(v.w, v.w));
+        }
+        __syncthreads();
+        if (tid == 0) s_inv = kr_fdiv(1.0f, kr_fsqrt(kr_fadd(kr_fdiv(kr_chain_lds(sq, K), (float)K), a.eps)));
+        __syncthreads();
+        quantize_to_lds(a.xf, K, xs, xds, a.nw, s_inv);
     } else {
         quantize_to_lds(a.xf, K, xs, xds);
     }
     __syncthreads();
-    {
-        int lr = tid / nb, b = tid - (tid / nb) * nb;
-        const int sr = MV_THREADS / nb, sb = MV_THREADS - sr * nb;
+
+    float acc = 0.0f;   // row sum of lane tid < nloc of wave 0
+    // one item: S[P] holds it; S[P ^ 1] receives the next one's loads
+    auto step = [&](auto P_) -> bool {
+        constexpr int P = decltype(P_)::value;
+        load_item(S[(P + MV_DEPTH - 1) % MV_DEPTH], I[(P + MV_DEPTH - 1) % MV_DEPTH]);
+        const MvItem cur = I[P];
+        int ntile = tile, nchunk = chunk;
+        next_item(ntile, nchunk);
+
+        float *T = t2 + (P & 1) * maxloc * ts;
+        {
+            int lr = tid / cur.nbc, b = tid - lr * cur.nbc;
+            const int sr = MV_THREADS / cur.nbc, sb = MV_THREADS - sr * cur.nbc;
+            const int n = cur.nloc * cur.nbc;
 #pragma unroll
-        for (int k = 0; k < MV_NPT; k++) {
-            if (tid + k * MV_THREADS < nblk) {
-                const int s = block_dot<QT>(w0[k], w1[k], xs + b * 32);
-                const float sc = D16 ? kr_h2f((uint16_t)wd[k]) : __uint_as_float(wd[k]);
-                t2[lr * stride + b] = kr_fmul(kr_fmul((float)s, sc), xds[b]);
+            for (int k = 0; k < MV_NPT; k++) {
+                if (tid + k * MV_THREADS < n) {
+                    const int bb = cur.c0 + b;
+                    const int sdot = block_dot<QT>(S[P].w0[k], S[P].w1[k], xs + bb * 32);
+                    const float sc = D16 ? kr_h2f((uint16_t)S[P].wd[k]) : __uint_as_float(S[P].wd[k]);
+                    T[lr * ts + b] = kr_fmul(kr_fmul((float)sdot, sc), xds[bb]);
+                }
+                b += sb;
+                lr += sr;
+                if (b >= cur.nbc) { b -= cur.nbc; lr++; }
             }
-            b += sb;
-            lr += sr;
-            if (b >= nb) { b -= nb; lr++; }
-        }
-    }
-    __syncthreads();
-
-    if (tid < nloc) {
-        const float *p = t2 + tid * stride;
-        float s = 0.0f;
-#pragma unroll 8
-        for (int b = 0; b < nb; b++) s = kr_fadd(s, p[b]);
-        sums[tid] = s;
-    }
-    __syncthreads();
-
-    if (EPI == EPI_STORE) {
-        if (tid < nr) pick3(mi, a.y[0], a.y[1], a.y[2])[row0 + tid] = sums[tid];
-    } else if (EPI == EPI_ADD) {
-        if (tid < nr) {
-            float *y = pick3(mi, a.y[0], a.y[1], a.y[2]) + row0 + tid;
-            *y = kr_fadd(*y, sums[tid]);
-        }
-    } else if (EPI == EPI_QKV) {
-        // bias (model/transformer.c:276-277), then RoPE on q and k
-        // (k_scalar.c:79-94: pairs 2i, 2i+1 of each head, unfused)
-        const float *bias = pick3(mi, a.bias[0], a.bias[1], a.bias[2]);
-        float v = 0.0f;
-        if (tid < nr) {
-            v = sums[tid];
-            if (bias) v = kr_fadd(v, bias[row0 + tid]);
         }
         __syncthreads();
-        if (tid < nr) sums[tid] = v;
-        __syncthreads();
-        if (tid < nr) {
-            const int row = row0 + tid, pos = *a.pos;
-            float o = v;
-            if (mi < 2) {
-                const int hd = a.head_dim, j = row % hd, h2 = hd >> 1;
-                const float c = a.rope_cos[(size_t)pos * h2 + (j >> 1)], s = a.rope_sin[(size_t)pos * h2 + (j >> 1)];
-                const float pa = sums[tid & ~1], pb = sums[tid | 1];
-                o = (j & 1) == 0 ? kr_fsub(kr_fmul(pa, c), kr_fmul(pb, s))
-                                 : kr_fadd(kr_fmul(pa, s), kr_fmul(pb, c));
+        if (tid < cur.nloc) {
+            if (chunk == 0) acc = 0.0f;
+            const float *p = T + tid * ts;
+            int j = 0;
+            for (; j + 32 <= cur.nbc; j += 32) {
+                float4 r[8];
+#pragma unroll
+                for (int k = 0; k < 8; k++) r[k] = *(const float4 *)(p + j + 4 * k);
+#pragma unroll
+                for (int k = 0; k < 8; k++) {
+                    acc = kr_fadd(acc, r[k].x);
+                    acc = kr_fadd(acc, r[k].y);
+                    acc = kr_fadd(acc, r[k].z);
+                    acc = kr_fadd(acc, r[k].w);
+                }
             }
-            if (mi == 0) a.y[0][row] = o;
-            else pick3(mi, a.y[0], a.y[1], a.y[2])[(size_t)pos * a.ld_cache + row] = o;
+            for (; j < cur.nbc; j++) acc = kr_fadd(acc, p[j]);
         }
-    } else if (EPI == EPI_SWIGLU) {
-        // g = g / (1 + expf(-g)) * u (k_scalar.c:96-98)
-        if (tid < nr) {
-            const float h1 = sums[tid], h3 = sums[nr + tid];
-            a.y[0][row0 + tid] = kr_fmul(kr_fdiv(h1, kr_fadd(1.0f, kr_expf(-h1))), h3);
+        if (nchunk == 0) {   // the tile's last chunk: epilogue
+            if (tid < cur.nloc) sums[tid] = acc;
+            __syncthreads();
+            const int mi = cur.mi, row0 = cur.row0, nr = cur.nr;
+            if (EPI == EPI_STORE) {
+                if (tid < nr) pick3(mi, a.y[0], a.y[1], a.y[2])[row0 + tid] = sums[tid];
+            } else if (EPI == EPI_ADD) {
+                if (tid < nr) {
+                    float *y = pick3(mi, a.y[0], a.y[1], a.y[2]) + row0 + tid;
+                    *y = kr_fadd(*y, sums[tid]);
+                }
+            } else if (EPI == EPI_QKV) {
+                // bias (model/transformer.c:276-277), then RoPE on q and k
+                // (k_scalar.c:79-94: pairs 2i, 2i+1 of each head, unfused)
+                const float *bias = pick3(mi, a.bias[0], a.bias[1], a.bias[2]);
+                float v = 0.0f;
+                if (tid < nr) {
+                    v = sums[tid];
+                    if (bias) v = kr_fadd(v, bias[row0 + tid]);
+                }
+                __syncthreads();
+                if (tid < nr) sums[tid] = v;
+                __syncthreads();
+                if (tid < nr) {
+                    const int row = row0 + tid, pos = *a.pos;
+                    float o = v;
+                    if (mi < 2) {
+                        const int hd = a.head_dim, j = row % hd, h2 = hd >> 1;
+                        const float c = a.rope_cos[(size_t)pos * h2 + (j >> 1)],
+                                    sn = a.rope_sin[(size_t)pos * h2 + (j >> 1)];
+                        const float pa = sums[tid & ~1], pb = sums[tid | 1];
+                        o = (j & 1) == 0 ? kr_fsub(kr_fmul(pa, c), kr_fmul(pb, sn))
+                                         : kr_fadd(kr_fmul(pa, sn), kr_fmul(pb, c));
+                    }
+                    if (mi == 0) a.y[0][row] = o;
+                    else pick3(mi, a.y[0], a.y[1], a.y[2])[(size_t)pos * a.ld_cache + row] = o;
+                }
+            } else if (EPI == EPI_SWIGLU) {
+                // g = g / (1 + expf(-g)) * u (k_scalar.c:96-98)
+                if (tid < nr) {
+                    const float h1 = sums[tid], h3 = sums[nr + tid];
+                    a.y[0][row0 + tid] = kr_fmul(kr_fdiv(h1, kr_fadd(1.0f, kr_expf(-h1))), h3);
+                }
+            }
+        }
+        tile = ntile;
+        chunk = nchunk;
+        return tile < ntiles;
+    };
+    static_assert(MV_DEPTH == 2 || MV_DEPTH == 4, "LDS halves alternate with the item parity");
+    if (MV_DEPTH == 2) {
+        while (step(std::integral_constant<int, 0>()) && step(std::integral_constant<int, 1>() )) {
+        }
+    } else {
+        while (step(std::integral_constant<int, 0>()) && step(std::integral_constant<int, 1 % MV_DEPTH>()) &&
+               step(std::integral_constant<int, 2 % MV_DEPTH>()) && step(std::integral_constant<int, 3 % MV_DEPTH>())) {
         }
     }
 }
 
-// Rows per workgroup: as many as MV_NPT blocks per thread allow (at most
-// cap, even for the RoPE pairs), halved down to 8 while the launch would have
-// fewer workgroups than compute units (measured on the 8B shapes: wo 4096x4096
-// is fastest at 16, w2 4096x14336 at 8 or more, the classifier at 32).
-int g_mv_rows_override = 0;   // krh_tune(KRH_TUNE_MV_ROWS, R): fixed rows per workgroup
+// Rows per tile: the largest power of two (at most cap, even for the RoPE
+// pairs) that still gives MV_MIN_TILES tiles; blocks per chunk: as many as
+// MV_NPT slots per thread allow (a multiple of 4, for the 16-byte term reads).
+int g_mv_rows_override = 0;   // krh_tune(KRH_TUNE_MV_ROWS, R): fixed rows per tile
+constexpr int MV_MIN_TILES = 512;
 
 int mv_rows(int K, int total_rows, int local_per_row, int cap) {
-    const int nb = K / KR_QK;
-    if (g_mv_rows_override > 0) {
-        int R = g_mv_rows_override;
-        while (R > 1 && R * local_per_row * nb > MV_NPT * MV_THREADS) R /= 2;
-        return R;
-    }
-    int R = MV_NPT * MV_THREADS / (nb * local_per_row);
-    if (R > cap) R = cap;
-    while (R > 8 && total_rows / R < 256) R /= 2;
+    (void)K;
+    int R = g_mv_rows_override > 0 ? g_mv_rows_override : cap / local_per_row;
+    if (R * local_per_row > 64) R = 64 / local_per_row;
+    if (g_mv_rows_override <= 0)
+        while (R > 2 && (total_rows + R - 1) / R < MV_MIN_TILES) R /= 2;
     if (R > 1) R &= ~1;
     return R < 1 ? 1 : R;
 }
+
+int mv_chunk(int nb, int nloc) {
+    int c = (MV_NPT * MV_THREADS / nloc) & ~3;
+    if (c < 4) c = 4;
+    return c < nb ? c : nb;
+}
+
+// workgroups resident at once: two per compute unit
+constexpr int MV_RESIDENT = 512;
 
 template <int EPI>
 void launch_mv(MvArgs &a, const KMat &W) {
     const int nb = a.K / KR_QK;
     const int nloc = EPI == EPI_SWIGLU ? 2 * a.R : a.R;
-    const size_t lds = (size_t)a.K + 4u * nb + 4u * (size_t)nloc * (nb | 1) + 4u * nloc;
-    const int grid = a.tile0[a.nmat];
-    if (a.K % KR_QK || lds > 64 * 1024 || grid <= 0 || nloc > MV_THREADS || nloc * nb > MV_NPT * MV_THREADS ||
+    a.nbc = mv_chunk(nb, nloc);
+    const size_t lds = (size_t)a.K + 4u * nb + 4u * 2 * (size_t)nloc * (a.nbc + 4) + 4u * nloc + (a.nw ? 4u * a.K : 0u);
+    const int ntiles = a.tile0[a.nmat];
+    const int grid = ntiles > MV_RESIDENT ? MV_RESIDENT : ntiles;
+    if (a.K % KR_QK || lds > 64 * 1024 || grid <= 0 || nloc > 64 || nloc * a.nbc > MV_NPT * MV_THREADS ||
         (!a.xq && !a.xf)) {
         kr_fail(ML_E_SHAPE, "matvec shape", hipSuccess);
         return;
@@ -293,25 +459,6 @@ void launch_mv(MvArgs &a, const KMat &W) {
 // n % 32 == 0; rows 16-byte aligned.
 constexpr int RN_THREADS = 256, RN_V4 = 16, RN_MAX = RN_THREADS * RN_V4 * 4;
 
-// 0 + v[0] + v[1] + ... + v[n-1] in index order (one lane), n % 32 == 0, v in
-// LDS: reads are batched 8 float4 at a time so the adds do not wait on each.
-__device__ __forceinline__ float kr_chain_lds(const float *v, int n) {
-    const float4 *p = (const float4 *)v;
-    float s = 0.0f;
-    for (int i = 0; i < n / 4; i += 8) {
-        float4 r[8];
-#pragma unroll
-        for (int k = 0; k < 8; k++) r[k] = p[i + k];
-#pragma unroll
-        for (int k = 0; k < 8; k++) {
-            s = kr_fadd(s, r[k].x);
-            s = kr_fadd(s, r[k].y);
-            s = kr_fadd(s, r[k].z);
-            s = kr_fadd(s, r[k].w);
-        }
-    }
-    return s;
-}
 
 __global__ void __launch_bounds__(RN_THREADS) k_rmsnorm_q8(int8_t *q, float *d, int dld, float *xb, const float *x,
                                                            const float *w, int n, float eps, int norm) {
@@ -529,23 +676,32 @@ __global__ void __launch_bounds__(AT_THREADS) k_attn_softmax(float *att, int max
 
 // out for one KV head's query heads and DW of their dims, one wave per
 // workgroup: lane = (head j of the group, dim d), DW = 64 / (group rounded up
-// to a power of two). Tiles of MX_TILE floats of V (MX_TILE / DW positions)
-// and the heads' weights for those positions are loaded MX_DEPTH tiles ahead
-// into registers, then passed through LDS; each lane runs its ordered chain
-// o += a_t * v_t,d (k_scalar.c:119-122). ao is written as floats (its
-// quantization happens where it is consumed).
-constexpr int MX_TILE = 1024;
+// to a power of two). Each lane runs its ordered chain o += a_t * v_t,d
+// (k_scalar.c:119-122). ao is written as floats (its quantization happens
+// where it is consumed).
+//
+// The chain is the bound (one dependent add per position), so everything else
+// is pipelined under it: tiles of MX_T positions of V and of the heads' weights
+// are loaded MX_DEPTH tiles ahead into registers; tile t + 1 is staged into
+// the other half of a double LDS buffer while tile t is read, V transposed
+// ([dim][position]) so one 16-byte LDS read feeds 4 steps; the reads of each
+// 16-step chunk are issued before the adds of the chunk before it. The
+// workgroup is one wave, whose LDS operations execute in order, so LDS needs
+// only compiler ordering (kr_lds_order), not barriers.
+constexpr int MX_T = 64, MX_TS = MX_T + 4;   // positions per tile; padded LDS row
+
+__device__ __forceinline__ void kr_lds_order() { asm volatile("" ::: "memory"); }
 
 template <int DW>
 __global__ void __launch_bounds__(64) k_attn_mix(float *ao, const float *att, const float *vc, int group, int hd,
                                                  int kv_dim, int max_seq, int window, const int *pos_p) {
-    constexpr int TP = MX_TILE / DW;         // positions per tile
-    constexpr int NV = MX_TILE / 4 / 64;     // float4 of V per lane per tile
-    constexpr int GP = 64 / DW;              // head slots per wave
-    constexpr int NA = (GP * TP + 255) / 256;   // float4 of weights per lane per tile
-    constexpr int MX_DEPTH = NA > 4 ? 2 : 6;    // tiles in flight
-    __shared__ __align__(16) float vt[2][MX_TILE];
-    __shared__ __align__(16) float aw[2][GP * TP];
+    constexpr int GP = 64 / DW;                    // head slots per wave
+    constexpr int NV = MX_T * DW / 4 / 64;         // float4 of V per lane per tile
+    constexpr int NA = (GP * MX_T / 4 + 63) / 64;  // float4 of weights per lane per tile
+    constexpr int MX_DEPTH = NV + NA > 8 ? 2 : 4;  // tiles in flight (even: LDS halves alternate)
+    __shared__ __align__(16) float vt[2][DW * MX_TS];
+    constexpr int AW = GP * MX_T > NA * 256 ? GP * MX_T : NA * 256;   // padded: every lane stores
+    __shared__ __align__(16) float aw[2][AW];
     int first, n;
     attn_range(pos_p, window, &first, &n);
     const int g = blockIdx.x, c0 = blockIdx.y * DW, lane = threadIdx.x;
@@ -554,61 +710,125 @@ __global__ void __launch_bounds__(64) k_attn_mix(float *ao, const float *att, co
     const size_t q_dim = (size_t)gridDim.x * group * hd;
     const float *abase = att + ((size_t)blockIdx.z * gridDim.x * group + (size_t)g * group) * max_seq;
     ao += blockIdx.z * q_dim;
-    const int ntiles = (n + TP - 1) / TP;
-    const int cw = min(DW, hd - c0);         // valid dims of the chunk (multiple of 4)
+    const int ntiles = (n + MX_T - 1) / MX_T;
+    const int cw = min(DW, hd - c0);   // valid dims of the chunk (a multiple of 4)
 
+    // Every load is unconditional from an address clamped into the live
+    // range (position n - 1, the chunk's last float4, the group's last head,
+    // the row's last float4): values loaded for positions >= n, dims >= cw or
+    // heads >= group only feed lanes and steps that are never stored or run,
+    // and a branch-free load stream lets the compiler's wait counts keep the
+    // loads of MX_DEPTH tiles in flight together.
     float4 rv[MX_DEPTH][NV], ra[MX_DEPTH][NA];
     auto load = [&](int tile, float4 *v, float4 *a) {
-        const int t0 = tile * TP;
+        const int t0 = min(tile, ntiles - 1) * MX_T;
 #pragma unroll
         for (int k = 0; k < NV; k++) {
-            const int e = (k * 64 + lane) * 4, r = e / DW, c = e % DW;
-            v[k] = t0 + r < n && c < cw ? *(const float4 *)(vbase + (size_t)(t0 + r) * kv_dim + c)
-                                        : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            const int e = (k * 64 + lane) * 4, r = e / DW, c = min(e % DW, cw - 4);   // position r, dims c..c+3
+            v[k] = *(const float4 *)(vbase + (size_t)min(t0 + r, n - 1) * kv_dim + c);
         }
 #pragma unroll
         for (int k = 0; k < NA; k++) {
-            const int e = (k * 64 + lane) * 4, jj = e / TP, r = e % TP;   // TP % 4 == 0
-            float4 x = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-            if (jj < group && e < GP * TP) {
-                const float *src = abase + (size_t)jj * max_seq + t0 + r;
-                if (t0 + r + 3 < n) x = make_float4(src[0], src[1], src[2], src[3]);
-                else {
-                    if (t0 + r < n) x.x = src[0];
-                    if (t0 + r + 1 < n) x.y = src[1];
-                    if (t0 + r + 2 < n) x.z = src[2];
-                }
-            }
-            a[k] = x;
+            const int e = (k * 64 + lane) * 4, jj = min(e / MX_T, group - 1), r = e % MX_T;
+            const float *src = abase + (size_t)jj * max_seq + min(t0 + r, max_seq - 4);
+            a[k] = make_float4(src[0], src[1], src[2], src[3]);
         }
     };
+    auto stage = [&](int buf, int tile, const float4 *v, const float4 *a) {
+        float *V = vt[buf], *A = aw[buf];
 #pragma unroll
-    for (int s = 0; s < MX_DEPTH; s++)
-        if (s < ntiles) load(s, rv[s], ra[s]);
+        for (int k = 0; k < NV; k++) {
+            const int e = (k * 64 + lane) * 4, r = e / DW, c = e % DW;
+            V[(c + 0) * MX_TS + r] = v[k].x;
+            V[(c + 1) * MX_TS + r] = v[k].y;
+            V[(c + 2) * MX_TS + r] = v[k].z;
+            V[(c + 3) * MX_TS + r] = v[k].w;
+        }
+#pragma unroll
+        for (int k = 0; k < NA; k++) {
+            const int e = (k * 64 + lane) * 4, r = e % MX_T;
+            // a float4 clamped back from the row's end holds position p at
+            // element p - (max_seq - 4): shift it down to element p - p0
+            const int sh = tile * MX_T + r - min(tile * MX_T + r, max_seq - 4);
+            const float4 x = a[k];
+            float4 y;
+            y.x = sh == 0 ? x.x : sh == 1 ? x.y : sh == 2 ? x.z : x.w;
+            y.y = sh == 0 ? x.y : sh == 1 ? x.z : x.w;
+            y.z = sh == 0 ? x.z : x.w;
+            y.w = x.w;
+            *(float4 *)(A + e) = y;
+        }
+        kr_lds_order();
+    };
+    struct Chunk { float4 v[4], a[4]; };   // 16 steps of one lane
+    auto read = [&](Chunk &c, int buf, int k) {
+        const float *V = vt[buf] + d * MX_TS + 16 * k, *A = aw[buf] + j * MX_T + 16 * k;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            c.v[i] = *(const float4 *)(V + 4 * i);
+            c.a[i] = *(const float4 *)(A + 4 * i);
+        }
+    };
     float o = 0.0f;
-    for (int k0 = 0; k0 < ntiles; k0 += MX_DEPTH) {
+    auto chain = [&](const Chunk &c) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            o = kr_fadd(o, kr_fmul(c.a[i].x, c.v[i].x));
+            o = kr_fadd(o, kr_fmul(c.a[i].y, c.v[i].y));
+            o = kr_fadd(o, kr_fmul(c.a[i].z, c.v[i].z));
+            o = kr_fadd(o, kr_fmul(c.a[i].w, c.v[i].w));
+        }
+    };
+
+#pragma unroll
+    for (int s = 0; s < MX_DEPTH; s++) load(s, rv[s], ra[s]);
+    stage(0, 0, rv[0], ra[0]);
+    load(MX_DEPTH, rv[0], ra[0]);
+    Chunk c0r, c1r;
+    read(c0r, 0, 0);
+    // main loop: groups of MX_DEPTH full tiles; tile k0 + s sits in LDS half
+    // s & 1 and its first chunk is in c0r when its step begins
+    const int ngroups = n / (MX_T * MX_DEPTH);
+    int k0 = 0;
+    for (; k0 < ngroups * MX_DEPTH; k0 += MX_DEPTH) {
 #pragma unroll
         for (int s = 0; s < MX_DEPTH; s++) {
-            const int tile = k0 + s;
-            if (tile >= ntiles) break;
-            float *V = vt[s & 1], *A = aw[s & 1];
+            const int b = s & 1, nx = (s + 1) % MX_DEPTH;
+            // phases fenced for the scheduler: a chunk's reads are issued
+            // one phase before its products and adds, and the staging of
+            // the next tile shares a phase with the first chunk's adds
+            read(c1r, b, 1);
+            __builtin_amdgcn_sched_barrier(0);
+            chain(c0r);
+            stage(b ^ 1, k0 + s + 1, rv[nx], ra[nx]);
+            load(k0 + s + 1 + MX_DEPTH, rv[nx], ra[nx]);
+            __builtin_amdgcn_sched_barrier(0);
+            read(c0r, b, 2);
+            __builtin_amdgcn_sched_barrier(0);
+            chain(c1r);
+            __builtin_amdgcn_sched_barrier(0);
+            read(c1r, b, 3);
+            __builtin_amdgcn_sched_barrier(0);
+            chain(c0r);
+            __builtin_amdgcn_sched_barrier(0);
+            read(c0r, b ^ 1, 0);
+            __builtin_amdgcn_sched_barrier(0);
+            chain(c1r);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+    // the last tiles (at most MX_DEPTH; tile k0 is staged in half 0, tile
+    // k0 + s is in rv[s]); the last may be partial, and only its live steps
+    // run: a zero weight would turn -0 to +0
 #pragma unroll
-            for (int k = 0; k < NV; k++) *(float4 *)(V + (k * 64 + lane) * 4) = rv[s][k];
-#pragma unroll
-            for (int k = 0; k < NA; k++) {
-                const int e = (k * 64 + lane) * 4;
-                if (e < GP * TP) *(float4 *)(A + e) = ra[s][k];
-            }
-            if (tile + MX_DEPTH < ntiles) load(tile + MX_DEPTH, rv[s], ra[s]);
-            __syncthreads();
-            const int nt = min(TP, n - tile * TP);
-            const float *ap = A + j * TP, *vp = V + d;
-            if (nt == TP) {
-#pragma unroll 16
-                for (int r = 0; r < TP; r++) o = kr_fadd(o, kr_fmul(ap[r], vp[r * DW]));
-            } else {
-                for (int r = 0; r < nt; r++) o = kr_fadd(o, kr_fmul(ap[r], vp[r * DW]));
-            }
+    for (int s = 0; s < MX_DEPTH; s++) {
+        const int tile = k0 + s;
+        if (tile < ntiles) {
+            if (s > 0) stage(s & 1, tile, rv[s], ra[s]);
+            const int nt = min(MX_T, n - tile * MX_T);
+            const float *V = vt[s & 1] + d * MX_TS, *A = aw[s & 1] + j * MX_T;
+            for (int r = 0; r < nt; r++) o = kr_fadd(o, kr_fmul(A[r], V[r]));
+            kr_lds_order();
         }
     }
     if (j < group && d < cw) ao[(size_t)(g * group + j) * hd + c0 + d] = o;
@@ -727,7 +947,7 @@ extern "C" void krh_quantize_q8_t(int8_t *q, float *d, int dld, const float *x, 
 }
 
 static void mv_plain(float *y, const krh_mat *W, const int8_t *xq, const float *xd, const float *xf,
-                     int accumulate) {
+                     const float *nw, float eps, int accumulate) {
     MvArgs a = {};
     a.m[0] = to_kmat(W);
     a.nmat = 1;
@@ -737,6 +957,8 @@ static void mv_plain(float *y, const krh_mat *W, const int8_t *xq, const float *
     a.xq = xq;
     a.xd = xd;
     a.xf = xf;
+    a.nw = nw;
+    a.eps = eps;
     a.K = W->cols;
     a.y[0] = y;
     if (accumulate) launch_mv<EPI_ADD>(a, a.m[0]);
@@ -748,17 +970,22 @@ extern "C" void krh_tune(int key, int value) {
 }
 
 extern "C" void krh_matvec(float *y, const krh_mat *W, const int8_t *xq, const float *xd, int accumulate) {
-    mv_plain(y, W, xq, xd, nullptr, accumulate);
+    mv_plain(y, W, xq, xd, nullptr, nullptr, 0.0f, accumulate);
 }
 
 extern "C" void krh_matvec_f(float *y, const krh_mat *W, const float *x, int accumulate) {
-    mv_plain(y, W, nullptr, nullptr, x, accumulate);
+    mv_plain(y, W, nullptr, nullptr, x, nullptr, 0.0f, accumulate);
 }
 
-extern "C" void krh_matvec_qkv(float *q, float *kc, float *vc, const krh_mat *wq, const krh_mat *wk,
-                               const krh_mat *wv, const float *bq, const float *bk, const float *bv, const int8_t *xq,
-                               const float *xd, const float *rope_cos, const float *rope_sin, int head_dim,
-                               const int *pos) {
+extern "C" void krh_rmsnorm_matvec(float *y, const krh_mat *W, const float *x, const float *nw, float eps,
+                                   int accumulate) {
+    mv_plain(y, W, nullptr, nullptr, x, nw, eps, accumulate);
+}
+
+static void qkv(float *q, float *kc, float *vc, const krh_mat *wq, const krh_mat *wk, const krh_mat *wv,
+                const float *bq, const float *bk, const float *bv, const int8_t *xq, const float *xd, const float *xf,
+                const float *nw, float eps, const float *rope_cos, const float *rope_sin, int head_dim,
+                const int *pos) {
     if (wq->cols != wk->cols || wq->cols != wv->cols || wk->rows != wv->rows || head_dim % 2 || wq->rows % 2 ||
         wk->rows % 2 || wq->type != wk->type || wq->d16 != wk->d16 || wv->d16 != wq->d16) {
         kr_fail(ML_E_SHAPE, "qkv shapes", hipSuccess);
@@ -776,6 +1003,9 @@ extern "C" void krh_matvec_qkv(float *q, float *kc, float *vc, const krh_mat *wq
     a.tile0[3] = a.tile0[2] + (wv->rows + a.R - 1) / a.R;
     a.xq = xq;
     a.xd = xd;
+    a.xf = xf;
+    a.nw = nw;
+    a.eps = eps;
     a.K = wq->cols;
     a.y[0] = q;
     a.y[1] = kc;
@@ -805,7 +1035,22 @@ extern "C" void krh_matvec_qkv(float *q, float *kc, float *vc, const krh_mat *wq
     launch_mv<EPI_QKV>(c, c.m[2]);
 }
 
-extern "C" void krh_matvec_swiglu(float *h, const krh_mat *w1, const krh_mat *w3, const int8_t *xq, const float *xd) {
+extern "C" void krh_matvec_qkv(float *q, float *kc, float *vc, const krh_mat *wq, const krh_mat *wk,
+                               const krh_mat *wv, const float *bq, const float *bk, const float *bv, const int8_t *xq,
+                               const float *xd, const float *rope_cos, const float *rope_sin, int head_dim,
+                               const int *pos) {
+    qkv(q, kc, vc, wq, wk, wv, bq, bk, bv, xq, xd, nullptr, nullptr, 0.0f, rope_cos, rope_sin, head_dim, pos);
+}
+
+extern "C" void krh_rmsnorm_matvec_qkv(float *q, float *kc, float *vc, const krh_mat *wq, const krh_mat *wk,
+                                       const krh_mat *wv, const float *bq, const float *bk, const float *bv,
+                                       const float *x, const float *nw, float eps, const float *rope_cos,
+                                       const float *rope_sin, int head_dim, const int *pos) {
+    qkv(q, kc, vc, wq, wk, wv, bq, bk, bv, nullptr, nullptr, x, nw, eps, rope_cos, rope_sin, head_dim, pos);
+}
+
+static void swiglu(float *h, const krh_mat *w1, const krh_mat *w3, const int8_t *xq, const float *xd, const float *xf,
+                   const float *nw, float eps) {
     if (w1->rows != w3->rows || w1->cols != w3->cols || w1->type != w3->type || w1->d16 != w3->d16) {
         kr_fail(ML_E_SHAPE, "swiglu shapes", hipSuccess);
         return;
@@ -819,20 +1064,32 @@ extern "C" void krh_matvec_swiglu(float *h, const krh_mat *w1, const krh_mat *w3
     a.tile0[1] = (w1->rows + a.R - 1) / a.R;
     a.xq = xq;
     a.xd = xd;
+    a.xf = xf;
+    a.nw = nw;
+    a.eps = eps;
     a.K = w1->cols;
     a.y[0] = h;
     launch_mv<EPI_SWIGLU>(a, a.m[0]);
+}
+
+extern "C" void krh_matvec_swiglu(float *h, const krh_mat *w1, const krh_mat *w3, const int8_t *xq, const float *xd) {
+    swiglu(h, w1, w3, xq, xd, nullptr, nullptr, 0.0f);
+}
+
+extern "C" void krh_rmsnorm_matvec_swiglu(float *h, const krh_mat *w1, const krh_mat *w3, const float *x,
+                                          const float *nw, float eps) {
+    swiglu(h, w1, w3, nullptr, nullptr, x, nw, eps);
 }
 
 static void attention(float *ao, float *att, const float *q, const float *kc, const float *vc, int n_heads,
                       int n_kv_heads, int head_dim, int max_seq, int window, float scale, const int *pos, int ntok,
                       int max_pos) {
     if (n_kv_heads <= 0 || n_heads % n_kv_heads || head_dim % 4 || (n_heads * head_dim) % KR_QK ||
-        n_heads / n_kv_heads > 16 || head_dim > 1024) {
+        n_heads / n_kv_heads > 16 || head_dim > 1024 || max_seq < 4) {
         kr_fail(ML_E_SHAPE, "attention shape", hipSuccess);
         return;
     }
-    const int group = n_heads / n_kv_heads, kv_dim = n_kv_heads * head_dim, q_dim = n_heads * head_dim;
+    const int group = n_heads / n_kv_heads, kv_dim = n_kv_heads * head_dim;
     const size_t lds = sizeof(float) * ((size_t)group * head_dim + (size_t)AT_T * (head_dim + 1));
     hipLaunchKernelGGL(k_attn_scores, dim3(n_kv_heads, (max_pos + AT_T) / AT_T, ntok), dim3(AT_THREADS), lds,
                        kr_stream(), att, q, kc, group, head_dim, kv_dim, max_seq, window, scale, pos);

@@ -25,8 +25,10 @@ struct kr_dev_layer {
     krh_mat wq, wk, wv, wo, w1, w2, w3;
 };
 
-ml_status kr_seterr(ml_status s, const char *fmt, ...);
-ml_status kr_parse_header(ml_config *cfg, int *shared, const uint8_t *h);
-double kr_now(void);
+/* internal to libkrafla.so (not exported) */
+#define KR_INTERNAL __attribute__((visibility("hidden")))
+KR_INTERNAL ml_status kr_seterr(ml_status s, const char *fmt, ...);
+KR_INTERNAL ml_status kr_parse_header(ml_config *cfg, int *shared, const uint8_t *h);
+KR_INTERNAL double kr_now(void);
 
 #endif

@@ -4,9 +4,8 @@
  *
  * One decode step (model/transformer.c:257-306), per layer:
  *   rmsnorm+quantize(attn_norm) -> q,k,v matvec + bias + RoPE + cache write
- *   -> attention (+ quantize of its output) -> x += wo.ao
- *   -> rmsnorm+quantize(ffn_norm) -> silu(w1.x) * (w3.x) + quantize
- *   -> x += w2.h
+ *   -> attention -> x += wo.q8(ao) -> rmsnorm+quantize(ffn_norm)
+ *   -> silu(w1.x) * (w3.x) -> quantize h -> x += w2.h
  * then rmsnorm+quantize(final_norm) -> logits = wcls.x. Every op reads the
  * token and position from device memory, so the captured step replays for
  * any position without new arguments. */

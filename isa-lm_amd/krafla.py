@@ -89,8 +89,32 @@ def _load(path):
     return C.CDLL(path, mode=C.RTLD_GLOBAL)
 
 
-hip = _load(LIB_HIP)
-host = _load(LIB_HOST)
+class _Lib:
+    """Only the declared functions of a library: calling an undeclared one
+    through ctypes would pass 64-bit pointers as 32-bit ints."""
+
+    def __init__(self, path):
+        self._dll = _load(path)
+        self._fns = {}
+
+    def declare(self, name, res, args):
+        f = getattr(self._dll, name)
+        f.restype = res
+        f.argtypes = args
+        self._fns[name] = f
+
+    def __getattr__(self, name):
+        try:
+            return self.__dict__["_fns"][name]
+        except KeyError:
+            raise AttributeError("%s is not declared in krafla.py" % name) from None
+
+    def declared(self):
+        return set(self._fns)
+
+
+hip = _Lib(LIB_HIP)
+host = _Lib(LIB_HOST)
 
 _P = C.c_void_p
 for name, res, args in [
@@ -111,6 +135,10 @@ for name, res, args in [
     ("krh_matvec_qkv", None, [_P, _P, _P, C.POINTER(KrhMat), C.POINTER(KrhMat), C.POINTER(KrhMat), _P, _P, _P,
                               _P, _P, _P, _P, C.c_int, _P]),
     ("krh_matvec_f", None, [_P, C.POINTER(KrhMat), _P, C.c_int]),
+    ("krh_rmsnorm_matvec", None, [_P, C.POINTER(KrhMat), _P, _P, C.c_float, C.c_int]),
+    ("krh_rmsnorm_matvec_qkv", None, [_P, _P, _P, C.POINTER(KrhMat), C.POINTER(KrhMat), C.POINTER(KrhMat), _P, _P,
+                                      _P, _P, _P, C.c_float, _P, _P, C.c_int, _P]),
+    ("krh_rmsnorm_matvec_swiglu", None, [_P, C.POINTER(KrhMat), C.POINTER(KrhMat), _P, _P, C.c_float]),
     ("krh_matvec_swiglu", None, [_P, C.POINTER(KrhMat), C.POINTER(KrhMat), _P, _P]),
     ("krh_attention", None, [_P, _P, _P, _P, _P, _P, _P, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_float,
                              _P]),
@@ -128,16 +156,23 @@ for name, res, args in [
     ("krh_math_batch", None, [C.c_int, _P, _P, _P, C.c_size_t]), ("krh_h2f_batch", None, [_P, _P, C.c_size_t]),
     ("krh_block_dots", None, [_P, C.POINTER(KrhMat), _P]),
     ("krh_tune", None, [C.c_int, C.c_int]),
+    ("krh_rmsnorm", None, [_P, _P, _P, C.c_int, C.c_float]), ("krh_add", None, [_P, _P, C.c_int]),
+    ("krh_rope", None, [_P, _P, _P, _P, C.c_int, C.c_int, C.c_int]),
+    ("krh_silu_mul", None, [_P, _P, C.c_int]), ("krh_gelu_mul", None, [_P, _P, C.c_int]),
+    ("krh_softmax", None, [_P, C.c_int]),
+    ("krh_dot_rows", None, [_P, _P, _P, C.c_size_t, C.c_int, C.c_int, C.c_float]),
+    ("krh_axpy_rows", None, [_P, _P, _P, C.c_size_t, C.c_int, C.c_int]),
+    ("krh_quantize_row", None, [_P, _P, _P, C.c_int]),
+    ("krh_softcap_rows", None, [_P, C.c_size_t, C.c_int, C.c_int, C.c_float]),
+    ("krh_set_int", None, [_P, C.c_int]), ("krh_transpose_scales", None, [_P, C.c_int, _P, C.c_int, C.c_int]),
     ("krh_gen_blocks", None, [_P, _P, C.c_uint64, C.c_int, C.c_int, C.c_int, C.c_int, C.c_float]),
 ]:
-    f = getattr(hip, name)
-    f.restype = res
-    f.argtypes = args
+    hip.declare(name, res, args)
 
 for name, res, args in [
     ("kr_status_str", C.c_char_p, [C.c_int]), ("kr_error", C.c_char_p, []),
     ("kr_model_load", C.c_int, [C.POINTER(_P), C.c_char_p]), ("kr_model_config", C.POINTER(MlConfig), [_P]),
-    ("kr_model_tok_emb", C.POINTER(MlQTensor), [_P]), ("kr_model_wcls", C.POINTER(MlQTensor), [_P]),
+    ("kr_model_tok_emb", C.POINTER(MlQTensor), [_P]), ("kr_model_layer", _P, [_P, C.c_int]), ("kr_model_wcls", C.POINTER(MlQTensor), [_P]),
     ("kr_model_upload", C.c_int, [_P]),
     ("kr_model_device_mat", C.POINTER(KrhMat), [_P, C.c_int, C.c_char_p]),
     ("kr_model_device_vec", _P, [_P, C.c_int, C.c_char_p]), ("kr_model_device_bytes", C.c_size_t, [_P]), ("kr_model_free", None, [_P]),
@@ -150,9 +185,7 @@ for name, res, args in [
     ("kr_gen_matrix", None, [_P, _P, C.c_int, C.c_int, C.c_int, C.c_uint64, C.c_int]),
     ("kr_gen_normal", None, [_P, C.c_size_t, C.c_uint64]),
 ]:
-    f = getattr(host, name)
-    f.restype = res
-    f.argtypes = args
+    host.declare(name, res, args)
 
 
 class KraflaError(RuntimeError):

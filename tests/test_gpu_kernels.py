@@ -293,7 +293,8 @@ def test_matvec_float_input(dev, typ, d16, rows, cols):
 
 
 @pytest.mark.parametrize("nh,nkv,hd,pos,window", [(6, 6, 48, 0, 0), (6, 6, 48, 200, 0), (14, 2, 64, 511, 0),
-                                                  (32, 8, 128, 2303, 0), (32, 8, 64, 4000, 0), (8, 2, 64, 100, 7)])
+                                                  (32, 8, 128, 2303, 0), (32, 8, 64, 4000, 0), (8, 2, 64, 100, 7),
+                                                  (16, 1, 64, 63, 0), (4, 2, 32, 64, 0), (12, 4, 96, 130, 0)])
 def test_attention(dev, nh, nkv, hd, pos, window):
     max_seq = max(256, pos + 1)
     kvd, qd = nkv * hd, nh * hd
@@ -468,3 +469,69 @@ def test_silu_quant(dev):
         oracle.kro_silu_mul(h.ctypes.data, f32(u[t]).ctypes.data, n)
         q0, d0 = O.quantize(h)
         assert np.array_equal(q[t], q0) and np.array_equal(bits(d[:, t]), bits(d0))
+
+
+# ---- rmsnorm fused into the consuming matvec ----
+
+def oracle_norm_q8(x, w, eps=1e-5):
+    o = np.zeros(len(x), np.float32)
+    oracle.kro_rmsnorm(o.ctypes.data, f32(x).ctypes.data, f32(w).ctypes.data, len(x), C.c_float(eps))
+    return O.quantize(o)
+
+
+@pytest.mark.parametrize("typ,d16", [(K.ML_Q8_0, 1), (K.ML_Q4_0, 0)])
+@pytest.mark.parametrize("rows,cols", [(32000, 288), (4096, 4096), (5000, 2048), (7, 64)])
+def test_rmsnorm_matvec(dev, typ, d16, rows, cols):
+    """the classifier launch: rmsnorm, quantize, matvec (model/transformer.c:299-303);
+    more row tiles than workgroups, so workgroups loop"""
+    q, d, dh = rand_mat(rows, cols, typ, d16)
+    x = f32(RNG.normal(0, 3, cols))
+    w = f32(RNG.normal(1, 0.1, cols))
+    W = dmat(dev, q, d, dh, rows, cols, typ, d16)
+    yb = dev.zeros(4 * rows)
+    K.hip.krh_rmsnorm_matvec(yb.ptr, C.byref(W), dev.put(x).ptr, dev.put(w).ptr, 1e-5, 0)
+    ok()
+    xq, xd = oracle_norm_q8(x, w)
+    assert np.array_equal(bits(yb.get(np.float32, rows)), bits(oracle_matvec(q, d, rows, cols, typ, xq, xd)))
+
+
+@pytest.mark.parametrize("dim,nh,nkv,hd,typ,vtyp,bias", [(896, 14, 2, 64, K.ML_Q4_0, K.ML_Q8_0, 1),
+                                                          (4096, 32, 8, 128, K.ML_Q8_0, K.ML_Q8_0, 0)])
+def test_rmsnorm_qkv_matches_unfused(dev, dim, nh, nkv, hd, typ, vtyp, bias):
+    qd, kvd, max_seq, pos = nh * hd, nkv * hd, 40, 31
+    typs = (typ, typ, vtyp)
+    mats = [rand_mat(r, dim, t, 1) for r, t in zip((qd, kvd, kvd), typs)]
+    Ws = [dmat(dev, q, d, dh, r, dim, t, 1) for (q, d, dh), r, t in zip(mats, (qd, kvd, kvd), typs)]
+    bb = [dev.put(f32(RNG.normal(0, 0.02, r))).ptr if bias else None for r in (qd, kvd, kvd)]
+    cs, sn = dev.put(f32(RNG.uniform(-1, 1, max_seq * hd // 2))), dev.put(f32(RNG.uniform(-1, 1, max_seq * hd // 2)))
+    x, w = f32(RNG.normal(0, 2, dim)), f32(RNG.normal(1, 0.1, dim))
+    posb = dev.put(np.array([pos], np.int32))
+    outs = []
+    for fused in (1, 0):
+        qb, kc, vc = dev.zeros(4 * qd), dev.zeros(4 * max_seq * kvd), dev.zeros(4 * max_seq * kvd)
+        if fused:
+            K.hip.krh_rmsnorm_matvec_qkv(qb.ptr, kc.ptr, vc.ptr, *[C.byref(W) for W in Ws], *bb, dev.put(x).ptr,
+                                         dev.put(w).ptr, 1e-5, cs.ptr, sn.ptr, hd, posb.ptr)
+        else:
+            xq, xd = oracle_norm_q8(x, w)
+            K.hip.krh_matvec_qkv(qb.ptr, kc.ptr, vc.ptr, *[C.byref(W) for W in Ws], *bb, dev.put(xq).ptr,
+                                 dev.put(xd).ptr, cs.ptr, sn.ptr, hd, posb.ptr)
+        ok()
+        outs.append([b.get(np.float32, n) for b, n in ((qb, qd), (kc, max_seq * kvd), (vc, max_seq * kvd))])
+    for a, b in zip(*outs):
+        assert np.array_equal(bits(a), bits(b))
+
+
+@pytest.mark.parametrize("rows,cols,typ", [(14336, 4096, K.ML_Q8_0), (4864, 896, K.ML_Q4_0)])
+def test_rmsnorm_swiglu(dev, rows, cols, typ):
+    (q1, d1, h1), (q3, d3, h3) = rand_mat(rows, cols, typ, 1), rand_mat(rows, cols, typ, 1)
+    W1, W3 = dmat(dev, q1, d1, h1, rows, cols, typ, 1), dmat(dev, q3, d3, h3, rows, cols, typ, 1)
+    x, w = f32(RNG.normal(0, 2, cols)), f32(RNG.normal(1, 0.1, cols))
+    hb = dev.zeros(4 * rows)
+    K.hip.krh_rmsnorm_matvec_swiglu(hb.ptr, C.byref(W1), C.byref(W3), dev.put(x).ptr, dev.put(w).ptr, 1e-5)
+    ok()
+    xq, xd = oracle_norm_q8(x, w)
+    g = oracle_matvec(q1, d1, rows, cols, typ, xq, xd)
+    u = oracle_matvec(q3, d3, rows, cols, typ, xq, xd)
+    oracle.kro_silu_mul(g.ctypes.data, u.ctypes.data, rows)
+    assert np.array_equal(bits(hb.get(np.float32, rows)), bits(g))

@@ -314,3 +314,14 @@ def test_hip_ml_run_guard_without_gpu(workdir):
     K.gen_mlb(path, **dict(K.CONFIGS["stories15m_q8"], n_layers=1, vocab=64, max_seq=16))
     r = subprocess.run([exe, path, "--tokens", "1,2", "-n", "3"], capture_output=True, text=True, timeout=60)
     assert r.returncode == 3 and "ISA=hip" in r.stderr
+
+
+def test_binding_declares_every_export():
+    """every C entry point of both libraries is declared with its argument
+    types in the ctypes binding (an undeclared call would truncate pointers)"""
+    import subprocess
+    for lib, libpath in ((K.hip, K.LIB_HIP), (K.host, K.LIB_HOST)):
+        out = subprocess.run(["nm", "-D", "--defined-only", libpath], capture_output=True, text=True).stdout
+        syms = {l.split()[-1] for l in out.splitlines() if " T " in l}
+        exported = {s for s in syms if s.startswith("krh_") or s.startswith("kr_")}
+        assert exported and exported <= lib.declared(), sorted(exported - lib.declared())
