@@ -14,6 +14,7 @@
 
 #include "kr_internal.h"
 #include "kr_numerics.h"
+#include "kr_chain.h"
 
 namespace {
 
@@ -53,7 +54,8 @@ constexpr int MV_THREADS = 256;
 constexpr int MV_NPT = 4;   // weight blocks per thread per work item
 constexpr int MV_DEPTH = 2;    // work items in flight per workgroup (the one in use included): a wave that
                                // issues more loads than the memory pipeline holds stalls at issue
-constexpr int MV_XQ_MAX = 16384;   // activations up to this length are staged from registers
+constexpr int MV_XQ_MAX = 16384;   // quantized activations up to this length are staged from registers
+constexpr int MV_XF_MAX = 8192;    // float activations up to this length are normalized and quantized from registers
 
 template <typename T> __device__ __forceinline__ T pick3(int i, T a, T b, T c) { return i == 0 ? a : (i == 1 ? b : c); }
 
@@ -84,30 +86,35 @@ __device__ __forceinline__ int block_dot(const int4 w0, const int4 w1, const int
     return s;
 }
 
-// 0 + v[0] + v[1] + ... + v[n-1] in index order (one lane), n % 32 == 0, v in
-// LDS: reads are batched 8 float4 at a time so the adds do not wait on each.
-__device__ __forceinline__ float kr_chain_lds(const float *v, int n) {
-    const float4 *p = (const float4 *)v;
-    float s = 0.0f;
-    for (int i = 0; i < n / 4; i += 8) {
-        float4 r[8];
-#pragma unroll
-        for (int k = 0; k < 8; k++) r[k] = p[i + k];
-#pragma unroll
-        for (int k = 0; k < 8; k++) {
-            s = kr_fadd(s, r[k].x);
-            s = kr_fadd(s, r[k].y);
-            s = kr_fadd(s, r[k].z);
-            s = kr_fadd(s, r[k].w);
-        }
+// Q8_0 of the 4 values v = x[i..i+3] (k_scalar.c:39-57): 8 consecutive
+// lanes hold a 32-block (all 8 must call together); the block max is exact in
+// any order. q[i..i+3] receive the values, d[(i / 32) * dstep] the scale.
+__device__ __forceinline__ void kr_quant4(float4 v, int i, int8_t *q, float *d, size_t dstep) {
+    float m = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+    m = fmaxf(m, __shfl_xor(m, 1, 8));
+    m = fmaxf(m, __shfl_xor(m, 2, 8));
+    m = fmaxf(m, __shfl_xor(m, 4, 8));
+    int packed = 0;
+    float dd = 0.0f;
+    if (!(m < KR_QUANT_TINY)) {
+        const float id = kr_fdiv(127.0f, m);
+        dd = kr_fdiv(m, 127.0f);
+        packed = (kr_q8_elem(v.x, id) & 0xff) | (kr_q8_elem(v.y, id) & 0xff) << 8 |
+                 (kr_q8_elem(v.z, id) & 0xff) << 16 | (int)((unsigned)kr_q8_elem(v.w, id) << 24);
     }
-    return s;
+    *(int *)(q + i) = packed;
+    if ((i & 31) == 0) d[(size_t)(i >> 5) * dstep] = dd;
 }
 
-// Q8_0 of K floats into LDS (k_scalar.c:39-57): each thread takes 4
-// consecutive values, 8 threads a 32-block; the block max is exact in any
-// order. K % 32 == 0, x 16-byte aligned.
-// With w: the rmsnorm output (x * inv) * w (k_scalar.c:63) is quantized.
+// the rmsnorm output (x * inv) * w (k_scalar.c:63)
+__device__ __forceinline__ float4 kr_norm4(float4 x, float inv, float4 w) {
+    return make_float4(kr_fmul(kr_fmul(x.x, inv), w.x), kr_fmul(kr_fmul(x.y, inv), w.y),
+                       kr_fmul(kr_fmul(x.z, inv), w.z), kr_fmul(kr_fmul(x.w, inv), w.w));
+}
+
+// Q8_0 of K floats into LDS: each thread takes 4 consecutive values, 8
+// threads a 32-block. K % 32 == 0, x 16-byte aligned. With w: the rmsnorm
+// output (x * inv) * w is quantized.
 __device__ __forceinline__ void quantize_to_lds(const float *x, int K, int8_t *xs, float *xds,
                                                 const float *w = nullptr, float inv = 1.0f) {
     constexpr int B = 4;   // float4 loads in flight per thread
@@ -123,27 +130,53 @@ __device__ __forceinline__ void quantize_to_lds(const float *x, int K, int8_t *x
         }
 #pragma unroll
         for (int k = 0; k < B; k++) {
-        const int i = base + 4 * (k * MV_THREADS + threadIdx.x);   // K % 32 == 0: 8-lane groups all in or all out
-        if (i < K) {
-            float4 v = vs[k];
-            if (w)
-                v = make_float4(kr_fmul(kr_fmul(v.x, inv), ws[k].x), kr_fmul(kr_fmul(v.y, inv), ws[k].y),
-                                kr_fmul(kr_fmul(v.z, inv), ws[k].z), kr_fmul(kr_fmul(v.w, inv), ws[k].w));
-            float m = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
-            m = fmaxf(m, __shfl_xor(m, 1, 8));
-            m = fmaxf(m, __shfl_xor(m, 2, 8));
-            m = fmaxf(m, __shfl_xor(m, 4, 8));
-            int packed = 0;
-            float dd = 0.0f;
-            if (!(m < KR_QUANT_TINY)) {
-                const float id = kr_fdiv(127.0f, m);
-                dd = kr_fdiv(m, 127.0f);
-                packed = (kr_q8_elem(v.x, id) & 0xff) | (kr_q8_elem(v.y, id) & 0xff) << 8 |
-                         (kr_q8_elem(v.z, id) & 0xff) << 16 | (int)((unsigned)kr_q8_elem(v.w, id) << 24);
-            }
-            *(int *)(xs + i) = packed;
-            if ((i & 31) == 0) xds[i >> 5] = dd;
+            const int i = base + 4 * (k * MV_THREADS + threadIdx.x);   // K % 32 == 0: 8-lane groups all in or all out
+            if (i < K) kr_quant4(w ? kr_norm4(vs[k], inv, ws[k]) : vs[k], i, xs, xds, 1);
         }
+    }
+}
+
+// rmsnorm + Q8_0 of one row of n floats by the NT threads of a workgroup
+// (n <= NT * V4 * 4, n % 32 == 0, rows 16-byte aligned): every thread keeps
+// its float4 slices of x and w in registers; the squares x_i * x_i (each one
+// rounded product, as in the scalar loop) go to LDS (sq: sc_terms_cap(n)
+// floats and then sc_lds_bytes(n, NT) bytes) for the ordered sum
+// (k_scalar.c:59-64); then every thread forms (x * inv) * w for its values
+// and 8-thread groups quantize their 32-element blocks (k_scalar.c:39-57).
+// q[i] and d[(i / 32) * dstep] receive them, xb (nullable) the floats.
+constexpr int RN_THREADS = 256, RN_V4 = 16, RN_MAX = RN_THREADS * RN_V4 * 4;
+
+template <int NT, int V4>
+__device__ __forceinline__ void rmsnorm_q8_block(int8_t *q, float *d, size_t dstep, float *xb, const float *x,
+                                                 const float *w, int n, float eps, bool norm, float *sq) {
+    const int tid = threadIdx.x;
+    float4 xv[V4], wv[V4];
+#pragma unroll
+    for (int k = 0; k < V4; k++) {
+        const int i = min((k * NT + tid) * 4, n - 4);
+        xv[k] = *(const float4 *)(x + i);
+        if (norm) wv[k] = *(const float4 *)(w + i);
+    }
+    float inv = 1.0f;
+    if (norm) {
+#pragma unroll
+        for (int k = 0; k < V4; k++) {
+            const int i = (k * NT + tid) * 4;
+            if (i < n)
+                *(float4 *)(sq + i) = make_float4(kr_fmul(xv[k].x, xv[k].x), kr_fmul(xv[k].y, xv[k].y),
+                                                  kr_fmul(xv[k].z, xv[k].z), kr_fmul(xv[k].w, xv[k].w));
+        }
+        __syncthreads();
+        const float ss = kr_spec_sum<NT>(sq, n, (unsigned char *)(sq + sc_terms_cap(n)));
+        inv = kr_fdiv(1.0f, kr_fsqrt(kr_fadd(kr_fdiv(ss, (float)n), eps)));
+    }
+#pragma unroll
+    for (int k = 0; k < V4; k++) {
+        const int i = (k * NT + tid) * 4;
+        if (i < n) {   // n % 32 == 0: 8-thread groups are all in or all out
+            const float4 o = norm ? kr_norm4(xv[k], inv, wv[k]) : xv[k];
+            if (xb) *(float4 *)(xb + i) = o;
+            kr_quant4(o, i, q, d, dstep);
         }
     }
 }
@@ -209,6 +242,26 @@ __device__ __forceinline__ void mv_load(MvSlots &S, const MvArgs &a, const MvIte
     }
 }
 
+// LDS layout of k_matvec (byte offsets, every region 16-byte aligned): the
+// Q8_0 activation and its scales, two halves of chunk terms (rows of ts
+// floats: a multiple of 4 plus 4, for 16-byte reads with a 4-bank shift
+// between rows), the row sums, and for a normalizing launch the squares and
+// the ordered sum's scratch.
+struct MvLds {
+    int ts, xds, t2, sums, sq, total;
+};
+__host__ __device__ constexpr int mv_align16(int b) { return (b + 15) & ~15; }
+__host__ __device__ inline MvLds mv_lds(int K, int maxloc, int nbc, bool norm) {
+    MvLds l = {};
+    l.ts = (nbc + 3) / 4 * 4 + 4;
+    l.xds = mv_align16(K);
+    l.t2 = mv_align16(l.xds + 4 * (K / KR_QK));
+    l.sums = mv_align16(l.t2 + 4 * 2 * maxloc * l.ts);
+    l.sq = mv_align16(l.sums + 4 * maxloc);
+    l.total = norm ? l.sq + 4 * sc_terms_cap(K) + sc_lds_bytes(K, MV_THREADS) : l.sq;
+    return l;
+}
+
 // y rows [row0, row0 + R) of up to three matrices sharing the activation
 // (QKV), or the w1 and w3 rows [row0, row0 + R) (SwiGLU). A workgroup walks
 // work items (its row tiles blockIdx.x, + gridDim.x, ..., each split into
@@ -227,13 +280,13 @@ __global__ void __launch_bounds__(MV_THREADS, 2) k_matvec(const MvArgs a) {
     extern __shared__ __align__(16) unsigned char smem[];
     const int K = a.K, nb = K / KR_QK, tid = threadIdx.x, ntiles = a.tile0[a.nmat];
     const int maxloc = EPI == EPI_SWIGLU ? 2 * a.R : a.R;
-    const int ts = a.nbc + 4;   // term row stride: 16-byte rows, 4-bank shift between rows
+    const MvLds L = mv_lds(K, maxloc, a.nbc, a.nw != nullptr);
+    const int ts = L.ts;
     int8_t *xs = (int8_t *)smem;
-    float *xds = (float *)(smem + K);
-    float *t2 = xds + nb;                    // [2][maxloc][ts]
-    float *sums = t2 + 2 * maxloc * ts;      // [maxloc]
-    float *sq = sums + maxloc;               // K floats, rmsnorm prologue only
-    __shared__ float s_inv;
+    float *xds = (float *)(smem + L.xds);
+    float *t2 = (float *)(smem + L.t2);      // [2][maxloc][ts]
+    float *sums = (float *)(smem + L.sums);  // [maxloc]
+    float *sq = (float *)(smem + L.sq);      // rmsnorm prologue only: the squares, then the ordered sum's scratch
     if ((int)blockIdx.x >= ntiles) return;
     const int nch = (nb + a.nbc - 1) / a.nbc;
 
@@ -269,28 +322,57 @@ __global__ void __launch_bounds__(MV_THREADS, 2) k_matvec(const MvArgs a) {
 #pragma unroll
         for (int k = 0; k < MV_XQ_MAX / 32 / MV_THREADS; k++)
             if (tid + k * MV_THREADS < nb) xds[tid + k * MV_THREADS] = xdv[k];
+    } else if (!a.xq && K <= MV_XF_MAX) {
+        // a float activation (normalized first when nw is set), held in
+        // registers: its loads go out before the weight loads; the squares
+        // and the quantization read the registers
+        constexpr int XV = MV_XF_MAX / 4 / MV_THREADS;
+        float4 xv[XV], wv[XV];
+#pragma unroll
+        for (int k = 0; k < XV; k++) {
+            const int i = min(4 * (k * MV_THREADS + tid), K - 4);
+            xv[k] = *(const float4 *)(a.xf + i);
+            if (a.nw) wv[k] = *(const float4 *)(a.nw + i);
+        }
+#pragma unroll
+        for (int d = 0; d < MV_DEPTH - 1; d++) load_item(S[d], I[d]);
+        float inv = 1.0f;
+        if (a.nw) {
+#pragma unroll
+            for (int k = 0; k < XV; k++) {
+                const int i = 4 * (k * MV_THREADS + tid);
+                if (i < K)
+                    *(float4 *)(sq + i) = make_float4(kr_fmul(xv[k].x, xv[k].x), kr_fmul(xv[k].y, xv[k].y),
+                                                      kr_fmul(xv[k].z, xv[k].z), kr_fmul(xv[k].w, xv[k].w));
+            }
+            __syncthreads();
+            const float ss = kr_spec_sum<MV_THREADS>(sq, K, (unsigned char *)(sq + sc_terms_cap(K)));
+            inv = kr_fdiv(1.0f, kr_fsqrt(kr_fadd(kr_fdiv(ss, (float)K), a.eps)));
+        }
+#pragma unroll
+        for (int k = 0; k < XV; k++) {
+            const int i = 4 * (k * MV_THREADS + tid);   // K % 32 == 0: 8-lane groups all in or all out
+            if (i < K) kr_quant4(a.nw ? kr_norm4(xv[k], inv, wv[k]) : xv[k], i, xs, xds, 1);
+        }
     } else {
 #pragma unroll
         for (int d = 0; d < MV_DEPTH - 1; d++) load_item(S[d], I[d]);
-    }
-
-    if (a.xq) {
-        if (K > MV_XQ_MAX) {
+        if (a.xq) {
             for (int i = tid; i < K / 16; i += MV_THREADS) ((int4 *)xs)[i] = ((const int4 *)a.xq)[i];
             for (int i = tid; i < nb; i += MV_THREADS) xds[i] = a.xd[i];
+        } else if (a.nw) {
+            for (int i = 4 * tid; i < K; i += 4 * MV_THREADS) {
+                const float4 v = *(const float4 *)(a.xf + i);
+                *(float4 *)(sq + i) = make_float4(kr_fmul(v.x, v.x), kr_fmul(v.y, v.y), kr_fmul(v.z, v.z),
+                                                  kr_fmul(v.w, v.w));
+            }
+            __syncthreads();
+            const float ss = kr_spec_sum<MV_THREADS>(sq, K, (unsigned char *)(sq + sc_terms_cap(K)));
+            const float inv = kr_fdiv(1.0f, kr_fsqrt(kr_fadd(kr_fdiv(ss, (float)K), a.eps)));
+            quantize_to_lds(a.xf, K, xs, xds, a.nw, inv);
+        } else {
+            quantize_to_lds(a.xf, K, xs, xds);
         }
-    } else if (a.nw) {
-        for (int i = 4 * tid; i < K; i += 4 * MV_THREADS) {
-            const float4 v = *(const float4 *)(a.xf + i);
-            *(float4 *)(sq + i) = make_float4(kr_fmul(v.x, v.x), kr_fmul(v.y, v.y), kr_fmul(v.z, v.z),
-                                              kr_fmul(v.w, v.w));
-        }
-        __syncthreads();
-        if (tid == 0) s_inv = kr_fdiv(1.0f, kr_fsqrt(kr_fadd(kr_fdiv(kr_chain_lds(sq, K), (float)K), a.eps)));
-        __syncthreads();
-        quantize_to_lds(a.xf, K, xs, xds, a.nw, s_inv);
-    } else {
-        quantize_to_lds(a.xf, K, xs, xds);
     }
     __syncthreads();
 
@@ -430,7 +512,7 @@ void launch_mv(MvArgs &a, const KMat &W) {
     const int nb = a.K / KR_QK;
     const int nloc = EPI == EPI_SWIGLU ? 2 * a.R : a.R;
     a.nbc = mv_chunk(nb, nloc);
-    const size_t lds = (size_t)a.K + 4u * nb + 4u * 2 * (size_t)nloc * (a.nbc + 4) + 4u * nloc + (a.nw ? 4u * a.K : 0u);
+    const size_t lds = mv_lds(a.K, nloc, a.nbc, a.nw != nullptr).total;
     const int ntiles = a.tile0[a.nmat];
     const int grid = ntiles > MV_RESIDENT ? MV_RESIDENT : ntiles;
     if (a.K % KR_QK || lds > 64 * 1024 || grid <= 0 || nloc > 64 || nloc * a.nbc > MV_NPT * MV_THREADS ||
@@ -452,74 +534,14 @@ void launch_mv(MvArgs &a, const KMat &W) {
 // ---- rmsnorm + quantize, quantize ----
 
 // One workgroup per token; each thread keeps its float4 slices of x and w in
-// registers (n <= RN_MAX). The squares x_i * x_i (each one rounded product,
-// as in the scalar loop) go to LDS and lane 0 adds them in index order
-// (k_scalar.c:61); then every thread forms (x * inv) * w for its values and
-// 8-thread groups quantize their 32-element blocks (k_scalar.c:39-57).
-// n % 32 == 0; rows 16-byte aligned.
-constexpr int RN_THREADS = 256, RN_V4 = 16, RN_MAX = RN_THREADS * RN_V4 * 4;
-
-
+// registers (n <= RN_MAX); see rmsnorm_q8_block.
 __global__ void __launch_bounds__(RN_THREADS) k_rmsnorm_q8(int8_t *q, float *d, int dld, float *xb, const float *x,
                                                            const float *w, int n, float eps, int norm) {
     const size_t t = blockIdx.x;
-    const int tid = threadIdx.x;
-    x += t * n;
-    q += t * n;
     // scales [t][n / 32], or transposed [n / 32][dld] when dld > 0
-    const size_t dstep = dld > 0 ? (size_t)dld : 1;
-    d += dld > 0 ? t : t * (n / KR_QK);
-    if (xb) xb += t * n;
-    extern __shared__ __align__(16) float sq[];   // n floats when norm
-    __shared__ float s_inv;
-    float4 xv[RN_V4], wv[RN_V4];
-#pragma unroll
-    for (int k = 0; k < RN_V4; k++) {
-        const int i = (k * RN_THREADS + tid) * 4;
-        if (i < n) {
-            xv[k] = *(const float4 *)(x + i);
-            if (norm) wv[k] = *(const float4 *)(w + i);
-        }
-    }
-    float inv = 1.0f;
-    if (norm) {
-#pragma unroll
-        for (int k = 0; k < RN_V4; k++) {
-            const int i = (k * RN_THREADS + tid) * 4;
-            if (i < n)
-                *(float4 *)(sq + i) = make_float4(kr_fmul(xv[k].x, xv[k].x), kr_fmul(xv[k].y, xv[k].y),
-                                                  kr_fmul(xv[k].z, xv[k].z), kr_fmul(xv[k].w, xv[k].w));
-        }
-        __syncthreads();
-        if (tid == 0) s_inv = kr_fdiv(1.0f, kr_fsqrt(kr_fadd(kr_fdiv(kr_chain_lds(sq, n), (float)n), eps)));
-        __syncthreads();
-        inv = s_inv;
-    }
-#pragma unroll
-    for (int k = 0; k < RN_V4; k++) {
-        const int i = (k * RN_THREADS + tid) * 4;
-        if (i < n) {   // n % 32 == 0: 8-thread groups are all in or all out
-            float4 o = xv[k];
-            if (norm)
-                o = make_float4(kr_fmul(kr_fmul(o.x, inv), wv[k].x), kr_fmul(kr_fmul(o.y, inv), wv[k].y),
-                                kr_fmul(kr_fmul(o.z, inv), wv[k].z), kr_fmul(kr_fmul(o.w, inv), wv[k].w));
-            if (xb) *(float4 *)(xb + i) = o;
-            float m = fmaxf(fmaxf(fabsf(o.x), fabsf(o.y)), fmaxf(fabsf(o.z), fabsf(o.w)));
-            m = fmaxf(m, __shfl_xor(m, 1, 8));
-            m = fmaxf(m, __shfl_xor(m, 2, 8));
-            m = fmaxf(m, __shfl_xor(m, 4, 8));
-            int packed = 0;
-            float dd = 0.0f;
-            if (!(m < KR_QUANT_TINY)) {
-                const float id = kr_fdiv(127.0f, m);
-                dd = kr_fdiv(m, 127.0f);
-                packed = (kr_q8_elem(o.x, id) & 0xff) | (kr_q8_elem(o.y, id) & 0xff) << 8 |
-                         (kr_q8_elem(o.z, id) & 0xff) << 16 | (int)((unsigned)kr_q8_elem(o.w, id) << 24);
-            }
-            *(int *)(q + i) = packed;
-            if ((i & 31) == 0) d[(size_t)(i >> 5) * dstep] = dd;
-        }
-    }
+    extern __shared__ __align__(16) float rn_smem[];
+    rmsnorm_q8_block<RN_THREADS, RN_V4>(q + t * n, d + (dld > 0 ? t : t * (n / KR_QK)), dld > 0 ? (size_t)dld : 1,
+                                        xb ? xb + t * n : nullptr, x + t * n, w, n, eps, norm != 0, rn_smem);
 }
 
 // Q8_0 of ntok rows of n floats, QZ_CHUNK values per workgroup: thread t
@@ -838,26 +860,75 @@ __global__ void __launch_bounds__(64) k_attn_mix(float *ao, const float *att, co
 
 // First index of the maximum (model/sampler.c:57-61): NaN entries never win,
 // and a NaN at index 0 keeps 0, as the sequential loop does.
-__global__ void __launch_bounds__(1024) k_argmax(int *tok, const float *v, int n, int *pos, int *log) {
-    __shared__ float sv[16];
-    __shared__ int si[16];
-    float bv = -INFINITY;
-    int bi = INT_MAX;
-    for (int i = threadIdx.x; i < n; i += 1024) {
-        const float x = v[i];
-        if (x > bv || (bi == INT_MAX && x == bv)) { bv = x; bi = i; }
-    }
-    for (int o = 32; o >= 1; o >>= 1) {
-        const float ov = __shfl_xor(bv, o);
-        const int oi = __shfl_xor(bi, o);
-        if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
-    }
+// Greedy pick (model/sampler.c:57-61): the first index of the largest value,
+// NaNs never chosen, index 0 when v[0] is NaN or every value is NaN. Each
+// workgroup reduces a span of float4s (all its loads in flight together) to
+// (value, smallest index among equal values); the last workgroup to finish
+// (a counter it resets, so graph replays need no memset) reduces the
+// partials. The partials live in static device memory: calls that overlap on
+// one device race.
+constexpr int AM_THREADS = 256, AM_V4 = 4;   // float4s per thread
+constexpr int AM_MAX_WG = 1024;
+__device__ float g_am_v[AM_MAX_WG];
+__device__ int g_am_i[AM_MAX_WG];
+__device__ unsigned g_am_count;
+
+__device__ __forceinline__ void am_take(float &bv, int &bi, float v, int i) {
+    if (v > bv || (v == bv && i < bi)) { bv = v; bi = i; }
+}
+
+__device__ __forceinline__ void am_reduce_block(float &bv, int &bi, float *sv, int *si) {
+    for (int o = 32; o >= 1; o >>= 1) am_take(bv, bi, __shfl_xor(bv, o), __shfl_xor(bi, o));
     const int w = threadIdx.x >> 6;
     if ((threadIdx.x & 63) == 0) { sv[w] = bv; si[w] = bi; }
     __syncthreads();
+    if (threadIdx.x == 0)
+        for (int k = 1; k < AM_THREADS / 64; k++) am_take(bv, bi, sv[k], si[k]);
+}
+
+__global__ void __launch_bounds__(AM_THREADS) k_argmax(int *tok, const float *v, int n, int *pos, int *log) {
+    __shared__ float sv[AM_THREADS / 64];
+    __shared__ int si[AM_THREADS / 64];
+    __shared__ bool last;
+    float bv = -INFINITY;
+    int bi = INT_MAX;   // -inf with no index: any real value, -inf included, replaces it
+    const int n4 = n / 4;
+    const int base = blockIdx.x * AM_THREADS * AM_V4 + threadIdx.x;
+    float4 x[AM_V4];
+    if (n4 > 0) {
+#pragma unroll
+        for (int k = 0; k < AM_V4; k++) {
+            const int i = base + k * AM_THREADS;
+            x[k] = ((const float4 *)v)[min(i, n4 - 1)];
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < AM_V4; k++) {
+        const int i = base + k * AM_THREADS;
+        if (i < n4) {
+            am_take(bv, bi, x[k].x, 4 * i);
+            am_take(bv, bi, x[k].y, 4 * i + 1);
+            am_take(bv, bi, x[k].z, 4 * i + 2);
+            am_take(bv, bi, x[k].w, 4 * i + 3);
+        }
+    }
+    if (blockIdx.x == gridDim.x - 1 && threadIdx.x < n - 4 * n4) am_take(bv, bi, v[4 * n4 + threadIdx.x], 4 * n4 + threadIdx.x);
+    am_reduce_block(bv, bi, sv, si);
     if (threadIdx.x == 0) {
-        for (int k = 1; k < 16; k++)
-            if (sv[k] > bv || (sv[k] == bv && si[k] < bi)) { bv = sv[k]; bi = si[k]; }
+        g_am_v[blockIdx.x] = bv;
+        g_am_i[blockIdx.x] = bi;
+        __threadfence();
+        last = atomicAdd(&g_am_count, 1u) == gridDim.x - 1;
+    }
+    __syncthreads();
+    if (!last) return;
+    __threadfence();
+    bv = -INFINITY;
+    bi = INT_MAX;
+    for (int k = threadIdx.x; k < (int)gridDim.x; k += AM_THREADS) am_take(bv, bi, g_am_v[k], g_am_i[k]);
+    am_reduce_block(bv, bi, sv, si);
+    if (threadIdx.x == 0) {
+        g_am_count = 0;
         if (bi == INT_MAX || v[0] != v[0]) bi = 0;
         *tok = bi;
         if (pos) {
@@ -881,6 +952,13 @@ __global__ void k_math_batch(int op, float *y, const float *a, const float *b, s
     case KRH_MATH_RMS_INV: y[i] = kr_fdiv(1.0f, kr_fsqrt(kr_fadd(kr_fdiv(a[i], b[i]), 1e-5f))); break;
     default: y[i] = 0.0f;
     }
+}
+__global__ void __launch_bounds__(256) k_ordered_sum(float *out, const float *t, int n) {
+    extern __shared__ __align__(16) float os_t[];
+    for (int i = threadIdx.x; i < n; i += 256) os_t[i] = t[i];
+    __syncthreads();
+    const float s = kr_spec_sum<256>(os_t, n, (unsigned char *)(os_t + sc_terms_cap(n)));
+    if (threadIdx.x == 0) *out = s;
 }
 __global__ void k_h2f_batch(float *y, const uint16_t *h, size_t n) {
     const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -923,12 +1001,13 @@ extern "C" void krh_rmsnorm_q8(int8_t *q, float *d, float *xb, const float *x, c
 
 extern "C" void krh_rmsnorm_q8_t(int8_t *q, float *d, int dld, float *xb, const float *x, const float *w, int n,
                                  float eps, int ntok) {
-    if (n % KR_QK || n > RN_MAX || ntok <= 0 || (dld > 0 && dld < ntok)) {
+    // LDS: the squares and the ordered sum's scratch, within 64 KB
+    const size_t lds = sizeof(float) * (size_t)sc_terms_cap(n) + sc_lds_bytes(n, RN_THREADS);
+    if (n % KR_QK || n > RN_MAX || lds > 64 * 1024 || ntok <= 0 || (dld > 0 && dld < ntok)) {
         kr_fail(ML_E_SHAPE, "rmsnorm shape", hipSuccess);
         return;
     }
-    hipLaunchKernelGGL(k_rmsnorm_q8, dim3(ntok), dim3(RN_THREADS), sizeof(float) * (size_t)n, kr_stream(), q, d, dld,
-                       xb, x, w, n, eps, 1);
+    hipLaunchKernelGGL(k_rmsnorm_q8, dim3(ntok), dim3(RN_THREADS), lds, kr_stream(), q, d, dld, xb, x, w, n, eps, 1);
     kr_check_launch("rmsnorm_q8");
 }
 
@@ -1126,7 +1205,13 @@ extern "C" void krh_attention_batch(float *ao, float *att, const float *q, const
 }
 
 extern "C" void krh_argmax(int *tok, const float *logits, int n, int *pos, int *log) {
-    hipLaunchKernelGGL(k_argmax, dim3(1), dim3(1024), 0, kr_stream(), tok, logits, n, pos, log);
+    const int per_wg = AM_THREADS * AM_V4 * 4;
+    const int grid = (n + per_wg - 1) / per_wg;
+    if (n < 1 || grid > AM_MAX_WG) {
+        kr_fail(ML_E_SHAPE, "argmax size", hipSuccess);
+        return;
+    }
+    hipLaunchKernelGGL(k_argmax, dim3(grid), dim3(AM_THREADS), 0, kr_stream(), tok, logits, n, pos, log);
     kr_check_launch("argmax");
 }
 
@@ -1143,6 +1228,16 @@ extern "C" void krh_advance(int *pos) {
 extern "C" void krh_math_batch(int op, float *y, const float *a, const float *b, size_t n) {
     hipLaunchKernelGGL(k_math_batch, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, kr_stream(), op, y, a, b, n);
     kr_check_launch("math_batch");
+}
+
+extern "C" void krh_ordered_sum(float *out, const float *t, int n) {
+    if (n < 1 || n > KRH_ORDERED_SUM_MAX) {
+        kr_fail(ML_E_SHAPE, "ordered_sum size", hipSuccess);
+        return;
+    }
+    const size_t lds = sizeof(float) * (size_t)sc_terms_cap(n) + sc_lds_bytes(n, RN_THREADS);
+    hipLaunchKernelGGL(k_ordered_sum, dim3(1), dim3(256), lds, kr_stream(), out, t, n);
+    kr_check_launch("ordered_sum");
 }
 
 extern "C" void krh_h2f_batch(float *y, const uint16_t *h, size_t n) {

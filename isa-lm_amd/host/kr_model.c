@@ -245,20 +245,19 @@ static void issue_step(kr_state *s, int cls) {
         const ml_layer *L = &m->layers[l];
         float *kc = s->kcache + (size_t)l * lkv, *vc = s->vcache + (size_t)l * lkv;
         const float *cs = L->local_rope ? s->rope_cos_l : s->rope_cos, *sn = L->local_rope ? s->rope_sin_l : s->rope_sin;
-        krh_rmsnorm_q8(s->qa_dim, s->qd_dim, NULL, s->x, D->attn_norm, c->dim, c->norm_eps, 1);
-        krh_matvec_qkv(s->q, kc, vc, &D->wq, &D->wk, &D->wv, D->bq, D->bk, D->bv, s->qa_dim, s->qd_dim, cs, sn,
-                       c->head_dim, s->pos);
+        /* each norm runs inside the launch that consumes it, under that
+         * launch's first weight loads */
+        krh_rmsnorm_matvec_qkv(s->q, kc, vc, &D->wq, &D->wk, &D->wv, D->bq, D->bk, D->bv, s->x, D->attn_norm,
+                               c->norm_eps, cs, sn, c->head_dim, s->pos);
         krh_attention(s->ao, NULL, NULL, s->att, s->q, kc, vc, c->n_heads, c->n_kv_heads, c->head_dim,
                       c->max_seq, L->window, c->attn_scale, s->pos);
         krh_matvec_f(s->x, &D->wo, s->ao, 1);
-        krh_rmsnorm_q8(s->qa_dim, s->qd_dim, NULL, s->x, D->ffn_norm, c->dim, c->norm_eps, 1);
-        krh_matvec_swiglu(s->hb, &D->w1, &D->w3, s->qa_dim, s->qd_dim);
+        krh_rmsnorm_matvec_swiglu(s->hb, &D->w1, &D->w3, s->x, D->ffn_norm, c->norm_eps);
         krh_quantize_q8(s->qa_hid, s->qd_hid, s->hb, c->hidden_dim, 1);
         krh_matvec(s->x, &D->w2, s->qa_hid, s->qd_hid, 1);
     }
     if (!cls) return;
-    krh_rmsnorm_q8(s->qa_dim, s->qd_dim, NULL, s->x, m->d_final_norm, c->dim, c->norm_eps, 1);
-    krh_matvec(s->logits, &m->d_wcls, s->qa_dim, s->qd_dim, 0);
+    krh_rmsnorm_matvec(s->logits, &m->d_wcls, s->x, m->d_final_norm, c->norm_eps, 0);
 }
 
 enum { STEP_LOGITS = 0, STEP_GREEDY = 1, STEP_PREFILL = 2 };

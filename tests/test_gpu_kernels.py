@@ -319,23 +319,107 @@ def test_attention(dev, nh, nkv, hd, pos, window):
     assert np.array_equal(bits(ad.get(np.float32, qd // 32)), bits(d0))
 
 
-@pytest.mark.parametrize("case", ["ties", "neg_inf", "random", "nan0"])
-def test_argmax(dev, case):
-    n = 151936
+def seq_sum_f32(t):
+    """((0 + t0) + t1) + ... in float32, one rounding per add (the reference's
+    loop order, kernels/scalar/k_scalar.c:61, :71-74)"""
+    return np.add.accumulate(np.concatenate([[np.float32(0)], t]).astype(np.float32), dtype=np.float32)[-1]
+
+
+def test_seq_sum_f32_is_sequential():
+    t = f32(RNG.normal(0, 1, 300) ** 2)
+    s = np.float32(0)
+    for v in t:
+        s = np.float32(s + v)
+    assert bits(np.float32(seq_sum_f32(t))) == bits(s)
+
+
+ORDERED_CASES = ["squares", "heavy", "outliers", "absorb", "absorb_late", "tiny", "zeros", "exps", "mixed_sign",
+                 "nan", "inf", "huge"]
+
+
+@pytest.mark.parametrize("case", ORDERED_CASES)
+@pytest.mark.parametrize("n", [1, 5, 127, 128, 129, 2175, 4096, 8192])
+def test_ordered_sum(dev, case, n):
+    """the chunked speculative sum returns the bits of the sequential fp32 sum,
+    through its window hits, its per-chunk fallback (absorbed terms push the
+    true sum hundreds of ulps from the estimate) and its non-finite path"""
+    x = RNG.normal(0, 1, n)
+    if case == "squares":
+        t = f32(x) * f32(x)
+    elif case == "heavy":
+        t = f32(x / np.sqrt(np.abs(RNG.normal(0, 1, n)) + 0.05)) ** 2
+    elif case == "outliers":
+        x[RNG.random(n) < 0.01] *= 80
+        t = f32(x) ** 2
+    elif case == "absorb":
+        t = f32(np.ones(n))
+        t[0] = 1e8
+    elif case == "absorb_late":
+        t = f32(np.full(n, 0.75))
+        t[n // 3] = 3e7
+    elif case == "tiny":
+        t = f32(np.abs(x) * 1e-41)
+    elif case == "zeros":
+        t = f32(np.zeros(n))
+    elif case == "exps":
+        t = f32(np.exp(-8 * RNG.random(n)))
+    elif case == "mixed_sign":
+        t = f32(x * 100)
+    elif case == "nan":
+        t = f32(x * x)
+        t[n // 2] = np.nan
+    elif case == "inf":
+        t = f32(x * x)
+        t[n - 1] = np.inf
+    else:   # huge: the sum overflows to inf part-way
+        t = f32(np.full(n, 3e37))
+    t = f32(t)
+    out = dev.zeros(4)
+    K.hip.krh_ordered_sum(out.ptr, dev.put(t).ptr, n)
+    ok()
+    got = out.get(np.float32, 1)[0]
+    want = seq_sum_f32(t)
+    if np.isnan(want):
+        assert np.isnan(got)
+    else:
+        assert bits(np.float32(got)) == bits(np.float32(want)), (got, want)
+
+
+@pytest.mark.parametrize("case", ["random", "ties", "neg_inf", "nan0", "nans", "signed_zero", "tail_max", "all_nan"])
+@pytest.mark.parametrize("n", [151936, 128256, 32003, 4097, 5, 3, 1])
+def test_argmax(dev, case, n):
+    """model/sampler.c:57-61 on the device: first index of the maximum, NaNs
+    skipped, 0 when v[0] is NaN; repeated calls (the partials counter is
+    reset by the kernel itself)"""
     v = f32(RNG.normal(0, 1, n))
     if case == "ties":
         v[:] = 0
-        v[40000] = v[9] = v[150000] = 3.0
+        for i in (40000, 9, 150000, n - 1):
+            if i < n:
+                v[i] = 3.0
     elif case == "neg_inf":
         v[:] = -np.inf
     elif case == "nan0":
         v[0] = np.nan
-    tb, pb, lb = dev.zeros(4), dev.put(np.array([5], np.int32)), dev.zeros(4 * 16)
-    K.hip.krh_argmax(tb.ptr, dev.put(v).ptr, n, pb.ptr, lb.ptr)
-    ok()
+    elif case == "nans":
+        v[RNG.integers(0, n, max(1, n // 7))] = np.nan
+        v[0] = 1.0
+    elif case == "signed_zero":
+        v[:] = -1.0
+        v[n // 2] = -0.0
+        v[n - 1] = 0.0
+    elif case == "tail_max":
+        v[n - 1] = 50.0
+    elif case == "all_nan":
+        v[:] = np.nan
     want = oracle.kro_argmax(v.ctypes.data, n)
-    assert tb.get(np.int32, 1)[0] == want
-    assert pb.get(np.int32, 1)[0] == 6 and lb.get(np.int32, 16)[6] == want
+    vb = dev.put(v)
+    for rep in range(3):
+        tb, pb, lb = dev.zeros(4), dev.put(np.array([5 + rep], np.int32)), dev.zeros(4 * 16)
+        K.hip.krh_argmax(tb.ptr, vb.ptr, n, pb.ptr, lb.ptr)
+        ok()
+        assert tb.get(np.int32, 1)[0] == want
+        assert pb.get(np.int32, 1)[0] == 6 + rep and lb.get(np.int32, 16)[6 + rep] == want
 
 
 @pytest.mark.parametrize("typ,d16,scale", [(K.ML_Q8_0, 0, 1.0), (K.ML_Q4_0, 1, 1.0), (K.ML_Q8_0, 1, 8.0)])
