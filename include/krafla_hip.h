@@ -201,11 +201,11 @@ void krh_h2f_batch(float *y, const uint16_t *h, size_t n);
 /* s[r*nb+b]: int32 block dots of rows [0, rows) (the exact integer part of
  * the matvec) */
 void krh_block_dots(int32_t *s, const krh_mat *W, const int8_t *xq);
-/* *out = ((0 + t[0]) + t[1]) + ... + t[n-1] in fp32, as the rmsnorm and
+/* *out = ((s0 + t[0]) + t[1]) + ... + t[n-1] in fp32, as the rmsnorm and
  * softmax kernels compute their ordered sums (chunked speculation with an
  * exact fallback); n <= KRH_ORDERED_SUM_MAX */
 enum { KRH_ORDERED_SUM_MAX = 8192 };
-void krh_ordered_sum(float *out, const float *t, int n);
+void krh_ordered_sum(float *out, const float *t, int n, float s0);
 
 #ifdef __cplusplus
 }

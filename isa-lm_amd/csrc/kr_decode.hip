@@ -52,8 +52,8 @@ struct MvArgs {
 
 constexpr int MV_THREADS = 256;
 constexpr int MV_NPT = 4;   // weight blocks per thread per work item
-constexpr int MV_DEPTH = 2;    // work items in flight per workgroup (the one in use included): a wave that
-                               // issues more loads than the memory pipeline holds stalls at issue
+constexpr int MV_DEPTH = 2;    // work items in flight per wave: a wave that issues more loads than the
+                               // memory pipeline holds stalls at issue
 constexpr int MV_XQ_MAX = 16384;   // quantized activations up to this length are staged from registers
 constexpr int MV_XF_MAX = 8192;    // float activations up to this length are normalized and quantized from registers
 
@@ -181,11 +181,11 @@ __device__ __forceinline__ void rmsnorm_q8_block(int8_t *q, float *d, size_t dst
     }
 }
 
-// Loads of one work item (row tile, block chunk): slot k of thread tid is
-// local block tid + k * MV_THREADS of the item, blocks fastest, so each wave
-// reads contiguous spans (a Q8_0 block as two 16-byte loads, a Q4_0 block as
-// one). Every slot loads (slots past the item re-read its first block and are
-// not used), so no load waits on a branch.
+// Loads of one work item (row tile, block chunk) by one wave: slot k of lane
+// l is local block l + 64 k of the item, blocks fastest, so each load
+// instruction reads contiguous spans (a Q8_0 block as two 16-byte loads, a
+// Q4_0 block as one). Every slot loads (slots past the item re-read its first
+// block and are not used), so no load waits on a branch.
 struct MvSlots {
     int4 w0[MV_NPT], w1[MV_NPT];
     uint32_t wd[MV_NPT];   // raw scale bits: widened at use, after every load is in flight
@@ -199,12 +199,15 @@ struct MvItem {
 
 template <int EPI>
 __device__ __forceinline__ MvItem mv_item(const MvArgs &a, int tile, int chunk, int nb) {
+    // constant indices only: a runtime index into the argument block makes
+    // the compiler read it with a vector load, whose wait would drain the
+    // weight loads in flight
     MvItem it;
     it.mi = 0;
     if (EPI != EPI_SWIGLU)
-        while (it.mi + 1 < a.nmat && tile >= a.tile0[it.mi + 1]) it.mi++;
+        it.mi = (a.nmat > 1 && tile >= a.tile0[1]) + (a.nmat > 2 && tile >= a.tile0[2]);
     const int rows = pick3(it.mi, a.m[0].rows, a.m[1].rows, a.m[2].rows);
-    it.row0 = (tile - a.tile0[it.mi]) * a.R;
+    it.row0 = (tile - pick3(it.mi, a.tile0[0], a.tile0[1], a.tile0[2])) * a.R;
     it.nr = min(a.R, rows - it.row0);
     it.nloc = EPI == EPI_SWIGLU ? 2 * it.nr : it.nr;
     it.c0 = chunk * a.nbc;
@@ -213,15 +216,15 @@ __device__ __forceinline__ MvItem mv_item(const MvArgs &a, int tile, int chunk, 
 }
 
 template <int EPI, int QT, int D16>
-__device__ __forceinline__ void mv_load(MvSlots &S, const MvArgs &a, const MvItem &it, int nb) {
+__device__ __forceinline__ void mv_load(MvSlots &S, const MvArgs &a, const MvItem &it, int nb, int lane) {
     const KMat W = pick3(it.mi, a.m[0], a.m[1], a.m[2]);
     const KMat W2 = a.m[1];
-    const int tid = threadIdx.x, n = it.nloc * it.nbc;
-    int lr = tid / it.nbc, b = tid - lr * it.nbc;
-    const int sr = MV_THREADS / it.nbc, sb = MV_THREADS - sr * it.nbc;
+    const int n = it.nloc * it.nbc;
+    int lr = lane / it.nbc, b = lane - lr * it.nbc;
+    const int sr = 64 / it.nbc, sb = 64 - sr * it.nbc;
 #pragma unroll
     for (int k = 0; k < MV_NPT; k++) {
-        const bool in = tid + k * MV_THREADS < n;
+        const bool in = lane + k * 64 < n;
         const bool second = EPI == EPI_SWIGLU && in && lr >= it.nr;
         const uint8_t *q = second ? W2.q : W.q;
         const void *d = second ? W2.d : W.d;
@@ -243,10 +246,11 @@ __device__ __forceinline__ void mv_load(MvSlots &S, const MvArgs &a, const MvIte
 }
 
 // LDS layout of k_matvec (byte offsets, every region 16-byte aligned): the
-// Q8_0 activation and its scales, two halves of chunk terms (rows of ts
-// floats: a multiple of 4 plus 4, for 16-byte reads with a 4-bank shift
-// between rows), the row sums, and for a normalizing launch the squares and
-// the ordered sum's scratch.
+// Q8_0 activation and its scales, each wave's chunk terms (rows of ts floats:
+// a multiple of 4 plus 4, for 16-byte reads with a 4-bank shift between
+// rows) and row sums, and for a normalizing launch the squares and the
+// ordered sum's scratch.
+constexpr int MV_WAVES = MV_THREADS / 64;
 struct MvLds {
     int ts, xds, t2, sums, sq, total;
 };
@@ -256,57 +260,72 @@ __host__ __device__ inline MvLds mv_lds(int K, int maxloc, int nbc, bool norm) {
     l.ts = (nbc + 3) / 4 * 4 + 4;
     l.xds = mv_align16(K);
     l.t2 = mv_align16(l.xds + 4 * (K / KR_QK));
-    l.sums = mv_align16(l.t2 + 4 * 2 * maxloc * l.ts);
-    l.sq = mv_align16(l.sums + 4 * maxloc);
+    l.sums = mv_align16(l.t2 + 4 * MV_WAVES * maxloc * l.ts);
+    l.sq = mv_align16(l.sums + 4 * MV_WAVES * maxloc);
     l.total = norm ? l.sq + 4 * sc_terms_cap(K) + sc_lds_bytes(K, MV_THREADS) : l.sq;
     return l;
 }
 
+// Orders one wave's LDS writes before its later reads for the compiler (a
+// wave's LDS operations execute in order).
+__device__ __forceinline__ void kr_wave_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 // y rows [row0, row0 + R) of up to three matrices sharing the activation
-// (QKV), or the w1 and w3 rows [row0, row0 + R) (SwiGLU). A workgroup walks
-// work items (its row tiles blockIdx.x, + gridDim.x, ..., each split into
-// chunks of nbc blocks), and issues the loads of item i + 1 before it uses
-// item i's: the weight stream never stops for the dots or the ordered sums.
-// Per item: the exact int32 block dots and their terms ((float)s * wd) * xd
-// go to one half of a double LDS buffer; after a barrier, one lane per row
-// continues its row's ordered sum over the chunk's terms, in block order
-// (kernels/scalar/k_scalar.c:13, :34), while the other waves go on to the
-// next item's dots. On a tile's last chunk the sums go through the epilogue.
-// Before the first item's dots the activation is staged into LDS (while the
-// first loads are in flight): copied, quantized, or normalized first
-// (rmsnorm's ordered sum by one lane, k_scalar.c:59-64) and quantized.
+// (QKV), or the w1 and w3 rows [row0, row0 + R) (SwiGLU). Each wave streams
+// its own row tiles (tiles gw, gw + GW, ... of the GW waves of the grid),
+// each split into chunks of nbc blocks, and issues the loads of item i + 1
+// before it uses item i's; waves never wait for each other, so the weight
+// stream never stops for the dots, the ordered sums or the epilogues. Per
+// item: the exact int32 block dots and their terms ((float)s * wd) * xd go to
+// the wave's LDS rows; one lane per row continues its row's ordered sum over
+// the chunk's terms, in block order (kernels/scalar/k_scalar.c:13, :34). On a
+// tile's last chunk the sums go through the epilogue. Before the first item's
+// dots the workgroup stages the activation into LDS (while the first loads
+// are in flight): copied, quantized, or normalized first (rmsnorm's ordered
+// sum, k_scalar.c:59-64) and quantized.
 template <int EPI, int QT, int D16>
 __global__ void __launch_bounds__(MV_THREADS, 2) k_matvec(const MvArgs a) {
     extern __shared__ __align__(16) unsigned char smem[];
-    const int K = a.K, nb = K / KR_QK, tid = threadIdx.x, ntiles = a.tile0[a.nmat];
+    const int K = a.K, nb = K / KR_QK, tid = threadIdx.x;
+    const int ntiles = a.nmat == 1 ? a.tile0[1] : a.nmat == 2 ? a.tile0[2] : a.tile0[3];
+    const int lane = tid & 63, wave = tid >> 6;
+    const int gw = blockIdx.x * MV_WAVES + wave, GW = gridDim.x * MV_WAVES;   // this wave; waves in the grid
+    const int pos = EPI == EPI_QKV ? *a.pos : 0;
     const int maxloc = EPI == EPI_SWIGLU ? 2 * a.R : a.R;
     const MvLds L = mv_lds(K, maxloc, a.nbc, a.nw != nullptr);
     const int ts = L.ts;
     int8_t *xs = (int8_t *)smem;
     float *xds = (float *)(smem + L.xds);
-    float *t2 = (float *)(smem + L.t2);      // [2][maxloc][ts]
-    float *sums = (float *)(smem + L.sums);  // [maxloc]
+    float *T = (float *)(smem + L.t2) + wave * maxloc * ts;   // this wave's terms [maxloc][ts]
+    float *sums = (float *)(smem + L.sums) + wave * maxloc;   // and row sums
     float *sq = (float *)(smem + L.sq);      // rmsnorm prologue only: the squares, then the ordered sum's scratch
-    if ((int)blockIdx.x >= ntiles) return;
+    if ((int)blockIdx.x * MV_WAVES >= ntiles) return;
     const int nch = (nb + a.nbc - 1) / a.nbc;
 
     // items are loaded MV_DEPTH - 1 ahead of the one whose dots run: S[P]
     // holds item P of every MV_DEPTH; (ltile, lchunk) is the next item to load
-    int tile = blockIdx.x, chunk = 0, ltile = blockIdx.x, lchunk = 0;
+    int tile = gw, chunk = 0, ltile = gw, lchunk = 0;
     auto next_item = [&](int &t, int &c) {
-        if (++c == nch) { c = 0; t += gridDim.x; }
+        if (++c == nch) { c = 0; t += GW; }
     };
     auto load_item = [&](MvSlots &dst, MvItem &it) {
-        // past the last item: reload the last tile's chunk (not used)
+        // past the last item: an item of no rows, whose slots all read one
+        // block (not used), so the prefetch beyond the end costs one line
         it = mv_item<EPI>(a, min(ltile, ntiles - 1), ltile < ntiles ? lchunk : 0, nb);
-        mv_load<EPI, QT, D16>(dst, a, it, nb);
+        it.nloc = ltile < ntiles ? it.nloc : 0;
+        mv_load<EPI, QT, D16>(dst, a, it, nb, lane);
         next_item(ltile, lchunk);
     };
     MvSlots S[MV_DEPTH];
     MvItem I[MV_DEPTH];
     if (a.xq && K <= MV_XQ_MAX) {
-        // a quantized activation: its loads go out before the weight loads,
-        // so storing it to LDS waits on it alone
+        // a quantized activation (just written by the previous launch, so
+        // not yet in this die's L2): it is read and stored to LDS before the
+        // weight stream starts, so it never queues behind it
         int4 xv[MV_XQ_MAX / 16 / MV_THREADS];
         float xdv[MV_XQ_MAX / 32 / MV_THREADS];
 #pragma unroll
@@ -315,13 +334,13 @@ __global__ void __launch_bounds__(MV_THREADS, 2) k_matvec(const MvArgs a) {
 #pragma unroll
         for (int k = 0; k < MV_XQ_MAX / 32 / MV_THREADS; k++) xdv[k] = a.xd[min(tid + k * MV_THREADS, nb - 1)];
 #pragma unroll
-        for (int d = 0; d < MV_DEPTH - 1; d++) load_item(S[d], I[d]);
-#pragma unroll
         for (int k = 0; k < MV_XQ_MAX / 16 / MV_THREADS; k++)
             if (tid + k * MV_THREADS < K / 16) ((int4 *)xs)[tid + k * MV_THREADS] = xv[k];
 #pragma unroll
         for (int k = 0; k < MV_XQ_MAX / 32 / MV_THREADS; k++)
             if (tid + k * MV_THREADS < nb) xds[tid + k * MV_THREADS] = xdv[k];
+#pragma unroll
+        for (int d = 0; d < MV_DEPTH - 1; d++) load_item(S[d], I[d]);
     } else if (!a.xq && K <= MV_XF_MAX) {
         // a float activation (normalized first when nw is set), held in
         // registers: its loads go out before the weight loads; the squares
@@ -334,10 +353,10 @@ __global__ void __launch_bounds__(MV_THREADS, 2) k_matvec(const MvArgs a) {
             xv[k] = *(const float4 *)(a.xf + i);
             if (a.nw) wv[k] = *(const float4 *)(a.nw + i);
         }
-#pragma unroll
-        for (int d = 0; d < MV_DEPTH - 1; d++) load_item(S[d], I[d]);
         float inv = 1.0f;
         if (a.nw) {
+            // the squares wait on x alone; the weight stream then runs under
+            // the ordered sum
 #pragma unroll
             for (int k = 0; k < XV; k++) {
                 const int i = 4 * (k * MV_THREADS + tid);
@@ -345,6 +364,8 @@ __global__ void __launch_bounds__(MV_THREADS, 2) k_matvec(const MvArgs a) {
                     *(float4 *)(sq + i) = make_float4(kr_fmul(xv[k].x, xv[k].x), kr_fmul(xv[k].y, xv[k].y),
                                                       kr_fmul(xv[k].z, xv[k].z), kr_fmul(xv[k].w, xv[k].w));
             }
+#pragma unroll
+            for (int d = 0; d < MV_DEPTH - 1; d++) load_item(S[d], I[d]);
             __syncthreads();
             const float ss = kr_spec_sum<MV_THREADS>(sq, K, (unsigned char *)(sq + sc_terms_cap(K)));
             inv = kr_fdiv(1.0f, kr_fsqrt(kr_fadd(kr_fdiv(ss, (float)K), a.eps)));
@@ -353,6 +374,10 @@ __global__ void __launch_bounds__(MV_THREADS, 2) k_matvec(const MvArgs a) {
         for (int k = 0; k < XV; k++) {
             const int i = 4 * (k * MV_THREADS + tid);   // K % 32 == 0: 8-lane groups all in or all out
             if (i < K) kr_quant4(a.nw ? kr_norm4(xv[k], inv, wv[k]) : xv[k], i, xs, xds, 1);
+        }
+        if (!a.nw) {
+#pragma unroll
+            for (int d = 0; d < MV_DEPTH - 1; d++) load_item(S[d], I[d]);
         }
     } else {
 #pragma unroll
@@ -376,23 +401,38 @@ __global__ void __launch_bounds__(MV_THREADS, 2) k_matvec(const MvArgs a) {
     }
     __syncthreads();
 
-    float acc = 0.0f;   // row sum of lane tid < nloc of wave 0
-    // one item: S[P] holds it; S[P ^ 1] receives the next one's loads
+    float acc = 0.0f;   // row sum of lane < nloc
+    // one item: S[P] holds it; S[P - 1] receives the loads MV_DEPTH - 1 ahead
     auto step = [&](auto P_) -> bool {
         constexpr int P = decltype(P_)::value;
-        load_item(S[(P + MV_DEPTH - 1) % MV_DEPTH], I[(P + MV_DEPTH - 1) % MV_DEPTH]);
         const MvItem cur = I[P];
+        load_item(S[(P + MV_DEPTH - 1) % MV_DEPTH], I[(P + MV_DEPTH - 1) % MV_DEPTH]);
         int ntile = tile, nchunk = chunk;
         next_item(ntile, nchunk);
-
-        float *T = t2 + (P & 1) * maxloc * ts;
+        // the epilogue's inputs for this tile's rows, read before this
+        // step's item loads go out, so the epilogue waits on them alone;
+        // every lane reads (a clamped row; a missing bias reads the RoPE
+        // table and is not used): no load sits in a branch
+        float ep0 = 0.0f, ep1 = 0.0f, ep2 = 0.0f;
         {
-            int lr = tid / cur.nbc, b = tid - lr * cur.nbc;
-            const int sr = MV_THREADS / cur.nbc, sb = MV_THREADS - sr * cur.nbc;
+            const int row = cur.row0 + min(lane, cur.nr - 1);
+            if (EPI == EPI_ADD) ep0 = pick3(cur.mi, a.y[0], a.y[1], a.y[2])[row];
+            if (EPI == EPI_QKV) {
+                const float *bias = pick3(cur.mi, a.bias[0], a.bias[1], a.bias[2]);
+                ep0 = *(bias ? bias + row : a.rope_cos);
+                const int hd = a.head_dim, h2 = hd >> 1, j = row % hd;
+                ep1 = a.rope_cos[(size_t)pos * h2 + (j >> 1)];
+                ep2 = a.rope_sin[(size_t)pos * h2 + (j >> 1)];
+            }
+        }
+
+        {
+            int lr = lane / cur.nbc, b = lane - lr * cur.nbc;
+            const int sr = 64 / cur.nbc, sb = 64 - sr * cur.nbc;
             const int n = cur.nloc * cur.nbc;
 #pragma unroll
             for (int k = 0; k < MV_NPT; k++) {
-                if (tid + k * MV_THREADS < n) {
+                if (lane + k * 64 < n) {
                     const int bb = cur.c0 + b;
                     const int sdot = block_dot<QT>(S[P].w0[k], S[P].w1[k], xs + bb * 32);
                     const float sc = D16 ? kr_h2f((uint16_t)S[P].wd[k]) : __uint_as_float(S[P].wd[k]);
@@ -403,10 +443,10 @@ __global__ void __launch_bounds__(MV_THREADS, 2) k_matvec(const MvArgs a) {
                 if (b >= cur.nbc) { b -= cur.nbc; lr++; }
             }
         }
-        __syncthreads();
-        if (tid < cur.nloc) {
+        kr_wave_sync();
+        if (lane < cur.nloc) {
             if (chunk == 0) acc = 0.0f;
-            const float *p = T + tid * ts;
+            const float *p = T + lane * ts;
             int j = 0;
             for (; j + 32 <= cur.nbc; j += 32) {
                 float4 r[8];
@@ -423,47 +463,42 @@ __global__ void __launch_bounds__(MV_THREADS, 2) k_matvec(const MvArgs a) {
             for (; j < cur.nbc; j++) acc = kr_fadd(acc, p[j]);
         }
         if (nchunk == 0) {   // the tile's last chunk: epilogue
-            if (tid < cur.nloc) sums[tid] = acc;
-            __syncthreads();
+            if (lane < cur.nloc) sums[lane] = acc;
+            kr_wave_sync();
             const int mi = cur.mi, row0 = cur.row0, nr = cur.nr;
             if (EPI == EPI_STORE) {
-                if (tid < nr) pick3(mi, a.y[0], a.y[1], a.y[2])[row0 + tid] = sums[tid];
+                if (lane < nr) pick3(mi, a.y[0], a.y[1], a.y[2])[row0 + lane] = sums[lane];
             } else if (EPI == EPI_ADD) {
-                if (tid < nr) {
-                    float *y = pick3(mi, a.y[0], a.y[1], a.y[2]) + row0 + tid;
-                    *y = kr_fadd(*y, sums[tid]);
-                }
+                if (lane < nr) pick3(mi, a.y[0], a.y[1], a.y[2])[row0 + lane] = kr_fadd(ep0, sums[lane]);
             } else if (EPI == EPI_QKV) {
                 // bias (model/transformer.c:276-277), then RoPE on q and k
                 // (k_scalar.c:79-94: pairs 2i, 2i+1 of each head, unfused)
                 const float *bias = pick3(mi, a.bias[0], a.bias[1], a.bias[2]);
                 float v = 0.0f;
-                if (tid < nr) {
-                    v = sums[tid];
-                    if (bias) v = kr_fadd(v, bias[row0 + tid]);
+                if (lane < nr) {
+                    v = sums[lane];
+                    if (bias) v = kr_fadd(v, ep0);
                 }
-                __syncthreads();
-                if (tid < nr) sums[tid] = v;
-                __syncthreads();
-                if (tid < nr) {
-                    const int row = row0 + tid, pos = *a.pos;
+                kr_wave_sync();
+                if (lane < nr) sums[lane] = v;
+                kr_wave_sync();
+                if (lane < nr) {
+                    const int row = row0 + lane;
                     float o = v;
                     if (mi < 2) {
-                        const int hd = a.head_dim, j = row % hd, h2 = hd >> 1;
-                        const float c = a.rope_cos[(size_t)pos * h2 + (j >> 1)],
-                                    sn = a.rope_sin[(size_t)pos * h2 + (j >> 1)];
-                        const float pa = sums[tid & ~1], pb = sums[tid | 1];
-                        o = (j & 1) == 0 ? kr_fsub(kr_fmul(pa, c), kr_fmul(pb, sn))
-                                         : kr_fadd(kr_fmul(pa, sn), kr_fmul(pb, c));
+                        const float c = ep1, sn = ep2;
+                        const float pa = sums[lane & ~1], pb = sums[lane | 1];
+                        o = (lane & 1) == 0 ? kr_fsub(kr_fmul(pa, c), kr_fmul(pb, sn))
+                                            : kr_fadd(kr_fmul(pa, sn), kr_fmul(pb, c));
                     }
                     if (mi == 0) a.y[0][row] = o;
                     else pick3(mi, a.y[0], a.y[1], a.y[2])[(size_t)pos * a.ld_cache + row] = o;
                 }
             } else if (EPI == EPI_SWIGLU) {
                 // g = g / (1 + expf(-g)) * u (k_scalar.c:96-98)
-                if (tid < nr) {
-                    const float h1 = sums[tid], h3 = sums[nr + tid];
-                    a.y[0][row0 + tid] = kr_fmul(kr_fdiv(h1, kr_fadd(1.0f, kr_expf(-h1))), h3);
+                if (lane < nr) {
+                    const float h1 = sums[lane], h3 = sums[nr + lane];
+                    a.y[0][row0 + lane] = kr_fmul(kr_fdiv(h1, kr_fadd(1.0f, kr_expf(-h1))), h3);
                 }
             }
         }
@@ -471,7 +506,8 @@ __global__ void __launch_bounds__(MV_THREADS, 2) k_matvec(const MvArgs a) {
         chunk = nchunk;
         return tile < ntiles;
     };
-    static_assert(MV_DEPTH == 2 || MV_DEPTH == 4, "LDS halves alternate with the item parity");
+    static_assert(MV_DEPTH == 2 || MV_DEPTH == 4, "the step loop is unrolled by 2 or 4");
+    if (gw >= ntiles) return;   // a wave with no tile (after the workgroup's one barrier)
     if (MV_DEPTH == 2) {
         while (step(std::integral_constant<int, 0>()) && step(std::integral_constant<int, 1>() )) {
         }
@@ -482,16 +518,22 @@ __global__ void __launch_bounds__(MV_THREADS, 2) k_matvec(const MvArgs a) {
     }
 }
 
-// Rows per tile: the largest power of two (at most cap, even for the RoPE
-// pairs) that still gives MV_MIN_TILES tiles; blocks per chunk: as many as
-// MV_NPT slots per thread allow (a multiple of 4, for the 16-byte term reads).
+// workgroups resident at once: two per compute unit
+constexpr int MV_RESIDENT = 512;
+
+// Rows per tile (one wave's): the largest power of two (at most cap, even for
+// the RoPE pairs) that still gives every resident wave a tile; blocks per
+// chunk: as many as MV_NPT slots per lane allow (a multiple of 4, for the
+// 16-byte term reads).
 int g_mv_rows_override = 0;   // krh_tune(KRH_TUNE_MV_ROWS, R): fixed rows per tile
-constexpr int MV_MIN_TILES = 512;
+constexpr int MV_MIN_TILES = MV_RESIDENT * MV_WAVES;
+constexpr int MV_MAX_LOC = 8;   // local rows per tile: a row's chunk then spans >= 32 blocks (1 KB of Q8_0)
 
 int mv_rows(int K, int total_rows, int local_per_row, int cap) {
     (void)K;
     int R = g_mv_rows_override > 0 ? g_mv_rows_override : cap / local_per_row;
     if (R * local_per_row > 64) R = 64 / local_per_row;
+    if (g_mv_rows_override <= 0 && R * local_per_row > MV_MAX_LOC) R = MV_MAX_LOC / local_per_row;
     if (g_mv_rows_override <= 0)
         while (R > 2 && (total_rows + R - 1) / R < MV_MIN_TILES) R /= 2;
     if (R > 1) R &= ~1;
@@ -499,13 +541,10 @@ int mv_rows(int K, int total_rows, int local_per_row, int cap) {
 }
 
 int mv_chunk(int nb, int nloc) {
-    int c = (MV_NPT * MV_THREADS / nloc) & ~3;
+    int c = (MV_NPT * 64 / nloc) & ~3;
     if (c < 4) c = 4;
     return c < nb ? c : nb;
 }
-
-// workgroups resident at once: two per compute unit
-constexpr int MV_RESIDENT = 512;
 
 template <int EPI>
 void launch_mv(MvArgs &a, const KMat &W) {
@@ -514,8 +553,9 @@ void launch_mv(MvArgs &a, const KMat &W) {
     a.nbc = mv_chunk(nb, nloc);
     const size_t lds = mv_lds(a.K, nloc, a.nbc, a.nw != nullptr).total;
     const int ntiles = a.tile0[a.nmat];
-    const int grid = ntiles > MV_RESIDENT ? MV_RESIDENT : ntiles;
-    if (a.K % KR_QK || lds > 64 * 1024 || grid <= 0 || nloc > 64 || nloc * a.nbc > MV_NPT * MV_THREADS ||
+    const int wgs = (ntiles + MV_WAVES - 1) / MV_WAVES;
+    const int grid = wgs > MV_RESIDENT ? MV_RESIDENT : wgs;
+    if (a.K % KR_QK || lds > 64 * 1024 || grid <= 0 || nloc > 64 || nloc * a.nbc > MV_NPT * 64 ||
         (!a.xq && !a.xf)) {
         kr_fail(ML_E_SHAPE, "matvec shape", hipSuccess);
         return;
@@ -645,18 +685,34 @@ __global__ void __launch_bounds__(AT_THREADS) k_attn_scores(float *att, const fl
     }
 }
 
-// Softmax of one head's n scores in place, AT_CHUNK at a time through LDS.
-constexpr int AT_CHUNK = 8192;
+// Softmax of one head's n scores in place (k_scalar.c:66-77): the max, the
+// exponentials x - max, their ordered sum (kr_spec_sum: the sequential
+// loop's bits), x * (1 / sum). Up to AT_CHUNK scores stay in registers
+// between one batched read and one write (every load issued at once, from an
+// index clamped into the row); longer rows go AT_CHUNK at a time through LDS,
+// the sum continuing from chunk to chunk.
+constexpr int AT_CHUNK = 8192, AT_V = AT_CHUNK / AT_THREADS;
 __global__ void __launch_bounds__(AT_THREADS) k_attn_softmax(float *att, int max_seq, int window, const int *pos_p) {
-    __shared__ __align__(16) float es[AT_CHUNK];
+    __shared__ __align__(16) float es[sc_terms_cap(AT_CHUNK)];
+    __shared__ __align__(16) unsigned char scr[sc_lds_bytes(AT_CHUNK, AT_THREADS)];
     __shared__ float red[AT_THREADS / 64];
-    __shared__ float s_inv;
+    __shared__ uint64_t xtab[32];   // expf's table
     int first, n;
     attn_range(pos_p, window, &first, &n);
     float *a = att + ((size_t)blockIdx.z * gridDim.x + blockIdx.x) * max_seq;
     const int tid = threadIdx.x;
+    if (tid < 32) xtab[tid] = kr_exp2_tab[tid];
+    const bool fits = n <= AT_CHUNK;
+    float v[AT_V];
     float m = -INFINITY;
-    for (int t = tid; t < n; t += AT_THREADS) m = fmaxf(m, a[t]);
+    if (fits) {
+#pragma unroll
+        for (int k = 0; k < AT_V; k++) v[k] = a[min(k * AT_THREADS + tid, n - 1)];
+#pragma unroll
+        for (int k = 0; k < AT_V; k++) m = fmaxf(m, v[k]);   // clamped repeats change no max
+    } else {
+        for (int t = tid; t < n; t += AT_THREADS) m = fmaxf(m, a[t]);
+    }
     for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
     if ((tid & 63) == 0) red[tid >> 6] = m;
     __syncthreads();
@@ -666,33 +722,36 @@ __global__ void __launch_bounds__(AT_THREADS) k_attn_softmax(float *att, int max
         for (int t = tid; t < n; t += AT_THREADS) a[t] = kr_fdiv(1.0f, (float)n);
         return;
     }
-    float sum = 0.0f;   // lane 0's running sum
+    if (fits) {
+#pragma unroll
+        for (int k = 0; k < AT_V; k++) {
+            if (k * AT_THREADS >= n) break;   // the rest of the slots are clamped repeats
+            const int t = k * AT_THREADS + tid;
+            v[k] = kr_expf_tab(kr_fsub(v[k], mx), xtab);
+            if (t < n) es[t] = v[k];
+        }
+        __syncthreads();
+        const float inv = kr_fdiv(1.0f, kr_spec_sum<AT_THREADS>(es, n, scr));
+#pragma unroll
+        for (int k = 0; k < AT_V; k++) {
+            if (k * AT_THREADS >= n) break;
+            const int t = k * AT_THREADS + tid;
+            if (t < n) a[t] = kr_fmul(v[k], inv);
+        }
+        return;
+    }
+    float sum = 0.0f;
     for (int c0 = 0; c0 < n; c0 += AT_CHUNK) {
         const int cn = min(AT_CHUNK, n - c0);
         for (int t = tid; t < cn; t += AT_THREADS) {
-            const float e = kr_expf(kr_fsub(a[c0 + t], mx));
+            const float e = kr_expf_tab(kr_fsub(a[c0 + t], mx), xtab);
             es[t] = e;
             a[c0 + t] = e;
         }
         __syncthreads();
-        if (tid == 0) {
-            int t = 0;
-            const float4 *p = (const float4 *)es;
-#pragma unroll 16
-            for (; t + 4 <= cn; t += 4) {
-                const float4 v = p[t >> 2];
-                sum = kr_fadd(sum, v.x);
-                sum = kr_fadd(sum, v.y);
-                sum = kr_fadd(sum, v.z);
-                sum = kr_fadd(sum, v.w);
-            }
-            for (; t < cn; t++) sum = kr_fadd(sum, es[t]);
-        }
-        __syncthreads();
+        sum = kr_spec_sum<AT_THREADS>(es, cn, scr, sum);   // ends with a barrier: es is free again
     }
-    if (tid == 0) s_inv = kr_fdiv(1.0f, sum);
-    __syncthreads();
-    const float inv = s_inv;
+    const float inv = kr_fdiv(1.0f, sum);
     for (int t = tid; t < n; t += AT_THREADS) a[t] = kr_fmul(a[t], inv);
 }
 
@@ -953,11 +1012,11 @@ __global__ void k_math_batch(int op, float *y, const float *a, const float *b, s
     default: y[i] = 0.0f;
     }
 }
-__global__ void __launch_bounds__(256) k_ordered_sum(float *out, const float *t, int n) {
+__global__ void __launch_bounds__(256) k_ordered_sum(float *out, const float *t, int n, float s0) {
     extern __shared__ __align__(16) float os_t[];
     for (int i = threadIdx.x; i < n; i += 256) os_t[i] = t[i];
     __syncthreads();
-    const float s = kr_spec_sum<256>(os_t, n, (unsigned char *)(os_t + sc_terms_cap(n)));
+    const float s = kr_spec_sum<256>(os_t, n, (unsigned char *)(os_t + sc_terms_cap(n)), s0);
     if (threadIdx.x == 0) *out = s;
 }
 __global__ void k_h2f_batch(float *y, const uint16_t *h, size_t n) {
@@ -1230,13 +1289,13 @@ extern "C" void krh_math_batch(int op, float *y, const float *a, const float *b,
     kr_check_launch("math_batch");
 }
 
-extern "C" void krh_ordered_sum(float *out, const float *t, int n) {
+extern "C" void krh_ordered_sum(float *out, const float *t, int n, float s0) {
     if (n < 1 || n > KRH_ORDERED_SUM_MAX) {
         kr_fail(ML_E_SHAPE, "ordered_sum size", hipSuccess);
         return;
     }
     const size_t lds = sizeof(float) * (size_t)sc_terms_cap(n) + sc_lds_bytes(n, RN_THREADS);
-    hipLaunchKernelGGL(k_ordered_sum, dim3(1), dim3(256), lds, kr_stream(), out, t, n);
+    hipLaunchKernelGGL(k_ordered_sum, dim3(1), dim3(256), lds, kr_stream(), out, t, n, s0);
     kr_check_launch("ordered_sum");
 }
 

@@ -40,15 +40,12 @@ __constant__ uint64_t kr_exp2_tab[32] = {
 // SiLU call glibc's expf (kernels/scalar/k_scalar.c:74, :97), whose x86-64 FMA
 // build evaluates x*32/ln2 = k + r with two fused multiply-adds and
 // 2^(k/32) * (1 + c2 r + (c0 r + c1) r^2) in double.
-__device__ __forceinline__ float kr_expf(float x) {
+// The same expf with the table read from tab (a copy of kr_exp2_tab, e.g.
+// in LDS) and the out-of-range cases selected rather than branched to: every
+// lane runs the same instructions.
+__device__ __forceinline__ float kr_expf_tab(float x, const uint64_t *tab) {
     const uint32_t ux = __float_as_uint(x);
     const uint32_t top = (ux >> 20) & 0x7ff;
-    if (top >= 0x42bu) {                       // |x| >= 88, inf or NaN
-        if (ux == 0xff800000u) return 0.0f;
-        if (top >= 0x7f8u) return x + x;
-        if (x > 0x1.62e42ep6f) return __uint_as_float(0x7f800000u);
-        if (x < -0x1.9fe368p6f) return 0.0f;
-    }
     const double inv_ln2_n = 0x1.71547652b82fep+0 * 32, shift = 0x1.8p+52;
     const double c0 = 0x1.c6af84b912394p-5 / 32 / 32 / 32, c1 = 0x1.ebfce50fac4f3p-3 / 32 / 32,
                  c2 = 0x1.62e42ff0c52d6p-1 / 32;
@@ -57,13 +54,22 @@ __device__ __forceinline__ float kr_expf(float x) {
     const uint64_t ki = (uint64_t)__double_as_longlong(kd);
     kd = kd - shift;
     const double r = __builtin_fma(inv_ln2_n, xd, -kd);
-    const double s = __longlong_as_double((long long)(kr_exp2_tab[ki & 31] + (ki << 47)));
+    const double s = __longlong_as_double((long long)(tab[ki & 31] + (ki << 47)));
     const double p = __builtin_fma(c0, r, c1);
     const double r2 = r * r;
     double y = __builtin_fma(c2, r, 1.0);
     y = __builtin_fma(p, r2, y);
-    return (float)(y * s);
+    float res = (float)(y * s);
+    if (top >= 0x42bu) {                       // |x| >= 88, inf or NaN
+        res = x < -0x1.9fe368p6f ? 0.0f : res;
+        res = x > 0x1.62e42ep6f ? __uint_as_float(0x7f800000u) : res;
+        res = top >= 0x7f8u ? x + x : res;
+        res = ux == 0xff800000u ? 0.0f : res;
+    }
+    return res;
 }
+
+__device__ __forceinline__ float kr_expf(float x) { return kr_expf_tab(x, kr_exp2_tab); }
 
 // IEEE binary16 -> float32; exact for every input (subnormals included).
 __device__ __forceinline__ float kr_h2f(uint16_t h) { return __half2float(__ushort_as_half(h)); }

@@ -294,7 +294,8 @@ def test_matvec_float_input(dev, typ, d16, rows, cols):
 
 @pytest.mark.parametrize("nh,nkv,hd,pos,window", [(6, 6, 48, 0, 0), (6, 6, 48, 200, 0), (14, 2, 64, 511, 0),
                                                   (32, 8, 128, 2303, 0), (32, 8, 64, 4000, 0), (8, 2, 64, 100, 7),
-                                                  (16, 1, 64, 63, 0), (4, 2, 32, 64, 0), (12, 4, 96, 130, 0)])
+                                                  (16, 1, 64, 63, 0), (4, 2, 32, 64, 0), (12, 4, 96, 130, 0),
+                                                  (4, 2, 32, 9000, 0), (8, 2, 64, 12000, 9000)])
 def test_attention(dev, nh, nkv, hd, pos, window):
     max_seq = max(256, pos + 1)
     kvd, qd = nkv * hd, nh * hd
@@ -319,10 +320,10 @@ def test_attention(dev, nh, nkv, hd, pos, window):
     assert np.array_equal(bits(ad.get(np.float32, qd // 32)), bits(d0))
 
 
-def seq_sum_f32(t):
-    """((0 + t0) + t1) + ... in float32, one rounding per add (the reference's
+def seq_sum_f32(t, s0=0.0):
+    """((s0 + t0) + t1) + ... in float32, one rounding per add (the reference's
     loop order, kernels/scalar/k_scalar.c:61, :71-74)"""
-    return np.add.accumulate(np.concatenate([[np.float32(0)], t]).astype(np.float32), dtype=np.float32)[-1]
+    return np.add.accumulate(np.concatenate([[np.float32(s0)], t]).astype(np.float32), dtype=np.float32)[-1]
 
 
 def test_seq_sum_f32_is_sequential():
@@ -337,9 +338,10 @@ ORDERED_CASES = ["squares", "heavy", "outliers", "absorb", "absorb_late", "tiny"
                  "nan", "inf", "huge"]
 
 
+@pytest.mark.parametrize("s0", [0.0, 1234.5678])
 @pytest.mark.parametrize("case", ORDERED_CASES)
 @pytest.mark.parametrize("n", [1, 5, 127, 128, 129, 2175, 4096, 8192])
-def test_ordered_sum(dev, case, n):
+def test_ordered_sum(dev, case, n, s0):
     """the chunked speculative sum returns the bits of the sequential fp32 sum,
     through its window hits, its per-chunk fallback (absorbed terms push the
     true sum hundreds of ulps from the estimate) and its non-finite path"""
@@ -375,10 +377,10 @@ def test_ordered_sum(dev, case, n):
         t = f32(np.full(n, 3e37))
     t = f32(t)
     out = dev.zeros(4)
-    K.hip.krh_ordered_sum(out.ptr, dev.put(t).ptr, n)
+    K.hip.krh_ordered_sum(out.ptr, dev.put(t).ptr, n, s0)
     ok()
     got = out.get(np.float32, 1)[0]
-    want = seq_sum_f32(t)
+    want = seq_sum_f32(t, s0)
     if np.isnan(want):
         assert np.isnan(got)
     else:
