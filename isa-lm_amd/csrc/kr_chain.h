@@ -3,206 +3,388 @@
 //
 // The reference adds such terms in index order (rmsnorm's sum of squares,
 // kernels/scalar/k_scalar.c:61; softmax's sum of exponentials,
-// k_scalar.c:71-74): s = (((0 + t0) + t1) + ...) with one rounding per add.
-// On one lane that is a chain of n dependent adds. Here the terms are split
-// into chunks of L; the fp32 running sum at a chunk's start lies within a few
-// ulps of the exact prefix, which a double-precision prefix sum estimates.
-// Each chunk is therefore run from all SC_W consecutive floats around its
-// estimate at once (one per lane of a wave). A walk over the chunks then
-// picks, for the true running value, the matching end value: the same adds
-// in the same order, so the same bits. A true value outside its chunk's
-// window is run through that chunk one add at a time, so the result is exact
-// whatever the terms; non-finite terms skip the speculation altogether.
+// k_scalar.c:71-74): s = (((s0 + t0) + t1) + ...) with one rounding per add.
+// On one lane that is a chain of n dependent adds.
+//
+// The shortcut rests on one property of round-to-nearest-even. In a binade
+// [2^e, 2^(e+1)) the floats are the multiples m u of one spacing u, and a
+// rounding picks the nearest multiple, ties to the even m. Moving a real sum
+// by an even number of spacings moves its rounding by the same amount, ties
+// included. So if a chain a_{j+1} = fl(a_j + t_j) over some terms stays
+// inside one binade, then started from a + 2 k u it ends exactly 2 k u higher
+// (and, the terms being >= 0, it is monotone, so its two ends tell whether it
+// stayed inside). In bits: a run maps a start s to s + d[s & 1], where d[0]
+// and d[1] come from running it from one even start and the odd start above.
+//
+// The terms are split into chunks (32 to 128 terms, at most 128 chunks). For
+// each chunk a pair of lanes runs the chain from an even and an odd start in
+// the binade where the prefix before the chunk lies (estimated by fp32
+// partial sums: only its binade matters), checking every SC_BLK terms
+// whether the pair left that binade. A block where it did is marked to be
+// added one term at a time later, and the pair starts again after it in the
+// new binade. Maps of the form s -> s + d[s & 1] compose into maps of the same
+// form, so the walk over the chunks is a segmented prefix scan of the chunks'
+// first runs across lanes; it cuts at the chunks with marked blocks, whose
+// rest (marked blocks term by term, later runs by their maps) runs on the
+// true value between segments. Then every run checks, from its true start,
+// that start, run start and moved end share one binade, which holds exactly
+// when the true chain stayed in it; from the first run that fails, the walk
+// goes on chunk by chunk and runs any failing run one add at a time. So the
+// result is the sequential loop's bits whatever the terms. A negative or
+// non-finite term sends the whole sum through the sequential loop.
 #pragma once
 #include "kr_numerics.h"
 
-#include <utility>
-
 namespace {
 
-constexpr int SC_W = 64;             // candidate start values per chunk: one per lane
-constexpr int SC_H = 32;             // window [estimate - 32 ulps, estimate + 31 ulps]
-constexpr int SC_MAX_CHUNKS = 32;
-constexpr int SC_LMIN = 128;         // chunk length, doubled while chunks > SC_MAX_CHUNKS
-constexpr int SC_BLK = 128;          // terms per register block of a chain (8 VGPRs x 16 lanes)
-constexpr unsigned SC_INVALID = 0xFFFFFFFFu;   // a negative NaN: never a sum of terms >= 0
+constexpr int SC_LOG_LMIN = 5;                // chunks of 32 terms, doubled while more than SC_MAXC
+constexpr int SC_MAXC = 128;
+constexpr int SC_PAD = 4;                     // floats after each chunk's terms (spreads LDS banks)
+constexpr int SC_BLK = 16;                    // terms between binade checks
+constexpr int SC_MAXNB = 8;                   // blocks per chunk, at most
+constexpr int SC_NSEG = SC_MAXNB / 2;         // runs of unbroken blocks in a chunk, at most
+constexpr int SC_CPW = 32;                    // chunks per wave: one lane pair each
+constexpr int SC_REC = 1 + 3 * SC_NSEG;       // ints of walk record per chunk
+constexpr int SC_MAX_N = SC_MAXC * SC_MAXNB * SC_BLK;
 
-__host__ __device__ constexpr int sc_chunk_len(int n) {
-    int L = SC_LMIN;
-    while ((n + L - 1) / L > SC_MAX_CHUNKS) L *= 2;
-    return L;
+// log2 of the chunk length for n terms
+__host__ __device__ constexpr int sc_log_len(int n) {
+    int sh = SC_LOG_LMIN;
+    while (((n + (1 << sh) - 1) >> sh) > SC_MAXC) sh++;
+    return sh;
 }
-__host__ __device__ constexpr int sc_chunks(int n) { return (n + sc_chunk_len(n) - 1) / sc_chunk_len(n); }
-// floats of term space the caller provides: n rounded up to whole chunks
-__host__ __device__ constexpr int sc_terms_cap(int n) { return sc_chunks(n) * sc_chunk_len(n); }
+__host__ __device__ constexpr int sc_chunks(int n) { return (n + (1 << sc_log_len(n)) - 1) >> sc_log_len(n); }
+// the LDS float index of term i, sh = sc_log_len(n) (every chunk padded)
+__host__ __device__ constexpr int sc_at(int i, int sh) { return i + ((i >> sh) << 2); }
+// floats of term space the caller provides
+__host__ __device__ constexpr int sc_terms_cap(int n) { return sc_chunks(n) * ((1 << sc_log_len(n)) + SC_PAD); }
 // bytes of LDS scratch kr_spec_sum<NT> needs beside the terms
 __host__ __device__ constexpr int sc_lds_bytes(int n, int nt) {
-    return sc_chunks(n) * SC_W * 4 + sc_chunks(n) * 8 + sc_chunks(n) * 4 + (nt / 64) * 4 + 16;
+    return (nt / 64) * 8 + sc_chunks(n) * SC_REC * 4 + 16;
 }
 
-// s + t[i0] + ... + t[i1 - 1], one add at a time (one lane)
-__device__ __forceinline__ float sc_seq(const float *t, int i0, int i1, float s) {
+__device__ __forceinline__ void kr_wave_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// s + t[i0] + ... + t[i1 - 1], one add at a time, i0 and i1 - 1 in one chunk
+__device__ __forceinline__ float sc_seq(const float *t, int sh, int i0, int i1, float s) {
+    const float *p = t + sc_at(i0, sh);
 #pragma unroll 8
-    for (int i = i0; i < i1; i++) s = kr_fadd(s, t[i]);
+    for (int i = 0; i < i1 - i0; i++) s = kr_fadd(s, p[i]);
+    return s;
+}
+__device__ __forceinline__ float sc_seq_all(const float *t, int n, int sh, float s) {
+    for (int i0 = 0; i0 < n; i0 += 1 << sh) s = sc_seq(t, sh, i0, min(i0 + (1 << sh), n), s);
+    return s;
+}
+__device__ __forceinline__ unsigned sc_uni(unsigned v) { return (unsigned)__builtin_amdgcn_readfirstlane((int)v); }
+__device__ __forceinline__ unsigned sc_lane(unsigned v, int l) { return (unsigned)__builtin_amdgcn_readlane((int)v, l); }
+
+template <int CTRL> __device__ __forceinline__ unsigned sc_quad(unsigned v) {
+    return (unsigned)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, false);
+}
+constexpr int SC_QP_SWAP = 0xB1;   // quad_perm [1, 0, 3, 2]: the other lane of the pair
+constexpr int SC_QP_EVEN = 0xA0;   // quad_perm [0, 0, 2, 2]: the pair's even lane
+// DPP moves of a wave scan: row_shr:1, 2, 4, 8 (lane l - n of the row of 16),
+// row_bcast:15 (lane 15 of the row before, into rows 1 and 3), row_bcast:31
+// (lane 31, into rows 2 and 3); a lane uses the moved value only where the
+// source lane exists
+template <int CTRL> __device__ __forceinline__ unsigned sc_mv(unsigned v) {
+    return (unsigned)__builtin_amdgcn_mov_dpp((int)v, CTRL, 0xF, 0xF, false);
+}
+constexpr int SC_SHR1 = 0x111, SC_SHR2 = 0x112, SC_SHR4 = 0x114, SC_SHR8 = 0x118, SC_BC15 = 0x142, SC_BC31 = 0x143;
+// the value of lane - 1 (0 for lane 0)
+__device__ __forceinline__ unsigned sc_prev(unsigned v, int lane) {
+    const unsigned a = sc_mv<SC_SHR1>(v), b15 = sc_mv<SC_BC15>(v), b31 = sc_mv<SC_BC31>(v);
+    return (lane & 15) ? a : (lane == 16 || lane == 48) ? b15 : lane == 32 ? b31 : 0u;
+}
+// inclusive prefix sum over the wave's lanes (fp32; an estimate)
+__device__ __forceinline__ float sc_scan_add(float v, int lane) {
+    const int rl = lane & 15;
+    float u;
+    u = __uint_as_float(sc_mv<SC_SHR1>(__float_as_uint(v)));
+    v = rl >= 1 ? v + u : v;
+    u = __uint_as_float(sc_mv<SC_SHR2>(__float_as_uint(v)));
+    v = rl >= 2 ? v + u : v;
+    u = __uint_as_float(sc_mv<SC_SHR4>(__float_as_uint(v)));
+    v = rl >= 4 ? v + u : v;
+    u = __uint_as_float(sc_mv<SC_SHR8>(__float_as_uint(v)));
+    v = rl >= 8 ? v + u : v;
+    u = __uint_as_float(sc_mv<SC_BC15>(__float_as_uint(v)));
+    v = (lane & 31) >= 16 ? v + u : v;
+    u = __uint_as_float(sc_mv<SC_BC31>(__float_as_uint(v)));
+    v = lane >= 32 ? v + u : v;
+    return v;
+}
+// one step of the segmented scan of run maps s -> s + d[s & 1]: the lane
+// prepends the window of the source lane unless its own window holds a
+// segment start (hf)
+template <int CTRL>
+__device__ __forceinline__ void sc_seg_step(unsigned &d0, unsigned &d1, unsigned &hf, bool valid) {
+    const unsigned p0 = sc_mv<CTRL>(d0), p1 = sc_mv<CTRL>(d1), ph = sc_mv<CTRL>(hf);
+    if (valid && !hf) {
+        const unsigned n0 = p0 + ((p0 & 1u) ? d1 : d0), n1 = p1 + ((p1 & 1u) ? d0 : d1);
+        d0 = n0;
+        d1 = n1;
+        hf = ph;
+    }
+}
+// s + 16 terms from i0 (a block), one add at a time, one batch of LDS reads
+__device__ __forceinline__ float sc_blk16(const float *t, int sh, int i0, float s) {
+    const float4 *q = (const float4 *)(t + sc_at(i0, sh));
+    const float4 v0 = q[0], v1 = q[1], v2 = q[2], v3 = q[3];
+    const float4 v[4] = {v0, v1, v2, v3};
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        s = kr_fadd(s, v[k].x);
+        s = kr_fadd(s, v[k].y);
+        s = kr_fadd(s, v[k].z);
+        s = kr_fadd(s, v[k].w);
+    }
     return s;
 }
 
-// s + (lane k of v's row of 16) for k = 0..15 in order: the term comes with
-// the add (DPP row broadcast), so a chain step is one instruction; 8 chains
-// interleaved
-template <int K> __device__ __forceinline__ float sc_bcast(float v) {
-    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x150 + K, 0xF, 0xF, false));
-}
-template <int... K>
-__device__ __forceinline__ void sc_add16x8(float (&s)[8], const float (&v)[8], std::integer_sequence<int, K...>) {
-    ((s[0] = kr_fadd(s[0], sc_bcast<K>(v[0])), s[1] = kr_fadd(s[1], sc_bcast<K>(v[1])),
-      s[2] = kr_fadd(s[2], sc_bcast<K>(v[2])), s[3] = kr_fadd(s[3], sc_bcast<K>(v[3])),
-      s[4] = kr_fadd(s[4], sc_bcast<K>(v[4])), s[5] = kr_fadd(s[5], sc_bcast<K>(v[5])),
-      s[6] = kr_fadd(s[6], sc_bcast<K>(v[6])), s[7] = kr_fadd(s[7], sc_bcast<K>(v[7]))), ...);
+// whether the run with even start b and ends e0, e1 maps the true start sv
+// to sv + (its end's offset) inside one binade; end: that value
+__device__ __forceinline__ bool sc_shift(unsigned sv, unsigned b, unsigned e0, unsigned e1, unsigned &end) {
+    const unsigned k = sv - b;
+    const unsigned par = k & 1u;
+    const unsigned e = par ? e1 : e0;
+    end = e + (k - par);
+    return ((sv ^ b) >> 23) == 0 && ((e ^ b) >> 23) == 0 && ((end ^ b) >> 23) == 0 && (b >> 23) < 0xFFu;
 }
 
-// The ordered sum s0 + t[0] + ... + t[n-1] (t in LDS, 16-byte aligned, room
-// for sc_terms_cap(n) floats: the tail is zero-filled, and s + 0 == s for
-// s >= +0) by all NT threads of the workgroup; every thread gets the result.
-// lds: sc_lds_bytes(n, NT) bytes, 8-byte aligned. s0 and the terms are
-// expected to be >= 0 (others only make the walk fall back more often).
-// Contains barriers: all threads must call it.
-//
-// Wave w owns chunks w, w + NW, ... (SC_CPW of them at most): it sums them
-// in double (16-term pieces per lane, reduced over 8 lanes), publishes the
-// sums, then forms its own chunks' window starts from the published sums
-// and runs their candidates, 8 chains interleaved.
-constexpr int SC_CPW = 8;   // chunks per wave: C <= NW * SC_CPW
+// chunk c from block blk (its run number seg) to its end, from the true
+// value sv: marked blocks one add at a time, runs by their maps (one add at a
+// time when the check fails)
+__device__ __forceinline__ unsigned sc_rest(const float *t, int sh, int c, int m, unsigned sv, int blk, int seg,
+                                            const int *rb, const int *re0, const int *re1) {
+    const int L = 1 << sh, NB = L / SC_BLK;
+    while (blk < NB) {
+        const int i0 = c * L + blk * SC_BLK;
+        if ((m >> blk) & 1) {
+            sv = sc_uni(__float_as_uint(sc_blk16(t, sh, i0, __uint_as_float(sv))));
+            blk++;
+        } else {
+            const int e = blk + __builtin_ctz(((unsigned)m >> blk) | (1u << (NB - blk)));
+            const int ri = c * SC_NSEG + seg;
+            unsigned end;
+            if (sc_shift(sv, sc_uni(rb[ri]), sc_uni(re0[ri]), sc_uni(re1[ri]), end))
+                sv = end;
+            else
+                sv = sc_uni(__float_as_uint(sc_seq(t, sh, i0, c * L + e * SC_BLK, __uint_as_float(sv))));
+            seg++;
+            blk = e;
+        }
+    }
+    return sv;
+}
+
+// The ordered sum s0 + t[0] + ... + t[n-1] (n <= SC_MAX_N) by all NT threads
+// of the workgroup; every thread gets the result. Term i sits at
+// t[sc_at(i, sc_log_len(n))] in LDS (16-byte aligned, sc_terms_cap(n)
+// floats: the last chunk's tail is zero-filled here, and s + 0 == s for
+// s >= +0). lds: sc_lds_bytes(n, NT) bytes, 4-byte aligned. s0 is expected to
+// be >= +0. Contains barriers: all threads must call it, after a barrier that
+// follows the terms' stores.
 template <int NT>
 __device__ __forceinline__ float kr_spec_sum(float *t, int n, unsigned char *lds, float s0 = 0.0f) {
     constexpr int NW = NT / 64;
-    static_assert(NW * SC_CPW >= SC_MAX_CHUNKS, "every chunk needs a wave");
+    static_assert(NW * SC_CPW >= SC_MAXC, "every chunk needs a lane pair");
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int L = sc_chunk_len(n), C = sc_chunks(n);
-    float *tab0 = (float *)lds;               // [C][SC_W] chunk end values per candidate
-    double *csum = (double *)(tab0 + C * SC_W);
-    int *lo = (int *)(csum + C);              // first candidate's bits per chunk
-    int *bad = lo + C;                        // [NW] a wave saw a non-finite term
-    float *res = (float *)(bad + NW);
+    const int sh = sc_log_len(n), L = 1 << sh, NB = L / SC_BLK;
+    const int C = (n + L - 1) >> sh, NA = (C + SC_CPW - 1) / SC_CPW;   // waves with chunks
+    float *wtot = (float *)lds;                   // [NW] a wave's chunk total
+    int *wbad = (int *)(wtot + NW);               // [NW] a wave saw a negative or non-finite term
+    int *rm = wbad + NW;                          // [C] marked blocks
+    int *rb = rm + C;                             // [C][SC_NSEG] even start of each run
+    int *re0 = rb + C * SC_NSEG, *re1 = re0 + C * SC_NSEG;   // its ends from the even and odd starts
+    float *res = (float *)(re1 + C * SC_NSEG);
 
-    if (n % L) {   // the last chunk's tail
-        for (int i = n + tid; i < C * L; i += NT) t[i] = 0.0f;
-        __syncthreads();
+    const int p = lane & 1, c = wave * SC_CPW + (lane >> 1);
+    if ((n & (L - 1)) && wave == (C - 1) / SC_CPW) {   // the wave that owns the last chunk
+        for (int i = n + lane; i < C * L; i += 64) t[sc_at(i, sh)] = 0.0f;
+        kr_wave_sync();
     }
-    // this wave's chunk sums: lane (j, p) sums terms [16 q, 16 q + 16) for
-    // q = p, p + 8, ... of chunk j of the wave, in double (two accumulators),
-    // then the 8 lanes of a chunk add theirs; non-finite terms flagged
-    {
-        const int j = lane >> 3, p = lane & 7, c = wave + j * NW;
-        double acc0 = 0.0, acc1 = 0.0;
-        bool nf = false;
-        if (c < C) {
-            for (int q = p; q < L / 16; q += 8) {
-                const float4 *r = (const float4 *)(t + c * L + 16 * q);
-                const float4 v0 = r[0], v1 = r[1], v2 = r[2], v3 = r[3];
-                const float M = 3.402823466e38f;   // FLT_MAX: NaN fails every comparison
-                const float4 vs[4] = {v0, v1, v2, v3};
+    // the chunk's sum (lane p: its half), the prefix sums over the wave's
+    // chunks; a set sign bit (a negative term, or -0) or a sum that is not
+    // finite (a term that is not) sends everything to the sequential loop
+    const float *tc = t + c * (L + SC_PAD);
+    float acc = 0.0f;
+    unsigned sg = 0;
+    if (c < C) {
+        const float4 *h = (const float4 *)(tc + (L / 2) * p);
+        float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
+        for (int k = 0; k < L / 8; k++) {
+            const float4 v = h[k];
+            sg |= __float_as_uint(v.x) | __float_as_uint(v.y) | __float_as_uint(v.z) | __float_as_uint(v.w);
+            a0 += v.x;
+            a1 += v.y;
+            a2 += v.z;
+            a3 += v.w;
+        }
+        acc = (a0 + a1) + (a2 + a3);
+    }
+    acc += __uint_as_float(sc_quad<SC_QP_SWAP>(__float_as_uint(acc)));
+    // prefix over chunks: each chunk counted at its even lane; the pair takes
+    // the even lane's exclusive value
+    const float inc = sc_scan_add(p ? 0.0f : acc, lane);
+    const float pre = __uint_as_float(sc_quad<SC_QP_EVEN>(sc_prev(__float_as_uint(inc), lane)));
+    const float wsum = __uint_as_float(sc_lane(__float_as_uint(inc), 63));
+    bool bad = __any((sg >> 31) != 0 || !(acc <= 3.402823466e38f));   // FLT_MAX: NaN fails
+    float before = s0;
+    if (NA > 1) {   // the other waves' chunk totals and flags
+        if (lane == 0 && wave < NA) {
+            wtot[wave] = wsum;
+            wbad[wave] = bad;
+        }
+        __syncthreads();
+        for (int w = 0; w < NA; w++) {
+            if (w < wave) before += wtot[w];
+            bad = bad || wbad[w];
+        }
+    }
+    // the pair's chains: lane p from the even start + p (chunk 0 from the
+    // true start: its chain is exact)
+    if (c < C && !bad) {
+        unsigned b = 0;
+        float s = s0;
+        if (c > 0) {
+            b = __float_as_uint(before + pre) & ~1u;
+            s = __uint_as_float(b | (unsigned)p);
+        }
+        int mask = 0, nseg = 0;
+        bool run = false;
+        int *re = p ? re1 : re0;
+        float4 cur[4], nxt[4];
 #pragma unroll
-                for (int k = 0; k < 4; k++) {
-                    const float4 v = vs[k];
-                    nf = nf || !(fabsf(v.x) <= M && fabsf(v.y) <= M && fabsf(v.z) <= M && fabsf(v.w) <= M);
-                    acc0 += (double)v.x + (double)v.y;
-                    acc1 += (double)v.z + (double)v.w;
+        for (int q = 0; q < 4; q++) cur[q] = ((const float4 *)tc)[q];
+        for (int blk = 0; blk < NB; blk++) {
+            const float4 *nb4 = (const float4 *)(tc + min(blk + 1, NB - 1) * SC_BLK);
+#pragma unroll
+            for (int q = 0; q < 4; q++) nxt[q] = nb4[q];
+            const float s_start = s;
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                s = kr_fadd(s, cur[q].x);
+                s = kr_fadd(s, cur[q].y);
+                s = kr_fadd(s, cur[q].z);
+                s = kr_fadd(s, cur[q].w);
+            }
+            const unsigned sb = __float_as_uint(s);
+            unsigned cr = (c > 0) && ((sb ^ b) >> 23) != 0;
+            cr |= sc_quad<SC_QP_SWAP>(cr);
+            const unsigned nbits = sc_quad<SC_QP_EVEN>(sb) & ~1u;
+            if (cr) {   // the pair left the binade in this block: mark it, start again after it
+                if (run) {
+                    if (p == 0) rb[c * SC_NSEG + nseg] = (int)b;
+                    re[c * SC_NSEG + nseg] = (int)__float_as_uint(s_start);
+                    nseg++;
                 }
-            }
-        }
-        double acc = acc0 + acc1;
-        acc += __shfl_xor(acc, 1);
-        acc += __shfl_xor(acc, 2);
-        acc += __shfl_xor(acc, 4);
-        const bool anynf = __any(nf);
-        if (p == 0 && c < C) csum[c] = acc;
-        if (lane == 0) bad[wave] = anynf;
-    }
-    __syncthreads();
-    bool anybad = false;
-#pragma unroll
-    for (int w = 0; w < NW; w++) anybad = anybad || bad[w];
-    if (anybad) {
-        if (tid == 0) *res = sc_seq(t, 0, n, s0);
-        __syncthreads();
-        return *res;
-    }
-    // the window starts of this wave's chunks: lane j < SC_CPW sums the chunk
-    // sums before chunk wave + j * NW (all read at once)
-    int lov = 0;
-    {
-        double cs[SC_MAX_CHUNKS];
-#pragma unroll
-        for (int k = 0; k < SC_MAX_CHUNKS; k++) cs[k] = csum[min(k, C - 1)];
-        const int c = wave + lane * NW;
-        double e = (double)s0;   // the exact prefix before chunk c, to within double rounding
-#pragma unroll
-        for (int k = 0; k < SC_MAX_CHUNKS; k++) e += k < min(c, C) ? cs[k] : 0.0;
-        lov = max(__float_as_int((float)e) - SC_H, 0);   // chunk 0: s0 is candidate SC_H (or lower near +0)
-        if (lane < SC_CPW && c < C) lo[c] = lov;
-    }
-    // every candidate start of this wave's chunks at once (chunk ids past the
-    // end repeat the wave's first chunk, unused); lane (row r, column k)
-    // holds terms 16 i + k of a 128-term block in v[i][.]
-    {
-        int cb[SC_CPW];
-        float s[SC_CPW];
-#pragma unroll
-        for (int j = 0; j < SC_CPW; j++) {
-            const int c = wave + j * NW < C ? wave + j * NW : wave;
-            cb[j] = c * L;
-            s[j] = __int_as_float(__builtin_amdgcn_readlane(lov, j) + lane);
-        }
-        if (wave < C) {
-            for (int b0 = 0; b0 < L; b0 += SC_BLK) {
-                float v[8][SC_CPW];
-#pragma unroll
-                for (int i = 0; i < 8; i++)
-#pragma unroll
-                    for (int j = 0; j < SC_CPW; j++) v[i][j] = t[cb[j] + b0 + 16 * i + (lane & 15)];
-#pragma unroll
-                for (int i = 0; i < 8; i++) sc_add16x8(s, v[i], std::make_integer_sequence<int, 16>());
+                mask |= 1 << blk;
+                b = nbits;
+                s = __uint_as_float(nbits | (unsigned)p);
+                run = false;
+            } else {
+                run = true;
             }
 #pragma unroll
-            for (int j = 0; j < SC_CPW; j++)
-                if (wave + j * NW < C) tab0[(wave + j * NW) * SC_W + lane] = s[j];
+            for (int q = 0; q < 4; q++) cur[q] = nxt[q];
         }
+        if (run) {
+            if (p == 0) rb[c * SC_NSEG + nseg] = (int)b;
+            re[c * SC_NSEG + nseg] = (int)__float_as_uint(s);
+        }
+        if (p == 0) rm[c] = mask;
     }
-    __syncthreads();
-    // the walk, in wave 0: chunk c's end values sit in one register (lane w:
-    // candidate w), so a step is a scalar subtract and compare on the
-    // running value and one read of the lane it selects, with no branch (an
-    // index out of the window is clamped and clears ok). Any miss: lane 0
-    // walks again, one add at a time in the chunks whose window it left
+    if (NA > 1) __syncthreads();
+    else kr_wave_sync();
+    // the walk, in wave 0, 64 chunks (one per lane) at a time
     if (wave == 0) {
-        float e[SC_MAX_CHUNKS];
-#pragma unroll
-        for (int c = 0; c < SC_MAX_CHUNKS; c++) e[c] = tab0[min(c, C - 1) * SC_W + lane];   // all at once
-        const int lv = lo[min(lane, C - 1)];
-        int sv = __float_as_int(s0);   // bits of the running value
-        bool ok = true;
-#pragma unroll
-        for (int c = 0; c < SC_MAX_CHUNKS; c++) {
-            const unsigned idx = (unsigned)(sv - __builtin_amdgcn_readlane(lv, c));
-            const int nv = __builtin_amdgcn_readlane(__float_as_int(e[c]), (int)(idx & (SC_W - 1)));
-            if (c < C) {
-                ok = ok && idx < (unsigned)SC_W;
-                sv = nv;
-            }
-        }
-        if (lane == 0) {
-            float f = __int_as_float(sv);
-            if (!ok) {
-                f = s0;
-                for (int c = 0; c < C; c++) {
-                    const int idx = __float_as_int(f) - lo[c];
-                    if ((unsigned)idx < (unsigned)SC_W) f = tab0[c * SC_W + idx];
-                    else f = sc_seq(t, c * L, c * L + L, f);
+        float r;
+        if (bad) {
+            r = sc_seq_all(t, n, sh, s0);
+        } else {
+            unsigned sv = sc_uni(re0[0]);   // chunk 0's end: exact
+            int cser = C;                   // chunks from here on go one by one
+            for (int g0 = 0; g0 < C; g0 += 64) {
+                const int cnt = min(64, C - g0), cc = g0 + lane, cl = min(cc, C - 1);
+                const int m = rm[cl];
+                const unsigned b = rb[cl * SC_NSEG], e0 = re0[cl * SC_NSEG], e1 = re1[cl * SC_NSEG];
+                // the run after a chunk's first marked block (its number: 1
+                // if a run comes before the mark, else 0)
+                const int r1 = cl * SC_NSEG + ((m & 1) ? 0 : 1);
+                const unsigned b1 = rb[r1], e01 = re0[r1], e11 = re1[r1];
+                // the chunk's first run (a run before its first marked block)
+                const bool pre = lane < cnt && cc > 0 && (m & 1) == 0;
+                const bool brk = lane < cnt && m != 0;
+                unsigned d0 = pre ? e0 - b : 0u, d1 = pre ? e1 - b - 1u : 0u;
+                const unsigned long long bm = __ballot(brk);
+                // segments start at lane 0 and after each chunk with marks;
+                // inclusive scan of the first-run maps within segments
+                const bool head = lane == 0 || (((bm << 1) >> lane) & 1ull);
+                unsigned hf = head;
+                const int rl = lane & 15;
+                sc_seg_step<SC_SHR1>(d0, d1, hf, rl >= 1);
+                sc_seg_step<SC_SHR2>(d0, d1, hf, rl >= 2);
+                sc_seg_step<SC_SHR4>(d0, d1, hf, rl >= 4);
+                sc_seg_step<SC_SHR8>(d0, d1, hf, rl >= 8);
+                sc_seg_step<SC_BC15>(d0, d1, hf, (lane & 31) >= 16);
+                sc_seg_step<SC_BC31>(d0, d1, hf, lane >= 32);
+                unsigned x0 = sc_prev(d0, lane), x1 = sc_prev(d1, lane);
+                if (head) x0 = x1 = 0u;
+                // the true value entering each segment, serially
+                unsigned hv = 0;
+                for (int pos = 0; pos < cnt;) {
+                    const unsigned long long rest = bm >> pos;
+                    const int k = rest ? pos + __builtin_ctzll(rest) : cnt - 1;
+                    if (lane >= pos && lane <= k) hv = sv;
+                    const unsigned kd0 = sc_lane(d0, k), kd1 = sc_lane(d1, k);
+                    sv += (sv & 1u) ? kd1 : kd0;
+                    if (rest & 1ull << (k - pos)) {   // chunk g0 + k has marks: the rest of it
+                        const int mk = (int)sc_lane((unsigned)m, k);
+                        const int fb = __builtin_ctz((unsigned)mk);
+                        const int i0 = (g0 + k) * L + fb * SC_BLK;
+                        sv = sc_uni(__float_as_uint(sc_blk16(t, sh, i0, __uint_as_float(sv))));
+                        if ((mk & (mk - 1)) == 0) {   // one mark: at most one run after it
+                            if (fb + 1 < NB) {
+                                unsigned end;
+                                if (sc_shift(sv, sc_lane(b1, k), sc_lane(e01, k), sc_lane(e11, k), end))
+                                    sv = end;
+                                else
+                                    sv = sc_uni(__float_as_uint(sc_seq(t, sh, i0 + SC_BLK, (g0 + k + 1) * L,
+                                                                       __uint_as_float(sv))));
+                            }
+                        } else {
+                            sv = sc_rest(t, sh, g0 + k, mk, sv, fb + 1, (mk & 1) ? 0 : 1, rb, re0, re1);
+                        }
+                    }
+                    pos = k + 1;
+                }
+                // every first run's check from its true start
+                const unsigned hp = hv & 1u;
+                const unsigned st = hv + (hp ? x1 : x0), en = hv + (hp ? d1 : d0);
+                bool ok = true;
+                if (pre) {
+                    const unsigned e = (st & 1u) ? e1 : e0;
+                    ok = ((st ^ b) >> 23) == 0 && ((e ^ b) >> 23) == 0 && ((en ^ b) >> 23) == 0 &&
+                         (b >> 23) < 0xFFu;
+                }
+                const unsigned long long fail = __ballot(!ok);
+                if (fail) {
+                    const int f = __builtin_ctzll(fail);
+                    sv = sc_lane(st, f);
+                    cser = g0 + f;
+                    break;
                 }
             }
-            *res = f;
+            for (int k = cser; k < C; k++) sv = sc_rest(t, sh, k, (int)sc_uni(rm[k]), sv, 0, 0, rb, re0, re1);
+            r = __uint_as_float(sv);
         }
+        if (lane == 0) *res = r;
     }
     __syncthreads();
     return *res;

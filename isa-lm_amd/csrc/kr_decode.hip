@@ -159,11 +159,12 @@ __device__ __forceinline__ void rmsnorm_q8_block(int8_t *q, float *d, size_t dst
     }
     float inv = 1.0f;
     if (norm) {
+        const int sh = sc_log_len(n);
 #pragma unroll
         for (int k = 0; k < V4; k++) {
             const int i = (k * NT + tid) * 4;
             if (i < n)
-                *(float4 *)(sq + i) = make_float4(kr_fmul(xv[k].x, xv[k].x), kr_fmul(xv[k].y, xv[k].y),
+                *(float4 *)(sq + sc_at(i, sh)) = make_float4(kr_fmul(xv[k].x, xv[k].x), kr_fmul(xv[k].y, xv[k].y),
                                                   kr_fmul(xv[k].z, xv[k].z), kr_fmul(xv[k].w, xv[k].w));
         }
         __syncthreads();
@@ -268,11 +269,6 @@ __host__ __device__ inline MvLds mv_lds(int K, int maxloc, int nbc, bool norm) {
 
 // Orders one wave's LDS writes before its later reads for the compiler (a
 // wave's LDS operations execute in order).
-__device__ __forceinline__ void kr_wave_sync() {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
 
 // y rows [row0, row0 + R) of up to three matrices sharing the activation
 // (QKV), or the w1 and w3 rows [row0, row0 + R) (SwiGLU). Each wave streams
@@ -357,11 +353,12 @@ __global__ void __launch_bounds__(MV_THREADS, 2) k_matvec(const MvArgs a) {
         if (a.nw) {
             // the squares wait on x alone; the weight stream then runs under
             // the ordered sum
+            const int sh = sc_log_len(K);
 #pragma unroll
             for (int k = 0; k < XV; k++) {
                 const int i = 4 * (k * MV_THREADS + tid);
                 if (i < K)
-                    *(float4 *)(sq + i) = make_float4(kr_fmul(xv[k].x, xv[k].x), kr_fmul(xv[k].y, xv[k].y),
+                    *(float4 *)(sq + sc_at(i, sh)) = make_float4(kr_fmul(xv[k].x, xv[k].x), kr_fmul(xv[k].y, xv[k].y),
                                                       kr_fmul(xv[k].z, xv[k].z), kr_fmul(xv[k].w, xv[k].w));
             }
 #pragma unroll
@@ -388,7 +385,7 @@ __global__ void __launch_bounds__(MV_THREADS, 2) k_matvec(const MvArgs a) {
         } else if (a.nw) {
             for (int i = 4 * tid; i < K; i += 4 * MV_THREADS) {
                 const float4 v = *(const float4 *)(a.xf + i);
-                *(float4 *)(sq + i) = make_float4(kr_fmul(v.x, v.x), kr_fmul(v.y, v.y), kr_fmul(v.z, v.z),
+                *(float4 *)(sq + sc_at(i, sc_log_len(K))) = make_float4(kr_fmul(v.x, v.x), kr_fmul(v.y, v.y), kr_fmul(v.z, v.z),
                                                   kr_fmul(v.w, v.w));
             }
             __syncthreads();
@@ -723,12 +720,13 @@ __global__ void __launch_bounds__(AT_THREADS) k_attn_softmax(float *att, int max
         return;
     }
     if (fits) {
+        const int sh = sc_log_len(n);
 #pragma unroll
         for (int k = 0; k < AT_V; k++) {
             if (k * AT_THREADS >= n) break;   // the rest of the slots are clamped repeats
             const int t = k * AT_THREADS + tid;
             v[k] = kr_expf_tab(kr_fsub(v[k], mx), xtab);
-            if (t < n) es[t] = v[k];
+            if (t < n) es[sc_at(t, sh)] = v[k];
         }
         __syncthreads();
         const float inv = kr_fdiv(1.0f, kr_spec_sum<AT_THREADS>(es, n, scr));
@@ -742,10 +740,10 @@ __global__ void __launch_bounds__(AT_THREADS) k_attn_softmax(float *att, int max
     }
     float sum = 0.0f;
     for (int c0 = 0; c0 < n; c0 += AT_CHUNK) {
-        const int cn = min(AT_CHUNK, n - c0);
+        const int cn = min(AT_CHUNK, n - c0), sh = sc_log_len(cn);
         for (int t = tid; t < cn; t += AT_THREADS) {
             const float e = kr_expf_tab(kr_fsub(a[c0 + t], mx), xtab);
-            es[t] = e;
+            es[sc_at(t, sh)] = e;
             a[c0 + t] = e;
         }
         __syncthreads();
@@ -1014,7 +1012,7 @@ __global__ void k_math_batch(int op, float *y, const float *a, const float *b, s
 }
 __global__ void __launch_bounds__(256) k_ordered_sum(float *out, const float *t, int n, float s0) {
     extern __shared__ __align__(16) float os_t[];
-    for (int i = threadIdx.x; i < n; i += 256) os_t[i] = t[i];
+    for (int i = threadIdx.x; i < n; i += 256) os_t[sc_at(i, sc_log_len(n))] = t[i];
     __syncthreads();
     const float s = kr_spec_sum<256>(os_t, n, (unsigned char *)(os_t + sc_terms_cap(n)), s0);
     if (threadIdx.x == 0) *out = s;

@@ -335,16 +335,18 @@ def test_seq_sum_f32_is_sequential():
 
 
 ORDERED_CASES = ["squares", "heavy", "outliers", "absorb", "absorb_late", "tiny", "zeros", "exps", "mixed_sign",
-                 "nan", "inf", "huge"]
+                 "nan", "inf", "huge", "ties", "steep", "late_growth", "neg_zero", "subnormal"]
 
 
 @pytest.mark.parametrize("s0", [0.0, 1234.5678])
 @pytest.mark.parametrize("case", ORDERED_CASES)
-@pytest.mark.parametrize("n", [1, 5, 127, 128, 129, 2175, 4096, 8192])
+@pytest.mark.parametrize("n", [1, 5, 31, 32, 33, 127, 128, 129, 2048, 2049, 2175, 4096, 4097, 8192])
 def test_ordered_sum(dev, case, n, s0):
-    """the chunked speculative sum returns the bits of the sequential fp32 sum,
-    through its window hits, its per-chunk fallback (absorbed terms push the
-    true sum hundreds of ulps from the estimate) and its non-finite path"""
+    """the chunked sum returns the bits of the sequential fp32 sum through its
+    shifted runs (ties to even included), its blocks where the running sum
+    changes binade (many of them for steep growth), its per-run fallback, the
+    sequential path for negative, -0 and non-finite terms, and sizes at the
+    chunk-length and chunk-count edges"""
     x = RNG.normal(0, 1, n)
     if case == "squares":
         t = f32(x) * f32(x)
@@ -373,6 +375,18 @@ def test_ordered_sum(dev, case, n, s0):
     elif case == "inf":
         t = f32(x * x)
         t[n - 1] = np.inf
+    elif case == "ties":   # few significant bits: rounding ties all along
+        t = f32(RNG.integers(0, 8, n)) * f32(2.0) ** f32(RNG.integers(-3, 4, n))
+    elif case == "steep":   # the running sum doubles every few terms
+        t = f32(2.0) ** f32(np.floor(np.arange(n) * 60.0 / max(n, 1)) - 30)
+    elif case == "late_growth":
+        t = f32(x * x)
+        t[: n // 2] = 0
+    elif case == "neg_zero":
+        t = f32(x * x)
+        t[RNG.random(n) < 0.05] = -0.0
+    elif case == "subnormal":
+        t = f32(np.abs(x) * 1e-44)
     else:   # huge: the sum overflows to inf part-way
         t = f32(np.full(n, 3e37))
     t = f32(t)
