@@ -753,33 +753,181 @@ __global__ void __launch_bounds__(AT_THREADS) k_attn_softmax(float *att, int max
     for (int t = tid; t < n; t += AT_THREADS) a[t] = kr_fmul(a[t], inv);
 }
 
-// out for one KV head's query heads and DW of their dims, one wave per
-// workgroup: lane = (head j of the group, dim d), DW = 64 / (group rounded up
+// out for one KV head's query heads and DW of their dims: lane = (head j of
+// the group, dim d), DW = 64 / (group rounded up to a power of two). Each
+// lane runs its ordered chain o += a_t * v_t,d (k_scalar.c:119-122). ao is
+// written as floats (its quantization happens where it is consumed).
+//
+// The chain (one dependent add per position) is the bound, so the workgroup
+// splits the work by role and keeps the adding wave free of everything else.
+// Wave 0 only adds. MX_P producer waves load V and the weights, form the
+// products a_t * v_t,d (each the rounded product, as in the scalar loop) and
+// hand them over through a ring of three LDS tiles of MX_T positions, laid out
+// [lane][position] so that one 16-byte read feeds 4 adds. Producer p owns
+// positions [p MX_TH, (p + 1) MX_TH) of every tile and loads them MX_D tiles
+// ahead into registers: a lane holds 4 dims of V at one position and the
+// weights of every head at that position, and writes its products straight
+// into the adder's layout (4-byte writes: the transpose costs no LDS reads).
+// LDS bandwidth is what the roles share, so each product crosses LDS once each
+// way. One barrier per step hands tiles over: producers write tile s in step
+// s; the adder reads tile s into registers in step s + 1 and adds it in step
+// s + 2, so no add waits on an LDS read.
+constexpr int MX_T = 64, MX_TS = MX_T + 4;   // positions per tile; padded product row
+constexpr int MX_P = 2, MX_TH = MX_T / MX_P;   // producers; their positions per tile
+
+__device__ __forceinline__ void kr_lds_order() { asm volatile("" ::: "memory"); }
+
+template <int DW>
+__global__ void __launch_bounds__(64 * (1 + MX_P)) k_attn_mix(float *ao, const float *att, const float *vc,
+                                                              int group, int hd, int kv_dim, int max_seq, int window,
+                                                              const int *pos_p) {
+    constexpr int GP = 64 / DW;                        // head slots
+    constexpr int NV = (MX_TH * DW / 4 + 63) / 64;     // float4 of V per producer lane per tile
+    constexpr int PT = 4 * NV + NV * GP;               // registers per tile: V and the weights
+    constexpr int LT = NV + NV * GP;                   // loads per tile
+    // tiles in flight: within 128 registers and within the 63 loads the wait
+    // counter can track (past that every wait would drain it)
+    constexpr int DR = 128 / PT < 60 / LT ? 128 / PT : 60 / LT;
+    constexpr int MX_D = DR > 8 ? 8 : DR < 2 ? 2 : DR;
+    __shared__ __align__(16) float prod[4][64 * MX_TS];   // the ring, and a sink for steps past the end
+    int first, n;
+    attn_range(pos_p, window, &first, &n);
+    const int g = blockIdx.x, c0 = blockIdx.y * DW, lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int j = lane / DW, d = lane % DW;
+    const int ntiles = (n + MX_T - 1) / MX_T;
+    const int steps = (ntiles + 2 + MX_D - 1) / MX_D * MX_D;   // every wave runs as many barriers
+    const size_t q_dim = (size_t)gridDim.x * group * hd;
+
+    if (wave == 0) {
+        // the adder: in step s it reads all of tile s - 1 into registers
+        // (finished a step earlier) while it adds tile s - 2 from the
+        // registers read in step s - 1, so every LDS read has a whole tile
+        // of adds to arrive in
+        float o = 0.0f;
+        auto step = [&](int s, float4 *cur, float4 *nxt) {
+            if (s - 1 >= 0 && s - 1 < ntiles) {
+                const float *P = prod[(s - 1) % 3] + lane * MX_TS;
+#pragma unroll
+                for (int i = 0; i < MX_T / 4; i++) nxt[i] = *(const float4 *)(P + 4 * i);
+            }
+            const int tile = s - 2;
+            if (tile >= 0 && tile < ntiles) {
+                const int nt = min(MX_T, n - tile * MX_T);
+                if (nt == MX_T) {
+#pragma unroll
+                    for (int i = 0; i < MX_T / 4; i++) {
+                        o = kr_fadd(o, cur[i].x);
+                        o = kr_fadd(o, cur[i].y);
+                        o = kr_fadd(o, cur[i].z);
+                        o = kr_fadd(o, cur[i].w);
+                    }
+                } else {   // the last, partial tile: only its live steps (a zero would turn -0 to +0)
+                    const float *P = prod[tile % 3] + lane * MX_TS;
+                    for (int r = 0; r < nt; r++) o = kr_fadd(o, P[r]);
+                }
+            }
+            kr_lds_order();
+            __syncthreads();
+        };
+        float4 ta[MX_T / 4], tb[MX_T / 4];
+        for (int s = 0; s < steps; s += 2) {
+            step(s, ta, tb);
+            if (s + 1 < steps) step(s + 1, tb, ta);
+        }
+        if (j < group && d < min(DW, hd - c0)) ao[blockIdx.z * q_dim + (size_t)(g * group + j) * hd + c0 + d] = o;
+        return;
+    }
+
+    // producer p: lane slot k holds V dims c..c+3 at position r of its half
+    // tile, and the weights of heads 0..GP-1 at that position
+    const int p = wave - 1;
+    const int cw = min(DW, hd - c0);   // valid dims of the chunk (a multiple of 4)
+    const float *vbase = vc + (size_t)first * kv_dim + (size_t)g * hd + c0;
+    const float *abase = att + ((size_t)blockIdx.z * gridDim.x * group + (size_t)g * group) * max_seq;
+    // Every load is unconditional from an address clamped into the live
+    // range (position n - 1, the chunk's last float4, the group's last head,
+    // the row's last element): values loaded for positions >= n, dims >= cw
+    // or heads >= group only feed products that are never added or stored,
+    // and a branch-free loop keeps the loads of MX_D tiles in flight.
+    float4 rv[MX_D][NV];
+    float ra[MX_D][NV][GP];
+    auto load = [&](int tile, float4 *v, float (*a)[GP]) {
+        const int t0 = min(tile, ntiles - 1) * MX_T + p * MX_TH;
+#pragma unroll
+        for (int k = 0; k < NV; k++) {
+            const int e = (k * 64 + lane) * 4, r = min(e / DW, MX_TH - 1), c = min(e % DW, cw - 4);
+            v[k] = *(const float4 *)(vbase + (size_t)min(t0 + r, n - 1) * kv_dim + c);
+            const int q = min(t0 + r, max_seq - 1);
+#pragma unroll
+            for (int jj = 0; jj < GP; jj++) a[k][jj] = abase[(size_t)min(jj, group - 1) * max_seq + q];
+        }
+    };
+    auto products = [&](int tile, const float4 *v, const float (*a)[GP]) {
+        float *P = prod[tile < ntiles ? tile % 3 : 3] + p * MX_TH;
+#pragma unroll
+        for (int k = 0; k < NV; k++) {
+            const int e = (k * 64 + lane) * 4, r = e / DW, c = e % DW;
+            if (r < MX_TH) {
+#pragma unroll
+                for (int jj = 0; jj < GP; jj++) {
+                    float *o = P + (jj * DW + c) * MX_TS + r;
+                    o[0] = kr_fmul(a[k][jj], v[k].x);
+                    o[MX_TS] = kr_fmul(a[k][jj], v[k].y);
+                    o[2 * MX_TS] = kr_fmul(a[k][jj], v[k].z);
+                    o[3 * MX_TS] = kr_fmul(a[k][jj], v[k].w);
+                }
+            }
+        }
+        kr_lds_order();
+    };
+    // in slot order (the loop's waits count on slot 0 being the oldest)
+#pragma unroll
+    for (int u = 0; u < MX_D; u++) {
+        load(u, rv[u], ra[u]);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    for (int s0 = 0; s0 < steps; s0 += MX_D) {
+#pragma unroll
+        for (int u = 0; u < MX_D; u++) {
+            const int s = s0 + u;   // tile s sits in slot u
+            // fenced for the scheduler: a step's products wait on its own
+            // slot's loads only
+            __builtin_amdgcn_sched_barrier(0);
+            products(s, rv[u], ra[u]);   // past the end: into the sink, unread
+            load(s + MX_D, rv[u], ra[u]);
+            __builtin_amdgcn_sched_barrier(0);
+            __syncthreads();
+        }
+    }
+}
+
+// The same for a batch of positions (prefill: one workgroup per position and
+// head chunk, so throughput, not one chain's latency, is what counts), one wave
+// per workgroup: lane = (head j of the group, dim d), DW = 64 / (group rounded up
 // to a power of two). Each lane runs its ordered chain o += a_t * v_t,d
 // (k_scalar.c:119-122). ao is written as floats (its quantization happens
 // where it is consumed).
 //
 // The chain is the bound (one dependent add per position), so everything else
-// is pipelined under it: tiles of MX_T positions of V and of the heads' weights
-// are loaded MX_DEPTH tiles ahead into registers; tile t + 1 is staged into
+// is pipelined under it: tiles of MB_T positions of V and of the heads' weights
+// are loaded MB_DEPTH tiles ahead into registers; tile t + 1 is staged into
 // the other half of a double LDS buffer while tile t is read, V transposed
 // ([dim][position]) so one 16-byte LDS read feeds 4 steps; the reads of each
 // 16-step chunk are issued before the adds of the chunk before it. The
 // workgroup is one wave, whose LDS operations execute in order, so LDS needs
 // only compiler ordering (kr_lds_order), not barriers.
-constexpr int MX_T = 64, MX_TS = MX_T + 4;   // positions per tile; padded LDS row
-
-__device__ __forceinline__ void kr_lds_order() { asm volatile("" ::: "memory"); }
+constexpr int MB_T = 64, MB_TS = MB_T + 4;   // positions per tile; padded LDS row
 
 template <int DW>
-__global__ void __launch_bounds__(64) k_attn_mix(float *ao, const float *att, const float *vc, int group, int hd,
+__global__ void __launch_bounds__(64) k_attn_mix_batch(float *ao, const float *att, const float *vc, int group, int hd,
                                                  int kv_dim, int max_seq, int window, const int *pos_p) {
     constexpr int GP = 64 / DW;                    // head slots per wave
-    constexpr int NV = MX_T * DW / 4 / 64;         // float4 of V per lane per tile
-    constexpr int NA = (GP * MX_T / 4 + 63) / 64;  // float4 of weights per lane per tile
-    constexpr int MX_DEPTH = NV + NA > 8 ? 2 : 4;  // tiles in flight (even: LDS halves alternate)
-    __shared__ __align__(16) float vt[2][DW * MX_TS];
-    constexpr int AW = GP * MX_T > NA * 256 ? GP * MX_T : NA * 256;   // padded: every lane stores
+    constexpr int NV = MB_T * DW / 4 / 64;         // float4 of V per lane per tile
+    constexpr int NA = (GP * MB_T / 4 + 63) / 64;  // float4 of weights per lane per tile
+    constexpr int MB_DEPTH = NV + NA > 8 ? 2 : 4;  // tiles in flight (even: LDS halves alternate)
+    __shared__ __align__(16) float vt[2][DW * MB_TS];
+    constexpr int AW = GP * MB_T > NA * 256 ? GP * MB_T : NA * 256;   // padded: every lane stores
     __shared__ __align__(16) float aw[2][AW];
     int first, n;
     attn_range(pos_p, window, &first, &n);
@@ -789,7 +937,7 @@ __global__ void __launch_bounds__(64) k_attn_mix(float *ao, const float *att, co
     const size_t q_dim = (size_t)gridDim.x * group * hd;
     const float *abase = att + ((size_t)blockIdx.z * gridDim.x * group + (size_t)g * group) * max_seq;
     ao += blockIdx.z * q_dim;
-    const int ntiles = (n + MX_T - 1) / MX_T;
+    const int ntiles = (n + MB_T - 1) / MB_T;
     const int cw = min(DW, hd - c0);   // valid dims of the chunk (a multiple of 4)
 
     // Every load is unconditional from an address clamped into the live
@@ -797,10 +945,10 @@ __global__ void __launch_bounds__(64) k_attn_mix(float *ao, const float *att, co
     // the row's last float4): values loaded for positions >= n, dims >= cw or
     // heads >= group only feed lanes and steps that are never stored or run,
     // and a branch-free load stream lets the compiler's wait counts keep the
-    // loads of MX_DEPTH tiles in flight together.
-    float4 rv[MX_DEPTH][NV], ra[MX_DEPTH][NA];
+    // loads of MB_DEPTH tiles in flight together.
+    float4 rv[MB_DEPTH][NV], ra[MB_DEPTH][NA];
     auto load = [&](int tile, float4 *v, float4 *a) {
-        const int t0 = min(tile, ntiles - 1) * MX_T;
+        const int t0 = min(tile, ntiles - 1) * MB_T;
 #pragma unroll
         for (int k = 0; k < NV; k++) {
             const int e = (k * 64 + lane) * 4, r = e / DW, c = min(e % DW, cw - 4);   // position r, dims c..c+3
@@ -808,7 +956,7 @@ __global__ void __launch_bounds__(64) k_attn_mix(float *ao, const float *att, co
         }
 #pragma unroll
         for (int k = 0; k < NA; k++) {
-            const int e = (k * 64 + lane) * 4, jj = min(e / MX_T, group - 1), r = e % MX_T;
+            const int e = (k * 64 + lane) * 4, jj = min(e / MB_T, group - 1), r = e % MB_T;
             const float *src = abase + (size_t)jj * max_seq + min(t0 + r, max_seq - 4);
             a[k] = make_float4(src[0], src[1], src[2], src[3]);
         }
@@ -818,17 +966,17 @@ __global__ void __launch_bounds__(64) k_attn_mix(float *ao, const float *att, co
 #pragma unroll
         for (int k = 0; k < NV; k++) {
             const int e = (k * 64 + lane) * 4, r = e / DW, c = e % DW;
-            V[(c + 0) * MX_TS + r] = v[k].x;
-            V[(c + 1) * MX_TS + r] = v[k].y;
-            V[(c + 2) * MX_TS + r] = v[k].z;
-            V[(c + 3) * MX_TS + r] = v[k].w;
+            V[(c + 0) * MB_TS + r] = v[k].x;
+            V[(c + 1) * MB_TS + r] = v[k].y;
+            V[(c + 2) * MB_TS + r] = v[k].z;
+            V[(c + 3) * MB_TS + r] = v[k].w;
         }
 #pragma unroll
         for (int k = 0; k < NA; k++) {
-            const int e = (k * 64 + lane) * 4, r = e % MX_T;
+            const int e = (k * 64 + lane) * 4, r = e % MB_T;
             // a float4 clamped back from the row's end holds position p at
             // element p - (max_seq - 4): shift it down to element p - p0
-            const int sh = tile * MX_T + r - min(tile * MX_T + r, max_seq - 4);
+            const int sh = tile * MB_T + r - min(tile * MB_T + r, max_seq - 4);
             const float4 x = a[k];
             float4 y;
             y.x = sh == 0 ? x.x : sh == 1 ? x.y : sh == 2 ? x.z : x.w;
@@ -841,7 +989,7 @@ __global__ void __launch_bounds__(64) k_attn_mix(float *ao, const float *att, co
     };
     struct Chunk { float4 v[4], a[4]; };   // 16 steps of one lane
     auto read = [&](Chunk &c, int buf, int k) {
-        const float *V = vt[buf] + d * MX_TS + 16 * k, *A = aw[buf] + j * MX_T + 16 * k;
+        const float *V = vt[buf] + d * MB_TS + 16 * k, *A = aw[buf] + j * MB_T + 16 * k;
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             c.v[i] = *(const float4 *)(V + 4 * i);
@@ -860,19 +1008,19 @@ __global__ void __launch_bounds__(64) k_attn_mix(float *ao, const float *att, co
     };
 
 #pragma unroll
-    for (int s = 0; s < MX_DEPTH; s++) load(s, rv[s], ra[s]);
+    for (int s = 0; s < MB_DEPTH; s++) load(s, rv[s], ra[s]);
     stage(0, 0, rv[0], ra[0]);
-    load(MX_DEPTH, rv[0], ra[0]);
+    load(MB_DEPTH, rv[0], ra[0]);
     Chunk c0r, c1r;
     read(c0r, 0, 0);
-    // main loop: groups of MX_DEPTH full tiles; tile k0 + s sits in LDS half
+    // main loop: groups of MB_DEPTH full tiles; tile k0 + s sits in LDS half
     // s & 1 and its first chunk is in c0r when its step begins
-    const int ngroups = n / (MX_T * MX_DEPTH);
+    const int ngroups = n / (MB_T * MB_DEPTH);
     int k0 = 0;
-    for (; k0 < ngroups * MX_DEPTH; k0 += MX_DEPTH) {
+    for (; k0 < ngroups * MB_DEPTH; k0 += MB_DEPTH) {
 #pragma unroll
-        for (int s = 0; s < MX_DEPTH; s++) {
-            const int b = s & 1, nx = (s + 1) % MX_DEPTH;
+        for (int s = 0; s < MB_DEPTH; s++) {
+            const int b = s & 1, nx = (s + 1) % MB_DEPTH;
             // phases fenced for the scheduler: a chunk's reads are issued
             // one phase before its products and adds, and the staging of
             // the next tile shares a phase with the first chunk's adds
@@ -880,7 +1028,7 @@ __global__ void __launch_bounds__(64) k_attn_mix(float *ao, const float *att, co
             __builtin_amdgcn_sched_barrier(0);
             chain(c0r);
             stage(b ^ 1, k0 + s + 1, rv[nx], ra[nx]);
-            load(k0 + s + 1 + MX_DEPTH, rv[nx], ra[nx]);
+            load(k0 + s + 1 + MB_DEPTH, rv[nx], ra[nx]);
             __builtin_amdgcn_sched_barrier(0);
             read(c0r, b, 2);
             __builtin_amdgcn_sched_barrier(0);
@@ -896,16 +1044,16 @@ __global__ void __launch_bounds__(64) k_attn_mix(float *ao, const float *att, co
             __builtin_amdgcn_sched_barrier(0);
         }
     }
-    // the last tiles (at most MX_DEPTH; tile k0 is staged in half 0, tile
+    // the last tiles (at most MB_DEPTH; tile k0 is staged in half 0, tile
     // k0 + s is in rv[s]); the last may be partial, and only its live steps
     // run: a zero weight would turn -0 to +0
 #pragma unroll
-    for (int s = 0; s < MX_DEPTH; s++) {
+    for (int s = 0; s < MB_DEPTH; s++) {
         const int tile = k0 + s;
         if (tile < ntiles) {
             if (s > 0) stage(s & 1, tile, rv[s], ra[s]);
-            const int nt = min(MX_T, n - tile * MX_T);
-            const float *V = vt[s & 1] + d * MX_TS, *A = aw[s & 1] + j * MX_T;
+            const int nt = min(MB_T, n - tile * MB_T);
+            const float *V = vt[s & 1] + d * MB_TS, *A = aw[s & 1] + j * MB_T;
             for (int r = 0; r < nt; r++) o = kr_fadd(o, kr_fmul(A[r], V[r]));
             kr_lds_order();
         }
@@ -1234,12 +1382,24 @@ static void attention(float *ao, float *att, const float *q, const float *kc, co
     const int gp = group <= 1 ? 1 : group <= 2 ? 2 : group <= 4 ? 4 : group <= 8 ? 8 : 16;
     const int dw = 64 / gp;
     const dim3 grid(n_kv_heads, (head_dim + dw - 1) / dw, ntok);
+    if (ntok > 1) {
+        switch (dw) {
+        case 64: hipLaunchKernelGGL(k_attn_mix_batch<64>, grid, dim3(64), 0, kr_stream(), ao, att, vc, group, head_dim, kv_dim, max_seq, window, pos); break;
+        case 32: hipLaunchKernelGGL(k_attn_mix_batch<32>, grid, dim3(64), 0, kr_stream(), ao, att, vc, group, head_dim, kv_dim, max_seq, window, pos); break;
+        case 16: hipLaunchKernelGGL(k_attn_mix_batch<16>, grid, dim3(64), 0, kr_stream(), ao, att, vc, group, head_dim, kv_dim, max_seq, window, pos); break;
+        case 8: hipLaunchKernelGGL(k_attn_mix_batch<8>, grid, dim3(64), 0, kr_stream(), ao, att, vc, group, head_dim, kv_dim, max_seq, window, pos); break;
+        default: hipLaunchKernelGGL(k_attn_mix_batch<4>, grid, dim3(64), 0, kr_stream(), ao, att, vc, group, head_dim, kv_dim, max_seq, window, pos); break;
+        }
+        kr_check_launch("attention");
+        return;
+    }
+    const dim3 block(64 * (1 + MX_P));
     switch (dw) {
-    case 64: hipLaunchKernelGGL(k_attn_mix<64>, grid, dim3(64), 0, kr_stream(), ao, att, vc, group, head_dim, kv_dim, max_seq, window, pos); break;
-    case 32: hipLaunchKernelGGL(k_attn_mix<32>, grid, dim3(64), 0, kr_stream(), ao, att, vc, group, head_dim, kv_dim, max_seq, window, pos); break;
-    case 16: hipLaunchKernelGGL(k_attn_mix<16>, grid, dim3(64), 0, kr_stream(), ao, att, vc, group, head_dim, kv_dim, max_seq, window, pos); break;
-    case 8: hipLaunchKernelGGL(k_attn_mix<8>, grid, dim3(64), 0, kr_stream(), ao, att, vc, group, head_dim, kv_dim, max_seq, window, pos); break;
-    default: hipLaunchKernelGGL(k_attn_mix<4>, grid, dim3(64), 0, kr_stream(), ao, att, vc, group, head_dim, kv_dim, max_seq, window, pos); break;
+    case 64: hipLaunchKernelGGL(k_attn_mix<64>, grid, block, 0, kr_stream(), ao, att, vc, group, head_dim, kv_dim, max_seq, window, pos); break;
+    case 32: hipLaunchKernelGGL(k_attn_mix<32>, grid, block, 0, kr_stream(), ao, att, vc, group, head_dim, kv_dim, max_seq, window, pos); break;
+    case 16: hipLaunchKernelGGL(k_attn_mix<16>, grid, block, 0, kr_stream(), ao, att, vc, group, head_dim, kv_dim, max_seq, window, pos); break;
+    case 8: hipLaunchKernelGGL(k_attn_mix<8>, grid, block, 0, kr_stream(), ao, att, vc, group, head_dim, kv_dim, max_seq, window, pos); break;
+    default: hipLaunchKernelGGL(k_attn_mix<4>, grid, block, 0, kr_stream(), ao, att, vc, group, head_dim, kv_dim, max_seq, window, pos); break;
     }
     kr_check_launch("attention");
 }
