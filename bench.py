@@ -17,17 +17,23 @@ Also reported on the same line:
                   54% of the weight bytes of a layer): algorithmic bytes per
                   launch (weights + f16 scales of w1 and w3) over its average
                   launch duration, timed with HIP events on the library
-                  stream, rotating through all 32 layers so the weights come
-                  from HBM and not from the 256 MB Infinity Cache
+                  stream around passes over all 32 layers (so the weights
+                  come from HBM and not from the 256 MB Infinity Cache)
   matvec          the isolated Q4_0/Q8_0 matvec microbench (4096x4096 and
                   14336x4096, f16 scales, activation quantize_q8(N(0,1))):
                   GB/s over 1000 launches, cache-resident (one matrix) and
                   HBM-rotating (copies totalling more than 1 GB)
+  roofline.traffic  HBM bytes per launch of that kernel, from the committed
+                  rocprofv3 --pmc summary (FETCH_SIZE and WRITE_SIZE per
+                  dispatch, each scaled by what the counter reads for k_add
+                  of known traffic); the command that made it is
+                  `bench.py --roofline-only`, which runs just the timed
+                  SwiGLU launches and the calibration launches
   cpu_baseline    the reference's best CPU build (avx512vnni, else avx2,
                   THREADS=pthread, built from its sources into oracle/_ref)
                   running ml_run on the same .mlb file on this host's cores,
-                  on a bounded sample: an 8-token prompt and 16 greedy
-                  decode tokens
+                  on a bounded sample of about 10 s: an 8-token prompt and
+                  256 greedy decode tokens
 """
 import argparse
 import ctypes as C
@@ -83,26 +89,52 @@ def mat_bytes(W):
 def time_swiglu(K, model, state, reps):
     """average duration (ms) of the decode step's SwiGLU launch -- w1|w3
     matvec on the normalized, quantized input, SiLU(w1 x) * (w3 x) -- over
-    all layers, and its algorithmic bytes per launch"""
+    all layers, and its algorithmic bytes per launch: HIP events on the
+    library stream around each pass over the layers (back-to-back launches,
+    so the figure includes the gaps between them), divided by the launches"""
     cfg = model.cfg
     xq = K.host.kr_state_buffer(state.ptr, b"qa_dim")
     xd = K.host.kr_state_buffer(state.ptr, b"qd_dim")
     hb = K.host.kr_state_buffer(state.ptr, b"hb")
+    mats = [(K.host.kr_model_device_mat(model.ptr, l, b"w1"), K.host.kr_model_device_mat(model.ptr, l, b"w3"))
+            for l in range(cfg.n_layers)]
+    nbytes = mat_bytes(mats[0][0].contents) + mat_bytes(mats[0][1].contents)
     t = K.hip.krh_timer_new()
-    total, n, nbytes = 0.0, 0, None
+    total, n = 0.0, 0
     for _ in range(reps):
-        for l in range(cfg.n_layers):
-            w1 = K.host.kr_model_device_mat(model.ptr, l, b"w1")
-            w3 = K.host.kr_model_device_mat(model.ptr, l, b"w3")
-            nbytes = mat_bytes(w1.contents) + mat_bytes(w3.contents)
-            K.hip.krh_timer_mark(t, 0)
+        K.hip.krh_timer_mark(t, 0)
+        for w1, w3 in mats:
             K.hip.krh_matvec_swiglu(hb, w1, w3, xq, xd)
-            K.hip.krh_timer_mark(t, 1)
-            total += K.hip.krh_timer_ms(t)
-            n += 1
+        K.hip.krh_timer_mark(t, 1)
+        total += K.hip.krh_timer_ms(t)
+        n += len(mats)
     K.hip.krh_timer_free(t)
     K.check(K.hip.krh_sync(), "swiglu timing")
     return total / n, nbytes
+
+
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "swiglu_matvec_traffic.json")
+CAL_N = 64 << 20   # k_add calibration: y += x over 64 Mi floats reads 512 MiB and writes 256 MiB
+
+
+def calibration_adds(K, reps=3):
+    """launches of k_add with known HBM traffic (y += x: 8 bytes read and 4
+    written per element) for scaling the FETCH_SIZE / WRITE_SIZE counters"""
+    y, x = K.DevBuf(4 * CAL_N), K.DevBuf(4 * CAL_N)
+    for _ in range(reps):
+        K.hip.krh_add(y.ptr, x.ptr, CAL_N)
+    K.check(K.hip.krh_sync(), "calibration adds")
+    y.free()
+    x.free()
+
+
+def committed_traffic():
+    """HBM bytes per SwiGLU launch from the committed counter summary, or None"""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            return json.load(f)
+    except (OSError, ValueError):
+        return None
 
 
 def matvec_microbench(K, iters=1000):
@@ -198,6 +230,9 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-matvec", action="store_true")
     ap.add_argument("--roofline-reps", type=int, default=3)
+    ap.add_argument("--roofline-only", action="store_true",
+                    help="only the timed SwiGLU launches and the k_add calibration launches (the command "
+                         "the committed rocprofv3 counter summaries are made with)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (the decode step would shard "
@@ -226,6 +261,16 @@ def main():
         dev_bytes = K.host.kr_model_device_bytes(model.ptr)
         log("uploaded %.2f GB to HBM in %.1f s" % (dev_bytes / 1e9, time.time() - t0))
         prompt = np.random.default_rng(2048).integers(1, V, P).astype(np.int32)
+        if args.roofline_only:
+            ms, nbytes = time_swiglu(K, model, state, args.roofline_reps)
+            calibration_adds(K)
+            print(json.dumps({"swiglu_avg_launch_us": round(ms * 1e3, 2), "swiglu_bytes_per_launch": nbytes,
+                              "swiglu_launches": args.roofline_reps * model.cfg.n_layers,
+                              "calibration": {"kernel": "k_add", "n": CAL_N, "launches": 3,
+                                              "read_bytes": 8 * CAL_N, "write_bytes": 4 * CAL_N}}), flush=True)
+            state.close()
+            model.close()
+            return
 
         ids_w, pre_w, _ = state.generate(prompt, P - 1 + args.warmup)
         log("warmup: prefill %d tokens %.3f s, %d decode tokens" % (P - 1, pre_w, args.warmup))
@@ -258,13 +303,14 @@ def main():
         cpu = None
         if not args.no_cpu_baseline:
             t0 = time.time()
-            cpu = cpu_baseline(path, prompt[:8], 16)
+            cpu = cpu_baseline(path, prompt[:8], 256)
             log("cpu baseline (%.1f s): %s" % (time.time() - t0, json.dumps(cpu)))
         state.close()
         model.close()
     finally:
         shutil.rmtree(tmp, ignore_errors=True)
 
+    traffic = committed_traffic()
     line = {
         "metric": METRIC, "value": round(tok_s, 3), "unit": "tok/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(1e3 * dec_s / args.steps, 4), "higher_is_better": True,
@@ -279,7 +325,8 @@ def main():
         "deterministic_ids": deterministic,
         "roofline": {"bound": "hbm", "kernel": "k_matvec<EPI_SWIGLU> (w1|w3 rows, SiLU(w1 x) * (w3 x))",
                      "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(gbs / HBM_PEAK_GBS, 4),
+                     "traffic": traffic["bytes_per_launch"] if traffic else None,
                      "bytes_per_launch": nbytes, "avg_launch_us": round(ms * 1e3, 2)},
         "matvec": mv,
         "cpu_baseline": cpu,

@@ -293,6 +293,7 @@ def test_matvec_float_input(dev, typ, d16, rows, cols):
 
 
 @pytest.mark.parametrize("nh,nkv,hd,pos,window", [(6, 6, 48, 0, 0), (6, 6, 48, 200, 0), (14, 2, 64, 511, 0),
+                                                    (32, 8, 128, 2175, 0), (32, 8, 128, 2174, 0),
                                                   (32, 8, 128, 2303, 0), (32, 8, 64, 4000, 0), (8, 2, 64, 100, 7),
                                                   (16, 1, 64, 63, 0), (4, 2, 32, 64, 0), (12, 4, 96, 130, 0),
                                                   (4, 2, 32, 9000, 0), (8, 2, 64, 12000, 9000)])
