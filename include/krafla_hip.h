@@ -202,8 +202,9 @@ void krh_h2f_batch(float *y, const uint16_t *h, size_t n);
  * the matvec) */
 void krh_block_dots(int32_t *s, const krh_mat *W, const int8_t *xq);
 /* *out = ((s0 + t[0]) + t[1]) + ... + t[n-1] in fp32, as the rmsnorm and
- * softmax kernels compute their ordered sums (chunked speculation with an
- * exact fallback); n <= KRH_ORDERED_SUM_MAX */
+ * softmax kernels compute their ordered sums (shifted runs with an exact
+ * per-run check and a sequential fallback); n in [1, KRH_ORDERED_SUM_MAX].
+ * No counterpart in the reference: a self-check of the kernels' summation. */
 enum { KRH_ORDERED_SUM_MAX = 8192 };
 void krh_ordered_sum(float *out, const float *t, int n, float s0);
 
