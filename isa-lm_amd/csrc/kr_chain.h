@@ -16,7 +16,7 @@
 // stayed inside). In bits: a run maps a start s to s + d[s & 1], where d[0]
 // and d[1] come from running it from one even start and the odd start above.
 //
-// The terms are split into chunks (32 to 128 terms, at most 128 chunks). For
+// The terms are split into chunks (128 terms, at most 128 chunks). For
 // each chunk a pair of lanes runs the chain from an even and an odd start in
 // the binade where the prefix before the chunk lies (estimated by fp32
 // partial sums: only its binade matters), checking every SC_BLK terms
@@ -37,7 +37,7 @@
 
 namespace {
 
-constexpr int SC_LOG_LMIN = 5;                // chunks of 32 terms, doubled while more than SC_MAXC
+constexpr int SC_LOG_LMIN = 7;                // chunks of 128 terms, doubled while more than SC_MAXC
 constexpr int SC_MAXC = 128;
 constexpr int SC_PAD = 4;                     // floats after each chunk's terms (spreads LDS banks)
 constexpr int SC_BLK = 16;                    // terms between binade checks
