@@ -3,7 +3,9 @@
  * pass (model/transformer.c). Compiled with -ffp-contract=off like the
  * reference's scalar build, so every float operation rounds where the
  * reference's does. */
+#include <immintrin.h>
 #include <math.h>
+#include <pthread.h>
 #include <stdlib.h>
 #include <string.h>
 #include "kro.h"
@@ -23,6 +25,52 @@ uint16_t kro_f32_to_f16(float f) {
     }
     x += 0xfff + ((x >> 13) & 1);
     return sign | (uint16_t)((x >> 13) - (112u << 10));
+}
+
+/* kro_f32_to_f16 over the inputs with bits lo .. lo + n - 1 */
+void kro_f32_to_f16_range(uint16_t *out, uint32_t lo, size_t n) {
+    for (size_t i = 0; i < n; i++) {
+        const uint32_t u = lo + (uint32_t)i;
+        float f;
+        memcpy(&f, &u, 4);
+        out[i] = kro_f32_to_f16(f);
+    }
+}
+
+/* The check of kro_f32_to_f16: the x86 F16C conversion (vcvtps2ph, IEEE
+ * round to nearest even) as the independent reference; NaN inputs must give
+ * the quiet NaN 0x7e00 with the input's sign, which F16C does not (it keeps
+ * payload bits). Counts mismatches over bit patterns [lo, hi). */
+typedef struct { uint64_t lo, hi, bad; } f16_span;
+
+__attribute__((target("f16c"))) static void *f16_scan(void *p) {
+    f16_span *sp = p;
+    for (uint64_t u = sp->lo; u < sp->hi; u++) {
+        const uint32_t b = (uint32_t)u;
+        float x;
+        memcpy(&x, &b, 4);
+        const uint16_t want = isnan(x) ? (uint16_t)(((b >> 16) & 0x8000) | 0x7e00)
+                                       : (uint16_t)_cvtss_sh(x, _MM_FROUND_TO_NEAREST_INT | _MM_FROUND_NO_EXC);
+        if (kro_f32_to_f16(x) != want) sp->bad++;
+    }
+    return NULL;
+}
+
+uint64_t kro_f32_to_f16_mismatches(uint64_t lo, uint64_t hi, int threads) {
+    if (!__builtin_cpu_supports("f16c")) return UINT64_MAX;
+    if (threads < 1) threads = 1;
+    if (threads > 64) threads = 64;
+    pthread_t th[64];
+    f16_span sp[64];
+    for (int i = 0; i < threads; i++) {
+        sp[i].lo = lo + (hi - lo) * (uint64_t)i / (uint64_t)threads;
+        sp[i].hi = lo + (hi - lo) * (uint64_t)(i + 1) / (uint64_t)threads;
+        sp[i].bad = 0;
+        pthread_create(&th[i], NULL, f16_scan, &sp[i]);
+    }
+    uint64_t bad = 0;
+    for (int i = 0; i < threads; i++) { pthread_join(th[i], NULL); bad += sp[i].bad; }
+    return bad;
 }
 
 /* core/ml.c:55-62 */
@@ -222,6 +270,62 @@ int kro_argmax(const float *v, int n) {
     for (int i = 1; i < n; i++) if (v[i] > v[best]) best = i;
     return best;
 }
+/* ops/ops.c:81-96: Q8 of a whole row with one scale (the Q8 KV cache's rows
+ * and the quantized query heads) */
+void kro_quantize_row(int8_t *q, float *d, const float *x, int n) {
+    float amax = 0.0f;
+    for (int i = 0; i < n; i++) amax = fmaxf(amax, fabsf(x[i]));
+    if (amax < ML_QUANT_TINY) {
+        *d = 0.0f;
+        memset(q, 0, (size_t)n);
+        return;
+    }
+    const float id = 127.0f / amax;
+    *d = amax / 127.0f;
+    for (int i = 0; i < n; i++) {
+        const float m = x[i] * id;
+        float v = truncf(m + copysignf(0.5f, x[i]));
+        v = fminf(fmaxf(v, -127.0f), 127.0f);
+        q[i] = (int8_t)v;
+    }
+}
+
+/* k_scalar.c:124-129 */
+void kro_dot_f16(float *s, const float *q, const uint16_t *k, size_t ldk, int rows, int n, float scale) {
+    for (int t = 0; t < rows; t++, k += ldk) {
+        float acc = 0.0f;
+        for (int i = 0; i < n; i++) acc = acc + q[i] * kro_f16_to_f32(k[i]);
+        s[t] = acc * scale;
+    }
+}
+
+/* k_scalar.c:131-135 */
+void kro_axpy_f16(float *y, const float *a, const uint16_t *x, size_t ldx, int rows, int n) {
+    for (int t = 0; t < rows; t++, x += ldx)
+        for (int i = 0; i < n; i++) y[i] = y[i] + a[t] * kro_f16_to_f32(x[i]);
+}
+
+/* k_scalar.c:137-146: exact int32 dot, then (float)sum * (dq * scale) * dk_t */
+void kro_dot_q8(float *s, const int8_t *q, float dq, const int8_t *k, const float *dk, size_t ldk, size_t lddk,
+                int rows, int n, float scale) {
+    const float c = dq * scale;
+    for (int t = 0; t < rows; t++) {
+        const int8_t *kt = k + (size_t)t * ldk;
+        int32_t sum = 0;
+        for (int i = 0; i < n; i++) sum += q[i] * kt[i];
+        s[t] = (float)sum * c * dk[(size_t)t * lddk];
+    }
+}
+
+/* k_scalar.c:148-155: w = a_t * dx_t, then y += w * x_t in position order */
+void kro_axpy_q8(float *y, const float *a, const int8_t *x, const float *dx, size_t ldx, size_t lddx, int rows,
+                 int n) {
+    for (int t = 0; t < rows; t++) {
+        const int8_t *xt = x + (size_t)t * ldx;
+        const float w = a[t] * dx[(size_t)t * lddx];
+        for (int i = 0; i < n; i++) y[i] = y[i] + w * (float)xt[i];
+    }
+}
 
 /* ops/ops.c:169-200 (attend) for the F32 cache, one query head at a time:
  * the 64-position blocks and head grouping of the reference leave each head's
@@ -231,15 +335,31 @@ void kro_attention(float *out, const float *q, const ml_kv_layer *kv, float *att
     const int hd = cfg->head_dim, group = cfg->n_heads / cfg->n_kv_heads;
     const int first = kv->window && pos >= kv->window ? pos + 1 - kv->window : 0;
     const int n = pos + 1 - first;
-    const size_t ld = (size_t)cfg->kv_dim;
+    const size_t ld = (size_t)cfg->kv_dim, ldd = (size_t)cfg->n_kv_heads;
+    /* the Q8 cache: each query head quantized once (ops/ops.c:171-173) */
+    int8_t *qq = NULL;
+    float *qd = NULL;
+    if (kv->kq) {
+        qq = malloc((size_t)cfg->q_dim);
+        qd = malloc(sizeof(float) * cfg->n_heads);
+        if (!qq || !qd) abort();
+        for (int h = 0; h < cfg->n_heads; h++) kro_quantize_row(qq + (size_t)h * hd, qd + h, q + (size_t)h * hd, hd);
+    }
     for (int h = 0; h < cfg->n_heads; h++) {
-        const size_t off = (size_t)(h / group) * hd + (size_t)first * ld;
-        kro_dot_f32(att, q + (size_t)h * hd, kv->k + off, ld, n, hd, cfg->attn_scale);
+        const int g = h / group;
+        const size_t off = (size_t)g * hd + (size_t)first * ld, offd = (size_t)first * ldd + g;
+        if (kv->k) kro_dot_f32(att, q + (size_t)h * hd, kv->k + off, ld, n, hd, cfg->attn_scale);
+        else if (kv->kh) kro_dot_f16(att, q + (size_t)h * hd, kv->kh + off, ld, n, hd, cfg->attn_scale);
+        else kro_dot_q8(att, qq + (size_t)h * hd, qd[h], kv->kq + off, kv->kd + offd, ld, ldd, n, hd, cfg->attn_scale);
         kro_softmax(att, n);
         float *o = out + (size_t)h * hd;
         for (int i = 0; i < hd; i++) o[i] = 0.0f;
-        kro_axpy_f32(o, att, kv->v + off, ld, n, hd);
+        if (kv->v) kro_axpy_f32(o, att, kv->v + off, ld, n, hd);
+        else if (kv->vh) kro_axpy_f16(o, att, kv->vh + off, ld, n, hd);
+        else kro_axpy_q8(o, att, kv->vq + off, kv->vd + offd, ld, ldd, n, hd);
     }
+    free(qq);
+    free(qd);
 }
 
 /* ---- model ---- */
@@ -260,7 +380,11 @@ const ml_config *kro_model_config(const kro_model *m) { return kro_mlb_config(m)
 struct kro_state {
     const kro_model *m;
     float *x, *xb, *xb2, *hb, *hb2, *q, *ao, *att, *logits;
-    float *kcache, *vcache;
+    int kv_type;
+    float *kcache, *vcache;   /* F32 cache; for F16 / Q8, the current K and V rows (kbuf, vbuf) */
+    uint16_t *kh, *vh;        /* F16 cache */
+    int8_t *kq, *vq;          /* Q8 cache and its row scales */
+    float *kd, *vd;
     float *rope_cos, *rope_sin, *rope_cos_local, *rope_sin_local;
     ml_qact qa_dim, qa_hidden, qa_q;
 };
@@ -290,19 +414,38 @@ static double rope_inv_freq(const ml_config *c, int i) {
     return (1.0 - smooth) * inv / f + smooth * inv;
 }
 
-int kro_state_new(kro_state **out, const kro_model *m) {
+int kro_state_new(kro_state **out, const kro_model *m) { return kro_state_new_kv(out, m, ML_F32); }
+
+/* model/transformer.c:51-166 with kv_type ML_F32, ML_F16 or ML_Q8_0 */
+int kro_state_new_kv(kro_state **out, const kro_model *m, int kv_type) {
     const ml_config *c = kro_mlb_config(m);
     if (c->act != ML_ACT_SILU || c->attn_softcap > 0.0f || c->final_softcap > 0.0f) return ML_E_SHAPE;
+    if (kv_type != ML_F32 && kv_type != ML_F16 && kv_type != ML_Q8_0) return ML_E_SHAPE;
     kro_state *s = calloc(1, sizeof *s);
     if (!s) return ML_E_NOMEM;
     s->m = m;
+    s->kv_type = kv_type;
     const size_t f = sizeof(float), kv = (size_t)c->n_layers * c->max_seq * c->kv_dim;
+    const size_t ks = (size_t)c->n_layers * c->max_seq * c->n_kv_heads;
     const size_t half = (size_t)c->max_seq * (c->head_dim / 2);
     s->x = calloc(c->dim, f); s->xb = calloc(c->dim, f); s->xb2 = calloc(c->dim, f);
     s->hb = calloc(c->hidden_dim, f); s->hb2 = calloc(c->hidden_dim, f);
     s->q = calloc(c->q_dim, f); s->ao = calloc(c->q_dim, f);
     s->att = calloc(c->max_seq, f); s->logits = calloc(c->vocab, f);
-    s->kcache = calloc(kv, f); s->vcache = calloc(kv, f);
+    if (kv_type == ML_F32) {
+        s->kcache = calloc(kv, f); s->vcache = calloc(kv, f);
+    } else {
+        s->kcache = calloc(c->kv_dim, f); s->vcache = calloc(c->kv_dim, f);
+        if (kv_type == ML_F16) {
+            s->kh = calloc(kv, 2); s->vh = calloc(kv, 2);
+        } else {
+            s->kq = calloc(kv, 1); s->vq = calloc(kv, 1); s->kd = calloc(ks, f); s->vd = calloc(ks, f);
+        }
+        if ((kv_type == ML_F16 && (!s->kh || !s->vh)) || (kv_type == ML_Q8_0 && (!s->kq || !s->vq || !s->kd || !s->vd))) {
+            kro_state_free(s);
+            return ML_E_NOMEM;
+        }
+    }
     s->rope_cos = calloc(half, f); s->rope_sin = calloc(half, f);
     s->qa_dim = (ml_qact){ malloc(c->dim), malloc(f * c->dim / QK), c->dim };
     s->qa_hidden = (ml_qact){ malloc(c->hidden_dim), malloc(f * c->hidden_dim / QK), c->hidden_dim };
@@ -336,6 +479,7 @@ void kro_state_free(kro_state *s) {
     if (!s) return;
     free(s->x); free(s->xb); free(s->xb2); free(s->hb); free(s->hb2); free(s->q); free(s->ao);
     free(s->att); free(s->logits); free(s->kcache); free(s->vcache);
+    free(s->kh); free(s->vh); free(s->kq); free(s->vq); free(s->kd); free(s->vd);
     free(s->rope_cos); free(s->rope_sin); free(s->rope_cos_local); free(s->rope_sin_local);
     free(s->qa_dim.q); free(s->qa_dim.d); free(s->qa_hidden.q); free(s->qa_hidden.d);
     free(s->qa_q.q); free(s->qa_q.d);
@@ -358,7 +502,39 @@ static void heads_norm(float *x, const float *w, int n, const ml_config *c) {
     for (int h = 0; h < n; h++) kro_rmsnorm(x + (size_t)h * c->head_dim, x + (size_t)h * c->head_dim, w, c->head_dim, c->norm_eps);
 }
 
-/* model/transformer.c:257-306 with the F32 cache; `cls` = run the classifier */
+/* model/transformer.c:191-205 (store_kv): the F16 cache rounds the position's
+ * K and V to half precision; the Q8 cache quantizes each KV head's rows */
+static void store_kv(kro_state *s, int l, int pos, const float *k, const float *v) {
+    if (s->kv_type == ML_F32) return;
+    const ml_config *c = kro_mlb_config(s->m);
+    const size_t row = (size_t)l * c->max_seq + pos;
+    if (s->kv_type == ML_F16) {
+        uint16_t *kh = s->kh + row * c->kv_dim, *vh = s->vh + row * c->kv_dim;
+        for (int i = 0; i < c->kv_dim; i++) { kh[i] = kro_f32_to_f16(k[i]); vh[i] = kro_f32_to_f16(v[i]); }
+        return;
+    }
+    for (int h = 0; h < c->n_kv_heads; h++) {
+        const size_t o = (size_t)h * c->head_dim;
+        kro_quantize_row(s->kq + row * c->kv_dim + o, s->kd + row * c->n_kv_heads + h, k + o, c->head_dim);
+        kro_quantize_row(s->vq + row * c->kv_dim + o, s->vd + row * c->n_kv_heads + h, v + o, c->head_dim);
+    }
+}
+
+/* model/transformer.c:169-180 (kv_layer): layer l's view of the cache */
+static ml_kv_layer kv_layer(const kro_state *s, int l, int window) {
+    const ml_config *c = kro_mlb_config(s->m);
+    const size_t rows = (size_t)l * c->max_seq;
+    if (s->kv_type == ML_F32)
+        return (ml_kv_layer){ s->kcache + rows * c->kv_dim, s->vcache + rows * c->kv_dim, NULL, NULL, NULL, NULL, window,
+                              NULL, NULL };
+    if (s->kv_type == ML_F16)
+        return (ml_kv_layer){ NULL, NULL, NULL, NULL, NULL, NULL, window, s->kh + rows * c->kv_dim, s->vh + rows * c->kv_dim };
+    return (ml_kv_layer){ NULL, NULL, s->kq + rows * c->kv_dim, s->vq + rows * c->kv_dim, s->kd + rows * c->n_kv_heads,
+                          s->vd + rows * c->n_kv_heads, window, NULL, NULL };
+}
+
+/* model/transformer.c:257-306; `cls` = run the classifier. With an F16 or Q8
+ * cache the projections write the staging rows, which store_kv converts. */
 static void forward(kro_state *s, int token, int pos, int cls) {
     const kro_model *m = s->m;
     const ml_config *c = kro_mlb_config(m);
@@ -368,7 +544,9 @@ static void forward(kro_state *s, int token, int pos, int cls) {
     for (int l = 0; l < c->n_layers; l++) {
         const ml_layer *L = kro_mlb_layer(m, l);
         const size_t row = (size_t)l * c->max_seq;
-        float *k = s->kcache + (row + pos) * c->kv_dim, *v = s->vcache + (row + pos) * c->kv_dim;
+        const int conv = s->kv_type != ML_F32;
+        float *k = conv ? s->kcache : s->kcache + (row + pos) * c->kv_dim;
+        float *v = conv ? s->vcache : s->vcache + (row + pos) * c->kv_dim;
         const size_t ro = (size_t)pos * (c->head_dim / 2);
         const float *cs = (L->local_rope ? s->rope_cos_local : s->rope_cos) + ro;
         const float *sn = (L->local_rope ? s->rope_sin_local : s->rope_sin) + ro;
@@ -380,8 +558,8 @@ static void forward(kro_state *s, int token, int pos, int cls) {
         if (L->bq) { kro_add(s->q, L->bq, c->q_dim); kro_add(k, L->bk, c->kv_dim); kro_add(v, L->bv, c->kv_dim); }
         if (L->q_norm) { heads_norm(s->q, L->q_norm, c->n_heads, c); heads_norm(k, L->k_norm, c->n_kv_heads, c); }
         kro_rope(s->q, k, cs, sn, c->head_dim, c->n_heads, c->n_kv_heads);
-        const ml_kv_layer kv = { s->kcache + row * c->kv_dim, s->vcache + row * c->kv_dim, NULL, NULL, NULL, NULL,
-                                 L->window, NULL, NULL };
+        store_kv(s, l, pos, k, v);
+        const ml_kv_layer kv = kv_layer(s, l, L->window);
         kro_attention(s->ao, s->q, &kv, s->att, c, pos);
         kro_quantize_q8(&s->qa_q, s->ao, c->q_dim);
         matvec(s->xb2, &L->wo, &s->qa_q);
@@ -446,6 +624,16 @@ int kro_generate(kro_state *s, const int *prompt, int np, int steps, int *out) {
 }
 
 const float *kro_state_x(const kro_state *s) { return s->x; }
+const void *kro_state_cache(const kro_state *s, const char *name) {
+    if (!strcmp(name, "kh")) return s->kh;
+    if (!strcmp(name, "vh")) return s->vh;
+    if (!strcmp(name, "kq")) return s->kq;
+    if (!strcmp(name, "vq")) return s->vq;
+    if (!strcmp(name, "kd")) return s->kd;
+    if (!strcmp(name, "vd")) return s->vd;
+    return NULL;
+}
+
 const float *kro_state_kcache(const kro_state *s, int layer) {
     const ml_config *c = kro_mlb_config(s->m);
     return s->kcache + (size_t)layer * c->max_seq * c->kv_dim;

@@ -15,7 +15,14 @@
  *                        (tests/test_quant.c:47-70, tests/test_sampler.c:33-40)
  *                        and closed forms (unit-scale matvec = exact int sum)
  *   kro_forward/prefill  logits bit-equal to oracle/_ref/scalar/ml_run
- *                        --dump-logits on generated .mlb models
+ *                        --dump-logits on generated .mlb models, with the
+ *                        F32, F16 and Q8 KV caches (--kv f32|f16|q8)
+ *   kro_f32_to_f16       exhaustively equal to the x86 F16C conversion (all
+ *                        2^32 inputs; NaN -> sign | 0x7e00) and to the
+ *                        reference's ml_f32_to_f16
+ *   F16/Q8 KV kernels    bit-equal to the reference's scalar kernels on the
+ *                        shapes of tests/test_kernels.c:334-426; unit-scale
+ *                        dot_q8 = exact int sum; quantize_row's known answers
  */
 #ifndef KRO_H
 #define KRO_H
@@ -36,6 +43,10 @@ uint64_t kro_expf_check(const float *x, const float *got, size_t n);
 uint64_t kro_expf_check_range(uint64_t lo, const float *got, size_t n, int threads);
 
 uint16_t kro_f32_to_f16(float f);
+void kro_f32_to_f16_range(uint16_t *out, uint32_t lo, size_t n);
+/* inputs in [lo, hi) where kro_f32_to_f16 differs from the x86 F16C
+ * conversion (NaN: the quiet 0x7e00); UINT64_MAX without F16C */
+uint64_t kro_f32_to_f16_mismatches(uint64_t lo, uint64_t hi, int threads);
 float kro_f16_to_f32(uint16_t h);
 
 /* kernels: same signatures and semantics as kernels/scalar/k_scalar.h:7-24 */
@@ -54,7 +65,14 @@ void kro_quantize_row_q4(int8_t *q, float *d, const float *x, int k);
 /* int32 block dot products s[r*nb + b] of rows [r0, r1) (exact) */
 void kro_block_dots(int32_t *s, const ml_qtensor *W, const ml_qact *x, int r0, int r1);
 int kro_argmax(const float *v, int n);
-/* F32-KV attention for one position (ops/ops.c:169-225 order) */
+void kro_quantize_row(int8_t *q, float *d, const float *x, int n);
+void kro_dot_f16(float *s, const float *q, const uint16_t *k, size_t ldk, int rows, int n, float scale);
+void kro_axpy_f16(float *y, const float *a, const uint16_t *x, size_t ldx, int rows, int n);
+void kro_dot_q8(float *s, const int8_t *q, float dq, const int8_t *k, const float *dk, size_t ldk, size_t lddk,
+                int rows, int n, float scale);
+void kro_axpy_q8(float *y, const float *a, const int8_t *x, const float *dx, size_t ldx, size_t lddx, int rows, int n);
+/* attention for one position (ops/ops.c:124-180 order) over the cache kv
+ * points at: F32 (k, v), F16 (kh, vh) or Q8 (kq, vq, kd, vd) */
 void kro_attention(float *out, const float *q, const ml_kv_layer *kv, float *att, const ml_config *cfg, int pos);
 
 /* whole model */
@@ -64,6 +82,8 @@ int kro_model_open(kro_model **m, const char *path);
 const ml_config *kro_model_config(const kro_model *m);
 void kro_model_close(kro_model *m);
 int kro_state_new(kro_state **s, const kro_model *m);
+/* the same with the KV cache type of ml_state_init: ML_F32, ML_F16, ML_Q8_0 */
+int kro_state_new_kv(kro_state **s, const kro_model *m, int kv_type);
 void kro_state_free(kro_state *s);
 /* logits of token at pos into out[vocab] (model/transformer.c:257-306) */
 int kro_forward(kro_state *s, int token, int pos, float *out);
@@ -77,6 +97,8 @@ const float *kro_state_x(const kro_state *s);
 const float *kro_state_kcache(const kro_state *s, int layer);
 /* internal buffer by name ("x", "q", "ao", "kcache", "vcache", "rope_cos", "rope_sin") */
 const float *kro_state_buffer(const kro_state *s, const char *name);
+/* the F16 / Q8 cache arrays by name ("kh", "vh", "kq", "vq", "kd", "vd"), or NULL */
+const void *kro_state_cache(const kro_state *s, const char *name);
 
 #ifdef __cplusplus
 }

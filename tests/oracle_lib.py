@@ -47,6 +47,25 @@ oracle.kro_expf_check.restype = C.c_uint64
 oracle.kro_expf_check.argtypes = [_P, _P, C.c_size_t]
 oracle.kro_expf_check_range.restype = C.c_uint64
 oracle.kro_expf_check_range.argtypes = [C.c_uint64, _P, C.c_size_t, C.c_int]
+oracle.kro_f32_to_f16.restype = C.c_uint16
+oracle.kro_f32_to_f16.argtypes = [C.c_float]
+oracle.kro_f32_to_f16_range.argtypes = [_P, C.c_uint32, C.c_size_t]
+oracle.kro_f32_to_f16_mismatches.restype = C.c_uint64
+oracle.kro_f32_to_f16_mismatches.argtypes = [C.c_uint64, C.c_uint64, C.c_int]
+KV_KERNELS = {
+    "dot_f16": [_P, _P, _P, C.c_size_t, C.c_int, C.c_int, C.c_float],
+    "axpy_f16": [_P, _P, _P, C.c_size_t, C.c_int, C.c_int],
+    "dot_q8": [_P, _P, C.c_float, _P, _P, C.c_size_t, C.c_size_t, C.c_int, C.c_int, C.c_float],
+    "axpy_q8": [_P, _P, _P, _P, C.c_size_t, C.c_size_t, C.c_int, C.c_int],
+}
+for name, args in KV_KERNELS.items():
+    getattr(oracle, "kro_" + name).argtypes = args
+    if ref is not None:
+        getattr(ref, "ml_k_%s_scalar" % name).argtypes = args
+oracle.kro_quantize_row.argtypes = [_P, _P, _P, C.c_int]
+oracle.kro_state_new_kv.argtypes = [C.POINTER(_P), _P, C.c_int]
+oracle.kro_state_cache.restype = _P
+oracle.kro_state_cache.argtypes = [_P, C.c_char_p]
 oracle.kro_f16_to_f32.restype = C.c_float
 oracle.kro_f16_to_f32.argtypes = [C.c_uint16]
 oracle.kro_dequant_row.argtypes = [_P, _P, C.c_int]
@@ -69,6 +88,9 @@ oracle.kro_state_buffer.argtypes = [_P, C.c_char_p]
 oracle.kro_state_x.restype = C.POINTER(C.c_float)
 oracle.kro_state_x.argtypes = [_P]
 if ref is not None:
+    ref.ml_quantize_row.argtypes = [_P, _P, _P, C.c_int]
+    ref.ml_f32_to_f16.restype = C.c_uint16
+    ref.ml_f32_to_f16.argtypes = [C.c_float]
     ref.ml_dequant_row.argtypes = [_P, _P, C.c_int]
     ref.ml_quantize_row_q4.argtypes = [_P, _P, _P, C.c_int]
 
@@ -99,13 +121,19 @@ def quantize(x):
 
 
 class OracleModel:
-    def __init__(self, path):
+    def __init__(self, path, kv_type=K.ML_F32):
         self.m = _P()
         st = oracle.kro_model_open(C.byref(self.m), path.encode())
         assert st == 0, "oracle cannot open %s (%d)" % (path, st)
         self.cfg = oracle.kro_model_config(self.m).contents
         self.s = _P()
-        assert oracle.kro_state_new(C.byref(self.s), self.m) == 0
+        assert oracle.kro_state_new_kv(C.byref(self.s), self.m, kv_type) == 0
+
+    def cache(self, name, count, dtype):
+        """the F16 / Q8 cache array by name ("kh", "vh", "kq", "vq", "kd", "vd")"""
+        p = oracle.kro_state_cache(self.s, name.encode())
+        assert p, name
+        return np.ctypeslib.as_array(C.cast(p, C.POINTER(np.ctypeslib.as_ctypes_type(dtype))), shape=(count,)).copy()
 
     def forward(self, tok, pos):
         out = np.empty(self.cfg.vocab, dtype=np.float32)

@@ -266,6 +266,129 @@ def test_f16_widening_closed_form():
     assert np.array_equal(bits(got[finite]), bits(w[finite]))
 
 
+# ---- F16 and Q8 KV caches (k_scalar.c:124-155, ops/ops.c:81-96) ----
+
+def test_f32_to_f16_exhaustive_vs_ieee():
+    # every float32 input against the x86 F16C conversion (IEEE round to
+    # nearest even); NaN inputs become the quiet NaN 0x7e00 with their sign
+    bad = oracle.kro_f32_to_f16_mismatches(0, 1 << 32, os.cpu_count() or 8)
+    if bad == 2**64 - 1:
+        pytest.skip("host CPU without F16C")
+    assert bad == 0
+
+
+def test_f32_to_f16_sample_vs_numpy():
+    # the same rule against numpy's IEEE cast on a sample of every binade
+    u = np.concatenate([RNG.integers(0, 1 << 32, 1 << 20, dtype=np.uint64),
+                        np.arange(0x477FE000, 0x47800100, dtype=np.uint64),
+                        np.arange(0x33000000 - 256, 0x33000000 + 256, dtype=np.uint64),
+                        np.arange(0x387FFF00, 0x38800100, dtype=np.uint64)]).astype(np.uint32)
+    u = np.concatenate([u, u | np.uint32(0x80000000)])
+    out = np.empty(1, np.uint16)
+    got = np.empty(len(u), np.uint16)
+    for i, b in enumerate(u[:4096]):
+        oracle.kro_f32_to_f16_range(out.ctypes.data, int(b), 1)
+        got[i] = out[0]
+    x = u[:4096].view(np.float32)
+    with np.errstate(over="ignore", invalid="ignore"):
+        want = x.astype(np.float16).view(np.uint16)
+    want = np.where(np.isnan(x), ((u[:4096] >> 16) & 0x8000).astype(np.uint16) | np.uint16(0x7E00), want)
+    assert np.array_equal(got[:4096], want)
+
+
+@needs_ref
+def test_f32_to_f16_matches_reference():
+    x = np.concatenate([f32(RNG.normal(0, 1, 4000)), f32(RNG.normal(0, 3e4, 1000)), f32(RNG.uniform(-1e-4, 1e-4, 1000)),
+                        f32([0.0, -0.0, 65504.0, 65519.99, 65520.0, -65520.0, 6.1e-5, 5.96e-8, 2.98e-8, 2.99e-8,
+                             np.inf, -np.inf, np.nan])])
+    got = [oracle.kro_f32_to_f16(float(v)) for v in x]
+    want = [ref.ml_f32_to_f16(float(v)) for v in x]
+    assert got == want
+
+
+def q8_rows(n):
+    return RNG.integers(-127, 128, n).astype(np.int8)
+
+
+@needs_ref
+@pytest.mark.parametrize("n", [1, 7, 32, 64, 128, 300])
+@pytest.mark.parametrize("rows", [1, 3, 4, 5, 9])
+def test_kv_kernels_match_reference(n, rows):
+    # the shapes of tests/test_kernels.c:334-426 (strided rows and scales)
+    A = f32(RNG.uniform(0, 1, n))
+    K16 = np.array([oracle.kro_f32_to_f16(float(v)) for v in RNG.uniform(0, 1, (n + 3) * rows)], np.uint16)
+    a = f32(RNG.uniform(0, 1, rows))
+    s0, s1 = np.zeros(rows, np.float32), np.zeros(rows, np.float32)
+    oracle.kro_dot_f16(s0.ctypes.data, A.ctypes.data, K16.ctypes.data, n + 3, rows, n, 0.125)
+    ref.ml_k_dot_f16_scalar(s1.ctypes.data, A.ctypes.data, K16.ctypes.data, n + 3, rows, n, 0.125)
+    assert np.array_equal(bits(s0), bits(s1))
+    y0 = f32(RNG.uniform(-2, 2, n))
+    y1 = y0.copy()
+    oracle.kro_axpy_f16(y0.ctypes.data, a.ctypes.data, K16.ctypes.data, n + 3, rows, n)
+    ref.ml_k_axpy_f16_scalar(y1.ctypes.data, a.ctypes.data, K16.ctypes.data, n + 3, rows, n)
+    assert np.array_equal(bits(y0), bits(y1))
+    Kq, q, dk = q8_rows((n + 5) * rows), q8_rows(n), f32(RNG.uniform(0.001, 0.05, 3 * rows))
+    oracle.kro_dot_q8(s0.ctypes.data, q.ctypes.data, 0.02, Kq.ctypes.data, dk.ctypes.data, n + 5, 3, rows, n, 0.125)
+    ref.ml_k_dot_q8_scalar(s1.ctypes.data, q.ctypes.data, 0.02, Kq.ctypes.data, dk.ctypes.data, n + 5, 3, rows, n,
+                           0.125)
+    assert np.array_equal(bits(s0), bits(s1))
+    dx = f32(RNG.uniform(0.001, 0.05, 2 * rows))
+    y0 = f32(RNG.uniform(-2, 2, n))
+    y1 = y0.copy()
+    oracle.kro_axpy_q8(y0.ctypes.data, a.ctypes.data, Kq.ctypes.data, dx.ctypes.data, n + 5, 2, rows, n)
+    ref.ml_k_axpy_q8_scalar(y1.ctypes.data, a.ctypes.data, Kq.ctypes.data, dx.ctypes.data, n + 5, 2, rows, n)
+    assert np.array_equal(bits(y0), bits(y1))
+
+
+def test_dot_q8_exact_integer_sum():
+    # unit scales: the score is the int32 dot itself, exactly (|sum| < 2^24)
+    n, rows = 128, 9
+    K8, q = q8_rows(n * rows), q8_rows(n)
+    dk = np.ones(rows, np.float32)
+    s = np.zeros(rows, np.float32)
+    oracle.kro_dot_q8(s.ctypes.data, q.ctypes.data, 1.0, K8.ctypes.data, dk.ctypes.data, n, 1, rows, n, 1.0)
+    want = (K8.reshape(rows, n).astype(np.int64) * q.astype(np.int64)).sum(axis=1)
+    assert np.array_equal(s.astype(np.int64), want)
+    # the float factors apply in the order ((float)sum * (dq * scale)) * dk
+    dk = f32(RNG.uniform(0.001, 0.05, rows))
+    oracle.kro_dot_q8(s.ctypes.data, q.ctypes.data, 0.02, K8.ctypes.data, dk.ctypes.data, n, 1, rows, n, 0.125)
+    c = np.float32(0.02) * np.float32(0.125)
+    assert np.allclose(s, want * float(c) * dk, rtol=1e-6)
+
+
+def test_axpy_q8_weight_then_value():
+    # y += (a_t * dx_t) * x_t: with x = 1 the increments are the weights a_t * dx_t
+    n, rows = 16, 5
+    a, dx = f32(RNG.uniform(0, 1, rows)), f32(RNG.uniform(0.001, 0.05, rows))
+    X = np.ones(n * rows, np.int8)
+    y = np.zeros(n, np.float32)
+    oracle.kro_axpy_q8(y.ctypes.data, a.ctypes.data, X.ctypes.data, dx.ctypes.data, n, 1, rows, n)
+    want = np.float32(0.0)
+    for t in range(rows):
+        want = np.float32(want + np.float32(a[t] * dx[t]))
+    assert np.all(bits(y) == bits(np.full(n, want, np.float32)))
+
+
+@needs_ref
+@pytest.mark.parametrize("n", [32, 64, 128, 300])
+def test_quantize_row_matches_reference(n):
+    for x in (f32(RNG.normal(0, 2, n)), np.zeros(n, np.float32), f32(np.full(n, 1e-37)),
+              f32(np.r_[[127.0, 0.5, -0.5, 1.5, 2.5, -2.5], np.zeros(n - 6)])):
+        q0, q1 = np.zeros(n, np.int8), np.zeros(n, np.int8)
+        d0, d1 = np.zeros(1, np.float32), np.zeros(1, np.float32)
+        oracle.kro_quantize_row(q0.ctypes.data, d0.ctypes.data, x.ctypes.data, n)
+        ref.ml_quantize_row(q1.ctypes.data, d1.ctypes.data, x.ctypes.data, n)
+        assert np.array_equal(q0, q1) and bits(d0)[0] == bits(d1)[0]
+
+
+def test_quantize_row_one_scale():
+    # one scale for the whole row, the largest magnitude at +-127, ties away from zero
+    x = f32(np.r_[[127.0, 0.5, -0.5, 1.5, 2.5, -2.5], RNG.uniform(-1, 1, 122)])
+    q, d = np.zeros(128, np.int8), np.zeros(1, np.float32)
+    oracle.kro_quantize_row(q.ctypes.data, d.ctypes.data, x.ctypes.data, 128)
+    assert d[0] == 1.0 and q[0] == 127 and q[1:6].tolist() == [1, -1, 2, 3, -3]
+
+
 # ---- whole model: the oracle's forward vs the reference's ml_run ----
 
 SMALL = {
@@ -325,3 +448,27 @@ def test_binding_declares_every_export():
         syms = {l.split()[-1] for l in out.splitlines() if " T " in l}
         exported = {s for s in syms if s.startswith("krh_") or s.startswith("kr_")}
         assert exported and exported <= lib.declared(), sorted(exported - lib.declared())
+
+
+@needs_ref
+@pytest.mark.parametrize("kv", ["q8", "f16"])
+@pytest.mark.parametrize("name", ["c1_q8", "llama3_rope_gqa_q4", "qwen_like_q4mix"])
+def test_forward_matches_reference_kv(name, kv, workdir):
+    # ml_run --kv q8 / --kv f16 (app/ml_run.c:277-281): logits and greedy ids
+    path = os.path.join(workdir, name + ".mlb")
+    K.gen_mlb(path, **SMALL[name])
+    kvt = K.ML_Q8_0 if kv == "q8" else K.ML_F16
+    om = O.OracleModel(path, kvt)
+    V = om.cfg.vocab
+    toks = [int(t) for t in np.random.default_rng(6).integers(1, V, 12)]
+    dump = path + "." + kv + ".logits"
+    O.ref_ml_run(path, toks, len(toks), dump=dump, extra=("--kv", kv))
+    want = np.fromfile(dump, dtype=np.float32).reshape(len(toks), V)
+    got = om.prefill(toks, 0, logits=True)
+    assert np.array_equal(bits(got), bits(want))
+    om.close()
+    om = O.OracleModel(path, kvt)
+    steps = min(om.cfg.max_seq, 60)
+    ids_ref, _ = O.ref_ml_run(path, toks[:5], steps, extra=("--kv", kv))
+    assert np.array_equal(om.generate(toks[:5], steps), ids_ref)
+    om.close()
