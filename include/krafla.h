@@ -41,8 +41,9 @@ void kr_model_free(kr_model *m);
 
 /* ---- decoding state (KV cache and activations in HBM) ---- */
 typedef struct kr_state kr_state;
-/* kv_type: ML_F32 only. ML_E_SHAPE for model features this backend does not
- * run (q/k norm, post-norms, GELU, soft-capping). */
+/* kv_type: ML_F32, ML_F16 or ML_Q8_0 (ml_state_init, model/transformer.c:51-56).
+ * ML_E_SHAPE for model features this backend does not run (q/k norm,
+ * post-norms, GELU, soft-capping). */
 ml_status kr_state_new(kr_state **s, kr_model *m, int kv_type);
 void kr_state_free(kr_state *s);
 /* ml_forward: logits of token at pos into logits[vocab] (host memory) */
@@ -57,7 +58,9 @@ int kr_generate(kr_state *s, const int *prompt, int np, int steps, int *out, dou
 const float *kr_state_x_device(const kr_state *s);
 /* device address of an internal buffer by name ("x", "q", "ao", "hb", "att",
  * "logits", "kcache", "vcache", "rope_cos", "rope_sin", "qa_dim", "qd_dim",
- * "qa_q", "qd_q", "qa_hid", "qd_hid"), or NULL; for tests */
+ * "qa_q", "qd_q", "qa_hid", "qd_hid", "kd", "vd"), or NULL; for tests. The
+ * caches hold floats, halves or int8 by kv_type; kd, vd are the Q8 cache's
+ * row scales [n_layers][max_seq][n_kv_heads]. */
 const void *kr_state_buffer(const kr_state *s, const char *name);
 /* tokens per batched prefill step (ml_state.batch, model/transformer.h:37):
  * 1 = token by token (replays of the decode step), 0 = the default (2048,

@@ -117,6 +117,13 @@ void krh_rmsnorm_matvec_qkv(float *q, float *kc, float *vc, const krh_mat *wq, c
                             float eps, const float *rope_cos, const float *rope_sin, int head_dim, const int *pos);
 void krh_rmsnorm_matvec_swiglu(float *h, const krh_mat *w1, const krh_mat *w3, const float *x, const float *nw,
                                float eps);
+/* krh_rmsnorm_matvec_qkv for an F16 or Q8 cache: k and v go to the staging
+ * rows k, v [kv_dim] (the state's kbuf, vbuf: model/transformer.c:262-263),
+ * which krh_store_kv then converts into the cache */
+void krh_rmsnorm_matvec_qkv_stage(float *q, float *k, float *v, const krh_mat *wq, const krh_mat *wk,
+                                  const krh_mat *wv, const float *bq, const float *bk, const float *bv, const float *x,
+                                  const float *nw, float eps, const float *rope_cos, const float *rope_sin,
+                                  int head_dim, const int *pos);
 
 /* Causal GQA attention of one position *pos over this layer's F32 cache
  * (ops/ops.c:169-225): ao [n_heads * head_dim]; aq, ad (nullable) receive its
@@ -124,6 +131,23 @@ void krh_rmsnorm_matvec_swiglu(float *h, const krh_mat *w1, const krh_mat *w3, c
  * == 0, at most 16 query heads per KV head. */
 void krh_attention(float *ao, int8_t *aq, float *ad, float *att, const float *q, const float *kc, const float *vc,
                    int n_heads, int n_kv_heads, int head_dim, int max_seq, int window, float scale, const int *pos);
+/* The same over one layer's cache of any type (ml_attention, ops/ops.c:124-180):
+ * kv (a host struct of device pointers, ops/ops.h:16-22) names the layer's F32
+ * rows (k, v), F16 rows (kh, vh) or Q8 rows and row scales (kq, vq, kd, vd),
+ * and the window. The Q8 scores quantize each query head with one scale
+ * (ops/ops.c:171-173) and take the exact int32 dot (k_scalar.c:137-155). ntok
+ * positions *pos0 + t, t < ntok (ml_attention_batch for ntok > 1): ao, q
+ * [ntok][q_dim], att [ntok][n_heads][max_seq]; last_pos = *pos0 + ntok - 1
+ * sizes the launch (max_seq - 1 when only the device knows *pos0). */
+void krh_attention_kv(float *ao, float *att, const float *q, const ml_kv_layer *kv, int n_heads, int n_kv_heads,
+                      int head_dim, int max_seq, float scale, const int *pos0, int ntok, int last_pos);
+/* store_kv (model/transformer.c:191-205) of positions *pos0 + t, t < ntok:
+ * the staging rows k, v [ntok][n_kv_heads * head_dim] into one layer's cache
+ * rows kc, vc [max_seq][kv_dim]. kv_type ML_F16: halves, rounded as
+ * core/ml.c:39-53 does; ML_Q8_0: int8, each KV head's row quantized with one
+ * scale (ops/ops.c:81-96) into kd, vd [max_seq][n_kv_heads]. */
+void krh_store_kv(int kv_type, void *kc, void *vc, float *kd, float *vd, const float *k, const float *v,
+                  int n_kv_heads, int head_dim, const int *pos0, int ntok);
 
 /* ---- batched prompt prefill (model/transformer.c:385-425) ---- */
 
@@ -139,6 +163,10 @@ void krh_matmul(float *Y, int ldy, const krh_mat *W, const int8_t *xq, const flo
 void krh_matmul_qkv(float *q, float *kc, float *vc, const krh_mat *wq, const krh_mat *wk, const krh_mat *wv,
                     const float *bq, const float *bk, const float *bv, const int8_t *xq, const float *xdT, int ldx,
                     int T, const float *rope_cos, const float *rope_sin, int head_dim, int pos0);
+/* the same for an F16 or Q8 cache: k and v to the staging rows [T][kv_dim] */
+void krh_matmul_qkv_stage(float *q, float *k, float *v, const krh_mat *wq, const krh_mat *wk, const krh_mat *wv,
+                          const float *bq, const float *bk, const float *bv, const int8_t *xq, const float *xdT,
+                          int ldx, int T, const float *rope_cos, const float *rope_sin, int head_dim, int pos0);
 /* causal attention of ntok tokens at positions *pos0 + t (ml_attention_batch,
  * ops/ops.c:216-238): ao, q [ntok][q_dim], att [ntok][n_heads][max_seq];
  * last_pos = *pos0 + ntok - 1 (sizes the launch) */
@@ -193,8 +221,9 @@ void krh_tune(int key, int value);
 
 /* ---- self-checks for tests ---- */
 /* y[i] = op(a[i], b[i]) as the kernels compute it: expf(a), sqrtf(a), a / b,
- * or rmsnorm's 1 / sqrtf(a / b + 1e-5) */
-enum { KRH_MATH_EXPF = 0, KRH_MATH_SQRT = 1, KRH_MATH_DIV = 2, KRH_MATH_RMS_INV = 3 };
+ * rmsnorm's 1 / sqrtf(a / b + 1e-5), or the F16 cache's rounding of a (the
+ * binary16 bits in the low 16 bits of y[i]) */
+enum { KRH_MATH_EXPF = 0, KRH_MATH_SQRT = 1, KRH_MATH_DIV = 2, KRH_MATH_RMS_INV = 3, KRH_MATH_F2H = 4 };
 void krh_math_batch(int op, float *y, const float *a, const float *b, size_t n);
 /* y[i] = f16 -> f32 of h[i] */
 void krh_h2f_batch(float *y, const uint16_t *h, size_t n);

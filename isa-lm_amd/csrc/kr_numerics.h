@@ -74,6 +74,16 @@ __device__ __forceinline__ float kr_expf(float x) { return kr_expf_tab(x, kr_exp
 // IEEE binary16 -> float32; exact for every input (subnormals included).
 __device__ __forceinline__ float kr_h2f(uint16_t h) { return __half2float(__ushort_as_half(h)); }
 
+// float32 -> IEEE binary16 bits as core/ml.c:39-53 gives them: round to
+// nearest even (the conversion instruction in the default round mode, with
+// half-precision subnormals kept), overflow to infinity, and every NaN to the
+// quiet NaN 0x7e00 with the input's sign.
+__device__ __forceinline__ uint16_t kr_f2h(float f) {
+    const uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)(((u >> 16) & 0x8000u) | 0x7e00u);
+    return __half_as_ushort(__float2half_rn(f));
+}
+
 __device__ __forceinline__ float kr_scale(const void *d, size_t i, int d16) {
     return d16 ? kr_h2f(((const uint16_t *)d)[i]) : ((const float *)d)[i];
 }

@@ -280,10 +280,11 @@ extern "C" void krh_matmul(float *Y, int ldy, const krh_mat *W, const int8_t *xq
     else launch_mm<MM_STORE>(a, a.w[0]);
 }
 
-extern "C" void krh_matmul_qkv(float *q, float *kc, float *vc, const krh_mat *wq, const krh_mat *wk,
-                               const krh_mat *wv, const float *bq, const float *bk, const float *bv, const int8_t *xq,
-                               const float *xdT, int ldx, int T, const float *rope_cos, const float *rope_sin,
-                               int head_dim, int pos0) {
+// k and v go to the F32 cache rows pos0 + t, or with stage set to the
+// staging rows kc, vc [T][kv_dim] of an F16 / Q8 cache
+static void matmul_qkv(float *q, float *kc, float *vc, const krh_mat *wq, const krh_mat *wk, const krh_mat *wv,
+                       const float *bq, const float *bk, const float *bv, const int8_t *xq, const float *xdT, int ldx,
+                       int T, const float *rope_cos, const float *rope_sin, int head_dim, int pos0, bool stage) {
     if (wq->cols != wk->cols || wq->cols != wv->cols || wk->rows != wv->rows || head_dim % 2 || wq->type != wk->type ||
         wq->d16 != wk->d16 || wv->d16 != wq->d16) {
         kr_fail(ML_E_SHAPE, "matmul qkv shapes", hipSuccess);
@@ -302,9 +303,9 @@ extern "C" void krh_matmul_qkv(float *q, float *kc, float *vc, const krh_mat *wq
     // q rows [t][q_dim]; k and v straight into the cache rows pos0 + t
     a.y[0] = q;
     a.ldy[0] = wq->rows;
-    a.y[1] = kc + (size_t)pos0 * wk->rows;
+    a.y[1] = kc + (stage ? 0 : (size_t)pos0 * wk->rows);
     a.ldy[1] = wk->rows;
-    a.y[2] = vc + (size_t)pos0 * wv->rows;
+    a.y[2] = vc + (stage ? 0 : (size_t)pos0 * wv->rows);
     a.ldy[2] = wv->rows;
     a.bias[0] = bq;
     a.bias[1] = bk;
@@ -331,6 +332,20 @@ extern "C" void krh_matmul_qkv(float *q, float *kc, float *vc, const krh_mat *wq
     c.w[0] = c.w[1] = c.w[2];
     c.nmat = 3;
     launch_mm<MM_QKV>(c, c.w[2]);
+}
+
+extern "C" void krh_matmul_qkv(float *q, float *kc, float *vc, const krh_mat *wq, const krh_mat *wk,
+                               const krh_mat *wv, const float *bq, const float *bk, const float *bv, const int8_t *xq,
+                               const float *xdT, int ldx, int T, const float *rope_cos, const float *rope_sin,
+                               int head_dim, int pos0) {
+    matmul_qkv(q, kc, vc, wq, wk, wv, bq, bk, bv, xq, xdT, ldx, T, rope_cos, rope_sin, head_dim, pos0, false);
+}
+
+extern "C" void krh_matmul_qkv_stage(float *q, float *k, float *v, const krh_mat *wq, const krh_mat *wk,
+                                     const krh_mat *wv, const float *bq, const float *bk, const float *bv,
+                                     const int8_t *xq, const float *xdT, int ldx, int T, const float *rope_cos,
+                                     const float *rope_sin, int head_dim, int pos0) {
+    matmul_qkv(q, k, v, wq, wk, wv, bq, bk, bv, xq, xdT, ldx, T, rope_cos, rope_sin, head_dim, pos0, true);
 }
 
 extern "C" void krh_silu_quant(int8_t *q, float *dT, int ldd, const float *g, const float *u, int n, int ntok) {

@@ -167,7 +167,11 @@ void kr_model_free(kr_model *m) {
 struct kr_state {
     kr_model *m;
     /* device buffers */
-    float *x, *q, *ao, *hb, *att, *logits, *kcache, *vcache, *rope_cos, *rope_sin, *rope_cos_l, *rope_sin_l;
+    float *x, *q, *ao, *hb, *att, *logits, *rope_cos, *rope_sin, *rope_cos_l, *rope_sin_l;
+    int kv_type;              /* ML_F32, ML_F16 or ML_Q8_0 (ml_state.kv_type, model/transformer.h:19-26) */
+    void *kcache, *vcache;    /* [n_layers][max_seq][kv_dim] floats, halves or int8 */
+    float *kd, *vd;           /* Q8: row scales [n_layers][max_seq][n_kv_heads] */
+    float *kst, *vst;         /* F16 / Q8: the projections' K and V rows (kbuf, vbuf) */
     int8_t *qa_dim, *qa_q, *qa_hid;
     float *qd_dim, *qd_q, *qd_hid;
     int *tok, *pos, *prompt, *log;
@@ -180,9 +184,43 @@ struct kr_state {
     /* batched prefill buffers (allocated on first use): [ldx] token rows */
     void *bmem;
     int ldx;                  /* capacity, a multiple of 128 */
-    float *bx, *bq, *bao, *bh1, *bh3, *batt, *blog, *bxd;
+    float *bx, *bq, *bao, *bh1, *bh3, *batt, *blog, *bxd, *bkst, *bvst;
     int8_t *bxq;
 };
+
+static size_t kv_elem(int kv_type) { return kv_type == ML_F32 ? 4 : kv_type == ML_F16 ? 2 : 1; }
+
+/* layer l's cache view (model/transformer.c:169-180) over device memory */
+static ml_kv_layer kv_layer(const kr_state *s, int l) {
+    const ml_config *c = &s->m->cfg;
+    const size_t rows = (size_t)l * c->max_seq, e = (size_t)c->kv_dim * kv_elem(s->kv_type);
+    const char *kc = (const char *)s->kcache + rows * e, *vc = (const char *)s->vcache + rows * e;
+    ml_kv_layer kv = { 0 };
+    kv.window = s->m->layers[l].window;
+    if (s->kv_type == ML_F32) {
+        kv.k = (const float *)kc;
+        kv.v = (const float *)vc;
+    } else if (s->kv_type == ML_F16) {
+        kv.kh = (const uint16_t *)kc;
+        kv.vh = (const uint16_t *)vc;
+    } else {
+        kv.kq = (const int8_t *)kc;
+        kv.vq = (const int8_t *)vc;
+        kv.kd = s->kd + rows * c->n_kv_heads;
+        kv.vd = s->vd + rows * c->n_kv_heads;
+    }
+    return kv;
+}
+
+/* store_kv of ntok positions from *s->pos into layer l (F16 / Q8) */
+static void store_kv(kr_state *s, int l, const float *k, const float *v, int ntok) {
+    const ml_config *c = &s->m->cfg;
+    const size_t rows = (size_t)l * c->max_seq, e = (size_t)c->kv_dim * kv_elem(s->kv_type);
+    const int q8 = s->kv_type == ML_Q8_0;
+    krh_store_kv(s->kv_type, (char *)s->kcache + rows * e, (char *)s->vcache + rows * e,
+                 q8 ? s->kd + rows * c->n_kv_heads : NULL, q8 ? s->vd + rows * c->n_kv_heads : NULL, k, v,
+                 c->n_kv_heads, c->head_dim, s->pos, ntok);
+}
 
 /* tokens per batched prefill step by default (the attention scratch is
  * [step][n_heads][max_seq] floats) */
@@ -243,14 +281,23 @@ static void issue_step(kr_state *s, int cls) {
     for (int l = 0; l < c->n_layers; l++) {
         const struct kr_dev_layer *D = &m->d_layers[l];
         const ml_layer *L = &m->layers[l];
-        float *kc = s->kcache + (size_t)l * lkv, *vc = s->vcache + (size_t)l * lkv;
         const float *cs = L->local_rope ? s->rope_cos_l : s->rope_cos, *sn = L->local_rope ? s->rope_sin_l : s->rope_sin;
         /* each norm runs inside the launch that consumes it, under that
          * launch's first weight loads */
-        krh_rmsnorm_matvec_qkv(s->q, kc, vc, &D->wq, &D->wk, &D->wv, D->bq, D->bk, D->bv, s->x, D->attn_norm,
-                               c->norm_eps, cs, sn, c->head_dim, s->pos);
-        krh_attention(s->ao, NULL, NULL, s->att, s->q, kc, vc, c->n_heads, c->n_kv_heads, c->head_dim,
-                      c->max_seq, L->window, c->attn_scale, s->pos);
+        if (s->kv_type == ML_F32) {
+            float *kc = (float *)s->kcache + (size_t)l * lkv, *vc = (float *)s->vcache + (size_t)l * lkv;
+            krh_rmsnorm_matvec_qkv(s->q, kc, vc, &D->wq, &D->wk, &D->wv, D->bq, D->bk, D->bv, s->x, D->attn_norm,
+                                   c->norm_eps, cs, sn, c->head_dim, s->pos);
+            krh_attention(s->ao, NULL, NULL, s->att, s->q, kc, vc, c->n_heads, c->n_kv_heads, c->head_dim,
+                          c->max_seq, L->window, c->attn_scale, s->pos);
+        } else {
+            const ml_kv_layer kv = kv_layer(s, l);
+            krh_rmsnorm_matvec_qkv_stage(s->q, s->kst, s->vst, &D->wq, &D->wk, &D->wv, D->bq, D->bk, D->bv, s->x,
+                                         D->attn_norm, c->norm_eps, cs, sn, c->head_dim, s->pos);
+            store_kv(s, l, s->kst, s->vst, 1);
+            krh_attention_kv(s->ao, s->att, s->q, &kv, c->n_heads, c->n_kv_heads, c->head_dim, c->max_seq,
+                             c->attn_scale, s->pos, 1, c->max_seq - 1);
+        }
         krh_matvec_f(s->x, &D->wo, s->ao, 1);
         krh_rmsnorm_matvec_swiglu(s->hb, &D->w1, &D->w3, s->x, D->ffn_norm, c->norm_eps);
         krh_quantize_q8(s->qa_hid, s->qd_hid, s->hb, c->hidden_dim, 1);
@@ -295,7 +342,8 @@ static ml_status run_step(kr_state *s, int kind) {
 ml_status kr_state_new(kr_state **out, kr_model *m, int kv_type) {
     *out = NULL;
     const ml_config *c = &m->cfg;
-    if (kv_type != ML_F32) return kr_seterr(ML_E_SHAPE, "only the F32 KV cache is supported");
+    if (kv_type != ML_F32 && kv_type != ML_F16 && kv_type != ML_Q8_0)
+        return kr_seterr(ML_E_SHAPE, "KV cache type %d: F32, F16 or Q8_0", kv_type);
     if (c->qk_norm || c->post_norms || c->act != ML_ACT_SILU || c->attn_softcap > 0.0f || c->final_softcap > 0.0f)
         return kr_seterr(ML_E_SHAPE, "model uses q/k norm, post-norms, GELU or soft-capping: not supported");
     ml_status st = kr_model_upload(m);
@@ -303,14 +351,19 @@ ml_status kr_state_new(kr_state **out, kr_model *m, int kv_type) {
     kr_state *s = calloc(1, sizeof *s);
     if (!s) return ML_E_NOMEM;
     s->m = m;
+    s->kv_type = kv_type;
     const size_t f = sizeof(float), kv = (size_t)c->n_layers * c->max_seq * c->kv_dim;
+    const size_t ks = (size_t)c->n_layers * c->max_seq * c->n_kv_heads;
+    const int q8 = kv_type == ML_Q8_0, conv = kv_type != ML_F32;
     const size_t half = (size_t)c->max_seq * (c->head_dim / 2);
     const int local = c->rope_local_theta > 0.0f;
     struct { void **p; size_t n; } parts[] = {
         { (void **)&s->x, f * c->dim }, { (void **)&s->q, f * c->q_dim }, { (void **)&s->ao, f * c->q_dim },
         { (void **)&s->hb, f * c->hidden_dim },
         { (void **)&s->att, f * (size_t)c->n_heads * c->max_seq }, { (void **)&s->logits, f * c->vocab },
-        { (void **)&s->kcache, f * kv }, { (void **)&s->vcache, f * kv },
+        { (void **)&s->kcache, kv_elem(kv_type) * kv }, { (void **)&s->vcache, kv_elem(kv_type) * kv },
+        { (void **)&s->kd, q8 ? f * ks : 0 }, { (void **)&s->vd, q8 ? f * ks : 0 },
+        { (void **)&s->kst, conv ? f * c->kv_dim : 0 }, { (void **)&s->vst, conv ? f * c->kv_dim : 0 },
         { (void **)&s->rope_cos, f * half }, { (void **)&s->rope_sin, f * half },
         { (void **)&s->rope_cos_l, local ? f * half : 0 }, { (void **)&s->rope_sin_l, local ? f * half : 0 },
         { (void **)&s->qa_dim, (size_t)c->dim }, { (void **)&s->qd_dim, f * c->dim / QK },
@@ -387,9 +440,9 @@ const float *kr_state_x_device(const kr_state *s) { return s->x; }
 
 const void *kr_state_buffer(const kr_state *s, const char *name) {
     static const char *const names[] = { "x", "q", "ao", "hb", "att", "logits", "kcache", "vcache", "rope_cos",
-                                         "rope_sin", "qa_dim", "qd_dim", "qa_q", "qd_q", "qa_hid", "qd_hid" };
+                                         "rope_sin", "qa_dim", "qd_dim", "qa_q", "qd_q", "qa_hid", "qd_hid", "kd", "vd" };
     const void *ptrs[] = { s->x, s->q, s->ao, s->hb, s->att, s->logits, s->kcache, s->vcache, s->rope_cos,
-                           s->rope_sin, s->qa_dim, s->qd_dim, s->qa_q, s->qd_q, s->qa_hid, s->qd_hid };
+                           s->rope_sin, s->qa_dim, s->qd_dim, s->qa_q, s->qd_q, s->qa_hid, s->qd_hid, s->kd, s->vd };
     for (size_t i = 0; i < sizeof names / sizeof names[0]; i++)
         if (!strcmp(names[i], name)) return ptrs[i];
     return NULL;
@@ -433,6 +486,8 @@ static ml_status batch_buffers(kr_state *s, int with_logits) {
         { (void **)&s->bh3, f * L * c->hidden_dim }, { (void **)&s->batt, f * L * c->n_heads * (size_t)c->max_seq },
         { (void **)&s->bxq, L * wide }, { (void **)&s->bxd, f * L * (wide / QK) },
         { (void **)&s->blog, with_logits ? f * L * c->vocab : 0 },
+        { (void **)&s->bkst, s->kv_type != ML_F32 ? f * L * c->kv_dim : 0 },
+        { (void **)&s->bvst, s->kv_type != ML_F32 ? f * L * c->kv_dim : 0 },
     };
     size_t total = 0;
     for (size_t i = 0; i < sizeof parts / sizeof parts[0]; i++) total += RUP(parts[i].n);
@@ -463,13 +518,22 @@ static ml_status prefill_step(kr_state *s, const int *tokens, int T, int p0, flo
     for (int l = 0; l < c->n_layers; l++) {
         const struct kr_dev_layer *D = &m->d_layers[l];
         const ml_layer *L = &m->layers[l];
-        float *kc = s->kcache + (size_t)l * lkv, *vc = s->vcache + (size_t)l * lkv;
         const float *cs = L->local_rope ? s->rope_cos_l : s->rope_cos, *sn = L->local_rope ? s->rope_sin_l : s->rope_sin;
         krh_rmsnorm_q8_t(s->bxq, s->bxd, ldx, NULL, s->bx, D->attn_norm, c->dim, c->norm_eps, T);
-        krh_matmul_qkv(s->bq, kc, vc, &D->wq, &D->wk, &D->wv, D->bq, D->bk, D->bv, s->bxq, s->bxd, ldx, T, cs, sn,
-                       c->head_dim, p0);
-        krh_attention_batch(s->bao, s->batt, s->bq, kc, vc, c->n_heads, c->n_kv_heads, c->head_dim, c->max_seq,
-                            L->window, c->attn_scale, s->pos, T, p0 + T - 1);
+        if (s->kv_type == ML_F32) {
+            float *kc = (float *)s->kcache + (size_t)l * lkv, *vc = (float *)s->vcache + (size_t)l * lkv;
+            krh_matmul_qkv(s->bq, kc, vc, &D->wq, &D->wk, &D->wv, D->bq, D->bk, D->bv, s->bxq, s->bxd, ldx, T, cs,
+                           sn, c->head_dim, p0);
+            krh_attention_batch(s->bao, s->batt, s->bq, kc, vc, c->n_heads, c->n_kv_heads, c->head_dim, c->max_seq,
+                                L->window, c->attn_scale, s->pos, T, p0 + T - 1);
+        } else {
+            const ml_kv_layer kv = kv_layer(s, l);
+            krh_matmul_qkv_stage(s->bq, s->bkst, s->bvst, &D->wq, &D->wk, &D->wv, D->bq, D->bk, D->bv, s->bxq, s->bxd,
+                                 ldx, T, cs, sn, c->head_dim, p0);
+            store_kv(s, l, s->bkst, s->bvst, T);
+            krh_attention_kv(s->bao, s->batt, s->bq, &kv, c->n_heads, c->n_kv_heads, c->head_dim, c->max_seq,
+                             c->attn_scale, s->pos, T, p0 + T - 1);
+        }
         krh_quantize_q8_t(s->bxq, s->bxd, ldx, s->bao, c->q_dim, T);
         krh_matmul(s->bx, c->dim, &D->wo, s->bxq, s->bxd, ldx, T, 1);
         krh_rmsnorm_q8_t(s->bxq, s->bxd, ldx, NULL, s->bx, D->ffn_norm, c->dim, c->norm_eps, T);

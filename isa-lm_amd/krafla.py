@@ -18,6 +18,12 @@ MATH_EXPF, MATH_SQRT, MATH_DIV, MATH_RMS_INV = range(4)
 Q8M_EMB, Q8M_CLS, Q8M_QK, Q8M_V, Q8M_O, Q8M_UP, Q8M_DOWN = 1, 2, 4, 8, 16, 32, 64
 
 
+class MlKvLayer(C.Structure):
+    """ml_kv_layer (ops/ops.h:16-22): one layer's cache view, device pointers"""
+    _fields_ = [("k", C.c_void_p), ("v", C.c_void_p), ("kq", C.c_void_p), ("vq", C.c_void_p), ("kd", C.c_void_p),
+                ("vd", C.c_void_p), ("window", C.c_int), ("kh", C.c_void_p), ("vh", C.c_void_p)]
+
+
 class MlConfig(C.Structure):
     """model/mlb.h:9-40"""
     _fields_ = [(n, C.c_int) for n in ("dim", "n_layers", "n_heads", "n_kv_heads", "hidden_dim", "vocab",
@@ -142,12 +148,19 @@ for name, res, args in [
     ("krh_matvec_swiglu", None, [_P, C.POINTER(KrhMat), C.POINTER(KrhMat), _P, _P]),
     ("krh_attention", None, [_P, _P, _P, _P, _P, _P, _P, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_float,
                              _P]),
+    ("krh_rmsnorm_matvec_qkv_stage", None, [_P, _P, _P, C.POINTER(KrhMat), C.POINTER(KrhMat), C.POINTER(KrhMat),
+                                            _P, _P, _P, _P, _P, C.c_float, _P, _P, C.c_int, _P]),
+    ("krh_attention_kv", None, [_P, _P, _P, C.POINTER(MlKvLayer), C.c_int, C.c_int, C.c_int, C.c_int, C.c_float,
+                                _P, C.c_int, C.c_int]),
+    ("krh_store_kv", None, [C.c_int, _P, _P, _P, _P, _P, _P, C.c_int, C.c_int, _P, C.c_int]),
     ("krh_argmax", None, [_P, _P, C.c_int, _P, _P]),
     ("krh_rmsnorm_q8_t", None, [_P, _P, C.c_int, _P, _P, _P, C.c_int, C.c_float, C.c_int]),
     ("krh_quantize_q8_t", None, [_P, _P, C.c_int, _P, C.c_int, C.c_int]),
     ("krh_matmul", None, [_P, C.c_int, C.POINTER(KrhMat), _P, _P, C.c_int, C.c_int, C.c_int]),
     ("krh_matmul_qkv", None, [_P, _P, _P, C.POINTER(KrhMat), C.POINTER(KrhMat), C.POINTER(KrhMat), _P, _P, _P,
                               _P, _P, C.c_int, C.c_int, _P, _P, C.c_int, C.c_int]),
+    ("krh_matmul_qkv_stage", None, [_P, _P, _P, C.POINTER(KrhMat), C.POINTER(KrhMat), C.POINTER(KrhMat), _P, _P,
+                                    _P, _P, _P, C.c_int, C.c_int, _P, _P, C.c_int, C.c_int]),
     ("krh_attention_batch", None, [_P, _P, _P, _P, _P, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_float,
                                    _P, C.c_int, C.c_int]),
     ("krh_silu_quant", None, [_P, _P, C.c_int, _P, _P, C.c_int, C.c_int]),

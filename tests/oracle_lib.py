@@ -95,10 +95,7 @@ if ref is not None:
     ref.ml_quantize_row_q4.argtypes = [_P, _P, _P, C.c_int]
 
 
-class KvLayer(C.Structure):
-    """ops/ops.h:16-22"""
-    _fields_ = [("k", _P), ("v", _P), ("kq", _P), ("vq", _P), ("kd", _P), ("vd", _P), ("window", C.c_int),
-                ("kh", _P), ("vh", _P)]
+KvLayer = K.MlKvLayer   # ops/ops.h:16-22
 
 
 def qtensor(q, d, rows, cols, typ):
