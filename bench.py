@@ -185,8 +185,9 @@ def matvec_microbench(K, iters=1000):
     return out
 
 
-def cpu_baseline(path, prompt, decode):
-    """the reference's ml_run on the same model file, on this host's cores"""
+def cpu_baseline(path, prompt, decode, kv="f32"):
+    """the reference's ml_run on the same model file and KV cache type, on
+    this host's cores"""
     cores = min(64, len(os.sched_getaffinity(0)))
     n = len(prompt) - 1 + decode
     for isa in ("avx512vnni", "avx2"):
@@ -194,7 +195,7 @@ def cpu_baseline(path, prompt, decode):
         if not os.path.exists(exe):
             continue
         cmd = [exe, path, "--tokens", ",".join(str(int(t)) for t in prompt), "-n", str(n), "-T", "0",
-               "-t", str(cores)]
+               "-t", str(cores), "--kv", kv]
         r = subprocess.run(cmd, capture_output=True, text=True, timeout=600)
         if r.returncode == 3:   # the reference's ISA guard: this CPU lacks the ISA
             continue
@@ -227,6 +228,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=16, help="untimed decode tokens before the timed run")
     ap.add_argument("--workload", default="llama8b_q8", choices=sorted(WORKLOADS))
     ap.add_argument("--prompt", type=int, default=None, help="prompt tokens (default: the workload's)")
+    ap.add_argument("--kv", default="f32", choices=["f32", "f16", "q8"],
+                    help="KV cache type (ml_run --kv): f32 is the headline configuration")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-matvec", action="store_true")
     ap.add_argument("--roofline-reps", type=int, default=3)
@@ -257,7 +260,8 @@ def main():
         log("generated %s (%.2f GB) in %.1f s" % (path, os.path.getsize(path) / 1e9, time.time() - t0))
         t0 = time.time()
         model = K.Model(path)
-        state = K.State(model)
+        kv_type = {"f32": K.ML_F32, "f16": K.ML_F16, "q8": K.ML_Q8_0}[args.kv]
+        state = K.State(model, kv_type)
         dev_bytes = K.host.kr_model_device_bytes(model.ptr)
         log("uploaded %.2f GB to HBM in %.1f s" % (dev_bytes / 1e9, time.time() - t0))
         prompt = np.random.default_rng(2048).integers(1, V, P).astype(np.int32)
@@ -291,10 +295,12 @@ def main():
             for w in (b"wq", b"wk", b"wv", b"wo", b"w1", b"w2", b"w3"):
                 per_tok += mat_bytes(K.host.kr_model_device_mat(model.ptr, l, w).contents)
         per_tok += mat_bytes(K.host.kr_model_device_mat(model.ptr, 0, b"wcls").contents)
-        # F32 KV cache: keys and values of positions 0..p read, row p written,
-        # at the mean position of the timed tokens
+        # KV cache: keys and values of positions 0..p read, row p written, at
+        # the mean position of the timed tokens (elements of 4, 2 or 1 bytes;
+        # the Q8 cache adds one float scale per KV head and row)
         p_mean = P - 1 + (args.steps - 1) / 2.0
-        kv_tok = int(2 * cfg.n_layers * (p_mean + 2) * cfg.kv_dim * 4)
+        row = cfg.kv_dim * {"f32": 4, "f16": 2, "q8": 1}[args.kv] + (4 * cfg.n_kv_heads if args.kv == "q8" else 0)
+        kv_tok = int(2 * cfg.n_layers * (p_mean + 2) * row)
         mv = None if args.no_matvec else matvec_microbench(K)
         if mv:
             for r in mv:
@@ -303,7 +309,7 @@ def main():
         cpu = None
         if not args.no_cpu_baseline:
             t0 = time.time()
-            cpu = cpu_baseline(path, prompt[:8], 256)
+            cpu = cpu_baseline(path, prompt[:8], 256, args.kv)
             log("cpu baseline (%.1f s): %s" % (time.time() - t0, json.dumps(cpu)))
         state.close()
         model.close()
@@ -317,7 +323,7 @@ def main():
         "scaling": "weak", "vs_baseline": None, "dtype": "int8", "data": "synthetic",
         "config": {"workload": desc, "prompt_tokens": P, "prefilled_tokens": P - 1, "decode_tokens": args.steps,
                    "first_decode_position": P - 1, "weight_bytes_per_token": per_tok,
-                   "kv_bytes_per_token": kv_tok,
+                   "kv_cache": args.kv, "kv_bytes_per_token": kv_tok,
                    "decode_roofline_tok_s": round(HBM_PEAK_GBS * 1e9 / (per_tok + kv_tok), 1),
                    "parallelism": "single GPU"},
         "prefill_tok_s": round(prefill_tok_s, 2) if prefill_tok_s else None,

@@ -1,0 +1,765 @@
+// Attention over one layer's KV cache for gfx950: scores, softmax and the
+// position-ordered mix, for the F32, F16 and Q8 caches (ops/ops.c:124-238,
+// kernels/scalar/k_scalar.c:66-77, :111-155), and the F16 / Q8 cache stores
+// (model/transformer.c:191-205). Every float operation is the reference's,
+// in its order.
+#include "kr_internal.h"
+#include "kr_numerics.h"
+#include "kr_chain.h"
+
+namespace {
+
+// ---- attention (F32 cache) ----
+//
+// Per layer and position (ops/ops.c:124-155): for query head h (KV head
+// h / group), s_t = (sum_i q_i k_t,i in index order) * scale
+// (k_scalar.c:111-117), softmax over t (k_scalar.c:66-77: max, expf(x - max),
+// the sum in position order, then x * (1 / sum)), and out_i = 0,
+// out_i += a_t v_t,i in position order (k_scalar.c:119-122). The ordered
+// chains run from LDS; the loads feeding them are wide and parallel.
+
+constexpr int AT_T = 64;          // positions per score tile
+constexpr int AT_THREADS = 256;
+
+// positions attended by token blockIdx.z of the launch, at position *pos_p + blockIdx.z
+__device__ __forceinline__ void attn_range(const int *pos_p, int window, int *first, int *n) {
+    const int pos = *pos_p + (int)blockIdx.z;
+    *first = window && pos >= window ? pos + 1 - window : 0;
+    *n = pos + 1 - *first;
+}
+
+// The cache a launch reads (ml_kv_layer, ops/ops.h:16-22, of one layer): K
+// and V rows [max_seq][kv_dim] of floats, halves or int8, and for the Q8
+// cache the row scales kd, vd [max_seq][n_kv_heads] (model/transformer.c:169-180).
+enum { KV_F32 = 0, KV_F16 = 1, KV_Q8 = 2 };
+struct KvView {
+    const void *k, *v;
+    const float *kd, *vd;
+    int n_kv;
+};
+
+// 4 consecutive cache elements: the registers as loaded, and widened to
+// floats (halves exactly, k_scalar.c:124-135; int8 to its value, :148-155)
+template <int KT> struct Kv4;
+template <> struct Kv4<KV_F32> {
+    using T = float4;
+    static constexpr int REGS = 4;
+    __device__ static T load(const void *p, size_t i) { return *(const float4 *)((const float *)p + i); }
+    __device__ static float4 wide(T v) { return v; }
+};
+template <> struct Kv4<KV_F16> {
+    using T = uint2;
+    static constexpr int REGS = 2;
+    __device__ static T load(const void *p, size_t i) { return *(const uint2 *)((const uint16_t *)p + i); }
+    __device__ static float4 wide(T v) {
+        return make_float4(kr_h2f((uint16_t)v.x), kr_h2f((uint16_t)(v.x >> 16)), kr_h2f((uint16_t)v.y),
+                           kr_h2f((uint16_t)(v.y >> 16)));
+    }
+};
+template <> struct Kv4<KV_Q8> {
+    using T = int;
+    static constexpr int REGS = 1;
+    __device__ static T load(const void *p, size_t i) { return *(const int *)((const int8_t *)p + i); }
+    __device__ static float4 wide(T v) {
+        return make_float4((float)(int8_t)v, (float)(int8_t)(v >> 8), (float)(int8_t)(v >> 16), (float)(v >> 24));
+    }
+};
+
+// Scores of one KV head's query heads for AT_T positions. The K tile is staged
+// in LDS as floats (row stride hd + 1: the lanes of a wave read distinct
+// banks; F16 rows widened exactly, k_scalar.c:124-129); thread (t, j) computes
+// heads j, j + 4, ... of the group for position t.
+template <int KT>
+__device__ __forceinline__ void attn_scores(float *att, const float *q, const KvView kv, int group, int hd, int kv_dim,
+                                            int max_seq, int window, float scale, const int *pos_p) {
+    extern __shared__ __align__(16) float at_smem[];
+    int first, n;
+    attn_range(pos_p, window, &first, &n);
+    att += (size_t)blockIdx.z * gridDim.x * group * max_seq;   // token z: [n_heads][max_seq]
+    q += (size_t)blockIdx.z * gridDim.x * group * hd;
+    const int g = blockIdx.x, t0 = blockIdx.y * AT_T, tid = threadIdx.x;
+    if (t0 >= n) return;
+    const int nt = min(AT_T, n - t0), ks = hd + 1;
+    float *qs = at_smem, *kt = at_smem + group * hd;
+    for (int i = tid; i < group * hd; i += AT_THREADS) qs[i] = q[(size_t)g * group * hd + i];
+    const int h4 = hd / 4;
+    for (int e = tid; e < nt * h4; e += AT_THREADS) {
+        const int r = e / h4, c = e - r * h4;
+        const float4 v = Kv4<KT>::wide(Kv4<KT>::load(kv.k, (size_t)(first + t0 + r) * kv_dim + (size_t)g * hd + 4 * c));
+        float *dst = kt + r * ks + 4 * c;
+        dst[0] = v.x; dst[1] = v.y; dst[2] = v.z; dst[3] = v.w;
+    }
+    __syncthreads();
+    const int t = tid % AT_T;
+    if (t >= nt) return;
+    const float *kr = kt + t * ks;
+    for (int j = tid / AT_T; j < group; j += AT_THREADS / AT_T) {
+        const float *qh = qs + j * hd;
+        float acc = 0.0f;
+#pragma unroll 8
+        for (int i = 0; i < hd; i++) acc = kr_fadd(acc, kr_fmul(qh[i], kr[i]));
+        att[(size_t)(g * group + j) * max_seq + t0 + t] = kr_fmul(acc, scale);
+    }
+}
+
+// the F32 cache (its own argument list: the view is built on the device)
+__global__ void __launch_bounds__(AT_THREADS) k_attn_scores(float *att, const float *q, const float *kc, int group,
+                                                            int hd, int kv_dim, int max_seq, int window, float scale,
+                                                            const int *pos_p) {
+    const KvView kv = { kc, nullptr, nullptr, nullptr, 0 };
+    attn_scores<KV_F32>(att, q, kv, group, hd, kv_dim, max_seq, window, scale, pos_p);
+}
+
+template <int KT>
+__global__ void __launch_bounds__(AT_THREADS) k_attn_scores_kv(float *att, const float *q, const KvView kv, int group,
+                                                               int hd, int kv_dim, int max_seq, int window, float scale,
+                                                               const int *pos_p) {
+    attn_scores<KT>(att, q, kv, group, hd, kv_dim, max_seq, window, scale, pos_p);
+}
+
+// Scores over the Q8 cache (ops/ops.c:171-173, k_scalar.c:137-146): each query
+// head of the group quantized with one scale (ops/ops.c:81-96; every
+// workgroup quantizes its group's heads itself, the same bits), then per
+// position the exact int32 dot of the int8 rows (v_dot4) and
+// ((float)sum * (dq * scale)) * dk_t. K rows are staged in LDS with a stride
+// of hd + 4 bytes (33 words for hd 128: the lanes of a wave spread over the
+// banks).
+__global__ void __launch_bounds__(AT_THREADS) k_attn_scores_q8(float *att, const float *q, const KvView kv, int group,
+                                                               int hd, int kv_dim, int max_seq, int window, float scale,
+                                                               const int *pos_p) {
+    extern __shared__ __align__(16) float at_smem[];
+    int first, n;
+    attn_range(pos_p, window, &first, &n);
+    att += (size_t)blockIdx.z * gridDim.x * group * max_seq;
+    q += (size_t)blockIdx.z * gridDim.x * group * hd;
+    const int g = blockIdx.x, t0 = blockIdx.y * AT_T, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    if (t0 >= n) return;
+    const int nt = min(AT_T, n - t0), ks = hd + 4;
+    float *qd = at_smem;                            // [16] query scales
+    int8_t *qs = (int8_t *)(at_smem + 16);          // [group][hd]
+    int8_t *kt = qs + (group * hd + 15) / 16 * 16;  // [AT_T][ks]
+    for (int j = wave; j < group; j += AT_THREADS / 64) {
+        const float *qh = q + (size_t)(g * group + j) * hd;
+        float m = 0.0f;
+        for (int i = lane; i < hd; i += 64) m = fmaxf(m, fabsf(qh[i]));
+        for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+        const bool zero = m < KR_QUANT_TINY;
+        const float id = zero ? 0.0f : kr_fdiv(127.0f, m);
+        for (int i = lane; i < hd; i += 64) qs[j * hd + i] = zero ? (int8_t)0 : (int8_t)kr_q8_elem(qh[i], id);
+        if (lane == 0) qd[j] = zero ? 0.0f : kr_fdiv(m, 127.0f);
+    }
+    const int h4 = hd / 4;
+    for (int e = tid; e < nt * h4; e += AT_THREADS) {
+        const int r = e / h4, c = e - r * h4;
+        *(int *)(kt + r * ks + 4 * c) =
+            *(const int *)((const int8_t *)kv.k + (size_t)(first + t0 + r) * kv_dim + (size_t)g * hd + 4 * c);
+    }
+    __syncthreads();
+    const int t = tid % AT_T;
+    if (t >= nt) return;
+    const int8_t *kr = kt + t * ks;
+    const float dk = kv.kd[(size_t)(first + t0 + t) * kv.n_kv + g];
+    for (int j = tid / AT_T; j < group; j += AT_THREADS / AT_T) {
+        const int8_t *qh = qs + j * hd;
+        int sum = 0;
+        for (int i = 0; i < hd; i += 4) sum = kr_dot4(*(const int *)(qh + i), *(const int *)(kr + i), sum);
+        const float c = kr_fmul(qd[j], scale);
+        att[(size_t)(g * group + j) * max_seq + t0 + t] = kr_fmul(kr_fmul((float)sum, c), dk);
+    }
+}
+
+// Softmax of one head's n scores in place (k_scalar.c:66-77): the max, the
+// exponentials x - max, their ordered sum (kr_spec_sum: the sequential
+// loop's bits), x * (1 / sum). Up to AT_CHUNK scores stay in registers
+// between one batched read and one write (every load issued at once, from an
+// index clamped into the row); longer rows go AT_CHUNK at a time through LDS,
+// the sum continuing from chunk to chunk.
+constexpr int AT_CHUNK = 8192, AT_V = AT_CHUNK / AT_THREADS;
+__global__ void __launch_bounds__(AT_THREADS) k_attn_softmax(float *att, int max_seq, int window, const int *pos_p) {
+    __shared__ __align__(16) float es[sc_terms_cap(AT_CHUNK)];
+    __shared__ __align__(16) unsigned char scr[sc_lds_bytes(AT_CHUNK, AT_THREADS)];
+    __shared__ float red[AT_THREADS / 64];
+    __shared__ uint64_t xtab[32];   // expf's table
+    int first, n;
+    attn_range(pos_p, window, &first, &n);
+    float *a = att + ((size_t)blockIdx.z * gridDim.x + blockIdx.x) * max_seq;
+    const int tid = threadIdx.x;
+    if (tid < 32) xtab[tid] = kr_exp2_tab[tid];
+    const bool fits = n <= AT_CHUNK;
+    float v[AT_V];
+    float m = -INFINITY;
+    if (fits) {
+#pragma unroll
+        for (int k = 0; k < AT_V; k++) v[k] = a[min(k * AT_THREADS + tid, n - 1)];
+#pragma unroll
+        for (int k = 0; k < AT_V; k++) m = fmaxf(m, v[k]);   // clamped repeats change no max
+    } else {
+        for (int t = tid; t < n; t += AT_THREADS) m = fmaxf(m, a[t]);
+    }
+    for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+    if ((tid & 63) == 0) red[tid >> 6] = m;
+    __syncthreads();
+    float mx = red[0];
+    for (int k = 1; k < AT_THREADS / 64; k++) mx = fmaxf(mx, red[k]);
+    if (mx == -INFINITY) {   // every score -inf: the scalar loop's 1/n
+        for (int t = tid; t < n; t += AT_THREADS) a[t] = kr_fdiv(1.0f, (float)n);
+        return;
+    }
+    if (fits) {
+        const int sh = sc_log_len(n);
+#pragma unroll
+        for (int k = 0; k < AT_V; k++) {
+            if (k * AT_THREADS >= n) break;   // the rest of the slots are clamped repeats
+            const int t = k * AT_THREADS + tid;
+            v[k] = kr_expf_tab(kr_fsub(v[k], mx), xtab);
+            if (t < n) es[sc_at(t, sh)] = v[k];
+        }
+        __syncthreads();
+        const float inv = kr_fdiv(1.0f, kr_spec_sum<AT_THREADS>(es, n, scr));
+#pragma unroll
+        for (int k = 0; k < AT_V; k++) {
+            if (k * AT_THREADS >= n) break;
+            const int t = k * AT_THREADS + tid;
+            if (t < n) a[t] = kr_fmul(v[k], inv);
+        }
+        return;
+    }
+    float sum = 0.0f;
+    for (int c0 = 0; c0 < n; c0 += AT_CHUNK) {
+        const int cn = min(AT_CHUNK, n - c0), sh = sc_log_len(cn);
+        for (int t = tid; t < cn; t += AT_THREADS) {
+            const float e = kr_expf_tab(kr_fsub(a[c0 + t], mx), xtab);
+            es[sc_at(t, sh)] = e;
+            a[c0 + t] = e;
+        }
+        __syncthreads();
+        sum = kr_spec_sum<AT_THREADS>(es, cn, scr, sum);   // ends with a barrier: es is free again
+    }
+    const float inv = kr_fdiv(1.0f, sum);
+    for (int t = tid; t < n; t += AT_THREADS) a[t] = kr_fmul(a[t], inv);
+}
+
+// out for one KV head's query heads and DW of their dims: lane = (head j of
+// the group, dim d), DW = 64 / (group rounded up to a power of two). Each
+// lane runs its ordered chain o += a_t * v_t,d (k_scalar.c:119-122). ao is
+// written as floats (its quantization happens where it is consumed).
+//
+// The chain (one dependent add per position) is the bound, so the workgroup
+// splits the work by role and keeps the adding wave free of everything else.
+// Wave 0 only adds. MX_P producer waves load V and the weights, form the
+// products a_t * v_t,d (each the rounded product, as in the scalar loop) and
+// hand them over through a ring of three LDS tiles of MX_T positions, laid out
+// [lane][position] so that one 16-byte read feeds 4 adds. Producer p owns
+// positions [p MX_TH, (p + 1) MX_TH) of every tile and loads them MX_D tiles
+// ahead into registers: a lane holds 4 dims of V at one position and the
+// weights of every head at that position, and writes its products straight
+// into the adder's layout (4-byte writes: the transpose costs no LDS reads).
+// LDS bandwidth is what the roles share, so each product crosses LDS once each
+// way. One barrier per step hands tiles over: producers write tile s in step
+// s; the adder reads tile s into registers in step s + 1 and adds it in step
+// s + 2, so no add waits on an LDS read.
+constexpr int MX_T = 64, MX_TS = MX_T + 4;   // positions per tile; padded product row
+constexpr int MX_P = 2, MX_TH = MX_T / MX_P;   // producers; their positions per tile
+
+__device__ __forceinline__ void kr_lds_order() { asm volatile("" ::: "memory"); }
+
+template <int DW, int KT>
+__device__ __forceinline__ void attn_mix(float *ao, const float *att, const KvView kv, int group, int hd, int kv_dim,
+                                         int max_seq, int window, const int *pos_p) {
+    constexpr int GP = 64 / DW;                        // head slots
+    constexpr int NV = (MX_TH * DW / 4 + 63) / 64;     // 4-element groups of V per producer lane per tile
+    constexpr int ND = KT == KV_Q8 ? NV : 0;           // V row scales per producer lane per tile
+    constexpr int PT = Kv4<KT>::REGS * NV + NV * GP + ND;   // registers per tile: V, the weights, the scales
+    constexpr int LT = NV + NV * GP + ND;              // loads per tile
+    // tiles in flight: within 128 registers and within the 63 loads the wait
+    // counter can track (past that every wait would drain it)
+    constexpr int DR = 128 / PT < 60 / LT ? 128 / PT : 60 / LT;
+    constexpr int MX_D = DR > 8 ? 8 : DR < 2 ? 2 : DR;
+    __shared__ __align__(16) float prod[4][64 * MX_TS];   // the ring, and a sink for steps past the end
+    int first, n;
+    attn_range(pos_p, window, &first, &n);
+    const int g = blockIdx.x, c0 = blockIdx.y * DW, lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int j = lane / DW, d = lane % DW;
+    const int ntiles = (n + MX_T - 1) / MX_T;
+    const int steps = (ntiles + 2 + MX_D - 1) / MX_D * MX_D;   // every wave runs as many barriers
+    const size_t q_dim = (size_t)gridDim.x * group * hd;
+
+    if (wave == 0) {
+        // the adder: in step s it reads all of tile s - 1 into registers
+        // (finished a step earlier) while it adds tile s - 2 from the
+        // registers read in step s - 1, so every LDS read has a whole tile
+        // of adds to arrive in
+        float o = 0.0f;
+        auto step = [&](int s, float4 *cur, float4 *nxt) {
+            if (s - 1 >= 0 && s - 1 < ntiles) {
+                const float *P = prod[(s - 1) % 3] + lane * MX_TS;
+#pragma unroll
+                for (int i = 0; i < MX_T / 4; i++) nxt[i] = *(const float4 *)(P + 4 * i);
+            }
+            const int tile = s - 2;
+            if (tile >= 0 && tile < ntiles) {
+                const int nt = min(MX_T, n - tile * MX_T);
+                if (nt == MX_T) {
+#pragma unroll
+                    for (int i = 0; i < MX_T / 4; i++) {
+                        o = kr_fadd(o, cur[i].x);
+                        o = kr_fadd(o, cur[i].y);
+                        o = kr_fadd(o, cur[i].z);
+                        o = kr_fadd(o, cur[i].w);
+                    }
+                } else {   // the last, partial tile: only its live steps (a zero would turn -0 to +0)
+                    const float *P = prod[tile % 3] + lane * MX_TS;
+                    for (int r = 0; r < nt; r++) o = kr_fadd(o, P[r]);
+                }
+            }
+            kr_lds_order();
+            __syncthreads();
+        };
+        float4 ta[MX_T / 4], tb[MX_T / 4];
+        for (int s = 0; s < steps; s += 2) {
+            step(s, ta, tb);
+            if (s + 1 < steps) step(s + 1, tb, ta);
+        }
+        if (j < group && d < min(DW, hd - c0)) ao[blockIdx.z * q_dim + (size_t)(g * group + j) * hd + c0 + d] = o;
+        return;
+    }
+
+    // producer p: lane slot k holds V dims c..c+3 at position r of its half
+    // tile, and the weights of heads 0..GP-1 at that position
+    const int p = wave - 1;
+    const int cw = min(DW, hd - c0);   // valid dims of the chunk (a multiple of 4)
+    const size_t vb = (size_t)first * kv_dim + (size_t)g * hd + c0;   // element offset of V row `first`
+    const float *abase = att + ((size_t)blockIdx.z * gridDim.x * group + (size_t)g * group) * max_seq;
+    // Every load is unconditional from an address clamped into the live
+    // range (position n - 1, the chunk's last 4 elements, the group's last
+    // head, the row's last element): values loaded for positions >= n, dims
+    // >= cw or heads >= group only feed products that are never added or
+    // stored, and a branch-free loop keeps the loads of MX_D tiles in flight.
+    using VT = typename Kv4<KT>::T;
+    VT rv[MX_D][NV];
+    float ra[MX_D][NV][GP];
+    float rd[MX_D][ND > 0 ? ND : 1];   // Q8: the V rows' scales
+    auto load = [&](int tile, VT *v, float (*a)[GP], float *dv) {
+        const int t0 = min(tile, ntiles - 1) * MX_T + p * MX_TH;
+#pragma unroll
+        for (int k = 0; k < NV; k++) {
+            const int e = (k * 64 + lane) * 4, r = min(e / DW, MX_TH - 1), c = min(e % DW, cw - 4);
+            const int t = min(t0 + r, n - 1);
+            v[k] = Kv4<KT>::load(kv.v, vb + (size_t)t * kv_dim + c);
+            if (KT == KV_Q8) dv[k] = kv.vd[(size_t)(first + t) * kv.n_kv + g];
+            const int q = min(t0 + r, max_seq - 1);
+#pragma unroll
+            for (int jj = 0; jj < GP; jj++) a[k][jj] = abase[(size_t)min(jj, group - 1) * max_seq + q];
+        }
+    };
+    auto products = [&](int tile, const VT *v, const float (*a)[GP], const float *dv) {
+        float *P = prod[tile < ntiles ? tile % 3 : 3] + p * MX_TH;
+#pragma unroll
+        for (int k = 0; k < NV; k++) {
+            const int e = (k * 64 + lane) * 4, r = e / DW, c = e % DW;
+            if (r < MX_TH) {
+                const float4 x = Kv4<KT>::wide(v[k]);
+#pragma unroll
+                for (int jj = 0; jj < GP; jj++) {
+                    // Q8: the weight a_t * dv_t, then its products (k_scalar.c:151-153)
+                    const float w = KT == KV_Q8 ? kr_fmul(a[k][jj], dv[k]) : a[k][jj];
+                    float *o = P + (jj * DW + c) * MX_TS + r;
+                    o[0] = kr_fmul(w, x.x);
+                    o[MX_TS] = kr_fmul(w, x.y);
+                    o[2 * MX_TS] = kr_fmul(w, x.z);
+                    o[3 * MX_TS] = kr_fmul(w, x.w);
+                }
+            }
+        }
+        kr_lds_order();
+    };
+    // in slot order (the loop's waits count on slot 0 being the oldest)
+#pragma unroll
+    for (int u = 0; u < MX_D; u++) {
+        load(u, rv[u], ra[u], rd[u]);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    for (int s0 = 0; s0 < steps; s0 += MX_D) {
+#pragma unroll
+        for (int u = 0; u < MX_D; u++) {
+            const int s = s0 + u;   // tile s sits in slot u
+            // fenced for the scheduler: a step's products wait on its own
+            // slot's loads only
+            __builtin_amdgcn_sched_barrier(0);
+            products(s, rv[u], ra[u], rd[u]);   // past the end: into the sink, unread
+            load(s + MX_D, rv[u], ra[u], rd[u]);
+            __builtin_amdgcn_sched_barrier(0);
+            __syncthreads();
+        }
+    }
+}
+
+template <int DW>
+__global__ void __launch_bounds__(64 * (1 + MX_P)) k_attn_mix(float *ao, const float *att, const float *vc,
+                                                              int group, int hd, int kv_dim, int max_seq, int window,
+                                                              const int *pos_p) {
+    const KvView kv = { nullptr, vc, nullptr, nullptr, 0 };
+    attn_mix<DW, KV_F32>(ao, att, kv, group, hd, kv_dim, max_seq, window, pos_p);
+}
+
+template <int DW, int KT>
+__global__ void __launch_bounds__(64 * (1 + MX_P)) k_attn_mix_kv(float *ao, const float *att, const KvView kv,
+                                                                 int group, int hd, int kv_dim, int max_seq,
+                                                                 int window, const int *pos_p) {
+    attn_mix<DW, KT>(ao, att, kv, group, hd, kv_dim, max_seq, window, pos_p);
+}
+
+// The same for a batch of positions (prefill: one workgroup per position and
+// head chunk, so throughput, not one chain's latency, is what counts), one wave
+// per workgroup: lane = (head j of the group, dim d), DW = 64 / (group rounded up
+// to a power of two). Each lane runs its ordered chain o += a_t * v_t,d
+// (k_scalar.c:119-122). ao is written as floats (its quantization happens
+// where it is consumed).
+//
+// The chain is the bound (one dependent add per position), so everything else
+// is pipelined under it: tiles of MB_T positions of V and of the heads' weights
+// are loaded MB_DEPTH tiles ahead into registers; tile t + 1 is staged into
+// the other half of a double LDS buffer while tile t is read, V transposed
+// ([dim][position]) so one 16-byte LDS read feeds 4 steps; the reads of each
+// 16-step chunk are issued before the adds of the chunk before it. The
+// workgroup is one wave, whose LDS operations execute in order, so LDS needs
+// only compiler ordering (kr_lds_order), not barriers.
+constexpr int MB_T = 64, MB_TS = MB_T + 4;   // positions per tile; padded LDS row
+
+template <int DW, int KT>
+__device__ __forceinline__ void attn_mix_batch(float *ao, const float *att, const KvView kv, int group, int hd,
+                                               int kv_dim, int max_seq, int window, const int *pos_p) {
+    constexpr int GP = 64 / DW;                    // head slots per wave
+    constexpr int NV = MB_T * DW / 4 / 64;         // float4 of V per lane per tile
+    constexpr int NA = (GP * MB_T / 4 + 63) / 64;  // float4 of weights per lane per tile
+    constexpr int MB_DEPTH = NV + NA > 8 ? 2 : 4;  // tiles in flight (even: LDS halves alternate)
+    __shared__ __align__(16) float vt[2][DW * MB_TS];
+    constexpr int AW = GP * MB_T > NA * 256 ? GP * MB_T : NA * 256;   // padded: every lane stores
+    __shared__ __align__(16) float aw[2][AW];
+    int first, n;
+    attn_range(pos_p, window, &first, &n);
+    const int g = blockIdx.x, c0 = blockIdx.y * DW, lane = threadIdx.x;
+    const int j = lane / DW, d = lane % DW;
+    const size_t vb = (size_t)first * kv_dim + (size_t)g * hd + c0;   // element offset of V row `first`
+    const size_t q_dim = (size_t)gridDim.x * group * hd;
+    const float *abase = att + ((size_t)blockIdx.z * gridDim.x * group + (size_t)g * group) * max_seq;
+    ao += blockIdx.z * q_dim;
+    const int ntiles = (n + MB_T - 1) / MB_T;
+    const int cw = min(DW, hd - c0);   // valid dims of the chunk (a multiple of 4)
+
+    // Every load is unconditional from an address clamped into the live
+    // range (position n - 1, the chunk's last float4, the group's last head,
+    // the row's last float4): values loaded for positions >= n, dims >= cw or
+    // heads >= group only feed lanes and steps that are never stored or run,
+    // and a branch-free load stream lets the compiler's wait counts keep the
+    // loads of MB_DEPTH tiles in flight together.
+    using VT = typename Kv4<KT>::T;
+    constexpr int ND = KT == KV_Q8 ? NA : 1;   // Q8: V row scales at the weights' positions
+    VT rv[MB_DEPTH][NV];
+    float4 ra[MB_DEPTH][NA], rd[MB_DEPTH][ND];
+    auto load = [&](int tile, VT *v, float4 *a, float4 *dv) {
+        const int t0 = min(tile, ntiles - 1) * MB_T;
+#pragma unroll
+        for (int k = 0; k < NV; k++) {
+            const int e = (k * 64 + lane) * 4, r = e / DW, c = min(e % DW, cw - 4);   // position r, dims c..c+3
+            v[k] = Kv4<KT>::load(kv.v, vb + (size_t)min(t0 + r, n - 1) * kv_dim + c);
+        }
+#pragma unroll
+        for (int k = 0; k < NA; k++) {
+            const int e = (k * 64 + lane) * 4, jj = min(e / MB_T, group - 1), r = e % MB_T;
+            const float *src = abase + (size_t)jj * max_seq + min(t0 + r, max_seq - 4);
+            a[k] = make_float4(src[0], src[1], src[2], src[3]);
+            if (KT == KV_Q8) {
+                const float *d = kv.vd + (size_t)first * kv.n_kv + g;
+                dv[k] = make_float4(d[(size_t)min(t0 + r, n - 1) * kv.n_kv], d[(size_t)min(t0 + r + 1, n - 1) * kv.n_kv],
+                                    d[(size_t)min(t0 + r + 2, n - 1) * kv.n_kv], d[(size_t)min(t0 + r + 3, n - 1) * kv.n_kv]);
+            }
+        }
+    };
+    auto stage = [&](int buf, int tile, const VT *v, const float4 *a, const float4 *dv) {
+        float *V = vt[buf], *A = aw[buf];
+#pragma unroll
+        for (int k = 0; k < NV; k++) {
+            const int e = (k * 64 + lane) * 4, r = e / DW, c = e % DW;
+            const float4 x = Kv4<KT>::wide(v[k]);
+            V[(c + 0) * MB_TS + r] = x.x;
+            V[(c + 1) * MB_TS + r] = x.y;
+            V[(c + 2) * MB_TS + r] = x.z;
+            V[(c + 3) * MB_TS + r] = x.w;
+        }
+#pragma unroll
+        for (int k = 0; k < NA; k++) {
+            const int e = (k * 64 + lane) * 4, r = e % MB_T;
+            // a float4 clamped back from the row's end holds position p at
+            // element p - (max_seq - 4): shift it down to element p - p0
+            const int sh = tile * MB_T + r - min(tile * MB_T + r, max_seq - 4);
+            const float4 x = a[k];
+            float4 y;
+            y.x = sh == 0 ? x.x : sh == 1 ? x.y : sh == 2 ? x.z : x.w;
+            y.y = sh == 0 ? x.y : sh == 1 ? x.z : x.w;
+            y.z = sh == 0 ? x.z : x.w;
+            y.w = x.w;
+            if (KT == KV_Q8) {   // the weights a_t * dv_t (k_scalar.c:151)
+                y.x = kr_fmul(y.x, dv[k].x);
+                y.y = kr_fmul(y.y, dv[k].y);
+                y.z = kr_fmul(y.z, dv[k].z);
+                y.w = kr_fmul(y.w, dv[k].w);
+            }
+            *(float4 *)(A + e) = y;
+        }
+        kr_lds_order();
+    };
+    struct Chunk { float4 v[4], a[4]; };   // 16 steps of one lane
+    auto read = [&](Chunk &c, int buf, int k) {
+        const float *V = vt[buf] + d * MB_TS + 16 * k, *A = aw[buf] + j * MB_T + 16 * k;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            c.v[i] = *(const float4 *)(V + 4 * i);
+            c.a[i] = *(const float4 *)(A + 4 * i);
+        }
+    };
+    float o = 0.0f;
+    auto chain = [&](const Chunk &c) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            o = kr_fadd(o, kr_fmul(c.a[i].x, c.v[i].x));
+            o = kr_fadd(o, kr_fmul(c.a[i].y, c.v[i].y));
+            o = kr_fadd(o, kr_fmul(c.a[i].z, c.v[i].z));
+            o = kr_fadd(o, kr_fmul(c.a[i].w, c.v[i].w));
+        }
+    };
+
+#pragma unroll
+    for (int s = 0; s < MB_DEPTH; s++) load(s, rv[s], ra[s], rd[s]);
+    stage(0, 0, rv[0], ra[0], rd[0]);
+    load(MB_DEPTH, rv[0], ra[0], rd[0]);
+    Chunk c0r, c1r;
+    read(c0r, 0, 0);
+    // main loop: groups of MB_DEPTH full tiles; tile k0 + s sits in LDS half
+    // s & 1 and its first chunk is in c0r when its step begins
+    const int ngroups = n / (MB_T * MB_DEPTH);
+    int k0 = 0;
+    for (; k0 < ngroups * MB_DEPTH; k0 += MB_DEPTH) {
+#pragma unroll
+        for (int s = 0; s < MB_DEPTH; s++) {
+            const int b = s & 1, nx = (s + 1) % MB_DEPTH;
+            // phases fenced for the scheduler: a chunk's reads are issued
+            // one phase before its products and adds, and the staging of
+            // the next tile shares a phase with the first chunk's adds
+            read(c1r, b, 1);
+            __builtin_amdgcn_sched_barrier(0);
+            chain(c0r);
+            stage(b ^ 1, k0 + s + 1, rv[nx], ra[nx], rd[nx]);
+            load(k0 + s + 1 + MB_DEPTH, rv[nx], ra[nx], rd[nx]);
+            __builtin_amdgcn_sched_barrier(0);
+            read(c0r, b, 2);
+            __builtin_amdgcn_sched_barrier(0);
+            chain(c1r);
+            __builtin_amdgcn_sched_barrier(0);
+            read(c1r, b, 3);
+            __builtin_amdgcn_sched_barrier(0);
+            chain(c0r);
+            __builtin_amdgcn_sched_barrier(0);
+            read(c0r, b ^ 1, 0);
+            __builtin_amdgcn_sched_barrier(0);
+            chain(c1r);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+    // the last tiles (at most MB_DEPTH; tile k0 is staged in half 0, tile
+    // k0 + s is in rv[s]); the last may be partial, and only its live steps
+    // run: a zero weight would turn -0 to +0
+#pragma unroll
+    for (int s = 0; s < MB_DEPTH; s++) {
+        const int tile = k0 + s;
+        if (tile < ntiles) {
+            if (s > 0) stage(s & 1, tile, rv[s], ra[s], rd[s]);
+            const int nt = min(MB_T, n - tile * MB_T);
+            const float *V = vt[s & 1] + d * MB_TS, *A = aw[s & 1] + j * MB_T;
+            for (int r = 0; r < nt; r++) o = kr_fadd(o, kr_fmul(A[r], V[r]));
+            kr_lds_order();
+        }
+    }
+    if (j < group && d < cw) ao[(size_t)(g * group + j) * hd + c0 + d] = o;
+}
+
+template <int DW>
+__global__ void __launch_bounds__(64) k_attn_mix_batch(float *ao, const float *att, const float *vc, int group, int hd,
+                                                       int kv_dim, int max_seq, int window, const int *pos_p) {
+    const KvView kv = { nullptr, vc, nullptr, nullptr, 0 };
+    attn_mix_batch<DW, KV_F32>(ao, att, kv, group, hd, kv_dim, max_seq, window, pos_p);
+}
+
+template <int DW, int KT>
+__global__ void __launch_bounds__(64) k_attn_mix_batch_kv(float *ao, const float *att, const KvView kv, int group,
+                                                          int hd, int kv_dim, int max_seq, int window,
+                                                          const int *pos_p) {
+    attn_mix_batch<DW, KT>(ao, att, kv, group, hd, kv_dim, max_seq, window, pos_p);
+}
+
+// ---- F16 / Q8 cache rows ----
+
+// store_kv (model/transformer.c:191-205) for the positions *pos0 + t: the
+// staging rows k, v [ntok][kv_dim] (the projections' output) into one
+// layer's F16 cache (every value rounded to half precision, core/ml.c:39-53)
+// or Q8 cache (each KV head's head_dim values with one scale,
+// ops/ops.c:81-96). One wave per (KV head, K or V, token).
+struct KvOut {
+    void *k, *v;
+    float *kd, *vd;
+    int n_kv;
+};
+
+template <int KT>
+__global__ void __launch_bounds__(64) k_store_kv(const KvOut o, const float *k, const float *v, int kv_dim, int hd,
+                                                 const int *pos0) {
+    const int h = blockIdx.x, which = blockIdx.y, t = blockIdx.z, lane = threadIdx.x;
+    const float *x = (which ? v : k) + (size_t)t * kv_dim + (size_t)h * hd;
+    const size_t at = (size_t)(*pos0 + t) * kv_dim + (size_t)h * hd;
+    if (KT == KV_F16) {
+        uint16_t *dst = (uint16_t *)(which ? o.v : o.k) + at;
+        for (int i = lane; i < hd; i += 64) dst[i] = kr_f2h(x[i]);
+        return;
+    }
+    int8_t *dst = (int8_t *)(which ? o.v : o.k) + at;
+    float m = 0.0f;
+    for (int i = lane; i < hd; i += 64) m = fmaxf(m, fabsf(x[i]));
+    for (int sh = 32; sh >= 1; sh >>= 1) m = fmaxf(m, __shfl_xor(m, sh));
+    const bool zero = m < KR_QUANT_TINY;
+    const float id = zero ? 0.0f : kr_fdiv(127.0f, m);
+    for (int i = lane; i < hd; i += 64) dst[i] = zero ? (int8_t)0 : (int8_t)kr_q8_elem(x[i], id);
+    if (lane == 0) (which ? o.vd : o.kd)[(size_t)(*pos0 + t) * o.n_kv + h] = zero ? 0.0f : kr_fdiv(m, 127.0f);
+}
+
+}   // namespace
+
+// ---- C ABI ----
+
+template <int KT, int DW>
+static void launch_mix(const dim3 &grid, int ntok, float *ao, const float *att, const KvView &kv, int group, int hd,
+                       int kv_dim, int max_seq, int window, const int *pos) {
+    const float *vc = (const float *)kv.v;
+    if (ntok > 1) {
+        if constexpr (KT == KV_F32)
+            hipLaunchKernelGGL(k_attn_mix_batch<DW>, grid, dim3(64), 0, kr_stream(), ao, att, vc, group, hd, kv_dim,
+                               max_seq, window, pos);
+        else
+            hipLaunchKernelGGL((k_attn_mix_batch_kv<DW, KT>), grid, dim3(64), 0, kr_stream(), ao, att, kv, group, hd,
+                               kv_dim, max_seq, window, pos);
+    } else {
+        if constexpr (KT == KV_F32)
+            hipLaunchKernelGGL(k_attn_mix<DW>, grid, dim3(64 * (1 + MX_P)), 0, kr_stream(), ao, att, vc, group, hd,
+                               kv_dim, max_seq, window, pos);
+        else
+            hipLaunchKernelGGL((k_attn_mix_kv<DW, KT>), grid, dim3(64 * (1 + MX_P)), 0, kr_stream(), ao, att, kv, group,
+                               hd, kv_dim, max_seq, window, pos);
+    }
+}
+
+// scores, softmax and mix of ntok positions *pos + t over one layer's cache
+// of type KT; max_pos (the last position) sizes the launch
+template <int KT>
+static void attention(float *ao, float *att, const float *q, const KvView &kv, int n_heads, int n_kv_heads,
+                      int head_dim, int max_seq, int window, float scale, const int *pos, int ntok, int max_pos) {
+    if (n_kv_heads <= 0 || n_heads % n_kv_heads || head_dim % 4 || (n_heads * head_dim) % KR_QK ||
+        n_heads / n_kv_heads > 16 || head_dim > 1024 || max_seq < 4) {
+        kr_fail(ML_E_SHAPE, "attention shape", hipSuccess);
+        return;
+    }
+    const int group = n_heads / n_kv_heads, kv_dim = n_kv_heads * head_dim;
+    const size_t lds = KT == KV_Q8 ? 64 + (size_t)(group * head_dim + 15) / 16 * 16 + (size_t)AT_T * (head_dim + 4)
+                                   : sizeof(float) * ((size_t)group * head_dim + (size_t)AT_T * (head_dim + 1));
+    if (lds > 64 * 1024) {
+        kr_fail(ML_E_SHAPE, "attention: head_dim too large for the score tile", hipSuccess);
+        return;
+    }
+    const dim3 sgrid(n_kv_heads, (max_pos + AT_T) / AT_T, ntok);
+    if constexpr (KT == KV_Q8)
+        hipLaunchKernelGGL(k_attn_scores_q8, sgrid, dim3(AT_THREADS), lds, kr_stream(), att, q, kv, group, head_dim,
+                           kv_dim, max_seq, window, scale, pos);
+    else if constexpr (KT == KV_F32)
+        hipLaunchKernelGGL(k_attn_scores, sgrid, dim3(AT_THREADS), lds, kr_stream(), att, q, (const float *)kv.k, group,
+                           head_dim, kv_dim, max_seq, window, scale, pos);
+    else
+        hipLaunchKernelGGL((k_attn_scores_kv<KT>), sgrid, dim3(AT_THREADS), lds, kr_stream(), att, q, kv, group,
+                           head_dim, kv_dim, max_seq, window, scale, pos);
+    hipLaunchKernelGGL(k_attn_softmax, dim3(n_heads, 1, ntok), dim3(AT_THREADS), 0, kr_stream(), att, max_seq, window,
+                       pos);
+    const int gp = group <= 1 ? 1 : group <= 2 ? 2 : group <= 4 ? 4 : group <= 8 ? 8 : 16;
+    const int dw = 64 / gp;
+    const dim3 grid(n_kv_heads, (head_dim + dw - 1) / dw, ntok);
+    switch (dw) {
+    case 64: launch_mix<KT, 64>(grid, ntok, ao, att, kv, group, head_dim, kv_dim, max_seq, window, pos); break;
+    case 32: launch_mix<KT, 32>(grid, ntok, ao, att, kv, group, head_dim, kv_dim, max_seq, window, pos); break;
+    case 16: launch_mix<KT, 16>(grid, ntok, ao, att, kv, group, head_dim, kv_dim, max_seq, window, pos); break;
+    case 8: launch_mix<KT, 8>(grid, ntok, ao, att, kv, group, head_dim, kv_dim, max_seq, window, pos); break;
+    default: launch_mix<KT, 4>(grid, ntok, ao, att, kv, group, head_dim, kv_dim, max_seq, window, pos); break;
+    }
+    kr_check_launch("attention");
+}
+
+static KvView f32_view(const float *kc, const float *vc) {
+    KvView v = { kc, vc, nullptr, nullptr, 0 };
+    return v;
+}
+
+extern "C" void krh_attention(float *ao, int8_t *aq, float *ad, float *att, const float *q, const float *kc,
+                              const float *vc, int n_heads, int n_kv_heads, int head_dim, int max_seq, int window,
+                              float scale, const int *pos) {
+    attention<KV_F32>(ao, att, q, f32_view(kc, vc), n_heads, n_kv_heads, head_dim, max_seq, window, scale, pos, 1,
+                      max_seq - 1);
+    if (aq) krh_quantize_q8(aq, ad, ao, n_heads * head_dim, 1);
+}
+
+extern "C" void krh_attention_batch(float *ao, float *att, const float *q, const float *kc, const float *vc,
+                                    int n_heads, int n_kv_heads, int head_dim, int max_seq, int window, float scale,
+                                    const int *pos0, int ntok, int last_pos) {
+    if (ntok <= 0 || last_pos >= max_seq) {
+        kr_fail(ML_E_SHAPE, "attention batch shape", hipSuccess);
+        return;
+    }
+    attention<KV_F32>(ao, att, q, f32_view(kc, vc), n_heads, n_kv_heads, head_dim, max_seq, window, scale, pos0, ntok,
+                      last_pos);
+}
+
+extern "C" void krh_attention_kv(float *ao, float *att, const float *q, const ml_kv_layer *kv, int n_heads,
+                                 int n_kv_heads, int head_dim, int max_seq, float scale, const int *pos0, int ntok,
+                                 int last_pos) {
+    if (ntok <= 0 || last_pos >= max_seq || !kv) {
+        kr_fail(ML_E_SHAPE, "attention shape", hipSuccess);
+        return;
+    }
+    if (kv->k && kv->v) {
+        attention<KV_F32>(ao, att, q, f32_view(kv->k, kv->v), n_heads, n_kv_heads, head_dim, max_seq, kv->window,
+                          scale, pos0, ntok, last_pos);
+    } else if (kv->kh && kv->vh) {
+        KvView v = { kv->kh, kv->vh, nullptr, nullptr, n_kv_heads };
+        attention<KV_F16>(ao, att, q, v, n_heads, n_kv_heads, head_dim, max_seq, kv->window, scale, pos0, ntok,
+                          last_pos);
+    } else if (kv->kq && kv->vq && kv->kd && kv->vd) {
+        KvView v = { kv->kq, kv->vq, kv->kd, kv->vd, n_kv_heads };
+        attention<KV_Q8>(ao, att, q, v, n_heads, n_kv_heads, head_dim, max_seq, kv->window, scale, pos0, ntok,
+                         last_pos);
+    } else {
+        kr_fail(ML_E_SHAPE, "attention: the cache view has no F32, F16 or Q8 rows", hipSuccess);
+    }
+}
+
+extern "C" void krh_store_kv(int kv_type, void *kc, void *vc, float *kd, float *vd, const float *k, const float *v,
+                             int n_kv_heads, int head_dim, const int *pos0, int ntok) {
+    if (ntok <= 0 || n_kv_heads <= 0 || head_dim <= 0 || head_dim % 4 || !kc || !vc ||
+        (kv_type == ML_Q8_0 && (!kd || !vd)) || (kv_type != ML_Q8_0 && kv_type != ML_F16)) {
+        kr_fail(ML_E_SHAPE, "store_kv: an F16 or Q8 cache and its shape", hipSuccess);
+        return;
+    }
+    const dim3 grid(n_kv_heads, 2, ntok);
+    const int kv_dim = n_kv_heads * head_dim;
+    KvOut o = { kc, vc, kd, vd, n_kv_heads };
+    if (kv_type == ML_F16)
+        hipLaunchKernelGGL(k_store_kv<KV_F16>, grid, dim3(64), 0, kr_stream(), o, k, v, kv_dim, head_dim, pos0);
+    else
+        hipLaunchKernelGGL(k_store_kv<KV_Q8>, grid, dim3(64), 0, kr_stream(), o, k, v, kv_dim, head_dim, pos0);
+    kr_check_launch("store_kv");
+}
+

@@ -20,8 +20,9 @@
  * any other buffer is staged to the device for the call and copied back.
  * The host reads activations only as logits: the classifier's matvec copies
  * them back and synchronizes, which is also where device errors surface.
- * Supported: the F32 KV cache, models without embed_scale != 1, no --imatrix
- * (those paths write or read arena memory on the host). */
+ * Supported: the F32 and Q8 KV caches, models without embed_scale != 1, no
+ * --imatrix (the F16 cache and those paths write or read arena memory on the
+ * host). */
 #include <math.h>
 #include <stdio.h>
 #include <stdlib.h>
@@ -476,9 +477,16 @@ int ml_attention_batch_heads(const ml_config *cfg, int nthreads) {
     return cfg->n_heads / cfg->n_kv_heads;
 }
 
+/* The F32 and Q8 caches. The F16 cache is converted by a host loop in
+ * store_kv (model/transformer.c:195-197) from K and V rows that live on the
+ * device here, so it cannot be served through this binding. */
 static int attn_supported(const ml_kv_layer *kv, const ml_config *cfg) {
-    if (!kv->k || !kv->v) {
-        fail_call("the F16 and Q8 KV caches are not built (use --kv f32)");
+    if (kv->kh || kv->vh) {
+        fail_call("the F16 KV cache is converted on the host by model/transformer.c (use --kv f32 or --kv q8)");
+        return 0;
+    }
+    if (!(kv->k && kv->v) && !(kv->kq && kv->vq && kv->kd && kv->vd)) {
+        fail_call("attention without KV cache rows");
         return 0;
     }
     if (cfg->attn_softcap > 0.0f) {
@@ -488,38 +496,58 @@ static int attn_supported(const ml_kv_layer *kv, const ml_config *cfg) {
     return ready();
 }
 
+/* the layer's cache as device pointers: F32 rows, or Q8 rows and their row
+ * scales (written on the device by ml_quantize_row in store_kv) */
+static ml_kv_layer dev_kv(kh_call *c, const ml_kv_layer *kv, const ml_config *cfg) {
+    const size_t n = (size_t)cfg->max_seq * cfg->kv_dim, ns = (size_t)cfg->max_seq * cfg->n_kv_heads;
+    ml_kv_layer d;
+    memset(&d, 0, sizeof d);
+    d.window = kv->window;
+    if (kv->k) {
+        d.k = arg(c, kv->k, F(n), 1, 0);
+        d.v = arg(c, kv->v, F(n), 1, 0);
+    } else {
+        d.kq = arg(c, kv->kq, n, 1, 0);
+        d.vq = arg(c, kv->vq, n, 1, 0);
+        d.kd = arg(c, kv->kd, F(ns), 1, 0);
+        d.vd = arg(c, kv->vd, F(ns), 1, 0);
+    }
+    return d;
+}
+
+/* ops/ops.c:169-180; the Q8 cache's quantized query heads (qq, qd) are
+ * formed inside the score kernel, so the caller's scratch is not used */
 void ml_attention(ml_pool *pool, float *out, const float *q, const ml_kv_layer *kv, float *att_scratch, int8_t *qq,
                   float *qd, const ml_config *cfg, int pos) {
     (void)pool; (void)qq; (void)qd;
     if (!attn_supported(kv, cfg)) return;
-    const size_t cache = F((size_t)cfg->max_seq * cfg->kv_dim);
     kh_call c = { 0 };
     float *o = arg(&c, out, F(cfg->q_dim), 0, 1);
     const float *qv = arg(&c, q, F(cfg->q_dim), 1, 0);
     float *att = arg(&c, att_scratch, F((size_t)cfg->n_heads * cfg->max_seq), 0, 0);
-    const float *kc = arg(&c, kv->k, cache, 1, 0), *vc = arg(&c, kv->v, cache, 1, 0);
+    const ml_kv_layer d = dev_kv(&c, kv, cfg);
     if (!c.fail) {
         krh_set_int(g_ints, pos);
-        krh_attention(o, NULL, NULL, att, qv, kc, vc, cfg->n_heads, cfg->n_kv_heads, cfg->head_dim, cfg->max_seq,
-                      kv->window, cfg->attn_scale, g_ints);
+        krh_attention_kv(o, att, qv, &d, cfg->n_heads, cfg->n_kv_heads, cfg->head_dim, cfg->max_seq,
+                         cfg->attn_scale, g_ints, 1, cfg->max_seq - 1);
     }
     done(&c);
 }
 
+/* ops/ops.c:216-238 */
 void ml_attention_batch(ml_pool *pool, float *out, const float *q, const ml_kv_layer *kv, float *att_scratch,
                         int8_t *qq, float *qd, const ml_config *cfg, int pos0, int n) {
     (void)pool; (void)qq; (void)qd; (void)att_scratch;
     if (n <= 0 || !attn_supported(kv, cfg)) return;
-    const size_t cache = F((size_t)cfg->max_seq * cfg->kv_dim);
     g_batt = grow(g_batt, &g_batt_n, F((size_t)n * cfg->n_heads * cfg->max_seq));
     kh_call c = { 0 };
     float *o = arg(&c, out, F((size_t)n * cfg->q_dim), 0, 1);
     const float *qv = arg(&c, q, F((size_t)n * cfg->q_dim), 1, 0);
-    const float *kc = arg(&c, kv->k, cache, 1, 0), *vc = arg(&c, kv->v, cache, 1, 0);
+    const ml_kv_layer d = dev_kv(&c, kv, cfg);
     if (!c.fail && g_batt) {
         krh_set_int(g_ints, pos0);
-        krh_attention_batch(o, g_batt, qv, kc, vc, cfg->n_heads, cfg->n_kv_heads, cfg->head_dim, cfg->max_seq,
-                            kv->window, cfg->attn_scale, g_ints, n, pos0 + n - 1);
+        krh_attention_kv(o, g_batt, qv, &d, cfg->n_heads, cfg->n_kv_heads, cfg->head_dim, cfg->max_seq,
+                         cfg->attn_scale, g_ints, n, pos0 + n - 1);
     }
     done(&c);
 }

@@ -65,3 +65,34 @@ def test_ml_bench_kernel_table():
     r = subprocess.run([os.path.join(O.REF_DIR, "hip", "ml_bench")], capture_output=True, text=True, timeout=600)
     assert r.returncode == 0, r.stderr
     assert "ISA: hip" in r.stdout and "matvec_q8 -> ml_k_matvec_q8_hip" in r.stdout
+
+
+@pytest.mark.parametrize("batch", [None, 1])
+@pytest.mark.parametrize("name", ["c1_q8", "llama3_rope_gqa_q4", "qwen_like_q4mix"])
+def test_ml_run_kv_q8(name, batch, workdir):
+    """--kv q8 (app/ml_run.c:277-281): store_kv quantizes through
+    ml_quantize_row on the device, attention reads the Q8 rows; the same
+    --dump-logits bytes and ids as the scalar build"""
+    path = model(name, workdir)
+    V = MODELS[name]["vocab"]
+    toks = [int(t) for t in np.random.default_rng(4).integers(1, V, 20)]
+    a, b = path + ".scalar.q8.logits", path + ".hip.q8.logits"
+    O.ref_ml_run(path, toks, len(toks), dump=a, extra=["--kv", "q8"])
+    O.ref_ml_run(path, toks, len(toks), dump=b, isa="hip",
+                 extra=["--kv", "q8"] + (["--batch", str(batch)] if batch else []))
+    x, y = np.fromfile(a, dtype=np.uint8), np.fromfile(b, dtype=np.uint8)
+    assert x.size == len(toks) * V * 4 and np.array_equal(x, y)
+    steps = min(MODELS[name]["max_seq"], 8 + 64)
+    want, _ = O.ref_ml_run(path, toks[:8], steps, extra=["--kv", "q8"])
+    got, _ = O.ref_ml_run(path, toks[:8], steps, isa="hip", extra=["--kv", "q8"])
+    assert np.array_equal(got, want)
+
+
+def test_ml_run_kv_f16_refused(workdir):
+    """the F16 cache is converted by a host loop of model/transformer.c, which
+    this binding cannot serve: the run says so on stderr"""
+    import subprocess
+    path = model("c1_q8", workdir)
+    r = subprocess.run([os.path.join(O.REF_DIR, "hip", "ml_run"), path, "--tokens", "1,2,3", "-n", "3", "-T", "0",
+                        "--kv", "f16"], capture_output=True, text=True, timeout=300)
+    assert "F16 KV cache" in r.stderr
