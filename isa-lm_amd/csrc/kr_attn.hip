@@ -66,9 +66,10 @@ template <> struct Kv4<KV_Q8> {
 };
 
 // Scores of one KV head's query heads for AT_T positions. The K tile is staged
-// in LDS as floats (row stride hd + 1: the lanes of a wave read distinct
-// banks; F16 rows widened exactly, k_scalar.c:124-129); thread (t, j) computes
-// heads j, j + 4, ... of the group for position t.
+// in LDS as floats (F16 rows widened exactly, k_scalar.c:124-129), rows hd + 4
+// floats apart so that the 16-byte reads of 8 consecutive lanes cover all
+// banks once; thread (t, j) computes heads j, j + 4, ... of the group for
+// position t, adding the products in index order.
 template <int KT>
 __device__ __forceinline__ void attn_scores(float *att, const float *q, const KvView kv, int group, int hd, int kv_dim,
                                             int max_seq, int window, float scale, const int *pos_p) {
@@ -79,15 +80,14 @@ __device__ __forceinline__ void attn_scores(float *att, const float *q, const Kv
     q += (size_t)blockIdx.z * gridDim.x * group * hd;
     const int g = blockIdx.x, t0 = blockIdx.y * AT_T, tid = threadIdx.x;
     if (t0 >= n) return;
-    const int nt = min(AT_T, n - t0), ks = hd + 1;
+    const int nt = min(AT_T, n - t0), ks = hd + 4, h4 = hd / 4;
     float *qs = at_smem, *kt = at_smem + group * hd;
-    for (int i = tid; i < group * hd; i += AT_THREADS) qs[i] = q[(size_t)g * group * hd + i];
-    const int h4 = hd / 4;
+    const float4 *qg = (const float4 *)(q + (size_t)g * group * hd);
+    for (int i = tid; i < group * h4; i += AT_THREADS) ((float4 *)qs)[i] = qg[i];
     for (int e = tid; e < nt * h4; e += AT_THREADS) {
         const int r = e / h4, c = e - r * h4;
-        const float4 v = Kv4<KT>::wide(Kv4<KT>::load(kv.k, (size_t)(first + t0 + r) * kv_dim + (size_t)g * hd + 4 * c));
-        float *dst = kt + r * ks + 4 * c;
-        dst[0] = v.x; dst[1] = v.y; dst[2] = v.z; dst[3] = v.w;
+        *(float4 *)(kt + r * ks + 4 * c) =
+            Kv4<KT>::wide(Kv4<KT>::load(kv.k, (size_t)(first + t0 + r) * kv_dim + (size_t)g * hd + 4 * c));
     }
     __syncthreads();
     const int t = tid % AT_T;
@@ -96,8 +96,14 @@ __device__ __forceinline__ void attn_scores(float *att, const float *q, const Kv
     for (int j = tid / AT_T; j < group; j += AT_THREADS / AT_T) {
         const float *qh = qs + j * hd;
         float acc = 0.0f;
-#pragma unroll 8
-        for (int i = 0; i < hd; i++) acc = kr_fadd(acc, kr_fmul(qh[i], kr[i]));
+#pragma unroll 4
+        for (int i = 0; i < hd; i += 4) {
+            const float4 a = *(const float4 *)(qh + i), b = *(const float4 *)(kr + i);
+            acc = kr_fadd(acc, kr_fmul(a.x, b.x));
+            acc = kr_fadd(acc, kr_fmul(a.y, b.y));
+            acc = kr_fadd(acc, kr_fmul(a.z, b.z));
+            acc = kr_fadd(acc, kr_fmul(a.w, b.w));
+        }
         att[(size_t)(g * group + j) * max_seq + t0 + t] = kr_fmul(acc, scale);
     }
 }
@@ -189,10 +195,14 @@ __global__ void __launch_bounds__(AT_THREADS) k_attn_softmax(float *att, int max
     float v[AT_V];
     float m = -INFINITY;
     if (fits) {
+        // slots past the row's end are skipped (a uniform test); the last
+        // live slot's index is clamped: repeats change no max
 #pragma unroll
-        for (int k = 0; k < AT_V; k++) v[k] = a[min(k * AT_THREADS + tid, n - 1)];
+        for (int k = 0; k < AT_V; k++)
+            if (k * AT_THREADS < n) v[k] = a[min(k * AT_THREADS + tid, n - 1)];
 #pragma unroll
-        for (int k = 0; k < AT_V; k++) m = fmaxf(m, v[k]);   // clamped repeats change no max
+        for (int k = 0; k < AT_V; k++)
+            if (k * AT_THREADS < n) m = fmaxf(m, v[k]);
     } else {
         for (int t = tid; t < n; t += AT_THREADS) m = fmaxf(m, a[t]);
     }
@@ -669,7 +679,7 @@ static void attention(float *ao, float *att, const float *q, const KvView &kv, i
     }
     const int group = n_heads / n_kv_heads, kv_dim = n_kv_heads * head_dim;
     const size_t lds = KT == KV_Q8 ? 64 + (size_t)(group * head_dim + 15) / 16 * 16 + (size_t)AT_T * (head_dim + 4)
-                                   : sizeof(float) * ((size_t)group * head_dim + (size_t)AT_T * (head_dim + 1));
+                                   : sizeof(float) * ((size_t)group * head_dim + (size_t)AT_T * (head_dim + 4));
     if (lds > 64 * 1024) {
         kr_fail(ML_E_SHAPE, "attention: head_dim too large for the score tile", hipSuccess);
         return;
