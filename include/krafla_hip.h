@@ -117,6 +117,13 @@ void krh_rmsnorm_matvec_qkv(float *q, float *kc, float *vc, const krh_mat *wq, c
                             float eps, const float *rope_cos, const float *rope_sin, int head_dim, const int *pos);
 void krh_rmsnorm_matvec_swiglu(float *h, const krh_mat *w1, const krh_mat *w3, const float *x, const float *nw,
                                float eps);
+/* krh_rmsnorm_matvec_qkv for the F16 cache: k and v go to row *pos of this
+ * layer's F16 cache (kc, vc: [max_seq][kv_dim] halves), each value rounded as
+ * store_kv rounds it (model/transformer.c:195-197, core/ml.c:39-53) */
+void krh_rmsnorm_matvec_qkv_f16(float *q, uint16_t *kc, uint16_t *vc, const krh_mat *wq, const krh_mat *wk,
+                                const krh_mat *wv, const float *bq, const float *bk, const float *bv, const float *x,
+                                const float *nw, float eps, const float *rope_cos, const float *rope_sin, int head_dim,
+                                const int *pos);
 /* krh_rmsnorm_matvec_qkv for an F16 or Q8 cache: k and v go to the staging
  * rows k, v [kv_dim] (the state's kbuf, vbuf: model/transformer.c:262-263),
  * which krh_store_kv then converts into the cache */

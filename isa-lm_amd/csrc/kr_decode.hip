@@ -48,6 +48,7 @@ struct MvArgs {
     const float *rope_cos, *rope_sin;
     int head_dim, ld_cache;
     const int *pos;
+    int kv16;            // EPI_QKV: k and v rows are the F16 cache's (halves)
 };
 
 constexpr int MV_THREADS = 256;
@@ -489,6 +490,8 @@ __global__ void __launch_bounds__(MV_THREADS, 2) k_matvec(const MvArgs a) {
                                             : kr_fadd(kr_fmul(pa, sn), kr_fmul(pb, c));
                     }
                     if (mi == 0) a.y[0][row] = o;
+                    else if (a.kv16)   // store_kv's rounding (model/transformer.c:195-197)
+                        ((uint16_t *)pick3(mi, a.y[0], a.y[1], a.y[2]))[(size_t)pos * a.ld_cache + row] = kr_f2h(o);
                     else pick3(mi, a.y[0], a.y[1], a.y[2])[(size_t)pos * a.ld_cache + row] = o;
                 }
             } else if (EPI == EPI_SWIGLU) {
@@ -833,12 +836,13 @@ extern "C" void krh_rmsnorm_matvec(float *y, const krh_mat *W, const float *x, c
     mv_plain(y, W, nullptr, nullptr, x, nw, eps, accumulate);
 }
 
-// k and v go to row *pos of the F32 cache, or with stage set to the staging
-// rows kc, vc of an F16 / Q8 cache (model/transformer.c:262-263)
+// k and v go to row *pos of the F32 cache (kv16: of the F16 cache, rounded
+// to halves), or with stage set to the staging rows kc, vc of a Q8 cache
+// (model/transformer.c:262-263)
 static void qkv(float *q, float *kc, float *vc, const krh_mat *wq, const krh_mat *wk, const krh_mat *wv,
                 const float *bq, const float *bk, const float *bv, const int8_t *xq, const float *xd, const float *xf,
                 const float *nw, float eps, const float *rope_cos, const float *rope_sin, int head_dim,
-                const int *pos, bool stage = false) {
+                const int *pos, bool stage = false, bool kv16 = false) {
     if (wq->cols != wk->cols || wq->cols != wv->cols || wk->rows != wv->rows || head_dim % 2 || wq->rows % 2 ||
         wk->rows % 2 || wq->type != wk->type || wq->d16 != wk->d16 || wv->d16 != wq->d16) {
         kr_fail(ML_E_SHAPE, "qkv shapes", hipSuccess);
@@ -871,6 +875,7 @@ static void qkv(float *q, float *kc, float *vc, const krh_mat *wq, const krh_mat
     a.head_dim = head_dim;
     a.ld_cache = stage ? 0 : wk->rows;
     a.pos = pos;
+    a.kv16 = kv16;
     // wq, wk and wv may differ in type (Q4 models keep wv in Q8): one launch
     // per type run
     if (wv->type == wq->type) {
@@ -900,6 +905,15 @@ extern "C" void krh_rmsnorm_matvec_qkv(float *q, float *kc, float *vc, const krh
                                        const float *x, const float *nw, float eps, const float *rope_cos,
                                        const float *rope_sin, int head_dim, const int *pos) {
     qkv(q, kc, vc, wq, wk, wv, bq, bk, bv, nullptr, nullptr, x, nw, eps, rope_cos, rope_sin, head_dim, pos);
+}
+
+extern "C" void krh_rmsnorm_matvec_qkv_f16(float *q, uint16_t *kc, uint16_t *vc, const krh_mat *wq,
+                                           const krh_mat *wk, const krh_mat *wv, const float *bq, const float *bk,
+                                           const float *bv, const float *x, const float *nw, float eps,
+                                           const float *rope_cos, const float *rope_sin, int head_dim,
+                                           const int *pos) {
+    qkv(q, (float *)kc, (float *)vc, wq, wk, wv, bq, bk, bv, nullptr, nullptr, x, nw, eps, rope_cos, rope_sin,
+        head_dim, pos, false, true);
 }
 
 extern "C" void krh_rmsnorm_matvec_qkv_stage(float *q, float *k, float *v, const krh_mat *wq, const krh_mat *wk,

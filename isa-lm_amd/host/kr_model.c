@@ -171,7 +171,7 @@ struct kr_state {
     int kv_type;              /* ML_F32, ML_F16 or ML_Q8_0 (ml_state.kv_type, model/transformer.h:19-26) */
     void *kcache, *vcache;    /* [n_layers][max_seq][kv_dim] floats, halves or int8 */
     float *kd, *vd;           /* Q8: row scales [n_layers][max_seq][n_kv_heads] */
-    float *kst, *vst;         /* F16 / Q8: the projections' K and V rows (kbuf, vbuf) */
+    float *kst, *vst;         /* Q8: the projections' K and V rows (kbuf, vbuf) */
     int8_t *qa_dim, *qa_q, *qa_hid;
     float *qd_dim, *qd_q, *qd_hid;
     int *tok, *pos, *prompt, *log;
@@ -292,9 +292,15 @@ static void issue_step(kr_state *s, int cls) {
                           c->max_seq, L->window, c->attn_scale, s->pos);
         } else {
             const ml_kv_layer kv = kv_layer(s, l);
-            krh_rmsnorm_matvec_qkv_stage(s->q, s->kst, s->vst, &D->wq, &D->wk, &D->wv, D->bq, D->bk, D->bv, s->x,
-                                         D->attn_norm, c->norm_eps, cs, sn, c->head_dim, s->pos);
-            store_kv(s, l, s->kst, s->vst, 1);
+            if (s->kv_type == ML_F16) {   /* the rows rounded to halves in the projection's epilogue */
+                uint16_t *kh = (uint16_t *)s->kcache + (size_t)l * lkv, *vh = (uint16_t *)s->vcache + (size_t)l * lkv;
+                krh_rmsnorm_matvec_qkv_f16(s->q, kh, vh, &D->wq, &D->wk, &D->wv, D->bq, D->bk, D->bv, s->x,
+                                           D->attn_norm, c->norm_eps, cs, sn, c->head_dim, s->pos);
+            } else {
+                krh_rmsnorm_matvec_qkv_stage(s->q, s->kst, s->vst, &D->wq, &D->wk, &D->wv, D->bq, D->bk, D->bv, s->x,
+                                             D->attn_norm, c->norm_eps, cs, sn, c->head_dim, s->pos);
+                store_kv(s, l, s->kst, s->vst, 1);
+            }
             krh_attention_kv(s->ao, s->att, s->q, &kv, c->n_heads, c->n_kv_heads, c->head_dim, c->max_seq,
                              c->attn_scale, s->pos, 1, c->max_seq - 1);
         }
@@ -354,7 +360,7 @@ ml_status kr_state_new(kr_state **out, kr_model *m, int kv_type) {
     s->kv_type = kv_type;
     const size_t f = sizeof(float), kv = (size_t)c->n_layers * c->max_seq * c->kv_dim;
     const size_t ks = (size_t)c->n_layers * c->max_seq * c->n_kv_heads;
-    const int q8 = kv_type == ML_Q8_0, conv = kv_type != ML_F32;
+    const int q8 = kv_type == ML_Q8_0;
     const size_t half = (size_t)c->max_seq * (c->head_dim / 2);
     const int local = c->rope_local_theta > 0.0f;
     struct { void **p; size_t n; } parts[] = {
@@ -363,7 +369,7 @@ ml_status kr_state_new(kr_state **out, kr_model *m, int kv_type) {
         { (void **)&s->att, f * (size_t)c->n_heads * c->max_seq }, { (void **)&s->logits, f * c->vocab },
         { (void **)&s->kcache, kv_elem(kv_type) * kv }, { (void **)&s->vcache, kv_elem(kv_type) * kv },
         { (void **)&s->kd, q8 ? f * ks : 0 }, { (void **)&s->vd, q8 ? f * ks : 0 },
-        { (void **)&s->kst, conv ? f * c->kv_dim : 0 }, { (void **)&s->vst, conv ? f * c->kv_dim : 0 },
+        { (void **)&s->kst, q8 ? f * c->kv_dim : 0 }, { (void **)&s->vst, q8 ? f * c->kv_dim : 0 },
         { (void **)&s->rope_cos, f * half }, { (void **)&s->rope_sin, f * half },
         { (void **)&s->rope_cos_l, local ? f * half : 0 }, { (void **)&s->rope_sin_l, local ? f * half : 0 },
         { (void **)&s->qa_dim, (size_t)c->dim }, { (void **)&s->qd_dim, f * c->dim / QK },

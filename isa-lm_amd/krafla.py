@@ -148,6 +148,8 @@ for name, res, args in [
     ("krh_matvec_swiglu", None, [_P, C.POINTER(KrhMat), C.POINTER(KrhMat), _P, _P]),
     ("krh_attention", None, [_P, _P, _P, _P, _P, _P, _P, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_float,
                              _P]),
+    ("krh_rmsnorm_matvec_qkv_f16", None, [_P, _P, _P, C.POINTER(KrhMat), C.POINTER(KrhMat), C.POINTER(KrhMat),
+                                          _P, _P, _P, _P, _P, C.c_float, _P, _P, C.c_int, _P]),
     ("krh_rmsnorm_matvec_qkv_stage", None, [_P, _P, _P, C.POINTER(KrhMat), C.POINTER(KrhMat), C.POINTER(KrhMat),
                                             _P, _P, _P, _P, _P, C.c_float, _P, _P, C.c_int, _P]),
     ("krh_attention_kv", None, [_P, _P, _P, C.POINTER(MlKvLayer), C.c_int, C.c_int, C.c_int, C.c_int, C.c_float,

@@ -215,3 +215,33 @@ def test_greedy_ids_match_reference_kv(name, kv, workdir):
     assert np.array_equal(ids, ids_ref)
     s.close()
     m.close()
+
+
+@pytest.mark.parametrize("dim,nh,nkv,hd,typ,vtyp,bias", [(896, 14, 2, 64, K.ML_Q4_0, K.ML_Q8_0, 1),
+                                                          (4096, 32, 8, 128, K.ML_Q8_0, K.ML_Q8_0, 0)])
+def test_rmsnorm_qkv_f16_rows(dev, dim, nh, nkv, hd, typ, vtyp, bias):
+    """the F16 cache's projection: the same q, and the cache row *pos holding
+    the half rounding of the F32 projection's k and v (store_kv folded into
+    the epilogue); no other row touched"""
+    from test_gpu_kernels import rand_mat, dmat
+    qd, kvd, max_seq, pos = nh * hd, nkv * hd, 40, 31
+    typs = (typ, typ, vtyp)
+    mats = [rand_mat(r, dim, t, 1) for r, t in zip((qd, kvd, kvd), typs)]
+    Ws = [dmat(dev, q, d, dh, r, dim, t, 1) for (q, d, dh), r, t in zip(mats, (qd, kvd, kvd), typs)]
+    bb = [dev.put(f32(RNG.normal(0, 0.02, r))).ptr if bias else None for r in (qd, kvd, kvd)]
+    cs, sn = dev.put(f32(RNG.uniform(-1, 1, max_seq * hd // 2))), dev.put(f32(RNG.uniform(-1, 1, max_seq * hd // 2)))
+    xb, wb = dev.put(f32(RNG.normal(0, 2, dim))), dev.put(f32(RNG.normal(1, 0.1, dim)))
+    posb = dev.put(np.array([pos], np.int32))
+    q32, k32, v32 = dev.zeros(4 * qd), dev.zeros(4 * max_seq * kvd), dev.zeros(4 * max_seq * kvd)
+    K.hip.krh_rmsnorm_matvec_qkv(q32.ptr, k32.ptr, v32.ptr, *[C.byref(W) for W in Ws], *bb, xb.ptr, wb.ptr, 1e-5,
+                                 cs.ptr, sn.ptr, hd, posb.ptr)
+    sentinel = np.full(max_seq * kvd, 0x1234, np.uint16)
+    q16, k16, v16 = dev.zeros(4 * qd), dev.put(sentinel), dev.put(sentinel)
+    K.hip.krh_rmsnorm_matvec_qkv_f16(q16.ptr, k16.ptr, v16.ptr, *[C.byref(W) for W in Ws], *bb, xb.ptr, wb.ptr, 1e-5,
+                                     cs.ptr, sn.ptr, hd, posb.ptr)
+    ok()
+    assert np.array_equal(bits(q16.get(np.float32, qd)), bits(q32.get(np.float32, qd)))
+    for a32, a16 in ((k32, k16), (v32, v16)):
+        want = sentinel.copy().reshape(max_seq, kvd)
+        want[pos] = f16_rule(a32.get(np.float32, max_seq * kvd).reshape(max_seq, kvd)[pos])
+        assert np.array_equal(a16.get(np.uint16, max_seq * kvd).reshape(max_seq, kvd), want)
