@@ -148,6 +148,13 @@ void krh_attention(float *ao, int8_t *aq, float *ad, float *att, const float *q,
  * sizes the launch (max_seq - 1 when only the device knows *pos0). */
 void krh_attention_kv(float *ao, float *att, const float *q, const ml_kv_layer *kv, int n_heads, int n_kv_heads,
                       int head_dim, int max_seq, float scale, const int *pos0, int ntok, int last_pos);
+/* Decode over the Q8 cache with row *pos not stored yet: krh_store_kv of the
+ * staging rows k_row, v_row [kv_dim] followed by krh_attention_kv (ntok 1),
+ * the store done by the score launch itself (the workgroup whose tile holds
+ * *pos). Same cache contents and results as the two calls. */
+void krh_attention_q8_store(float *ao, float *att, const float *q, const ml_kv_layer *kv, const float *k_row,
+                            const float *v_row, int n_heads, int n_kv_heads, int head_dim, int max_seq, float scale,
+                            const int *pos);
 /* store_kv (model/transformer.c:191-205) of positions *pos0 + t, t < ntok:
  * the staging rows k, v [ntok][n_kv_heads * head_dim] into one layer's cache
  * rows kc, vc [max_seq][kv_dim]. kv_type ML_F16: halves, rounded as

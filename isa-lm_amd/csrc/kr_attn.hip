@@ -36,6 +36,7 @@ struct KvView {
     const void *k, *v;
     const float *kd, *vd;
     int n_kv;
+    const float *ks, *vs;   // Q8 decode: row *pos's K and V, still to be stored (else null)
 };
 
 // 4 consecutive cache elements: the registers as loaded, and widened to
@@ -154,9 +155,34 @@ __global__ void __launch_bounds__(AT_THREADS) k_attn_scores_q8(float *att, const
         for (int i = lane; i < hd; i += 64) qs[j * hd + i] = zero ? (int8_t)0 : (int8_t)kr_q8_elem(qh[i], id);
         if (lane == 0) qd[j] = zero ? 0.0f : kr_fdiv(m, 127.0f);
     }
+    // store_kv folded into decode (model/transformer.c:198-203): the tile
+    // holding the current position quantizes its KV head's K row (wave 0,
+    // straight into the tile as well) and V row (wave 1) into the cache
+    __shared__ float fresh_dk;
+    const bool fresh = kv.ks && t0 + nt == n;
+    if (fresh && wave < 2) {
+        const float *x = (wave ? kv.vs : kv.ks) + (size_t)g * hd;
+        float m = 0.0f;
+        for (int i = lane; i < hd; i += 64) m = fmaxf(m, fabsf(x[i]));
+        for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+        const bool zero = m < KR_QUANT_TINY;
+        const float id = zero ? 0.0f : kr_fdiv(127.0f, m), d = zero ? 0.0f : kr_fdiv(m, 127.0f);
+        const size_t row = (size_t)(first + n - 1);
+        int8_t *dst = (int8_t *)(wave ? kv.v : kv.k) + row * kv_dim + (size_t)g * hd;
+        for (int i = lane; i < hd; i += 64) {
+            const int8_t qv = zero ? (int8_t)0 : (int8_t)kr_q8_elem(x[i], id);
+            dst[i] = qv;
+            if (wave == 0) kt[(nt - 1) * ks + i] = qv;
+        }
+        if (lane == 0) {
+            ((float *)(wave ? kv.vd : kv.kd))[row * kv.n_kv + g] = d;
+            if (wave == 0) fresh_dk = d;
+        }
+    }
     const int h4 = hd / 4;
     for (int e = tid; e < nt * h4; e += AT_THREADS) {
         const int r = e / h4, c = e - r * h4;
+        if (fresh && r == nt - 1) continue;   // written above
         *(int *)(kt + r * ks + 4 * c) =
             *(const int *)((const int8_t *)kv.k + (size_t)(first + t0 + r) * kv_dim + (size_t)g * hd + 4 * c);
     }
@@ -164,7 +190,7 @@ __global__ void __launch_bounds__(AT_THREADS) k_attn_scores_q8(float *att, const
     const int t = tid % AT_T;
     if (t >= nt) return;
     const int8_t *kr = kt + t * ks;
-    const float dk = kv.kd[(size_t)(first + t0 + t) * kv.n_kv + g];
+    const float dk = fresh && t == nt - 1 ? fresh_dk : kv.kd[(size_t)(first + t0 + t) * kv.n_kv + g];
     for (int j = tid / AT_T; j < group; j += AT_THREADS / AT_T) {
         const int8_t *qh = qs + j * hd;
         int sum = 0;
@@ -754,6 +780,17 @@ extern "C" void krh_attention_kv(float *ao, float *att, const float *q, const ml
     } else {
         kr_fail(ML_E_SHAPE, "attention: the cache view has no F32, F16 or Q8 rows", hipSuccess);
     }
+}
+
+extern "C" void krh_attention_q8_store(float *ao, float *att, const float *q, const ml_kv_layer *kv,
+                                       const float *k_row, const float *v_row, int n_heads, int n_kv_heads,
+                                       int head_dim, int max_seq, float scale, const int *pos) {
+    if (!kv || !kv->kq || !kv->vq || !kv->kd || !kv->vd || !k_row || !v_row) {
+        kr_fail(ML_E_SHAPE, "attention_q8_store: a Q8 cache view and the staging rows", hipSuccess);
+        return;
+    }
+    KvView v = { kv->kq, kv->vq, kv->kd, kv->vd, n_kv_heads, k_row, v_row };
+    attention<KV_Q8>(ao, att, q, v, n_heads, n_kv_heads, head_dim, max_seq, kv->window, scale, pos, 1, max_seq - 1);
 }
 
 extern "C" void krh_store_kv(int kv_type, void *kc, void *vc, float *kd, float *vd, const float *k, const float *v,

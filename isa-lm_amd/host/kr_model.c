@@ -296,13 +296,14 @@ static void issue_step(kr_state *s, int cls) {
                 uint16_t *kh = (uint16_t *)s->kcache + (size_t)l * lkv, *vh = (uint16_t *)s->vcache + (size_t)l * lkv;
                 krh_rmsnorm_matvec_qkv_f16(s->q, kh, vh, &D->wq, &D->wk, &D->wv, D->bq, D->bk, D->bv, s->x,
                                            D->attn_norm, c->norm_eps, cs, sn, c->head_dim, s->pos);
-            } else {
+                krh_attention_kv(s->ao, s->att, s->q, &kv, c->n_heads, c->n_kv_heads, c->head_dim, c->max_seq,
+                                 c->attn_scale, s->pos, 1, c->max_seq - 1);
+            } else {   /* Q8: the score launch stores row *pos (store_kv) before reading it */
                 krh_rmsnorm_matvec_qkv_stage(s->q, s->kst, s->vst, &D->wq, &D->wk, &D->wv, D->bq, D->bk, D->bv, s->x,
                                              D->attn_norm, c->norm_eps, cs, sn, c->head_dim, s->pos);
-                store_kv(s, l, s->kst, s->vst, 1);
+                krh_attention_q8_store(s->ao, s->att, s->q, &kv, s->kst, s->vst, c->n_heads, c->n_kv_heads,
+                                       c->head_dim, c->max_seq, c->attn_scale, s->pos);
             }
-            krh_attention_kv(s->ao, s->att, s->q, &kv, c->n_heads, c->n_kv_heads, c->head_dim, c->max_seq,
-                             c->attn_scale, s->pos, 1, c->max_seq - 1);
         }
         krh_matvec_f(s->x, &D->wo, s->ao, 1);
         krh_rmsnorm_matvec_swiglu(s->hb, &D->w1, &D->w3, s->x, D->ffn_norm, c->norm_eps);

@@ -154,6 +154,8 @@ for name, res, args in [
                                             _P, _P, _P, _P, _P, C.c_float, _P, _P, C.c_int, _P]),
     ("krh_attention_kv", None, [_P, _P, _P, C.POINTER(MlKvLayer), C.c_int, C.c_int, C.c_int, C.c_int, C.c_float,
                                 _P, C.c_int, C.c_int]),
+    ("krh_attention_q8_store", None, [_P, _P, _P, C.POINTER(MlKvLayer), _P, _P, C.c_int, C.c_int, C.c_int, C.c_int,
+                                      C.c_float, _P]),
     ("krh_store_kv", None, [C.c_int, _P, _P, _P, _P, _P, _P, C.c_int, C.c_int, _P, C.c_int]),
     ("krh_argmax", None, [_P, _P, C.c_int, _P, _P]),
     ("krh_rmsnorm_q8_t", None, [_P, _P, C.c_int, _P, _P, _P, C.c_int, C.c_float, C.c_int]),

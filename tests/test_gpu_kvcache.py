@@ -245,3 +245,36 @@ def test_rmsnorm_qkv_f16_rows(dev, dim, nh, nkv, hd, typ, vtyp, bias):
         want = sentinel.copy().reshape(max_seq, kvd)
         want[pos] = f16_rule(a32.get(np.float32, max_seq * kvd).reshape(max_seq, kvd)[pos])
         assert np.array_equal(a16.get(np.uint16, max_seq * kvd).reshape(max_seq, kvd), want)
+
+
+@pytest.mark.parametrize("nh,nkv,hd,pos,window", [(32, 8, 128, 2175, 0), (14, 2, 64, 63, 0), (8, 2, 64, 100, 7),
+                                                  (6, 6, 48, 0, 0)])
+def test_attention_q8_store_folded(dev, nh, nkv, hd, pos, window):
+    """decode over the Q8 cache with row *pos still in the staging rows: the
+    same cache contents and output as krh_store_kv then krh_attention_kv"""
+    max_seq = max(256, pos + 1)
+    kvd, qd = nkv * hd, nh * hd
+    q = f32(RNG.normal(0, 1, qd))
+    k, v, kd, vd = rand_cache(K.ML_Q8_0, max_seq, kvd, nkv)
+    krow, vrow = f32(RNG.normal(0, 1, kvd)), f32(RNG.normal(0, 2, kvd))
+    krow[:hd] = 0.0   # an all-zero head: scale 0
+    scale = float(np.float32(1.0) / np.sqrt(np.float32(hd)))
+    posb = dev.put(np.array([pos], np.int32))
+    outs = []
+    for folded in (0, 1):
+        kb, vb, kdb, vdb = dev.put(k), dev.put(v), dev.put(kd), dev.put(vd)
+        view = K.MlKvLayer(None, None, kb.ptr, vb.ptr, kdb.ptr, vdb.ptr, window, None, None)
+        ao, att = dev.zeros(4 * qd), dev.zeros(4 * nh * max_seq)
+        if folded:
+            K.hip.krh_attention_q8_store(ao.ptr, att.ptr, dev.put(q).ptr, C.byref(view), dev.put(krow).ptr,
+                                         dev.put(vrow).ptr, nh, nkv, hd, max_seq, scale, posb.ptr)
+        else:
+            K.hip.krh_store_kv(K.ML_Q8_0, kb.ptr, vb.ptr, kdb.ptr, vdb.ptr, dev.put(krow).ptr, dev.put(vrow).ptr, nkv,
+                               hd, posb.ptr, 1)
+            K.hip.krh_attention_kv(ao.ptr, att.ptr, dev.put(q).ptr, C.byref(view), nh, nkv, hd, max_seq, scale,
+                                   posb.ptr, 1, max_seq - 1)
+        ok()
+        outs.append([ao.get(np.float32, qd).view(np.uint32), kb.get(np.int8, max_seq * kvd), vb.get(np.int8, max_seq * kvd),
+                     kdb.get(np.float32, max_seq * nkv).view(np.uint32), vdb.get(np.float32, max_seq * nkv).view(np.uint32)])
+    for a, b in zip(*outs):
+        assert np.array_equal(a, b)
