@@ -185,9 +185,9 @@ def matvec_microbench(K, iters=1000):
     return out
 
 
-def cpu_baseline(path, prompt, decode, kv="f32"):
-    """the reference's ml_run on the same model file and KV cache type, on
-    this host's cores"""
+def cpu_baseline(path, prompt, decode, kv="f32", sample=None):
+    """the reference's ml_run on the same model file, KV cache type and
+    sampling options, on this host's cores"""
     cores = min(64, len(os.sched_getaffinity(0)))
     n = len(prompt) - 1 + decode
     for isa in ("avx512vnni", "avx2"):
@@ -196,6 +196,9 @@ def cpu_baseline(path, prompt, decode, kv="f32"):
             continue
         cmd = [exe, path, "--tokens", ",".join(str(int(t)) for t in prompt), "-n", str(n), "-T", "0",
                "-t", str(cores), "--kv", kv]
+        if sample:
+            cmd += ["-T", repr(sample.temperature), "-p", repr(sample.topp), "--top-k", str(sample.topk),
+                    "-s", str(sample.seed)]
         r = subprocess.run(cmd, capture_output=True, text=True, timeout=600)
         if r.returncode == 3:   # the reference's ISA guard: this CPU lacks the ISA
             continue
@@ -214,7 +217,8 @@ def cpu_baseline(path, prompt, decode, kv="f32"):
             pass
         return {"value": round(dec, 3), "unit": "tok/s", "cores": cores, "kind": "reference",
                 "build": "ISA=%s THREADS=pthread" % isa, "cpu": cpu,
-                "sample": "ml_run on the same .mlb: %d-token prompt (%d prefilled), %d greedy decode tokens "
+                "sample": "ml_run on the same .mlb: %d-token prompt (%d prefilled), %d " +
+                          ("sampled" if sample else "greedy") + " decode tokens "
                           "at positions %d..%d; decode tok/s = (positions - prefilled) / (positions / tok/s - "
                           "prefill s)" % (len(prompt), P, pos - P, P, pos - 1),
                 "prefill_tok_s": round(P / (M / 1000.0), 2) if M > 0 else None}
@@ -230,6 +234,9 @@ def main():
     ap.add_argument("--prompt", type=int, default=None, help="prompt tokens (default: the workload's)")
     ap.add_argument("--kv", default="f32", choices=["f32", "f16", "q8"],
                     help="KV cache type (ml_run --kv): f32 is the headline configuration")
+    ap.add_argument("--sample", default=None, metavar="T[,TOPP[,TOPK]]",
+                    help="draw the decode tokens with the device sampler (ml_run -T, -p, --top-k; seed 1) "
+                         "instead of the greedy pick")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-matvec", action="store_true")
     ap.add_argument("--roofline-reps", type=int, default=3)
@@ -276,7 +283,15 @@ def main():
             model.close()
             return
 
+        sample = None
+        if args.sample:
+            f = args.sample.split(",")
+            sample = K.sampler_opts(temperature=float(f[0]), topp=float(f[1]) if len(f) > 1 else 0.9,
+                                    topk=int(f[2]) if len(f) > 2 else 0)
+            state.set_sampler(sample)   # a fresh sampler per run: the same draws
         ids_w, pre_w, _ = state.generate(prompt, P - 1 + args.warmup)
+        if sample:
+            state.set_sampler(sample)
         log("warmup: prefill %d tokens %.3f s, %d decode tokens" % (P - 1, pre_w, args.warmup))
         ids, pre_s, dec_s = state.generate(prompt, P - 1 + args.steps)
         n = min(len(ids_w), len(ids))
@@ -309,7 +324,7 @@ def main():
         cpu = None
         if not args.no_cpu_baseline:
             t0 = time.time()
-            cpu = cpu_baseline(path, prompt[:8], 256, args.kv)
+            cpu = cpu_baseline(path, prompt[:8], 256, args.kv, sample)
             log("cpu baseline (%.1f s): %s" % (time.time() - t0, json.dumps(cpu)))
         state.close()
         model.close()
@@ -324,6 +339,8 @@ def main():
         "config": {"workload": desc, "prompt_tokens": P, "prefilled_tokens": P - 1, "decode_tokens": args.steps,
                    "first_decode_position": P - 1, "weight_bytes_per_token": per_tok,
                    "kv_cache": args.kv, "kv_bytes_per_token": kv_tok,
+                   "sampler": ({"temperature": sample.temperature, "topp": sample.topp, "topk": sample.topk,
+                                "seed": sample.seed} if sample else "greedy"),
                    "decode_roofline_tok_s": round(HBM_PEAK_GBS * 1e9 / (per_tok + kv_tok), 1),
                    "parallelism": "single GPU"},
         "prefill_tok_s": round(prefill_tok_s, 2) if prefill_tok_s else None,

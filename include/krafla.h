@@ -50,9 +50,11 @@ void kr_state_free(kr_state *s);
 ml_status kr_forward(kr_state *s, int token, int pos, float *logits);
 /* ml_prefill: n tokens from pos0 into the cache; logits [n][vocab] if non-NULL */
 ml_status kr_prefill(kr_state *s, const int *tokens, int n, int pos0, float *logits);
-/* ml_run's greedy loop (-T 0, no --eos): prompt of np ids, `steps`
- * positions; out receives the ids ml_run prints (returns their count, or
- * -1). Times of the prefill and of the decode loop in seconds, if non-NULL. */
+/* ml_run's loop (no --eos): prompt of np ids, `steps` positions; out
+ * receives the ids ml_run prints (returns their count, or -1). Greedy (-T 0),
+ * or drawn by the sampler of kr_state_set_sampler, which accepts the prompt's
+ * ids first and each drawn id after its draw (app/ml_run.c:361-392). Times of
+ * the prefill and of the decode loop in seconds, if non-NULL. */
 int kr_generate(kr_state *s, const int *prompt, int np, int steps, int *out, double *prefill_s, double *decode_s);
 /* device address of the residual stream x (dim floats), for tests */
 const float *kr_state_x_device(const kr_state *s);
@@ -66,6 +68,10 @@ const void *kr_state_buffer(const kr_state *s, const char *name);
  * 1 = token by token (replays of the decode step), 0 = the default (2048,
  * at most max_seq) */
 void kr_state_set_batch(kr_state *s, int batch);
+/* the sampler kr_generate draws with (ml_run's -T, -p, --top-k,
+ * --repeat-penalty, --repeat-last-n, -s; model/sampler.h:9-16): a new device
+ * sampler, its generator seeded and no ids seen; NULL: greedy (the default) */
+ml_status kr_state_set_sampler(kr_state *s, const krh_sampler_opts *o);
 
 /* ---- seeded synthetic models ---- */
 typedef struct {

@@ -202,6 +202,34 @@ void krh_take_token(int *tok, const int *prompt, const int *pos);
 /* *pos += 1 */
 void krh_advance(int *pos);
 
+/* ---- the device sampler (model/sampler.h:9-35, model/sampler.c) ----
+ * The reference's ml_sample on device logits, with its results: the same id,
+ * the same penalized logits and the same generator state after each draw
+ * (greedy, multinomial, top-k and top-p draws, the repetition penalty). */
+typedef struct {            /* ml_sampler_opts (model/sampler.h:9-16): same fields, same order */
+    float temperature;      /* 0 = greedy */
+    float topp;             /* 0 or 1 = off */
+    int topk;               /* 0 = off */
+    float repeat_penalty;   /* 1 = off */
+    int repeat_last_n;      /* ids the penalty looks back at */
+    uint64_t seed;          /* 0: the reference's fixed constant */
+} krh_sampler_opts;
+typedef struct krh_sampler krh_sampler;
+/* ml_sampler_init (model/sampler.c:6-18): device state for ids below vocab */
+ml_status krh_sampler_new(krh_sampler **s, int vocab, const krh_sampler_opts *o);
+/* ml_sampler_free (:20-28) */
+void krh_sampler_free(krh_sampler *s);
+/* ml_sampler_accept (:30-35) for n ids in device memory, in order */
+void krh_sampler_accept(krh_sampler *s, const int *tokens, int n);
+/* ml_sample (:155-165) on device logits[n], n <= vocab (the penalty writes
+ * them, as there), then ml_sampler_accept of the id (app/ml_run.c:391-392):
+ * *tok = the id; when pos is non-NULL, log[*pos + 1] = id (log non-NULL) and
+ * *pos += 1, as krh_argmax does. Stream-ordered; no host synchronization, so
+ * it can be captured into a graph. */
+void krh_sample(krh_sampler *s, int *tok, float *logits, int n, int *pos, int *log);
+/* the generator state (a synchronous read; for checks) */
+uint64_t krh_sampler_rng(const krh_sampler *s);
+
 /* ---- the reference's unfused kernels (the ml_k_<op>_hip op table) ----
  * Each computes the scalar kernel of kernels/scalar/k_scalar.c in its float
  * order, on device pointers. */

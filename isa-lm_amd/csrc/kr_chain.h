@@ -32,6 +32,11 @@
 // goes on chunk by chunk and runs any failing run one add at a time. So the
 // result is the sequential loop's bits whatever the terms. A negative or
 // non-finite term sends the whole sum through the sequential loop.
+//
+// With REC the walk also records each chunk's true start value (the partial
+// sum before its first term): from those, any prefix sum is one chunk's
+// chain away, which is how a sequential "first partial sum above a bound"
+// search runs in parallel.
 #pragma once
 #include "kr_numerics.h"
 
@@ -189,9 +194,13 @@ __device__ __forceinline__ unsigned sc_rest(const float *t, int sh, int c, int m
 // floats: the last chunk's tail is zero-filled here, and s + 0 == s for
 // s >= +0). lds: sc_lds_bytes(n, NT) bytes, 4-byte aligned. s0 is expected to
 // be >= +0. Contains barriers: all threads must call it, after a barrier that
-// follows the terms' stores.
-template <int NT>
-__device__ __forceinline__ float kr_spec_sum(float *t, int n, unsigned char *lds, float s0 = 0.0f) {
+// follows the terms' stores. REC: cst[c] (c < sc_chunks(n)) receives the bits
+// of the partial sum before chunk c, and cst[sc_chunks(n)] is 1 when a
+// negative or non-finite term sent the sum through the sequential loop (the
+// starts are then not written), else 0.
+template <int NT, bool REC = false>
+__device__ __forceinline__ float kr_spec_sum(float *t, int n, unsigned char *lds, float s0 = 0.0f,
+                                             unsigned *cst = nullptr) {
     constexpr int NW = NT / 64;
     static_assert(NW * SC_CPW >= SC_MAXC, "every chunk needs a lane pair");
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -305,6 +314,12 @@ __device__ __forceinline__ float kr_spec_sum(float *t, int n, unsigned char *lds
     // the walk, in wave 0, 64 chunks (one per lane) at a time
     if (wave == 0) {
         float r;
+        if constexpr (REC) {
+            if (lane == 0) {
+                cst[0] = __float_as_uint(s0);
+                cst[C] = bad ? 1u : 0u;
+            }
+        }
         if (bad) {
             r = sc_seq_all(t, n, sh, s0);
         } else {
@@ -374,6 +389,10 @@ __device__ __forceinline__ float kr_spec_sum(float *t, int n, unsigned char *lds
                          (b >> 23) < 0xFFu;
                 }
                 const unsigned long long fail = __ballot(!ok);
+                if constexpr (REC) {   // starts up to the first failed run are true
+                    const int lim = fail ? __builtin_ctzll(fail) : cnt - 1;
+                    if (lane <= lim && cc > 0) cst[cc] = st;
+                }
                 if (fail) {
                     const int f = __builtin_ctzll(fail);
                     sv = sc_lane(st, f);
@@ -381,7 +400,12 @@ __device__ __forceinline__ float kr_spec_sum(float *t, int n, unsigned char *lds
                     break;
                 }
             }
-            for (int k = cser; k < C; k++) sv = sc_rest(t, sh, k, (int)sc_uni(rm[k]), sv, 0, 0, rb, re0, re1);
+            for (int k = cser; k < C; k++) {
+                if constexpr (REC) {
+                    if (lane == 0) cst[k] = sv;
+                }
+                sv = sc_rest(t, sh, k, (int)sc_uni(rm[k]), sv, 0, 0, rb, re0, re1);
+            }
             r = __uint_as_float(sv);
         }
         if (lane == 0) *res = r;

@@ -178,7 +178,8 @@ struct kr_state {
     void *mem;
     float *h_logits;          /* pinned */
     int *h_ints;              /* pinned: tok, pos */
-    krh_graph *g_logits, *g_greedy, *g_prefill;
+    krh_graph *g_logits, *g_greedy, *g_prefill, *g_sample;
+    krh_sampler *smp;         /* the device sampler of kr_generate, or NULL: greedy */
     int batch;                /* tokens per batched prefill step; 1: token by token */
     int eager;                /* issue ops directly instead of replaying graphs */
     /* batched prefill buffers (allocated on first use): [ldx] token rows */
@@ -314,15 +315,17 @@ static void issue_step(kr_state *s, int cls) {
     krh_rmsnorm_matvec(s->logits, &m->d_wcls, s->x, m->d_final_norm, c->norm_eps, 0);
 }
 
-enum { STEP_LOGITS = 0, STEP_GREEDY = 1, STEP_PREFILL = 2 };
+enum { STEP_LOGITS = 0, STEP_GREEDY = 1, STEP_PREFILL = 2, STEP_SAMPLE = 3 };
 
 /* The ops of one replayed step: STEP_LOGITS (ml_forward), STEP_GREEDY
  * (ml_forward + the greedy pick, appended to the id log), STEP_PREFILL (the
- * next prompt token into the cache, no classifier). */
+ * next prompt token into the cache, no classifier), STEP_SAMPLE (ml_forward
+ * + the sampler's draw and accept, appended to the id log). */
 static void issue(kr_state *s, int kind) {
     if (kind == STEP_PREFILL) krh_take_token(s->tok, s->prompt, s->pos);
     issue_step(s, kind != STEP_PREFILL);
     if (kind == STEP_GREEDY) krh_argmax(s->tok, s->logits, s->m->cfg.vocab, s->pos, s->log);
+    if (kind == STEP_SAMPLE) krh_sample(s->smp, s->tok, s->logits, s->m->cfg.vocab, s->pos, s->log);
     if (kind == STEP_PREFILL) krh_advance(s->pos);
 }
 
@@ -342,7 +345,10 @@ static ml_status run_step(kr_state *s, int kind) {
         issue(s, kind);
         return krh_status();
     }
-    const krh_graph *g = kind == STEP_LOGITS ? s->g_logits : kind == STEP_GREEDY ? s->g_greedy : s->g_prefill;
+    const krh_graph *g = kind == STEP_LOGITS   ? s->g_logits
+                         : kind == STEP_GREEDY ? s->g_greedy
+                         : kind == STEP_SAMPLE ? s->g_sample
+                                               : s->g_prefill;
     return krh_graph_launch(g);
 }
 
@@ -428,10 +434,28 @@ void kr_state_free(kr_state *s) {
     krh_graph_free(s->g_logits);
     krh_graph_free(s->g_greedy);
     krh_graph_free(s->g_prefill);
+    krh_graph_free(s->g_sample);
+    krh_sampler_free(s->smp);
     krh_free(s->mem);
     krh_host_free(s->h_logits);
     krh_host_free(s->h_ints);
     free(s);
+}
+
+ml_status kr_state_set_sampler(kr_state *s, const krh_sampler_opts *o) {
+    krh_graph_free(s->g_sample);
+    krh_sampler_free(s->smp);
+    s->g_sample = NULL;
+    s->smp = NULL;
+    if (!o) return ML_OK;
+    ml_status st = krh_sampler_new(&s->smp, s->m->cfg.vocab, o);
+    if (st == ML_OK && !s->eager) st = capture(s, &s->g_sample, STEP_SAMPLE);
+    if (st != ML_OK) {
+        krh_sampler_free(s->smp);
+        s->smp = NULL;
+        return kr_seterr(st, "%s", krh_last_error());
+    }
+    return ML_OK;
 }
 
 void kr_state_set_batch(kr_state *s, int batch) {
@@ -596,6 +620,10 @@ int kr_generate(kr_state *s, const int *prompt, int np, int steps, int *out, dou
     int n = 0, pos = 0, token = prompt[0];
     const int npre = np - 1 < steps - 1 ? np - 1 : steps - 1;
     double t0 = kr_now();
+    if (s->smp) {   /* app/ml_run.c:369: the prompt's ids first */
+        if (krh_copy_h2d(s->prompt, prompt, sizeof(int) * (size_t)np) != ML_OK) return -1;
+        krh_sampler_accept(s->smp, s->prompt, np);
+    }
     if (npre > 0) {
         if (kr_prefill(s, prompt, npre, 0, NULL) != ML_OK) return -1;
         for (pos = 0; pos < npre; pos++) out[n++] = prompt[pos + 1];
@@ -614,8 +642,9 @@ int kr_generate(kr_state *s, const int *prompt, int np, int steps, int *out, dou
     if (pos < steps) {
         const int first = pos;
         if (set_ints(s, token, pos) != ML_OK) return -1;
+        const int kind = s->smp ? STEP_SAMPLE : STEP_GREEDY;
         for (; pos < steps; pos++)
-            if (run_step(s, STEP_GREEDY) != ML_OK) return -1;
+            if (run_step(s, kind) != ML_OK) return -1;
         if (dev_status() != ML_OK) return -1;
         if (krh_copy_d2h(out + n, s->log + first + 1, sizeof(int) * (size_t)(steps - first)) != ML_OK) return -1;
         n += steps - first;

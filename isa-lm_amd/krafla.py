@@ -158,6 +158,9 @@ for name, res, args in [
                                       C.c_float, _P]),
     ("krh_store_kv", None, [C.c_int, _P, _P, _P, _P, _P, _P, C.c_int, C.c_int, _P, C.c_int]),
     ("krh_argmax", None, [_P, _P, C.c_int, _P, _P]),
+    ("krh_sampler_new", C.c_int, [_P, C.c_int, _P]), ("krh_sampler_free", None, [_P]),
+    ("krh_sampler_accept", None, [_P, _P, C.c_int]), ("krh_sample", None, [_P, _P, _P, C.c_int, _P, _P]),
+    ("krh_sampler_rng", C.c_uint64, [_P]),
     ("krh_rmsnorm_q8_t", None, [_P, _P, C.c_int, _P, _P, _P, C.c_int, C.c_float, C.c_int]),
     ("krh_quantize_q8_t", None, [_P, _P, C.c_int, _P, C.c_int, C.c_int]),
     ("krh_matmul", None, [_P, C.c_int, C.POINTER(KrhMat), _P, _P, C.c_int, C.c_int, C.c_int]),
@@ -198,6 +201,7 @@ for name, res, args in [
     ("kr_prefill", C.c_int, [_P, _P, C.c_int, C.c_int, _P]),
     ("kr_generate", C.c_int, [_P, _P, C.c_int, C.c_int, _P, C.POINTER(C.c_double), C.POINTER(C.c_double)]),
     ("kr_state_x_device", _P, [_P]), ("kr_state_buffer", _P, [_P, C.c_char_p]), ("kr_state_set_batch", None, [_P, C.c_int]),
+    ("kr_state_set_sampler", C.c_int, [_P, _P]),
     ("kr_gen_mlb", C.c_int, [C.c_char_p, C.POINTER(GenSpec)]),
     ("kr_gen_matrix", None, [_P, _P, C.c_int, C.c_int, C.c_int, C.c_uint64, C.c_int]),
     ("kr_gen_normal", None, [_P, C.c_size_t, C.c_uint64]),
@@ -230,6 +234,42 @@ def init_device():
         raise KraflaError("no usable gfx950 device: " + hip.krh_last_error().decode(errors="replace"))
 
 
+class SamplerOpts(C.Structure):
+    """krh_sampler_opts: ml_sampler_opts (model/sampler.h:9-16), same layout"""
+    _fields_ = [("temperature", C.c_float), ("topp", C.c_float), ("topk", C.c_int),
+                ("repeat_penalty", C.c_float), ("repeat_last_n", C.c_int), ("seed", C.c_uint64)]
+
+
+def sampler_opts(temperature=0.0, topp=0.9, topk=0, repeat_penalty=1.0, repeat_last_n=64, seed=1):
+    """ml_run's defaults (app/ml_run.c:244-246)"""
+    return SamplerOpts(temperature, topp, topk, repeat_penalty, repeat_last_n, seed)
+
+
+class Sampler:
+    """The device sampler (krh_sampler): ml_sample on device logits"""
+
+    def __init__(self, vocab, opts):
+        self.ptr = _P()
+        check(hip.krh_sampler_new(C.byref(self.ptr), vocab, C.byref(opts)), "sampler")
+
+    def accept(self, tokens_dev, n):
+        """ml_sampler_accept of n ids at a device address"""
+        hip.krh_sampler_accept(self.ptr, tokens_dev, n)
+
+    def sample(self, tok_dev, logits_dev, n, pos_dev=None, log_dev=None):
+        """the draw into *tok_dev (device addresses), then its accept"""
+        hip.krh_sample(self.ptr, tok_dev, logits_dev, n, pos_dev, log_dev)
+
+    @property
+    def rng(self):
+        return hip.krh_sampler_rng(self.ptr)
+
+    def close(self):
+        if self.ptr:
+            hip.krh_sampler_free(self.ptr)
+            self.ptr = _P()
+
+
 class Model:
     def __init__(self, path):
         self.ptr = _P()
@@ -257,6 +297,10 @@ class State:
 
     def set_batch(self, batch):
         host.kr_state_set_batch(self.ptr, batch)
+
+    def set_sampler(self, opts):
+        """the sampler generate() draws with (SamplerOpts), or None: greedy"""
+        check(host.kr_state_set_sampler(self.ptr, C.byref(opts) if opts is not None else None), "sampler")
 
     def prefill(self, tokens, pos0, logits=None):
         import numpy as np

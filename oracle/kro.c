@@ -649,3 +649,183 @@ const float *kro_state_buffer(const kro_state *s, const char *name) {
     if (!strcmp(name, "rope_sin")) return s->rope_sin;
     return NULL;
 }
+
+/* ---- the sampler: model/sampler.c ----
+ * Restated from the reference's steps: the penalty once per distinct recent
+ * token, temperature, the softmax above, one xorshift64* draw, then the
+ * multinomial walk, the top-k cut or the top-p nucleus, each summed one add
+ * at a time from +0 in the order the reference sums. Candidates are ordered
+ * by (probability descending, id ascending): a total order when the
+ * probabilities are numbers, so any correct sort gives the reference's
+ * sequence. When they are NaN (a NaN logit, or +inf: inf - inf), all of them
+ * are, and the reference's heap and qsort then keep id order; that case is
+ * written out where it matters. */
+struct kro_sampler {
+    kro_sampler_opts o;
+    uint64_t rng;
+    int vocab, n_recent, recent_at;
+    int *recent;
+    float *probs;
+    int *ids;
+};
+
+/* model/sampler.c:6-18 */
+int kro_sampler_new(kro_sampler **out, int vocab, const kro_sampler_opts *o) {
+    kro_sampler *s = calloc(1, sizeof *s);
+    if (!s) return ML_E_NOMEM;
+    s->o = *o;
+    s->vocab = vocab;
+    s->rng = o->seed ? o->seed : 0x9E3779B97F4A7C15ull;
+    if (s->o.repeat_last_n < 0) s->o.repeat_last_n = 0;
+    s->recent = malloc(sizeof(int) * (size_t)(s->o.repeat_last_n > 0 ? s->o.repeat_last_n : 1));
+    s->probs = malloc(sizeof(float) * (size_t)vocab);
+    s->ids = malloc(sizeof(int) * (size_t)vocab);
+    if (!s->recent || !s->probs || !s->ids) { kro_sampler_free(s); return ML_E_NOMEM; }
+    *out = s;
+    return ML_OK;
+}
+
+void kro_sampler_free(kro_sampler *s) {
+    if (!s) return;
+    free(s->recent);
+    free(s->probs);
+    free(s->ids);
+    free(s);
+}
+
+uint64_t kro_sampler_rng(const kro_sampler *s) { return s->rng; }
+
+/* model/sampler.c:30-35: a ring of the last repeat_last_n ids */
+void kro_sampler_accept(kro_sampler *s, int token) {
+    const int R = s->o.repeat_last_n;
+    if (R <= 0 || token < 0 || token >= s->vocab) return;
+    s->recent[s->recent_at] = token;
+    s->recent_at = (s->recent_at + 1) % R;
+    if (s->n_recent < R) s->n_recent++;
+}
+
+/* model/sampler.c:39-48: each distinct id of the ring (below n) once: a
+ * positive logit divided by the penalty, any other multiplied */
+static void smp_penalize(kro_sampler *s, float *logits, int n) {
+    const float rp = s->o.repeat_penalty;
+    if (rp == 1.0f || s->n_recent == 0) return;
+    for (int i = 0; i < s->n_recent; i++) {
+        const int t = s->recent[i];
+        if (t >= n) continue;
+        int dup = 0;
+        for (int j = 0; j < i && !dup; j++) dup = s->recent[j] == t;
+        if (dup) continue;
+        logits[t] = logits[t] > 0.0f ? logits[t] / rp : logits[t] * rp;
+    }
+}
+
+/* model/sampler.c:50-55: xorshift64*, the top 24 bits of the product's high
+ * word over 2^24 */
+static float smp_coin(uint64_t *st) {
+    uint64_t x = *st;
+    x ^= x >> 12;
+    x ^= x << 25;
+    x ^= x >> 27;
+    *st = x;
+    const uint32_t hi = (uint32_t)((x * 0x2545F4914F6CDD1Dull) >> 32);
+    return (float)(hi >> 8) / 16777216.0f;
+}
+
+static const float *g_sort_p;   /* the probabilities qsort orders ids by */
+static int smp_cmp(const void *a, const void *b) {
+    const int i = *(const int *)a, j = *(const int *)b;
+    const float pi = g_sort_p[i], pj = g_sort_p[j];
+    if (pi != pj) return pi > pj ? -1 : 1;
+    return i < j ? -1 : i > j;
+}
+
+/* the first i < m with thr < p[ids[0]] + ... + p[ids[i]] (one add at a time
+ * from +0), or -1; *sum: that partial sum, or the sum of all m */
+static int smp_first_above(const float *p, const int *ids, int m, float thr, float *sum) {
+    float s = 0.0f;
+    for (int i = 0; i < m; i++) {
+        s += p[ids ? ids[i] : i];
+        if (thr < s) { *sum = s; return i; }
+    }
+    *sum = s;
+    return -1;
+}
+
+/* model/sampler.c:155-165 with the draws of :63-70, :84-130 and :132-153 */
+int kro_sample(kro_sampler *s, float *logits, int n) {
+    smp_penalize(s, logits, n);
+    if (s->o.temperature == 0.0f) return kro_argmax(logits, n);
+    float *p = s->probs;
+    for (int i = 0; i < n; i++) p[i] = logits[i] / s->o.temperature;
+    kro_softmax(p, n);
+    const float coin = smp_coin(&s->rng);
+    const float topp = s->o.topp;
+    const int nucleus = topp > 0.0f && topp < 1.0f;
+    const int isnan_p = p[0] != p[0];   /* then every probability is NaN */
+    if (s->o.topk > 0 && s->o.topk < n) {
+        /* :84-130: the k first candidates, their sum, the nucleus cut at
+         * topp of that sum, the draw at coin times the kept mass */
+        const int k = s->o.topk;
+        for (int i = 0; i < n; i++) s->ids[i] = i;
+        if (!isnan_p) {
+            g_sort_p = p;
+            qsort(s->ids, (size_t)n, sizeof(int), smp_cmp);
+        }
+        float total, cum;
+        smp_first_above(p, s->ids, k, INFINITY, &total);
+        int last = k - 1;
+        if (nucleus) {
+            const int i = smp_first_above(p, s->ids, k, topp * total, &cum);
+            if (i >= 0) last = i;
+            total = cum;
+        }
+        float c;
+        const int j = smp_first_above(p, s->ids, last + 1, coin * total, &c);
+        return s->ids[j >= 0 ? j : last];
+    }
+    if (!nucleus) {   /* :63-70 */
+        float c;
+        const int j = smp_first_above(p, NULL, n, coin, &c);
+        return j >= 0 ? j : n - 1;
+    }
+    /* :132-153: candidates at or above (1 - topp) / (n - 1), sorted; the
+     * nucleus is the shortest prefix whose sum exceeds topp */
+    const float cutoff = n > 1 ? (1.0f - topp) / (float)(n - 1) : 0.0f;
+    int m = 0;
+    for (int i = 0; i < n; i++)
+        if (p[i] >= cutoff) s->ids[m++] = i;
+    if (m == 0) return kro_argmax(p, n);
+    g_sort_p = p;
+    qsort(s->ids, (size_t)m, sizeof(int), smp_cmp);
+    float cum, c;
+    const int i = smp_first_above(p, s->ids, m, topp, &cum);
+    const int last = i >= 0 ? i : m - 1;
+    const int j = smp_first_above(p, s->ids, last + 1, coin * cum, &c);
+    return s->ids[j >= 0 ? j : last];
+}
+
+/* app/ml_run.c:361-404 with a sampler: the prompt's ids accepted, every
+ * drawn id accepted after its draw; no --eos */
+int kro_generate_sampled(kro_state *s, kro_sampler *smp, const int *prompt, int np, int steps, int *out) {
+    const ml_config *c = kro_mlb_config(s->m);
+    if (np < 1 || np > c->max_seq) return -1;
+    for (int i = 0; i < np; i++) kro_sampler_accept(smp, prompt[i]);
+    if (steps > c->max_seq) steps = c->max_seq;
+    int token = prompt[0], pos = 0, n = 0;
+    const int npre = np - 1 < steps - 1 ? np - 1 : steps - 1;
+    if (npre > 0) {
+        if (kro_prefill(s, prompt, npre, 0, NULL) != ML_OK) return -1;
+        for (pos = 0; pos < npre; pos++) out[n++] = prompt[pos + 1];
+        token = prompt[npre];
+    }
+    while (pos < steps) {
+        forward(s, token, pos, 1);
+        const int sampled = pos + 1 >= np;
+        const int next = sampled ? kro_sample(smp, s->logits, c->vocab) : prompt[pos + 1];
+        if (sampled) kro_sampler_accept(smp, next);
+        pos++;
+        out[n++] = next;
+        token = next;
+    }
+    return n;
+}

@@ -23,6 +23,9 @@
  *   F16/Q8 KV kernels    bit-equal to the reference's scalar kernels on the
  *                        shapes of tests/test_kernels.c:334-426; unit-scale
  *                        dot_q8 = exact int sum; quantize_row's known answers
+ *   kro_sample           the same ids, rng state and penalized logits as the
+ *                        reference's ml_sample on seeded logits over every
+ *                        option path, plus tests/test_sampler.c's answers
  */
 #ifndef KRO_H
 #define KRO_H
@@ -99,6 +102,23 @@ const float *kro_state_kcache(const kro_state *s, int layer);
 const float *kro_state_buffer(const kro_state *s, const char *name);
 /* the F16 / Q8 cache arrays by name ("kh", "vh", "kq", "vq", "kd", "vd"), or NULL */
 const void *kro_state_cache(const kro_state *s, const char *name);
+
+/* the sampler (model/sampler.h:9-35): options as ml_sampler_opts */
+typedef struct {
+    float temperature, topp;
+    int topk;
+    float repeat_penalty;
+    int repeat_last_n;
+    uint64_t seed;
+} kro_sampler_opts;
+typedef struct kro_sampler kro_sampler;
+int kro_sampler_new(kro_sampler **s, int vocab, const kro_sampler_opts *o);   /* model/sampler.c:6-18 */
+void kro_sampler_free(kro_sampler *s);
+void kro_sampler_accept(kro_sampler *s, int token);                          /* :30-35 */
+int kro_sample(kro_sampler *s, float *logits, int n);                        /* :155-165 */
+uint64_t kro_sampler_rng(const kro_sampler *s);
+/* ml_run's loop with sampling (app/ml_run.c:361-404) */
+int kro_generate_sampled(kro_state *s, kro_sampler *smp, const int *prompt, int np, int steps, int *out);
 
 #ifdef __cplusplus
 }

@@ -151,6 +151,13 @@ class OracleModel:
         assert n >= 0
         return out[:n].copy()
 
+    def generate_sampled(self, sampler, prompt, steps):
+        p = np.ascontiguousarray(prompt, dtype=np.int32)
+        out = np.zeros(steps + len(p) + 2, dtype=np.int32)
+        n = oracle.kro_generate_sampled(self.s, sampler.s, p.ctypes.data, len(p), steps, out.ctypes.data)
+        assert n >= 0
+        return out[:n].copy()
+
     def buffer(self, name, count):
         p = oracle.kro_state_buffer(self.s, name.encode())
         return np.ctypeslib.as_array(p, shape=(count,)).copy()
@@ -158,6 +165,75 @@ class OracleModel:
     def close(self):
         oracle.kro_state_free(self.s)
         oracle.kro_model_close(self.m)
+
+
+# ml_sampler_opts (model/sampler.h:9-16): kro_sampler_opts and
+# krh_sampler_opts share its layout
+SamplerOpts = K.SamplerOpts
+sampler_opts = K.sampler_opts
+
+
+class RefSampler(C.Structure):
+    """ml_sampler (model/sampler.h:18-27)"""
+    _fields_ = [("o", SamplerOpts), ("rng", C.c_uint64), ("vocab", C.c_int), ("probs", _P), ("cand", _P),
+                ("recent", _P), ("n_recent", C.c_int), ("recent_at", C.c_int), ("mark", _P), ("stamp", C.c_int)]
+
+
+oracle.kro_sampler_new.argtypes = [_P, C.c_int, C.POINTER(SamplerOpts)]
+oracle.kro_sampler_free.argtypes = [_P]
+oracle.kro_sampler_accept.argtypes = [_P, C.c_int]
+oracle.kro_sample.argtypes = [_P, _P, C.c_int]
+oracle.kro_sampler_rng.restype = C.c_uint64
+oracle.kro_sampler_rng.argtypes = [_P]
+oracle.kro_generate_sampled.argtypes = [_P, _P, _P, C.c_int, C.c_int, _P]
+if ref is not None:
+    ref.ml_sampler_init.argtypes = [C.POINTER(RefSampler), C.c_int, C.POINTER(SamplerOpts)]
+    ref.ml_sampler_accept.argtypes = [C.POINTER(RefSampler), C.c_int]
+    ref.ml_sample.argtypes = [C.POINTER(RefSampler), _P, C.c_int]
+    ref.ml_sampler_free.argtypes = [C.POINTER(RefSampler)]
+
+
+class OracleSampler:
+    def __init__(self, vocab, opts):
+        self.s = _P()
+        assert oracle.kro_sampler_new(C.byref(self.s), vocab, C.byref(opts)) == 0
+
+    def accept(self, tok):
+        oracle.kro_sampler_accept(self.s, int(tok))
+
+    def sample(self, logits):
+        """the id; logits (float32, modified in place as the reference does)"""
+        assert logits.dtype == np.float32 and logits.flags.c_contiguous
+        return oracle.kro_sample(self.s, logits.ctypes.data, len(logits))
+
+    @property
+    def rng(self):
+        return oracle.kro_sampler_rng(self.s)
+
+    def close(self):
+        oracle.kro_sampler_free(self.s)
+
+
+class ReferenceSampler:
+    """the reference's own ml_sampler (oracle/_ref/libkrafla_ref_scalar.so)"""
+
+    def __init__(self, vocab, opts):
+        self.s = RefSampler()
+        assert ref.ml_sampler_init(C.byref(self.s), vocab, C.byref(opts)) == 0
+
+    def accept(self, tok):
+        ref.ml_sampler_accept(C.byref(self.s), int(tok))
+
+    def sample(self, logits):
+        assert logits.dtype == np.float32 and logits.flags.c_contiguous
+        return ref.ml_sample(C.byref(self.s), logits.ctypes.data, len(logits))
+
+    @property
+    def rng(self):
+        return self.s.rng
+
+    def close(self):
+        ref.ml_sampler_free(C.byref(self.s))
 
 
 def ref_ml_run(model, tokens, steps, threads=1, dump=None, isa="scalar", timeout=600, extra=()):

@@ -450,6 +450,24 @@ def test_binding_declares_every_export():
         assert exported and exported <= lib.declared(), sorted(exported - lib.declared())
 
 
+def test_libraries_export_every_declared_function():
+    """every function include/krafla_hip.h and include/krafla.h declare is
+    exported by libkrafla_hip.so or libkrafla.so"""
+    import re
+    import subprocess
+    exported = set()
+    for libpath in (K.LIB_HIP, K.LIB_HOST):
+        out = subprocess.run(["nm", "-D", "--defined-only", libpath], capture_output=True, text=True).stdout
+        exported |= {l.split()[-1] for l in out.splitlines() if " T " in l}
+    declared = set()
+    for h in ("krafla_hip.h", "krafla.h"):
+        text = open(os.path.join(O.ROOT, "include", h)).read()
+        text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+        declared |= set(re.findall(r"^[A-Za-z_][\w \t\*]*?\b(krh?_\w+)\s*\(", text, flags=re.M))
+    assert len(declared) > 50 and "krh_sample" in declared
+    assert declared <= exported, sorted(declared - exported)
+
+
 @needs_ref
 @pytest.mark.parametrize("kv", ["q8", "f16"])
 @pytest.mark.parametrize("name", ["c1_q8", "llama3_rope_gqa_q4", "qwen_like_q4mix"])
