@@ -89,6 +89,8 @@ typedef struct {
     uint64_t seed;
     int threads;
     int device;            /* draw the matrices on the GPU (krh_gen_blocks) */
+    int qk_norm;           /* per-head q/k RMSNorm weights (Qwen3) */
+    int post_norms;        /* post-attention and post-FFN RMSNorm weights (Gemma 3) */
 } kr_gen_spec;
 /* Writes an .mlb: matrices and embedding N(0, std^2), norms 1 + 0.01 N,
  * biases 0.02 N, quantized by the format's rules (docs/file-format.md:133-159). */

@@ -202,6 +202,17 @@ void krh_take_token(int *tok, const int *prompt, const int *pos);
 /* *pos += 1 */
 void krh_advance(int *pos);
 
+/* ---- the families' steps (model/transformer.c:240-248) ----
+ * q heads [0, n_heads) and k heads [0, n_kv_heads): each RMS-normalized with
+ * q_norm / k_norm when they are non-NULL (Qwen3's heads_norm, :246-248;
+ * kernels/scalar/k_scalar.c:59-64), then rotated (k_scalar.c:79-94) by row
+ * *pos of the tables (head_dim / 2 floats a row). head_dim even, <= 512. */
+void krh_heads_norm_rope(float *q, float *k, const float *q_norm, const float *k_norm, const float *cos_t,
+                         const float *sin_t, int head_dim, int n_heads, int n_kv_heads, float eps, const int *pos);
+/* F32 cache rows: kc[*pos][i] = k[i], vc[*pos][i] = v[i] for i < kv_dim
+ * (the reference's projections write them in place, model/transformer.c:263-264) */
+void krh_store_rows_f32(float *kc, float *vc, const float *k, const float *v, int kv_dim, const int *pos);
+
 /* ---- the device sampler (model/sampler.h:9-35, model/sampler.c) ----
  * The reference's ml_sample on device logits, with its results: the same id,
  * the same penalized logits and the same generator state after each draw

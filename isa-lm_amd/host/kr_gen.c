@@ -191,6 +191,8 @@ ml_status kr_gen_mlb(const char *path, const kr_gen_spec *sp) {
     }
     wr32(h, 72, sp->wtype == ML_Q4_0 ? sp->q8_mask : 0u);
     wr32(h, 76, sp->qkv_bias ? 1u : 0u);
+    wr32(h, 84, sp->qk_norm ? 1u : 0u);
+    wr32(h, 108, sp->post_norms ? 1u : 0u);
     wr32(h, 120, sp->scale_f16 ? 1u : 0u);
     ml_config c;
     int shared;
@@ -231,10 +233,21 @@ ml_status kr_gen_mlb(const char *path, const kr_gen_spec *sp) {
             put_vec(&w, stream_key(sp->seed, s++), c.kv_dim, 0.0f, 0.02f);
             put_vec(&w, stream_key(sp->seed, s++), c.kv_dim, 0.0f, 0.02f);
         }
+        /* the family norms draw from streams of their own: the other tensors
+         * stay those of the same model without them */
+        const uint64_t fam = sp->seed ^ 0x3C6EF372FE94F82BULL;
+        if (c.qk_norm) {   /* q_norm, k_norm (model/mlb.c's order) */
+            put_vec(&w, stream_key(fam, 4 * (uint64_t)l), c.head_dim, 1.0f, 0.1f);
+            put_vec(&w, stream_key(fam, 4 * (uint64_t)l + 1), c.head_dim, 1.0f, 0.1f);
+        }
         put_vec(&w, stream_key(sp->seed, s++), c.dim, 1.0f, 0.01f);
         put_mat(&w, stream_key(sp->seed, s++), c.hidden_dim, c.dim, WT(ML_Q8M_UP), f16, sd, th);
         put_mat(&w, stream_key(sp->seed, s++), c.dim, c.hidden_dim, WT(ML_Q8M_DOWN), f16, sd, th);
         put_mat(&w, stream_key(sp->seed, s++), c.hidden_dim, c.dim, WT(ML_Q8M_UP), f16, sd, th);
+        if (c.post_norms) {   /* post_attn_norm, post_ffn_norm */
+            put_vec(&w, stream_key(fam, 4 * (uint64_t)l + 2), c.dim, 1.0f, 0.1f);
+            put_vec(&w, stream_key(fam, 4 * (uint64_t)l + 3), c.dim, 1.0f, 0.1f);
+        }
     }
     put_vec(&w, stream_key(sp->seed, s++), c.dim, 1.0f, 0.01f);
     if (!shared) put_mat(&w, stream_key(sp->seed, s++), c.vocab, c.dim, WT(ML_Q8M_CLS), f16, sd, th);

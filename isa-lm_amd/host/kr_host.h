@@ -22,6 +22,7 @@ struct kr_model {
 
 struct kr_dev_layer {
     const float *attn_norm, *ffn_norm, *bq, *bk, *bv;
+    const float *q_norm, *k_norm, *post_attn_norm, *post_ffn_norm;   /* NULL unless the model has them */
     krh_mat wq, wk, wv, wo, w1, w2, w3;
 };
 

@@ -94,6 +94,8 @@ ml_status kr_model_upload(kr_model *m) {
         for (int k = 0; k < 7; k++) total += mat_bytes(ws[k], f16);
         total += 2 * RUP(fd);
         if (L->bq) total += RUP(sizeof(float) * c->q_dim) + 2 * RUP(sizeof(float) * c->kv_dim);
+        if (L->q_norm) total += 2 * RUP(sizeof(float) * c->head_dim);
+        if (L->post_attn_norm) total += 2 * RUP(fd);
     }
     m->dev = krh_alloc(total);
     if (!m->dev) return kr_seterr(ML_E_NOMEM, "cannot allocate %zu bytes of HBM for the weights", total);
@@ -118,6 +120,14 @@ ml_status kr_model_upload(kr_model *m) {
             D->bq = place(&p, L->bq, sizeof(float) * c->q_dim);
             D->bk = place(&p, L->bk, sizeof(float) * c->kv_dim);
             D->bv = place(&p, L->bv, sizeof(float) * c->kv_dim);
+        }
+        if (L->q_norm) {
+            D->q_norm = place(&p, L->q_norm, sizeof(float) * c->head_dim);
+            D->k_norm = place(&p, L->k_norm, sizeof(float) * c->head_dim);
+        }
+        if (L->post_attn_norm) {
+            D->post_attn_norm = place(&p, L->post_attn_norm, fd);
+            D->post_ffn_norm = place(&p, L->post_ffn_norm, fd);
         }
     }
     m->d_final_norm = place(&p, m->final_norm, fd);
@@ -171,7 +181,9 @@ struct kr_state {
     int kv_type;              /* ML_F32, ML_F16 or ML_Q8_0 (ml_state.kv_type, model/transformer.h:19-26) */
     void *kcache, *vcache;    /* [n_layers][max_seq][kv_dim] floats, halves or int8 */
     float *kd, *vd;           /* Q8: row scales [n_layers][max_seq][n_kv_heads] */
-    float *kst, *vst;         /* Q8: the projections' K and V rows (kbuf, vbuf) */
+    float *kst, *vst;         /* Q8 and the families' path: the projections' K and V rows (kbuf, vbuf) */
+    float *yb;                /* post-norms: a block's output before its norm (xb2) */
+    int family;               /* q/k-norm or post-norms: the unfused layer path */
     int8_t *qa_dim, *qa_q, *qa_hid;
     float *qd_dim, *qd_q, *qd_hid;
     int *tok, *pos, *prompt, *log;
@@ -274,6 +286,7 @@ static void rope_tables(const ml_config *c, float *cs, float *sn, float *cs_l, f
 
 /* ml_forward's ops for the token in s->tok at position s->pos; cls: run the
  * final norm and the classifier too */
+static void issue_family_layer(kr_state *s, int l, const float *cs, const float *sn);
 static void issue_step(kr_state *s, int cls) {
     const kr_model *m = s->m;
     const ml_config *c = &m->cfg;
@@ -283,6 +296,10 @@ static void issue_step(kr_state *s, int cls) {
         const struct kr_dev_layer *D = &m->d_layers[l];
         const ml_layer *L = &m->layers[l];
         const float *cs = L->local_rope ? s->rope_cos_l : s->rope_cos, *sn = L->local_rope ? s->rope_sin_l : s->rope_sin;
+        if (s->family) {
+            issue_family_layer(s, l, cs, sn);
+            continue;
+        }
         /* each norm runs inside the launch that consumes it, under that
          * launch's first weight loads */
         if (s->kv_type == ML_F32) {
@@ -313,6 +330,51 @@ static void issue_step(kr_state *s, int cls) {
     }
     if (!cls) return;
     krh_rmsnorm_matvec(s->logits, &m->d_wcls, s->x, m->d_final_norm, c->norm_eps, 0);
+}
+
+/* A layer of a model with q/k-norm (Qwen3) or post-norms (Gemma 3), in
+ * ml_forward's order with unfused launches (model/transformer.c:266-297): the
+ * projections store q and the staging rows k, v unrotated; the biases; each
+ * head normalized, then rotated at *pos; the cache row stored; attention;
+ * each block's output normalized before its residual add. */
+static void issue_family_layer(kr_state *s, int l, const float *cs, const float *sn) {
+    const kr_model *m = s->m;
+    const ml_config *c = &m->cfg;
+    const struct kr_dev_layer *D = &m->d_layers[l];
+    krh_rmsnorm_q8(s->qa_dim, s->qd_dim, NULL, s->x, D->attn_norm, c->dim, c->norm_eps, 1);
+    krh_matvec(s->q, &D->wq, s->qa_dim, s->qd_dim, 0);
+    krh_matvec(s->kst, &D->wk, s->qa_dim, s->qd_dim, 0);
+    krh_matvec(s->vst, &D->wv, s->qa_dim, s->qd_dim, 0);
+    if (D->bq) {
+        krh_add(s->q, D->bq, c->q_dim);
+        krh_add(s->kst, D->bk, c->kv_dim);
+        krh_add(s->vst, D->bv, c->kv_dim);
+    }
+    krh_heads_norm_rope(s->q, s->kst, D->q_norm, D->k_norm, cs, sn, c->head_dim, c->n_heads, c->n_kv_heads,
+                        c->norm_eps, s->pos);
+    const ml_kv_layer kv = kv_layer(s, l);
+    if (s->kv_type == ML_F32)
+        krh_store_rows_f32((float *)kv.k, (float *)kv.v, s->kst, s->vst, c->kv_dim, s->pos);
+    else
+        store_kv(s, l, s->kst, s->vst, 1);
+    krh_attention_kv(s->ao, s->att, s->q, &kv, c->n_heads, c->n_kv_heads, c->head_dim, c->max_seq, c->attn_scale,
+                     s->pos, 1, c->max_seq - 1);
+    if (D->post_attn_norm) {
+        krh_matvec_f(s->yb, &D->wo, s->ao, 0);
+        krh_rmsnorm(s->yb, s->yb, D->post_attn_norm, c->dim, c->norm_eps);
+        krh_add(s->x, s->yb, c->dim);
+    } else {
+        krh_matvec_f(s->x, &D->wo, s->ao, 1);
+    }
+    krh_rmsnorm_matvec_swiglu(s->hb, &D->w1, &D->w3, s->x, D->ffn_norm, c->norm_eps);
+    krh_quantize_q8(s->qa_hid, s->qd_hid, s->hb, c->hidden_dim, 1);
+    if (D->post_ffn_norm) {
+        krh_matvec(s->yb, &D->w2, s->qa_hid, s->qd_hid, 0);
+        krh_rmsnorm(s->yb, s->yb, D->post_ffn_norm, c->dim, c->norm_eps);
+        krh_add(s->x, s->yb, c->dim);
+    } else {
+        krh_matvec(s->x, &D->w2, s->qa_hid, s->qd_hid, 1);
+    }
 }
 
 enum { STEP_LOGITS = 0, STEP_GREEDY = 1, STEP_PREFILL = 2, STEP_SAMPLE = 3 };
@@ -357,8 +419,8 @@ ml_status kr_state_new(kr_state **out, kr_model *m, int kv_type) {
     const ml_config *c = &m->cfg;
     if (kv_type != ML_F32 && kv_type != ML_F16 && kv_type != ML_Q8_0)
         return kr_seterr(ML_E_SHAPE, "KV cache type %d: F32, F16 or Q8_0", kv_type);
-    if (c->qk_norm || c->post_norms || c->act != ML_ACT_SILU || c->attn_softcap > 0.0f || c->final_softcap > 0.0f)
-        return kr_seterr(ML_E_SHAPE, "model uses q/k norm, post-norms, GELU or soft-capping: not supported");
+    if (c->act != ML_ACT_SILU || c->attn_softcap > 0.0f || c->final_softcap > 0.0f)
+        return kr_seterr(ML_E_SHAPE, "model uses GELU or soft-capping: not supported");
     ml_status st = kr_model_upload(m);
     if (st != ML_OK) return st;
     kr_state *s = calloc(1, sizeof *s);
@@ -367,7 +429,8 @@ ml_status kr_state_new(kr_state **out, kr_model *m, int kv_type) {
     s->kv_type = kv_type;
     const size_t f = sizeof(float), kv = (size_t)c->n_layers * c->max_seq * c->kv_dim;
     const size_t ks = (size_t)c->n_layers * c->max_seq * c->n_kv_heads;
-    const int q8 = kv_type == ML_Q8_0;
+    const int q8 = kv_type == ML_Q8_0, fam = c->qk_norm || c->post_norms;
+    s->family = fam;
     const size_t half = (size_t)c->max_seq * (c->head_dim / 2);
     const int local = c->rope_local_theta > 0.0f;
     struct { void **p; size_t n; } parts[] = {
@@ -376,7 +439,8 @@ ml_status kr_state_new(kr_state **out, kr_model *m, int kv_type) {
         { (void **)&s->att, f * (size_t)c->n_heads * c->max_seq }, { (void **)&s->logits, f * c->vocab },
         { (void **)&s->kcache, kv_elem(kv_type) * kv }, { (void **)&s->vcache, kv_elem(kv_type) * kv },
         { (void **)&s->kd, q8 ? f * ks : 0 }, { (void **)&s->vd, q8 ? f * ks : 0 },
-        { (void **)&s->kst, q8 ? f * c->kv_dim : 0 }, { (void **)&s->vst, q8 ? f * c->kv_dim : 0 },
+        { (void **)&s->kst, q8 || fam ? f * c->kv_dim : 0 }, { (void **)&s->vst, q8 || fam ? f * c->kv_dim : 0 },
+        { (void **)&s->yb, c->post_norms ? f * c->dim : 0 },
         { (void **)&s->rope_cos, f * half }, { (void **)&s->rope_sin, f * half },
         { (void **)&s->rope_cos_l, local ? f * half : 0 }, { (void **)&s->rope_sin_l, local ? f * half : 0 },
         { (void **)&s->qa_dim, (size_t)c->dim }, { (void **)&s->qd_dim, f * c->dim / QK },
@@ -415,6 +479,7 @@ ml_status kr_state_new(kr_state **out, kr_model *m, int kv_type) {
     if (st == ML_OK && local) st = krh_copy_h2d(s->rope_sin_l, snl, f * half);
     free(cs); free(sn); free(csl); free(snl);
     s->batch = c->max_seq < KR_PREFILL_STEP ? c->max_seq : KR_PREFILL_STEP;
+    if (fam) s->batch = 1;   /* the batched prefill kernels fuse RoPE: these models replay the decode step */
     const char *ev = getenv("KRAFLA_EAGER");
     s->eager = ev && ev[0] == '1';
     if (st == ML_OK && !s->eager) st = capture(s, &s->g_logits, STEP_LOGITS);
@@ -460,6 +525,7 @@ ml_status kr_state_set_sampler(kr_state *s, const krh_sampler_opts *o) {
 
 void kr_state_set_batch(kr_state *s, int batch) {
     if (batch < 1) batch = KR_PREFILL_STEP;
+    if (s->family) batch = 1;
     if (batch > s->m->cfg.max_seq) batch = s->m->cfg.max_seq;
     if (batch != s->batch && s->bmem) {   /* re-sized on next use */
         krh_free(s->bmem);

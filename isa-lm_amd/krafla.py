@@ -58,7 +58,8 @@ class GenSpec(C.Structure):
         ("rope_theta", C.c_float), ("norm_eps", C.c_float), ("wtype", C.c_int), ("q8_mask", C.c_uint),
         ("shared", C.c_int), ("qkv_bias", C.c_int), ("scale_f16", C.c_int), ("rope_type", C.c_int),
         ("rope_factor", C.c_float), ("rope_low_freq_factor", C.c_float), ("rope_high_freq_factor", C.c_float),
-        ("rope_orig_max_seq", C.c_int), ("std", C.c_float), ("seed", C.c_uint64), ("threads", C.c_int), ("device", C.c_int)]
+        ("rope_orig_max_seq", C.c_int), ("std", C.c_float), ("seed", C.c_uint64), ("threads", C.c_int), ("device", C.c_int),
+        ("qk_norm", C.c_int), ("post_norms", C.c_int)]
 
 
 # The workloads, by name. Shapes and quantization as the benchmark configs
@@ -69,7 +70,7 @@ class GenSpec(C.Structure):
 def _spec(**kw):
     base = dict(rope_theta=1e4, norm_eps=1e-5, wtype=ML_Q8_0, q8_mask=0, shared=0, qkv_bias=0, scale_f16=0,
                 rope_type=ML_ROPE_NONE, rope_factor=0.0, rope_low_freq_factor=0.0, rope_high_freq_factor=0.0,
-                rope_orig_max_seq=0, std=0.02, seed=1, threads=8, device=0)
+                rope_orig_max_seq=0, std=0.02, seed=1, threads=8, device=0, qk_norm=0, post_norms=0)
     base.update(kw)
     return base
 
@@ -161,6 +162,8 @@ for name, res, args in [
     ("krh_sampler_new", C.c_int, [_P, C.c_int, _P]), ("krh_sampler_free", None, [_P]),
     ("krh_sampler_accept", None, [_P, _P, C.c_int]), ("krh_sample", None, [_P, _P, _P, C.c_int, _P, _P]),
     ("krh_sampler_rng", C.c_uint64, [_P]),
+    ("krh_heads_norm_rope", None, [_P, _P, _P, _P, _P, _P, C.c_int, C.c_int, C.c_int, C.c_float, _P]),
+    ("krh_store_rows_f32", None, [_P, _P, _P, _P, C.c_int, _P]),
     ("krh_rmsnorm_q8_t", None, [_P, _P, C.c_int, _P, _P, _P, C.c_int, C.c_float, C.c_int]),
     ("krh_quantize_q8_t", None, [_P, _P, C.c_int, _P, C.c_int, C.c_int]),
     ("krh_matmul", None, [_P, C.c_int, C.POINTER(KrhMat), _P, _P, C.c_int, C.c_int, C.c_int]),

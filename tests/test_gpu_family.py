@@ -1,0 +1,121 @@
+"""The families' layer path on the device: q/k RMSNorm per head (Qwen3) and
+post-norms (Gemma 3), model/transformer.c:240-248. The heads' norm and RoPE
+kernel against the oracle's kernels; whole-model logits and greedy ids
+against the reference's ml_run, with each KV cache type."""
+import ctypes as C
+import os
+
+import numpy as np
+import pytest
+
+import krafla as K
+import oracle_lib as O
+from oracle_lib import oracle
+
+pytestmark = pytest.mark.gpu
+
+FAMILY = {
+    "qk_norm_bias_gqa": dict(K.CONFIGS["qwen05b_mixed"], dim=128, n_layers=2, n_heads=4, n_kv_heads=2,
+                             hidden_dim=256, vocab=512, max_seq=96, std=0.1, qk_norm=1),
+    "post_norms_q8": dict(K.CONFIGS["stories15m_q8"], std=0.1, seed=3, post_norms=1),
+    "qk_post_norms_f16": dict(K.CONFIGS["llama8b_q8"], dim=256, n_layers=2, n_heads=2, n_kv_heads=1,
+                              hidden_dim=384, vocab=600, max_seq=128, std=0.1, qk_norm=1, post_norms=1),
+}
+KV = {"f32": K.ML_F32, "f16": K.ML_F16, "q8": K.ML_Q8_0}
+
+
+@pytest.fixture(scope="module", autouse=True)
+def device():
+    K.init_device()
+    yield
+    K.hip.krh_sync()
+
+
+def ok():
+    st = K.hip.krh_sync()
+    assert st == 0, K.hip.krh_last_error().decode()
+
+
+def bits(a):
+    return np.ascontiguousarray(a, dtype=np.float32).view(np.uint32)
+
+
+@pytest.mark.parametrize("hd,nh,nkv,normed", [(128, 32, 8, True), (64, 4, 2, True), (256, 3, 1, True),
+                                             (128, 4, 4, False), (2, 1, 1, True)])
+def test_heads_norm_rope(hd, nh, nkv, normed):
+    """each head: k_scalar.c:59-64's rmsnorm with the head weight, then
+    k_scalar.c:79-94's rotation by the tables' row *pos"""
+    rng = np.random.default_rng(hd + nh)
+    q = (rng.standard_normal(nh * hd) * 3).astype(np.float32)
+    k = (rng.standard_normal(nkv * hd) * 3).astype(np.float32)
+    qw = (1 + 0.1 * rng.standard_normal(hd)).astype(np.float32)
+    kw = (1 + 0.1 * rng.standard_normal(hd)).astype(np.float32)
+    P, pos = 40, 33
+    ang = rng.uniform(-3, 3, (P, hd // 2))
+    cs, sn = np.cos(ang).astype(np.float32), np.sin(ang).astype(np.float32)
+    eps = np.float32(1e-6)
+    wq, wk = q.copy(), k.copy()
+    if normed:
+        for h in range(nh):
+            seg = wq[h * hd:(h + 1) * hd].copy()
+            oracle.kro_rmsnorm(wq[h * hd:].ctypes.data, seg.ctypes.data, qw.ctypes.data, hd, eps)
+        for h in range(nkv):
+            seg = wk[h * hd:(h + 1) * hd].copy()
+            oracle.kro_rmsnorm(wk[h * hd:].ctypes.data, seg.ctypes.data, kw.ctypes.data, hd, eps)
+    c0, s0 = np.ascontiguousarray(cs[pos]), np.ascontiguousarray(sn[pos])
+    oracle.kro_rope(wq.ctypes.data, wk.ctypes.data, c0.ctypes.data, s0.ctypes.data, hd, nh, nkv)
+    bufs = [K.DevBuf.of(a) for a in (q, k, qw, kw, cs, sn, np.array([pos], np.int32))]
+    qb, kb, qwb, kwb, cb, sb, pb = bufs
+    K.hip.krh_heads_norm_rope(qb.ptr, kb.ptr, qwb.ptr if normed else None, kwb.ptr if normed else None, cb.ptr,
+                              sb.ptr, hd, nh, nkv, eps, pb.ptr)
+    ok()
+    assert np.array_equal(bits(qb.get(np.float32, nh * hd)), bits(wq))
+    assert np.array_equal(bits(kb.get(np.float32, nkv * hd)), bits(wk))
+    for b in bufs:
+        b.free()
+
+
+def test_store_rows_f32():
+    n, rows, pos = 640, 9, 7
+    k = np.arange(n, dtype=np.float32)
+    v = -k
+    kc, vc = K.DevBuf.of(np.zeros(rows * n, np.float32)), K.DevBuf.of(np.zeros(rows * n, np.float32))
+    kb, vb, pb = K.DevBuf.of(k), K.DevBuf.of(v), K.DevBuf.of(np.array([pos], np.int32))
+    K.hip.krh_store_rows_f32(kc.ptr, vc.ptr, kb.ptr, vb.ptr, n, pb.ptr)
+    ok()
+    want = np.zeros((rows, n), np.float32)
+    want[pos] = k
+    assert np.array_equal(kc.get(np.float32, rows * n).reshape(rows, n), want)
+    want[pos] = v
+    assert np.array_equal(vc.get(np.float32, rows * n).reshape(rows, n), want)
+    for b in (kc, vc, kb, vb, pb):
+        b.free()
+
+
+@pytest.mark.parametrize("kv", sorted(KV))
+@pytest.mark.parametrize("name", sorted(FAMILY))
+def test_family_model_matches_reference(name, kv, workdir):
+    """logits of every prompt position (ml_run --dump-logits --kv) and greedy
+    ids (ml_run -T 0 --kv) on a generated model of the family"""
+    path = os.path.join(workdir, "fam_" + name + ".mlb")
+    if not os.path.exists(path):
+        K.gen_mlb(path, **FAMILY[name])
+    m = K.Model(path)
+    s = K.State(m, KV[kv])
+    V = m.cfg.vocab
+    toks = [int(t) for t in np.random.default_rng(5).integers(1, V, 12)]
+    dump = path + "." + kv + ".logits"
+    print("family", name, kv, flush=True)
+    O.ref_ml_run(path, toks, len(toks), dump=dump, extra=("--kv", kv))
+    want = np.fromfile(dump, dtype=np.float32).reshape(len(toks), V)
+    got = np.empty((len(toks), V), dtype=np.float32)
+    s.prefill(toks, 0, logits=got)
+    assert np.array_equal(bits(got), bits(want))
+    s.close()
+    s = K.State(m, KV[kv])
+    steps = min(m.cfg.max_seq, 8 + 80)
+    want_ids, _ = O.ref_ml_run(path, toks[:8], steps, extra=("--kv", kv))
+    got_ids, _, _ = s.generate(toks[:8], steps)
+    assert np.array_equal(got_ids, want_ids)
+    s.close()
+    m.close()

@@ -400,6 +400,12 @@ SMALL = {
                                hidden_dim=512, vocab=1000, max_seq=200, std=0.1, rope_orig_max_seq=64),
     "q8_f16_untied": dict(K.CONFIGS["llama8b_q8"], dim=256, n_layers=2, n_heads=4, n_kv_heads=1, hidden_dim=384,
                           vocab=700, max_seq=160, std=0.1),
+    # the families' norms: q/k RMSNorm per head (Qwen3), post-norms (Gemma 3)
+    "qk_norm_bias_gqa": dict(K.CONFIGS["qwen05b_mixed"], dim=128, n_layers=2, n_heads=4, n_kv_heads=2,
+                             hidden_dim=256, vocab=512, max_seq=96, std=0.1, qk_norm=1),
+    "post_norms_q8": dict(K.CONFIGS["stories15m_q8"], std=0.1, seed=3, post_norms=1),
+    "qk_post_norms_f16": dict(K.CONFIGS["llama8b_q8"], dim=256, n_layers=2, n_heads=2, n_kv_heads=1,
+                              hidden_dim=384, vocab=600, max_seq=128, std=0.1, qk_norm=1, post_norms=1),
 }
 
 
