@@ -91,6 +91,12 @@ typedef struct {
     int device;            /* draw the matrices on the GPU (krh_gen_blocks) */
     int qk_norm;           /* per-head q/k RMSNorm weights (Qwen3) */
     int post_norms;        /* post-attention and post-FFN RMSNorm weights (Gemma 3) */
+    int sliding_window;    /* positions a windowed layer attends to; 0: all */
+    unsigned layer_sliding, layer_local;   /* per-layer flags (bit l: layer l, at most 32 layers): the
+                                            * window applies; RoPE of rope_local_theta. Both 0: no
+                                            * flags, the window (if any) in every layer */
+    float rope_local_theta;
+    float rope_attn_factor; /* yarn (rope_type ML_ROPE_YARN) */
 } kr_gen_spec;
 /* Writes an .mlb: matrices and embedding N(0, std^2), norms 1 + 0.01 N,
  * biases 0.02 N, quantized by the format's rules (docs/file-format.md:133-159). */

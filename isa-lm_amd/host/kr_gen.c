@@ -185,10 +185,16 @@ ml_status kr_gen_mlb(const char *path, const kr_gen_spec *sp) {
     wrf(h, 36, sp->rope_theta); wrf(h, 40, sp->norm_eps);
     wr32(h, 44, (uint32_t)sp->wtype); wr32(h, 48, sp->shared ? 1u : 0u);
     wr32(h, 52, (uint32_t)sp->rope_type);
-    if (sp->rope_type == ML_ROPE_LLAMA3) {
+    if (sp->rope_type == ML_ROPE_LLAMA3 || sp->rope_type == ML_ROPE_YARN) {
         wrf(h, 56, sp->rope_factor); wrf(h, 60, sp->rope_low_freq_factor); wrf(h, 64, sp->rope_high_freq_factor);
         wr32(h, 68, (uint32_t)sp->rope_orig_max_seq);
     }
+    if (sp->rope_type == ML_ROPE_LINEAR) wrf(h, 56, sp->rope_factor);
+    if (sp->rope_type == ML_ROPE_YARN) wrf(h, 88, sp->rope_attn_factor);
+    const int lflags = sp->layer_sliding || sp->layer_local;
+    wr32(h, 92, (uint32_t)sp->sliding_window);
+    wr32(h, 96, lflags ? 1u : 0u);
+    wrf(h, 100, sp->rope_local_theta);
     wr32(h, 72, sp->wtype == ML_Q4_0 ? sp->q8_mask : 0u);
     wr32(h, 76, sp->qkv_bias ? 1u : 0u);
     wr32(h, 84, sp->qk_norm ? 1u : 0u);
@@ -217,6 +223,14 @@ ml_status kr_gen_mlb(const char *path, const kr_gen_spec *sp) {
     if (!f) { krh_free(dev); return kr_seterr(ML_E_IO, "cannot write %s", path); }
     writer w = { f, 0, 1, dev };
     put(&w, h, sizeof h);
+    if (lflags) {   /* one byte a layer after the header (model/mlb.c's order) */
+        uint8_t fl[64] = { 0 };
+        for (int l = 0; l < c.n_layers && l < 32; l++)
+            fl[l] = (uint8_t)(((sp->layer_sliding >> l) & 1u) * ML_LAYER_SLIDING |
+                              ((sp->layer_local >> l) & 1u) * ML_LAYER_LOCAL_ROPE);
+        if (c.n_layers > 32) w.ok = 0;
+        put(&w, fl, (size_t)c.n_layers);
+    }
     const int f16 = sp->scale_f16, th = sp->device ? -1 : sp->threads;
     const float sd = sp->std > 0.0f ? sp->std : 0.02f;
     uint64_t s = 0;

@@ -21,6 +21,21 @@ FAMILY = {
     "qk_post_norms_f16": dict(K.CONFIGS["llama8b_q8"], dim=256, n_layers=2, n_heads=2, n_kv_heads=1,
                               hidden_dim=384, vocab=600, max_seq=128, std=0.1, qk_norm=1, post_norms=1),
 }
+# attention windows and RoPE variants (ops/ops.c:127-128, model/transformer.c:16-38, :182-186)
+VARIANTS = {
+    "window_all_layers": dict(K.CONFIGS["stories15m_q8"], std=0.1, seed=21, sliding_window=5),
+    "window_local_rope_layers": dict(K.CONFIGS["qwen05b_mixed"], dim=128, n_layers=3, n_heads=4, n_kv_heads=2,
+                                     hidden_dim=256, vocab=512, max_seq=96, std=0.1, rope_theta=1e6,
+                                     sliding_window=4, layer_sliding=0b101, layer_local=0b001,
+                                     rope_local_theta=1e4),
+    "rope_linear": dict(K.CONFIGS["stories15m_q8"], std=0.1, seed=22, rope_type=K.ML_ROPE_LINEAR, rope_factor=4.0),
+    "rope_yarn": dict(K.CONFIGS["stories15m_q8"], std=0.1, seed=23, rope_type=K.ML_ROPE_YARN, rope_factor=4.0,
+                      rope_low_freq_factor=32.0, rope_high_freq_factor=1.0, rope_orig_max_seq=64,
+                      rope_attn_factor=1.2),
+    "window_qk_norm": dict(K.CONFIGS["qwen05b_mixed"], dim=128, n_layers=2, n_heads=4, n_kv_heads=2,
+                           hidden_dim=256, vocab=512, max_seq=96, std=0.1, qk_norm=1, sliding_window=6,
+                           layer_sliding=0b10, layer_local=0b10, rope_local_theta=1e4),
+}
 KV = {"f32": K.ML_F32, "f16": K.ML_F16, "q8": K.ML_Q8_0}
 
 
@@ -93,13 +108,13 @@ def test_store_rows_f32():
 
 
 @pytest.mark.parametrize("kv", sorted(KV))
-@pytest.mark.parametrize("name", sorted(FAMILY))
+@pytest.mark.parametrize("name", sorted(FAMILY) + sorted(VARIANTS))
 def test_family_model_matches_reference(name, kv, workdir):
     """logits of every prompt position (ml_run --dump-logits --kv) and greedy
     ids (ml_run -T 0 --kv) on a generated model of the family"""
     path = os.path.join(workdir, "fam_" + name + ".mlb")
     if not os.path.exists(path):
-        K.gen_mlb(path, **FAMILY[name])
+        K.gen_mlb(path, **(FAMILY.get(name) or VARIANTS[name]))
     m = K.Model(path)
     s = K.State(m, KV[kv])
     V = m.cfg.vocab

@@ -406,6 +406,16 @@ SMALL = {
     "post_norms_q8": dict(K.CONFIGS["stories15m_q8"], std=0.1, seed=3, post_norms=1),
     "qk_post_norms_f16": dict(K.CONFIGS["llama8b_q8"], dim=256, n_layers=2, n_heads=2, n_kv_heads=1,
                               hidden_dim=384, vocab=600, max_seq=128, std=0.1, qk_norm=1, post_norms=1),
+    # attention windows and RoPE variants (ops/ops.c:127-128, model/transformer.c:16-38, :182-186)
+    "window_all_layers": dict(K.CONFIGS["stories15m_q8"], std=0.1, seed=21, sliding_window=5),
+    "window_local_rope_layers": dict(K.CONFIGS["qwen05b_mixed"], dim=128, n_layers=3, n_heads=4, n_kv_heads=2,
+                                     hidden_dim=256, vocab=512, max_seq=96, std=0.1, rope_theta=1e6,
+                                     sliding_window=4, layer_sliding=0b101, layer_local=0b001,
+                                     rope_local_theta=1e4),
+    "rope_linear": dict(K.CONFIGS["stories15m_q8"], std=0.1, seed=22, rope_type=K.ML_ROPE_LINEAR, rope_factor=4.0),
+    "rope_yarn": dict(K.CONFIGS["stories15m_q8"], std=0.1, seed=23, rope_type=K.ML_ROPE_YARN, rope_factor=4.0,
+                      rope_low_freq_factor=32.0, rope_high_freq_factor=1.0, rope_orig_max_seq=64,
+                      rope_attn_factor=1.2),
 }
 
 
