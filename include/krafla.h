@@ -97,6 +97,9 @@ typedef struct {
                                             * flags, the window (if any) in every layer */
     float rope_local_theta;
     float rope_attn_factor; /* yarn (rope_type ML_ROPE_YARN) */
+    int act;               /* ML_ACT_SILU or ML_ACT_GELU_TANH */
+    float embed_scale;     /* 0: 1 */
+    float attn_softcap, final_softcap;   /* 0: off */
 } kr_gen_spec;
 /* Writes an .mlb: matrices and embedding N(0, std^2), norms 1 + 0.01 N,
  * biases 0.02 N, quantized by the format's rules (docs/file-format.md:133-159). */

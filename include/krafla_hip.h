@@ -212,6 +212,15 @@ void krh_heads_norm_rope(float *q, float *k, const float *q_norm, const float *k
 /* F32 cache rows: kc[*pos][i] = k[i], vc[*pos][i] = v[i] for i < kv_dim
  * (the reference's projections write them in place, model/transformer.c:263-264) */
 void krh_store_rows_f32(float *kc, float *vc, const float *k, const float *v, int kv_dim, const int *pos);
+/* ops/ops.c:141: score rows (token t, head h) of att ([ntok][n_heads][max_seq])
+ * become cap * tanhf(score / cap) over the positions attended from *pos + t */
+void krh_softcap_att(float *att, int n_heads, int max_seq, int window, const int *pos, int ntok, float cap);
+/* krh_attention_kv with soft-capped scores (cap > 0, ops/ops.c:141): Gemma 2 */
+void krh_attention_kv_softcap(float *ao, float *att, const float *q, const ml_kv_layer *kv, int n_heads,
+                              int n_kv_heads, int head_dim, int max_seq, float scale, const int *pos0, int ntok,
+                              int last_pos, float cap);
+/* y[i] = tanhf of the float with bits lo + i (the device's C-library tanhf; for checks) */
+void krh_tanhf_range(float *y, uint32_t lo, size_t n);
 
 /* ---- the device sampler (model/sampler.h:9-35, model/sampler.c) ----
  * The reference's ml_sample on device logits, with its results: the same id,

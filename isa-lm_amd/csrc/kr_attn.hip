@@ -697,7 +697,8 @@ static void launch_mix(const dim3 &grid, int ntok, float *ao, const float *att, 
 // of type KT; max_pos (the last position) sizes the launch
 template <int KT>
 static void attention(float *ao, float *att, const float *q, const KvView &kv, int n_heads, int n_kv_heads,
-                      int head_dim, int max_seq, int window, float scale, const int *pos, int ntok, int max_pos) {
+                      int head_dim, int max_seq, int window, float scale, const int *pos, int ntok, int max_pos,
+                      float cap = 0.0f) {
     if (n_kv_heads <= 0 || n_heads % n_kv_heads || head_dim % 4 || (n_heads * head_dim) % KR_QK ||
         n_heads / n_kv_heads > 16 || head_dim > 1024 || max_seq < 4) {
         kr_fail(ML_E_SHAPE, "attention shape", hipSuccess);
@@ -720,6 +721,7 @@ static void attention(float *ao, float *att, const float *q, const KvView &kv, i
     else
         hipLaunchKernelGGL((k_attn_scores_kv<KT>), sgrid, dim3(AT_THREADS), lds, kr_stream(), att, q, kv, group,
                            head_dim, kv_dim, max_seq, window, scale, pos);
+    if (cap > 0.0f) krh_softcap_att(att, n_heads, max_seq, window, pos, ntok, cap);   // ops/ops.c:141
     hipLaunchKernelGGL(k_attn_softmax, dim3(n_heads, 1, ntok), dim3(AT_THREADS), 0, kr_stream(), att, max_seq, window,
                        pos);
     const int gp = group <= 1 ? 1 : group <= 2 ? 2 : group <= 4 ? 4 : group <= 8 ? 8 : 16;
@@ -762,21 +764,27 @@ extern "C" void krh_attention_batch(float *ao, float *att, const float *q, const
 extern "C" void krh_attention_kv(float *ao, float *att, const float *q, const ml_kv_layer *kv, int n_heads,
                                  int n_kv_heads, int head_dim, int max_seq, float scale, const int *pos0, int ntok,
                                  int last_pos) {
+    krh_attention_kv_softcap(ao, att, q, kv, n_heads, n_kv_heads, head_dim, max_seq, scale, pos0, ntok, last_pos, 0.0f);
+}
+
+extern "C" void krh_attention_kv_softcap(float *ao, float *att, const float *q, const ml_kv_layer *kv, int n_heads,
+                                         int n_kv_heads, int head_dim, int max_seq, float scale, const int *pos0,
+                                         int ntok, int last_pos, float cap) {
     if (ntok <= 0 || last_pos >= max_seq || !kv) {
         kr_fail(ML_E_SHAPE, "attention shape", hipSuccess);
         return;
     }
     if (kv->k && kv->v) {
         attention<KV_F32>(ao, att, q, f32_view(kv->k, kv->v), n_heads, n_kv_heads, head_dim, max_seq, kv->window,
-                          scale, pos0, ntok, last_pos);
+                          scale, pos0, ntok, last_pos, cap);
     } else if (kv->kh && kv->vh) {
         KvView v = { kv->kh, kv->vh, nullptr, nullptr, n_kv_heads };
         attention<KV_F16>(ao, att, q, v, n_heads, n_kv_heads, head_dim, max_seq, kv->window, scale, pos0, ntok,
-                          last_pos);
+                          last_pos, cap);
     } else if (kv->kq && kv->vq && kv->kd && kv->vd) {
         KvView v = { kv->kq, kv->vq, kv->kd, kv->vd, n_kv_heads };
         attention<KV_Q8>(ao, att, q, v, n_heads, n_kv_heads, head_dim, max_seq, kv->window, scale, pos0, ntok,
-                         last_pos);
+                         last_pos, cap);
     } else {
         kr_fail(ML_E_SHAPE, "attention: the cache view has no F32, F16 or Q8 rows", hipSuccess);
     }

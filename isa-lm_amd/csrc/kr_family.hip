@@ -45,6 +45,22 @@ __global__ void __launch_bounds__(64) k_heads_norm_rope(float *q, float *k, cons
     }
 }
 
+// ops/ops.c:141: the scores of the positions attended become
+// cap * tanhf(score / cap) before the softmax. Row (token z, head x) holds
+// max_seq floats; its length follows from the position and the window as
+// the score kernels count it.
+__global__ void k_softcap_att(float *att, int max_seq, int window, const int *pos_p, float cap) {
+    const int pos = *pos_p + (int)blockIdx.z;
+    const int first = window && pos >= window ? pos + 1 - window : 0, n = pos + 1 - first;
+    float *a = att + ((size_t)blockIdx.z * gridDim.x + blockIdx.x) * max_seq;
+    for (int t = (int)threadIdx.x; t < n; t += (int)blockDim.x) a[t] = kr_fmul(cap, kr_tanhf(kr_fdiv(a[t], cap)));
+}
+
+__global__ void k_tanhf_range(float *y, unsigned lo, size_t n) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) y[i] = kr_tanhf(__uint_as_float(lo + (unsigned)i));
+}
+
 __global__ void k_store_rows_f32(float *kc, float *vc, const float *k, const float *v, int n, const int *pos) {
     const int i = (int)(blockIdx.x * blockDim.x + threadIdx.x);
     if (i < n) {
@@ -78,4 +94,21 @@ extern "C" void krh_store_rows_f32(float *kc, float *vc, const float *k, const f
     hipLaunchKernelGGL(k_store_rows_f32, dim3((kv_dim + 255) / 256), dim3(256), 0, kr_stream(), kc, vc, k, v, kv_dim,
                        pos);
     kr_check_launch("store_rows_f32");
+}
+
+extern "C" void krh_softcap_att(float *att, int n_heads, int max_seq, int window, const int *pos, int ntok,
+                                float cap) {
+    if (n_heads <= 0 || ntok <= 0 || !(cap > 0.0f)) {
+        kr_fail(ML_E_SHAPE, "softcap_att shape", hipSuccess);
+        return;
+    }
+    hipLaunchKernelGGL(k_softcap_att, dim3(n_heads, 1, ntok), dim3(256), 0, kr_stream(), att, max_seq, window, pos,
+                       cap);
+    kr_check_launch("softcap_att");
+}
+
+extern "C" void krh_tanhf_range(float *y, uint32_t lo, size_t n) {
+    if (n == 0) return;
+    hipLaunchKernelGGL(k_tanhf_range, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, kr_stream(), y, lo, n);
+    kr_check_launch("tanhf_range");
 }

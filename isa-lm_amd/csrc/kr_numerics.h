@@ -71,6 +71,98 @@ __device__ __forceinline__ float kr_expf_tab(float x, const uint64_t *tab) {
 
 __device__ __forceinline__ float kr_expf(float x) { return kr_expf_tab(x, kr_exp2_tab); }
 
+// The C library's expm1f and tanhf, bit for bit: the reference's GELU and
+// soft-capping call glibc's tanhf (kernels/scalar/k_scalar.c:100-105,
+// ops/ops.c:98-101), which glibc 2.35 builds from the fdlibm algorithm:
+// tanh(x) = 1 - 2/(expm1(2|x|) + 2) from |x| = 1, -t/(t + 2) with
+// t = expm1(-2|x|) below; expm1 reduces x = k ln2 + r with the reduction's
+// rounding error carried, fits r by a rational form in r^2/2 and scales by
+// 2^k through the exponent bits. Checked on every float32 input against the
+// host library.
+__device__ __forceinline__ float kr_expm1f(float x) {
+    const float ln2_hi = 6.9313812256e-01f, ln2_lo = 9.0580006145e-06f, invln2 = 1.4426950216e+00f;
+    const float Q1 = -3.3333335072e-02f, Q2 = 1.5873016091e-03f, Q3 = -7.9365076090e-05f, Q4 = 4.0082177293e-06f,
+                Q5 = -2.0109921195e-07f;
+    unsigned hx = __float_as_uint(x);
+    const unsigned neg = hx >> 31;
+    hx &= 0x7fffffffu;
+    if (hx >= 0x4195b844u) {
+        if (hx >= 0x42b17218u) {
+            if (hx > 0x7f800000u) return kr_fadd(x, x);
+            if (hx == 0x7f800000u) return neg ? -1.0f : x;
+            if (x > 8.8721679688e+01f) return __uint_as_float(0x7f800000u);
+        }
+        if (neg) return -1.0f;
+    }
+    float hi, lo, c = 0.0f;
+    int k;
+    if (hx > 0x3eb17218u) {
+        if (hx < 0x3F851592u) {
+            k = neg ? -1 : 1;
+            hi = neg ? kr_fadd(x, ln2_hi) : kr_fsub(x, ln2_hi);
+            lo = neg ? -ln2_lo : ln2_lo;
+        } else {
+            k = (int)kr_fadd(kr_fmul(invln2, x), neg ? -0.5f : 0.5f);
+            const float t = (float)k;
+            hi = kr_fsub(x, kr_fmul(t, ln2_hi));
+            lo = kr_fmul(t, ln2_lo);
+        }
+        x = kr_fsub(hi, lo);
+        c = kr_fsub(kr_fsub(hi, x), lo);
+    } else if (hx < 0x33000000u) {
+        return x;
+    } else {
+        k = 0;
+    }
+    const float hfx = kr_fmul(0.5f, x), hxs = kr_fmul(x, hfx);
+    float r1 = kr_fmul(hxs, Q5);
+    r1 = kr_fmul(hxs, kr_fadd(Q4, r1));
+    r1 = kr_fmul(hxs, kr_fadd(Q3, r1));
+    r1 = kr_fmul(hxs, kr_fadd(Q2, r1));
+    r1 = kr_fadd(1.0f, kr_fmul(hxs, kr_fadd(Q1, r1)));
+    const float t = kr_fsub(3.0f, kr_fmul(r1, hfx));
+    float e = kr_fmul(hxs, kr_fdiv(kr_fsub(r1, t), kr_fsub(6.0f, kr_fmul(x, t))));
+    if (k == 0) return kr_fsub(x, kr_fsub(kr_fmul(x, e), hxs));
+    e = kr_fsub(kr_fmul(x, kr_fsub(e, c)), c);
+    e = kr_fsub(e, hxs);
+    if (k == -1) return kr_fsub(kr_fmul(0.5f, kr_fsub(x, e)), 0.5f);
+    if (k == 1)
+        return x < -0.25f ? kr_fmul(-2.0f, kr_fsub(e, kr_fadd(x, 0.5f))) : kr_fadd(1.0f, kr_fmul(2.0f, kr_fsub(x, e)));
+    float y;
+    if (k <= -2 || k > 56) {
+        y = kr_fsub(1.0f, kr_fsub(e, x));
+        y = k == 128 ? kr_fmul(kr_fmul(y, 2.0f), 0x1p127f) : __uint_as_float(__float_as_uint(y) + ((unsigned)k << 23));
+        return kr_fsub(y, 1.0f);
+    }
+    if (k < 23) {
+        y = kr_fsub(__uint_as_float(0x3f800000u - (0x1000000u >> k)), kr_fsub(e, x));
+    } else {
+        y = kr_fsub(x, kr_fadd(e, __uint_as_float((unsigned)(0x7f - k) << 23)));
+        y = kr_fadd(y, 1.0f);
+    }
+    return __uint_as_float(__float_as_uint(y) + ((unsigned)k << 23));
+}
+__device__ __forceinline__ float kr_tanhf(float x) {
+    const unsigned jx = __float_as_uint(x), ix = jx & 0x7fffffffu;
+    if (ix >= 0x7f800000u) return (jx >> 31) ? kr_fsub(kr_fdiv(1.0f, x), 1.0f) : kr_fadd(kr_fdiv(1.0f, x), 1.0f);
+    float z;
+    if (ix < 0x41b00000u) {
+        if (ix == 0) return x;
+        if (ix < 0x24000000u) return kr_fmul(x, kr_fadd(1.0f, x));
+        const float ax = __uint_as_float(ix);
+        if (ix >= 0x3f800000u) {
+            const float t = kr_expm1f(kr_fmul(2.0f, ax));
+            z = kr_fsub(1.0f, kr_fdiv(2.0f, kr_fadd(t, 2.0f)));
+        } else {
+            const float t = kr_expm1f(kr_fmul(-2.0f, ax));
+            z = kr_fdiv(-t, kr_fadd(t, 2.0f));
+        }
+    } else {
+        z = 1.0f;
+    }
+    return (jx >> 31) ? -z : z;
+}
+
 // IEEE binary16 -> float32; exact for every input (subnormals included).
 __device__ __forceinline__ float kr_h2f(uint16_t h) { return __half2float(__ushort_as_half(h)); }
 

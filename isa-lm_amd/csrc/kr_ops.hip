@@ -51,14 +51,13 @@ __global__ void k_silu_mul(float *g, const float *u, int n) {   // k_scalar.c:96
     if (i < n) g[i] = kr_fmul(kr_fdiv(g[i], kr_fadd(1.0f, kr_expf(-g[i]))), u[i]);
 }
 
-// k_scalar.c:100-105 with the device library's tanhf (its bits are not the C
-// library's: parity of this op is not pinned)
+// k_scalar.c:100-105, with the C library's tanhf (kr_tanhf)
 __global__ void k_gelu_mul(float *g, const float *u, int n) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= n) return;
     const float x = g[i];
     const float c = kr_fmul(kr_fmul(kr_fmul(0.044715f, x), x), x);
-    const float t = tanhf(kr_fmul(0.7978845608f, kr_fadd(x, c)));
+    const float t = kr_tanhf(kr_fmul(0.7978845608f, kr_fadd(x, c)));
     g[i] = kr_fmul(kr_fmul(kr_fmul(0.5f, x), kr_fadd(1.0f, t)), u[i]);
 }
 
@@ -130,12 +129,12 @@ __global__ void __launch_bounds__(OP_T) k_quantize_row(int8_t *q, float *d, cons
     for (int i = tid; i < n; i += OP_T) q[i] = (int8_t)kr_q8_elem(x[i], id);
 }
 
-// x = cap * tanhf(x / cap) (ops/ops.c:98-101; tanhf: parity not pinned)
+// x = cap * tanhf(x / cap) (ops/ops.c:98-101; the C library's tanhf)
 __global__ void k_softcap(float *x, size_t ld, int rows, int n, float cap) {
     const size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (e >= (size_t)rows * n) return;
     float *p = x + (e / n) * ld + e % n;
-    *p = kr_fmul(cap, tanhf(kr_fdiv(*p, cap)));
+    *p = kr_fmul(cap, kr_tanhf(kr_fdiv(*p, cap)));
 }
 
 __global__ void k_set_int(int *dst, int v) { *dst = v; }

@@ -199,6 +199,10 @@ ml_status kr_gen_mlb(const char *path, const kr_gen_spec *sp) {
     wr32(h, 76, sp->qkv_bias ? 1u : 0u);
     wr32(h, 84, sp->qk_norm ? 1u : 0u);
     wr32(h, 108, sp->post_norms ? 1u : 0u);
+    wr32(h, 104, (uint32_t)sp->act);
+    wrf(h, 112, sp->embed_scale);
+    wrf(h, 124, sp->attn_softcap);
+    wrf(h, 128, sp->final_softcap);
     wr32(h, 120, sp->scale_f16 ? 1u : 0u);
     ml_config c;
     int shared;

@@ -183,7 +183,8 @@ struct kr_state {
     float *kd, *vd;           /* Q8: row scales [n_layers][max_seq][n_kv_heads] */
     float *kst, *vst;         /* Q8 and the families' path: the projections' K and V rows (kbuf, vbuf) */
     float *yb;                /* post-norms: a block's output before its norm (xb2) */
-    int family;               /* q/k-norm or post-norms: the unfused layer path */
+    float *hb2;               /* GELU: the up projection (hb2) */
+    int family;               /* q/k-norm, post-norms, GELU or soft-capping: the unfused layer path */
     int8_t *qa_dim, *qa_q, *qa_hid;
     float *qd_dim, *qd_q, *qd_hid;
     int *tok, *pos, *prompt, *log;
@@ -330,9 +331,12 @@ static void issue_step(kr_state *s, int cls) {
     }
     if (!cls) return;
     krh_rmsnorm_matvec(s->logits, &m->d_wcls, s->x, m->d_final_norm, c->norm_eps, 0);
+    if (c->final_softcap > 0.0f)   /* model/transformer.c:304 */
+        krh_softcap_rows(s->logits, (size_t)c->vocab, 1, c->vocab, c->final_softcap);
 }
 
-/* A layer of a model with q/k-norm (Qwen3) or post-norms (Gemma 3), in
+/* A layer of a model with q/k-norm (Qwen3), post-norms (Gemma 3), GELU or
+ * soft-capped scores (Gemma 2), in
  * ml_forward's order with unfused launches (model/transformer.c:266-297): the
  * projections store q and the staging rows k, v unrotated; the biases; each
  * head normalized, then rotated at *pos; the cache row stored; attention;
@@ -357,8 +361,8 @@ static void issue_family_layer(kr_state *s, int l, const float *cs, const float 
         krh_store_rows_f32((float *)kv.k, (float *)kv.v, s->kst, s->vst, c->kv_dim, s->pos);
     else
         store_kv(s, l, s->kst, s->vst, 1);
-    krh_attention_kv(s->ao, s->att, s->q, &kv, c->n_heads, c->n_kv_heads, c->head_dim, c->max_seq, c->attn_scale,
-                     s->pos, 1, c->max_seq - 1);
+    krh_attention_kv_softcap(s->ao, s->att, s->q, &kv, c->n_heads, c->n_kv_heads, c->head_dim, c->max_seq,
+                             c->attn_scale, s->pos, 1, c->max_seq - 1, c->attn_softcap);
     if (D->post_attn_norm) {
         krh_matvec_f(s->yb, &D->wo, s->ao, 0);
         krh_rmsnorm(s->yb, s->yb, D->post_attn_norm, c->dim, c->norm_eps);
@@ -366,7 +370,14 @@ static void issue_family_layer(kr_state *s, int l, const float *cs, const float 
     } else {
         krh_matvec_f(s->x, &D->wo, s->ao, 1);
     }
-    krh_rmsnorm_matvec_swiglu(s->hb, &D->w1, &D->w3, s->x, D->ffn_norm, c->norm_eps);
+    if (c->act == ML_ACT_GELU_TANH) {   /* act_mul (model/transformer.c:233-236) */
+        krh_rmsnorm_q8(s->qa_dim, s->qd_dim, NULL, s->x, D->ffn_norm, c->dim, c->norm_eps, 1);
+        krh_matvec(s->hb, &D->w1, s->qa_dim, s->qd_dim, 0);
+        krh_matvec(s->hb2, &D->w3, s->qa_dim, s->qd_dim, 0);
+        krh_gelu_mul(s->hb, s->hb2, c->hidden_dim);
+    } else {
+        krh_rmsnorm_matvec_swiglu(s->hb, &D->w1, &D->w3, s->x, D->ffn_norm, c->norm_eps);
+    }
     krh_quantize_q8(s->qa_hid, s->qd_hid, s->hb, c->hidden_dim, 1);
     if (D->post_ffn_norm) {
         krh_matvec(s->yb, &D->w2, s->qa_hid, s->qd_hid, 0);
@@ -419,8 +430,6 @@ ml_status kr_state_new(kr_state **out, kr_model *m, int kv_type) {
     const ml_config *c = &m->cfg;
     if (kv_type != ML_F32 && kv_type != ML_F16 && kv_type != ML_Q8_0)
         return kr_seterr(ML_E_SHAPE, "KV cache type %d: F32, F16 or Q8_0", kv_type);
-    if (c->act != ML_ACT_SILU || c->attn_softcap > 0.0f || c->final_softcap > 0.0f)
-        return kr_seterr(ML_E_SHAPE, "model uses GELU or soft-capping: not supported");
     ml_status st = kr_model_upload(m);
     if (st != ML_OK) return st;
     kr_state *s = calloc(1, sizeof *s);
@@ -429,7 +438,9 @@ ml_status kr_state_new(kr_state **out, kr_model *m, int kv_type) {
     s->kv_type = kv_type;
     const size_t f = sizeof(float), kv = (size_t)c->n_layers * c->max_seq * c->kv_dim;
     const size_t ks = (size_t)c->n_layers * c->max_seq * c->n_kv_heads;
-    const int q8 = kv_type == ML_Q8_0, fam = c->qk_norm || c->post_norms;
+    const int gelu = c->act == ML_ACT_GELU_TANH;
+    const int q8 = kv_type == ML_Q8_0,
+              fam = c->qk_norm || c->post_norms || gelu || c->attn_softcap > 0.0f || c->final_softcap > 0.0f;
     s->family = fam;
     const size_t half = (size_t)c->max_seq * (c->head_dim / 2);
     const int local = c->rope_local_theta > 0.0f;
@@ -440,7 +451,7 @@ ml_status kr_state_new(kr_state **out, kr_model *m, int kv_type) {
         { (void **)&s->kcache, kv_elem(kv_type) * kv }, { (void **)&s->vcache, kv_elem(kv_type) * kv },
         { (void **)&s->kd, q8 ? f * ks : 0 }, { (void **)&s->vd, q8 ? f * ks : 0 },
         { (void **)&s->kst, q8 || fam ? f * c->kv_dim : 0 }, { (void **)&s->vst, q8 || fam ? f * c->kv_dim : 0 },
-        { (void **)&s->yb, c->post_norms ? f * c->dim : 0 },
+        { (void **)&s->yb, c->post_norms ? f * c->dim : 0 }, { (void **)&s->hb2, gelu ? f * c->hidden_dim : 0 },
         { (void **)&s->rope_cos, f * half }, { (void **)&s->rope_sin, f * half },
         { (void **)&s->rope_cos_l, local ? f * half : 0 }, { (void **)&s->rope_sin_l, local ? f * half : 0 },
         { (void **)&s->qa_dim, (size_t)c->dim }, { (void **)&s->qd_dim, f * c->dim / QK },

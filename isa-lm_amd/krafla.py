@@ -14,6 +14,7 @@ LIB_HOST = os.path.join(HERE, "libkrafla.so")
 ML_OK, ML_E_IO, ML_E_FORMAT, ML_E_SHAPE, ML_E_NOMEM, ML_E_ISA = range(6)
 ML_F32, ML_Q8_0, ML_Q4_0, ML_F16 = 0, 1, 2, 3
 ML_ROPE_NONE, ML_ROPE_LLAMA3, ML_ROPE_LINEAR, ML_ROPE_YARN = 0, 1, 2, 3
+ML_ACT_SILU, ML_ACT_GELU_TANH = 0, 1
 MATH_EXPF, MATH_SQRT, MATH_DIV, MATH_RMS_INV = range(4)
 Q8M_EMB, Q8M_CLS, Q8M_QK, Q8M_V, Q8M_O, Q8M_UP, Q8M_DOWN = 1, 2, 4, 8, 16, 32, 64
 
@@ -60,7 +61,8 @@ class GenSpec(C.Structure):
         ("rope_factor", C.c_float), ("rope_low_freq_factor", C.c_float), ("rope_high_freq_factor", C.c_float),
         ("rope_orig_max_seq", C.c_int), ("std", C.c_float), ("seed", C.c_uint64), ("threads", C.c_int), ("device", C.c_int),
         ("qk_norm", C.c_int), ("post_norms", C.c_int), ("sliding_window", C.c_int), ("layer_sliding", C.c_uint),
-        ("layer_local", C.c_uint), ("rope_local_theta", C.c_float), ("rope_attn_factor", C.c_float)]
+        ("layer_local", C.c_uint), ("rope_local_theta", C.c_float), ("rope_attn_factor", C.c_float),
+        ("act", C.c_int), ("embed_scale", C.c_float), ("attn_softcap", C.c_float), ("final_softcap", C.c_float)]
 
 
 # The workloads, by name. Shapes and quantization as the benchmark configs
@@ -72,7 +74,8 @@ def _spec(**kw):
     base = dict(rope_theta=1e4, norm_eps=1e-5, wtype=ML_Q8_0, q8_mask=0, shared=0, qkv_bias=0, scale_f16=0,
                 rope_type=ML_ROPE_NONE, rope_factor=0.0, rope_low_freq_factor=0.0, rope_high_freq_factor=0.0,
                 rope_orig_max_seq=0, std=0.02, seed=1, threads=8, device=0, qk_norm=0, post_norms=0,
-                sliding_window=0, layer_sliding=0, layer_local=0, rope_local_theta=0.0, rope_attn_factor=0.0)
+                sliding_window=0, layer_sliding=0, layer_local=0, rope_local_theta=0.0, rope_attn_factor=0.0,
+                act=0, embed_scale=0.0, attn_softcap=0.0, final_softcap=0.0)
     base.update(kw)
     return base
 
@@ -166,6 +169,10 @@ for name, res, args in [
     ("krh_sampler_rng", C.c_uint64, [_P]),
     ("krh_heads_norm_rope", None, [_P, _P, _P, _P, _P, _P, C.c_int, C.c_int, C.c_int, C.c_float, _P]),
     ("krh_store_rows_f32", None, [_P, _P, _P, _P, C.c_int, _P]),
+    ("krh_softcap_att", None, [_P, C.c_int, C.c_int, C.c_int, _P, C.c_int, C.c_float]),
+    ("krh_attention_kv_softcap", None, [_P, _P, _P, C.POINTER(MlKvLayer), C.c_int, C.c_int, C.c_int, C.c_int, C.c_float, _P, C.c_int,
+                                        C.c_int, C.c_float]),
+    ("krh_tanhf_range", None, [_P, C.c_uint32, C.c_size_t]),
     ("krh_rmsnorm_q8_t", None, [_P, _P, C.c_int, _P, _P, _P, C.c_int, C.c_float, C.c_int]),
     ("krh_quantize_q8_t", None, [_P, _P, C.c_int, _P, C.c_int, C.c_int]),
     ("krh_matmul", None, [_P, C.c_int, C.POINTER(KrhMat), _P, _P, C.c_int, C.c_int, C.c_int]),

@@ -184,6 +184,20 @@ void kro_softmax(float *x, int n) {
     for (int i = 0; i < n; i++) x[i] *= inv;
 }
 
+/* k_scalar.c:100-105, in the C expression's order */
+void kro_gelu_mul(float *g, const float *u, int n) {
+    for (int i = 0; i < n; i++) {
+        const float x = g[i];
+        g[i] = 0.5f * x * (1.0f + kro_tanhf(0.7978845608f * (x + 0.044715f * x * x * x))) * u[i];
+    }
+}
+
+/* ops/ops.c:98-101 */
+void kro_softcap_rows(float *x, size_t ld, int rows, int n, float cap) {
+    for (int r = 0; r < rows; r++)
+        for (int i = 0; i < n; i++) x[(size_t)r * ld + i] = cap * kro_tanhf(x[(size_t)r * ld + i] / cap);
+}
+
 /* k_scalar.c:79-94: interleaved pairs (2i, 2i+1) of every head */
 static void rope_heads(float *v, const float *c, const float *s, int hd, int nh) {
     for (int h = 0; h < nh; h++) {
@@ -351,6 +365,7 @@ void kro_attention(float *out, const float *q, const ml_kv_layer *kv, float *att
         if (kv->k) kro_dot_f32(att, q + (size_t)h * hd, kv->k + off, ld, n, hd, cfg->attn_scale);
         else if (kv->kh) kro_dot_f16(att, q + (size_t)h * hd, kv->kh + off, ld, n, hd, cfg->attn_scale);
         else kro_dot_q8(att, qq + (size_t)h * hd, qd[h], kv->kq + off, kv->kd + offd, ld, ldd, n, hd, cfg->attn_scale);
+        if (cfg->attn_softcap > 0.0f) kro_softcap_rows(att, (size_t)n, 1, n, cfg->attn_softcap);   /* ops/ops.c:141 */
         kro_softmax(att, n);
         float *o = out + (size_t)h * hd;
         for (int i = 0; i < hd; i++) o[i] = 0.0f;
@@ -419,7 +434,6 @@ int kro_state_new(kro_state **out, const kro_model *m) { return kro_state_new_kv
 /* model/transformer.c:51-166 with kv_type ML_F32, ML_F16 or ML_Q8_0 */
 int kro_state_new_kv(kro_state **out, const kro_model *m, int kv_type) {
     const ml_config *c = kro_mlb_config(m);
-    if (c->act != ML_ACT_SILU || c->attn_softcap > 0.0f || c->final_softcap > 0.0f) return ML_E_SHAPE;
     if (kv_type != ML_F32 && kv_type != ML_F16 && kv_type != ML_Q8_0) return ML_E_SHAPE;
     kro_state *s = calloc(1, sizeof *s);
     if (!s) return ML_E_NOMEM;
@@ -568,7 +582,8 @@ static void forward(kro_state *s, int token, int pos, int cls) {
         kro_quantize_q8(&s->qa_dim, s->xb, c->dim);
         matvec(s->hb, &L->w1, &s->qa_dim);
         matvec(s->hb2, &L->w3, &s->qa_dim);
-        kro_silu_mul(s->hb, s->hb2, c->hidden_dim);
+        if (c->act == ML_ACT_GELU_TANH) kro_gelu_mul(s->hb, s->hb2, c->hidden_dim);   /* act_mul */
+        else kro_silu_mul(s->hb, s->hb2, c->hidden_dim);
         kro_quantize_q8(&s->qa_hidden, s->hb, c->hidden_dim);
         matvec(s->xb2, &L->w2, &s->qa_hidden);
         residual_add(c, s->x, s->xb2, L->post_ffn_norm);
@@ -577,6 +592,7 @@ static void forward(kro_state *s, int token, int pos, int cls) {
     kro_rmsnorm(s->xb, s->x, kro_mlb_final_norm(m), c->dim, c->norm_eps);
     kro_quantize_q8(&s->qa_dim, s->xb, c->dim);
     matvec(s->logits, kro_mlb_wcls(m), &s->qa_dim);
+    if (c->final_softcap > 0.0f) kro_softcap_rows(s->logits, (size_t)c->vocab, 1, c->vocab, c->final_softcap);
 }
 
 int kro_forward(kro_state *s, int token, int pos, float *out) {

@@ -17,6 +17,9 @@
  *   kro_forward/prefill  logits bit-equal to oracle/_ref/scalar/ml_run
  *                        --dump-logits on generated .mlb models, with the
  *                        F32, F16 and Q8 KV caches (--kv f32|f16|q8)
+ *   kro_tanhf            exhaustively equal to the host libm (all 2^32 inputs;
+ *                        expm1f too); gelu_mul and softcap bit-equal to the
+ *                        reference's scalar kernels
  *   kro_f32_to_f16       exhaustively equal to the x86 F16C conversion (all
  *                        2^32 inputs; NaN -> sign | 0x7e00) and to the
  *                        reference's ml_f32_to_f16
@@ -36,6 +39,17 @@ extern "C" {
 #endif
 
 float kro_expf(float x);
+/* the C library's tanhf and expm1f (fdlibm's algorithm, glibc 2.35), and
+ * the count of inputs in [lo, hi) where either differs from the host libm */
+float kro_tanhf(float x);
+float kro_expm1f(float x);
+uint64_t kro_tanhf_mismatches(uint64_t lo, uint64_t hi, int threads);
+/* mismatches of got[i] against the host libm's tanhf of the float with bits lo + i */
+uint64_t kro_tanhf_check_range(uint64_t lo, const float *got, size_t n, int threads);
+/* k_scalar.c:100-105: g = 0.5 x (1 + tanhf(0.7978845608 (x + 0.044715 x^3))) u */
+void kro_gelu_mul(float *g, const float *u, int n);
+/* ops/ops.c:98-101: x = cap tanhf(x / cap) over rows of n (stride ld) */
+void kro_softcap_rows(float *x, size_t ld, int rows, int n, float cap);
 /* counts inputs in [lo, hi) (as uint32 bit patterns) where kro_expf differs
  * from the C library's expf; threads > 1 splits the range */
 uint64_t kro_expf_mismatches(uint64_t lo, uint64_t hi, int threads);

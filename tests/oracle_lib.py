@@ -47,6 +47,17 @@ oracle.kro_expf_check.restype = C.c_uint64
 oracle.kro_expf_check.argtypes = [_P, _P, C.c_size_t]
 oracle.kro_expf_check_range.restype = C.c_uint64
 oracle.kro_expf_check_range.argtypes = [C.c_uint64, _P, C.c_size_t, C.c_int]
+oracle.kro_tanhf.restype = C.c_float
+oracle.kro_tanhf.argtypes = [C.c_float]
+oracle.kro_tanhf_mismatches.restype = C.c_uint64
+oracle.kro_tanhf_mismatches.argtypes = [C.c_uint64, C.c_uint64, C.c_int]
+oracle.kro_gelu_mul.argtypes = [_P, _P, C.c_int]
+oracle.kro_tanhf_check_range.restype = C.c_uint64
+oracle.kro_tanhf_check_range.argtypes = [C.c_uint64, _P, C.c_size_t, C.c_int]
+oracle.kro_softcap_rows.argtypes = [_P, C.c_size_t, C.c_int, C.c_int, C.c_float]
+if ref is not None:
+    ref.ml_k_gelu_mul_scalar.argtypes = [_P, _P, C.c_int]
+    ref.ml_softcap_rows.argtypes = [_P, C.c_size_t, C.c_int, C.c_int, C.c_float]
 oracle.kro_f32_to_f16.restype = C.c_uint16
 oracle.kro_f32_to_f16.argtypes = [C.c_float]
 oracle.kro_f32_to_f16_range.argtypes = [_P, C.c_uint32, C.c_size_t]

@@ -36,6 +36,14 @@ VARIANTS = {
                            hidden_dim=256, vocab=512, max_seq=96, std=0.1, qk_norm=1, sliding_window=6,
                            layer_sliding=0b10, layer_local=0b10, rope_local_theta=1e4),
 }
+# GELU and soft-capping (Gemma 2 / 3 shapes)
+VARIANTS["gelu_softcap_gemma2"] = dict(K.CONFIGS["stories15m_q8"], std=0.1, seed=24, act=K.ML_ACT_GELU_TANH,
+                                       embed_scale=16.0, attn_softcap=5.0, final_softcap=3.0, sliding_window=6,
+                                       layer_sliding=0b101010)
+VARIANTS["gelu_post_qk_gemma3"] = dict(K.CONFIGS["qwen05b_mixed"], dim=128, n_layers=2, n_heads=4, n_kv_heads=2,
+                                       hidden_dim=256, vocab=512, max_seq=96, std=0.1, act=K.ML_ACT_GELU_TANH,
+                                       post_norms=1, qk_norm=1, final_softcap=8.0, rope_local_theta=1e4,
+                                       layer_local=0b01, layer_sliding=0b01, sliding_window=5)
 KV = {"f32": K.ML_F32, "f16": K.ML_F16, "q8": K.ML_Q8_0}
 
 
@@ -87,6 +95,45 @@ def test_heads_norm_rope(hd, nh, nkv, normed):
     assert np.array_equal(bits(qb.get(np.float32, nh * hd)), bits(wq))
     assert np.array_equal(bits(kb.get(np.float32, nkv * hd)), bits(wk))
     for b in bufs:
+        b.free()
+
+
+def test_tanhf_exhaustive():
+    """the device tanhf (and the expm1f under it) equals the host C library's
+    on every float32 input"""
+    n = 1 << 26
+    y = K.DevBuf(4 * n)
+    try:
+        for lo in range(0, 1 << 32, n):
+            K.hip.krh_tanhf_range(y.ptr, lo, n)
+            ok()
+            got = y.get(np.float32, n)
+            assert oracle.kro_tanhf_check_range(lo, got.ctypes.data, n, 16) == 0, hex(lo)
+    finally:
+        y.free()
+
+
+@pytest.mark.parametrize("n", [1, 333, 14336])
+def test_gelu_softcap_ops(n):
+    """the op table's gelu_mul and softcap kernels against the oracle's
+    (pinned to the reference's scalar kernels)"""
+    rng = np.random.default_rng(n)
+    g = (rng.standard_normal(n) * 4).astype(np.float32)
+    u = rng.standard_normal(n).astype(np.float32)
+    want = g.copy()
+    oracle.kro_gelu_mul(want.ctypes.data, u.ctypes.data, n)
+    gb, ub = K.DevBuf.of(g), K.DevBuf.of(u)
+    K.hip.krh_gelu_mul(gb.ptr, ub.ptr, n)
+    ok()
+    assert np.array_equal(bits(gb.get(np.float32, n)), bits(want))
+    x = (rng.standard_normal(2 * n) * 40).astype(np.float32)
+    want = x.copy()
+    oracle.kro_softcap_rows(want.ctypes.data, n, 2, n, 30.0)
+    xb = K.DevBuf.of(x)
+    K.hip.krh_softcap_rows(xb.ptr, n, 2, n, 30.0)
+    ok()
+    assert np.array_equal(bits(xb.get(np.float32, 2 * n)), bits(want))
+    for b in (gb, ub, xb):
         b.free()
 
 

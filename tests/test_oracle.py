@@ -268,6 +268,37 @@ def test_f16_widening_closed_form():
 
 # ---- F16 and Q8 KV caches (k_scalar.c:124-155, ops/ops.c:81-96) ----
 
+def test_tanhf_exhaustive_vs_libm():
+    """the restated tanhf and expm1f equal the host C library's (glibc 2.35,
+    which the reference calls) on every float32 input"""
+    assert O.oracle.kro_tanhf_mismatches(0, 1 << 32, os.cpu_count() or 8) == 0
+
+
+def test_tanhf_specials():
+    for x, want in [(0.0, 0.0), (-0.0, -0.0), (float("inf"), 1.0), (float("-inf"), -1.0), (30.0, 1.0)]:
+        got = O.oracle.kro_tanhf(x)
+        assert got == want and np.signbit(np.float32(got)) == np.signbit(np.float32(want))
+    assert np.isnan(O.oracle.kro_tanhf(float("nan")))
+
+
+@needs_ref
+@pytest.mark.parametrize("n", [1, 77, 4096])
+def test_gelu_softcap_match_reference(n):
+    rng = np.random.default_rng(n)
+    g = (rng.standard_normal(n) * 4).astype(np.float32)
+    g[: min(n, 4)] = [0.0, -0.0, 1e-30, -40.0][: min(n, 4)]
+    u = rng.standard_normal(n).astype(np.float32)
+    a, b = g.copy(), g.copy()
+    O.oracle.kro_gelu_mul(a.ctypes.data, u.ctypes.data, n)
+    ref.ml_k_gelu_mul_scalar(b.ctypes.data, u.ctypes.data, n)
+    assert np.array_equal(bits(a), bits(b))
+    x = (rng.standard_normal(3 * n) * 30).astype(np.float32)
+    a, b = x.copy(), x.copy()
+    O.oracle.kro_softcap_rows(a.ctypes.data, n, 3, n - (n > 1), 7.5)
+    ref.ml_softcap_rows(b.ctypes.data, n, 3, n - (n > 1), 7.5)
+    assert np.array_equal(bits(a), bits(b))
+
+
 def test_f32_to_f16_exhaustive_vs_ieee():
     # every float32 input against the x86 F16C conversion (IEEE round to
     # nearest even); NaN inputs become the quiet NaN 0x7e00 with their sign
@@ -416,6 +447,14 @@ SMALL = {
     "rope_yarn": dict(K.CONFIGS["stories15m_q8"], std=0.1, seed=23, rope_type=K.ML_ROPE_YARN, rope_factor=4.0,
                       rope_low_freq_factor=32.0, rope_high_freq_factor=1.0, rope_orig_max_seq=64,
                       rope_attn_factor=1.2),
+    # GELU and soft-capping (k_scalar.c:100-105, ops/ops.c:98-101, :141, model/transformer.c:304)
+    "gelu_softcap_gemma2": dict(K.CONFIGS["stories15m_q8"], std=0.1, seed=24, act=K.ML_ACT_GELU_TANH,
+                                embed_scale=16.0, attn_softcap=5.0, final_softcap=3.0, sliding_window=6,
+                                layer_sliding=0b101010),
+    "gelu_post_qk_gemma3": dict(K.CONFIGS["qwen05b_mixed"], dim=128, n_layers=2, n_heads=4, n_kv_heads=2,
+                                hidden_dim=256, vocab=512, max_seq=96, std=0.1, act=K.ML_ACT_GELU_TANH,
+                                post_norms=1, qk_norm=1, final_softcap=8.0, rope_local_theta=1e4,
+                                layer_local=0b01, layer_sliding=0b01, sliding_window=5),
 }
 
 
