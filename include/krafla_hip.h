@@ -258,12 +258,12 @@ void krh_add(float *y, const float *x, int n);                                  
 void krh_rope(float *q, float *k, const float *cos_t, const float *sin_t, int head_dim, int n_heads,
               int n_kv_heads);                                                           /* :79-94 */
 void krh_silu_mul(float *g, const float *u, int n);                                     /* :96-98 */
-void krh_gelu_mul(float *g, const float *u, int n);        /* :100-105; device tanhf (not the C library's) */
+void krh_gelu_mul(float *g, const float *u, int n);        /* :100-105, with the C library's tanhf */
 void krh_softmax(float *x, int n);                                                      /* :66-77 */
 void krh_dot_rows(float *s, const float *q, const float *k, size_t ldk, int rows, int n, float scale); /* :111-117 */
 void krh_axpy_rows(float *y, const float *a, const float *x, size_t ldx, int rows, int n);              /* :119-122 */
 void krh_quantize_row(int8_t *q, float *d, const float *x, int n);    /* ops/ops.c:81-96: one scale for the row */
-void krh_softcap_rows(float *x, size_t ld, int rows, int n, float cap);    /* ops/ops.c:98-101; device tanhf */
+void krh_softcap_rows(float *x, size_t ld, int rows, int n, float cap);    /* ops/ops.c:98-101, the C library's tanhf */
 /* *dst = value, in stream order (positions and token ids of op-table calls) */
 void krh_set_int(int *dst, int value);
 /* dT[b * ldx + t] = d[t * nb + b]: batch scales to krh_matmul's layout */

@@ -24,7 +24,9 @@ struct krh_sampler_dev {
     unsigned *keys;            // [2][vocab]: sort keys, two buffers
     int *ids;                  // [2][vocab]
     int *hist;                 // [blocks][256]: digit counts per sort workgroup
-    int *meta;                 // [4]: see MT_*
+    float *part;               // [blocks]: the elementwise workgroups' maxima
+    int *pnan;                 // [blocks]: and whether they saw a NaN
+    int *meta;                 // [8]: see MT_*
 };
 
 struct krh_sampler {
@@ -37,6 +39,8 @@ namespace {
 constexpr int SM_NT = 1024;                                       // threads of the one-workgroup kernels
 constexpr int SM_G = 12288;                                       // terms per ordered-sum group (in LDS)
 constexpr int SM_RT = 256, SM_ROWS = 4, SM_E = SM_RT * SM_ROWS;   // radix sort: threads, rows, ids per workgroup
+constexpr int SM_HB = 16;                                         // digit counts read at a time
+constexpr int SM_EB = 2048;                                       // ids per elementwise workgroup (256 x 8)
 constexpr int SM_TERMS = sc_terms_cap(SM_G) * 4;
 constexpr int SM_SCR = (sc_lds_bytes(SM_G, SM_NT) + 15) & ~15;
 constexpr int SM_CST = (sc_chunks(SM_G) + 1) * 4;
@@ -47,7 +51,10 @@ static_assert(SM_LDS <= 64 * 1024, "LDS");
 enum { SM_GREEDY = 0, SM_MULT = 1, SM_TOPK = 2, SM_TOPP = 3 };
 // meta: candidates after the sort's first pass, the coin's bits, whether the
 // id is already decided (NaN probabilities), and that id
-enum { MT_M = 0, MT_COIN = 1, MT_DONE = 2, MT_ID = 3 };
+enum { MT_M = 0, MT_COIN = 1, MT_DONE = 2, MT_ID = 3, MT_KIND = 4 };
+// the softmax's case, from the maxima: numerators expf(p - max), all -inf
+// (uniform 1/n), or a NaN term (every probability NaN)
+enum { SK_EXP = 0, SK_UNIFORM = 1, SK_NAN = 2 };
 
 using Dev = krh_sampler_dev;
 
@@ -60,17 +67,6 @@ __device__ __forceinline__ void sm_sync_global() {
     __threadfence();
     __syncthreads();
     __threadfence();
-}
-
-// max over the workgroup, NaN-ignoring as fmaxf (NaN only when all are)
-__device__ float sm_max(float v, float *red) {
-    for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
-    if ((sm_tid() & 63) == 0) red[sm_tid() >> 6] = v;
-    __syncthreads();
-    float r = red[0];
-    for (int w = 1; w < SM_NT / 64; w++) r = fmaxf(r, red[w]);
-    __syncthreads();
-    return r;
 }
 
 // model/sampler.c:57-61: the first index of the largest value; NaN never
@@ -211,55 +207,93 @@ __device__ int sm_first_above(Term term, int m, float thr, unsigned char *lds, f
     return -1;
 }
 
-// The penalty, then the greedy pick; or the temperature softmax
-// (model/sampler.c:158-159, kernels/scalar/k_scalar.c:66-77), the coin and,
-// for the multinomial walk, the draw. For the sorted draws it leaves the
-// probabilities and the coin for the kernels after it.
-template <int MODE>
-__global__ void __launch_bounds__(SM_NT) k_smp_main(int *tok, float *logits, int n, Dev d, int *pos, int *log) {
-    extern __shared__ __align__(16) unsigned char sm_lds[];
-    __shared__ float rv[SM_NT / 64];
-    __shared__ int ri[SM_NT / 64];
-    __shared__ float scoin;
-    const int tid = sm_tid();
-    sm_penalize(logits, n, d);
-    if constexpr (MODE == SM_GREEDY) {
-        const int t = sm_argmax(logits, n, rv, ri);
-        if (tid == 0) sm_finish(t, tok, pos, log, d);
-        return;
-    } else {
-        float *p = d.probs;
-        float mx = __int_as_float(0x7fc00000);
-        int nan = 0;
-        for (int i = tid; i < n; i += SM_NT) {
+// The penalty alone (one workgroup), ahead of the kernels that read the logits.
+__global__ void __launch_bounds__(SM_NT) k_smp_penalize(float *logits, int n, Dev d) { sm_penalize(logits, n, d); }
+
+// Temperature (model/sampler.c:158): p = logits / T, and each workgroup's
+// maximum (NaN-ignoring, as fmaxf) and whether it saw a NaN.
+__global__ void __launch_bounds__(256) k_smp_scale(const float *logits, int n, Dev d) {
+    __shared__ float red[4];
+    __shared__ int rn[4];
+    float mx = __int_as_float(0x7fc00000);
+    int nan = 0;
+    const int base = (int)blockIdx.x * SM_EB + sm_tid();
+#pragma unroll
+    for (int k = 0; k < SM_EB / 256; k++) {
+        const int i = base + k * 256;
+        if (i < n) {
             const float v = kr_fdiv(logits[i], d.temperature);
-            p[i] = v;
+            d.probs[i] = v;
             mx = fmaxf(mx, v);
             nan |= v != v;
         }
-        mx = sm_max(mx, rv);
-        nan = __syncthreads_or(nan);
-        int decided = -1;
-        if (mx == -INFINITY) {   // every value -inf: uniform
-            const float u = kr_fdiv(1.0f, (float)n);
-            for (int i = tid; i < n; i += SM_NT) p[i] = u;
-        } else if (nan || mx != mx || mx == INFINITY) {
-            // a NaN term (a NaN value, or inf - inf): the sum and every
-            // probability are NaN. The walk then passes no coin (the last
-            // id), top-p keeps no candidate (the argmax of all-NaN: 0) and
-            // top-k keeps the first k ids in id order (the last of them).
-            for (int i = tid; i < n; i += SM_NT) p[i] = __int_as_float(0x7fc00000);
-            decided = MODE == SM_MULT ? n - 1 : MODE == SM_TOPK ? d.topk - 1 : 0;
-        } else {
+    }
+    for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+    nan = __any(nan);
+    if ((sm_tid() & 63) == 0) {
+        red[sm_tid() >> 6] = mx;
+        rn[sm_tid() >> 6] = nan;
+    }
+    __syncthreads();
+    if (sm_tid() == 0) {
+        d.part[blockIdx.x] = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+        d.pnan[blockIdx.x] = rn[0] | rn[1] | rn[2] | rn[3];
+    }
+}
+
+// The softmax's numerators (kernels/scalar/k_scalar.c:66-77): the maximum
+// of all workgroups' maxima, then expf(p - max); every value -inf: 1/n; a NaN
+// term (a NaN value, or inf - inf): NaN everywhere, as the sum and every
+// probability become.
+__global__ void __launch_bounds__(256) k_smp_exp(int n, int nblk, Dev d) {
+    __shared__ float sp[256];
+    __shared__ int sn[256];
+    if (sm_tid() < nblk) {
+        sp[sm_tid()] = d.part[sm_tid()];
+        sn[sm_tid()] = d.pnan[sm_tid()];
+    }
+    __syncthreads();
+    float mx = __int_as_float(0x7fc00000);
+    int nan = 0;
+    for (int k = 0; k < nblk; k++) {
+        mx = fmaxf(mx, sp[k]);
+        nan |= sn[k];
+    }
+    const int kind = mx == -INFINITY ? SK_UNIFORM : (nan || mx != mx || mx == INFINITY) ? SK_NAN : SK_EXP;
+    if (blockIdx.x == 0 && sm_tid() == 0) d.meta[MT_KIND] = kind;
+    const float u = kr_fdiv(1.0f, (float)n);
+    const int base = (int)blockIdx.x * SM_EB + sm_tid();
+#pragma unroll
+    for (int k = 0; k < SM_EB / 256; k++) {
+        const int i = base + k * 256;
+        if (i < n) {
+            const float p = d.probs[i];
+            d.probs[i] = kind == SK_EXP ? kr_expf(kr_fsub(p, mx)) : kind == SK_UNIFORM ? u : __int_as_float(0x7fc00000);
+        }
+    }
+}
+
+// The softmax's ordered sum and x * (1/sum) (kernels/scalar/k_scalar.c:
+// 73-76), the coin, and for the multinomial walk the draw. For the sorted
+// draws it leaves the probabilities and the coin for the kernels after it.
+template <int MODE>
+__global__ void __launch_bounds__(SM_NT) k_smp_main(int *tok, int n, Dev d, int *pos, int *log) {
+    extern __shared__ __align__(16) unsigned char sm_lds[];
+    __shared__ float scoin;
+    const int tid = sm_tid();
+    {
+        float *p = d.probs;
+        const int kind = d.meta[MT_KIND];
+        // NaN probabilities: the walk passes no coin (the last id), top-p
+        // keeps no candidate (the argmax of all-NaN: 0), and top-k keeps the
+        // first k ids in id order (the last of them)
+        const int decided = kind != SK_NAN ? -1 : MODE == SM_MULT ? n - 1 : MODE == SM_TOPK ? d.topk - 1 : 0;
+        if (kind == SK_EXP) {
             float *t = (float *)sm_lds;
             float S = 0.0f;
             for (int g0 = 0; g0 < n; g0 += SM_G) {
                 const int ng = min(SM_G, n - g0), sh = sc_log_len(ng);
-                for (int i = tid; i < ng; i += SM_NT) {
-                    const float e = kr_expf(kr_fsub(p[g0 + i], mx));
-                    t[sc_at(i, sh)] = e;
-                    p[g0 + i] = e;
-                }
+                for (int i = tid; i < ng; i += SM_NT) t[sc_at(i, sh)] = p[g0 + i];
                 __syncthreads();
                 S = kr_spec_sum<SM_NT>(t, ng, sm_lds + SM_TERMS, S);
             }
@@ -342,12 +376,19 @@ __global__ void __launch_bounds__(SM_RT) k_smp_scatter(Dev d, int n, float cutof
     if (d.meta[MT_DONE]) return;
     const int tid = sm_tid(), lane = tid & 63, w = tid >> 6, NB = (int)gridDim.x, b = (int)blockIdx.x;
     const int m = P == 0 ? n : d.meta[MT_M];
-    // digit tid: ids of this digit in earlier workgroups, and in all
+    // digit tid: ids of this digit in earlier workgroups, and in all; the
+    // counts are read SM_HB at a time, so their L2 latencies overlap
     int tot = 0, pre = 0;
-    for (int k = 0; k < NB; k++) {
-        const int c = d.hist[k * 256 + tid];
-        tot += c;
-        pre += k < b ? c : 0;
+    for (int k0 = 0; k0 < NB; k0 += SM_HB) {
+        int c[SM_HB];
+#pragma unroll
+        for (int j = 0; j < SM_HB; j++) c[j] = d.hist[min(k0 + j, NB - 1) * 256 + tid];
+#pragma unroll
+        for (int j = 0; j < SM_HB; j++) {
+            const int v = k0 + j < NB ? c[j] : 0;
+            tot += v;
+            pre += k0 + j < b ? v : 0;
+        }
     }
     int inc = tot;
     for (int o = 1; o < 64; o <<= 1) {
@@ -475,8 +516,13 @@ extern "C" ml_status krh_sampler_new(krh_sampler **out, int vocab, const krh_sam
     d.R = o->repeat_last_n > 0 ? o->repeat_last_n : 0;
     d.vocab = vocab;
     const size_t V = (size_t)vocab, nb = (V + SM_E - 1) / SM_E;
-    // rng, probs, keys and ids (two buffers each), hist, meta, first, ring
-    const size_t bytes = 8 + 4 * (V + 4 * V + nb * 256 + 4 + V + 2 + (size_t)d.R);
+    if (V > (size_t)256 * SM_EB) {   // the exp kernel gathers at most 256 workgroup maxima
+        free(s);
+        kr_fail(ML_E_SHAPE, "sampler vocab", hipSuccess);
+        return ML_E_SHAPE;
+    }
+    // rng, probs, keys and ids (two buffers each), hist, part, pnan, meta, first, ring
+    const size_t bytes = 8 + 4 * (V + 4 * V + nb * 256 + 2 * nb + 8 + V + 2 + (size_t)d.R);
     hipError_t e = hipMalloc(&s->mem, bytes);
     if (e != hipSuccess) {
         free(s);
@@ -494,8 +540,12 @@ extern "C" ml_status krh_sampler_new(krh_sampler **out, int vocab, const krh_sam
     p += 8 * V;
     d.hist = (int *)p;
     p += 4 * nb * 256;
+    d.part = (float *)p;
+    p += 4 * nb;
+    d.pnan = (int *)p;
+    p += 4 * nb;
     d.meta = (int *)p;
-    p += 16;
+    p += 32;
     d.first = (int *)p;
     p += 4 * V;
     d.ring = (int *)p;
@@ -547,21 +597,28 @@ extern "C" void krh_sample(krh_sampler *s, int *tok, float *logits, int n, int *
                      : (d.topp <= 0.0f || d.topp >= 1.0f) ? SM_MULT
                                                           : SM_TOPP;
     hipStream_t st = kr_stream();
+    if (d.rp != 1.0f) hipLaunchKernelGGL(k_smp_penalize, dim3(1), dim3(SM_NT), 0, st, logits, n, d);
+    if (mode == SM_GREEDY) {   // the many-workgroup argmax; the ring only matters with a penalty
+        krh_argmax(tok, logits, n, pos, log);
+        if (d.rp != 1.0f) hipLaunchKernelGGL(k_smp_accept, dim3(1), dim3(1), 0, st, d, (const int *)tok, 1);
+        kr_check_launch("sample");
+        return;
+    }
+    const int nblk = (n + SM_EB - 1) / SM_EB;
+    hipLaunchKernelGGL(k_smp_scale, dim3(nblk), dim3(256), 0, st, logits, n, d);
+    hipLaunchKernelGGL(k_smp_exp, dim3(nblk), dim3(256), 0, st, n, nblk, d);
     switch (mode) {
-    case SM_GREEDY:
-        hipLaunchKernelGGL(k_smp_main<SM_GREEDY>, dim3(1), dim3(SM_NT), 0, st, tok, logits, n, d, pos, log);
-        break;
     case SM_MULT:
-        hipLaunchKernelGGL(k_smp_main<SM_MULT>, dim3(1), dim3(SM_NT), SM_LDS, st, tok, logits, n, d, pos, log);
+        hipLaunchKernelGGL(k_smp_main<SM_MULT>, dim3(1), dim3(SM_NT), SM_LDS, st, tok, n, d, pos, log);
         break;
     default: {
         const int topp = mode == SM_TOPP;
         // model/sampler.c:134, in float as there
         const float cutoff = topp && n > 1 ? (1.0f - d.topp) / (float)(n - 1) : 0.0f;
         if (topp)
-            hipLaunchKernelGGL(k_smp_main<SM_TOPP>, dim3(1), dim3(SM_NT), SM_LDS, st, tok, logits, n, d, pos, log);
+            hipLaunchKernelGGL(k_smp_main<SM_TOPP>, dim3(1), dim3(SM_NT), SM_LDS, st, tok, n, d, pos, log);
         else
-            hipLaunchKernelGGL(k_smp_main<SM_TOPK>, dim3(1), dim3(SM_NT), SM_LDS, st, tok, logits, n, d, pos, log);
+            hipLaunchKernelGGL(k_smp_main<SM_TOPK>, dim3(1), dim3(SM_NT), SM_LDS, st, tok, n, d, pos, log);
         sort_pass<0>(d, n, cutoff, topp);
         sort_pass<1>(d, n, cutoff, topp);
         sort_pass<2>(d, n, cutoff, topp);
