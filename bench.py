@@ -217,10 +217,10 @@ def cpu_baseline(path, prompt, decode, kv="f32", sample=None):
             pass
         return {"value": round(dec, 3), "unit": "tok/s", "cores": cores, "kind": "reference",
                 "build": "ISA=%s THREADS=pthread" % isa, "cpu": cpu,
-                "sample": "ml_run on the same .mlb: %d-token prompt (%d prefilled), %d " +
-                          ("sampled" if sample else "greedy") + " decode tokens "
-                          "at positions %d..%d; decode tok/s = (positions - prefilled) / (positions / tok/s - "
-                          "prefill s)" % (len(prompt), P, pos - P, P, pos - 1),
+                "sample": ("ml_run on the same .mlb: %d-token prompt (%d prefilled), %d %s decode tokens "
+                           "at positions %d..%d; decode tok/s = (positions - prefilled) / (positions / tok/s - "
+                           "prefill s)" % (len(prompt), P, pos - P, "sampled" if sample else "greedy",
+                                           P, pos - 1)),
                 "prefill_tok_s": round(P / (M / 1000.0), 2) if M > 0 else None}
     return {"value": None, "error": "no reference CPU build in oracle/_ref (build() needs the reference sources)"}
 
