@@ -46,7 +46,6 @@ struct MmArgs {
     int head_dim, pos0;
 };
 
-constexpr int MM_TR = 128;   // weight rows per workgroup
 constexpr int MM_TT = 128;   // tokens per workgroup
 
 // 16 signed quant bytes of half h (elements 16h .. 16h+15) of a weight block
@@ -72,12 +71,13 @@ __device__ __forceinline__ v4i weight_frag(const uint8_t *blk, int h) {
 // A wave computes MM_NG row groups x 1 token group of 32 (MM_NG MFMA tiles
 // per block); the workgroup's 4 waves take 4 token groups of the same rows.
 constexpr int MM_NG = 4;
+constexpr int MM_TR = 32 * MM_NG;   // weight rows per workgroup
 
 struct Frag {
     v4i xa;              // the wave's 32 tokens
     v4i wb[MM_NG];       // row groups
     uint32_t wd[MM_NG];  // raw scale bits of the lane's row in each row group
-    float4 xd[4];        // token scales: quad q -> tokens 8q + 4(l/32) + 0..3
+    float xs;            // scale of token l % 32 of the wave's group
 };
 
 template <int QT, int D16>
@@ -87,9 +87,7 @@ __device__ __forceinline__ void mm_load(Frag &f, const MmArgs &a, const MMat &W,
         const int t = tokl + ln;   // readable: the caller pads the activations to ldx rows
         const int4 v = *(const int4 *)(a.xq + (size_t)t * a.K + (size_t)b * 32 + 16 * hf);
         f.xa = v4i{ v.x, v.y, v.z, v.w };
-        const float *xs = a.xdT + (size_t)b * a.ldx + tokl + 4 * hf;
-#pragma unroll
-        for (int q = 0; q < 4; q++) f.xd[q] = *(const float4 *)(xs + 8 * q);
+        f.xs = a.xdT[(size_t)b * a.ldx + t];
     }
 #pragma unroll
     for (int g = 0; g < MM_NG; g++) {
@@ -102,21 +100,28 @@ __device__ __forceinline__ void mm_load(Frag &f, const MmArgs &a, const MMat &W,
 }
 
 // The MFMA of row group g + 1 is issued before the rescale of group g, so
-// its latency runs under that VALU work.
+// its latency runs under that VALU work. The 16 token scales a lane needs
+// (tokens 8 (r / 4) + 4 (lane / 32) + r % 4) come from the lanes that loaded
+// them, over the LDS crossbar: one 4-byte load per lane and block instead of
+// four 16-byte broadcast loads, and 15 fewer registers per fragment.
 template <int D16>
-__device__ __forceinline__ void mm_step(float (&acc)[MM_NG][16], const Frag &f) {
+__device__ __forceinline__ void mm_step(float (&acc)[MM_NG][16], const Frag &f, int lane) {
+    float xd[16];
+    const int hb = 4 * (lane >> 5);
+#pragma unroll
+    for (int r = 0; r < 16; r++) xd[r] = __shfl(f.xs, 8 * (r >> 2) + hb + (r & 3), 64);
     v16i s = __builtin_amdgcn_mfma_i32_32x32x32_i8(f.xa, f.wb[0], v16i{}, 0, 0, 0);
 #pragma unroll
     for (int g = 0; g < MM_NG; g++) {
         v16i sn;
         if (g + 1 < MM_NG) sn = __builtin_amdgcn_mfma_i32_32x32x32_i8(f.xa, f.wb[g + 1], v16i{}, 0, 0, 0);
+        // keeps the next MFMA from being hoisted further: two result sets
+        // live instead of four, which keeps the kernel within 256 VGPRs
+        __builtin_amdgcn_sched_barrier(0);
         const float wd = D16 ? kr_h2f((uint16_t)f.wd[g]) : __uint_as_float(f.wd[g]);
 #pragma unroll
-        for (int r = 0; r < 16; r++) {
-            const float4 xq = f.xd[r >> 2];
-            const float xd = (r & 3) == 0 ? xq.x : (r & 3) == 1 ? xq.y : (r & 3) == 2 ? xq.z : xq.w;
-            acc[g][r] = kr_fadd(acc[g][r], kr_fmul(kr_fmul((float)s[r], wd), xd));
-        }
+        for (int r = 0; r < 16; r++)
+            acc[g][r] = kr_fadd(acc[g][r], kr_fmul(kr_fmul((float)s[r], wd), xd[r]));
         if (g + 1 < MM_NG) s = sn;
     }
 }
@@ -141,16 +146,19 @@ __global__ void __launch_bounds__(256, 2) k_matmul(const MmArgs a) {
 #pragma unroll
         for (int r = 0; r < 16; r++) acc[g][r] = 0.0f;
 
+    // Loads are unconditional (block indices past the end re-read the last
+    // block, unused): a load issued on only one path makes the wait-count
+    // pass drain every in-flight load at the loop head, which would cancel
+    // the one-block prefetch. Only the odd tail's step is conditional.
     Frag f0, f1;
+    const int bl = nb - 1;
     mm_load<QT, D16>(f0, a, W, 0, rowl, tokl, lane);
-    if (nb > 1) mm_load<QT, D16>(f1, a, W, 1, rowl, tokl, lane);
+    mm_load<QT, D16>(f1, a, W, 1 < bl ? 1 : bl, rowl, tokl, lane);
     for (int b = 0; b < nb; b += 2) {
-        mm_step<D16>(acc, f0);
-        if (b + 2 < nb) mm_load<QT, D16>(f0, a, W, b + 2, rowl, tokl, lane);
-        if (b + 1 < nb) {
-            mm_step<D16>(acc, f1);
-            if (b + 3 < nb) mm_load<QT, D16>(f1, a, W, b + 3, rowl, tokl, lane);
-        }
+        mm_step<D16>(acc, f0, lane);
+        mm_load<QT, D16>(f0, a, W, b + 2 < bl ? b + 2 : bl, rowl, tokl, lane);
+        if (b + 1 < nb) mm_step<D16>(acc, f1, lane);
+        mm_load<QT, D16>(f1, a, W, b + 3 < bl ? b + 3 : bl, rowl, tokl, lane);
     }
 
     // epilogue: lane = one row (32 g + lane % 32), tokens 8 (r / 4) + 4 (lane / 32) + r % 4
