@@ -73,52 +73,76 @@ __device__ __forceinline__ v4i weight_frag(const uint8_t *blk, int h) {
 constexpr int MM_NG = 4;
 constexpr int MM_TR = 32 * MM_NG;   // weight rows per workgroup
 
-struct Frag {
+// Per wave and block: the wave's 32 tokens and their scales.
+struct XFrag {
     v4i xa;              // the wave's 32 tokens
-    v4i wb[MM_NG];       // row groups
-    uint32_t wd[MM_NG];  // raw scale bits of the lane's row in each row group
     float xs;            // scale of token l % 32 of the wave's group
 };
 
+// Per thread and block, for the workgroup's weight tile: 16 quant bytes of
+// row tid / 2 (half tid % 2, Q4 unpacked to n - 8) and that row's raw scale.
+struct WReg {
+    v4i w;
+    uint32_t d;
+};
+
+constexpr int MM_ST = 3;   // LDS ring stages of the weight tile
+
+struct MmLds {
+    v4i w[MM_ST][MM_TR][2];       // [stage][row][half]
+    uint32_t d[MM_ST][MM_TR];     // [stage][row] raw scale bits
+};
+
+__device__ __forceinline__ void x_load(XFrag &f, const MmArgs &a, int b, int tokl, int lane) {
+    const int t = tokl + (lane & 31);   // readable: the caller pads the activations to ldx rows
+    const int4 v = *(const int4 *)(a.xq + (size_t)t * a.K + (size_t)b * 32 + 16 * (lane >> 5));
+    f.xa = v4i{ v.x, v.y, v.z, v.w };
+    f.xs = a.xdT[(size_t)b * a.ldx + t];
+}
+
 template <int QT, int D16>
-__device__ __forceinline__ void mm_load(Frag &f, const MmArgs &a, const MMat &W, int b, int rowl, int tokl, int lane) {
-    const int nb = a.K / KR_QK, hf = lane >> 5, ln = lane & 31;
-    {
-        const int t = tokl + ln;   // readable: the caller pads the activations to ldx rows
-        const int4 v = *(const int4 *)(a.xq + (size_t)t * a.K + (size_t)b * 32 + 16 * hf);
-        f.xa = v4i{ v.x, v.y, v.z, v.w };
-        f.xs = a.xdT[(size_t)b * a.ldx + t];
-    }
-#pragma unroll
-    for (int g = 0; g < MM_NG; g++) {
-        int r = rowl + 32 * g + ln;
-        r = r < W.rows ? r : W.rows - 1;   // rows past the end re-read the last row (not stored)
-        const size_t blk = (size_t)r * nb + b;
-        f.wb[g] = weight_frag<QT>(W.q + blk * (QT == ML_Q8_0 ? 32 : 16), hf);
-        f.wd[g] = D16 ? (uint32_t)((const uint16_t *)W.d)[blk] : ((const uint32_t *)W.d)[blk];
-    }
+__device__ __forceinline__ void w_load(WReg &R, const MMat &W, int nb, int b, int rowl, int tid) {
+    int r = rowl + (tid >> 1);
+    r = r < W.rows ? r : W.rows - 1;   // rows past the end re-read the last row (not stored)
+    const size_t blk = (size_t)r * nb + b;
+    R.w = weight_frag<QT>(W.q + blk * (QT == ML_Q8_0 ? 32 : 16), tid & 1);
+    R.d = D16 ? (uint32_t)((const uint16_t *)W.d)[blk] : ((const uint32_t *)W.d)[blk];
+}
+
+__device__ __forceinline__ void w_store(MmLds &L, int st, const WReg &R, int tid) {
+    L.w[st][tid >> 1][tid & 1] = R.w;
+    if ((tid & 1) == 0) L.d[st][tid >> 1] = R.d;
 }
 
 // The MFMA of row group g + 1 is issued before the rescale of group g, so
 // its latency runs under that VALU work. The 16 token scales a lane needs
 // (tokens 8 (r / 4) + 4 (lane / 32) + r % 4) come from the lanes that loaded
 // them, over the LDS crossbar: one 4-byte load per lane and block instead of
-// four 16-byte broadcast loads, and 15 fewer registers per fragment.
+// four 16-byte broadcast loads. The weight fragments and scales come from
+// the workgroup's LDS tile.
 template <int D16>
-__device__ __forceinline__ void mm_step(float (&acc)[MM_NG][16], const Frag &f, int lane) {
+__device__ __forceinline__ void mm_step(float (&acc)[MM_NG][16], const XFrag &f, const MmLds &L, int st, int lane) {
+    const int ln = lane & 31, hf = lane >> 5;
+    v4i wb[MM_NG];
+    uint32_t wdr[MM_NG];
+#pragma unroll
+    for (int g = 0; g < MM_NG; g++) {
+        wb[g] = L.w[st][32 * g + ln][hf];
+        wdr[g] = L.d[st][32 * g + ln];
+    }
     float xd[16];
-    const int hb = 4 * (lane >> 5);
+    const int hb = 4 * hf;
 #pragma unroll
     for (int r = 0; r < 16; r++) xd[r] = __shfl(f.xs, 8 * (r >> 2) + hb + (r & 3), 64);
-    v16i s = __builtin_amdgcn_mfma_i32_32x32x32_i8(f.xa, f.wb[0], v16i{}, 0, 0, 0);
+    v16i s = __builtin_amdgcn_mfma_i32_32x32x32_i8(f.xa, wb[0], v16i{}, 0, 0, 0);
 #pragma unroll
     for (int g = 0; g < MM_NG; g++) {
         v16i sn;
-        if (g + 1 < MM_NG) sn = __builtin_amdgcn_mfma_i32_32x32x32_i8(f.xa, f.wb[g + 1], v16i{}, 0, 0, 0);
+        if (g + 1 < MM_NG) sn = __builtin_amdgcn_mfma_i32_32x32x32_i8(f.xa, wb[g + 1], v16i{}, 0, 0, 0);
         // keeps the next MFMA from being hoisted further: two result sets
-        // live instead of four, which keeps the kernel within 256 VGPRs
+        // live instead of four
         __builtin_amdgcn_sched_barrier(0);
-        const float wd = D16 ? kr_h2f((uint16_t)f.wd[g]) : __uint_as_float(f.wd[g]);
+        const float wd = D16 ? kr_h2f((uint16_t)wdr[g]) : __uint_as_float(wdr[g]);
 #pragma unroll
         for (int r = 0; r < 16; r++)
             acc[g][r] = kr_fadd(acc[g][r], kr_fmul(kr_fmul((float)s[r], wd), xd[r]));
@@ -127,16 +151,21 @@ __device__ __forceinline__ void mm_step(float (&acc)[MM_NG][16], const Frag &f, 
 }
 
 // Workgroup = 4 waves over a 128-row x 128-token tile; wave w takes all 128
-// rows (4 row groups) and tokens 32 w .. 32 w + 31.
+// rows (4 row groups) and tokens 32 w .. 32 w + 31. The 256 threads load
+// each block's 128 x 32-byte weight tile and its scales once (16 bytes and
+// one scale per thread) into an LDS ring of 3 stages: block b + 1 is stored
+// during step b into the stage step b - 2 read, and the barrier closing each
+// step orders those stores before step b + 1 reads them.
 template <int EPI, int QT, int D16>
 __global__ void __launch_bounds__(256, 2) k_matmul(const MmArgs a) {
+    __shared__ MmLds L;
     int mi = 0;
     while (mi + 1 < a.nmat && (int)blockIdx.x >= a.tile0[mi + 1]) mi++;
     const MMat W = mi == 0 ? a.w[0] : (mi == 1 ? a.w[1] : a.w[2]);
     const int ntt = (a.T + MM_TT - 1) / MM_TT;
     const int local = (int)blockIdx.x - a.tile0[mi];
     const int rt = local / ntt, tt = local - rt * ntt;
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int rowl = rt * MM_TR, tokl = tt * MM_TT + 32 * wave;
     const int nb = a.K / KR_QK;
 
@@ -149,16 +178,31 @@ __global__ void __launch_bounds__(256, 2) k_matmul(const MmArgs a) {
     // Loads are unconditional (block indices past the end re-read the last
     // block, unused): a load issued on only one path makes the wait-count
     // pass drain every in-flight load at the loop head, which would cancel
-    // the one-block prefetch. Only the odd tail's step is conditional.
-    Frag f0, f1;
+    // the prefetch. Only the odd tail's step is conditional; every thread
+    // reaches every barrier.
     const int bl = nb - 1;
-    mm_load<QT, D16>(f0, a, W, 0, rowl, tokl, lane);
-    mm_load<QT, D16>(f1, a, W, 1 < bl ? 1 : bl, rowl, tokl, lane);
+    WReg R;
+    XFrag x0, x1;
+    w_load<QT, D16>(R, W, nb, 0, rowl, tid);
+    w_store(L, 0, R, tid);
+    w_load<QT, D16>(R, W, nb, 1 < bl ? 1 : bl, rowl, tid);
+    x_load(x0, a, 0, tokl, lane);
+    x_load(x1, a, 1 < bl ? 1 : bl, tokl, lane);
+    __syncthreads();
+    int st = 0;   // stage of block b
     for (int b = 0; b < nb; b += 2) {
-        mm_step<D16>(acc, f0, lane);
-        mm_load<QT, D16>(f0, a, W, b + 2 < bl ? b + 2 : bl, rowl, tokl, lane);
-        if (b + 1 < nb) mm_step<D16>(acc, f1, lane);
-        mm_load<QT, D16>(f1, a, W, b + 3 < bl ? b + 3 : bl, rowl, tokl, lane);
+        const int s1 = st == MM_ST - 1 ? 0 : st + 1, s2 = s1 == MM_ST - 1 ? 0 : s1 + 1;
+        w_store(L, s1, R, tid);
+        w_load<QT, D16>(R, W, nb, b + 2 < bl ? b + 2 : bl, rowl, tid);
+        mm_step<D16>(acc, x0, L, st, lane);
+        x_load(x0, a, b + 2 < bl ? b + 2 : bl, tokl, lane);
+        __syncthreads();
+        w_store(L, s2, R, tid);
+        w_load<QT, D16>(R, W, nb, b + 3 < bl ? b + 3 : bl, rowl, tid);
+        if (b + 1 < nb) mm_step<D16>(acc, x1, L, s1, lane);
+        x_load(x1, a, b + 3 < bl ? b + 3 : bl, tokl, lane);
+        __syncthreads();
+        st = s2;
     }
 
     // epilogue: lane = one row (32 g + lane % 32), tokens 8 (r / 4) + 4 (lane / 32) + r % 4
