@@ -5,9 +5,8 @@
 // element i of a matrix is normal i of the stream `key`, drawn as Box-Muller
 // pairs in double from splitmix64 of a Weyl sequence, times std, then
 // quantized per 32-block by the .mlb writer rules (docs/file-format.md:
-// 133-159). The double log/sqrt/sin/cos are the device library's, so a rare
-// element may differ from the host generator's in its last bit; a model file
-// is then read by every consumer as the same bytes.
+// 133-159). The double log/sqrt/sin/cos are kr_normal.h's, evaluated from
+// IEEE arithmetic alone, so the device writes the host generator's bytes.
 #include "kr_internal.h"
 #include "kr_numerics.h"
 
@@ -19,13 +18,11 @@ __device__ __forceinline__ uint64_t mix64(uint64_t z) {
     return z ^ (z >> 31);
 }
 
+#define KR_NORMAL_FN static __device__ inline
+#include "kr_normal.h"
+
 __device__ __forceinline__ void normal_pair(uint64_t key, uint64_t j, float *a, float *b) {
-    const uint64_t z = mix64(key + (j + 1) * 0x9E3779B97F4A7C15ULL);
-    const double u1 = ((double)(z >> 32) + 0.5) * (1.0 / 4294967296.0);
-    const double u2 = ((double)(z & 0xffffffffu) + 0.5) * (1.0 / 4294967296.0);
-    const double r = sqrt(-2.0 * log(u1)), t = 6.283185307179586 * u2;
-    *a = (float)(r * cos(t));
-    *b = (float)(r * sin(t));
+    krn_pair(mix64(key + (j + 1) * 0x9E3779B97F4A7C15ULL), a, b);
 }
 
 // One thread per 32-block: the same float operations as the host writer.

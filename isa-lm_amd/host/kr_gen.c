@@ -3,7 +3,9 @@
  * Random numbers: element i of stream s is splitmix64 of a Weyl sequence
  * keyed by (seed, s), so any element can be drawn independently and the
  * output does not depend on the thread count. Normals come in Box-Muller
- * pairs from the two 32-bit halves of one draw. Streams are numbered in file
+ * pairs from the two 32-bit halves of one draw, with log, sqrt, sin and cos
+ * evaluated from IEEE arithmetic alone (csrc/kr_normal.h), so that the device
+ * generator writes the same bytes. Streams are numbered in file
  * order. Quantization follows docs/file-format.md:133-159: Q8 with the
  * activation rule (d rounded to f16 first when scales are f16, quants against
  * the rounded d); Q4 with the amax/7 rule of core/quant_ref.c:21-38. */
@@ -26,15 +28,12 @@ static uint64_t stream_key(uint64_t seed, uint64_t stream) {
 
 static uint64_t draw(uint64_t key, uint64_t i) { return mix64(key + (i + 1) * 0x9E3779B97F4A7C15ULL); }
 
-/* normals 2j and 2j+1 of the stream */
-static void normal_pair(uint64_t key, uint64_t j, float *a, float *b) {
-    const uint64_t z = draw(key, j);
-    const double u1 = ((double)(z >> 32) + 0.5) * (1.0 / 4294967296.0);
-    const double u2 = ((double)(z & 0xffffffffu) + 0.5) * (1.0 / 4294967296.0);
-    const double r = sqrt(-2.0 * log(u1)), t = 6.283185307179586 * u2;
-    *a = (float)(r * cos(t));
-    *b = (float)(r * sin(t));
-}
+#define KR_NORMAL_FN static inline
+#include "../csrc/kr_normal.h"
+
+/* normals 2j and 2j+1 of the stream (the device generator draws the same
+ * bits: csrc/kr_normal.h) */
+static void normal_pair(uint64_t key, uint64_t j, float *a, float *b) { krn_pair(draw(key, j), a, b); }
 
 static float normal_at(uint64_t key, uint64_t i) {
     float a, b;

@@ -1,7 +1,21 @@
-/* .mlb loader: maps the file and points ml_qtensor views into it, with the
- * reference loader's validation rules and status codes (model/mlb.c:80-218,
- * docs/file-format.md:16-119, :214-222). Scales stay in the file's width
- * (f32 or f16): the device widens f16 exactly where it reads them. */
+/* .mlb model loader, written from the format specification
+ * (docs/file-format.md:16-119, validation table :214-222).
+ *
+ * The file is mapped read-only and the model's tensors are views into it.
+ * Loading runs in three stages:
+ *   1. the 256-byte header through a table of per-field rules (offset, type,
+ *      accepted range, status when outside it), then the rules that relate
+ *      fields to each other (derived dimensions, the q8 mask, RoPE scaling);
+ *   2. the per-layer flag bytes, when the header announces them;
+ *   3. a plan of the body: every array the configuration implies, in file
+ *      order, each with its byte size and the pointer it fills; one pass lays
+ *      the plan out at 64-byte boundaries against the file's size and checks
+ *      the Q8 quants for the forbidden -128.
+ * The status codes are the reference loader's: ML_E_IO when the file cannot
+ * be read, ML_E_FORMAT for encodings and truncation, ML_E_SHAPE for
+ * impossible dimensions. f16 scales stay f16 here: the device widens them
+ * exactly where it reads them. Sizes are size_t products of dimensions
+ * bounded by 2^24 x 2^16, which cannot overflow on a 64-bit host. */
 #include <fcntl.h>
 #include <math.h>
 #include <stdio.h>
@@ -12,179 +26,318 @@
 #include <unistd.h>
 #include "kr_host.h"
 
-#define MAX_DIM (1 << 16)
-#define MAX_TOKENS (1 << 24)
+#define HEADER_BYTES 256
+#define LIM_DIM 65536.0        /* dim, n_layers, heads, hidden_dim, head_dim */
+#define LIM_TOKENS 16777216.0  /* vocab, max_seq, sliding_window */
 
-typedef struct { const uint8_t *base; size_t off, size; int ok; } cursor;
+/* ---- stage 1: the header ---- */
 
-static const void *take(cursor *c, size_t n) {
-    if (!c->ok || n > c->size - c->off) { c->ok = 0; return NULL; }
-    const void *p = c->base + c->off;
-    c->off += n;
-    c->off = (c->off + ML_ALIGN - 1) & ~(size_t)(ML_ALIGN - 1);
-    if (c->off > c->size) c->off = c->size;
-    return p;
+enum { FIELD_U32 = 0, FIELD_F32 = 1 };
+
+/* one header field's acceptance rule: lo < v (open) or lo <= v, and v < hi
+ * (open) or v <= hi; a NaN passes no rule */
+typedef struct {
+    uint8_t off, kind, status, lo_open, hi_open;
+    double lo, hi;
+    const char *name;
+} field_rule;
+
+#define U32(off, lo, hi, st, name) { off, FIELD_U32, st, 0, 0, lo, hi, name }
+#define F32(off, lo_open, lo, hi, hi_open, name) { off, FIELD_F32, ML_E_FORMAT, lo_open, hi_open, lo, hi, name }
+
+static const field_rule FIELD_RULES[] = {
+    U32(8, 1, LIM_DIM, ML_E_SHAPE, "dim"),
+    U32(12, 1, LIM_DIM, ML_E_SHAPE, "n_layers"),
+    U32(16, 1, LIM_DIM, ML_E_SHAPE, "n_heads"),
+    U32(20, 1, LIM_DIM, ML_E_SHAPE, "n_kv_heads"),
+    U32(24, 1, LIM_DIM, ML_E_SHAPE, "hidden_dim"),
+    U32(28, 3, LIM_TOKENS, ML_E_SHAPE, "vocab"),   /* ids 1 and 2 are BOS and EOS */
+    U32(32, 1, LIM_TOKENS, ML_E_SHAPE, "max_seq"),
+    F32(36, 1, 0.0, INFINITY, 0, "rope_theta"),
+    F32(40, 0, 0.0, INFINITY, 0, "norm_eps"),
+    U32(44, ML_Q8_0, ML_Q4_0, ML_E_FORMAT, "wtype"),
+    U32(52, ML_ROPE_NONE, ML_ROPE_YARN, ML_E_FORMAT, "rope_type"),
+    U32(76, 0, 1, ML_E_FORMAT, "qkv_bias"),
+    U32(80, 0, LIM_DIM, ML_E_SHAPE, "head_dim"),
+    U32(84, 0, 1, ML_E_FORMAT, "qk_norm"),
+    U32(92, 0, LIM_TOKENS, ML_E_FORMAT, "sliding_window"),
+    U32(96, 0, 1, ML_E_FORMAT, "layer_flags"),
+    F32(100, 0, 0.0, 1e30, 1, "rope_local_theta"),
+    U32(104, ML_ACT_SILU, ML_ACT_GELU_TANH, ML_E_FORMAT, "act"),
+    U32(108, 0, 1, ML_E_FORMAT, "post_norms"),
+    F32(112, 0, 0.0, 1e6, 1, "embed_scale"),
+    F32(116, 0, 0.0, 1e6, 1, "attn_scale"),
+    U32(120, 0, 1, ML_E_FORMAT, "scale_f16"),
+    F32(124, 0, 0.0, 1e6, 1, "attn_softcap"),
+    F32(128, 0, 0.0, 1e6, 1, "final_softcap"),
+};
+#undef U32
+#undef F32
+
+static uint32_t le32(const uint8_t *h, int off) {
+    uint32_t v;
+    memcpy(&v, h + off, 4);
+    return v;
 }
 
-/* model/mlb.c:24-38: quants, then scales; a Q8 quant of -128 is rejected */
-static ml_qtensor take_mat(cursor *c, int rows, int cols, int type, int f16) {
-    ml_qtensor t = { NULL, NULL, rows, cols, (uint8_t)type, NULL, NULL, NULL, 0 };
-    const size_t n = (size_t)rows * cols, nd = n / QK * (f16 ? 2 : 4);
-    t.q = take(c, type == ML_Q4_0 ? n / 2 : n);
-    if (f16) t.dh = take(c, nd);
-    else t.d = take(c, nd);
-    if (c->ok && type == ML_Q8_0 && memchr(t.q, 0x80, n)) c->ok = 0;
-    return t;
+static float lef(const uint8_t *h, int off) {
+    float v;
+    memcpy(&v, h + off, 4);
+    return v;
 }
 
-static uint32_t rd32(const uint8_t *p) { uint32_t v; memcpy(&v, p, 4); return v; }
-static float rdf(const uint8_t *p) { float v; memcpy(&v, p, 4); return v; }
+static double field_value(const uint8_t *h, const field_rule *r) {
+    return r->kind == FIELD_U32 ? (double)le32(h, r->off) : (double)lef(h, r->off);
+}
 
-/* model/mlb.c:80-159 */
+static int field_ok(double v, const field_rule *r) {
+    const int lo = r->lo_open ? v > r->lo : v >= r->lo;
+    const int hi = r->hi_open ? v < r->hi : v <= r->hi;
+    return lo && hi;
+}
+
+/* the RoPE scaling parameters of each rope_type (the specification's header
+ * notes at offsets 52-68 and 88) */
+static int rope_params_ok(const ml_config *c) {
+    const float f = c->rope_factor, lo = c->rope_low_freq_factor, hi = c->rope_high_freq_factor;
+    const int factor_ok = f > 0.0f && f < 1e6f;
+    switch (c->rope_type) {
+    case ML_ROPE_NONE:
+        return 1;
+    case ML_ROPE_LINEAR:
+        return factor_ok;
+    case ML_ROPE_LLAMA3:
+        return factor_ok && lo > 0.0f && hi > lo && hi < 1e6f && c->rope_orig_max_seq > 0;
+    default:   /* yarn: lo is beta_fast, hi beta_slow, with beta_fast > beta_slow > 0 */
+        return factor_ok && hi > 0.0f && lo > hi && lo < 1e6f && c->rope_orig_max_seq > 0 &&
+               c->rope_attn_factor > 0.0f && c->rope_attn_factor < 1e3f;
+    }
+}
+
 ml_status kr_parse_header(ml_config *cfg, int *shared, const uint8_t *h) {
     memset(cfg, 0, sizeof *cfg);
-    if (memcmp(h, "MLB1", 4) != 0 || rd32(h + 4) != 1) return ML_E_FORMAT;
-    uint32_t v[7];
-    for (int i = 0; i < 7; i++) v[i] = rd32(h + 8 + 4 * i);
-    for (int i = 0; i < 7; i++)
-        if (v[i] == 0 || v[i] > (i == 5 || i == 6 ? MAX_TOKENS : MAX_DIM)) return ML_E_SHAPE;
-    if (v[5] < 3) return ML_E_SHAPE;
-    cfg->dim = (int)v[0]; cfg->n_layers = (int)v[1]; cfg->n_heads = (int)v[2];
-    cfg->n_kv_heads = (int)v[3]; cfg->hidden_dim = (int)v[4]; cfg->vocab = (int)v[5];
-    cfg->max_seq = (int)v[6];
-    cfg->rope_theta = rdf(h + 36);
-    cfg->norm_eps = rdf(h + 40);
-    cfg->wtype = (int)rd32(h + 44);
-    *shared = rd32(h + 48) != 0;
-    if (cfg->wtype != ML_Q8_0 && cfg->wtype != ML_Q4_0) return ML_E_FORMAT;
-    cfg->q8_mask = rd32(h + 72);
-    if ((cfg->q8_mask & ~(unsigned)ML_Q8M_ALL) || (cfg->wtype == ML_Q8_0 && cfg->q8_mask)) return ML_E_FORMAT;
-    const uint32_t bias = rd32(h + 76);
-    if (bias > 1) return ML_E_FORMAT;
-    cfg->qkv_bias = (int)bias;
-    if (cfg->dim % QK || cfg->hidden_dim % QK) return ML_E_SHAPE;
-    if (cfg->n_heads % cfg->n_kv_heads) return ML_E_SHAPE;
-    const uint32_t hd = rd32(h + 80);
-    if (hd > MAX_DIM || (!hd && cfg->dim % cfg->n_heads)) return ML_E_SHAPE;
-    cfg->head_dim = hd ? (int)hd : cfg->dim / cfg->n_heads;
-    if ((uint64_t)cfg->head_dim * (uint64_t)cfg->n_heads > MAX_DIM) return ML_E_SHAPE;
-    cfg->q_dim = cfg->head_dim * cfg->n_heads;
-    cfg->kv_dim = cfg->head_dim * cfg->n_kv_heads;
-    if (cfg->head_dim % 2 || cfg->q_dim % QK) return ML_E_SHAPE;
-    const uint32_t qkn = rd32(h + 84), win = rd32(h + 92);
-    if (qkn > 1 || win > MAX_TOKENS) return ML_E_FORMAT;
-    cfg->qk_norm = (int)qkn;
-    cfg->sliding_window = (int)win;
-    const uint32_t lflags = rd32(h + 96);
-    if (lflags > 1) return ML_E_FORMAT;
-    cfg->layer_flags = (int)lflags;
-    cfg->rope_local_theta = rdf(h + 100);
-    if (!(cfg->rope_local_theta >= 0.0f && cfg->rope_local_theta < 1e30f)) return ML_E_FORMAT;
-    const uint32_t act = rd32(h + 104), pn = rd32(h + 108);
-    if (act > ML_ACT_GELU_TANH || pn > 1) return ML_E_FORMAT;
-    cfg->act = (int)act;
-    cfg->post_norms = (int)pn;
-    cfg->embed_scale = rdf(h + 112);
-    cfg->attn_scale = rdf(h + 116);
-    if (!(cfg->embed_scale >= 0.0f && cfg->embed_scale < 1e6f) || !(cfg->attn_scale >= 0.0f && cfg->attn_scale < 1e6f))
-        return ML_E_FORMAT;
-    if (cfg->embed_scale == 0.0f) cfg->embed_scale = 1.0f;
-    if (cfg->attn_scale == 0.0f) cfg->attn_scale = 1.0f / sqrtf((float)cfg->head_dim);
-    const uint32_t f16 = rd32(h + 120);
-    if (f16 > 1) return ML_E_FORMAT;
-    cfg->scale_f16 = (int)f16;
-    cfg->attn_softcap = rdf(h + 124);
-    cfg->final_softcap = rdf(h + 128);
-    if (!(cfg->attn_softcap >= 0.0f && cfg->attn_softcap < 1e6f) || !(cfg->final_softcap >= 0.0f && cfg->final_softcap < 1e6f))
-        return ML_E_FORMAT;
-    if (!(cfg->rope_theta > 0.0f) || !(cfg->norm_eps >= 0.0f)) return ML_E_FORMAT;
-    cfg->rope_type = (int)rd32(h + 52);
-    cfg->rope_factor = rdf(h + 56);
-    cfg->rope_low_freq_factor = rdf(h + 60);
-    cfg->rope_high_freq_factor = rdf(h + 64);
-    cfg->rope_orig_max_seq = (int)rd32(h + 68);
-    cfg->rope_attn_factor = rdf(h + 88);
-    if (cfg->rope_type != ML_ROPE_YARN && cfg->rope_attn_factor != 0.0f) return ML_E_FORMAT;
-    if (cfg->rope_type == ML_ROPE_LLAMA3) {
-        if (!(cfg->rope_factor > 0.0f && cfg->rope_factor < 1e6f) || !(cfg->rope_low_freq_factor > 0.0f) ||
-            !(cfg->rope_high_freq_factor > cfg->rope_low_freq_factor && cfg->rope_high_freq_factor < 1e6f) ||
-            cfg->rope_orig_max_seq <= 0)
-            return ML_E_FORMAT;
-    } else if (cfg->rope_type == ML_ROPE_LINEAR) {
-        if (!(cfg->rope_factor > 0.0f && cfg->rope_factor < 1e6f)) return ML_E_FORMAT;
-    } else if (cfg->rope_type == ML_ROPE_YARN) {
-        if (!(cfg->rope_factor > 0.0f && cfg->rope_factor < 1e6f) || !(cfg->rope_high_freq_factor > 0.0f) ||
-            !(cfg->rope_low_freq_factor > cfg->rope_high_freq_factor && cfg->rope_low_freq_factor < 1e6f) ||
-            cfg->rope_orig_max_seq <= 0 || !(cfg->rope_attn_factor > 0.0f && cfg->rope_attn_factor < 1e3f))
-            return ML_E_FORMAT;
-    } else if (cfg->rope_type != ML_ROPE_NONE) {
-        return ML_E_FORMAT;
+    if (memcmp(h, "MLB1", 4) != 0) return kr_seterr(ML_E_FORMAT, "magic is not MLB1");
+    if (le32(h, 4) != 1) return kr_seterr(ML_E_FORMAT, "version %u (1 expected)", le32(h, 4));
+    for (size_t i = 0; i < sizeof FIELD_RULES / sizeof FIELD_RULES[0]; i++) {
+        const field_rule *r = &FIELD_RULES[i];
+        const double v = field_value(h, r);
+        if (!field_ok(v, r)) return kr_seterr((ml_status)r->status, "header field %s = %g out of range", r->name, v);
     }
+    ml_config *c = cfg;
+    c->dim = (int)le32(h, 8);
+    c->n_layers = (int)le32(h, 12);
+    c->n_heads = (int)le32(h, 16);
+    c->n_kv_heads = (int)le32(h, 20);
+    c->hidden_dim = (int)le32(h, 24);
+    c->vocab = (int)le32(h, 28);
+    c->max_seq = (int)le32(h, 32);
+    c->rope_theta = lef(h, 36);
+    c->norm_eps = lef(h, 40);
+    c->wtype = (int)le32(h, 44);
+    *shared = le32(h, 48) != 0;
+    c->rope_type = (int)le32(h, 52);
+    c->rope_factor = lef(h, 56);
+    c->rope_low_freq_factor = lef(h, 60);
+    c->rope_high_freq_factor = lef(h, 64);
+    c->rope_orig_max_seq = (int)le32(h, 68);
+    c->q8_mask = le32(h, 72);
+    c->qkv_bias = (int)le32(h, 76);
+    const int head_dim = (int)le32(h, 80);
+    c->qk_norm = (int)le32(h, 84);
+    c->rope_attn_factor = lef(h, 88);
+    c->sliding_window = (int)le32(h, 92);
+    c->layer_flags = (int)le32(h, 96);
+    c->rope_local_theta = lef(h, 100);
+    c->act = (int)le32(h, 104);
+    c->post_norms = (int)le32(h, 108);
+    c->embed_scale = lef(h, 112);
+    c->attn_scale = lef(h, 116);
+    c->scale_f16 = (int)le32(h, 120);
+    c->attn_softcap = lef(h, 124);
+    c->final_softcap = lef(h, 128);
+
+    /* rules between fields */
+    if ((c->q8_mask & ~(unsigned)ML_Q8M_ALL) || (c->wtype == ML_Q8_0 && c->q8_mask))
+        return kr_seterr(ML_E_FORMAT, "q8_mask 0x%x with wtype %d", c->q8_mask, c->wtype);
+    if (c->dim % QK || c->hidden_dim % QK) return kr_seterr(ML_E_SHAPE, "dim and hidden_dim must be multiples of 32");
+    if (c->n_heads % c->n_kv_heads) return kr_seterr(ML_E_SHAPE, "n_kv_heads must divide n_heads");
+    if (!head_dim && c->dim % c->n_heads) return kr_seterr(ML_E_SHAPE, "n_heads must divide dim");
+    c->head_dim = head_dim ? head_dim : c->dim / c->n_heads;
+    if ((double)c->head_dim * c->n_heads > LIM_DIM) return kr_seterr(ML_E_SHAPE, "q_dim above 65536");
+    c->q_dim = c->head_dim * c->n_heads;
+    c->kv_dim = c->head_dim * c->n_kv_heads;
+    if (c->head_dim % 2 || c->q_dim % QK) return kr_seterr(ML_E_SHAPE, "odd head_dim or q_dim not a multiple of 32");
+    if (c->rope_type != ML_ROPE_YARN && c->rope_attn_factor != 0.0f)
+        return kr_seterr(ML_E_FORMAT, "rope_attn_factor without yarn scaling");
+    if (!rope_params_ok(c)) return kr_seterr(ML_E_FORMAT, "RoPE scaling parameters of rope_type %d", c->rope_type);
+
+    /* zeros that stand for defaults */
+    if (c->embed_scale == 0.0f) c->embed_scale = 1.0f;
+    if (c->attn_scale == 0.0f) c->attn_scale = 1.0f / sqrtf((float)c->head_dim);
+    return ML_OK;
+}
+
+/* ---- stage 3: the body plan ---- */
+
+typedef struct {
+    size_t bytes;
+    const void **dst;   /* receives the array's address */
+    int q8;             /* Q8 quants: no byte may be -128 */
+} plan_item;
+
+typedef struct {
+    plan_item *items;
+    int n, cap;
+} body_plan;
+
+static void plan_array(body_plan *p, const void *dst_field, size_t bytes, int q8) {
+    if (p->n < p->cap) p->items[p->n++] = (plan_item){ bytes, (const void **)dst_field, q8 };
+}
+
+/* storage type of a matrix class: Q8 when the model is, or when one of its
+ * q8_mask bits is set */
+static int class_type(const ml_config *c, unsigned bits) {
+    return c->wtype == ML_Q8_0 || (c->q8_mask & bits) ? ML_Q8_0 : ML_Q4_0;
+}
+
+/* a quantized matrix: its quants, then its scales (f32 or f16) */
+static void plan_matrix(body_plan *p, ml_qtensor *t, const ml_config *c, int rows, int cols, unsigned bits) {
+    const int type = class_type(c, bits);
+    const size_t n = (size_t)rows * (size_t)cols, nblocks = n / QK;
+    memset(t, 0, sizeof *t);
+    t->rows = rows;
+    t->cols = cols;
+    t->type = (uint8_t)type;
+    plan_array(p, &t->q, type == ML_Q4_0 ? n / 2 : n, type == ML_Q8_0);
+    if (c->scale_f16) plan_array(p, &t->dh, nblocks * 2, 0);
+    else plan_array(p, &t->d, nblocks * 4, 0);
+}
+
+static void plan_floats(body_plan *p, const float **dst, int n) { plan_array(p, dst, (size_t)n * sizeof(float), 0); }
+
+/* every array after the layer flags, in the order the specification lists
+ * them (docs/file-format.md:81-101) */
+static void plan_body(body_plan *p, kr_model *m) {
+    const ml_config *c = &m->cfg;
+    plan_matrix(p, &m->tok_emb, c, c->vocab, c->dim, ML_Q8M_EMB | (m->shared ? ML_Q8M_CLS : 0));
+    for (int l = 0; l < c->n_layers; l++) {
+        ml_layer *L = &m->layers[l];
+        plan_floats(p, &L->attn_norm, c->dim);
+        plan_matrix(p, &L->wq, c, c->q_dim, c->dim, ML_Q8M_QK);
+        plan_matrix(p, &L->wk, c, c->kv_dim, c->dim, ML_Q8M_QK);
+        plan_matrix(p, &L->wv, c, c->kv_dim, c->dim, ML_Q8M_V);
+        plan_matrix(p, &L->wo, c, c->dim, c->q_dim, ML_Q8M_O);
+        if (c->qkv_bias) {
+            plan_floats(p, &L->bq, c->q_dim);
+            plan_floats(p, &L->bk, c->kv_dim);
+            plan_floats(p, &L->bv, c->kv_dim);
+        }
+        if (c->qk_norm) {
+            plan_floats(p, &L->q_norm, c->head_dim);
+            plan_floats(p, &L->k_norm, c->head_dim);
+        }
+        plan_floats(p, &L->ffn_norm, c->dim);
+        plan_matrix(p, &L->w1, c, c->hidden_dim, c->dim, ML_Q8M_UP);
+        plan_matrix(p, &L->w2, c, c->dim, c->hidden_dim, ML_Q8M_DOWN);
+        plan_matrix(p, &L->w3, c, c->hidden_dim, c->dim, ML_Q8M_UP);
+        if (c->post_norms) {
+            plan_floats(p, &L->post_attn_norm, c->dim);
+            plan_floats(p, &L->post_ffn_norm, c->dim);
+        }
+    }
+    plan_floats(p, &m->final_norm, c->dim);
+    if (!m->shared) plan_matrix(p, &m->wcls, c, c->vocab, c->dim, ML_Q8M_CLS);
+}
+
+static size_t align_up(size_t off) { return (off + ML_ALIGN - 1) & ~(size_t)(ML_ALIGN - 1); }
+
+/* lays the plan out from byte `off` of the map: each array must lie within
+ * the file (the padding after the last one may be missing) */
+static ml_status lay_out(const body_plan *p, const uint8_t *map, size_t size, size_t off) {
+    for (int i = 0; i < p->n; i++) {
+        const plan_item *it = &p->items[i];
+        if (off > size || it->bytes > size - off)
+            return kr_seterr(ML_E_FORMAT, "file ends inside array %d of the body (%zu bytes at offset %zu)", i,
+                             it->bytes, off);
+        *it->dst = map + off;
+        if (it->q8 && memchr(map + off, 0x80, it->bytes))
+            return kr_seterr(ML_E_FORMAT, "a Q8 quant equal to -128 in array %d", i);
+        off = align_up(off + it->bytes);
+    }
+    return ML_OK;
+}
+
+/* ---- loading ---- */
+
+static ml_status map_file(const char *path, void **map, size_t *size) {
+    const int fd = open(path, O_RDONLY);
+    if (fd < 0) return kr_seterr(ML_E_IO, "cannot open %s", path);
+    struct stat st;
+    if (fstat(fd, &st) != 0 || !S_ISREG(st.st_mode)) {
+        close(fd);
+        return kr_seterr(ML_E_IO, "%s is not a readable file", path);
+    }
+    if (st.st_size < HEADER_BYTES) {
+        close(fd);
+        return kr_seterr(ML_E_FORMAT, "%s: %lld bytes, shorter than the header", path, (long long)st.st_size);
+    }
+    void *p = mmap(NULL, (size_t)st.st_size, PROT_READ, MAP_PRIVATE, fd, 0);
+    close(fd);
+    if (p == MAP_FAILED) return kr_seterr(ML_E_IO, "cannot map %s", path);
+    *map = p;
+    *size = (size_t)st.st_size;
+    return ML_OK;
+}
+
+static ml_status load(kr_model *m) {
+    ml_status s = kr_parse_header(&m->cfg, &m->shared, m->map);
+    if (s != ML_OK) return s;
+    const ml_config *c = &m->cfg;
+    const uint8_t *map = m->map;
+    m->layers = calloc((size_t)c->n_layers, sizeof(ml_layer));
+    if (!m->layers) return kr_seterr(ML_E_NOMEM, "layer table");
+
+    /* stage 2: one flag byte per layer; without them a window applies to
+     * every layer */
+    size_t off = HEADER_BYTES;
+    const uint8_t *flags = NULL;
+    if (c->layer_flags) {
+        if ((size_t)c->n_layers > m->size - off) return kr_seterr(ML_E_FORMAT, "file ends inside the layer flags");
+        flags = map + off;
+        off = align_up(off + (size_t)c->n_layers);
+        for (int l = 0; l < c->n_layers; l++) {
+            if (flags[l] & ~ML_LAYER_ALL) return kr_seterr(ML_E_FORMAT, "layer %d: unknown flag bits 0x%x", l, flags[l]);
+            if ((flags[l] & ML_LAYER_LOCAL_ROPE) && !(c->rope_local_theta > 0.0f))
+                return kr_seterr(ML_E_FORMAT, "layer %d: local RoPE without rope_local_theta", l);
+        }
+    }
+    for (int l = 0; l < c->n_layers; l++) {
+        m->layers[l].window = !flags || (flags[l] & ML_LAYER_SLIDING) ? c->sliding_window : 0;
+        m->layers[l].local_rope = flags && (flags[l] & ML_LAYER_LOCAL_ROPE);
+    }
+
+    /* stage 3 */
+    body_plan plan = { NULL, 0, 5 + 23 * c->n_layers };   /* tok_emb, final_norm, wcls; 23 arrays a layer at most */
+    plan.items = malloc(sizeof(plan_item) * (size_t)plan.cap);
+    if (!plan.items) return kr_seterr(ML_E_NOMEM, "body plan");
+    plan_body(&plan, m);
+    s = lay_out(&plan, map, m->size, off);
+    free(plan.items);
+    if (s != ML_OK) return s;
+    if (m->shared) m->wcls = m->tok_emb;
     return ML_OK;
 }
 
 ml_status kr_model_load(kr_model **out, const char *path) {
     *out = NULL;
-    const int fd = open(path, O_RDONLY);
-    if (fd < 0) return kr_seterr(ML_E_IO, "cannot open %s", path);
-    struct stat st;
-    if (fstat(fd, &st) != 0) { close(fd); return kr_seterr(ML_E_IO, "cannot stat %s", path); }
-    if (st.st_size < 256) { close(fd); return kr_seterr(ML_E_FORMAT, "%s: shorter than the header", path); }
-    void *map = mmap(NULL, (size_t)st.st_size, PROT_READ, MAP_PRIVATE, fd, 0);
-    close(fd);
-    if (map == MAP_FAILED) return kr_seterr(ML_E_IO, "cannot map %s", path);
     kr_model *m = calloc(1, sizeof *m);
-    if (!m) { munmap(map, (size_t)st.st_size); return ML_E_NOMEM; }
-    m->map = map;
-    m->size = (size_t)st.st_size;
-    int shared = 0;
-    ml_status s = kr_parse_header(&m->cfg, &shared, map);
-    if (s != ML_OK) { kr_model_free(m); return kr_seterr(s, "%s: bad header", path); }
-    const ml_config *c = &m->cfg;
-#define WT(bits) (c->wtype == ML_Q8_0 || (c->q8_mask & (bits)) ? ML_Q8_0 : ML_Q4_0)
-    m->layers = calloc((size_t)c->n_layers, sizeof(ml_layer));
-    if (!m->layers) { kr_model_free(m); return ML_E_NOMEM; }
-    cursor cur = { map, 256, m->size, 1 };
-    const size_t normsz = (size_t)c->dim * sizeof(float);
-    const uint8_t *lf = c->layer_flags ? take(&cur, (size_t)c->n_layers) : NULL;
-    for (int l = 0; lf && cur.ok && l < c->n_layers; l++)
-        if ((lf[l] & ~ML_LAYER_ALL) || ((lf[l] & ML_LAYER_LOCAL_ROPE) && !(c->rope_local_theta > 0.0f))) {
-            kr_model_free(m);
-            return kr_seterr(ML_E_FORMAT, "%s: bad layer flags", path);
-        }
-    m->tok_emb = take_mat(&cur, c->vocab, c->dim, WT(ML_Q8M_EMB | (shared ? ML_Q8M_CLS : 0)), c->scale_f16);
-    for (int l = 0; l < c->n_layers; l++) {
-        ml_layer *L = &m->layers[l];
-        L->window = !lf || (lf[l] & ML_LAYER_SLIDING) ? c->sliding_window : 0;
-        L->local_rope = lf && (lf[l] & ML_LAYER_LOCAL_ROPE);
-        L->attn_norm = take(&cur, normsz);
-        L->wq = take_mat(&cur, c->q_dim, c->dim, WT(ML_Q8M_QK), c->scale_f16);
-        L->wk = take_mat(&cur, c->kv_dim, c->dim, WT(ML_Q8M_QK), c->scale_f16);
-        L->wv = take_mat(&cur, c->kv_dim, c->dim, WT(ML_Q8M_V), c->scale_f16);
-        L->wo = take_mat(&cur, c->dim, c->q_dim, WT(ML_Q8M_O), c->scale_f16);
-        if (c->qkv_bias) {
-            L->bq = take(&cur, (size_t)c->q_dim * sizeof(float));
-            L->bk = take(&cur, (size_t)c->kv_dim * sizeof(float));
-            L->bv = take(&cur, (size_t)c->kv_dim * sizeof(float));
-        }
-        if (c->qk_norm) {
-            L->q_norm = take(&cur, (size_t)c->head_dim * sizeof(float));
-            L->k_norm = take(&cur, (size_t)c->head_dim * sizeof(float));
-        }
-        L->ffn_norm = take(&cur, normsz);
-        L->w1 = take_mat(&cur, c->hidden_dim, c->dim, WT(ML_Q8M_UP), c->scale_f16);
-        L->w2 = take_mat(&cur, c->dim, c->hidden_dim, WT(ML_Q8M_DOWN), c->scale_f16);
-        L->w3 = take_mat(&cur, c->hidden_dim, c->dim, WT(ML_Q8M_UP), c->scale_f16);
-        if (c->post_norms) {
-            L->post_attn_norm = take(&cur, normsz);
-            L->post_ffn_norm = take(&cur, normsz);
-        }
+    if (!m) return kr_seterr(ML_E_NOMEM, "model");
+    ml_status s = map_file(path, &m->map, &m->size);
+    if (s == ML_OK) s = load(m);
+    if (s != ML_OK) {
+        kr_model_free(m);
+        return s;
     }
-    m->final_norm = take(&cur, normsz);
-    m->shared = shared;
-    m->wcls = shared ? m->tok_emb : take_mat(&cur, c->vocab, c->dim, WT(ML_Q8M_CLS), c->scale_f16);
-#undef WT
-    if (!cur.ok) { kr_model_free(m); return kr_seterr(ML_E_FORMAT, "%s: truncated or bad tensor data", path); }
     *out = m;
     return ML_OK;
 }

@@ -107,9 +107,9 @@ def test_stories15m_shape_128_greedy(workdir):
 
 
 def test_device_generator_matches_host(workdir):
-    """the device generator draws the same streams as the host one: the
-    files agree byte for byte but for rare last-bit differences of the
-    device's double log/sin/cos, which may move a quant by one step"""
+    """the device generator draws the same streams as the host one and
+    evaluates them with the same arithmetic (csrc/kr_normal.h): the files
+    agree byte for byte"""
     spec = dict(K.CONFIGS["qwen05b_mixed"], dim=128, n_layers=2, n_heads=4, n_kv_heads=2, hidden_dim=256,
                 vocab=300, max_seq=64)
     a, b = os.path.join(workdir, "gen_host.mlb"), os.path.join(workdir, "gen_dev.mlb")
@@ -117,6 +117,6 @@ def test_device_generator_matches_host(workdir):
     K.gen_mlb(b, **dict(spec, device=1))
     x, y = np.fromfile(a, dtype=np.uint8), np.fromfile(b, dtype=np.uint8)
     assert x.size == y.size
-    assert np.count_nonzero(x != y) <= x.size // 100000 + 2
+    assert np.array_equal(x, y)
     m = K.Model(b)   # the loader accepts it
     m.close()
