@@ -13,27 +13,34 @@ positions 2047, 2048, ..., with the model and KV cache resident in HBM.
 
 Also reported on the same line:
   prefill_tok_s   prompt tokens per second of the 2047-token prefill
-  roofline        the dominant decode kernel (the fused w1/w3 SwiGLU matvec,
-                  54% of the weight bytes of a layer): algorithmic bytes per
-                  launch (weights + f16 scales of w1 and w3) over its average
-                  launch duration, timed with HIP events on the library
-                  stream around passes over all 32 layers (so the weights
-                  come from HBM and not from the 256 MB Infinity Cache)
-  matvec          the isolated Q4_0/Q8_0 matvec microbench (4096x4096 and
-                  14336x4096, f16 scales, activation quantize_q8(N(0,1))):
-                  GB/s over 1000 launches, cache-resident (one matrix) and
-                  HBM-rotating (copies totalling more than 1 GB)
+  roofline        the dominant decode kernel as the decode step issues it:
+                  the FFN rmsnorm + Q8_0 of x fused with the w1|w3 SwiGLU
+                  matvec (54% of a layer's weight bytes); algorithmic bytes
+                  per launch (weights + f16 scales of w1 and w3) over its
+                  average launch duration, timed with HIP events on the
+                  library stream around passes over all 32 layers (so the
+                  weights come from HBM and not from the 256 MB Infinity
+                  Cache); also against the measured plain HBM read rate (a
+                  read-only streaming kernel over 4 GiB)
   roofline.traffic  HBM bytes per launch of that kernel, from the committed
                   rocprofv3 --pmc summary (FETCH_SIZE and WRITE_SIZE per
                   dispatch, each scaled by what the counter reads for k_add
                   of known traffic); the command that made it is
                   `bench.py --roofline-only`, which runs just the timed
                   SwiGLU launches and the calibration launches
+  prefill_roofline  the dominant prefill kernel (the int8-MFMA matmul of w1
+                  over the 2047 prompt tokens): int8 TOP/s against the
+                  5.0 POP/s peak and against the exact-order VALU bound
+  matvec          the isolated Q4_0/Q8_0 matvec microbench (4096x4096 and
+                  14336x4096, f16 scales, activation quantize_q8(N(0,1))):
+                  GB/s over 1000 launches, cache-resident (one matrix) and
+                  HBM-rotating (copies totalling more than 1 GB)
   cpu_baseline    the reference's best CPU build (avx512vnni, else avx2,
                   THREADS=pthread, built from its sources into oracle/_ref)
-                  running ml_run on the same .mlb file on this host's cores,
-                  on a bounded sample of about 10 s: an 8-token prompt and
-                  256 greedy decode tokens
+                  running ml_run on the same .mlb file and the same prompt
+                  on this host's cores: the 2047-token prefill, then 32
+                  greedy decode tokens at positions 2047..2078, the positions
+                  the GPU decodes
 """
 import argparse
 import ctypes as C
@@ -87,30 +94,53 @@ def mat_bytes(W):
 
 
 def time_swiglu(K, model, state, reps):
-    """average duration (ms) of the decode step's SwiGLU launch -- w1|w3
-    matvec on the normalized, quantized input, SiLU(w1 x) * (w3 x) -- over
-    all layers, and its algorithmic bytes per launch: HIP events on the
-    library stream around each pass over the layers (back-to-back launches,
-    so the figure includes the gaps between them), divided by the launches"""
+    """average duration (ms) of the decode step's SwiGLU launch as the step
+    issues it -- the FFN rmsnorm of the residual stream x, its Q8_0
+    quantization and the w1|w3 matvec with SiLU(w1 x) * (w3 x), one fused
+    launch (krh_rmsnorm_matvec_swiglu) -- over all layers, and its
+    algorithmic bytes per launch: HIP events on the library stream around
+    each pass over the layers (back-to-back launches, so the figure includes
+    the gaps between them), divided by the launches"""
     cfg = model.cfg
-    xq = K.host.kr_state_buffer(state.ptr, b"qa_dim")
-    xd = K.host.kr_state_buffer(state.ptr, b"qd_dim")
+    x = K.host.kr_state_buffer(state.ptr, b"x")
     hb = K.host.kr_state_buffer(state.ptr, b"hb")
-    mats = [(K.host.kr_model_device_mat(model.ptr, l, b"w1"), K.host.kr_model_device_mat(model.ptr, l, b"w3"))
-            for l in range(cfg.n_layers)]
-    nbytes = mat_bytes(mats[0][0].contents) + mat_bytes(mats[0][1].contents)
+    layers = [(K.host.kr_model_device_mat(model.ptr, l, b"w1"), K.host.kr_model_device_mat(model.ptr, l, b"w3"),
+               K.host.kr_model_device_vec(model.ptr, l, b"ffn_norm")) for l in range(cfg.n_layers)]
+    nbytes = mat_bytes(layers[0][0].contents) + mat_bytes(layers[0][1].contents)
     t = K.hip.krh_timer_new()
     total, n = 0.0, 0
     for _ in range(reps):
         K.hip.krh_timer_mark(t, 0)
-        for w1, w3 in mats:
-            K.hip.krh_matvec_swiglu(hb, w1, w3, xq, xd)
+        for w1, w3, nw in layers:
+            K.hip.krh_rmsnorm_matvec_swiglu(hb, w1, w3, x, nw, cfg.norm_eps)
         K.hip.krh_timer_mark(t, 1)
         total += K.hip.krh_timer_ms(t)
-        n += len(mats)
+        n += len(layers)
     K.hip.krh_timer_free(t)
     K.check(K.hip.krh_sync(), "swiglu timing")
     return total / n, nbytes
+
+
+def hbm_read_peak(K, nbytes=4 << 30, reps=4):
+    """the plain HBM read rate (GB/s): the best of a few launch shapes of a
+    read-only streaming kernel (every 16-byte word of a 4 GiB buffer read
+    once), HIP events around each launch"""
+    buf, out = K.DevBuf(nbytes), K.DevBuf(4 * 65536)
+    t = K.hip.krh_timer_new()
+    best = 0.0
+    cus = K.hip.krh_device_cus()
+    for grid in (cus, 2 * cus, 8 * cus, 32 * cus, 64 * cus):
+        K.hip.krh_stream_read(out.ptr, buf.ptr, nbytes, grid)
+        for _ in range(reps):
+            K.hip.krh_timer_mark(t, 0)
+            K.hip.krh_stream_read(out.ptr, buf.ptr, nbytes, grid)
+            K.hip.krh_timer_mark(t, 1)
+            best = max(best, nbytes / (K.hip.krh_timer_ms(t) * 1e-3) / 1e9)
+    K.check(K.hip.krh_sync(), "stream read")
+    K.hip.krh_timer_free(t)
+    buf.free()
+    out.free()
+    return round(best, 1)
 
 
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "swiglu_matvec_traffic.json")
@@ -183,6 +213,53 @@ def matvec_microbench(K, iters=1000):
     for b in (xb, xq, xdb):
         b.free()
     return out
+
+
+def prefill_roofline(K, model, ntok, prefill_s, reps=2):
+    """the dominant prefill kernel: the int8-MFMA matmul of w1 (hidden x dim)
+    over ntok tokens, timed with HIP events over every layer's w1 on a random
+    quantized activation batch; int8 ops = 2 * rows * cols * ntok per launch,
+    against the 5.0 POP/s dense int8 peak and against the exact-order VALU
+    bound (4 unfused VALU operations -- cvt, mul, mul, add -- per output and
+    32-block, at 64 lanes x CUs x 2.4 GHz); plus the whole prefill's int8 ops
+    over its wall time (attention, norms and launches included)"""
+    cfg = model.cfg
+    T = ntok
+    ldx = (T + 127) // 128 * 128
+    w1 = [K.host.kr_model_device_mat(model.ptr, l, b"w1") for l in range(cfg.n_layers)]
+    rows, cols = w1[0].contents.rows, w1[0].contents.cols
+    rng = np.random.default_rng(7)
+    xq = K.DevBuf.of(rng.integers(-127, 128, ldx * cols).astype(np.int8))
+    xd = K.DevBuf.of(np.abs(rng.normal(0, 0.01, (cols // 32) * ldx)).astype(np.float32))
+    y = K.DevBuf(4 * T * rows)
+    t = K.hip.krh_timer_new()
+    K.hip.krh_matmul(y.ptr, rows, w1[0], xq.ptr, xd.ptr, ldx, T, 0)
+    total, n = 0.0, 0
+    for _ in range(reps):
+        K.hip.krh_timer_mark(t, 0)
+        for w in w1:
+            K.hip.krh_matmul(y.ptr, rows, w, xq.ptr, xd.ptr, ldx, T, 0)
+        K.hip.krh_timer_mark(t, 1)
+        total += K.hip.krh_timer_ms(t)
+        n += len(w1)
+    K.check(K.hip.krh_sync(), "matmul timing")
+    K.hip.krh_timer_free(t)
+    for b in (xq, xd, y):
+        b.free()
+    us = total / n * 1e3
+    ops = 2.0 * rows * cols * T
+    tops = ops / (us * 1e-6) / 1e12
+    valu_tops = 64 * K.hip.krh_device_cus() * 2.4e9 * (2 * 32 / 4) / 1e12   # int8 ops per exact-order VALU lane-op: 64 / 4
+    layer_ops = 0
+    for l in range(cfg.n_layers):
+        for wn in (b"wq", b"wk", b"wv", b"wo", b"w1", b"w2", b"w3"):
+            m = K.host.kr_model_device_mat(model.ptr, l, wn).contents
+            layer_ops += 2.0 * m.rows * m.cols
+    return {"bound": "valu (exact per-block rescale order)", "kernel": "k_matmul (w1, %dx%d, %d tokens)" % (rows, cols, T),
+            "achieved": round(tops, 1), "peak": 5000.0, "unit": "TOP/s", "frac": round(tops / 5000.0, 4),
+            "avg_launch_us": round(us, 1), "valu_bound": round(valu_tops, 1),
+            "frac_of_valu_bound": round(tops / valu_tops, 4),
+            "whole_prefill_int8_tops": round(layer_ops * T / prefill_s / 1e12, 1) if prefill_s else None}
 
 
 def cpu_baseline(path, prompt, decode, kv="f32", sample=None):
@@ -303,7 +380,11 @@ def main():
 
         ms, nbytes = time_swiglu(K, model, state, args.roofline_reps)
         gbs = nbytes / (ms * 1e-3) / 1e9
-        log("swiglu matvec: %.1f us per launch, %.1f GB/s" % (ms * 1e3, gbs))
+        log("rmsnorm + swiglu matvec: %.1f us per launch, %.1f GB/s" % (ms * 1e3, gbs))
+        hbm = hbm_read_peak(K)
+        log("plain HBM read rate: %.1f GB/s" % hbm)
+        pre_rl = prefill_roofline(K, model, P - 1, pre_s)
+        log("prefill matmul: %s" % json.dumps(pre_rl))
         cfg = model.cfg
         per_tok = 0
         for l in range(cfg.n_layers):
@@ -324,7 +405,7 @@ def main():
         cpu = None
         if not args.no_cpu_baseline:
             t0 = time.time()
-            cpu = cpu_baseline(path, prompt[:8], 256, args.kv, sample)
+            cpu = cpu_baseline(path, prompt, min(32, args.steps), args.kv, sample)
             log("cpu baseline (%.1f s): %s" % (time.time() - t0, json.dumps(cpu)))
         state.close()
         model.close()
@@ -346,11 +427,15 @@ def main():
         "prefill_tok_s": round(prefill_tok_s, 2) if prefill_tok_s else None,
         "decode_frac_of_hbm_roofline": round(tok_s * (per_tok + kv_tok) / (HBM_PEAK_GBS * 1e9), 4),
         "deterministic_ids": deterministic,
-        "roofline": {"bound": "hbm", "kernel": "k_matvec<EPI_SWIGLU> (w1|w3 rows, SiLU(w1 x) * (w3 x))",
+        "roofline": {"bound": "hbm",
+                     "kernel": "k_matvec<EPI_SWIGLU> with the rmsnorm prologue (krh_rmsnorm_matvec_swiglu: FFN "
+                               "rmsnorm + Q8_0 of x, w1|w3 rows, SiLU(w1 x) * (w3 x)), as the decode step issues it",
                      "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4),
                      "traffic": traffic["bytes_per_launch"] if traffic else None,
-                     "bytes_per_launch": nbytes, "avg_launch_us": round(ms * 1e3, 2)},
+                     "bytes_per_launch": nbytes, "avg_launch_us": round(ms * 1e3, 2),
+                     "measured_read_peak": hbm, "frac_of_measured_read_peak": round(gbs / hbm, 4)},
+        "prefill_roofline": pre_rl,
         "matvec": mv,
         "cpu_baseline": cpu,
     }

@@ -41,9 +41,10 @@ void kr_model_free(kr_model *m);
 
 /* ---- decoding state (KV cache and activations in HBM) ---- */
 typedef struct kr_state kr_state;
-/* kv_type: ML_F32, ML_F16 or ML_Q8_0 (ml_state_init, model/transformer.c:51-56).
- * ML_E_SHAPE for model features this backend does not run (q/k norm,
- * post-norms, GELU, soft-capping). */
+/* kv_type: ML_F32, ML_F16 or ML_Q8_0 (ml_state_init, model/transformer.c:51-56);
+ * ML_E_SHAPE for any other type, ML_E_NOMEM when HBM runs out. Every model
+ * the loader accepts runs: models with q/k-norm, post-norms, GELU or
+ * soft-capping take the unfused layer path. */
 ml_status kr_state_new(kr_state **s, kr_model *m, int kv_type);
 void kr_state_free(kr_state *s);
 /* ml_forward: logits of token at pos into logits[vocab] (host memory) */

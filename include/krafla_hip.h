@@ -43,6 +43,8 @@ typedef struct krh_graph krh_graph;
  * counterpart of ml_isa_check, core/isa_check.h:8-9). Idempotent. */
 ml_status krh_init(void);
 const char *krh_device_arch(void);
+/* compute units of device 0 (0 before krh_init) */
+int krh_device_cus(void);
 /* ML_OK, or the first error since the last krh_clear_error() */
 ml_status krh_status(void);
 const char *krh_last_error(void);
@@ -255,6 +257,10 @@ uint64_t krh_sampler_rng(const krh_sampler *s);
  * order, on device pointers. */
 void krh_rmsnorm(float *o, const float *x, const float *w, int n, float eps);         /* :59-64, n <= 16384 */
 void krh_add(float *y, const float *x, int n);                                          /* :107-109 */
+/* Measurement op (no reference counterpart): reads the `bytes` (a multiple of
+ * 16) at p once with `grid` workgroups; out[grid] receives an XOR fold of
+ * each workgroup's words. Times the plain HBM read rate. */
+void krh_stream_read(unsigned *out, const void *p, size_t bytes, int grid);
 void krh_rope(float *q, float *k, const float *cos_t, const float *sin_t, int head_dim, int n_heads,
               int n_kv_heads);                                                           /* :79-94 */
 void krh_silu_mul(float *g, const float *u, int n);                                     /* :96-98 */
@@ -275,11 +281,6 @@ void krh_transpose_scales(float *dT, int ldx, const float *d, int n, int nb);
  * quantized per 32-block by the .mlb writer rules; q: rows*cols (Q8) or
  * rows*cols/2 bytes, d: rows*cols/32 scales, f16 when f16 != 0. */
 void krh_gen_blocks(void *q, void *d, uint64_t key, int rows, int cols, int type, int f16, float std);
-
-/* ---- tuning ---- */
-/* KRH_TUNE_MV_ROWS: rows per matvec workgroup (0 = the built-in choice) */
-enum { KRH_TUNE_MV_ROWS = 1 };
-void krh_tune(int key, int value);
 
 /* ---- self-checks for tests ---- */
 /* y[i] = op(a[i], b[i]) as the kernels compute it: expf(a), sqrtf(a), a / b,

@@ -57,6 +57,7 @@ constexpr int MV_DEPTH = 2;    // work items in flight per wave: a wave that iss
                                // memory pipeline holds stalls at issue
 constexpr int MV_XQ_MAX = 16384;   // quantized activations up to this length are staged from registers
 constexpr int MV_XF_MAX = 8192;    // float activations up to this length are normalized and quantized from registers
+constexpr int MV_XF_PLAIN_MAX = 16384;   // float activations without a norm: quantized from registers up to this length
 
 template <typename T> __device__ __forceinline__ T pick3(int i, T a, T b, T c) { return i == 0 ? a : (i == 1 ? b : c); }
 
@@ -91,7 +92,8 @@ __device__ __forceinline__ int block_dot(const int4 w0, const int4 w1, const int
 // lanes hold a 32-block (all 8 must call together); the block max is exact in
 // any order. q[i..i+3] receive the values, d[(i / 32) * dstep] the scale.
 __device__ __forceinline__ void kr_quant4(float4 v, int i, int8_t *q, float *d, size_t dstep) {
-    float m = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+    // seeded with 0 as the reference's loop is: NaNs never raise the max
+    float m = fmaxf(fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))), 0.0f);
     m = fmaxf(m, __shfl_xor(m, 1, 8));
     m = fmaxf(m, __shfl_xor(m, 2, 8));
     m = fmaxf(m, __shfl_xor(m, 4, 8));
@@ -338,6 +340,21 @@ __global__ void __launch_bounds__(MV_THREADS, 2) k_matvec(const MvArgs a) {
             if (tid + k * MV_THREADS < nb) xds[tid + k * MV_THREADS] = xdv[k];
 #pragma unroll
         for (int d = 0; d < MV_DEPTH - 1; d++) load_item(S[d], I[d]);
+    } else if (!a.xq && !a.nw && K <= MV_XF_PLAIN_MAX) {
+        // a float activation without a norm (ao before wo, h before w2): its
+        // loads go out first, then the first item's weight loads, and the
+        // quantization waits on the activation alone
+        constexpr int XV = MV_XF_PLAIN_MAX / 4 / MV_THREADS;
+        float4 xv[XV];
+#pragma unroll
+        for (int k = 0; k < XV; k++) xv[k] = *(const float4 *)(a.xf + min(4 * (k * MV_THREADS + tid), K - 4));
+#pragma unroll
+        for (int d = 0; d < MV_DEPTH - 1; d++) load_item(S[d], I[d]);
+#pragma unroll
+        for (int k = 0; k < XV; k++) {
+            const int i = 4 * (k * MV_THREADS + tid);   // K % 32 == 0: 8-lane groups all in or all out
+            if (i < K) kr_quant4(xv[k], i, xs, xds, 1);
+        }
     } else if (!a.xq && K <= MV_XF_MAX) {
         // a float activation (normalized first when nw is set), held in
         // registers: its loads go out before the weight loads; the squares
@@ -525,17 +542,15 @@ constexpr int MV_RESIDENT = 512;
 // the RoPE pairs) that still gives every resident wave a tile; blocks per
 // chunk: as many as MV_NPT slots per lane allow (a multiple of 4, for the
 // 16-byte term reads).
-int g_mv_rows_override = 0;   // krh_tune(KRH_TUNE_MV_ROWS, R): fixed rows per tile
 constexpr int MV_MIN_TILES = MV_RESIDENT * MV_WAVES;
 constexpr int MV_MAX_LOC = 8;   // local rows per tile: a row's chunk then spans >= 32 blocks (1 KB of Q8_0)
 
 int mv_rows(int K, int total_rows, int local_per_row, int cap) {
     (void)K;
-    int R = g_mv_rows_override > 0 ? g_mv_rows_override : cap / local_per_row;
+    int R = cap / local_per_row;
     if (R * local_per_row > 64) R = 64 / local_per_row;
-    if (g_mv_rows_override <= 0 && R * local_per_row > MV_MAX_LOC) R = MV_MAX_LOC / local_per_row;
-    if (g_mv_rows_override <= 0)
-        while (R > 2 && (total_rows + R - 1) / R < MV_MIN_TILES) R /= 2;
+    if (R * local_per_row > MV_MAX_LOC) R = MV_MAX_LOC / local_per_row;
+    while (R > 2 && (total_rows + R - 1) / R < MV_MIN_TILES) R /= 2;
     if (R > 1) R &= ~1;
     return R < 1 ? 1 : R;
 }
@@ -592,7 +607,7 @@ __global__ void __launch_bounds__(256) k_quantize_q8(int8_t *q, float *d, int dl
     const int i = blockIdx.x * QZ_CHUNK + 4 * threadIdx.x;
     if (i >= n) return;   // n % 32 == 0: 8-thread groups are all in or all out
     const float4 v = *(const float4 *)(x + row * n + i);
-    float m = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+    float m = fmaxf(fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))), 0.0f);   // seeded with 0
     m = fmaxf(m, __shfl_xor(m, 1, 8));
     m = fmaxf(m, __shfl_xor(m, 2, 8));
     m = fmaxf(m, __shfl_xor(m, 4, 8));
@@ -819,10 +834,6 @@ static void mv_plain(float *y, const krh_mat *W, const int8_t *xq, const float *
     else launch_mv<EPI_STORE>(a, a.m[0]);
 }
 
-extern "C" void krh_tune(int key, int value) {
-    if (key == KRH_TUNE_MV_ROWS) g_mv_rows_override = value;
-}
-
 extern "C" void krh_matvec(float *y, const krh_mat *W, const int8_t *xq, const float *xd, int accumulate) {
     mv_plain(y, W, xq, xd, nullptr, nullptr, 0.0f, accumulate);
 }
@@ -933,7 +944,7 @@ static void swiglu(float *h, const krh_mat *w1, const krh_mat *w3, const int8_t 
     a.m[0] = to_kmat(w1);
     a.m[1] = to_kmat(w3);
     a.nmat = 1;
-    a.R = mv_rows(w1->cols, w1->rows, 2, 64);
+    a.R = mv_rows(w1->cols, w1->rows, 2, 4);   // 2 rows of w1 and w3 a tile: measured fastest
     a.tile0[0] = 0;
     a.tile0[1] = (w1->rows + a.R - 1) / a.R;
     a.xq = xq;

@@ -200,7 +200,7 @@ __device__ __forceinline__ float kr_max32(float v) {
 // Quantizes the 32 values held by the 32 lanes of a half-wave (lane j holds
 // element j of the block) into q (this lane's element) and the block scale.
 __device__ __forceinline__ void kr_quant_block32(float x, int8_t *q, float *d) {
-    const float amax = kr_max32(fabsf(x));
+    const float amax = fmaxf(kr_max32(fabsf(x)), 0.0f);   // seeded with 0: NaNs never raise it
     if (amax < KR_QUANT_TINY) {
         *q = 0;
         *d = 0.0f;

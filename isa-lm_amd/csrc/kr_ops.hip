@@ -156,6 +156,41 @@ extern "C" void krh_rmsnorm(float *o, const float *x, const float *w, int n, flo
     hipLaunchKernelGGL(k_rmsnorm, dim3(1), dim3(OP_T), sizeof(float) * (size_t)n, kr_stream(), o, x, w, n, eps);
     kr_check_launch("rmsnorm");
 }
+// Plain HBM read rate (a measurement op): every 16-byte word of p read once,
+// UNROLL loads in flight per thread, XOR-folded into one word per workgroup
+// (out[blockIdx.x]) so that no load is dropped.
+constexpr int SR_T = 256, SR_UNROLL = 8;
+__global__ void __launch_bounds__(SR_T) k_stream_read(unsigned *out, const int4 *p, size_t n16) {
+    __shared__ unsigned red[SR_T / 64];
+    const size_t stride = (size_t)gridDim.x * SR_T;
+    size_t i = (size_t)blockIdx.x * SR_T + threadIdx.x;
+    unsigned acc = 0;
+    for (; i + (SR_UNROLL - 1) * stride < n16; i += SR_UNROLL * stride) {
+        int4 v[SR_UNROLL];
+#pragma unroll
+        for (int k = 0; k < SR_UNROLL; k++) v[k] = p[i + k * stride];
+#pragma unroll
+        for (int k = 0; k < SR_UNROLL; k++) acc ^= (unsigned)(v[k].x ^ v[k].y ^ v[k].z ^ v[k].w);
+    }
+    for (; i < n16; i += stride) {
+        const int4 v = p[i];
+        acc ^= (unsigned)(v.x ^ v.y ^ v.z ^ v.w);
+    }
+    for (int o = 32; o >= 1; o >>= 1) acc ^= __shfl_xor(acc, o);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = acc;
+    __syncthreads();
+    if (threadIdx.x == 0) out[blockIdx.x] = red[0] ^ red[1] ^ red[2] ^ red[3];
+}
+
+extern "C" void krh_stream_read(unsigned *out, const void *p, size_t bytes, int grid) {
+    if (bytes % 16 || grid <= 0 || ((uintptr_t)p & 15)) {
+        kr_fail(ML_E_SHAPE, "stream_read: 16-byte aligned bytes and a positive grid", hipSuccess);
+        return;
+    }
+    hipLaunchKernelGGL(k_stream_read, dim3(grid), dim3(SR_T), 0, kr_stream(), out, (const int4 *)p, bytes / 16);
+    kr_check_launch("stream_read");
+}
+
 extern "C" void krh_add(float *y, const float *x, int n) {
     if (n <= 0) return;
     hipLaunchKernelGGL(k_add, dim3(blocks(n)), dim3(OP_T), 0, kr_stream(), y, x, n);

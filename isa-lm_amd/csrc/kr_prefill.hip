@@ -277,7 +277,7 @@ __global__ void __launch_bounds__(256) k_silu_quant(int8_t *q, float *dT, int ld
     v.y = kr_fmul(kr_fdiv(gv.y, kr_fadd(1.0f, kr_expf(-gv.y))), uv.y);
     v.z = kr_fmul(kr_fdiv(gv.z, kr_fadd(1.0f, kr_expf(-gv.z))), uv.z);
     v.w = kr_fmul(kr_fdiv(gv.w, kr_fadd(1.0f, kr_expf(-gv.w))), uv.w);
-    float m = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+    float m = fmaxf(fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))), 0.0f);   // seeded with 0
     m = fmaxf(m, __shfl_xor(m, 1, 8));
     m = fmaxf(m, __shfl_xor(m, 2, 8));
     m = fmaxf(m, __shfl_xor(m, 4, 8));

@@ -8,6 +8,7 @@
 static int g_ready = 0;
 static hipStream_t g_stream = nullptr;
 static char g_arch[64] = "";
+static int g_cus = 0;
 static ml_status g_status = ML_OK;
 static char g_msg[512] = "";
 
@@ -37,6 +38,7 @@ extern "C" ml_status krh_init(void) {
         return ML_E_ISA;
     }
     snprintf(g_arch, sizeof g_arch, "%s", p.gcnArchName);
+    g_cus = p.multiProcessorCount;
     if (strncmp(p.gcnArchName, "gfx950", 6) != 0) {
         snprintf(g_msg, sizeof g_msg, "device 0 is %s, this build needs gfx950", p.gcnArchName);
         return ML_E_ISA;
@@ -50,6 +52,7 @@ extern "C" ml_status krh_init(void) {
 }
 
 extern "C" const char *krh_device_arch(void) { return g_arch; }
+extern "C" int krh_device_cus(void) { return g_cus; }
 extern "C" ml_status krh_status(void) { return g_status; }
 extern "C" const char *krh_last_error(void) { return g_msg; }
 extern "C" void krh_clear_error(void) { g_status = ML_OK; g_msg[0] = 0; }

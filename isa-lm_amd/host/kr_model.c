@@ -5,7 +5,7 @@
  * One decode step (model/transformer.c:257-306), per layer:
  *   rmsnorm+quantize(attn_norm) -> q,k,v matvec + bias + RoPE + cache write
  *   -> attention -> x += wo.q8(ao) -> rmsnorm+quantize(ffn_norm)
- *   -> silu(w1.x) * (w3.x) -> quantize h -> x += w2.h
+ *   -> silu(w1.x) * (w3.x) -> x += w2.q8(h)
  * then rmsnorm+quantize(final_norm) -> logits = wcls.x. Every op reads the
  * token and position from device memory, so the captured step replays for
  * any position without new arguments. */
@@ -326,8 +326,7 @@ static void issue_step(kr_state *s, int cls) {
         }
         krh_matvec_f(s->x, &D->wo, s->ao, 1);
         krh_rmsnorm_matvec_swiglu(s->hb, &D->w1, &D->w3, s->x, D->ffn_norm, c->norm_eps);
-        krh_quantize_q8(s->qa_hid, s->qd_hid, s->hb, c->hidden_dim, 1);
-        krh_matvec(s->x, &D->w2, s->qa_hid, s->qd_hid, 1);
+        krh_matvec_f(s->x, &D->w2, s->hb, 1);   /* h quantized in the w2 launch's prologue */
     }
     if (!cls) return;
     krh_rmsnorm_matvec(s->logits, &m->d_wcls, s->x, m->d_final_norm, c->norm_eps, 0);
@@ -378,13 +377,12 @@ static void issue_family_layer(kr_state *s, int l, const float *cs, const float 
     } else {
         krh_rmsnorm_matvec_swiglu(s->hb, &D->w1, &D->w3, s->x, D->ffn_norm, c->norm_eps);
     }
-    krh_quantize_q8(s->qa_hid, s->qd_hid, s->hb, c->hidden_dim, 1);
     if (D->post_ffn_norm) {
-        krh_matvec(s->yb, &D->w2, s->qa_hid, s->qd_hid, 0);
+        krh_matvec_f(s->yb, &D->w2, s->hb, 0);
         krh_rmsnorm(s->yb, s->yb, D->post_ffn_norm, c->dim, c->norm_eps);
         krh_add(s->x, s->yb, c->dim);
     } else {
-        krh_matvec(s->x, &D->w2, s->qa_hid, s->qd_hid, 1);
+        krh_matvec_f(s->x, &D->w2, s->hb, 1);
     }
 }
 

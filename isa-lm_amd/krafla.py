@@ -131,6 +131,7 @@ host = _Lib(LIB_HOST)
 _P = C.c_void_p
 for name, res, args in [
     ("krh_init", C.c_int, []), ("krh_device_arch", C.c_char_p, []), ("krh_status", C.c_int, []),
+    ("krh_device_cus", C.c_int, []), ("krh_stream_read", None, [_P, _P, C.c_size_t, C.c_int]),
     ("krh_last_error", C.c_char_p, []), ("krh_clear_error", None, []),
     ("krh_alloc", _P, [C.c_size_t]), ("krh_free", None, [_P]),
     ("krh_host_alloc", _P, [C.c_size_t]), ("krh_host_free", None, [_P]),
@@ -187,7 +188,6 @@ for name, res, args in [
     ("krh_take_token", None, [_P, _P, _P]), ("krh_advance", None, [_P]),
     ("krh_math_batch", None, [C.c_int, _P, _P, _P, C.c_size_t]), ("krh_h2f_batch", None, [_P, _P, C.c_size_t]),
     ("krh_block_dots", None, [_P, C.POINTER(KrhMat), _P]), ("krh_ordered_sum", None, [_P, _P, C.c_int, C.c_float]),
-    ("krh_tune", None, [C.c_int, C.c_int]),
     ("krh_rmsnorm", None, [_P, _P, _P, C.c_int, C.c_float]), ("krh_add", None, [_P, _P, C.c_int]),
     ("krh_rope", None, [_P, _P, _P, _P, C.c_int, C.c_int, C.c_int]),
     ("krh_silu_mul", None, [_P, _P, C.c_int]), ("krh_gelu_mul", None, [_P, _P, C.c_int]),

@@ -130,6 +130,9 @@ def test_quantize(dev, n, ntok):
         x[32:64] = [1e-37 if i % 2 else -2e-37 for i in range(32)]
         x[64:96] = 0.0
         x[64:70] = [127.0, 0.5, -0.5, 1.5, 2.5, -2.5]
+    if n >= 160:   # an all-NaN block (max seeded with 0: scale 0, quants 0) and a half-NaN one
+        x[96:128] = np.nan
+        x[128:160:2] = np.nan
     xb, qb, db = dev.put(x), dev.zeros(n * ntok), dev.zeros(4 * n * ntok // 32)
     K.hip.krh_quantize_q8(qb.ptr, db.ptr, xb.ptr, n, ntok)
     ok()
@@ -211,6 +214,8 @@ def test_matvec_accumulate(dev):
 @pytest.mark.parametrize("n,ntok", [(288, 1), (4096, 1), (896, 3)])
 def test_rmsnorm_q8(dev, n, ntok):
     x = f32(RNG.normal(0, 2, n * ntok))
+    if ntok > 1:
+        x[n + 5] = np.nan   # token 1: a NaN sum, every block all-NaN
     w = f32(RNG.normal(1, 0.1, n))
     qb, db, ob = dev.zeros(n * ntok), dev.zeros(4 * n * ntok // 32), dev.zeros(4 * n * ntok)
     K.hip.krh_rmsnorm_q8(qb.ptr, db.ptr, ob.ptr, dev.put(x).ptr, dev.put(w).ptr, n, 1e-5, ntok)
@@ -220,7 +225,9 @@ def test_rmsnorm_q8(dev, n, ntok):
         xt = f32(x[t * n:(t + 1) * n])
         oracle.kro_rmsnorm(o.ctypes.data, xt.ctypes.data, w.ctypes.data, n, C.c_float(1e-5))
         q0, d0 = O.quantize(o)
-        assert np.array_equal(bits(ob.get(np.float32, n * ntok)[t * n:(t + 1) * n]), bits(o))
+        got_o = ob.get(np.float32, n * ntok)[t * n:(t + 1) * n]
+        assert np.array_equal(np.isnan(got_o), np.isnan(o))
+        assert np.array_equal(bits(got_o[~np.isnan(o)]), bits(o[~np.isnan(o)]))
         assert np.array_equal(qb.get(np.int8, n * ntok)[t * n:(t + 1) * n], q0)
         assert np.array_equal(bits(db.get(np.float32, n * ntok // 32)[t * n // 32:(t + 1) * n // 32]), bits(d0))
 
@@ -559,6 +566,8 @@ def test_attention_batch_matches_decode(dev, nh, nkv, hd, pos0, T, window):
 def test_silu_quant(dev):
     n, T = 4864, 9
     g, u = f32(RNG.normal(0, 3, (T, n))), f32(RNG.normal(0, 1, (T, n)))
+    g[2, :32] = np.nan   # an all-NaN block
+    u[3, 40] = np.nan    # one NaN in a block
     ldx = 128
     qb, db = dev.zeros(T * n), dev.zeros(4 * (n // 32) * ldx)
     K.hip.krh_silu_quant(qb.ptr, db.ptr, ldx, dev.put(g).ptr, dev.put(u).ptr, n, T)
