@@ -140,6 +140,17 @@ void krh_rmsnorm_matvec_qkv_stage(float *q, float *k, float *v, const krh_mat *w
  * == 0, at most 16 query heads per KV head. */
 void krh_attention(float *ao, int8_t *aq, float *ad, float *att, const float *q, const float *kc, const float *vc,
                    int n_heads, int n_kv_heads, int head_dim, int max_seq, int window, float scale, const int *pos);
+/* krh_attention without the att workspace and without the quantized copy:
+ * the score rows live in a static device array of KRH_ATTN_SCRATCH_FLOATS
+ * floats per device, so the call allocates nothing (no hipMalloc, no
+ * library allocation). No counterpart in the reference: it is for callers
+ * that cannot allocate (code under graph capture, serving loops that forbid
+ * allocation). n_heads * max_seq must not exceed KRH_ATTN_SCRATCH_FLOATS
+ * (ML_E_SHAPE otherwise). Calls that overlap on one device race on the
+ * array. Results equal krh_attention's bit for bit. */
+#define KRH_ATTN_SCRATCH_FLOATS (1 << 21)
+void krh_attention_noalloc(float *ao, const float *q, const float *kc, const float *vc, int n_heads, int n_kv_heads,
+                           int head_dim, int max_seq, int window, float scale, const int *pos);
 /* The same over one layer's cache of any type (ml_attention, ops/ops.c:124-180):
  * kv (a host struct of device pointers, ops/ops.h:16-22) names the layer's F32
  * rows (k, v), F16 rows (kh, vh) or Q8 rows and row scales (kq, vq, kd, vd),

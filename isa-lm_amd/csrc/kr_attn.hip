@@ -750,6 +750,49 @@ extern "C" void krh_attention(float *ao, int8_t *aq, float *ad, float *att, cons
     if (aq) krh_quantize_q8(aq, ad, ao, n_heads * head_dim, 1);
 }
 
+// ---- decode attention without a workspace argument ----
+//
+// The score rows live in one file-scope device array, `scratch`, of
+// KRH_ATTN_SCRATCH_FLOATS floats (8 MiB), which each device holds for the
+// life of the process. Host code never passes the array's name to a kernel
+// (on the host it only names a stand-in): its device address, one per device,
+// comes from hipGetSymbolAddress at set-up (kr_attn_setup, from krh_init).
+// Every call on a device shares that device's array, so calls that overlap on
+// one device race. No entry of it needs clearing: each call writes every
+// score row entry it reads back.
+static __device__ __align__(256) float scratch[KRH_ATTN_SCRATCH_FLOATS];
+static float *g_scratch_ptr[KR_MAX_DEVICES];
+
+ml_status kr_attn_setup(int dev) {
+    if (dev < 0 || dev >= KR_MAX_DEVICES) return ML_E_ISA;
+    if (g_scratch_ptr[dev]) return ML_OK;
+    void *ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr) {
+        kr_fail(ML_E_ISA, "hipGetSymbolAddress(scratch)", e);
+        return ML_E_ISA;
+    }
+    g_scratch_ptr[dev] = (float *)ptr;
+    return ML_OK;
+}
+
+extern "C" void krh_attention_noalloc(float *ao, const float *q, const float *kc, const float *vc, int n_heads,
+                                      int n_kv_heads, int head_dim, int max_seq, int window, float scale,
+                                      const int *pos) {
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= KR_MAX_DEVICES || !g_scratch_ptr[dev]) {
+        kr_fail(ML_E_ISA, "attention_noalloc: the device's scratch address is not set up (krh_init)", hipSuccess);
+        return;
+    }
+    if (n_heads <= 0 || max_seq <= 0 || (size_t)n_heads * (size_t)max_seq > (size_t)KRH_ATTN_SCRATCH_FLOATS) {
+        kr_fail(ML_E_SHAPE, "attention_noalloc: n_heads * max_seq exceeds the static scratch of "
+                            "KRH_ATTN_SCRATCH_FLOATS floats", hipSuccess);
+        return;
+    }
+    attention<KV_F32>(ao, g_scratch_ptr[dev], q, f32_view(kc, vc), n_heads, n_kv_heads, head_dim, max_seq, window,
+                      scale, pos, 1, max_seq - 1);
+}
+
 extern "C" void krh_attention_batch(float *ao, float *att, const float *q, const float *kc, const float *vc,
                                     int n_heads, int n_kv_heads, int head_dim, int max_seq, int window, float scale,
                                     const int *pos0, int ntok, int last_pos) {

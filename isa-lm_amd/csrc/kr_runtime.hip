@@ -43,6 +43,10 @@ extern "C" ml_status krh_init(void) {
         snprintf(g_msg, sizeof g_msg, "device 0 is %s, this build needs gfx950", p.gcnArchName);
         return ML_E_ISA;
     }
+    if (kr_attn_setup(0) != ML_OK) {
+        snprintf(g_msg, sizeof g_msg, "cannot take the address of the attention scratch array");
+        return ML_E_ISA;
+    }
     if (hipStreamCreateWithFlags(&g_stream, hipStreamNonBlocking) != hipSuccess) {
         snprintf(g_msg, sizeof g_msg, "cannot create a stream");
         return ML_E_ISA;
