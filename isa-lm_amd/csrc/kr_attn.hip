@@ -18,7 +18,8 @@ namespace {
 // out_i += a_t v_t,i in position order (k_scalar.c:119-122). The ordered
 // chains run from LDS; the loads feeding them are wide and parallel.
 
-constexpr int AT_T = 64;          // positions per score tile
+constexpr int AT_T = 64;          // positions per score tile of a batched (prefill) launch
+constexpr int AT_TD = 16;         // of a decode launch: more, smaller tiles hide the K loads better
 constexpr int AT_THREADS = 256;
 
 // positions attended by token blockIdx.z of the launch, at position *pos_p + blockIdx.z
@@ -66,12 +67,12 @@ template <> struct Kv4<KV_Q8> {
     }
 };
 
-// Scores of one KV head's query heads for AT_T positions. The K tile is staged
+// Scores of one KV head's query heads for TT positions. The K tile is staged
 // in LDS as floats (F16 rows widened exactly, k_scalar.c:124-129), rows hd + 4
 // floats apart so that the 16-byte reads of 8 consecutive lanes cover all
 // banks once; thread (t, j) computes heads j, j + 4, ... of the group for
 // position t, adding the products in index order.
-template <int KT>
+template <int KT, int TT>
 __device__ __forceinline__ void attn_scores(float *att, const float *q, const KvView kv, int group, int hd, int kv_dim,
                                             int max_seq, int window, float scale, const int *pos_p) {
     extern __shared__ __align__(16) float at_smem[];
@@ -79,9 +80,9 @@ __device__ __forceinline__ void attn_scores(float *att, const float *q, const Kv
     attn_range(pos_p, window, &first, &n);
     att += (size_t)blockIdx.z * gridDim.x * group * max_seq;   // token z: [n_heads][max_seq]
     q += (size_t)blockIdx.z * gridDim.x * group * hd;
-    const int g = blockIdx.x, t0 = blockIdx.y * AT_T, tid = threadIdx.x;
+    const int g = blockIdx.x, t0 = blockIdx.y * TT, tid = threadIdx.x;
     if (t0 >= n) return;
-    const int nt = min(AT_T, n - t0), ks = hd + 4, h4 = hd / 4;
+    const int nt = min(TT, n - t0), ks = hd + 4, h4 = hd / 4;
     float *qs = at_smem, *kt = at_smem + group * hd;
     const float4 *qg = (const float4 *)(q + (size_t)g * group * hd);
     for (int i = tid; i < group * h4; i += AT_THREADS) ((float4 *)qs)[i] = qg[i];
@@ -91,10 +92,10 @@ __device__ __forceinline__ void attn_scores(float *att, const float *q, const Kv
             Kv4<KT>::wide(Kv4<KT>::load(kv.k, (size_t)(first + t0 + r) * kv_dim + (size_t)g * hd + 4 * c));
     }
     __syncthreads();
-    const int t = tid % AT_T;
+    const int t = tid % TT;
     if (t >= nt) return;
     const float *kr = kt + t * ks;
-    for (int j = tid / AT_T; j < group; j += AT_THREADS / AT_T) {
+    for (int j = tid / TT; j < group; j += AT_THREADS / TT) {
         const float *qh = qs + j * hd;
         float acc = 0.0f;
 #pragma unroll 4
@@ -110,18 +111,19 @@ __device__ __forceinline__ void attn_scores(float *att, const float *q, const Kv
 }
 
 // the F32 cache (its own argument list: the view is built on the device)
+template <int TT>
 __global__ void __launch_bounds__(AT_THREADS) k_attn_scores(float *att, const float *q, const float *kc, int group,
                                                             int hd, int kv_dim, int max_seq, int window, float scale,
                                                             const int *pos_p) {
     const KvView kv = { kc, nullptr, nullptr, nullptr, 0 };
-    attn_scores<KV_F32>(att, q, kv, group, hd, kv_dim, max_seq, window, scale, pos_p);
+    attn_scores<KV_F32, TT>(att, q, kv, group, hd, kv_dim, max_seq, window, scale, pos_p);
 }
 
 template <int KT>
 __global__ void __launch_bounds__(AT_THREADS) k_attn_scores_kv(float *att, const float *q, const KvView kv, int group,
                                                                int hd, int kv_dim, int max_seq, int window, float scale,
                                                                const int *pos_p) {
-    attn_scores<KT>(att, q, kv, group, hd, kv_dim, max_seq, window, scale, pos_p);
+    attn_scores<KT, AT_T>(att, q, kv, group, hd, kv_dim, max_seq, window, scale, pos_p);
 }
 
 // Scores over the Q8 cache (ops/ops.c:171-173, k_scalar.c:137-146): each query
@@ -299,6 +301,22 @@ constexpr int MX_P = 2, MX_TH = MX_T / MX_P;   // producers; their positions per
 
 __device__ __forceinline__ void kr_lds_order() { asm volatile("" ::: "memory"); }
 
+// Slot k of a producer lane: position r of the producer's MX_TH positions and
+// first dim c of its 4 dims. Lanes 0-31 and 32-63 take neighbouring dim
+// quads of the same 32 positions, so the 32 stores of a half-wave into the
+// adder's rows (MX_TS floats apart: 4 quads = 16 banks) hit 32 distinct banks.
+static_assert(MX_TH == 32, "the slot map covers 32 positions a slot");
+template <int DW>
+__device__ __forceinline__ void mx_slot(int k, int lane, int &r, int &c) {
+    if (DW >= 8) {
+        r = lane & 31;
+        c = 4 * (2 * k + (lane >> 5));
+    } else {   // one dim quad: lanes 32-63 hold no slot (r >= MX_TH)
+        r = lane;
+        c = 0;
+    }
+}
+
 template <int DW, int KT>
 __device__ __forceinline__ void attn_mix(float *ao, const float *att, const KvView kv, int group, int hd, int kv_dim,
                                          int max_seq, int window, const int *pos_p) {
@@ -380,7 +398,10 @@ __device__ __forceinline__ void attn_mix(float *ao, const float *att, const KvVi
         const int t0 = min(tile, ntiles - 1) * MX_T + p * MX_TH;
 #pragma unroll
         for (int k = 0; k < NV; k++) {
-            const int e = (k * 64 + lane) * 4, r = min(e / DW, MX_TH - 1), c = min(e % DW, cw - 4);
+            int r, c;
+            mx_slot<DW>(k, lane, r, c);
+            r = min(r, MX_TH - 1);
+            c = min(c, cw - 4);
             const int t = min(t0 + r, n - 1);
             v[k] = Kv4<KT>::load(kv.v, vb + (size_t)t * kv_dim + c);
             if (KT == KV_Q8) dv[k] = kv.vd[(size_t)(first + t) * kv.n_kv + g];
@@ -393,7 +414,8 @@ __device__ __forceinline__ void attn_mix(float *ao, const float *att, const KvVi
         float *P = prod[tile < ntiles ? tile % 3 : 3] + p * MX_TH;
 #pragma unroll
         for (int k = 0; k < NV; k++) {
-            const int e = (k * 64 + lane) * 4, r = e / DW, c = e % DW;
+            int r, c;
+            mx_slot<DW>(k, lane, r, c);
             if (r < MX_TH) {
                 const float4 x = Kv4<KT>::wide(v[k]);
 #pragma unroll
@@ -715,9 +737,16 @@ static void attention(float *ao, float *att, const float *q, const KvView &kv, i
     if constexpr (KT == KV_Q8)
         hipLaunchKernelGGL(k_attn_scores_q8, sgrid, dim3(AT_THREADS), lds, kr_stream(), att, q, kv, group, head_dim,
                            kv_dim, max_seq, window, scale, pos);
-    else if constexpr (KT == KV_F32)
-        hipLaunchKernelGGL(k_attn_scores, sgrid, dim3(AT_THREADS), lds, kr_stream(), att, q, (const float *)kv.k, group,
-                           head_dim, kv_dim, max_seq, window, scale, pos);
+    else if constexpr (KT == KV_F32) {
+        if (ntok == 1) {   // decode: tiles of AT_TD positions
+            const dim3 dgrid(n_kv_heads, (max_pos + AT_TD) / AT_TD, 1);
+            hipLaunchKernelGGL(k_attn_scores<AT_TD>, dgrid, dim3(AT_THREADS), lds, kr_stream(), att, q,
+                               (const float *)kv.k, group, head_dim, kv_dim, max_seq, window, scale, pos);
+        } else {
+            hipLaunchKernelGGL(k_attn_scores<AT_T>, sgrid, dim3(AT_THREADS), lds, kr_stream(), att, q,
+                               (const float *)kv.k, group, head_dim, kv_dim, max_seq, window, scale, pos);
+        }
+    }
     else
         hipLaunchKernelGGL((k_attn_scores_kv<KT>), sgrid, dim3(AT_THREADS), lds, kr_stream(), att, q, kv, group,
                            head_dim, kv_dim, max_seq, window, scale, pos);
