@@ -262,6 +262,34 @@ def prefill_roofline(K, model, ntok, prefill_s, reps=2):
             "whole_prefill_int8_tops": round(layer_ops * T / prefill_s / 1e12, 1) if prefill_s else None}
 
 
+def reference_route(path, prompt, decode, gpu_ids):
+    """the reference's own ml_run, its model and app code unchanged, bound to
+    this backend through the ISA=hip op table (oracle/_ref/hip/ml_run, built
+    from the reference's sources by oracle/Makefile): the same model file and
+    prompt, greedy; tok/s from its stderr lines (app/ml_run.c:406-410) and
+    whether its printed ids equal the native token loop's"""
+    exe = os.path.join(REF_DIR, "hip", "ml_run")
+    if not os.path.exists(exe):
+        return {"value": None, "error": "oracle/_ref/hip/ml_run is not built"}
+    n = len(prompt) - 1 + decode
+    r = subprocess.run([exe, path, "--tokens", ",".join(str(int(t)) for t in prompt), "-n", str(n), "-T", "0"],
+                       capture_output=True, text=True, timeout=600)
+    if r.returncode != 0:
+        return {"value": None, "error": "ml_run exited %d: %s" % (r.returncode, r.stderr[-300:])}
+    ids = np.array([int(v) for v in r.stdout.split()], dtype=np.int32)
+    qm = re.search(r"positions: (\d+), tok/s: ([\d.]+)", r.stderr)
+    pm = re.search(r"prefill: (\d+) tokens in ([\d.]+) ms", r.stderr)
+    pos, X = int(qm.group(1)), float(qm.group(2))
+    P, M = (int(pm.group(1)), float(pm.group(2))) if pm else (0, 0.0)
+    dec = (pos - P) / (pos / X - M / 1000.0)
+    k = min(len(ids), len(gpu_ids))
+    return {"value": round(dec, 3), "unit": "tok/s", "prefill_tok_s": round(P / (M / 1000.0), 2) if M > 0 else None,
+            "ids_equal_native": bool(k == n and np.array_equal(ids[:k], gpu_ids[:k])),
+            "sample": "oracle/_ref/hip/ml_run (the reference's app/ml_run.c and model/transformer.c over the "
+                      "ISA=hip op table): %d-token prompt (%d prefilled), %d greedy decode tokens; decode tok/s = "
+                      "(positions - prefilled) / (positions / tok/s - prefill s)" % (len(prompt), P, pos - P)}
+
+
 def cpu_baseline(path, prompt, decode, kv="f32", sample=None):
     """the reference's ml_run on the same model file, KV cache type and
     sampling options, on this host's cores"""
@@ -316,6 +344,9 @@ def main():
                          "instead of the greedy pick")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-matvec", action="store_true")
+    ap.add_argument("--reference-route", action="store_true",
+                    help="also time the reference's unchanged ml_run over this backend's ISA=hip op table on the "
+                         "same model and prompt")
     ap.add_argument("--roofline-reps", type=int, default=3)
     ap.add_argument("--roofline-only", action="store_true",
                     help="only the timed SwiGLU launches and the k_add calibration launches (the command "
@@ -402,6 +433,11 @@ def main():
             for r in mv:
                 log("matvec %s: %.1f GB/s resident, %.1f GB/s rotating" % (r["shape"], r["gbs_resident"],
                                                                            r["gbs_hbm_rotating"]))
+        route = None
+        if args.reference_route:
+            t0 = time.time()
+            route = reference_route(path, prompt, args.steps, ids)
+            log("reference route (%.1f s): %s" % (time.time() - t0, json.dumps(route)))
         cpu = None
         if not args.no_cpu_baseline:
             t0 = time.time()
@@ -439,6 +475,8 @@ def main():
         "matvec": mv,
         "cpu_baseline": cpu,
     }
+    if route is not None:
+        line["reference_route"] = route
     print(json.dumps(line), flush=True)
 
 

@@ -119,6 +119,86 @@ __global__ void __launch_bounds__(AT_THREADS) k_attn_scores(float *att, const fl
     attn_scores<KV_F32, TT>(att, q, kv, group, hd, kv_dim, max_seq, window, scale, pos_p);
 }
 
+// Batched (prefill) scores over the F32 cache without a window, a block of
+// AT_TB tokens at a time. Every token of the block attends from position 0,
+// so one K tile of AT_T positions, staged once in LDS, serves the whole block
+// (the per-token kernel stages it again for every token). The queries of qb
+// tokens at a time follow in LDS; thread (position t, head j) runs the chains
+// of AT_TI tokens together, one K read feeding all of them. Each chain is the
+// per-token kernel's: s = sum_i q_i k_i in index order, then * scale; a token
+// stores only the positions it attends.
+// HD: the head size when it is 64 or 128 (the loop over it then unrolls and
+// its LDS reads are scheduled ahead of the arithmetic), else 0 (any head size).
+constexpr int AT_TB = 16, AT_TI = 4;
+template <int HD>
+__global__ void __launch_bounds__(AT_THREADS) k_attn_scores_blk(float *att, const float *q, const float *kc, int group,
+                                                                int hd_arg, int kv_dim, int max_seq, float scale,
+                                                                const int *pos_p, int ntok, int qb) {
+    extern __shared__ __align__(16) float at_smem[];
+    const int hd = HD ? HD : hd_arg;
+    const int g = blockIdx.x, t0 = blockIdx.y * AT_T, z0 = blockIdx.z * AT_TB, tid = threadIdx.x;
+    const int pos0 = *pos_p, zn = min(AT_TB, ntok - z0);
+    const int nlast = pos0 + z0 + zn;   // positions the block's last token attends
+    if (t0 >= nlast) return;
+    const int nt = min(AT_T, nlast - t0), ks = hd + 4, h4 = hd / 4, n_heads = gridDim.x * group;
+    float *kt = at_smem, *qs = at_smem + AT_T * ks;   // K tile [AT_T][ks]; queries [qb][group][hd]
+    for (int e = tid; e < nt * h4; e += AT_THREADS) {
+        const int r = e / h4, c = e - r * h4;
+        *(float4 *)(kt + r * ks + 4 * c) = *(const float4 *)(kc + (size_t)(t0 + r) * kv_dim + (size_t)g * hd + 4 * c);
+    }
+    const int t = tid % AT_T, p = t0 + t;   // this thread's position (absolute: no window)
+    for (int zb = 0; zb < zn; zb += qb) {
+        const int qn = min(qb, zn - zb), gh4 = group * h4;
+        __syncthreads();   // the last queries are read
+        for (int e = tid; e < qn * gh4; e += AT_THREADS) {
+            const int zz = e / gh4, r = e - zz * gh4;
+            ((float4 *)qs)[e] = ((const float4 *)(q + (size_t)(z0 + zb + zz) * n_heads * hd + (size_t)g * group * hd))[r];
+        }
+        __syncthreads();
+        if (t >= nt) continue;
+        const float *kr = kt + t * ks;
+        for (int j = tid / AT_T; j < group; j += AT_THREADS / AT_T) {
+            for (int zi = 0; zi < qn; zi += AT_TI) {
+                // tokens zb + zi + u (u < AT_TI; slots past qn read queries
+                // of an earlier block and are not stored)
+                const float *qh = qs + ((size_t)zi * group + j) * hd;
+                float acc[AT_TI];
+#pragma unroll
+                for (int u = 0; u < AT_TI; u++) acc[u] = 0.0f;
+                // the LDS reads of step i + 4 go out before step i's
+                // arithmetic (the last step re-reads its own: unused)
+                float4 b = *(const float4 *)kr, a[AT_TI];
+#pragma unroll
+                for (int u = 0; u < AT_TI; u++) a[u] = *(const float4 *)(qh + (size_t)u * group * hd);
+#pragma unroll 2
+                for (int i = 0; i < hd; i += 4) {
+                    const int in = min(i + 4, hd - 4);
+                    const float4 bn = *(const float4 *)(kr + in);
+                    float4 an[AT_TI];
+#pragma unroll
+                    for (int u = 0; u < AT_TI; u++) an[u] = *(const float4 *)(qh + (size_t)u * group * hd + in);
+#pragma unroll
+                    for (int u = 0; u < AT_TI; u++) {
+                        acc[u] = kr_fadd(acc[u], kr_fmul(a[u].x, b.x));
+                        acc[u] = kr_fadd(acc[u], kr_fmul(a[u].y, b.y));
+                        acc[u] = kr_fadd(acc[u], kr_fmul(a[u].z, b.z));
+                        acc[u] = kr_fadd(acc[u], kr_fmul(a[u].w, b.w));
+                    }
+                    b = bn;
+#pragma unroll
+                    for (int u = 0; u < AT_TI; u++) a[u] = an[u];
+                }
+#pragma unroll
+                for (int u = 0; u < AT_TI; u++) {
+                    const int z = z0 + zb + zi + u;
+                    if (zi + u < qn && p <= pos0 + z)
+                        att[((size_t)z * n_heads + (size_t)g * group + j) * max_seq + p] = kr_fmul(acc[u], scale);
+                }
+            }
+        }
+    }
+}
+
 template <int KT>
 __global__ void __launch_bounds__(AT_THREADS) k_attn_scores_kv(float *att, const float *q, const KvView kv, int group,
                                                                int hd, int kv_dim, int max_seq, int window, float scale,
@@ -642,6 +722,117 @@ __device__ __forceinline__ void attn_mix_batch(float *ao, const float *att, cons
     if (j < group && d < cw) ao[(size_t)(g * group + j) * hd + c0 + d] = o;
 }
 
+// Batched (prefill) mix without a window, by blocks of MK_W tokens: a
+// workgroup per (KV head g, DW dims from c0, MK_W consecutive tokens), one
+// wave per token, lane = (head j of the group, dim d); each lane runs its chain
+// o += a_t * v_t,d over positions t in order (k_scalar.c:119-122), each
+// product rounded before its add. The block's waves share each V tile, staged
+// once in LDS as [dim][position] so one 16-byte read gives a lane 4
+// positions. The weights take no LDS: a lane holds its head's weights of 16
+// positions in one register (lane d of a 16-lane row holds position t0 + d),
+// and a DPP row broadcast (row_newbcast) hands position t0 + k's weight to
+// every lane of the row as the multiply's operand. So a row of 16 lanes must
+// hold one head: DW >= 16. Tiles are double-buffered: tile k + 1 is stored
+// while tile k is read, the loads of tile k + 2 already in flight.
+constexpr int MK_W = 4, MK_T = 64, MK_TS = MK_T + 4;
+
+template <int K> __device__ __forceinline__ float row_bcast(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x150 + K, 0xF, 0xF, false));
+}
+
+// o += a_{t0+4q+i} * v4.i for i < 4, positions t0 + 4q + i of a 16-position
+// block whose weights sit in a (lane k of each row: position t0 + k)
+template <int Q>
+__device__ __forceinline__ void mk_quad(float &o, float a, float4 v) {
+    o = kr_fadd(o, kr_fmul(row_bcast<4 * Q + 0>(a), v.x));
+    o = kr_fadd(o, kr_fmul(row_bcast<4 * Q + 1>(a), v.y));
+    o = kr_fadd(o, kr_fmul(row_bcast<4 * Q + 2>(a), v.z));
+    o = kr_fadd(o, kr_fmul(row_bcast<4 * Q + 3>(a), v.w));
+}
+
+template <int DW>
+__global__ void __launch_bounds__(64 * MK_W) k_attn_mix_blk(float *ao, const float *att, const float *vc, int group,
+                                                            int hd, int kv_dim, int max_seq, const int *pos_p,
+                                                            int ntok) {
+    static_assert(DW >= 16, "a 16-lane row must hold one head");
+    constexpr int QPR = DW / 4;                 // float4 per staged row of DW dims
+    constexpr int RPP = 64 * MK_W / QPR;        // rows the workgroup stages per pass
+    constexpr int NP = MK_T / RPP;              // passes per tile
+    __shared__ __align__(16) float vt[2][DW * MK_TS];
+    const int g = blockIdx.x, c0 = blockIdx.y * DW, z0 = blockIdx.z * MK_W, tid = threadIdx.x;
+    const int wave = tid >> 6, lane = tid & 63, j = lane / DW, d = lane % DW;
+    const int z = z0 + wave, pos0 = *pos_p;
+    const int n = z < ntok ? pos0 + z + 1 : 0;                  // positions this wave's token attends
+    const int nmax = pos0 + min(z0 + MK_W, ntok);               // the block's last token's
+    const int n_heads = gridDim.x * group, cw = min(DW, hd - c0), ntiles = (nmax + MK_T - 1) / MK_T;
+    const float *arow = att + ((size_t)min(z, ntok - 1) * n_heads + (size_t)g * group + min(j, group - 1)) * max_seq;
+    const float *vbase = vc + (size_t)g * hd + c0;
+    // staging slot of this thread in pass p: row p * RPP + srow, dims scol .. scol + 3
+    const int srow = tid / QPR, scol = min(4 * (tid % QPR), cw - 4);
+    float4 sv[NP];
+    auto stage_load = [&](int tile) {
+#pragma unroll
+        for (int p = 0; p < NP; p++)
+            sv[p] = *(const float4 *)(vbase + (size_t)min(tile * MK_T + p * RPP + srow, nmax - 1) * kv_dim + scol);
+    };
+    auto stage_store = [&](int buf) {
+        float *V = vt[buf];
+#pragma unroll
+        for (int p = 0; p < NP; p++) {
+            const int r = p * RPP + srow, c = 4 * (tid % QPR);
+            V[(c + 0) * MK_TS + r] = sv[p].x;
+            V[(c + 1) * MK_TS + r] = sv[p].y;
+            V[(c + 2) * MK_TS + r] = sv[p].z;
+            V[(c + 3) * MK_TS + r] = sv[p].w;
+        }
+    };
+    auto a_load = [&](int tile, float *a) {
+#pragma unroll
+        for (int b = 0; b < MK_T / 16; b++) a[b] = arow[min(tile * MK_T + 16 * b + (lane & 15), max_seq - 1)];
+    };
+    float o = 0.0f;
+    float acur[MK_T / 16], anext[MK_T / 16];
+    stage_load(0);
+    stage_store(0);
+    a_load(0, acur);
+    if (ntiles > 1) stage_load(1);
+    __syncthreads();
+    for (int k = 0; k < ntiles; k++) {
+        const int buf = k & 1, t0 = k * MK_T;
+        if (k + 1 < ntiles) stage_store(buf ^ 1);   // its last reader finished before the last barrier
+        a_load(min(k + 1, ntiles - 1), anext);
+        if (k + 2 < ntiles) stage_load(k + 2);
+        const float *V = vt[buf] + d * MK_TS;
+        if (t0 + MK_T <= n) {   // a full tile for this token
+#pragma unroll
+            for (int b = 0; b < MK_T / 16; b++) {
+                const float4 v0 = *(const float4 *)(V + 16 * b), v1 = *(const float4 *)(V + 16 * b + 4);
+                const float4 v2 = *(const float4 *)(V + 16 * b + 8), v3 = *(const float4 *)(V + 16 * b + 12);
+                mk_quad<0>(o, acur[b], v0);
+                mk_quad<1>(o, acur[b], v1);
+                mk_quad<2>(o, acur[b], v2);
+                mk_quad<3>(o, acur[b], v3);
+            }
+        } else if (t0 < n) {    // the token's last tile: its live positions only
+#pragma unroll
+            for (int b = 0; b < MK_T / 16; b++) {
+                const float ab = acur[b];
+                float w[16];
+                w[0] = row_bcast<0>(ab); w[1] = row_bcast<1>(ab); w[2] = row_bcast<2>(ab); w[3] = row_bcast<3>(ab);
+                w[4] = row_bcast<4>(ab); w[5] = row_bcast<5>(ab); w[6] = row_bcast<6>(ab); w[7] = row_bcast<7>(ab);
+                w[8] = row_bcast<8>(ab); w[9] = row_bcast<9>(ab); w[10] = row_bcast<10>(ab); w[11] = row_bcast<11>(ab);
+                w[12] = row_bcast<12>(ab); w[13] = row_bcast<13>(ab); w[14] = row_bcast<14>(ab); w[15] = row_bcast<15>(ab);
+                for (int i = 0; i < 16 && t0 + 16 * b + i < n; i++) o = kr_fadd(o, kr_fmul(w[i], V[16 * b + i]));
+            }
+        }
+#pragma unroll
+        for (int b = 0; b < MK_T / 16; b++) acur[b] = anext[b];
+        kr_lds_order();
+        __syncthreads();
+    }
+    if (z < ntok && j < group && d < cw) ao[(size_t)z * n_heads * hd + (size_t)(g * group + j) * hd + c0 + d] = o;
+}
+
 template <int DW>
 __global__ void __launch_bounds__(64) k_attn_mix_batch(float *ao, const float *att, const float *vc, int group, int hd,
                                                        int kv_dim, int max_seq, int window, const int *pos_p) {
@@ -698,6 +889,14 @@ template <int KT, int DW>
 static void launch_mix(const dim3 &grid, int ntok, float *ao, const float *att, const KvView &kv, int group, int hd,
                        int kv_dim, int max_seq, int window, const int *pos) {
     const float *vc = (const float *)kv.v;
+    if constexpr (KT == KV_F32 && DW >= 16) {
+        if (ntok > 1 && window == 0) {   // prefill without a window: blocks of MK_W tokens share the V tiles
+            const dim3 bgrid(grid.x, grid.y, (ntok + MK_W - 1) / MK_W);
+            hipLaunchKernelGGL(k_attn_mix_blk<DW>, bgrid, dim3(64 * MK_W), 0, kr_stream(), ao, att, vc, group, hd,
+                               kv_dim, max_seq, pos, ntok);
+            return;
+        }
+    }
     if (ntok > 1) {
         if constexpr (KT == KV_F32)
             hipLaunchKernelGGL(k_attn_mix_batch<DW>, grid, dim3(64), 0, kr_stream(), ao, att, vc, group, hd, kv_dim,
@@ -738,7 +937,21 @@ static void attention(float *ao, float *att, const float *q, const KvView &kv, i
         hipLaunchKernelGGL(k_attn_scores_q8, sgrid, dim3(AT_THREADS), lds, kr_stream(), att, q, kv, group, head_dim,
                            kv_dim, max_seq, window, scale, pos);
     else if constexpr (KT == KV_F32) {
-        if (ntok == 1) {   // decode: tiles of AT_TD positions
+        // the queries of qb tokens beside the K tile, within 64 KB of LDS
+        const size_t ktile = sizeof(float) * (size_t)AT_T * (head_dim + 4);
+        const int qb = (int)((64 * 1024 - ktile) / (sizeof(float) * (size_t)group * head_dim)) / AT_TI * AT_TI;
+        if (ntok > 1 && window == 0 && qb >= AT_TI) {   // prefill: blocks of AT_TB tokens share a K tile
+            const int qbb = qb < AT_TB ? qb : AT_TB;
+            const dim3 bgrid(n_kv_heads, (max_pos + AT_T) / AT_T, (ntok + AT_TB - 1) / AT_TB);
+            const size_t blds = ktile + sizeof(float) * (size_t)qbb * group * head_dim;
+            auto go = [&](auto kern) {
+                hipLaunchKernelGGL(kern, bgrid, dim3(AT_THREADS), blds, kr_stream(), att, q, (const float *)kv.k,
+                                   group, head_dim, kv_dim, max_seq, scale, pos, ntok, qbb);
+            };
+            if (head_dim == 128) go(k_attn_scores_blk<128>);
+            else if (head_dim == 64) go(k_attn_scores_blk<64>);
+            else go(k_attn_scores_blk<0>);
+        } else if (ntok == 1) {   // decode: tiles of AT_TD positions
             const dim3 dgrid(n_kv_heads, (max_pos + AT_TD) / AT_TD, 1);
             hipLaunchKernelGGL(k_attn_scores<AT_TD>, dgrid, dim3(AT_THREADS), lds, kr_stream(), att, q,
                                (const float *)kv.k, group, head_dim, kv_dim, max_seq, window, scale, pos);
