@@ -122,18 +122,18 @@ __global__ void __launch_bounds__(AT_THREADS) k_attn_scores(float *att, const fl
 // Batched (prefill) scores over the F32 cache without a window, a block of
 // AT_TB tokens at a time. Every token of the block attends from position 0,
 // so one K tile of AT_T positions, staged once in LDS, serves the whole block
-// (the per-token kernel stages it again for every token). The queries of qb
-// tokens at a time follow in LDS; thread (position t, head j) runs the chains
-// of AT_TI tokens together, one K read feeding all of them. Each chain is the
-// per-token kernel's: s = sum_i q_i k_i in index order, then * scale; a token
-// stores only the positions it attends.
-// HD: the head size when it is 64 or 128 (the loop over it then unrolls and
-// its LDS reads are scheduled ahead of the arithmetic), else 0 (any head size).
-constexpr int AT_TB = 16, AT_TI = 4;
-template <int HD>
+// (the per-token kernel stages it again for every token). The queries of QB
+// tokens at a time follow in LDS; thread (position t, head j) runs the QB
+// chains of those tokens in one pass over the head's dims, one K read feeding
+// them all (QB independent chains: the LDS latency hides under them). Each
+// chain is the per-token kernel's: s = sum_i q_i k_i in index order, then
+// * scale; a token stores only the positions it attends. HD: the head size
+// when it is 64 or 128, else 0 (any).
+constexpr int AT_TB = 16;
+template <int HD, int QB>
 __global__ void __launch_bounds__(AT_THREADS) k_attn_scores_blk(float *att, const float *q, const float *kc, int group,
                                                                 int hd_arg, int kv_dim, int max_seq, float scale,
-                                                                const int *pos_p, int ntok, int qb) {
+                                                                const int *pos_p, int ntok) {
     extern __shared__ __align__(16) float at_smem[];
     const int hd = HD ? HD : hd_arg;
     const int g = blockIdx.x, t0 = blockIdx.y * AT_T, z0 = blockIdx.z * AT_TB, tid = threadIdx.x;
@@ -141,14 +141,15 @@ __global__ void __launch_bounds__(AT_THREADS) k_attn_scores_blk(float *att, cons
     const int nlast = pos0 + z0 + zn;   // positions the block's last token attends
     if (t0 >= nlast) return;
     const int nt = min(AT_T, nlast - t0), ks = hd + 4, h4 = hd / 4, n_heads = gridDim.x * group;
-    float *kt = at_smem, *qs = at_smem + AT_T * ks;   // K tile [AT_T][ks]; queries [qb][group][hd]
+    float *kt = at_smem, *qs = at_smem + AT_T * ks;   // K tile [AT_T][ks]; queries [QB][group][hd]
     for (int e = tid; e < nt * h4; e += AT_THREADS) {
         const int r = e / h4, c = e - r * h4;
         *(float4 *)(kt + r * ks + 4 * c) = *(const float4 *)(kc + (size_t)(t0 + r) * kv_dim + (size_t)g * hd + 4 * c);
     }
     const int t = tid % AT_T, p = t0 + t;   // this thread's position (absolute: no window)
-    for (int zb = 0; zb < zn; zb += qb) {
-        const int qn = min(qb, zn - zb), gh4 = group * h4;
+    const size_t qstride = (size_t)group * hd;   // floats between two tokens' queries in LDS
+    for (int zb = 0; zb < zn; zb += QB) {
+        const int qn = min(QB, zn - zb), gh4 = group * h4;
         __syncthreads();   // the last queries are read
         for (int e = tid; e < qn * gh4; e += AT_THREADS) {
             const int zz = e / gh4, r = e - zz * gh4;
@@ -158,42 +159,29 @@ __global__ void __launch_bounds__(AT_THREADS) k_attn_scores_blk(float *att, cons
         if (t >= nt) continue;
         const float *kr = kt + t * ks;
         for (int j = tid / AT_T; j < group; j += AT_THREADS / AT_T) {
-            for (int zi = 0; zi < qn; zi += AT_TI) {
-                // tokens zb + zi + u (u < AT_TI; slots past qn read queries
-                // of an earlier block and are not stored)
-                const float *qh = qs + ((size_t)zi * group + j) * hd;
-                float acc[AT_TI];
+            // tokens zb + u, u < QB (slots past qn read an earlier block's
+            // queries and are not stored)
+            const float *qh = qs + (size_t)j * hd;
+            float acc[QB];
 #pragma unroll
-                for (int u = 0; u < AT_TI; u++) acc[u] = 0.0f;
-                // the LDS reads of step i + 4 go out before step i's
-                // arithmetic (the last step re-reads its own: unused)
-                float4 b = *(const float4 *)kr, a[AT_TI];
-#pragma unroll
-                for (int u = 0; u < AT_TI; u++) a[u] = *(const float4 *)(qh + (size_t)u * group * hd);
+            for (int u = 0; u < QB; u++) acc[u] = 0.0f;
 #pragma unroll 2
-                for (int i = 0; i < hd; i += 4) {
-                    const int in = min(i + 4, hd - 4);
-                    const float4 bn = *(const float4 *)(kr + in);
-                    float4 an[AT_TI];
+            for (int i = 0; i < hd; i += 4) {
+                const float4 b = *(const float4 *)(kr + i);
 #pragma unroll
-                    for (int u = 0; u < AT_TI; u++) an[u] = *(const float4 *)(qh + (size_t)u * group * hd + in);
-#pragma unroll
-                    for (int u = 0; u < AT_TI; u++) {
-                        acc[u] = kr_fadd(acc[u], kr_fmul(a[u].x, b.x));
-                        acc[u] = kr_fadd(acc[u], kr_fmul(a[u].y, b.y));
-                        acc[u] = kr_fadd(acc[u], kr_fmul(a[u].z, b.z));
-                        acc[u] = kr_fadd(acc[u], kr_fmul(a[u].w, b.w));
-                    }
-                    b = bn;
-#pragma unroll
-                    for (int u = 0; u < AT_TI; u++) a[u] = an[u];
+                for (int u = 0; u < QB; u++) {
+                    const float4 a = *(const float4 *)(qh + u * qstride + i);
+                    acc[u] = kr_fadd(acc[u], kr_fmul(a.x, b.x));
+                    acc[u] = kr_fadd(acc[u], kr_fmul(a.y, b.y));
+                    acc[u] = kr_fadd(acc[u], kr_fmul(a.z, b.z));
+                    acc[u] = kr_fadd(acc[u], kr_fmul(a.w, b.w));
                 }
+            }
 #pragma unroll
-                for (int u = 0; u < AT_TI; u++) {
-                    const int z = z0 + zb + zi + u;
-                    if (zi + u < qn && p <= pos0 + z)
-                        att[((size_t)z * n_heads + (size_t)g * group + j) * max_seq + p] = kr_fmul(acc[u], scale);
-                }
+            for (int u = 0; u < QB; u++) {
+                const int z = z0 + zb + u;
+                if (u < qn && p <= pos0 + z)
+                    att[((size_t)z * n_heads + (size_t)g * group + j) * max_seq + p] = kr_fmul(acc[u], scale);
             }
         }
     }
@@ -937,20 +925,26 @@ static void attention(float *ao, float *att, const float *q, const KvView &kv, i
         hipLaunchKernelGGL(k_attn_scores_q8, sgrid, dim3(AT_THREADS), lds, kr_stream(), att, q, kv, group, head_dim,
                            kv_dim, max_seq, window, scale, pos);
     else if constexpr (KT == KV_F32) {
-        // the queries of qb tokens beside the K tile, within 64 KB of LDS
+        // the queries of QB tokens beside the K tile, within 64 KB of LDS
         const size_t ktile = sizeof(float) * (size_t)AT_T * (head_dim + 4);
-        const int qb = (int)((64 * 1024 - ktile) / (sizeof(float) * (size_t)group * head_dim)) / AT_TI * AT_TI;
-        if (ntok > 1 && window == 0 && qb >= AT_TI) {   // prefill: blocks of AT_TB tokens share a K tile
-            const int qbb = qb < AT_TB ? qb : AT_TB;
+        const size_t qtok = sizeof(float) * (size_t)group * head_dim;
+        const int qb = ktile + 8 * qtok <= 64 * 1024 ? 8 : ktile + 4 * qtok <= 64 * 1024 ? 4 : 0;
+        if (ntok > 1 && window == 0 && qb) {   // prefill: blocks of AT_TB tokens share a K tile
             const dim3 bgrid(n_kv_heads, (max_pos + AT_T) / AT_T, (ntok + AT_TB - 1) / AT_TB);
-            const size_t blds = ktile + sizeof(float) * (size_t)qbb * group * head_dim;
+            const size_t blds = ktile + qb * qtok;
             auto go = [&](auto kern) {
                 hipLaunchKernelGGL(kern, bgrid, dim3(AT_THREADS), blds, kr_stream(), att, q, (const float *)kv.k,
-                                   group, head_dim, kv_dim, max_seq, scale, pos, ntok, qbb);
+                                   group, head_dim, kv_dim, max_seq, scale, pos, ntok);
             };
-            if (head_dim == 128) go(k_attn_scores_blk<128>);
-            else if (head_dim == 64) go(k_attn_scores_blk<64>);
-            else go(k_attn_scores_blk<0>);
+            if (qb == 8) {
+                if (head_dim == 128) go(k_attn_scores_blk<128, 8>);
+                else if (head_dim == 64) go(k_attn_scores_blk<64, 8>);
+                else go(k_attn_scores_blk<0, 8>);
+            } else {
+                if (head_dim == 128) go(k_attn_scores_blk<128, 4>);
+                else if (head_dim == 64) go(k_attn_scores_blk<64, 4>);
+                else go(k_attn_scores_blk<0, 4>);
+            }
         } else if (ntok == 1) {   // decode: tiles of AT_TD positions
             const dim3 dgrid(n_kv_heads, (max_pos + AT_TD) / AT_TD, 1);
             hipLaunchKernelGGL(k_attn_scores<AT_TD>, dgrid, dim3(AT_THREADS), lds, kr_stream(), att, q,
