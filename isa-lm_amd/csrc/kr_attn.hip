@@ -345,6 +345,61 @@ __global__ void __launch_bounds__(AT_THREADS) k_attn_softmax(float *att, int max
     for (int t = tid; t < n; t += AT_THREADS) a[t] = kr_fmul(a[t], inv);
 }
 
+// Batched (prefill) softmax, one row per wave and RW rows per workgroup:
+// rows r = token * n_heads + head of up to SM_WN = 4096 entries (the
+// single-wave ordered sum's limit). Per row, as k_attn_softmax: the max,
+// the exponentials x - max, their ordered sum (kr_spec_sum in single-wave
+// mode), x * (1 / sum); an all -inf row becomes 1/n. The per-row kernel keeps
+// three of its four waves idle in the ordered sum of rows this short; here
+// every wave sums its own row.
+constexpr int SM_WN = SC_CPW << SC_LOG_LMIN, SM_V = SM_WN / 64;
+template <int RW>
+__global__ void __launch_bounds__(64 * RW) k_attn_softmax_rows(float *att, int n_heads, int max_seq, int window,
+                                                               const int *pos_p, int nrows, int terms_cap,
+                                                               int scr_bytes) {
+    extern __shared__ __align__(16) unsigned char sm_lds[];
+    __shared__ uint64_t xtab[32];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    if (threadIdx.x < 32) xtab[threadIdx.x] = kr_exp2_tab[threadIdx.x];
+    __syncthreads();
+    const int r = blockIdx.x * RW + wave;
+    if (r >= nrows) return;
+    const int z = r / n_heads, pos = *pos_p + z;
+    const int first = window && pos >= window ? pos + 1 - window : 0, n = pos + 1 - first;
+    float *a = att + (size_t)r * max_seq;
+    float *es = (float *)(sm_lds + (size_t)wave * (4 * terms_cap + scr_bytes));
+    unsigned char *scr = (unsigned char *)(es + terms_cap);
+    float v[SM_V];
+    float m = -INFINITY;
+#pragma unroll
+    for (int k = 0; k < SM_V; k++)
+        if (k * 64 < n) v[k] = a[min(k * 64 + lane, n - 1)];   // the last live slot clamped: repeats change no max
+#pragma unroll
+    for (int k = 0; k < SM_V; k++)
+        if (k * 64 < n) m = fmaxf(m, v[k]);
+    for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+    if (m == -INFINITY) {   // every score -inf: the scalar loop's 1/n
+        for (int t = lane; t < n; t += 64) a[t] = kr_fdiv(1.0f, (float)n);
+        return;
+    }
+    const int sh = sc_log_len(n);
+#pragma unroll
+    for (int k = 0; k < SM_V; k++) {
+        if (k * 64 >= n) break;
+        const int t = k * 64 + lane;
+        v[k] = kr_expf_tab(kr_fsub(v[k], m), xtab);
+        if (t < n) es[sc_at(t, sh)] = v[k];
+    }
+    kr_wave_sync();
+    const float inv = kr_fdiv(1.0f, kr_spec_sum<64, false, true>(es, n, scr));
+#pragma unroll
+    for (int k = 0; k < SM_V; k++) {
+        if (k * 64 >= n) break;
+        const int t = k * 64 + lane;
+        if (t < n) a[t] = kr_fmul(v[k], inv);
+    }
+}
+
 // out for one KV head's query heads and DW of their dims: lane = (head j of
 // the group, dim d), DW = 64 / (group rounded up to a power of two). Each
 // lane runs its ordered chain o += a_t * v_t,d (k_scalar.c:119-122). ao is
@@ -958,8 +1013,20 @@ static void attention(float *ao, float *att, const float *q, const KvView &kv, i
         hipLaunchKernelGGL((k_attn_scores_kv<KT>), sgrid, dim3(AT_THREADS), lds, kr_stream(), att, q, kv, group,
                            head_dim, kv_dim, max_seq, window, scale, pos);
     if (cap > 0.0f) krh_softcap_att(att, n_heads, max_seq, window, pos, ntok, cap);   // ops/ops.c:141
-    hipLaunchKernelGGL(k_attn_softmax, dim3(n_heads, 1, ntok), dim3(AT_THREADS), 0, kr_stream(), att, max_seq, window,
-                       pos);
+    if (ntok > 1 && max_pos + 1 <= SM_WN) {   // prefill rows short enough for one wave each
+        const int tcap = sc_terms_cap(max_pos + 1), scr = (sc_lds_bytes(max_pos + 1, 64) + 15) / 16 * 16;
+        const size_t per_wave = 4 * (size_t)tcap + scr;
+        const int nrows = n_heads * ntok;
+        if (4 * per_wave <= 64 * 1024)
+            hipLaunchKernelGGL(k_attn_softmax_rows<4>, dim3((nrows + 3) / 4), dim3(256), 4 * per_wave, kr_stream(),
+                               att, n_heads, max_seq, window, pos, nrows, tcap, scr);
+        else
+            hipLaunchKernelGGL(k_attn_softmax_rows<2>, dim3((nrows + 1) / 2), dim3(128), 2 * per_wave, kr_stream(),
+                               att, n_heads, max_seq, window, pos, nrows, tcap, scr);
+    } else {
+        hipLaunchKernelGGL(k_attn_softmax, dim3(n_heads, 1, ntok), dim3(AT_THREADS), 0, kr_stream(), att, max_seq,
+                           window, pos);
+    }
     const int gp = group <= 1 ? 1 : group <= 2 ? 2 : group <= 4 ? 4 : group <= 8 ? 8 : 16;
     const int dw = 64 / gp;
     const dim3 grid(n_kv_heads, (head_dim + dw - 1) / dw, ntok);

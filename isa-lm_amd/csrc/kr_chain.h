@@ -197,13 +197,15 @@ __device__ __forceinline__ unsigned sc_rest(const float *t, int sh, int c, int m
 // follows the terms' stores. REC: cst[c] (c < sc_chunks(n)) receives the bits
 // of the partial sum before chunk c, and cst[sc_chunks(n)] is 1 when a
 // negative or non-finite term sent the sum through the sequential loop (the
-// starts are then not written), else 0.
-template <int NT, bool REC = false>
+// starts are then not written), else 0. WAVE: the calling wave alone
+// (NT = 64) computes the sum, with wave syncs in place of barriers, for n of
+// at most SC_CPW chunks (4096 terms); the workgroup's other waves take no part.
+template <int NT, bool REC = false, bool WAVE = false>
 __device__ __forceinline__ float kr_spec_sum(float *t, int n, unsigned char *lds, float s0 = 0.0f,
                                              unsigned *cst = nullptr) {
     constexpr int NW = NT / 64;
-    static_assert(NW * SC_CPW >= SC_MAXC, "every chunk needs a lane pair");
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    static_assert(WAVE ? NT == 64 : NW * SC_CPW >= SC_MAXC, "every chunk needs a lane pair");
+    const int tid = WAVE ? (int)(threadIdx.x & 63) : (int)threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int sh = sc_log_len(n), L = 1 << sh, NB = L / SC_BLK;
     const int C = (n + L - 1) >> sh, NA = (C + SC_CPW - 1) / SC_CPW;   // waves with chunks
     float *wtot = (float *)lds;                   // [NW] a wave's chunk total
@@ -245,7 +247,7 @@ __device__ __forceinline__ float kr_spec_sum(float *t, int n, unsigned char *lds
     const float wsum = __uint_as_float(sc_lane(__float_as_uint(inc), 63));
     bool bad = __any((sg >> 31) != 0 || !(acc <= 3.402823466e38f));   // FLT_MAX: NaN fails
     float before = s0;
-    if (NA > 1) {   // the other waves' chunk totals and flags
+    if (!WAVE && NA > 1) {   // the other waves' chunk totals and flags
         if (lane == 0 && wave < NA) {
             wtot[wave] = wsum;
             wbad[wave] = bad;
@@ -309,7 +311,7 @@ __device__ __forceinline__ float kr_spec_sum(float *t, int n, unsigned char *lds
         }
         if (p == 0) rm[c] = mask;
     }
-    if (NA > 1) __syncthreads();
+    if (!WAVE && NA > 1) __syncthreads();
     else kr_wave_sync();
     // the walk, in wave 0, 64 chunks (one per lane) at a time
     if (wave == 0) {
@@ -410,7 +412,8 @@ __device__ __forceinline__ float kr_spec_sum(float *t, int n, unsigned char *lds
         }
         if (lane == 0) *res = r;
     }
-    __syncthreads();
+    if (WAVE) kr_wave_sync();
+    else __syncthreads();
     return *res;
 }
 

@@ -750,6 +750,17 @@ __global__ void __launch_bounds__(256) k_ordered_sum(float *out, const float *t,
     const float s = kr_spec_sum<256>(os_t, n, (unsigned char *)(os_t + sc_terms_cap(n)), s0);
     if (threadIdx.x == 0) *out = s;
 }
+// the single-wave mode, run by the second wave of the workgroup (its lanes
+// and LDS are not the workgroup's first)
+__global__ void __launch_bounds__(128) k_ordered_sum_wave(float *out, const float *t, int n, float s0) {
+    extern __shared__ __align__(16) float osw_t[];
+    if (threadIdx.x < 64) return;
+    const int lane = threadIdx.x & 63, sh = sc_log_len(n);
+    for (int i = lane; i < n; i += 64) osw_t[sc_at(i, sh)] = t[i];
+    kr_wave_sync();
+    const float s = kr_spec_sum<64, false, true>(osw_t, n, (unsigned char *)(osw_t + sc_terms_cap(n)), s0);
+    if (lane == 0) *out = s;
+}
 __global__ void k_h2f_batch(float *y, const uint16_t *h, size_t n) {
     const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i < n) y[i] = kr_h2f(h[i]);
@@ -1000,6 +1011,16 @@ extern "C" void krh_ordered_sum(float *out, const float *t, int n, float s0) {
     const size_t lds = sizeof(float) * (size_t)sc_terms_cap(n) + sc_lds_bytes(n, RN_THREADS);
     hipLaunchKernelGGL(k_ordered_sum, dim3(1), dim3(256), lds, kr_stream(), out, t, n, s0);
     kr_check_launch("ordered_sum");
+}
+
+extern "C" void krh_ordered_sum_wave(float *out, const float *t, int n, float s0) {
+    if (n < 1 || n > KRH_ORDERED_SUM_WAVE_MAX) {
+        kr_fail(ML_E_SHAPE, "ordered_sum_wave size", hipSuccess);
+        return;
+    }
+    const size_t lds = sizeof(float) * (size_t)sc_terms_cap(n) + sc_lds_bytes(n, 64);
+    hipLaunchKernelGGL(k_ordered_sum_wave, dim3(1), dim3(128), lds, kr_stream(), out, t, n, s0);
+    kr_check_launch("ordered_sum_wave");
 }
 
 extern "C" void krh_h2f_batch(float *y, const uint16_t *h, size_t n) {

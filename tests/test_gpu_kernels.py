@@ -346,15 +346,8 @@ ORDERED_CASES = ["squares", "heavy", "outliers", "absorb", "absorb_late", "tiny"
                  "nan", "inf", "huge", "ties", "steep", "late_growth", "neg_zero", "subnormal"]
 
 
-@pytest.mark.parametrize("s0", [0.0, 1234.5678])
-@pytest.mark.parametrize("case", ORDERED_CASES)
-@pytest.mark.parametrize("n", [1, 5, 31, 32, 33, 127, 128, 129, 2048, 2049, 2175, 4096, 4097, 8192])
-def test_ordered_sum(dev, case, n, s0):
-    """the chunked sum returns the bits of the sequential fp32 sum through its
-    shifted runs (ties to even included), its blocks where the running sum
-    changes binade (many of them for steep growth), its per-run fallback, the
-    sequential path for negative, -0 and non-finite terms, and sizes at the
-    chunk-length and chunk-count edges"""
+def ordered_terms(case, n):
+    """the terms of one ordered-sum case"""
     x = RNG.normal(0, 1, n)
     if case == "squares":
         t = f32(x) * f32(x)
@@ -397,9 +390,39 @@ def test_ordered_sum(dev, case, n, s0):
         t = f32(np.abs(x) * 1e-44)
     else:   # huge: the sum overflows to inf part-way
         t = f32(np.full(n, 3e37))
-    t = f32(t)
+    return f32(t)
+
+
+@pytest.mark.parametrize("s0", [0.0, 1234.5678])
+@pytest.mark.parametrize("case", ORDERED_CASES)
+@pytest.mark.parametrize("n", [1, 5, 31, 32, 33, 127, 128, 129, 2048, 2049, 2175, 4096, 4097, 8192])
+def test_ordered_sum(dev, case, n, s0):
+    """the chunked sum returns the bits of the sequential fp32 sum through its
+    shifted runs (ties to even included), its blocks where the running sum
+    changes binade (many of them for steep growth), its per-run fallback, the
+    sequential path for negative, -0 and non-finite terms, and sizes at the
+    chunk-length and chunk-count edges"""
+    t = ordered_terms(case, n)
     out = dev.zeros(4)
     K.hip.krh_ordered_sum(out.ptr, dev.put(t).ptr, n, s0)
+    ok()
+    got = out.get(np.float32, 1)[0]
+    want = seq_sum_f32(t, s0)
+    if np.isnan(want):
+        assert np.isnan(got)
+    else:
+        assert bits(np.float32(got)) == bits(np.float32(want)), (got, want)
+
+
+@pytest.mark.parametrize("s0", [0.0, 1234.5678])
+@pytest.mark.parametrize("case", ORDERED_CASES)
+@pytest.mark.parametrize("n", [1, 5, 31, 32, 33, 127, 128, 129, 2047, 2048, 2049, 4095, 4096])
+def test_ordered_sum_wave(dev, case, n, s0):
+    """the single-wave mode of the ordered sum (the batched softmax's), run by
+    a workgroup's second wave: the sequential fp32 sum's bits on every case"""
+    t = ordered_terms(case, n)
+    out = dev.zeros(4)
+    K.hip.krh_ordered_sum_wave(out.ptr, dev.put(t).ptr, n, s0)
     ok()
     got = out.get(np.float32, 1)[0]
     want = seq_sum_f32(t, s0)
