@@ -266,28 +266,44 @@ def reference_route(path, prompt, decode, gpu_ids):
     """the reference's own ml_run, its model and app code unchanged, bound to
     this backend through the ISA=hip op table (oracle/_ref/hip/ml_run, built
     from the reference's sources by oracle/Makefile): the same model file and
-    prompt, greedy; tok/s from its stderr lines (app/ml_run.c:406-410) and
-    whether its printed ids equal the native token loop's"""
+    prompt, greedy, and whether its printed ids equal the native token loop's.
+    Its prefill timer (app/ml_run.c:396-404) stops when the host has issued
+    the prefill, before the device has run it, so the rates come from two
+    runs' totals instead (positions / tok/s, app/ml_run.c:406-410): run A
+    prefills and decodes one token, run B decodes `decode`; decode tok/s =
+    (B positions - A positions) / (B time - A time), prefill tok/s =
+    prefilled / (A time - one decode step)."""
     exe = os.path.join(REF_DIR, "hip", "ml_run")
     if not os.path.exists(exe):
         return {"value": None, "error": "oracle/_ref/hip/ml_run is not built"}
+
+    def one(n):
+        r = subprocess.run([exe, path, "--tokens", ",".join(str(int(t)) for t in prompt), "-n", str(n), "-T", "0"],
+                           capture_output=True, text=True, timeout=600)
+        if r.returncode != 0:
+            raise RuntimeError("ml_run exited %d: %s" % (r.returncode, r.stderr[-300:]))
+        qm = re.search(r"positions: (\d+), tok/s: ([\d.]+)", r.stderr)
+        pm = re.search(r"prefill: (\d+) tokens in ([\d.]+) ms", r.stderr)
+        pos = int(qm.group(1))
+        return r.stdout, pos, pos / float(qm.group(2)), int(pm.group(1)) if pm else 0
+
+    try:
+        one(len(prompt))                                  # warm: page-in and first-launch costs
+        _, pa, ta, P = one(len(prompt))
+        out, pb, tb, _ = one(len(prompt) - 1 + decode)
+    except RuntimeError as e:
+        return {"value": None, "error": str(e)}
+    ids = np.array([int(v) for v in out.split()], dtype=np.int32)
+    step = (tb - ta) / (pb - pa)
     n = len(prompt) - 1 + decode
-    r = subprocess.run([exe, path, "--tokens", ",".join(str(int(t)) for t in prompt), "-n", str(n), "-T", "0"],
-                       capture_output=True, text=True, timeout=600)
-    if r.returncode != 0:
-        return {"value": None, "error": "ml_run exited %d: %s" % (r.returncode, r.stderr[-300:])}
-    ids = np.array([int(v) for v in r.stdout.split()], dtype=np.int32)
-    qm = re.search(r"positions: (\d+), tok/s: ([\d.]+)", r.stderr)
-    pm = re.search(r"prefill: (\d+) tokens in ([\d.]+) ms", r.stderr)
-    pos, X = int(qm.group(1)), float(qm.group(2))
-    P, M = (int(pm.group(1)), float(pm.group(2))) if pm else (0, 0.0)
-    dec = (pos - P) / (pos / X - M / 1000.0)
     k = min(len(ids), len(gpu_ids))
-    return {"value": round(dec, 3), "unit": "tok/s", "prefill_tok_s": round(P / (M / 1000.0), 2) if M > 0 else None,
+    return {"value": round((pb - pa) / (tb - ta), 3), "unit": "tok/s",
+            "prefill_tok_s": round(P / (ta - step), 2) if P and ta > step else None,
             "ids_equal_native": bool(k == n and np.array_equal(ids[:k], gpu_ids[:k])),
             "sample": "oracle/_ref/hip/ml_run (the reference's app/ml_run.c and model/transformer.c over the "
-                      "ISA=hip op table): %d-token prompt (%d prefilled), %d greedy decode tokens; decode tok/s = "
-                      "(positions - prefilled) / (positions / tok/s - prefill s)" % (len(prompt), P, pos - P)}
+                      "ISA=hip op table), greedy: %d-token prompt (%d prefilled) run to %d and to %d positions; "
+                      "decode tok/s = position difference / time difference, prefill tok/s = prefilled / "
+                      "(first run's time - one decode step)" % (len(prompt), P, pa, pb)}
 
 
 def cpu_baseline(path, prompt, decode, kv="f32", sample=None):

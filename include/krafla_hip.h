@@ -92,6 +92,14 @@ void krh_quantize_q8_t(int8_t *q, float *d, int dld, const float *x, int n, int 
 /* y = W x (k_scalar.c:4-37); accumulate != 0: y += W x, the residual add of
  * model/transformer.c:240-243 */
 void krh_matvec(float *y, const krh_mat *W, const int8_t *xq, const float *xd, int accumulate);
+/* y = W x and r += y in one launch (model/transformer.c:284-287: the
+ * projection into a scratch row, then ml_k_add into the residual); r and y
+ * do not overlap */
+void krh_matvec_residual(float *r, float *y, const krh_mat *W, const int8_t *xq, const float *xd);
+/* y[i] = W[i] x for nmat (1..3) matrices of one input length, type and
+ * scale kind, in one launch (the ml_matvec calls of model/transformer.c:273-275
+ * and :290-291 that share their input) */
+void krh_matvec_multi(float *const *y, const krh_mat *const *W, int nmat, const int8_t *xq, const float *xd);
 /* the same with a float input x[W->cols], quantized to Q8_0 first
  * (k_scalar.c:39-57) inside the launch */
 void krh_matvec_f(float *y, const krh_mat *W, const float *x, int accumulate);
@@ -110,6 +118,10 @@ void krh_matvec_qkv(float *q, float *kc, float *vc, const krh_mat *wq, const krh
 
 /* h = silu(w1 x) * (w3 x) (k_scalar.c:96-98; model/transformer.c:291-293) */
 void krh_matvec_swiglu(float *h, const krh_mat *w1, const krh_mat *w3, const int8_t *xq, const float *xd);
+/* the same, with u = w3 x stored as well (the two ml_matvec outputs and the
+ * ml_k_silu_mul of model/transformer.c:290-293, all three effects) */
+void krh_matvec_swiglu_keep(float *h, float *u, const krh_mat *w1, const krh_mat *w3, const int8_t *xq,
+                            const float *xd);
 
 /* krh_matvec_qkv and krh_matvec_swiglu with their input normalized first
  * (the attention and FFN norms, model/transformer.c:270-271, :288-289): x is
@@ -280,6 +292,22 @@ void krh_softmax(float *x, int n);                                              
 void krh_dot_rows(float *s, const float *q, const float *k, size_t ldk, int rows, int n, float scale); /* :111-117 */
 void krh_axpy_rows(float *y, const float *a, const float *x, size_t ldx, int rows, int n);              /* :119-122 */
 void krh_quantize_row(int8_t *q, float *d, const float *x, int n);    /* ops/ops.c:81-96: one scale for the row */
+/* The same ops over `rows` rows at once, row r of each pointer argument at
+ * p + r * ld_p elements (ld_p = 0: one vector shared by every row); each row
+ * gets the single call's bits. The batch form of the per-token loops of
+ * model/transformer.c:366-376 (token_task). rows <= KRH_ROWS_MAX. */
+enum { KRH_ROWS_MAX = 65535 };
+void krh_rmsnorm_rows(float *o, size_t ldo, const float *x, size_t ldx, const float *w, size_t ldw, int n,
+                      float eps, int rows);
+void krh_add_rows(float *y, size_t ldy, const float *x, size_t ldx, int n, int rows);
+void krh_rope_rows(float *q, size_t ldq, float *k, size_t ldk, const float *cos_t, size_t ldc, const float *sin_t,
+                   size_t lds, int head_dim, int n_heads, int n_kv_heads, int rows);
+void krh_silu_mul_rows(float *g, size_t ldg, const float *u, size_t ldu, int n, int rows);
+void krh_gelu_mul_rows(float *g, size_t ldg, const float *u, size_t ldu, int n, int rows);
+void krh_quantize_row_rows(int8_t *q, size_t ldq, float *d, size_t ldd, const float *x, size_t ldx, int n, int rows);
+/* Q8_0 of rows of n floats (k_scalar.c:39-57): q + r*ldq, scales d + r*ldd,
+ * x + r*ldx; x 16-byte and q 4-byte aligned, ldx and ldq multiples of 4 */
+void krh_quantize_q8_rows(int8_t *q, size_t ldq, float *d, size_t ldd, const float *x, size_t ldx, int n, int rows);
 void krh_softcap_rows(float *x, size_t ld, int rows, int n, float cap);    /* ops/ops.c:98-101, the C library's tanhf */
 /* *dst = value, in stream order (positions and token ids of op-table calls) */
 void krh_set_int(int *dst, int value);

@@ -49,6 +49,7 @@ struct MvArgs {
     int head_dim, ld_cache;
     const int *pos;
     int kv16;            // EPI_QKV: k and v rows are the F16 cache's (halves)
+    float *keep;         // EPI_ADD: receives the product W x as well; EPI_SWIGLU: receives w3 x
 };
 
 constexpr int MV_THREADS = 256;
@@ -484,7 +485,10 @@ __global__ void __launch_bounds__(MV_THREADS, 2) k_matvec(const MvArgs a) {
             if (EPI == EPI_STORE) {
                 if (lane < nr) pick3(mi, a.y[0], a.y[1], a.y[2])[row0 + lane] = sums[lane];
             } else if (EPI == EPI_ADD) {
-                if (lane < nr) pick3(mi, a.y[0], a.y[1], a.y[2])[row0 + lane] = kr_fadd(ep0, sums[lane]);
+                if (lane < nr) {
+                    pick3(mi, a.y[0], a.y[1], a.y[2])[row0 + lane] = kr_fadd(ep0, sums[lane]);
+                    if (a.keep) a.keep[row0 + lane] = sums[lane];
+                }
             } else if (EPI == EPI_QKV) {
                 // bias (model/transformer.c:276-277), then RoPE on q and k
                 // (k_scalar.c:79-94: pairs 2i, 2i+1 of each head, unfused)
@@ -516,6 +520,7 @@ __global__ void __launch_bounds__(MV_THREADS, 2) k_matvec(const MvArgs a) {
                 if (lane < nr) {
                     const float h1 = sums[lane], h3 = sums[nr + lane];
                     a.y[0][row0 + lane] = kr_fmul(kr_fdiv(h1, kr_fadd(1.0f, kr_expf(-h1))), h3);
+                    if (a.keep) a.keep[row0 + lane] = h3;
                 }
             }
         }
@@ -602,11 +607,12 @@ __global__ void __launch_bounds__(RN_THREADS) k_rmsnorm_q8(int8_t *q, float *d, 
 // Q8_0 of ntok rows of n floats, QZ_CHUNK values per workgroup: thread t
 // takes 4 consecutive values, 8 threads a 32-block (k_scalar.c:39-57).
 constexpr int QZ_CHUNK = 1024;
-__global__ void __launch_bounds__(256) k_quantize_q8(int8_t *q, float *d, int dld, const float *x, int n) {
+__global__ void __launch_bounds__(256) k_quantize_q8(int8_t *q, size_t ldq, float *d, size_t ldd, int dld,
+                                                    const float *x, size_t ldx, int n) {
     const size_t row = blockIdx.y;
     const int i = blockIdx.x * QZ_CHUNK + 4 * threadIdx.x;
     if (i >= n) return;   // n % 32 == 0: 8-thread groups are all in or all out
-    const float4 v = *(const float4 *)(x + row * n + i);
+    const float4 v = *(const float4 *)(x + row * ldx + i);
     float m = fmaxf(fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))), 0.0f);   // seeded with 0
     m = fmaxf(m, __shfl_xor(m, 1, 8));
     m = fmaxf(m, __shfl_xor(m, 2, 8));
@@ -619,10 +625,10 @@ __global__ void __launch_bounds__(256) k_quantize_q8(int8_t *q, float *d, int dl
         packed = (kr_q8_elem(v.x, id) & 0xff) | (kr_q8_elem(v.y, id) & 0xff) << 8 |
                  (kr_q8_elem(v.z, id) & 0xff) << 16 | (int)((unsigned)kr_q8_elem(v.w, id) << 24);
     }
-    *(int *)(q + row * n + i) = packed;
+    *(int *)(q + row * ldq + i) = packed;
     if ((i & 31) == 0) {
         if (dld > 0) d[(size_t)(i >> 5) * dld + row] = dd;
-        else d[row * (n / KR_QK) + (i >> 5)] = dd;
+        else d[row * ldd + (i >> 5)] = dd;
     }
 }
 
@@ -821,14 +827,28 @@ extern "C" void krh_quantize_q8_t(int8_t *q, float *d, int dld, const float *x, 
         kr_fail(ML_E_SHAPE, "quantize shape", hipSuccess);
         return;
     }
-    hipLaunchKernelGGL(k_quantize_q8, dim3((n + QZ_CHUNK - 1) / QZ_CHUNK, ntok), dim3(256), 0, kr_stream(), q, d, dld,
-                       x, n);
+    hipLaunchKernelGGL(k_quantize_q8, dim3((n + QZ_CHUNK - 1) / QZ_CHUNK, ntok), dim3(256), 0, kr_stream(), q,
+                       (size_t)n, d, (size_t)(n / KR_QK), dld, x, (size_t)n, n);
+    kr_check_launch("quantize_q8");
+}
+
+extern "C" void krh_quantize_q8_rows(int8_t *q, size_t ldq, float *d, size_t ldd, const float *x, size_t ldx, int n,
+                                     int rows) {
+    if (n % KR_QK || n <= 0 || rows < 0 || rows > KRH_ROWS_MAX || ldq % 4 || ldx % 4 || ((uintptr_t)x & 15) ||
+        ((uintptr_t)q & 3)) {
+        kr_fail(ML_E_SHAPE, "quantize_q8 rows: shape or alignment", hipSuccess);
+        return;
+    }
+    if (rows == 0) return;
+    hipLaunchKernelGGL(k_quantize_q8, dim3((n + QZ_CHUNK - 1) / QZ_CHUNK, rows), dim3(256), 0, kr_stream(), q, ldq, d,
+                       ldd, 0, x, ldx, n);
     kr_check_launch("quantize_q8");
 }
 
 static void mv_plain(float *y, const krh_mat *W, const int8_t *xq, const float *xd, const float *xf,
-                     const float *nw, float eps, int accumulate) {
+                     const float *nw, float eps, int accumulate, float *keep = nullptr) {
     MvArgs a = {};
+    a.keep = keep;
     a.m[0] = to_kmat(W);
     a.nmat = 1;
     a.R = mv_rows(W->cols, W->rows, 1, 64);
@@ -847,6 +867,38 @@ static void mv_plain(float *y, const krh_mat *W, const int8_t *xq, const float *
 
 extern "C" void krh_matvec(float *y, const krh_mat *W, const int8_t *xq, const float *xd, int accumulate) {
     mv_plain(y, W, xq, xd, nullptr, nullptr, 0.0f, accumulate);
+}
+
+extern "C" void krh_matvec_residual(float *r, float *y, const krh_mat *W, const int8_t *xq, const float *xd) {
+    mv_plain(r, W, xq, xd, nullptr, nullptr, 0.0f, 1, y);
+}
+
+extern "C" void krh_matvec_multi(float *const *y, const krh_mat *const *W, int nmat, const int8_t *xq,
+                                 const float *xd) {
+    if (nmat < 1 || nmat > 3) {
+        kr_fail(ML_E_SHAPE, "matvec_multi: 1 to 3 matrices", hipSuccess);
+        return;
+    }
+    for (int i = 1; i < nmat; i++)
+        if (W[i]->cols != W[0]->cols || W[i]->type != W[0]->type || W[i]->d16 != W[0]->d16) {
+            kr_fail(ML_E_SHAPE, "matvec_multi: one input length, type and scale kind", hipSuccess);
+            return;
+        }
+    MvArgs a = {};
+    int rows = 0;
+    for (int i = 0; i < nmat; i++) rows += W[i]->rows;
+    a.nmat = nmat;
+    a.R = mv_rows(W[0]->cols, rows, 1, 64);
+    a.tile0[0] = 0;
+    for (int i = 0; i < nmat; i++) {
+        a.m[i] = to_kmat(W[i]);
+        a.y[i] = y[i];
+        a.tile0[i + 1] = a.tile0[i] + (W[i]->rows + a.R - 1) / a.R;
+    }
+    a.xq = xq;
+    a.xd = xd;
+    a.K = W[0]->cols;
+    launch_mv<EPI_STORE>(a, a.m[0]);
 }
 
 extern "C" void krh_matvec_f(float *y, const krh_mat *W, const float *x, int accumulate) {
@@ -946,7 +998,7 @@ extern "C" void krh_rmsnorm_matvec_qkv_stage(float *q, float *k, float *v, const
 }
 
 static void swiglu(float *h, const krh_mat *w1, const krh_mat *w3, const int8_t *xq, const float *xd, const float *xf,
-                   const float *nw, float eps) {
+                   const float *nw, float eps, float *keep = nullptr) {
     if (w1->rows != w3->rows || w1->cols != w3->cols || w1->type != w3->type || w1->d16 != w3->d16) {
         kr_fail(ML_E_SHAPE, "swiglu shapes", hipSuccess);
         return;
@@ -965,7 +1017,13 @@ static void swiglu(float *h, const krh_mat *w1, const krh_mat *w3, const int8_t 
     a.eps = eps;
     a.K = w1->cols;
     a.y[0] = h;
+    a.keep = keep;
     launch_mv<EPI_SWIGLU>(a, a.m[0]);
+}
+
+extern "C" void krh_matvec_swiglu_keep(float *h, float *u, const krh_mat *w1, const krh_mat *w3, const int8_t *xq,
+                                       const float *xd) {
+    swiglu(h, w1, w3, xq, xd, nullptr, nullptr, 0.0f, u);
 }
 
 extern "C" void krh_matvec_swiglu(float *h, const krh_mat *w1, const krh_mat *w3, const int8_t *xq, const float *xd) {

@@ -196,6 +196,17 @@ for name, res, args in [
     ("krh_dot_rows", None, [_P, _P, _P, C.c_size_t, C.c_int, C.c_int, C.c_float]),
     ("krh_axpy_rows", None, [_P, _P, _P, C.c_size_t, C.c_int, C.c_int]),
     ("krh_quantize_row", None, [_P, _P, _P, C.c_int]),
+    ("krh_rmsnorm_rows", None, [_P, C.c_size_t, _P, C.c_size_t, _P, C.c_size_t, C.c_int, C.c_float, C.c_int]),
+    ("krh_add_rows", None, [_P, C.c_size_t, _P, C.c_size_t, C.c_int, C.c_int]),
+    ("krh_rope_rows", None, [_P, C.c_size_t, _P, C.c_size_t, _P, C.c_size_t, _P, C.c_size_t, C.c_int, C.c_int,
+                             C.c_int, C.c_int]),
+    ("krh_silu_mul_rows", None, [_P, C.c_size_t, _P, C.c_size_t, C.c_int, C.c_int]),
+    ("krh_gelu_mul_rows", None, [_P, C.c_size_t, _P, C.c_size_t, C.c_int, C.c_int]),
+    ("krh_quantize_row_rows", None, [_P, C.c_size_t, _P, C.c_size_t, _P, C.c_size_t, C.c_int, C.c_int]),
+    ("krh_quantize_q8_rows", None, [_P, C.c_size_t, _P, C.c_size_t, _P, C.c_size_t, C.c_int, C.c_int]),
+    ("krh_matvec_residual", None, [_P, _P, _P, _P, _P]),
+    ("krh_matvec_multi", None, [_P, _P, C.c_int, _P, _P]),
+    ("krh_matvec_swiglu_keep", None, [_P, _P, _P, _P, _P, _P]),
     ("krh_softcap_rows", None, [_P, C.c_size_t, C.c_int, C.c_int, C.c_float]),
     ("krh_set_int", None, [_P, C.c_int]), ("krh_transpose_scales", None, [_P, C.c_int, _P, C.c_int, C.c_int]),
     ("krh_gen_blocks", None, [_P, _P, C.c_uint64, C.c_int, C.c_int, C.c_int, C.c_int, C.c_float]),

@@ -1,7 +1,9 @@
 /* Compile-time kernel binding for ISA=hip: every ml_k_<op> the model and
- * ops code call resolves to the MI355X kernel set (kernels/hip/k_hip.h); the
- * F16/Q8 KV-cache kernels stay scalar (host buffers only: this backend runs
- * the F32 cache). The hip counterpart of the reference's config/ml_config.h:41-417. */
+ * ops code call resolves to the MI355X kernel set (kernels/hip/k_hip.h). The
+ * per-row F16/Q8 dot and axpy kernels stay scalar: the reference calls them
+ * only from its own attention loop (ops/ops.c), which this backend replaces
+ * with device attention over the F32 or Q8 cache (ml_attention in ml_hip.c).
+ * The hip counterpart of the reference's config/ml_config.h:41-417. */
 #ifndef ML_CONFIG_H
 #define ML_CONFIG_H
 

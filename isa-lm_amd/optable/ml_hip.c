@@ -20,6 +20,8 @@
  * any other buffer is staged to the device for the call and copied back.
  * The host reads activations only as logits: the classifier's matvec copies
  * them back and synchronizes, which is also where device errors surface.
+ * Row ops on arena buffers are queued and launched row-batched (below, "the
+ * per-token op queue"); every other call first launches what is queued.
  * Supported: the F32 and Q8 KV caches, models without embed_scale != 1, no
  * --imatrix (the F16 cache and those paths write or read arena memory on the
  * host). */
@@ -49,7 +51,7 @@ typedef struct {
 #define KH_RANGES 64
 static kh_range g_rg[KH_RANGES];
 static int g_nrg;
-static int *g_ints;                 /* device ints: [0] position, [1] token row */
+static int *g_ints;                 /* device ints: [0] position, [1] token row, [2] zero */
 static float *g_dT, *g_batt;        /* matmul scales, batched attention scratch */
 static size_t g_dT_n, g_batt_n;
 static const void *g_cls_q;         /* the classifier's quants (ml_model_pack) */
@@ -57,7 +59,7 @@ static int g_reported;
 
 static int ready(void) {
     if (krh_init() != ML_OK) return 0;
-    if (!g_ints) g_ints = krh_alloc(2 * sizeof(int));
+    if (!g_ints && (g_ints = krh_alloc(3 * sizeof(int)))) krh_set_int(g_ints + 2, 0);
     return g_ints != NULL;
 }
 
@@ -160,8 +162,17 @@ static void fail_call(const char *what) {
     g_reported = 1;
 }
 
-ml_status ml_hip_status(void) { return krh_status(); }
-const char *ml_hip_last_error(void) { return krh_last_error(); }
+
+#include "kh_queue.h"
+
+ml_status ml_hip_status(void) {
+    q_flush();
+    return krh_status();
+}
+const char *ml_hip_last_error(void) {
+    q_flush();
+    return krh_last_error();
+}
 
 /* ---- core/isa_check.c ---- */
 
@@ -202,6 +213,7 @@ void *ml_arena_alloc(ml_arena *a, size_t n) {
 
 void ml_arena_free(ml_arena *a) {
     if (a->base) {
+        q_flush();
         krh_sync();
         uint8_t *d = dev_addr(a->base, 1);
         drop_range(a->base);
@@ -220,6 +232,7 @@ ml_status ml_pool_create(ml_pool **p, int n) {
     (void)n;
     *p = NULL;
     if (!ready()) return ML_E_ISA;
+    q_flush();
     for (int i = 0; i < g_nrg; i++)   /* the arenas, as the host has filled them */
         if (!g_rg[i].uploaded) {
             if (krh_copy_h2d(g_rg[i].d, g_rg[i].h, g_rg[i].n) != ML_OK) return ML_E_IO;
@@ -234,13 +247,17 @@ ml_status ml_pool_create(ml_pool **p, int n) {
 void ml_pool_run(ml_pool *p, ml_task_fn fn, void *ctx) { (void)p; fn(ctx, 0, 1); }
 int ml_pool_size(const ml_pool *p) { (void)p; return 1; }
 int ml_pool_threads(int n) { (void)n; return 1; }
-void ml_pool_destroy(ml_pool *p) { free(p); }
+void ml_pool_destroy(ml_pool *p) {
+    q_flush();
+    free(p);
+}
 
 /* ---- model/pack_model.c: the model file to HBM, once ---- */
 
 ml_status ml_model_pack(ml_model *m, ml_pool *pool) {
     (void)pool;
     if (!ready()) return ML_E_ISA;
+    q_flush();
     const uint8_t *h = m->file.data;
     const size_t n = m->file.size;
     uint8_t *d = dev_addr(h, n);
@@ -269,6 +286,7 @@ int ml_pack_group(void) { return 0; }
 /* ---- core/quant_ref.c ---- */
 
 void ml_dequant_row(float *out, const ml_qtensor *W, int row) {
+    q_flush();
     if (dev_addr(out, sizeof(float) * (size_t)W->cols) && ready()) {   /* the embedding of ml_forward */
         kh_call c = { 0 };
         krh_mat m;
@@ -321,8 +339,24 @@ void ml_quantize_row_q4(int8_t *q, float *d, const float *x, int k) {
 
 #define F(n) (sizeof(float) * (size_t)(n))
 
+/* a product on arena buffers into the queue (not the classifier's: the host
+ * reads the logits next) */
+static int queue_matvec(float *y, const ml_qtensor *W, const ml_qact *x, int r0, int r1) {
+    if (W->q == g_cls_q) return 0;
+    const size_t nb = (size_t)W->cols / QK, rowq = W->type == ML_Q8_0 ? (size_t)W->cols : (size_t)W->cols / 2;
+    const size_t nr = (size_t)(r1 - r0);
+    const void *h[] = { y + r0, x->q, x->d, (const uint8_t *)W->q + (size_t)r0 * rowq,
+                        W->dh ? (const void *)(W->dh + (size_t)r0 * nb) : (const void *)(W->d + (size_t)r0 * nb) };
+    const size_t len[] = { F(nr), (size_t)W->cols, F(nb), nr * rowq, nr * nb * (W->dh ? 2 : 4) };
+    const int wr[] = { 1, 0, 0, 0, 0 };
+    g_qzero = g_ints + 2;
+    return q_push(QOP_MATVEC, (int)nr, W->cols, W->type | (W->dh ? 1 << 8 : 0), 0.0f, 5, h, len, wr);
+}
+
 static void matvec_rows(float *y, const ml_qtensor *W, const ml_qact *x, int r0, int r1) {
     if (r0 >= r1 || !ready()) return;
+    if (queue_matvec(y, W, x, r0, r1)) return;
+    q_flush();
     kh_call c = { 0 };
     krh_mat m;
     mat_of(&c, W, r0, r1, &m);
@@ -346,6 +380,11 @@ void ml_k_matvec_q4_hip(float *y, const ml_qtensor *W, const ml_qact *x, int r0,
 
 void ml_k_quantize_q8_hip(ml_qact *out, const float *x, int k) {
     if (!ready()) return;
+    const void *h[] = { out->q, out->d, x };
+    const size_t len[] = { (size_t)k, F(k / QK), F(k) };
+    const int wr[] = { 1, 1, 0 };
+    if (q_push(QOP_QUANT_Q8, k, 0, 0, 0.0f, 3, h, len, wr)) return;
+    q_flush();
     kh_call c = { 0 };
     const float *xd = arg(&c, x, F(k), 1, 0);
     int8_t *q = arg(&c, out->q, (size_t)k, 0, 1);
@@ -356,6 +395,11 @@ void ml_k_quantize_q8_hip(ml_qact *out, const float *x, int k) {
 
 void ml_k_rmsnorm_hip(float *o, const float *x, const float *w, int n, float eps) {
     if (!ready()) return;
+    const void *h[] = { o, x, w };
+    const size_t len[] = { F(n), F(n), F(n) };
+    const int wr[] = { 1, 0, 0 };
+    if (q_push(QOP_RMSNORM, n, 0, 0, eps, 3, h, len, wr)) return;
+    q_flush();
     kh_call c = { 0 };
     const float *xd = arg(&c, x, F(n), 1, 0), *wd = arg(&c, w, F(n), 1, 0);
     float *od = arg(&c, o, F(n), 0, 1);
@@ -365,6 +409,7 @@ void ml_k_rmsnorm_hip(float *o, const float *x, const float *w, int n, float eps
 
 void ml_k_softmax_hip(float *x, int n) {
     if (!ready()) return;
+    q_flush();
     kh_call c = { 0 };
     float *xd = arg(&c, x, F(n), 1, 1);
     if (!c.fail) krh_softmax(xd, n);
@@ -374,6 +419,11 @@ void ml_k_softmax_hip(float *x, int n) {
 void ml_k_rope_hip(float *q, float *k, const float *cos_t, const float *sin_t, int head_dim, int n_heads,
                    int n_kv_heads) {
     if (!ready()) return;
+    const void *h[] = { q, k, cos_t, sin_t };
+    const size_t len[] = { F(n_heads * head_dim), F(n_kv_heads * head_dim), F(head_dim / 2), F(head_dim / 2) };
+    const int wr[] = { 1, 1, 0, 0 };
+    if (q_push(QOP_ROPE, head_dim, n_heads, n_kv_heads, 0.0f, 4, h, len, wr)) return;
+    q_flush();
     kh_call c = { 0 };
     float *qd = arg(&c, q, F(n_heads * head_dim), 1, 1), *kd = arg(&c, k, F(n_kv_heads * head_dim), 1, 1);
     const float *cd = arg(&c, cos_t, F(head_dim / 2), 1, 0), *sd = arg(&c, sin_t, F(head_dim / 2), 1, 0);
@@ -381,8 +431,13 @@ void ml_k_rope_hip(float *q, float *k, const float *cos_t, const float *sin_t, i
     done(&c);
 }
 
-static void pair_op(void (*op)(float *, const float *, int), float *g, const float *u, int n) {
+static void pair_op(int qop, void (*op)(float *, const float *, int), float *g, const float *u, int n) {
     if (!ready()) return;
+    const void *h[] = { g, u };
+    const size_t len[] = { F(n), F(n) };
+    const int wr[] = { 1, 0 };
+    if (q_push(qop, n, 0, 0, 0.0f, 2, h, len, wr)) return;
+    q_flush();
     kh_call c = { 0 };
     float *gd = arg(&c, g, F(n), 1, 1);
     const float *ud = arg(&c, u, F(n), 1, 0);
@@ -390,12 +445,13 @@ static void pair_op(void (*op)(float *, const float *, int), float *g, const flo
     done(&c);
 }
 
-void ml_k_silu_mul_hip(float *g, const float *u, int n) { pair_op(krh_silu_mul, g, u, n); }
-void ml_k_gelu_mul_hip(float *g, const float *u, int n) { pair_op(krh_gelu_mul, g, u, n); }
-void ml_k_add_hip(float *y, const float *x, int n) { pair_op(krh_add, y, x, n); }
+void ml_k_silu_mul_hip(float *g, const float *u, int n) { pair_op(QOP_SILU_MUL, krh_silu_mul, g, u, n); }
+void ml_k_gelu_mul_hip(float *g, const float *u, int n) { pair_op(QOP_GELU_MUL, krh_gelu_mul, g, u, n); }
+void ml_k_add_hip(float *y, const float *x, int n) { pair_op(QOP_ADD, krh_add, y, x, n); }
 
 void ml_k_dot_f32_hip(float *s, const float *q, const float *k, size_t ldk, int rows, int n, float scale) {
     if (rows <= 0 || !ready()) return;
+    q_flush();
     kh_call c = { 0 };
     float *sd = arg(&c, s, F(rows), 0, 1);
     const float *qd = arg(&c, q, F(n), 1, 0), *kd = arg(&c, k, F((size_t)(rows - 1) * ldk + n), 1, 0);
@@ -405,6 +461,7 @@ void ml_k_dot_f32_hip(float *s, const float *q, const float *k, size_t ldk, int 
 
 void ml_k_axpy_f32_hip(float *y, const float *a, const float *x, size_t ldx, int rows, int n) {
     if (rows <= 0 || !ready()) return;
+    q_flush();
     kh_call c = { 0 };
     float *yd = arg(&c, y, F(n), 1, 1);
     const float *ad = arg(&c, a, F(rows), 1, 0), *xd = arg(&c, x, F((size_t)(rows - 1) * ldx + n), 1, 0);
@@ -425,6 +482,7 @@ void ml_matmul(ml_pool *pool, float *Y, int ldy, const ml_qtensor *W, const ml_q
     (void)pool;
     const int n = X->n, k = X->k, nb = k / QK, ldx = (n + 127) / 128 * 128;
     if (n <= 0 || !ready()) return;
+    q_flush();
     g_dT = grow(g_dT, &g_dT_n, F((size_t)nb * ldx));
     kh_call c = { 0 };
     krh_mat m;
@@ -453,6 +511,11 @@ void ml_matmul(ml_pool *pool, float *Y, int ldy, const ml_qtensor *W, const ml_q
 
 void ml_quantize_row(int8_t *q, float *d, const float *x, int n) {
     if (!ready()) return;
+    const void *h[] = { q, d, x };
+    const size_t len[] = { (size_t)n, F(1), F(n) };
+    const int wr[] = { 1, 1, 0 };
+    if (q_push(QOP_QUANT_ROW, n, 0, 0, 0.0f, 3, h, len, wr)) return;
+    q_flush();
     kh_call c = { 0 };
     const float *xd = arg(&c, x, F(n), 1, 0);
     int8_t *qd = arg(&c, q, (size_t)n, 0, 1);
@@ -463,6 +526,7 @@ void ml_quantize_row(int8_t *q, float *d, const float *x, int n) {
 
 void ml_softcap_rows(float *x, size_t ld, int rows, int n, float cap) {
     if (rows <= 0 || !ready()) return;
+    q_flush();
     kh_call c = { 0 };
     const size_t bytes = F((size_t)(rows - 1) * ld + n);
     float *xd = arg(&c, x, bytes, 1, 1);
@@ -493,7 +557,9 @@ static int attn_supported(const ml_kv_layer *kv, const ml_config *cfg) {
         fail_call("attention soft-capping is not built");
         return 0;
     }
-    return ready();
+    if (!ready()) return 0;
+    q_flush();
+    return 1;
 }
 
 /* the layer's cache as device pointers: F32 rows, or Q8 rows and their row

@@ -668,3 +668,140 @@ def test_rmsnorm_swiglu(dev, rows, cols, typ):
     u = oracle_matvec(q3, d3, rows, cols, typ, xq, xd)
     oracle.kro_silu_mul(g.ctypes.data, u.ctypes.data, rows)
     assert np.array_equal(bits(hb.get(np.float32, rows)), bits(g))
+
+
+@pytest.mark.parametrize("n,T", [(288, 37), (64, 5), (4096, 3)])
+def test_rows_ops_match_single_calls(dev, n, T):
+    """krh_<op>_rows over T rows with padded and zero row strides gives each
+    row the single call's bits and leaves the gaps between rows alone (the
+    op-table binding's batched replay of model/transformer.c:366-376)"""
+    H = K.hip
+    rng = np.random.default_rng(n + T)
+    pad = 36
+
+    def rows_pair(width, dtype=np.float32, fill=True):
+        a = (rng.standard_normal(T * width) * 3).astype(np.float32) if fill else np.zeros(T * width, np.float32)
+        if dtype is not np.float32:
+            a = np.zeros(T * width, dtype)
+        return dev.put(a), dev.put(a.copy()), a.nbytes
+
+    F = 4
+    ld = n + pad
+    x = dev.put((rng.standard_normal(T * ld) * 2).astype(np.float32))
+    x_host = x.get(np.float32, T * ld).copy()
+    x_host[ld:ld + n] = 0.0                                   # a row under the quantizers' tiny threshold
+    K.check(H.krh_copy_h2d(x.ptr, x_host.ctypes.data, x_host.nbytes), "copy")
+    w = dev.put(rng.standard_normal(n).astype(np.float32))
+
+    # rmsnorm: w shared by every row (stride 0)
+    o1, o2, nb = rows_pair(ld, fill=False)
+    H.krh_rmsnorm_rows(o1.ptr, ld, x.ptr, ld, w.ptr, 0, n, 1e-5, T)
+    for r in range(T):
+        H.krh_rmsnorm(o2.ptr + F * r * ld, x.ptr + F * r * ld, w.ptr, n, 1e-5)
+    ok()
+    assert np.array_equal(o1.get(np.uint32, T * ld), o2.get(np.uint32, T * ld))
+
+    # add (bias with stride 0, and a row-strided operand), silu_mul, gelu_mul
+    for name, single in (("add", H.krh_add), ("silu_mul", H.krh_silu_mul), ("gelu_mul", H.krh_gelu_mul)):
+        for xs in (0, ld):
+            y1, y2, _ = rows_pair(ld)
+            getattr(H, "krh_%s_rows" % name)(y1.ptr, ld, x.ptr, xs, n, T)
+            for r in range(T):
+                single(y2.ptr + F * r * ld, x.ptr + F * r * xs, n)
+            ok()
+            assert np.array_equal(y1.get(np.uint32, T * ld), y2.get(np.uint32, T * ld)), (name, xs)
+
+    # rope: q and k rows of heads, cos/sin rows of consecutive positions
+    hd = 64 if n >= 64 else 16
+    nh, nkv = max(1, n // hd), max(1, n // hd // 2)
+    ldq, ldk, h2 = nh * hd + 8, nkv * hd + 4, hd // 2
+    q1, q2, _ = rows_pair(ldq)
+    k1, k2, _ = rows_pair(ldk)
+    cs = dev.put(rng.uniform(-1, 1, (T + 3) * h2).astype(np.float32))
+    sn = dev.put(rng.uniform(-1, 1, (T + 3) * h2).astype(np.float32))
+    H.krh_rope_rows(q1.ptr, ldq, k1.ptr, ldk, cs.ptr + F * 3 * h2, h2, sn.ptr + F * 3 * h2, h2, hd, nh, nkv, T)
+    for r in range(T):
+        H.krh_rope(q2.ptr + F * r * ldq, k2.ptr + F * r * ldk, cs.ptr + F * (3 + r) * h2, sn.ptr + F * (3 + r) * h2,
+                   hd, nh, nkv)
+    ok()
+    assert np.array_equal(q1.get(np.uint32, T * ldq), q2.get(np.uint32, T * ldq))
+    assert np.array_equal(k1.get(np.uint32, T * ldk), k2.get(np.uint32, T * ldk))
+
+    # quantize_row (one scale per row, scales 3 floats apart) and Q8_0 rows
+    ldqb, ldd = n + 12, 3
+    qa, qb = dev.zeros(T * ldqb), dev.zeros(T * ldqb)
+    da, db = dev.zeros(F * T * ldd), dev.zeros(F * T * ldd)
+    H.krh_quantize_row_rows(qa.ptr, ldqb, da.ptr, ldd, x.ptr, ld, n, T)
+    for r in range(T):
+        H.krh_quantize_row(qb.ptr + r * ldqb, db.ptr + F * r * ldd, x.ptr + F * r * ld, n)
+    ok()
+    assert np.array_equal(qa.get(np.int8, T * ldqb), qb.get(np.int8, T * ldqb))
+    assert np.array_equal(da.get(np.uint32, T * ldd), db.get(np.uint32, T * ldd))
+    ldd8 = n // 32 + 5
+    qa, qb = dev.zeros(T * ldqb), dev.zeros(T * ldqb)
+    da, db = dev.zeros(F * T * ldd8), dev.zeros(F * T * ldd8)
+    H.krh_quantize_q8_rows(qa.ptr, ldqb, da.ptr, ldd8, x.ptr, ld, n, T)
+    for r in range(T):
+        H.krh_quantize_q8(qb.ptr + r * ldqb, db.ptr + F * r * ldd8, x.ptr + F * r * ld, n, 1)
+    ok()
+    assert np.array_equal(qa.get(np.int8, T * ldqb), qb.get(np.int8, T * ldqb))
+    assert np.array_equal(da.get(np.uint32, T * ldd8), db.get(np.uint32, T * ldd8))
+
+
+def test_rows_ops_reject_bad_shapes(dev):
+    """misaligned Q8_0 rows and row counts past KRH_ROWS_MAX are refused
+    before any launch, with ML_E_SHAPE"""
+    H = K.hip
+    buf = dev.zeros(4096)
+    H.krh_quantize_q8_rows(buf.ptr, 32, buf.ptr + 1024, 1, buf.ptr + 2048 + 4, 32, 32, 2)
+    assert H.krh_status() == K.ML_E_SHAPE
+    H.krh_clear_error()
+    H.krh_add_rows(buf.ptr, 0, buf.ptr, 0, 4, 65536)
+    assert H.krh_status() == K.ML_E_SHAPE
+    H.krh_clear_error()
+    ok()
+
+
+@pytest.mark.parametrize("rows,cols,typ,d16", [(768, 288, K.ML_Q8_0, 0), (4864, 896, K.ML_Q4_0, 1),
+                                               (14336, 4096, K.ML_Q8_0, 1), (40, 96, K.ML_Q8_0, 0)])
+def test_matvec_fused_op_sequences(dev, rows, cols, typ, d16):
+    """The launches the op-table binding fuses the reference's per-op calls
+    into, each with every effect of those calls: krh_matvec_swiglu_keep
+    (h = silu(w1 x) * (w3 x) and u = w3 x), krh_matvec_residual (y = W x,
+    r += y) and krh_matvec_multi (three products of one input), bit for bit
+    against the oracle's matvec, silu_mul and add"""
+    H = K.hip
+    mats = [rand_mat(rows, cols, typ, d16) for _ in range(2)]
+    W1, W3 = (dmat(dev, q, d, dh, rows, cols, typ, d16) for q, d, dh in mats)
+    xq, xd = O.quantize(f32(RNG.normal(0, 1, cols) * 30))
+    xqb, xdb = dev.put(xq), dev.put(xd)
+    g = oracle_matvec(mats[0][0], mats[0][1], rows, cols, typ, xq, xd)
+    u = oracle_matvec(mats[1][0], mats[1][1], rows, cols, typ, xq, xd)
+    h = g.copy()
+    oracle.kro_silu_mul(h.ctypes.data, u.ctypes.data, rows)
+
+    hb, ub = dev.zeros(4 * rows), dev.zeros(4 * rows)
+    H.krh_matvec_swiglu_keep(hb.ptr, ub.ptr, C.byref(W1), C.byref(W3), xqb.ptr, xdb.ptr)
+    ok()
+    assert np.array_equal(bits(hb.get(np.float32, rows)), bits(h))
+    assert np.array_equal(bits(ub.get(np.float32, rows)), bits(u))
+
+    r0 = f32(RNG.normal(0, 1, rows))
+    rb, yb = dev.put(r0), dev.zeros(4 * rows)
+    H.krh_matvec_residual(rb.ptr, yb.ptr, C.byref(W1), xqb.ptr, xdb.ptr)
+    ok()
+    assert np.array_equal(bits(yb.get(np.float32, rows)), bits(g))
+    assert np.array_equal(bits(rb.get(np.float32, rows)), bits((r0 + g).astype(np.float32)))
+
+    # three matrices of different row counts
+    rws = [rows, max(2, rows // 4), max(2, rows // 4) + 2]
+    ms = [rand_mat(r, cols, typ, d16) for r in rws]
+    Ws = [dmat(dev, q, d, dh, r, cols, typ, d16) for (q, d, dh), r in zip(ms, rws)]
+    ys = [dev.zeros(4 * r) for r in rws]
+    yp = (C.c_void_p * 3)(*[y.ptr for y in ys])
+    wp = (C.c_void_p * 3)(*[C.addressof(W) for W in Ws])
+    for nmat in (3, 2):
+        H.krh_matvec_multi(yp, wp, nmat, xqb.ptr, xdb.ptr)
+        ok()
+        for (q, d, dh), r, y in list(zip(ms, rws, ys))[:nmat]:
+            assert np.array_equal(bits(y.get(np.float32, r)), bits(oracle_matvec(q, d, r, cols, typ, xq, xd)))

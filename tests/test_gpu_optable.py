@@ -23,6 +23,14 @@ MODELS = {
                                hidden_dim=512, vocab=1000, max_seq=200, std=0.1, rope_orig_max_seq=64),
     "q8_f16_untied": dict(K.CONFIGS["llama8b_q8"], dim=256, n_layers=2, n_heads=4, n_kv_heads=1, hidden_dim=384,
                           vocab=700, max_seq=160, std=0.1),
+    # per-head q/k norms (heads_norm, model/transformer.c:246-248)
+    "qk_norm_q4mix": dict(K.CONFIGS["qwen05b_mixed"], dim=128, n_layers=2, n_heads=4, n_kv_heads=2, hidden_dim=256,
+                          vocab=512, max_seq=400, std=0.1, qk_norm=1, qkv_bias=0),
+    # post-norms, GELU, sliding-window layers with the local RoPE base
+    "post_norm_gelu_window": dict(K.CONFIGS["stories15m_q8"], dim=128, n_layers=3, n_heads=4, n_kv_heads=1,
+                                  hidden_dim=256, vocab=600, max_seq=400, std=0.1, qk_norm=1, post_norms=1, act=1,
+                                  sliding_window=40, layer_sliding=0b101, layer_local=0b101, rope_local_theta=1e4,
+                                  rope_theta=1e6),
 }
 
 
@@ -96,3 +104,23 @@ def test_ml_run_kv_f16_refused(workdir):
     r = subprocess.run([os.path.join(O.REF_DIR, "hip", "ml_run"), path, "--tokens", "1,2,3", "-n", "3", "-T", "0",
                         "--kv", "f16"], capture_output=True, text=True, timeout=300)
     assert "F16 KV cache" in r.stderr
+
+
+@pytest.mark.parametrize("name", ["qk_norm_q4mix", "post_norm_gelu_window", "llama3_rope_gqa_q4", "c1_q8"])
+def test_ml_run_long_prompt(name, workdir):
+    """A prompt over several batched prefill steps (128 tokens each,
+    model/transformer.h:48): the binding replays each step's per-token op
+    loops as row-batched launches; the --dump-logits bytes and the greedy ids
+    that follow match the scalar build's"""
+    path = model(name, workdir)
+    V, S = MODELS[name]["vocab"], MODELS[name]["max_seq"]
+    n = min(300, S - 40)
+    toks = [int(t) for t in np.random.default_rng(5).integers(1, V, n)]
+    a, b = path + ".scalar.long.logits", path + ".hip.long.logits"
+    O.ref_ml_run(path, toks, n, dump=a)
+    O.ref_ml_run(path, toks, n, dump=b, isa="hip")
+    x, y = np.fromfile(a, dtype=np.uint8), np.fromfile(b, dtype=np.uint8)
+    assert x.size == n * V * 4 and np.array_equal(x, y)
+    want, _ = O.ref_ml_run(path, toks, n + 32)
+    got, _ = O.ref_ml_run(path, toks, n + 32, isa="hip")
+    assert np.array_equal(got, want)
