@@ -488,7 +488,6 @@ ml_status kr_state_new(kr_state **out, kr_model *m, int kv_type) {
     if (st == ML_OK && local) st = krh_copy_h2d(s->rope_sin_l, snl, f * half);
     free(cs); free(sn); free(csl); free(snl);
     s->batch = c->max_seq < KR_PREFILL_STEP ? c->max_seq : KR_PREFILL_STEP;
-    if (fam) s->batch = 1;   /* the batched prefill kernels fuse RoPE: these models replay the decode step */
     const char *ev = getenv("KRAFLA_EAGER");
     s->eager = ev && ev[0] == '1';
     if (st == ML_OK && !s->eager) st = capture(s, &s->g_logits, STEP_LOGITS);
@@ -534,7 +533,6 @@ ml_status kr_state_set_sampler(kr_state *s, const krh_sampler_opts *o) {
 
 void kr_state_set_batch(kr_state *s, int batch) {
     if (batch < 1) batch = KR_PREFILL_STEP;
-    if (s->family) batch = 1;
     if (batch > s->m->cfg.max_seq) batch = s->m->cfg.max_seq;
     if (batch != s->batch && s->bmem) {   /* re-sized on next use */
         krh_free(s->bmem);
@@ -589,11 +587,11 @@ static ml_status batch_buffers(kr_state *s, int with_logits) {
     struct { void **p; size_t n; } parts[] = {
         { (void **)&s->bx, f * L * c->dim }, { (void **)&s->bq, f * L * c->q_dim },
         { (void **)&s->bao, f * L * c->q_dim }, { (void **)&s->bh1, f * L * c->hidden_dim },
-        { (void **)&s->bh3, f * L * c->hidden_dim }, { (void **)&s->batt, f * L * c->n_heads * (size_t)c->max_seq },
+        { (void **)&s->bh3, f * L * (c->hidden_dim > c->dim ? c->hidden_dim : c->dim) }, { (void **)&s->batt, f * L * c->n_heads * (size_t)c->max_seq },
         { (void **)&s->bxq, L * wide }, { (void **)&s->bxd, f * L * (wide / QK) },
         { (void **)&s->blog, with_logits ? f * L * c->vocab : 0 },
-        { (void **)&s->bkst, s->kv_type != ML_F32 ? f * L * c->kv_dim : 0 },
-        { (void **)&s->bvst, s->kv_type != ML_F32 ? f * L * c->kv_dim : 0 },
+        { (void **)&s->bkst, s->kv_type != ML_F32 || s->family ? f * L * c->kv_dim : 0 },
+        { (void **)&s->bvst, s->kv_type != ML_F32 || s->family ? f * L * c->kv_dim : 0 },
     };
     size_t total = 0;
     for (size_t i = 0; i < sizeof parts / sizeof parts[0]; i++) total += RUP(parts[i].n);
@@ -606,6 +604,84 @@ static ml_status batch_buffers(kr_state *s, int with_logits) {
     }
     s->ldx = ldx;
     return ML_OK;
+}
+
+/* rmsnorm of rows rows of n floats in place, w shared, in launches of at
+ * most KRH_ROWS_MAX rows (the per-head norms of a batch) */
+static void norm_rows(float *x, const float *w, int n, float eps, long rows) {
+    for (long r = 0; r < rows; r += KRH_ROWS_MAX) {
+        const int k = rows - r < KRH_ROWS_MAX ? (int)(rows - r) : KRH_ROWS_MAX;
+        krh_rmsnorm_rows(x + (size_t)r * n, (size_t)n, x + (size_t)r * n, (size_t)n, w, 0, n, eps, k);
+    }
+}
+
+/* A block's output y [T][dim] into the residual x (residual_add,
+ * model/transformer.c:240-243): normalized first when the model has
+ * post-norms */
+static void residual_rows(kr_state *s, float *y, const float *post_norm, int T) {
+    const ml_config *c = &s->m->cfg;
+    if (post_norm) krh_rmsnorm_rows(y, (size_t)c->dim, y, (size_t)c->dim, post_norm, 0, c->dim, c->norm_eps, T);
+    krh_add_rows(s->bx, (size_t)c->dim, y, (size_t)c->dim, c->dim, T);
+}
+
+/* One batched layer of a model with q/k-norm, post-norms, GELU or
+ * soft-capped scores: the per-token stages of model/transformer.c:324-365
+ * (token_stage) as row launches over the T tokens, the products as int8
+ * MFMA matmuls without fused RoPE. K and V rows go straight into an F32
+ * cache's rows (its rows are the projections' outputs, :390-391), else to
+ * the staging rows that store_kv converts. */
+static void family_prefill_layer(kr_state *s, int l, int T, int p0) {
+    const kr_model *m = s->m;
+    const ml_config *c = &m->cfg;
+    const struct kr_dev_layer *D = &m->d_layers[l];
+    const ml_layer *L = &m->layers[l];
+    const int ldx = s->ldx, hd = c->head_dim, h2 = hd / 2;
+    const size_t lkv = (size_t)c->max_seq * c->kv_dim;
+    const float *cs = L->local_rope ? s->rope_cos_l : s->rope_cos, *sn = L->local_rope ? s->rope_sin_l : s->rope_sin;
+    const int f32 = s->kv_type == ML_F32;
+    float *k = f32 ? (float *)s->kcache + (size_t)l * lkv + (size_t)p0 * c->kv_dim : s->bkst;
+    float *v = f32 ? (float *)s->vcache + (size_t)l * lkv + (size_t)p0 * c->kv_dim : s->bvst;
+    krh_rmsnorm_q8_t(s->bxq, s->bxd, ldx, NULL, s->bx, D->attn_norm, c->dim, c->norm_eps, T);   /* TOK_ATTN_IN */
+    krh_matmul(s->bq, c->q_dim, &D->wq, s->bxq, s->bxd, ldx, T, 0);
+    krh_matmul(k, c->kv_dim, &D->wk, s->bxq, s->bxd, ldx, T, 0);
+    krh_matmul(v, c->kv_dim, &D->wv, s->bxq, s->bxd, ldx, T, 0);
+    if (D->bq) {   /* TOK_QKV_OUT */
+        krh_add_rows(s->bq, (size_t)c->q_dim, D->bq, 0, c->q_dim, T);
+        krh_add_rows(k, (size_t)c->kv_dim, D->bk, 0, c->kv_dim, T);
+        krh_add_rows(v, (size_t)c->kv_dim, D->bv, 0, c->kv_dim, T);
+    }
+    if (D->q_norm) {
+        norm_rows(s->bq, D->q_norm, hd, c->norm_eps, (long)T * c->n_heads);
+        norm_rows(k, D->k_norm, hd, c->norm_eps, (long)T * c->n_kv_heads);
+    }
+    krh_rope_rows(s->bq, (size_t)c->q_dim, k, (size_t)c->kv_dim, cs + (size_t)p0 * h2, (size_t)h2,
+                  sn + (size_t)p0 * h2, (size_t)h2, hd, c->n_heads, c->n_kv_heads, T);
+    if (!f32) store_kv(s, l, s->bkst, s->bvst, T);
+    const ml_kv_layer kv = kv_layer(s, l);
+    krh_attention_kv_softcap(s->bao, s->batt, s->bq, &kv, c->n_heads, c->n_kv_heads, hd, c->max_seq,
+                             c->attn_scale, s->pos, T, p0 + T - 1, c->attn_softcap);
+    krh_quantize_q8_t(s->bxq, s->bxd, ldx, s->bao, c->q_dim, T);   /* TOK_WO_IN */
+    if (D->post_attn_norm) {   /* TOK_FFN_IN: bh3 holds the block's output rows [T][dim] */
+        krh_matmul(s->bh3, c->dim, &D->wo, s->bxq, s->bxd, ldx, T, 0);
+        residual_rows(s, s->bh3, D->post_attn_norm, T);
+    } else {
+        krh_matmul(s->bx, c->dim, &D->wo, s->bxq, s->bxd, ldx, T, 1);
+    }
+    krh_rmsnorm_q8_t(s->bxq, s->bxd, ldx, NULL, s->bx, D->ffn_norm, c->dim, c->norm_eps, T);
+    krh_matmul(s->bh1, c->hidden_dim, &D->w1, s->bxq, s->bxd, ldx, T, 0);
+    krh_matmul(s->bh3, c->hidden_dim, &D->w3, s->bxq, s->bxd, ldx, T, 0);
+    if (c->act == ML_ACT_GELU_TANH) {   /* TOK_DOWN_IN */
+        krh_gelu_mul_rows(s->bh1, (size_t)c->hidden_dim, s->bh3, (size_t)c->hidden_dim, c->hidden_dim, T);
+        krh_quantize_q8_t(s->bxq, s->bxd, ldx, s->bh1, c->hidden_dim, T);
+    } else {
+        krh_silu_quant(s->bxq, s->bxd, ldx, s->bh1, s->bh3, c->hidden_dim, T);
+    }
+    if (D->post_ffn_norm) {   /* TOK_RESID */
+        krh_matmul(s->bh3, c->dim, &D->w2, s->bxq, s->bxd, ldx, T, 0);
+        residual_rows(s, s->bh3, D->post_ffn_norm, T);
+    } else {
+        krh_matmul(s->bx, c->dim, &D->w2, s->bxq, s->bxd, ldx, T, 1);
+    }
 }
 
 /* One batched step (model/transformer.c:385-425): T tokens at positions
@@ -625,6 +701,10 @@ static ml_status prefill_step(kr_state *s, const int *tokens, int T, int p0, flo
         const struct kr_dev_layer *D = &m->d_layers[l];
         const ml_layer *L = &m->layers[l];
         const float *cs = L->local_rope ? s->rope_cos_l : s->rope_cos, *sn = L->local_rope ? s->rope_sin_l : s->rope_sin;
+        if (s->family) {
+            family_prefill_layer(s, l, T, p0);
+            continue;
+        }
         krh_rmsnorm_q8_t(s->bxq, s->bxd, ldx, NULL, s->bx, D->attn_norm, c->dim, c->norm_eps, T);
         if (s->kv_type == ML_F32) {
             float *kc = (float *)s->kcache + (size_t)l * lkv, *vc = (float *)s->vcache + (size_t)l * lkv;
@@ -651,6 +731,8 @@ static ml_status prefill_step(kr_state *s, const int *tokens, int T, int p0, flo
     if (logits) {
         krh_rmsnorm_q8_t(s->bxq, s->bxd, ldx, NULL, s->bx, m->d_final_norm, c->dim, c->norm_eps, T);
         krh_matmul(s->blog, c->vocab, &m->d_wcls, s->bxq, s->bxd, ldx, T, 0);
+        if (c->final_softcap > 0.0f)   /* model/transformer.c:304 */
+            krh_softcap_rows(s->blog, (size_t)c->vocab, T, c->vocab, c->final_softcap);
         st = krh_copy_d2h(logits, s->blog, sizeof(float) * (size_t)T * c->vocab);
         if (st != ML_OK) return kr_seterr(st, "%s", krh_last_error());
     }

@@ -22,9 +22,12 @@
  * them back and synchronizes, which is also where device errors surface.
  * Row ops on arena buffers are queued and launched row-batched (below, "the
  * per-token op queue"); every other call first launches what is queued.
- * Supported: the F32 and Q8 KV caches, models without embed_scale != 1, no
- * --imatrix (the F16 cache and those paths write or read arena memory on the
- * host). */
+ * The embedding's scale (model/transformer.c:228-229, a host loop over the
+ * row) is applied on the device by ml_dequant_row instead, so the host loop
+ * only touches the arena's host copy, which nothing reads.
+ * Supported: the F32 and Q8 KV caches, no --imatrix (the F16 cache's
+ * conversion and the importance statistics read activations on the host:
+ * model/transformer.c:195-197, :250-255). */
 #include <math.h>
 #include <stdio.h>
 #include <stdlib.h>
@@ -55,6 +58,8 @@ static int *g_ints;                 /* device ints: [0] position, [1] token row,
 static float *g_dT, *g_batt;        /* matmul scales, batched attention scratch */
 static size_t g_dT_n, g_batt_n;
 static const void *g_cls_q;         /* the classifier's quants (ml_model_pack) */
+static const ml_qtensor *g_emb;     /* the embedding table and its row scale (ml_model_pack) */
+static float g_emb_scale = 1.0f;
 static int g_reported;
 
 static int ready(void) {
@@ -272,6 +277,8 @@ ml_status ml_model_pack(ml_model *m, ml_pool *pool) {
         return ML_E_IO;
     }
     g_cls_q = m->wcls.q;
+    g_emb = &m->tok_emb;
+    g_emb_scale = m->cfg.embed_scale;
     return ML_OK;
 }
 
@@ -294,7 +301,7 @@ void ml_dequant_row(float *out, const ml_qtensor *W, int row) {
         float *o = arg(&c, out, sizeof(float) * (size_t)W->cols, 0, 1);
         if (!c.fail) {
             krh_set_int(g_ints + 1, 0);
-            krh_embed(o, &m, g_ints + 1, 1.0f);
+            krh_embed(o, &m, g_ints + 1, W == g_emb ? g_emb_scale : 1.0f);
         }
         done(&c);
         return;
@@ -553,10 +560,6 @@ static int attn_supported(const ml_kv_layer *kv, const ml_config *cfg) {
         fail_call("attention without KV cache rows");
         return 0;
     }
-    if (cfg->attn_softcap > 0.0f) {
-        fail_call("attention soft-capping is not built");
-        return 0;
-    }
     if (!ready()) return 0;
     q_flush();
     return 1;
@@ -594,8 +597,8 @@ void ml_attention(ml_pool *pool, float *out, const float *q, const ml_kv_layer *
     const ml_kv_layer d = dev_kv(&c, kv, cfg);
     if (!c.fail) {
         krh_set_int(g_ints, pos);
-        krh_attention_kv(o, att, qv, &d, cfg->n_heads, cfg->n_kv_heads, cfg->head_dim, cfg->max_seq,
-                         cfg->attn_scale, g_ints, 1, cfg->max_seq - 1);
+        krh_attention_kv_softcap(o, att, qv, &d, cfg->n_heads, cfg->n_kv_heads, cfg->head_dim, cfg->max_seq,
+                                 cfg->attn_scale, g_ints, 1, cfg->max_seq - 1, cfg->attn_softcap);
     }
     done(&c);
 }
@@ -612,8 +615,8 @@ void ml_attention_batch(ml_pool *pool, float *out, const float *q, const ml_kv_l
     const ml_kv_layer d = dev_kv(&c, kv, cfg);
     if (!c.fail && g_batt) {
         krh_set_int(g_ints, pos0);
-        krh_attention_kv(o, g_batt, qv, &d, cfg->n_heads, cfg->n_kv_heads, cfg->head_dim, cfg->max_seq,
-                         cfg->attn_scale, g_ints, n, pos0 + n - 1);
+        krh_attention_kv_softcap(o, g_batt, qv, &d, cfg->n_heads, cfg->n_kv_heads, cfg->head_dim, cfg->max_seq,
+                                 cfg->attn_scale, g_ints, n, pos0 + n - 1, cfg->attn_softcap);
     }
     done(&c);
 }

@@ -181,3 +181,35 @@ def test_family_model_matches_reference(name, kv, workdir):
     assert np.array_equal(got_ids, want_ids)
     s.close()
     m.close()
+
+
+@pytest.mark.parametrize("kv", sorted(KV))
+@pytest.mark.parametrize("name", ["qk_norm_bias_gqa", "qk_post_norms_f16", "window_local_rope_layers",
+                                  "gelu_softcap_gemma2", "gelu_post_qk_gemma3"])
+def test_family_batched_prefill(name, kv, workdir):
+    """the families' batched prefill (token_stage's per-token stages as row
+    launches, model/transformer.c:324-365) over a prompt that passes the
+    sliding windows, in one step, in ragged steps of 7 and token by token:
+    every position's logits equal ml_run --dump-logits"""
+    spec = FAMILY.get(name) or VARIANTS[name]
+    path = os.path.join(workdir, "fam_" + name + ".mlb")
+    if not os.path.exists(path):
+        K.gen_mlb(path, **spec)
+    m = K.Model(path)
+    V = m.cfg.vocab
+    n = min(m.cfg.max_seq - 2, 90)
+    toks = [int(t) for t in np.random.default_rng(9).integers(1, V, n)]
+    dump = path + "." + kv + ".long.logits"
+    print("family batched", name, kv, n, flush=True)
+    O.ref_ml_run(path, toks, n, dump=dump, extra=("--kv", kv))
+    want = np.fromfile(dump, dtype=np.float32).reshape(n, V)
+    for batch in (0, 7, 1):
+        s = K.State(m, KV[kv])
+        if batch:
+            s.set_batch(batch)
+        got = np.empty((n, V), dtype=np.float32)
+        s.prefill(toks, 0, logits=got)
+        s.close()
+        bad = np.nonzero(~np.all(bits(got) == bits(want), axis=1))[0]
+        assert bad.size == 0, "batch %d: positions %s differ" % (batch, bad[:8])
+    m.close()

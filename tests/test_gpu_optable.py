@@ -31,6 +31,12 @@ MODELS = {
                                   hidden_dim=256, vocab=600, max_seq=400, std=0.1, qk_norm=1, post_norms=1, act=1,
                                   sliding_window=40, layer_sliding=0b101, layer_local=0b101, rope_local_theta=1e4,
                                   rope_theta=1e6),
+    # the embedding's scale (applied on the device by ml_dequant_row) and
+    # soft-capped scores and logits
+    "softcap_embed_scale": dict(K.CONFIGS["stories15m_q8"], dim=128, n_layers=2, n_heads=4, n_kv_heads=2,
+                                hidden_dim=256, vocab=600, max_seq=400, std=0.1, post_norms=1, act=1,
+                                embed_scale=11.3137, attn_softcap=50.0, final_softcap=30.0, sliding_window=32,
+                                layer_sliding=0b01),
 }
 
 
@@ -106,7 +112,8 @@ def test_ml_run_kv_f16_refused(workdir):
     assert "F16 KV cache" in r.stderr
 
 
-@pytest.mark.parametrize("name", ["qk_norm_q4mix", "post_norm_gelu_window", "llama3_rope_gqa_q4", "c1_q8"])
+@pytest.mark.parametrize("name", ["qk_norm_q4mix", "post_norm_gelu_window", "softcap_embed_scale",
+                                  "llama3_rope_gqa_q4", "c1_q8"])
 def test_ml_run_long_prompt(name, workdir):
     """A prompt over several batched prefill steps (128 tokens each,
     model/transformer.h:48): the binding replays each step's per-token op
