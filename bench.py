@@ -159,7 +159,9 @@ def calibration_adds(K, reps=3):
 
 
 def committed_traffic():
-    """HBM bytes per SwiGLU launch from the committed counter summary, or None"""
+    """HBM bytes per SwiGLU launch from the committed counter summary, or None;
+    it was counted on the 8B shape's w1|w3 (its algorithmic_bytes), so other
+    workloads report no traffic"""
     try:
         with open(TRAFFIC_FILE) as f:
             return json.load(f)
@@ -296,10 +298,10 @@ def reference_route(path, prompt, decode, gpu_ids):
     ids = np.array([int(v) for v in out.split()], dtype=np.int32)
     step = (tb - ta) / (pb - pa)
     n = len(prompt) - 1 + decode
-    k = min(len(ids), len(gpu_ids))
+    k = min(len(ids), len(gpu_ids)) if gpu_ids is not None else 0
     return {"value": round((pb - pa) / (tb - ta), 3), "unit": "tok/s",
             "prefill_tok_s": round(P / (ta - step), 2) if P and ta > step else None,
-            "ids_equal_native": bool(k == n and np.array_equal(ids[:k], gpu_ids[:k])),
+            "ids_equal_native": bool(k == n and np.array_equal(ids[:k], gpu_ids[:k])) if gpu_ids is not None else None,
             "sample": "oracle/_ref/hip/ml_run (the reference's app/ml_run.c and model/transformer.c over the "
                       "ISA=hip op table), greedy: %d-token prompt (%d prefilled) run to %d and to %d positions; "
                       "decode tok/s = position difference / time difference, prefill tok/s = prefilled / "
@@ -363,6 +365,8 @@ def main():
     ap.add_argument("--reference-route", action="store_true",
                     help="also time the reference's unchanged ml_run over this backend's ISA=hip op table on the "
                          "same model and prompt")
+    ap.add_argument("--route-only", action="store_true",
+                    help="only the reference route on the generated model (for profiling it alone)")
     ap.add_argument("--roofline-reps", type=int, default=3)
     ap.add_argument("--roofline-only", action="store_true",
                     help="only the timed SwiGLU launches and the k_add calibration launches (the command "
@@ -396,6 +400,12 @@ def main():
         dev_bytes = K.host.kr_model_device_bytes(model.ptr)
         log("uploaded %.2f GB to HBM in %.1f s" % (dev_bytes / 1e9, time.time() - t0))
         prompt = np.random.default_rng(2048).integers(1, V, P).astype(np.int32)
+        if args.route_only:
+            state.close()
+            model.close()
+            route = reference_route(path, prompt, args.steps, None)
+            print(json.dumps({"workload": desc, "reference_route": route}), flush=True)
+            return
         if args.roofline_only:
             ms, nbytes = time_swiglu(K, model, state, args.roofline_reps)
             calibration_adds(K)
@@ -484,7 +494,8 @@ def main():
                                "rmsnorm + Q8_0 of x, w1|w3 rows, SiLU(w1 x) * (w3 x)), as the decode step issues it",
                      "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4),
-                     "traffic": traffic["bytes_per_launch"] if traffic else None,
+                     "traffic": traffic["bytes_per_launch"] if traffic and
+                     traffic.get("algorithmic_bytes") == nbytes else None,
                      "bytes_per_launch": nbytes, "avg_launch_us": round(ms * 1e3, 2),
                      "measured_read_peak": hbm, "frac_of_measured_read_peak": round(gbs / hbm, 4)},
         "prefill_roofline": pre_rl,

@@ -44,6 +44,7 @@ struct MmArgs {
     const float *bias[3];
     const float *rope_cos, *rope_sin;
     int head_dim, pos0;
+    int ng;              // row groups per wave (the kernel's NG)
 };
 
 constexpr int MM_TT = 128;   // tokens per workgroup
@@ -68,10 +69,12 @@ __device__ __forceinline__ v4i weight_frag(const uint8_t *blk, int h) {
     return r;
 }
 
-// A wave computes MM_NG row groups x 1 token group of 32 (MM_NG MFMA tiles
-// per block); the workgroup's 4 waves take 4 token groups of the same rows.
-constexpr int MM_NG = 4;
-constexpr int MM_TR = 32 * MM_NG;   // weight rows per workgroup
+// A wave computes NG row groups x 1 token group of 32 (NG MFMA tiles per
+// block); the workgroup's 4 waves take 4 token groups of the same 32 NG rows.
+// NG = 4 when the grid of 128-row tiles fills the device (long prompts);
+// NG = 1 gives four times the workgroups for short batches (the reference's
+// 128-token prefill steps), whose few 128-row tiles would leave most CUs idle
+// with each tile's VALU work in series.
 
 // Per wave and block: the wave's 32 tokens and their scales.
 struct XFrag {
@@ -88,9 +91,10 @@ struct WReg {
 
 constexpr int MM_ST = 3;   // LDS ring stages of the weight tile
 
+template <int NG>
 struct MmLds {
-    v4i w[MM_ST][MM_TR][2];       // [stage][row][half]
-    uint32_t d[MM_ST][MM_TR];     // [stage][row] raw scale bits
+    v4i w[MM_ST][32 * NG][2];     // [stage][row][half]
+    uint32_t d[MM_ST][32 * NG];   // [stage][row] raw scale bits
 };
 
 __device__ __forceinline__ void x_load(XFrag &f, const MmArgs &a, int b, int tokl, int lane) {
@@ -100,16 +104,21 @@ __device__ __forceinline__ void x_load(XFrag &f, const MmArgs &a, int b, int tok
     f.xs = a.xdT[(size_t)b * a.ldx + t];
 }
 
-template <int QT, int D16>
+// thread tid loads half tid % 2 of tile row (tid / 2) mod 32 NG (for NG < 4
+// the surplus threads repeat a row's load, which keeps every load
+// unconditional; only the first 64 NG store it)
+template <int QT, int D16, int NG>
 __device__ __forceinline__ void w_load(WReg &R, const MMat &W, int nb, int b, int rowl, int tid) {
-    int r = rowl + (tid >> 1);
+    int r = rowl + ((tid >> 1) & (32 * NG - 1));
     r = r < W.rows ? r : W.rows - 1;   // rows past the end re-read the last row (not stored)
     const size_t blk = (size_t)r * nb + b;
     R.w = weight_frag<QT>(W.q + blk * (QT == ML_Q8_0 ? 32 : 16), tid & 1);
     R.d = D16 ? (uint32_t)((const uint16_t *)W.d)[blk] : ((const uint32_t *)W.d)[blk];
 }
 
-__device__ __forceinline__ void w_store(MmLds &L, int st, const WReg &R, int tid) {
+template <int NG>
+__device__ __forceinline__ void w_store(MmLds<NG> &L, int st, const WReg &R, int tid) {
+    if ((tid >> 1) >= 32 * NG) return;
     L.w[st][tid >> 1][tid & 1] = R.w;
     if ((tid & 1) == 0) L.d[st][tid >> 1] = R.d;
 }
@@ -120,13 +129,13 @@ __device__ __forceinline__ void w_store(MmLds &L, int st, const WReg &R, int tid
 // them, over the LDS crossbar: one 4-byte load per lane and block instead of
 // four 16-byte broadcast loads. The weight fragments and scales come from
 // the workgroup's LDS tile.
-template <int D16>
-__device__ __forceinline__ void mm_step(float (&acc)[MM_NG][16], const XFrag &f, const MmLds &L, int st, int lane) {
+template <int D16, int NG>
+__device__ __forceinline__ void mm_step(float (&acc)[NG][16], const XFrag &f, const MmLds<NG> &L, int st, int lane) {
     const int ln = lane & 31, hf = lane >> 5;
-    v4i wb[MM_NG];
-    uint32_t wdr[MM_NG];
+    v4i wb[NG];
+    uint32_t wdr[NG];
 #pragma unroll
-    for (int g = 0; g < MM_NG; g++) {
+    for (int g = 0; g < NG; g++) {
         wb[g] = L.w[st][32 * g + ln][hf];
         wdr[g] = L.d[st][32 * g + ln];
     }
@@ -136,9 +145,9 @@ __device__ __forceinline__ void mm_step(float (&acc)[MM_NG][16], const XFrag &f,
     for (int r = 0; r < 16; r++) xd[r] = __shfl(f.xs, 8 * (r >> 2) + hb + (r & 3), 64);
     v16i s = __builtin_amdgcn_mfma_i32_32x32x32_i8(f.xa, wb[0], v16i{}, 0, 0, 0);
 #pragma unroll
-    for (int g = 0; g < MM_NG; g++) {
+    for (int g = 0; g < NG; g++) {
         v16i sn;
-        if (g + 1 < MM_NG) sn = __builtin_amdgcn_mfma_i32_32x32x32_i8(f.xa, wb[g + 1], v16i{}, 0, 0, 0);
+        if (g + 1 < NG) sn = __builtin_amdgcn_mfma_i32_32x32x32_i8(f.xa, wb[g + 1], v16i{}, 0, 0, 0);
         // keeps the next MFMA from being hoisted further: two result sets
         // live instead of four
         __builtin_amdgcn_sched_barrier(0);
@@ -146,19 +155,19 @@ __device__ __forceinline__ void mm_step(float (&acc)[MM_NG][16], const XFrag &f,
 #pragma unroll
         for (int r = 0; r < 16; r++)
             acc[g][r] = kr_fadd(acc[g][r], kr_fmul(kr_fmul((float)s[r], wd), xd[r]));
-        if (g + 1 < MM_NG) s = sn;
+        if (g + 1 < NG) s = sn;
     }
 }
 
-// Workgroup = 4 waves over a 128-row x 128-token tile; wave w takes all 128
-// rows (4 row groups) and tokens 32 w .. 32 w + 31. The 256 threads load
-// each block's 128 x 32-byte weight tile and its scales once (16 bytes and
+// Workgroup = 4 waves over a 32 NG-row x 128-token tile; wave w takes all
+// the tile's rows (NG row groups) and tokens 32 w .. 32 w + 31. The 256
+// threads load each block's weight tile and its scales once (16 bytes and
 // one scale per thread) into an LDS ring of 3 stages: block b + 1 is stored
 // during step b into the stage step b - 2 read, and the barrier closing each
 // step orders those stores before step b + 1 reads them.
-template <int EPI, int QT, int D16>
+template <int EPI, int QT, int D16, int NG>
 __global__ void __launch_bounds__(256, 2) k_matmul(const MmArgs a) {
-    __shared__ MmLds L;
+    __shared__ MmLds<NG> L;
     int mi = 0;
     while (mi + 1 < a.nmat && (int)blockIdx.x >= a.tile0[mi + 1]) mi++;
     const MMat W = mi == 0 ? a.w[0] : (mi == 1 ? a.w[1] : a.w[2]);
@@ -166,12 +175,12 @@ __global__ void __launch_bounds__(256, 2) k_matmul(const MmArgs a) {
     const int local = (int)blockIdx.x - a.tile0[mi];
     const int rt = local / ntt, tt = local - rt * ntt;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int rowl = rt * MM_TR, tokl = tt * MM_TT + 32 * wave;
+    const int rowl = rt * 32 * NG, tokl = tt * MM_TT + 32 * wave;
     const int nb = a.K / KR_QK;
 
-    float acc[MM_NG][16];
+    float acc[NG][16];
 #pragma unroll
-    for (int g = 0; g < MM_NG; g++)
+    for (int g = 0; g < NG; g++)
 #pragma unroll
         for (int r = 0; r < 16; r++) acc[g][r] = 0.0f;
 
@@ -183,9 +192,9 @@ __global__ void __launch_bounds__(256, 2) k_matmul(const MmArgs a) {
     const int bl = nb - 1;
     WReg R;
     XFrag x0, x1;
-    w_load<QT, D16>(R, W, nb, 0, rowl, tid);
+    w_load<QT, D16, NG>(R, W, nb, 0, rowl, tid);
     w_store(L, 0, R, tid);
-    w_load<QT, D16>(R, W, nb, 1 < bl ? 1 : bl, rowl, tid);
+    w_load<QT, D16, NG>(R, W, nb, 1 < bl ? 1 : bl, rowl, tid);
     x_load(x0, a, 0, tokl, lane);
     x_load(x1, a, 1 < bl ? 1 : bl, tokl, lane);
     __syncthreads();
@@ -193,13 +202,13 @@ __global__ void __launch_bounds__(256, 2) k_matmul(const MmArgs a) {
     for (int b = 0; b < nb; b += 2) {
         const int s1 = st == MM_ST - 1 ? 0 : st + 1, s2 = s1 == MM_ST - 1 ? 0 : s1 + 1;
         w_store(L, s1, R, tid);
-        w_load<QT, D16>(R, W, nb, b + 2 < bl ? b + 2 : bl, rowl, tid);
-        mm_step<D16>(acc, x0, L, st, lane);
+        w_load<QT, D16, NG>(R, W, nb, b + 2 < bl ? b + 2 : bl, rowl, tid);
+        mm_step<D16, NG>(acc, x0, L, st, lane);
         x_load(x0, a, b + 2 < bl ? b + 2 : bl, tokl, lane);
         __syncthreads();
         w_store(L, s2, R, tid);
-        w_load<QT, D16>(R, W, nb, b + 3 < bl ? b + 3 : bl, rowl, tid);
-        if (b + 1 < nb) mm_step<D16>(acc, x1, L, s1, lane);
+        w_load<QT, D16, NG>(R, W, nb, b + 3 < bl ? b + 3 : bl, rowl, tid);
+        if (b + 1 < nb) mm_step<D16, NG>(acc, x1, L, s1, lane);
         x_load(x1, a, b + 3 < bl ? b + 3 : bl, tokl, lane);
         __syncthreads();
         st = s2;
@@ -210,7 +219,7 @@ __global__ void __launch_bounds__(256, 2) k_matmul(const MmArgs a) {
     const int ldy = mi == 0 ? a.ldy[0] : (mi == 1 ? a.ldy[1] : a.ldy[2]);
     const float *bias = mi == 0 ? a.bias[0] : (mi == 1 ? a.bias[1] : a.bias[2]);
 #pragma unroll
-    for (int g = 0; g < MM_NG; g++) {
+    for (int g = 0; g < NG; g++) {
         const int row = rowl + 32 * g + (lane & 31);
         const bool rin = row < W.rows;
 #pragma unroll
@@ -247,10 +256,18 @@ void launch_mm(const MmArgs &a, const MMat &W) {
         return;
     }
     auto go = [&](auto kern) { hipLaunchKernelGGL(kern, dim3(grid), dim3(256), 0, kr_stream(), a); };
-    if (W.type == ML_Q8_0) {
-        if (W.d16) go(k_matmul<EPI, ML_Q8_0, 1>); else go(k_matmul<EPI, ML_Q8_0, 0>);
+    if (a.ng == 4) {
+        if (W.type == ML_Q8_0) {
+            if (W.d16) go(k_matmul<EPI, ML_Q8_0, 1, 4>); else go(k_matmul<EPI, ML_Q8_0, 0, 4>);
+        } else {
+            if (W.d16) go(k_matmul<EPI, ML_Q4_0, 1, 4>); else go(k_matmul<EPI, ML_Q4_0, 0, 4>);
+        }
     } else {
-        if (W.d16) go(k_matmul<EPI, ML_Q4_0, 1>); else go(k_matmul<EPI, ML_Q4_0, 0>);
+        if (W.type == ML_Q8_0) {
+            if (W.d16) go(k_matmul<EPI, ML_Q8_0, 1, 1>); else go(k_matmul<EPI, ML_Q8_0, 0, 1>);
+        } else {
+            if (W.d16) go(k_matmul<EPI, ML_Q4_0, 1, 1>); else go(k_matmul<EPI, ML_Q4_0, 0, 1>);
+        }
     }
     kr_check_launch("matmul");
 }
@@ -260,7 +277,15 @@ MMat to_mmat(const krh_mat *m) {
     return k;
 }
 
-int row_tiles(int rows) { return (rows + MM_TR - 1) / MM_TR; }
+int row_tiles(int rows, int ng) { return (rows + 32 * ng - 1) / (32 * ng); }
+
+// NG for a launch over these row counts and ntt token tiles: 4 when its
+// 128-row tiles give every CU two workgroups, else 1
+int pick_ng(int rows0, int rows1, int rows2, int ntt) {
+    const int tiles = row_tiles(rows0, 4) + row_tiles(rows1, 4) + row_tiles(rows2, 4);
+    const int cus = krh_device_cus() > 0 ? krh_device_cus() : 256;
+    return (long)tiles * ntt >= 2L * cus ? 4 : 1;
+}
 
 // ---- per-token work of a batched step ----
 
@@ -320,7 +345,9 @@ extern "C" void krh_matmul(float *Y, int ldy, const krh_mat *W, const int8_t *xq
     a.w[0] = to_mmat(W);
     a.nmat = 1;
     a.tile0[0] = 0;
-    a.tile0[1] = row_tiles(W->rows) * ((T + MM_TT - 1) / MM_TT);
+    const int ntt = (T + MM_TT - 1) / MM_TT;
+    a.ng = pick_ng(W->rows, 0, 0, ntt);
+    a.tile0[1] = row_tiles(W->rows, a.ng) * ntt;
     a.xq = xq;
     a.xdT = xdT;
     a.ldx = ldx;
@@ -366,10 +393,11 @@ static void matmul_qkv(float *q, float *kc, float *vc, const krh_mat *wq, const 
     a.rope_sin = rope_sin;
     a.head_dim = head_dim;
     a.pos0 = pos0;
+    a.ng = pick_ng(wq->rows, wk->rows, wv->rows, ntt);
     a.tile0[0] = 0;
-    a.tile0[1] = row_tiles(wq->rows) * ntt;
-    a.tile0[2] = a.tile0[1] + row_tiles(wk->rows) * ntt;
-    a.tile0[3] = a.tile0[2] + row_tiles(wv->rows) * ntt;
+    a.tile0[1] = row_tiles(wq->rows, a.ng) * ntt;
+    a.tile0[2] = a.tile0[1] + row_tiles(wk->rows, a.ng) * ntt;
+    a.tile0[3] = a.tile0[2] + row_tiles(wv->rows, a.ng) * ntt;
     if (wv->type == wq->type) {
         a.nmat = 3;
         launch_mm<MM_QKV>(a, a.w[0]);
@@ -380,7 +408,7 @@ static void matmul_qkv(float *q, float *kc, float *vc, const krh_mat *wq, const 
     launch_mm<MM_QKV>(b, b.w[0]);
     MmArgs c = a;   // v alone, as matrix 2 of the same epilogue
     c.tile0[0] = c.tile0[1] = c.tile0[2] = 0;
-    c.tile0[3] = row_tiles(wv->rows) * ntt;
+    c.tile0[3] = row_tiles(wv->rows, a.ng) * ntt;
     c.w[0] = c.w[1] = c.w[2];
     c.nmat = 3;
     launch_mm<MM_QKV>(c, c.w[2]);
