@@ -90,6 +90,7 @@ struct WReg {
 };
 
 constexpr int MM_ST = 3;   // LDS ring stages of the weight tile
+constexpr int MM_PD = 8;   // NG = 1: blocks of load lookahead (even: the LDS stage of step k is k % 2)
 
 template <int NG>
 struct MmLds {
@@ -190,28 +191,61 @@ __global__ void __launch_bounds__(256, 2) k_matmul(const MmArgs a) {
     // the prefetch. Only the odd tail's step is conditional; every thread
     // reaches every barrier.
     const int bl = nb - 1;
-    WReg R;
-    XFrag x0, x1;
-    w_load<QT, D16, NG>(R, W, nb, 0, rowl, tid);
-    w_store(L, 0, R, tid);
-    w_load<QT, D16, NG>(R, W, nb, 1 < bl ? 1 : bl, rowl, tid);
-    x_load(x0, a, 0, tokl, lane);
-    x_load(x1, a, 1 < bl ? 1 : bl, tokl, lane);
-    __syncthreads();
-    int st = 0;   // stage of block b
-    for (int b = 0; b < nb; b += 2) {
-        const int s1 = st == MM_ST - 1 ? 0 : st + 1, s2 = s1 == MM_ST - 1 ? 0 : s1 + 1;
-        w_store(L, s1, R, tid);
-        w_load<QT, D16, NG>(R, W, nb, b + 2 < bl ? b + 2 : bl, rowl, tid);
-        mm_step<D16, NG>(acc, x0, L, st, lane);
-        x_load(x0, a, b + 2 < bl ? b + 2 : bl, tokl, lane);
+    if constexpr (NG == 4) {
+        WReg R;
+        XFrag x0, x1;
+        w_load<QT, D16, NG>(R, W, nb, 0, rowl, tid);
+        w_store(L, 0, R, tid);
+        w_load<QT, D16, NG>(R, W, nb, 1 < bl ? 1 : bl, rowl, tid);
+        x_load(x0, a, 0, tokl, lane);
+        x_load(x1, a, 1 < bl ? 1 : bl, tokl, lane);
         __syncthreads();
-        w_store(L, s2, R, tid);
-        w_load<QT, D16, NG>(R, W, nb, b + 3 < bl ? b + 3 : bl, rowl, tid);
-        if (b + 1 < nb) mm_step<D16, NG>(acc, x1, L, s1, lane);
-        x_load(x1, a, b + 3 < bl ? b + 3 : bl, tokl, lane);
+        int st = 0;   // stage of block b
+        for (int b = 0; b < nb; b += 2) {
+            const int s1 = st == MM_ST - 1 ? 0 : st + 1, s2 = s1 == MM_ST - 1 ? 0 : s1 + 1;
+            w_store(L, s1, R, tid);
+            w_load<QT, D16, NG>(R, W, nb, b + 2 < bl ? b + 2 : bl, rowl, tid);
+            mm_step<D16, NG>(acc, x0, L, st, lane);
+            x_load(x0, a, b + 2 < bl ? b + 2 : bl, tokl, lane);
+            __syncthreads();
+            w_store(L, s2, R, tid);
+            w_load<QT, D16, NG>(R, W, nb, b + 3 < bl ? b + 3 : bl, rowl, tid);
+            if (b + 1 < nb) mm_step<D16, NG>(acc, x1, L, s1, lane);
+            x_load(x1, a, b + 3 < bl ? b + 3 : bl, tokl, lane);
+            __syncthreads();
+            st = s2;
+        }
+    } else {
+        // One row group: a block's VALU work is a quarter of NG = 4's, too
+        // little to cover a load's latency, so the weight and token loads
+        // run MM_PD blocks ahead in register rings (R[j], x[j]: the blocks
+        // congruent to j mod MM_PD), and the weight tile passes through a
+        // 2-stage LDS ring. Step t stores block t + 1 (loaded MM_PD steps
+        // earlier) into stage (t + 1) % 2, loads block t + 1 + MM_PD in its
+        // place, runs block t from stage t % 2 and reloads x with block
+        // t + MM_PD; the barrier closing each step orders the stage writes
+        // against the reads of the steps either side.
+        WReg R[MM_PD];
+        XFrag x[MM_PD];
+#pragma unroll
+        for (int j = 0; j < MM_PD; j++) {
+            w_load<QT, D16, NG>(R[j], W, nb, j < bl ? j : bl, rowl, tid);
+            x_load(x[j], a, j < bl ? j : bl, tokl, lane);
+        }
+        w_store(L, 0, R[0], tid);
+        w_load<QT, D16, NG>(R[0], W, nb, MM_PD < bl ? MM_PD : bl, rowl, tid);
         __syncthreads();
-        st = s2;
+        for (int b0 = 0; b0 < nb; b0 += MM_PD) {
+#pragma unroll
+            for (int k = 0; k < MM_PD; k++) {
+                const int t = b0 + k, k1 = (k + 1) % MM_PD;
+                w_store(L, (k + 1) & 1, R[k1], tid);
+                w_load<QT, D16, NG>(R[k1], W, nb, t + 1 + MM_PD < bl ? t + 1 + MM_PD : bl, rowl, tid);
+                if (t < nb) mm_step<D16, NG>(acc, x[k], L, k & 1, lane);
+                x_load(x[k], a, t + MM_PD < bl ? t + MM_PD : bl, tokl, lane);
+                __syncthreads();
+            }
+        }
     }
 
     // epilogue: lane = one row (32 g + lane % 32), tokens 8 (r / 4) + 4 (lane / 32) + r % 4
