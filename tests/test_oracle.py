@@ -545,3 +545,21 @@ def test_forward_matches_reference_kv(name, kv, workdir):
     ids_ref, _ = O.ref_ml_run(path, toks[:5], steps, extra=("--kv", kv))
     assert np.array_equal(om.generate(toks[:5], steps), ids_ref)
     om.close()
+
+
+def test_integration_stub_compiles(tmp_path):
+    """the reference-side C stub in INTEGRATION.md compiles against include/
+    and links against both libraries (no calls: no GPU here)"""
+    import re
+    import subprocess
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    text = open(os.path.join(root, "INTEGRATION.md")).read()
+    blocks = re.findall(r"```c\n(.*?)```", text, re.S)
+    stub = next(b for b in blocks if "ml_main_hip" in b)
+    src = tmp_path / "ml_run_hip.c"
+    src.write_text(stub + "\nint main(void) { return 0; }\n")
+    lib = os.path.join(root, "isa-lm_amd")
+    r = subprocess.run(["gcc", "-std=c11", "-Wall", "-Werror", str(src), "-I", os.path.join(root, "include"),
+                        "-L", lib, "-lkrafla", "-lkrafla_hip", "-Wl,-rpath," + lib, "-o", str(tmp_path / "stub")],
+                       capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr
