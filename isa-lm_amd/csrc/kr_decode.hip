@@ -540,14 +540,14 @@ __global__ void __launch_bounds__(MV_THREADS, 2) k_matvec(const MvArgs a) {
     }
 }
 
-// workgroups resident at once: two per compute unit
-constexpr int MV_RESIDENT = 512;
+// workgroups resident at once: two per compute unit of this device (512 on
+// an MI355X's 256 CUs)
+int mv_resident() { return 2 * (krh_device_cus() > 0 ? krh_device_cus() : 256); }
 
 // Rows per tile (one wave's): the largest power of two (at most cap, even for
 // the RoPE pairs) that still gives every resident wave a tile; blocks per
 // chunk: as many as MV_NPT slots per lane allow (a multiple of 4, for the
 // 16-byte term reads).
-constexpr int MV_MIN_TILES = MV_RESIDENT * MV_WAVES;
 constexpr int MV_MAX_LOC = 8;   // local rows per tile: a row's chunk then spans >= 32 blocks (1 KB of Q8_0)
 
 int mv_rows(int K, int total_rows, int local_per_row, int cap) {
@@ -555,7 +555,7 @@ int mv_rows(int K, int total_rows, int local_per_row, int cap) {
     int R = cap / local_per_row;
     if (R * local_per_row > 64) R = 64 / local_per_row;
     if (R * local_per_row > MV_MAX_LOC) R = MV_MAX_LOC / local_per_row;
-    while (R > 2 && (total_rows + R - 1) / R < MV_MIN_TILES) R /= 2;
+    while (R > 2 && (total_rows + R - 1) / R < mv_resident() * MV_WAVES) R /= 2;
     if (R > 1) R &= ~1;
     return R < 1 ? 1 : R;
 }
@@ -574,7 +574,7 @@ void launch_mv(MvArgs &a, const KMat &W) {
     const size_t lds = mv_lds(a.K, nloc, a.nbc, a.nw != nullptr).total;
     const int ntiles = a.tile0[a.nmat];
     const int wgs = (ntiles + MV_WAVES - 1) / MV_WAVES;
-    const int grid = wgs > MV_RESIDENT ? MV_RESIDENT : wgs;
+    const int grid = wgs > mv_resident() ? mv_resident() : wgs;
     if (a.K % KR_QK || lds > 64 * 1024 || grid <= 0 || nloc > 64 || nloc * a.nbc > MV_NPT * 64 ||
         (!a.xq && !a.xf)) {
         kr_fail(ML_E_SHAPE, "matvec shape", hipSuccess);
