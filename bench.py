@@ -41,6 +41,13 @@ Also reported on the same line:
                   on this host's cores: the 2047-token prefill, then 32
                   greedy decode tokens at positions 2047..2078, the positions
                   the GPU decodes
+  matvec_cpu_baseline  the reference's ml_bench kernel table (no model,
+                  single-threaded) on one pinned core: its 4096x4096 matvec
+                  rows in GB/s, beside the GPU matvec microbench
+  reference_route (--reference-route) the reference's unchanged ml_run over
+                  this backend's ISA=hip op table on the same model and
+                  prompt: decode and prefill tok/s and whether its ids equal
+                  the native loop's
 """
 import argparse
 import ctypes as C
@@ -308,6 +315,31 @@ def reference_route(path, prompt, decode, gpu_ids):
                       "(first run's time - one decode step)" % (len(prompt), P, pa, pb)}
 
 
+def cpu_matvec_baseline():
+    """the reference's ml_bench kernel table (no model, app/ml_bench.c:37-61:
+    single-threaded), pinned to one core, on its best CPU build: GB/s of the
+    4096x4096 and 14336x4096-class matvec rows, weight and scale bytes as
+    app/ml_bench.c:39 counts them"""
+    for isa in ("avx512vnni", "avx2"):
+        exe = os.path.join(REF_DIR, isa, "ml_bench")
+        if not os.path.exists(exe):
+            continue
+        cmd = ([shutil.which("taskset"), "-c", str(min(os.sched_getaffinity(0)))] if shutil.which("taskset") else []) + [exe]
+        r = subprocess.run(cmd, capture_output=True, text=True, timeout=300)
+        if r.returncode == 3:
+            continue
+        if r.returncode != 0:
+            return {"value": None, "error": "ml_bench %s exited %d" % (isa, r.returncode)}
+        rows = []
+        for line in r.stdout.splitlines():
+            f = line.split()
+            if len(f) >= 4 and f[0].startswith("matvec_") and f[1] in ("4096x4096",):
+                rows.append({"op": f[0], "shape": f[1], "gbs": float(f[3])})
+        return {"kind": "reference", "build": "ISA=%s" % isa, "cores": 1, "rows": rows,
+                "sample": "ml_bench with no model (its kernel table), one pinned core"}
+    return {"value": None, "error": "no reference CPU build in oracle/_ref"}
+
+
 def cpu_baseline(path, prompt, decode, kv="f32", sample=None):
     """the reference's ml_run on the same model file, KV cache type and
     sampling options, on this host's cores"""
@@ -455,10 +487,14 @@ def main():
         row = cfg.kv_dim * {"f32": 4, "f16": 2, "q8": 1}[args.kv] + (4 * cfg.n_kv_heads if args.kv == "q8" else 0)
         kv_tok = int(2 * cfg.n_layers * (p_mean + 2) * row)
         mv = None if args.no_matvec else matvec_microbench(K)
+        mv_cpu = None
         if mv:
             for r in mv:
                 log("matvec %s: %.1f GB/s resident, %.1f GB/s rotating" % (r["shape"], r["gbs_resident"],
                                                                            r["gbs_hbm_rotating"]))
+            if not args.no_cpu_baseline:
+                mv_cpu = cpu_matvec_baseline()
+                log("matvec cpu baseline: %s" % json.dumps(mv_cpu))
         route = None
         if args.reference_route:
             t0 = time.time()
@@ -500,6 +536,7 @@ def main():
                      "measured_read_peak": hbm, "frac_of_measured_read_peak": round(gbs / hbm, 4)},
         "prefill_roofline": pre_rl,
         "matvec": mv,
+        "matvec_cpu_baseline": mv_cpu,
         "cpu_baseline": cpu,
     }
     if route is not None:
