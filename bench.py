@@ -30,7 +30,9 @@ Also reported on the same line:
                   SwiGLU launches and the calibration launches
   prefill_roofline  the dominant prefill kernel (the int8-MFMA matmul of w1
                   over the 2047 prompt tokens): int8 TOP/s against the
-                  5.0 POP/s peak and against the exact-order VALU bound
+                  5.0 POP/s peak, against the exact-order VALU bound, and
+                  against the measured int8 MFMA issue rate (a kernel of
+                  back-to-back 32x32x32 MFMAs on register operands)
   matvec          the isolated Q4_0/Q8_0 matvec microbench (4096x4096 and
                   14336x4096, f16 scales, activation quantize_q8(N(0,1))):
                   GB/s over 1000 launches, cache-resident (one matrix) and
@@ -150,6 +152,28 @@ def hbm_read_peak(K, nbytes=4 << 30, reps=4):
     return round(best, 1)
 
 
+def mfma_int8_rate(K, iters=4096, reps=3):
+    """the achievable int8 MFMA rate (TOP/s): the best of a few grid sizes of
+    a kernel issuing only 32x32x32 int8 MFMAs on register operands (four
+    independent accumulators per wave), HIP events around each launch"""
+    cus = K.hip.krh_device_cus()
+    out = K.DevBuf(4 * 4 * 16 * cus)
+    t = K.hip.krh_timer_new()
+    best = 0.0
+    for grid in (cus, 2 * cus, 4 * cus, 16 * cus // 4):
+        K.hip.krh_mfma_rate(out.ptr, grid, iters)
+        for _ in range(reps):
+            K.hip.krh_timer_mark(t, 0)
+            K.hip.krh_mfma_rate(out.ptr, grid, iters)
+            K.hip.krh_timer_mark(t, 1)
+            ops = 4.0 * grid * iters * 4 * 65536
+            best = max(best, ops / (K.hip.krh_timer_ms(t) * 1e-3) / 1e12)
+    K.check(K.hip.krh_sync(), "mfma rate")
+    K.hip.krh_timer_free(t)
+    out.free()
+    return round(best, 1)
+
+
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "swiglu_matvec_traffic.json")
 CAL_N = 64 << 20   # k_add calibration: y += x over 64 Mi floats reads 512 MiB and writes 256 MiB
 
@@ -256,6 +280,7 @@ def prefill_roofline(K, model, ntok, prefill_s, reps=2):
     for b in (xq, xd, y):
         b.free()
     us = total / n * 1e3
+    mfma = mfma_int8_rate(K)
     ops = 2.0 * rows * cols * T
     tops = ops / (us * 1e-6) / 1e12
     valu_tops = 64 * K.hip.krh_device_cus() * 2.4e9 * (2 * 32 / 4) / 1e12   # int8 ops per exact-order VALU lane-op: 64 / 4
@@ -268,6 +293,7 @@ def prefill_roofline(K, model, ntok, prefill_s, reps=2):
             "achieved": round(tops, 1), "peak": 5000.0, "unit": "TOP/s", "frac": round(tops / 5000.0, 4),
             "avg_launch_us": round(us, 1), "valu_bound": round(valu_tops, 1),
             "frac_of_valu_bound": round(tops / valu_tops, 4),
+            "measured_mfma_int8_tops": mfma, "frac_of_measured_mfma": round(tops / mfma, 4) if mfma else None,
             "whole_prefill_int8_tops": round(layer_ops * T / prefill_s / 1e12, 1) if prefill_s else None}
 
 

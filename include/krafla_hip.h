@@ -284,6 +284,11 @@ void krh_add(float *y, const float *x, int n);                                  
  * 16) at p once with `grid` workgroups; out[grid] receives an XOR fold of
  * each workgroup's words. Times the plain HBM read rate. */
 void krh_stream_read(unsigned *out, const void *p, size_t bytes, int grid);
+/* Measurement op (no reference counterpart): grid workgroups of 4 waves,
+ * each wave iters x 4 int8 MFMAs of 32x32x32 (65,536 int8 operations each)
+ * on register operands; out[4 * grid] receives one word per wave. Times the
+ * achievable int8 MFMA rate. */
+void krh_mfma_rate(int *out, int grid, int iters);
 void krh_rope(float *q, float *k, const float *cos_t, const float *sin_t, int head_dim, int n_heads,
               int n_kv_heads);                                                           /* :79-94 */
 void krh_silu_mul(float *g, const float *u, int n);                                     /* :96-98 */

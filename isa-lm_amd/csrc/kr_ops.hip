@@ -245,6 +245,38 @@ extern "C" void krh_stream_read(unsigned *out, const void *p, size_t bytes, int 
     kr_check_launch("stream_read");
 }
 
+// Int8 MFMA issue rate (a measurement op): every wave runs iters rounds of
+// four independent v_mfma_i32_32x32x32_i8 accumulations (65,536 int8
+// operations each) on register operands, then stores one word per wave
+// (out[wave]) so that no MFMA is dropped.
+__global__ void __launch_bounds__(256) k_mfma_rate(int *out, int iters) {
+    typedef int v4i __attribute__((ext_vector_type(4)));
+    typedef int v16i __attribute__((ext_vector_type(16)));
+    const int tid = threadIdx.x;
+    const v4i a = v4i{ tid, tid * 3 + 1, tid ^ 0x55, tid + 7 }, b = v4i{ tid * 5, tid + 11, ~tid, tid * 7 + 2 };
+    v16i c0 = {}, c1 = {}, c2 = {}, c3 = {};
+    for (int i = 0; i < iters; i++) {
+        c0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c0, 0, 0, 0);
+        c1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(b, a, c1, 0, 0, 0);
+        c2 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, a, c2, 0, 0, 0);
+        c3 = __builtin_amdgcn_mfma_i32_32x32x32_i8(b, b, c3, 0, 0, 0);
+    }
+    int v = 0;
+#pragma unroll
+    for (int r = 0; r < 16; r++) v ^= c0[r] + c1[r] + c2[r] + c3[r];
+    for (int o = 32; o >= 1; o >>= 1) v ^= __shfl_xor(v, o);
+    if ((tid & 63) == 0) out[blockIdx.x * 4 + (tid >> 6)] = v;
+}
+
+extern "C" void krh_mfma_rate(int *out, int grid, int iters) {
+    if (grid <= 0 || iters <= 0) {
+        kr_fail(ML_E_SHAPE, "mfma_rate: a positive grid and iteration count", hipSuccess);
+        return;
+    }
+    hipLaunchKernelGGL(k_mfma_rate, dim3(grid), dim3(256), 0, kr_stream(), out, iters);
+    kr_check_launch("mfma_rate");
+}
+
 extern "C" void krh_add(float *y, const float *x, int n) { krh_add_rows(y, 0, x, 0, n, 1); }
 extern "C" void krh_add_rows(float *y, size_t ldy, const float *x, size_t ldx, int n, int rows) {
     if (n <= 0 || !rows_ok(rows, "add rows") || rows == 0) return;

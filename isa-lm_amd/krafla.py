@@ -132,7 +132,7 @@ _P = C.c_void_p
 for name, res, args in [
     ("krh_init", C.c_int, []), ("krh_device_arch", C.c_char_p, []), ("krh_status", C.c_int, []),
     ("krh_device_cus", C.c_int, []), ("krh_ordered_sum_wave", None, [_P, _P, C.c_int, C.c_float]),
-    ("krh_attention_noalloc", None, [_P, _P, _P, _P, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_float, _P]), ("krh_stream_read", None, [_P, _P, C.c_size_t, C.c_int]),
+    ("krh_attention_noalloc", None, [_P, _P, _P, _P, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_float, _P]), ("krh_stream_read", None, [_P, _P, C.c_size_t, C.c_int]), ("krh_mfma_rate", None, [_P, C.c_int, C.c_int]),
     ("krh_last_error", C.c_char_p, []), ("krh_clear_error", None, []),
     ("krh_alloc", _P, [C.c_size_t]), ("krh_free", None, [_P]),
     ("krh_host_alloc", _P, [C.c_size_t]), ("krh_host_free", None, [_P]),
