@@ -96,6 +96,11 @@ void krh_matvec(float *y, const krh_mat *W, const int8_t *xq, const float *xd, i
  * projection into a scratch row, then ml_k_add into the residual); r and y
  * do not overlap */
 void krh_matvec_residual(float *r, float *y, const krh_mat *W, const int8_t *xq, const float *xd);
+/* krh_matvec_residual from a float input x quantized inside the launch, which
+ * also stores that Q8_0 of x into xq, xd (W->cols <= 16384): the reference's
+ * quantize_q8 of x, product into y and add into r as one launch
+ * (model/transformer.c:282-287) */
+void krh_matvec_f_residual_keep(float *r, float *y, const krh_mat *W, const float *x, int8_t *xq, float *xd);
 /* y[i] = W[i] x for nmat (1..3) matrices of one input length, type and
  * scale kind, in one launch (the ml_matvec calls of model/transformer.c:273-275
  * and :290-291 that share their input) */
@@ -131,6 +136,17 @@ void krh_rmsnorm_matvec_qkv(float *q, float *kc, float *vc, const krh_mat *wq, c
                             float eps, const float *rope_cos, const float *rope_sin, int head_dim, const int *pos);
 void krh_rmsnorm_matvec_swiglu(float *h, const krh_mat *w1, const krh_mat *w3, const float *x, const float *nw,
                                float eps);
+/* The fused-norm launches with every effect of the reference's separate calls
+ * (model/transformer.c:270-293): xb receives rmsnorm(x) * nw and xq, xd its
+ * Q8_0 (as ml_k_rmsnorm and ml_k_quantize_q8 leave them), u receives w3 x,
+ * and k, v go to the rows k, v with RoPE at tables row *pos; dim <= 8192,
+ * xb and xq 16-byte aligned */
+void krh_rmsnorm_matvec_swiglu_keep(float *h, float *u, const krh_mat *w1, const krh_mat *w3, const float *x,
+                                    const float *nw, float eps, float *xb, int8_t *xq, float *xd);
+void krh_rmsnorm_matvec_qkv_keep(float *q, float *k, float *v, const krh_mat *wq, const krh_mat *wk,
+                                 const krh_mat *wv, const float *bq, const float *bk, const float *bv, const float *x,
+                                 const float *nw, float eps, const float *rope_cos, const float *rope_sin,
+                                 int head_dim, const int *pos, float *xb, int8_t *xq, float *xd);
 /* krh_rmsnorm_matvec_qkv for the F16 cache: k and v go to row *pos of this
  * layer's F16 cache (kc, vc: [max_seq][kv_dim] halves), each value rounded as
  * store_kv rounds it (model/transformer.c:195-197, core/ml.c:39-53) */

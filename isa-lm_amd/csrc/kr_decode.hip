@@ -50,6 +50,13 @@ struct MvArgs {
     const int *pos;
     int kv16;            // EPI_QKV: k and v rows are the F16 cache's (halves)
     float *keep;         // EPI_ADD: receives the product W x as well; EPI_SWIGLU: receives w3 x
+    // workgroup 0 stores the prologue's results when set (float inputs held
+    // in registers only): the normalized x (with nw) and its Q8_0 quants and
+    // scales, as the reference's separate rmsnorm and quantize_q8 calls
+    // leave them in memory
+    float *keep_xb;
+    int8_t *keep_xq;
+    float *keep_xd;
 };
 
 constexpr int MV_THREADS = 256;
@@ -386,10 +393,15 @@ __global__ void __launch_bounds__(MV_THREADS, 2) k_matvec(const MvArgs a) {
             const float ss = kr_spec_sum<MV_THREADS>(sq, K, (unsigned char *)(sq + sc_terms_cap(K)));
             inv = kr_fdiv(1.0f, kr_fsqrt(kr_fadd(kr_fdiv(ss, (float)K), a.eps)));
         }
+        const bool kxb = a.keep_xb && blockIdx.x == 0;
 #pragma unroll
         for (int k = 0; k < XV; k++) {
             const int i = 4 * (k * MV_THREADS + tid);   // K % 32 == 0: 8-lane groups all in or all out
-            if (i < K) kr_quant4(a.nw ? kr_norm4(xv[k], inv, wv[k]) : xv[k], i, xs, xds, 1);
+            if (i < K) {
+                const float4 o = a.nw ? kr_norm4(xv[k], inv, wv[k]) : xv[k];
+                kr_quant4(o, i, xs, xds, 1);
+                if (kxb) *(float4 *)(a.keep_xb + i) = o;
+            }
         }
         if (!a.nw) {
 #pragma unroll
@@ -416,6 +428,10 @@ __global__ void __launch_bounds__(MV_THREADS, 2) k_matvec(const MvArgs a) {
         }
     }
     __syncthreads();
+    if (a.keep_xq && blockIdx.x == 0) {   // the prologue's Q8_0 of x, from LDS
+        for (int i = tid; i < K / 16; i += MV_THREADS) ((int4 *)a.keep_xq)[i] = ((const int4 *)xs)[i];
+        for (int i = tid; i < nb; i += MV_THREADS) a.keep_xd[i] = xds[i];
+    }
 
     float acc = 0.0f;   // row sum of lane < nloc
     // one item: S[P] holds it; S[P - 1] receives the loads MV_DEPTH - 1 ahead
@@ -845,10 +861,35 @@ extern "C" void krh_quantize_q8_rows(int8_t *q, size_t ldq, float *d, size_t ldd
     kr_check_launch("quantize_q8");
 }
 
+// the prologue results a launch also stores (MvArgs::keep_*): only for a
+// float input held in registers (K up to MV_XF_MAX with a norm,
+// MV_XF_PLAIN_MAX without), and the normalized x only with a norm
+struct MvKeep {
+    float *xb;
+    int8_t *xq;
+    float *xd;
+};
+
+static bool keep_ok(const MvKeep &k, const float *xf, const float *nw, int K) {
+    if (!k.xb && !k.xq) return true;
+    const bool ok = xf && (k.xq != nullptr) == (k.xd != nullptr) && (!k.xb || nw) &&
+                    K <= (nw ? MV_XF_MAX : MV_XF_PLAIN_MAX) && !((uintptr_t)k.xq & 15) && !((uintptr_t)k.xb & 15);
+    if (!ok) kr_fail(ML_E_SHAPE, "matvec keep: a float input in registers, 16-byte aligned outputs", hipSuccess);
+    return ok;
+}
+
+static void set_keep(MvArgs &a, const MvKeep &k) {
+    a.keep_xb = k.xb;
+    a.keep_xq = k.xq;
+    a.keep_xd = k.xd;
+}
+
 static void mv_plain(float *y, const krh_mat *W, const int8_t *xq, const float *xd, const float *xf,
-                     const float *nw, float eps, int accumulate, float *keep = nullptr) {
+                     const float *nw, float eps, int accumulate, float *keep = nullptr, MvKeep kp = {}) {
+    if (!keep_ok(kp, xf, nw, W->cols)) return;
     MvArgs a = {};
     a.keep = keep;
+    set_keep(a, kp);
     a.m[0] = to_kmat(W);
     a.nmat = 1;
     a.R = mv_rows(W->cols, W->rows, 1, 64);
@@ -871,6 +912,11 @@ extern "C" void krh_matvec(float *y, const krh_mat *W, const int8_t *xq, const f
 
 extern "C" void krh_matvec_residual(float *r, float *y, const krh_mat *W, const int8_t *xq, const float *xd) {
     mv_plain(r, W, xq, xd, nullptr, nullptr, 0.0f, 1, y);
+}
+
+extern "C" void krh_matvec_f_residual_keep(float *r, float *y, const krh_mat *W, const float *x, int8_t *xq,
+                                           float *xd) {
+    mv_plain(r, W, nullptr, nullptr, x, nullptr, 0.0f, 1, y, MvKeep{ nullptr, xq, xd });
 }
 
 extern "C" void krh_matvec_multi(float *const *y, const krh_mat *const *W, int nmat, const int8_t *xq,
@@ -916,12 +962,13 @@ extern "C" void krh_rmsnorm_matvec(float *y, const krh_mat *W, const float *x, c
 static void qkv(float *q, float *kc, float *vc, const krh_mat *wq, const krh_mat *wk, const krh_mat *wv,
                 const float *bq, const float *bk, const float *bv, const int8_t *xq, const float *xd, const float *xf,
                 const float *nw, float eps, const float *rope_cos, const float *rope_sin, int head_dim,
-                const int *pos, bool stage = false, bool kv16 = false) {
+                const int *pos, bool stage = false, bool kv16 = false, MvKeep kp = {}) {
     if (wq->cols != wk->cols || wq->cols != wv->cols || wk->rows != wv->rows || head_dim % 2 || wq->rows % 2 ||
         wk->rows % 2 || wq->type != wk->type || wq->d16 != wk->d16 || wv->d16 != wq->d16) {
         kr_fail(ML_E_SHAPE, "qkv shapes", hipSuccess);
         return;
     }
+    if (!keep_ok(kp, xf, nw, wq->cols)) return;
     MvArgs a = {};
     a.m[0] = to_kmat(wq);
     a.m[1] = to_kmat(wk);
@@ -950,6 +997,7 @@ static void qkv(float *q, float *kc, float *vc, const krh_mat *wq, const krh_mat
     a.ld_cache = stage ? 0 : wk->rows;
     a.pos = pos;
     a.kv16 = kv16;
+    set_keep(a, kp);
     // wq, wk and wv may differ in type (Q4 models keep wv in Q8): one launch
     // per type run
     if (wv->type == wq->type) {
@@ -990,6 +1038,15 @@ extern "C" void krh_rmsnorm_matvec_qkv_f16(float *q, uint16_t *kc, uint16_t *vc,
         head_dim, pos, false, true);
 }
 
+extern "C" void krh_rmsnorm_matvec_qkv_keep(float *q, float *k, float *v, const krh_mat *wq, const krh_mat *wk,
+                                            const krh_mat *wv, const float *bq, const float *bk, const float *bv,
+                                            const float *x, const float *nw, float eps, const float *rope_cos,
+                                            const float *rope_sin, int head_dim, const int *pos, float *xb,
+                                            int8_t *xq, float *xd) {
+    qkv(q, k, v, wq, wk, wv, bq, bk, bv, nullptr, nullptr, x, nw, eps, rope_cos, rope_sin, head_dim, pos, true, false,
+        MvKeep{ xb, xq, xd });
+}
+
 extern "C" void krh_rmsnorm_matvec_qkv_stage(float *q, float *k, float *v, const krh_mat *wq, const krh_mat *wk,
                                              const krh_mat *wv, const float *bq, const float *bk, const float *bv,
                                              const float *x, const float *nw, float eps, const float *rope_cos,
@@ -998,7 +1055,8 @@ extern "C" void krh_rmsnorm_matvec_qkv_stage(float *q, float *k, float *v, const
 }
 
 static void swiglu(float *h, const krh_mat *w1, const krh_mat *w3, const int8_t *xq, const float *xd, const float *xf,
-                   const float *nw, float eps, float *keep = nullptr) {
+                   const float *nw, float eps, float *keep = nullptr, MvKeep kp = {}) {
+    if (!keep_ok(kp, xf, nw, w1->cols)) return;
     if (w1->rows != w3->rows || w1->cols != w3->cols || w1->type != w3->type || w1->d16 != w3->d16) {
         kr_fail(ML_E_SHAPE, "swiglu shapes", hipSuccess);
         return;
@@ -1018,7 +1076,14 @@ static void swiglu(float *h, const krh_mat *w1, const krh_mat *w3, const int8_t 
     a.K = w1->cols;
     a.y[0] = h;
     a.keep = keep;
+    set_keep(a, kp);
     launch_mv<EPI_SWIGLU>(a, a.m[0]);
+}
+
+extern "C" void krh_rmsnorm_matvec_swiglu_keep(float *h, float *u, const krh_mat *w1, const krh_mat *w3,
+                                               const float *x, const float *nw, float eps, float *xb, int8_t *xq,
+                                               float *xd) {
+    swiglu(h, w1, w3, nullptr, nullptr, x, nw, eps, u, MvKeep{ xb, xq, xd });
 }
 
 extern "C" void krh_matvec_swiglu_keep(float *h, float *u, const krh_mat *w1, const krh_mat *w3, const int8_t *xq,

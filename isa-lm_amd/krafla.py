@@ -207,6 +207,10 @@ for name, res, args in [
     ("krh_matvec_residual", None, [_P, _P, _P, _P, _P]),
     ("krh_matvec_multi", None, [_P, _P, C.c_int, _P, _P]),
     ("krh_matvec_swiglu_keep", None, [_P, _P, _P, _P, _P, _P]),
+    ("krh_matvec_f_residual_keep", None, [_P, _P, _P, _P, _P, _P]),
+    ("krh_rmsnorm_matvec_swiglu_keep", None, [_P, _P, _P, _P, _P, _P, C.c_float, _P, _P, _P]),
+    ("krh_rmsnorm_matvec_qkv_keep", None, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, C.c_float, _P, _P, C.c_int,
+                                           _P, _P, _P, _P]),
     ("krh_softcap_rows", None, [_P, C.c_size_t, C.c_int, C.c_int, C.c_float]),
     ("krh_set_int", None, [_P, C.c_int]), ("krh_transpose_scales", None, [_P, C.c_int, _P, C.c_int, C.c_int]),
     ("krh_gen_blocks", None, [_P, _P, C.c_uint64, C.c_int, C.c_int, C.c_int, C.c_int, C.c_float]),

@@ -20,6 +20,11 @@
  * single calls that model/transformer.c makes for one token are launched as
  * one fused kernel with the same effects on memory, every intermediate
  * buffer included (fuse_at):
+ *   rmsnorm + quantize_q8 + q, k, v [+ biases]
+ *     + RoPE                                     krh_rmsnorm_matvec_qkv_keep
+ *   rmsnorm + quantize_q8 + w1, w3 + silu_mul    krh_rmsnorm_matvec_swiglu_keep
+ *   quantize_q8 of x + its product + the add
+ *     of the product into a residual             krh_matvec_f_residual_keep
  *   rmsnorm into o, quantize_q8 of o             krh_rmsnorm_q8 (also for runs)
  *   ml_matvec q, k, v [+ bias adds] + rope       krh_matvec_qkv (:273-281)
  *   ml_matvec w1, w3 + silu_mul                  krh_matvec_swiglu_keep (:290-293)
@@ -125,15 +130,17 @@ static void launch(const kh_op *o, const ptrdiff_t *st, int T) {
  * in link (op offset and argument index of each end: 16 * j + p) are one
  * buffer passed along (same address and length required); every other pair
  * of arguments, one of them written, must be apart. */
+#define KH_FUSE_OPS 12   /* calls in one fused pattern, at most */
 static int fusable(int i, int k, const unsigned char (*link)[2], int nlink) {
-    int cls[8 * 16];
-    for (int e = 0; e < 8 * 16; e++) cls[e] = e;
+    int cls[KH_FUSE_OPS * 16];
+    if (k > KH_FUSE_OPS) return 0;
+    for (int e = 0; e < KH_FUSE_OPS * 16; e++) cls[e] = e;
     for (int l = 0; l < nlink; l++) {
         const int a = link[l][0], b = link[l][1];
         const kh_op *x = &g_q[i + (a >> 4)], *y = &g_q[i + (b >> 4)];
         if (x->d[a & 15] != y->d[b & 15] || x->len[a & 15] != y->len[b & 15]) return 0;
         const int ca = cls[a], cb = cls[b];
-        for (int e = 0; e < 8 * 16; e++)
+        for (int e = 0; e < KH_FUSE_OPS * 16; e++)
             if (cls[e] == cb) cls[e] = ca;
     }
     for (int ja = 0; ja < k; ja++)
@@ -182,10 +189,87 @@ static int norm_q8_ok(const kh_op *nm, const kh_op *qz, const ptrdiff_t *sn, con
     return sn[0] == 4 * n && sn[1] == 4 * n && sn[2] == 0 && sq[0] == n && sq[1] == 4 * (n / 32) && sq[2] == 4 * n;
 }
 
+/* quantize_q8 at queue index z feeds the product at m (its q and scales are
+ * the product's input) */
+static int feeds(int z, int m) {
+    return g_q[m].d[1] == g_q[z].d[0] && g_q[m].d[2] == g_q[z].d[1] && g_q[m].len[1] == g_q[z].len[0] &&
+           g_q[m].len[2] == g_q[z].len[1];
+}
+
+/* rmsnorm at i into o, quantize_q8 of o at i + 1, for a launch whose
+ * prologue normalizes x in registers (n <= 8192) and stores o and its Q8_0
+ * (16-byte aligned x, weight, o and quants; o apart from x: the other
+ * workgroups read x after the first one wrote o) */
+static int norm_keep_ok(int i) {
+    const kh_op *nm = &g_q[i], *qz = &g_q[i + 1];
+    const int n = nm->n;
+    return qz->d[2] == nm->d[0] && qz->n == n && n % 32 == 0 && n <= 8192 &&
+           !(((uintptr_t)nm->d[0] | (uintptr_t)nm->d[1] | (uintptr_t)nm->d[2] | (uintptr_t)qz->d[0]) & 15) &&
+           (nm->d[0] + 4 * (size_t)n <= nm->d[1] || nm->d[1] + 4 * (size_t)n <= nm->d[0]);
+}
+
 /* A fused launch for the single calls at queue index i: how many calls it
  * covers (0: none applies). */
 static int fuse_at(int i) {
     const kh_op *o = &g_q[i];
+    /* rmsnorm + quantize_q8 + q, k, v [+ biases] + RoPE, or + w1, w3 + silu_mul */
+    if (o->op == QOP_RMSNORM && is_op(i + 1, QOP_QUANT_Q8) && is_op(i + 2, QOP_MATVEC) && is_op(i + 3, QOP_MATVEC) &&
+        norm_keep_ok(i) && feeds(i + 1, i + 2) && feeds(i + 1, i + 3) && g_q[i + 2].m.cols == o->n) {
+        const kh_op *z = &g_q[i + 1];
+        if (is_op(i + 4, QOP_MATVEC) && feeds(i + 1, i + 4) && g_qzero) {
+            const kh_op *q = &g_q[i + 2], *k = &g_q[i + 3], *v = &g_q[i + 4];
+            int j = i + 5;
+            const uint8_t *bias[3] = { NULL, NULL, NULL };
+            if (is_op(j, QOP_ADD) && is_op(j + 1, QOP_ADD) && is_op(j + 2, QOP_ADD) && g_q[j].d[0] == q->d[0] &&
+                g_q[j + 1].d[0] == k->d[0] && g_q[j + 2].d[0] == v->d[0] && g_q[j].n == q->n &&
+                g_q[j + 1].n == k->n && g_q[j + 2].n == v->n) {
+                for (int b = 0; b < 3; b++) bias[b] = g_q[j + b].d[1];
+                j += 3;
+            }
+            const kh_op *r = is_op(j, QOP_ROPE) ? &g_q[j] : NULL;
+            const int hd = r ? r->n : 0, jr = j - i;
+            const unsigned char l_nqkv[15][2] = {
+                { KH_L(0, 0), KH_L(1, 2) }, { KH_L(1, 0), KH_L(2, 1) }, { KH_L(1, 1), KH_L(2, 2) },
+                { KH_L(1, 0), KH_L(3, 1) }, { KH_L(1, 1), KH_L(3, 2) }, { KH_L(1, 0), KH_L(4, 1) },
+                { KH_L(1, 1), KH_L(4, 2) }, { KH_L(2, 0), KH_L(jr, 0) }, { KH_L(3, 0), KH_L(jr, 1) },
+                { KH_L(2, 0), KH_L(5, 0) }, { KH_L(3, 0), KH_L(6, 0) }, { KH_L(4, 0), KH_L(7, 0) } };
+            if (r && r->d[0] == q->d[0] && r->d[1] == k->d[0] && r->a * hd == q->n && r->b * hd == k->n &&
+                k->n == v->n && hd % 2 == 0 && q->n % 2 == 0 && k->n % 2 == 0 && same_kind(&q->m, &k->m) &&
+                q->m.cols == v->m.cols && q->m.d16 == v->m.d16 &&
+                KH_FUSABLE(i, jr + 1, l_nqkv, bias[0] ? 12 : 9)) {
+                krh_rmsnorm_matvec_qkv_keep((float *)q->d[0], (float *)k->d[0], (float *)v->d[0], &q->m, &k->m, &v->m,
+                                            (const float *)bias[0], (const float *)bias[1], (const float *)bias[2],
+                                            (const float *)o->d[1], (const float *)o->d[2], o->f,
+                                            (const float *)r->d[2], (const float *)r->d[3], hd, g_qzero,
+                                            (float *)o->d[0], (int8_t *)z->d[0], (float *)z->d[1]);
+                return jr + 1;
+            }
+        }
+        static const unsigned char l_nsw[7][2] = {
+            { KH_L(0, 0), KH_L(1, 2) }, { KH_L(1, 0), KH_L(2, 1) }, { KH_L(1, 1), KH_L(2, 2) },
+            { KH_L(1, 0), KH_L(3, 1) }, { KH_L(1, 1), KH_L(3, 2) }, { KH_L(2, 0), KH_L(4, 0) },
+            { KH_L(3, 0), KH_L(4, 1) } };
+        const kh_op *w1 = &g_q[i + 2], *w3 = &g_q[i + 3], *sm = is_op(i + 4, QOP_SILU_MUL) ? &g_q[i + 4] : NULL;
+        if (sm && sm->d[0] == w1->d[0] && sm->d[1] == w3->d[0] && sm->n == w1->n && w1->n == w3->n &&
+            same_kind(&w1->m, &w3->m) && KH_FUSABLE(i, 5, l_nsw, 7)) {
+            krh_rmsnorm_matvec_swiglu_keep((float *)w1->d[0], (float *)w3->d[0], &w1->m, &w3->m,
+                                           (const float *)o->d[1], (const float *)o->d[2], o->f, (float *)o->d[0],
+                                           (int8_t *)z->d[0], (float *)z->d[1]);
+            return 5;
+        }
+    }
+    /* quantize_q8 of x + its product into y + the add of y into r */
+    static const unsigned char l_qres[3][2] = { { KH_L(0, 0), KH_L(1, 1) }, { KH_L(0, 1), KH_L(1, 2) },
+                                                { KH_L(1, 0), KH_L(2, 1) } };
+    if (o->op == QOP_QUANT_Q8 && is_op(i + 1, QOP_MATVEC) && is_op(i + 2, QOP_ADD) && feeds(i, i + 1) &&
+        g_q[i + 1].m.cols == o->n && o->n % 32 == 0 && o->n <= 16384 &&
+        !(((uintptr_t)o->d[0] | (uintptr_t)o->d[2]) & 15) && g_q[i + 2].d[1] == g_q[i + 1].d[0] &&
+        g_q[i + 2].n == g_q[i + 1].n && KH_FUSABLE(i, 3, l_qres, 3)) {
+        const kh_op *mv = &g_q[i + 1];
+        krh_matvec_f_residual_keep((float *)g_q[i + 2].d[0], (float *)mv->d[0], &mv->m, (const float *)o->d[2],
+                                   (int8_t *)o->d[0], (float *)o->d[1]);
+        return 3;
+    }
     static const unsigned char l_nq[2][2] = { { KH_L(0, 0), KH_L(1, 2) }, { KH_L(0, 0), KH_L(0, 1) } };
     if (o->op == QOP_RMSNORM && is_op(i + 1, QOP_QUANT_Q8) && norm_q8_ok(o, &g_q[i + 1], NULL, NULL) &&
         KH_FUSABLE(i, 2, l_nq, o->d[0] == o->d[1] ? 2 : 1)) {

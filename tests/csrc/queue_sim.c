@@ -20,7 +20,8 @@
  *   queue_sim fuse [trials] [mutate]
  * one token's decode sequences (rmsnorm + quantize, q/k/v products + bias
  * adds + RoPE, w1/w3 products + silu_mul, a product + residual add, products
- * of one input) with random buffer choices, some of them aliased: the fused
+ * of one input; rmsnorm + quantize + q/k/v or w1/w3, quantize + product +
+ * residual add) with random buffer choices, some of them aliased: the fused
  * launches (emulated as the calls they stand for) must leave the same bytes
  * as the calls one by one, and every pattern must fire in some trial.
  * mutate = 1 drops the aliasing checks of the patterns. */
@@ -46,7 +47,8 @@ static int fusable_or_not(int i, int k, const unsigned char (*link)[2], int nlin
 #define KH_FUSABLE fusable_or_not
 #include "kh_queue.h"
 
-static long g_fired[6];   /* rmsnorm_q8, qkv, swiglu, residual, multi, rmsnorm_q8 rows */
+static long g_fired[9];   /* rmsnorm_q8, qkv, swiglu, residual, multi, rmsnorm_q8 rows, norm+qkv, norm+swiglu,
+                             quantize+residual */
 
 static int fusable_or_not(int i, int k, const unsigned char (*link)[2], int nlink) {
     return g_mutate ? 1 : fusable(i, k, link, nlink);
@@ -54,15 +56,29 @@ static int fusable_or_not(int i, int k, const unsigned char (*link)[2], int nlin
 
 static long g_launches;
 
+/* the emulated arithmetic of one row (the rows stubs and the fused stubs
+ * share it, so a fused launch's bytes equal the calls it stands for) */
+static void sim_norm(float *out, const float *x, const float *w, int n, float eps) {
+    float ss = 0;
+    for (int i = 0; i < n; i++) ss += x[i] * x[i];
+    const float inv = 1.0f / sqrtf(ss / n + eps);
+    for (int i = 0; i < n; i++) out[i] = x[i] * inv * w[i];
+}
+static void sim_q8(int8_t *q, float *d, const float *x, int n) {
+    for (int b = 0; b < n / 32; b++) {
+        float m = 0;
+        for (int i = 0; i < 32; i++) m = fmaxf(m, fabsf(x[b * 32 + i]));
+        d[b] = m / 127;
+        for (int i = 0; i < 32; i++) q[b * 32 + i] = (int8_t)(m > 0 ? roundf(x[b * 32 + i] * 127 / m) : 0);
+    }
+}
+
 void krh_rmsnorm_rows(float *o, size_t ldo, const float *x, size_t ldx, const float *w, size_t ldw, int n, float eps,
                       int rows) {
     g_launches++;
     float tmp[1024];
     for (int r = 0; r < rows; r++) {
-        float ss = 0;
-        for (int i = 0; i < n; i++) ss += x[r * ldx + i] * x[r * ldx + i];
-        const float inv = 1.0f / sqrtf(ss / n + eps);
-        for (int i = 0; i < n; i++) tmp[i] = x[r * ldx + i] * inv * w[r * ldw + i];
+        sim_norm(tmp, x + r * ldx, w + r * ldw, n, eps);
         memcpy(o + r * ldo, tmp, sizeof(float) * n);
     }
 }
@@ -109,14 +125,13 @@ void krh_quantize_q8_rows(int8_t *q, size_t ldq, float *d, size_t ldd, const flo
         printf("quantize_q8 rows: misaligned\n");
         exit(2);
     }
-    for (int r = 0; r < rows; r++)
-        for (int b = 0; b < n / 32; b++) {
-            float m = 0;
-            for (int i = 0; i < 32; i++) m = fmaxf(m, fabsf(x[r * ldx + b * 32 + i]));
-            d[r * ldd + b] = m / 127;
-            for (int i = 0; i < 32; i++)
-                q[r * ldq + b * 32 + i] = (int8_t)(m > 0 ? roundf(x[r * ldx + b * 32 + i] * 127 / m) : 0);
-        }
+    for (int r = 0; r < rows; r++) {
+        int8_t qq[1024];
+        float dd[32];
+        sim_q8(qq, dd, x + r * ldx, n);
+        memcpy(q + r * ldq, qq, (size_t)n);
+        memcpy(d + r * ldd, dd, sizeof(float) * (n / 32));
+    }
 }
 
 /* products: y[r] (+)= sum_c W[r][c] * x[c] * the two block scales (int8
@@ -193,6 +208,75 @@ void krh_matvec_qkv(float *q, float *kc, float *vc, const krh_mat *wq, const krh
     memcpy(kc, o[1], sizeof(float) * wk->rows);
     memcpy(vc, o[2], sizeof(float) * wv->rows);
 }
+/* the keep forms: the norm and Q8_0 of x computed first, every output
+ * written after every input is read */
+void krh_rmsnorm_matvec_qkv_keep(float *q, float *k, float *v, const krh_mat *wq, const krh_mat *wk,
+                                 const krh_mat *wv, const float *bq, const float *bk, const float *bv, const float *x,
+                                 const float *nw, float eps, const float *rope_cos, const float *rope_sin,
+                                 int head_dim, const int *pos, float *xb, int8_t *xq, float *xd) {
+    g_fired[6]++;
+    const int n = wq->cols;
+    float o[1024], dd[32];
+    int8_t qq[1024];
+    sim_norm(o, x, nw, n, eps);
+    sim_q8(qq, dd, o, n);
+    float out[3][1024], c[512], sn[512];
+    mv(out[0], wq, qq, dd);
+    mv(out[1], wk, qq, dd);
+    mv(out[2], wv, qq, dd);
+    const size_t off = (size_t)*pos * (head_dim / 2);
+    memcpy(c, rope_cos + off, sizeof(float) * (head_dim / 2));
+    memcpy(sn, rope_sin + off, sizeof(float) * (head_dim / 2));
+    if (bq) {
+        for (int i = 0; i < wq->rows; i++) out[0][i] += bq[i];
+        for (int i = 0; i < wk->rows; i++) out[1][i] += bk[i];
+        for (int i = 0; i < wv->rows; i++) out[2][i] += bv[i];
+    }
+    for (int m = 0; m < 2; m++)
+        for (int p = 0; p < (m ? wk->rows : wq->rows) / 2; p++) {
+            const int i = p % (head_dim / 2);
+            const float a = out[m][2 * p], b = out[m][2 * p + 1];
+            out[m][2 * p] = a * c[i] - b * sn[i];
+            out[m][2 * p + 1] = a * sn[i] + b * c[i];
+        }
+    memcpy(xb, o, sizeof(float) * n);
+    memcpy(xq, qq, (size_t)n);
+    memcpy(xd, dd, sizeof(float) * (n / 32));
+    memcpy(q, out[0], sizeof(float) * wq->rows);
+    memcpy(k, out[1], sizeof(float) * wk->rows);
+    memcpy(v, out[2], sizeof(float) * wv->rows);
+}
+void krh_rmsnorm_matvec_swiglu_keep(float *h, float *u, const krh_mat *w1, const krh_mat *w3, const float *x,
+                                    const float *nw, float eps, float *xb, int8_t *xq, float *xd) {
+    g_fired[7]++;
+    const int n = w1->cols;
+    float o[1024], dd[32], a[1024], b[1024];
+    int8_t qq[1024];
+    sim_norm(o, x, nw, n, eps);
+    sim_q8(qq, dd, o, n);
+    mv(a, w1, qq, dd);
+    mv(b, w3, qq, dd);
+    for (int i = 0; i < w1->rows; i++) a[i] = a[i] * 0.5f * b[i] + 1.0f;
+    memcpy(xb, o, sizeof(float) * n);
+    memcpy(xq, qq, (size_t)n);
+    memcpy(xd, dd, sizeof(float) * (n / 32));
+    memcpy(h, a, sizeof(float) * w1->rows);
+    memcpy(u, b, sizeof(float) * w3->rows);
+}
+void krh_matvec_f_residual_keep(float *r, float *y, const krh_mat *W, const float *x, int8_t *xq, float *xd) {
+    g_fired[8]++;
+    const int n = W->cols;
+    float dd[32], out[1024], res[1024];
+    int8_t qq[1024];
+    sim_q8(qq, dd, x, n);
+    mv(out, W, qq, dd);
+    for (int i = 0; i < W->rows; i++) res[i] = r[i] + out[i];
+    memcpy(xq, qq, (size_t)n);
+    memcpy(xd, dd, sizeof(float) * (n / 32));
+    memcpy(y, out, sizeof(float) * W->rows);
+    memcpy(r, res, sizeof(float) * W->rows);
+}
+
 void krh_rmsnorm_q8(int8_t *q, float *d, float *xb, const float *x, const float *w, int n, float eps, int ntok) {
     g_fired[ntok > 1 ? 5 : 0]++;
     for (int t = 0; t < ntok; t++) {
@@ -351,7 +435,7 @@ static void seq_add(int queued, float *y, const float *x, int n) {
 
 /* pattern: 0 rmsnorm + quantize, 1 q/k/v [+ biases] + rope, 2 w1/w3 +
  * silu_mul, 3 product + residual add, 4 products of one input */
-static void one_seq(int queued, const fuse_mem *m, int pat, uint64_t seed) {
+static void one_seq(int queued, const fuse_mem *m, int pat, uint64_t seed) {   /* pat: 0..7 */
     g_rs = seed;
     const int K = 32 * (2 + (int)rnd(3)), hd = 16, nh = 2 + (int)rnd(3), nkv = 1 + (int)rnd(2), den = 4;
     int8_t *xq = (int8_t *)(m->base + m->i8);
@@ -364,26 +448,34 @@ static void one_seq(int queued, const fuse_mem *m, int pat, uint64_t seed) {
         b[i] = (int)rnd(FB);
         sh[i] = 0;
     }
-    if (pat == 0) {
+    if (pat == 0 || pat == 5 || pat == 6 || pat == 7) {
+        /* rmsnorm into o and quantize_q8 of o into the products' input (5, 6),
+         * or quantize_q8 of a float row alone (7) */
         const int n = K;
-        b[0] = pick(b[0], b[1], den, &sh[0]);
-        float *o = fbuf(m, b[0], sh[0]), *x = fbuf(m, b[1], 0), *w = fbuf(m, b[2], 0);
+        int nb_[3], ns = 0;
+        for (int i = 0; i < 3; i++) nb_[i] = (int)rnd(FB);
+        nb_[0] = pick(nb_[0], nb_[1], den, &ns);
+        float *o = fbuf(m, nb_[0], ns), *x = fbuf(m, nb_[1], 0), *w = fbuf(m, nb_[2], 0);
         int8_t *q = xq;
-        float *d = rnd(den) ? xd : fbuf(m, b[1], 0);   /* sometimes the scales land on x */
+        float *d = rnd(den) ? xd : fbuf(m, nb_[1], 0);   /* sometimes the scales land on x */
         if (!queued) {
-            krh_rmsnorm_rows(o, 0, x, 0, w, 0, n, 1e-5f, 1);
-            krh_quantize_q8_rows(q, 0, d, 0, o, 0, n, 1);
-            return;
+            if (pat != 7) krh_rmsnorm_rows(o, 0, x, 0, w, 0, n, 1e-5f, 1);
+            krh_quantize_q8_rows(q, 0, d, 0, pat == 7 ? x : o, 0, n, 1);
+        } else {
+            if (pat != 7) {
+                const void *h1[] = { o, x, w };
+                const size_t l1[] = { 4 * (size_t)n, 4 * (size_t)n, 4 * (size_t)n };
+                const int w1[] = { 1, 0, 0 };
+                push(QOP_RMSNORM, n, 0, 0, 1e-5f, 3, h1, l1, w1);
+            }
+            const void *h2[] = { q, d, pat == 7 ? x : o };
+            const size_t l2[] = { (size_t)n, 4 * (size_t)(n / 32), 4 * (size_t)n };
+            const int w2[] = { 1, 1, 0 };
+            push(QOP_QUANT_Q8, n, 0, 0, 0.0f, 3, h2, l2, w2);
         }
-        const void *h1[] = { o, x, w };
-        const size_t l1[] = { 4 * (size_t)n, 4 * (size_t)n, 4 * (size_t)n };
-        const int w1[] = { 1, 0, 0 };
-        push(QOP_RMSNORM, n, 0, 0, 1e-5f, 3, h1, l1, w1);
-        const void *h2[] = { q, d, o };
-        const size_t l2[] = { (size_t)n, 4 * (size_t)(n / 32), 4 * (size_t)n };
-        const int w2[] = { 1, 1, 0 };
-        push(QOP_QUANT_Q8, n, 0, 0, 0.0f, 3, h2, l2, w2);
-        return;
+        if (pat == 0) return;
+        if (d != xd) return;   /* the products read xq, xd: no chain to fuse */
+        pat = pat == 5 ? 1 : pat == 6 ? 2 : 3;
     }
     const int nm = pat == 1 ? 3 : pat == 2 ? 2 : pat == 3 ? 1 : 2 + (int)rnd(2);
     if (pat == 1) {
@@ -465,7 +557,7 @@ static int check_fuse(int trials) {
             for (size_t i = m->i8; i < m->d8; i++) m->base[i] = (uint8_t)(i * 37 + (size_t)trial);
             for (size_t i = m->wq; i < m->wd; i++) m->base[i] = (uint8_t)(i * 13 + (size_t)trial * 7);
         }
-        const int pat = trial % 5;
+        const int pat = trial % 8;
         for (int side = 0; side < 2; side++) {
             one_seq(side, &mem[side], pat, 0xABCDEFull ^ (uint64_t)trial * 31);
             if (side) q_flush();
@@ -474,10 +566,11 @@ static int check_fuse(int trials) {
             if (++fails <= 5) printf("fuse trial %d (pattern %d) differs\n", trial, pat);
         }
     }
-    printf("fuse trials %d failures %d fired rmsnorm_q8 %ld qkv %ld swiglu %ld residual %ld multi %ld\n", trials,
-           fails, g_fired[0], g_fired[1], g_fired[2], g_fired[3], g_fired[4]);
-    for (int i = 0; i < 5; i++)
-        if (!g_fired[i]) {
+    printf("fuse trials %d failures %d fired rmsnorm_q8 %ld qkv %ld swiglu %ld residual %ld multi %ld norm+qkv %ld "
+           "norm+swiglu %ld quantize+residual %ld\n", trials, fails, g_fired[0], g_fired[1], g_fired[2], g_fired[3],
+           g_fired[4], g_fired[6], g_fired[7], g_fired[8]);
+    for (int i = 0; i < 9; i++)
+        if (i != 5 && !g_fired[i]) {
             printf("pattern %d never fired\n", i);
             return 1;
         }

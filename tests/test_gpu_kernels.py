@@ -805,3 +805,85 @@ def test_matvec_fused_op_sequences(dev, rows, cols, typ, d16):
         ok()
         for (q, d, dh), r, y in list(zip(ms, rws, ys))[:nmat]:
             assert np.array_equal(bits(y.get(np.float32, r)), bits(oracle_matvec(q, d, r, cols, typ, xq, xd)))
+
+
+@pytest.mark.parametrize("dim,nh,nkv,hd,typ,vtyp,bias,hidden", [(288, 6, 6, 48, K.ML_Q8_0, K.ML_Q8_0, 0, 768),
+                                                                 (896, 14, 2, 64, K.ML_Q4_0, K.ML_Q8_0, 1, 4864),
+                                                                 (4096, 32, 8, 128, K.ML_Q8_0, K.ML_Q8_0, 0, 14336)])
+def test_matvec_keep_prologues(dev, dim, nh, nkv, hd, typ, vtyp, bias, hidden):
+    """the fused-norm and float-input launches that also store their
+    prologue's results (the op-table binding's replacement of the reference's
+    rmsnorm, quantize_q8 and products, model/transformer.c:270-293): xb, the
+    Q8_0 of xb (or of x), and every product, bit for bit against the oracle's
+    rmsnorm, quantize, matvec, add, rope and silu_mul"""
+    H = K.hip
+    qd, kvd, pos = nh * hd, nkv * hd, 17
+    x = f32(RNG.normal(0, 2, dim))
+    nw = f32(RNG.normal(1, 0.1, dim))
+    xb_want = np.zeros(dim, np.float32)
+    oracle.kro_rmsnorm(xb_want.ctypes.data, x.ctypes.data, nw.ctypes.data, dim, C.c_float(1e-5))
+    xq_want, xd_want = O.quantize(xb_want)
+    xdev, nwdev = dev.put(x), dev.put(nw)
+
+    def kept(xbb, xqb, xdb, want_xb=True):
+        if want_xb:
+            assert np.array_equal(bits(xbb.get(np.float32, dim)), bits(xb_want))
+        assert np.array_equal(xqb.get(np.int8, dim), xq_want)
+        assert np.array_equal(bits(xdb.get(np.float32, dim // 32)), bits(xd_want))
+
+    # q, k, v with the attention norm, biases and RoPE into the staging rows
+    typs = (typ, typ, vtyp)
+    mats = [rand_mat(r, dim, t, 1) for r, t in zip((qd, kvd, kvd), typs)]
+    Ws = [dmat(dev, q, d, dh, r, dim, t, 1) for (q, d, dh), r, t in zip(mats, (qd, kvd, kvd), typs)]
+    biases = [f32(RNG.normal(0, 0.02, r)) for r in (qd, kvd, kvd)]
+    cs, sn = f32(RNG.uniform(-1, 1, 40 * hd // 2)), f32(RNG.uniform(-1, 1, 40 * hd // 2))
+    qb, kb, vb = dev.zeros(4 * qd), dev.zeros(4 * kvd), dev.zeros(4 * kvd)
+    xbb, xqb, xdb = dev.zeros(4 * dim), dev.zeros(dim), dev.zeros(4 * dim // 32)
+    bb = [dev.put(b) if bias else None for b in biases]
+    H.krh_rmsnorm_matvec_qkv_keep(qb.ptr, kb.ptr, vb.ptr, C.byref(Ws[0]), C.byref(Ws[1]), C.byref(Ws[2]),
+                                  *[b.ptr if b else None for b in bb], xdev.ptr, nwdev.ptr, C.c_float(1e-5),
+                                  dev.put(cs).ptr, dev.put(sn).ptr, hd, dev.put(np.array([pos], np.int32)).ptr,
+                                  xbb.ptr, xqb.ptr, xdb.ptr)
+    ok()
+    kept(xbb, xqb, xdb)
+    outs = []
+    for (q, d, dh), r, b, t in zip(mats, (qd, kvd, kvd), biases, typs):
+        y = oracle_matvec(q, d, r, dim, t, xq_want, xd_want)
+        if bias:
+            oracle.kro_add(y.ctypes.data, b.ctypes.data, r)
+        outs.append(y)
+    c0, s0 = f32(cs[pos * hd // 2:(pos + 1) * hd // 2]), f32(sn[pos * hd // 2:(pos + 1) * hd // 2])
+    oracle.kro_rope(outs[0].ctypes.data, outs[1].ctypes.data, c0.ctypes.data, s0.ctypes.data, hd, nh, nkv)
+    for got, want, r in ((qb, outs[0], qd), (kb, outs[1], kvd), (vb, outs[2], kvd)):
+        assert np.array_equal(bits(got.get(np.float32, r)), bits(want))
+
+    # w1, w3 with the FFN norm: h = silu(w1 xb) * (w3 xb), u = w3 xb
+    m1, m3 = rand_mat(hidden, dim, typ, 1), rand_mat(hidden, dim, typ, 1)
+    W1, W3 = dmat(dev, *m1, hidden, dim, typ, 1), dmat(dev, *m3, hidden, dim, typ, 1)
+    hb, ub = dev.zeros(4 * hidden), dev.zeros(4 * hidden)
+    xbb, xqb, xdb = dev.zeros(4 * dim), dev.zeros(dim), dev.zeros(4 * dim // 32)
+    H.krh_rmsnorm_matvec_swiglu_keep(hb.ptr, ub.ptr, C.byref(W1), C.byref(W3), xdev.ptr, nwdev.ptr,
+                                     C.c_float(1e-5), xbb.ptr, xqb.ptr, xdb.ptr)
+    ok()
+    kept(xbb, xqb, xdb)
+    g = oracle_matvec(m1[0], m1[1], hidden, dim, typ, xq_want, xd_want)
+    u = oracle_matvec(m3[0], m3[1], hidden, dim, typ, xq_want, xd_want)
+    h = g.copy()
+    oracle.kro_silu_mul(h.ctypes.data, u.ctypes.data, hidden)
+    assert np.array_equal(bits(hb.get(np.float32, hidden)), bits(h))
+    assert np.array_equal(bits(ub.get(np.float32, hidden)), bits(u))
+
+    # w2 from the float h, quantized in the launch: y = W2 q8(h), r += y
+    m2 = rand_mat(dim, hidden, vtyp, 1)
+    W2 = dmat(dev, *m2, dim, hidden, vtyp, 1)
+    r0 = f32(RNG.normal(0, 1, dim))
+    rb, yb = dev.put(r0), dev.zeros(4 * dim)
+    hq, hd_ = dev.zeros(hidden), dev.zeros(4 * hidden // 32)
+    H.krh_matvec_f_residual_keep(rb.ptr, yb.ptr, C.byref(W2), dev.put(h).ptr, hq.ptr, hd_.ptr)
+    ok()
+    hq_want, hd_want = O.quantize(h)
+    assert np.array_equal(hq.get(np.int8, hidden), hq_want)
+    assert np.array_equal(bits(hd_.get(np.float32, hidden // 32)), bits(hd_want))
+    y = oracle_matvec(m2[0], m2[1], dim, hidden, vtyp, hq_want, hd_want)
+    assert np.array_equal(bits(yb.get(np.float32, dim)), bits(y))
+    assert np.array_equal(bits(rb.get(np.float32, dim)), bits((r0 + y).astype(np.float32)))
