@@ -163,6 +163,46 @@ def test_workload_matches_reference(name):
         shutil.rmtree(tmp, ignore_errors=True)
 
 
+@pytest.mark.parametrize("name", ["qwen05b_mixed", "llama1b_mixed"])
+def test_route_workload_matches_reference(name):
+    """the reference's own ml_run over this backend's op table
+    (oracle/_ref/hip/ml_run: model/transformer.c and app/ml_run.c unchanged,
+    the per-token op queue batching and fusing their calls) on the full-size
+    model: the greedy ids the scalar build printed, and for the 0.5B shape
+    every teacher-forced position's --dump-logits row against the fixture's
+    hashes"""
+    exe = os.path.join(O.REF_DIR, "hip", "ml_run")
+    if not os.path.exists(exe):
+        pytest.skip("oracle/_ref/hip not built (needs the reference sources at build time)")
+    fx = os.path.join(GOLDEN, name + ".npz")
+    if not os.path.exists(fx):
+        pytest.skip("no golden fixture %s" % fx)
+    g = np.load(fx)
+    tmp = scratch(int(g["mlb_bytes"]) * 3)
+    try:
+        path = os.path.join(tmp, name + ".mlb")
+        K.gen_mlb(path, **dict(K.CONFIGS[name], device=1))
+        assert file_sha256(path) == str(g["mlb_sha256"]), "the device generator wrote other bytes"
+        t0 = time.time()
+        ids, err = O.ref_ml_run(path, g["prompt"], int(g["steps"]), isa="hip")
+        say("%s: route ml_run %.1f s: %s" % (name, time.time() - t0, err.strip().splitlines()[-1][:120]))
+        assert "isa: hip" in err
+        want = g["ids"]
+        first = int(np.argmax(ids != want)) if ids.shape == want.shape and not np.array_equal(ids, want) else -1
+        assert np.array_equal(ids, want), "route ids differ from the reference's from index %d" % first
+        if name == "qwen05b_mixed":
+            forced = g["forced"]
+            dump = os.path.join(tmp, "route.logits")
+            O.ref_ml_run(path, forced, forced.size, dump=dump, isa="hip")
+            V = K.CONFIGS[name]["vocab"]
+            logits = np.fromfile(dump, dtype=np.float32).reshape(forced.size, V)
+            bad = np.nonzero(row_hashes(logits) != g["row_hash"])[0]
+            assert bad.size == 0, "%d of %d route logits rows differ, first %d" % (bad.size, forced.size,
+                                                                                   bad[0] if bad.size else -1)
+    finally:
+        shutil.rmtree(tmp, ignore_errors=True)
+
+
 # ---- 2. the batched kernels at the prompt lengths ----
 
 def sample_tokens(T):
