@@ -313,12 +313,18 @@ MMat to_mmat(const krh_mat *m) {
 
 int row_tiles(int rows, int ng) { return (rows + 32 * ng - 1) / (32 * ng); }
 
-// NG for a launch over these row counts and ntt token tiles: 4 when its
-// 128-row tiles give every CU two workgroups, else 1
+// NG for a launch over these row counts and ntt token tiles: 4 when it has
+// at least 3/4 of a 128-row tile per CU, else 1. Measured (K = 4096, 256
+// CUs): a 128-row tile does 4 times a 32-row tile's work in 1.9 times its
+// time, so from about 200 tiles, where the 32-row grid needs two rounds of
+// resident workgroups, the 128-row grid's one round is the shorter (14336
+// rows at T = 512: 152 against 300 us); below it, 32-row tiles keep more CUs
+// busy (T = 128, 112 tiles: 89 us, where one round of 128-row tiles takes
+// about what it takes at T = 192, 125 us).
 int pick_ng(int rows0, int rows1, int rows2, int ntt) {
     const int tiles = row_tiles(rows0, 4) + row_tiles(rows1, 4) + row_tiles(rows2, 4);
     const int cus = krh_device_cus() > 0 ? krh_device_cus() : 256;
-    return (long)tiles * ntt >= 2L * cus ? 4 : 1;
+    return 4L * tiles * ntt >= 3L * cus ? 4 : 1;
 }
 
 // ---- per-token work of a batched step ----
