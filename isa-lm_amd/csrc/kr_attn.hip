@@ -351,9 +351,11 @@ __global__ void __launch_bounds__(AT_THREADS) k_attn_softmax(float *att, int max
 // the exponentials x - max, their ordered sum (kr_spec_sum in single-wave
 // mode), x * (1 / sum); an all -inf row becomes 1/n. The per-row kernel keeps
 // three of its four waves idle in the ordered sum of rows this short; here
-// every wave sums its own row.
+// every wave sums its own row. SV: register slots per lane (rows of at most
+// 64 SV entries): 32 for rows up to 2048 keep the kernel at fewer registers,
+// so more rows are in flight.
 constexpr int SM_WN = SC_CPW << SC_LOG_LMIN, SM_V = SM_WN / 64;
-template <int RW>
+template <int RW, int SV = SM_V>
 __global__ void __launch_bounds__(64 * RW) k_attn_softmax_rows(float *att, int n_heads, int max_seq, int window,
                                                                const int *pos_p, int nrows, int terms_cap,
                                                                int scr_bytes) {
@@ -369,13 +371,13 @@ __global__ void __launch_bounds__(64 * RW) k_attn_softmax_rows(float *att, int n
     float *a = att + (size_t)r * max_seq;
     float *es = (float *)(sm_lds + (size_t)wave * (4 * terms_cap + scr_bytes));
     unsigned char *scr = (unsigned char *)(es + terms_cap);
-    float v[SM_V];
+    float v[SV];
     float m = -INFINITY;
 #pragma unroll
-    for (int k = 0; k < SM_V; k++)
+    for (int k = 0; k < SV; k++)
         if (k * 64 < n) v[k] = a[min(k * 64 + lane, n - 1)];   // the last live slot clamped: repeats change no max
 #pragma unroll
-    for (int k = 0; k < SM_V; k++)
+    for (int k = 0; k < SV; k++)
         if (k * 64 < n) m = fmaxf(m, v[k]);
     for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
     if (m == -INFINITY) {   // every score -inf: the scalar loop's 1/n
@@ -384,7 +386,7 @@ __global__ void __launch_bounds__(64 * RW) k_attn_softmax_rows(float *att, int n
     }
     const int sh = sc_log_len(n);
 #pragma unroll
-    for (int k = 0; k < SM_V; k++) {
+    for (int k = 0; k < SV; k++) {
         if (k * 64 >= n) break;
         const int t = k * 64 + lane;
         v[k] = kr_expf_tab(kr_fsub(v[k], m), xtab);
@@ -393,7 +395,7 @@ __global__ void __launch_bounds__(64 * RW) k_attn_softmax_rows(float *att, int n
     kr_wave_sync();
     const float inv = kr_fdiv(1.0f, kr_spec_sum<64, false, true>(es, n, scr));
 #pragma unroll
-    for (int k = 0; k < SM_V; k++) {
+    for (int k = 0; k < SV; k++) {
         if (k * 64 >= n) break;
         const int t = k * 64 + lane;
         if (t < n) a[t] = kr_fmul(v[k], inv);
@@ -1017,7 +1019,10 @@ static void attention(float *ao, float *att, const float *q, const KvView &kv, i
         const int tcap = sc_terms_cap(max_pos + 1), scr = (sc_lds_bytes(max_pos + 1, 64) + 15) / 16 * 16;
         const size_t per_wave = 4 * (size_t)tcap + scr;
         const int nrows = n_heads * ntok;
-        if (4 * per_wave <= 64 * 1024)
+        if (4 * per_wave <= 64 * 1024 && max_pos + 1 <= SM_WN / 2)
+            hipLaunchKernelGGL((k_attn_softmax_rows<4, SM_V / 2>), dim3((nrows + 3) / 4), dim3(256), 4 * per_wave,
+                               kr_stream(), att, n_heads, max_seq, window, pos, nrows, tcap, scr);
+        else if (4 * per_wave <= 64 * 1024)
             hipLaunchKernelGGL(k_attn_softmax_rows<4>, dim3((nrows + 3) / 4), dim3(256), 4 * per_wave, kr_stream(),
                                att, n_heads, max_seq, window, pos, nrows, tcap, scr);
         else
