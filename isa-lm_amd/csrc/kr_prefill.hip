@@ -11,8 +11,8 @@
 // lane l supplies A[l % 32][16 (l / 32) .. +15] and B[16 (l / 32) .. +15][l % 32];
 // result register r of lane l is C[8 (r / 4) + 4 (l / 32) + r % 4][l % 32].
 // A = the tokens' activations, B = the weight rows, so each lane holds one
-// weight row (one scale per block) and 16 tokens, whose scales are read from
-// the transposed activation scales xdT[b][t]. The per-block rescale and the
+// weight row (one scale per block) and 16 tokens, whose scales come from the
+// transposed activation scales xdT[b][t] through the workgroup's LDS tile. The per-block rescale and the
 // ordered accumulation are 4 unfused VALU operations per output and block,
 // which bound the kernel, not the MFMA.
 #include "kr_internal.h"
@@ -76,17 +76,18 @@ __device__ __forceinline__ v4i weight_frag(const uint8_t *blk, int h) {
 // 128-token prefill steps), whose few 128-row tiles would leave most CUs idle
 // with each tile's VALU work in series.
 
-// Per wave and block: the wave's 32 tokens and their scales.
+// Per wave and block: the wave's 32 tokens.
 struct XFrag {
     v4i xa;              // the wave's 32 tokens
-    float xs;            // scale of token l % 32 of the wave's group
 };
 
-// Per thread and block, for the workgroup's weight tile: 16 quant bytes of
-// row tid / 2 (half tid % 2, Q4 unpacked to n - 8) and that row's raw scale.
+// Per thread and block, for the workgroup's tile: 16 quant bytes of weight
+// row tid / 2 (half tid % 2, Q4 unpacked to n - 8), that row's raw scale, and
+// the scale of the workgroup's token tid % 128.
 struct WReg {
     v4i w;
     uint32_t d;
+    float xs;
 };
 
 constexpr int MM_ST = 3;   // LDS ring stages of the weight tile
@@ -96,29 +97,34 @@ template <int NG>
 struct MmLds {
     v4i w[MM_ST][32 * NG][2];     // [stage][row][half]
     uint32_t d[MM_ST][32 * NG];   // [stage][row] raw scale bits
+    float xs[MM_ST][MM_TT];       // [stage][token] the tokens' scales
 };
 
 __device__ __forceinline__ void x_load(XFrag &f, const MmArgs &a, int b, int tokl, int lane) {
     const int t = tokl + (lane & 31);   // readable: the caller pads the activations to ldx rows
     const int4 v = *(const int4 *)(a.xq + (size_t)t * a.K + (size_t)b * 32 + 16 * (lane >> 5));
     f.xa = v4i{ v.x, v.y, v.z, v.w };
-    f.xs = a.xdT[(size_t)b * a.ldx + t];
 }
 
 // thread tid loads half tid % 2 of tile row (tid / 2) mod 32 NG (for NG < 4
 // the surplus threads repeat a row's load, which keeps every load
 // unconditional; only the first 64 NG store it)
+// (xcol: the workgroup's first token column of xdT; every thread loads a
+// token scale, threads 128.. the same as thread tid - 128, unused)
 template <int QT, int D16, int NG>
-__device__ __forceinline__ void w_load(WReg &R, const MMat &W, int nb, int b, int rowl, int tid) {
+__device__ __forceinline__ void w_load(WReg &R, const MMat &W, const float *xcol, int ldx, int nb, int b, int rowl,
+                                       int tid) {
     int r = rowl + ((tid >> 1) & (32 * NG - 1));
     r = r < W.rows ? r : W.rows - 1;   // rows past the end re-read the last row (not stored)
     const size_t blk = (size_t)r * nb + b;
     R.w = weight_frag<QT>(W.q + blk * (QT == ML_Q8_0 ? 32 : 16), tid & 1);
     R.d = D16 ? (uint32_t)((const uint16_t *)W.d)[blk] : ((const uint32_t *)W.d)[blk];
+    R.xs = xcol[(size_t)b * ldx + (tid & (MM_TT - 1))];
 }
 
 template <int NG>
 __device__ __forceinline__ void w_store(MmLds<NG> &L, int st, const WReg &R, int tid) {
+    if (tid < MM_TT) L.xs[st][tid] = R.xs;
     if ((tid >> 1) >= 32 * NG) return;
     L.w[st][tid >> 1][tid & 1] = R.w;
     if ((tid & 1) == 0) L.d[st][tid >> 1] = R.d;
@@ -126,12 +132,14 @@ __device__ __forceinline__ void w_store(MmLds<NG> &L, int st, const WReg &R, int
 
 // The MFMA of row group g + 1 is issued before the rescale of group g, so
 // its latency runs under that VALU work. The 16 token scales a lane needs
-// (tokens 8 (r / 4) + 4 (lane / 32) + r % 4) come from the lanes that loaded
-// them, over the LDS crossbar: one 4-byte load per lane and block instead of
-// four 16-byte broadcast loads. The weight fragments and scales come from
-// the workgroup's LDS tile.
+// (tokens 8 (r / 4) + 4 (lane / 32) + r % 4 of the wave's 32: the same for
+// the 32 lanes of a half-wave) are four 16-byte LDS broadcast reads of the
+// tile's token scales (16 cross-lane shuffles of one loaded scale per lane
+// cost 3-6% more time). The weight fragments and scales come from the
+// workgroup's LDS tile as well.
 template <int D16, int NG>
-__device__ __forceinline__ void mm_step(float (&acc)[NG][16], const XFrag &f, const MmLds<NG> &L, int st, int lane) {
+__device__ __forceinline__ void mm_step(float (&acc)[NG][16], const XFrag &f, const MmLds<NG> &L, int st, int lane,
+                                        int tokw) {
     const int ln = lane & 31, hf = lane >> 5;
     v4i wb[NG];
     uint32_t wdr[NG];
@@ -141,9 +149,15 @@ __device__ __forceinline__ void mm_step(float (&acc)[NG][16], const XFrag &f, co
         wdr[g] = L.d[st][32 * g + ln];
     }
     float xd[16];
-    const int hb = 4 * hf;
+    const float4 *xv = (const float4 *)&L.xs[st][tokw + 4 * hf];
 #pragma unroll
-    for (int r = 0; r < 16; r++) xd[r] = __shfl(f.xs, 8 * (r >> 2) + hb + (r & 3), 64);
+    for (int q = 0; q < 4; q++) {
+        const float4 v = xv[2 * q];   // tokens 8 q + 4 hf .. + 3
+        xd[4 * q] = v.x;
+        xd[4 * q + 1] = v.y;
+        xd[4 * q + 2] = v.z;
+        xd[4 * q + 3] = v.w;
+    }
     v16i s = __builtin_amdgcn_mfma_i32_32x32x32_i8(f.xa, wb[0], v16i{}, 0, 0, 0);
 #pragma unroll
     for (int g = 0; g < NG; g++) {
@@ -178,6 +192,7 @@ __global__ void __launch_bounds__(256, 2) k_matmul(const MmArgs a) {
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int rowl = rt * 32 * NG, tokl = tt * MM_TT + 32 * wave;
     const int nb = a.K / KR_QK;
+    const float *xcol = a.xdT + (size_t)tt * MM_TT;
 
     float acc[NG][16];
 #pragma unroll
@@ -194,9 +209,9 @@ __global__ void __launch_bounds__(256, 2) k_matmul(const MmArgs a) {
     if constexpr (NG == 4) {
         WReg R;
         XFrag x0, x1;
-        w_load<QT, D16, NG>(R, W, nb, 0, rowl, tid);
+        w_load<QT, D16, NG>(R, W, xcol, a.ldx, nb, 0, rowl, tid);
         w_store(L, 0, R, tid);
-        w_load<QT, D16, NG>(R, W, nb, 1 < bl ? 1 : bl, rowl, tid);
+        w_load<QT, D16, NG>(R, W, xcol, a.ldx, nb, 1 < bl ? 1 : bl, rowl, tid);
         x_load(x0, a, 0, tokl, lane);
         x_load(x1, a, 1 < bl ? 1 : bl, tokl, lane);
         __syncthreads();
@@ -204,13 +219,13 @@ __global__ void __launch_bounds__(256, 2) k_matmul(const MmArgs a) {
         for (int b = 0; b < nb; b += 2) {
             const int s1 = st == MM_ST - 1 ? 0 : st + 1, s2 = s1 == MM_ST - 1 ? 0 : s1 + 1;
             w_store(L, s1, R, tid);
-            w_load<QT, D16, NG>(R, W, nb, b + 2 < bl ? b + 2 : bl, rowl, tid);
-            mm_step<D16, NG>(acc, x0, L, st, lane);
+            w_load<QT, D16, NG>(R, W, xcol, a.ldx, nb, b + 2 < bl ? b + 2 : bl, rowl, tid);
+            mm_step<D16, NG>(acc, x0, L, st, lane, 32 * wave);
             x_load(x0, a, b + 2 < bl ? b + 2 : bl, tokl, lane);
             __syncthreads();
             w_store(L, s2, R, tid);
-            w_load<QT, D16, NG>(R, W, nb, b + 3 < bl ? b + 3 : bl, rowl, tid);
-            if (b + 1 < nb) mm_step<D16, NG>(acc, x1, L, s1, lane);
+            w_load<QT, D16, NG>(R, W, xcol, a.ldx, nb, b + 3 < bl ? b + 3 : bl, rowl, tid);
+            if (b + 1 < nb) mm_step<D16, NG>(acc, x1, L, s1, lane, 32 * wave);
             x_load(x1, a, b + 3 < bl ? b + 3 : bl, tokl, lane);
             __syncthreads();
             st = s2;
@@ -229,19 +244,19 @@ __global__ void __launch_bounds__(256, 2) k_matmul(const MmArgs a) {
         XFrag x[MM_PD];
 #pragma unroll
         for (int j = 0; j < MM_PD; j++) {
-            w_load<QT, D16, NG>(R[j], W, nb, j < bl ? j : bl, rowl, tid);
+            w_load<QT, D16, NG>(R[j], W, xcol, a.ldx, nb, j < bl ? j : bl, rowl, tid);
             x_load(x[j], a, j < bl ? j : bl, tokl, lane);
         }
         w_store(L, 0, R[0], tid);
-        w_load<QT, D16, NG>(R[0], W, nb, MM_PD < bl ? MM_PD : bl, rowl, tid);
+        w_load<QT, D16, NG>(R[0], W, xcol, a.ldx, nb, MM_PD < bl ? MM_PD : bl, rowl, tid);
         __syncthreads();
         for (int b0 = 0; b0 < nb; b0 += MM_PD) {
 #pragma unroll
             for (int k = 0; k < MM_PD; k++) {
                 const int t = b0 + k, k1 = (k + 1) % MM_PD;
                 w_store(L, (k + 1) & 1, R[k1], tid);
-                w_load<QT, D16, NG>(R[k1], W, nb, t + 1 + MM_PD < bl ? t + 1 + MM_PD : bl, rowl, tid);
-                if (t < nb) mm_step<D16, NG>(acc, x[k], L, k & 1, lane);
+                w_load<QT, D16, NG>(R[k1], W, xcol, a.ldx, nb, t + 1 + MM_PD < bl ? t + 1 + MM_PD : bl, rowl, tid);
+                if (t < nb) mm_step<D16, NG>(acc, x[k], L, k & 1, lane, 32 * wave);
                 x_load(x[k], a, t + MM_PD < bl ? t + MM_PD : bl, tokl, lane);
                 __syncthreads();
             }
