@@ -212,6 +212,16 @@ void krh_store_kv(int kv_type, void *kc, void *vc, float *kd, float *vd, const f
  * 128 and >= T; xq must be readable for ldx rows. */
 void krh_matmul(float *Y, int ldy, const krh_mat *W, const int8_t *xq, const float *xdT, int ldx, int T,
                 int accumulate);
+/* The FFN's products and activation of a prompt step in one launch
+ * (model/transformer.c:410-413: the w1 and w3 ml_matmul calls, then
+ * TOK_DOWN_IN's act_mul and quantize_row_t, :353-355): per
+ * token t, h = silu(w1 x_t) * (w3 x_t) (k_scalar.c:96-98), quantized to Q8_0
+ * (k_scalar.c:39-57) into hq [T][rows] and the transposed scales hdT
+ * [rows / 32][ldx], the layout krh_matmul reads. The same bits as two
+ * krh_matmul calls and krh_silu_quant; hq, hdT must not overlap xq, xdT.
+ * w1, w3: one shape, type and scale width, rows % 32 == 0. */
+void krh_matmul_swiglu(int8_t *hq, float *hdT, const krh_mat *w1, const krh_mat *w3, const int8_t *xq,
+                       const float *xdT, int ldx, int T);
 /* the three attention projections of T tokens at positions pos0.. with bias
  * and RoPE: q [T][q_dim], k and v into cache rows pos0 + t
  * (model/transformer.c:400-402, :335-344) */

@@ -270,13 +270,18 @@ __device__ __forceinline__ float kr_spec_sum(float *t, int n, unsigned char *lds
         int mask = 0, nseg = 0;
         bool run = false;
         int *re = p ? re1 : re0;
-        float4 cur[4], nxt[4];
+        // two register buffers in turn: block blk + 1's LDS reads are issued
+        // before block blk's adds and arrive under them (a copy out of one
+        // prefetch buffer let the compiler issue the reads after the adds,
+        // so every block waited out the LDS latency)
+        float4 ba[4], bb[4];
 #pragma unroll
-        for (int q = 0; q < 4; q++) cur[q] = ((const float4 *)tc)[q];
-        for (int blk = 0; blk < NB; blk++) {
+        for (int q = 0; q < 4; q++) ba[q] = ((const float4 *)tc)[q];
+        auto block = [&](int blk, const float4 (&cur)[4], float4 (&nxt)[4]) {
             const float4 *nb4 = (const float4 *)(tc + min(blk + 1, NB - 1) * SC_BLK);
 #pragma unroll
             for (int q = 0; q < 4; q++) nxt[q] = nb4[q];
+            __builtin_amdgcn_sched_barrier(0);
             const float s_start = s;
 #pragma unroll
             for (int q = 0; q < 4; q++) {
@@ -302,8 +307,10 @@ __device__ __forceinline__ float kr_spec_sum(float *t, int n, unsigned char *lds
             } else {
                 run = true;
             }
-#pragma unroll
-            for (int q = 0; q < 4; q++) cur[q] = nxt[q];
+        };
+        for (int blk = 0; blk < NB; blk += 2) {   // NB = L / 16 is even (L >= 128)
+            block(blk, ba, bb);
+            block(blk + 1, bb, ba);
         }
         if (run) {
             if (p == 0) rb[c * SC_NSEG + nseg] = (int)b;

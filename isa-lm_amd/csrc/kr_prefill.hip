@@ -29,7 +29,7 @@ struct MMat {
     int rows, cols, type, d16;
 };
 
-enum { MM_STORE = 0, MM_ADD = 1, MM_QKV = 2 };
+enum { MM_STORE = 0, MM_ADD = 1, MM_QKV = 2, MM_SWIGLU = 3 };
 
 struct MmArgs {
     MMat w[3];
@@ -45,6 +45,8 @@ struct MmArgs {
     const float *rope_cos, *rope_sin;
     int head_dim, pos0;
     int ng;              // row groups per wave (the kernel's NG)
+    int8_t *hq;          // MM_SWIGLU: h's Q8_0 quants [T][rows] and scales [rows / 32][ldx]
+    float *hdT;
 };
 
 constexpr int MM_TT = 128;   // tokens per workgroup
@@ -110,15 +112,20 @@ __device__ __forceinline__ void x_load(XFrag &f, const MmArgs &a, int b, int tok
 // the surplus threads repeat a row's load, which keeps every load
 // unconditional; only the first 64 NG store it)
 // (xcol: the workgroup's first token column of xdT; every thread loads a
-// token scale, threads 128.. the same as thread tid - 128, unused)
-template <int QT, int D16, int NG>
+// token scale, threads 128.. the same as thread tid - 128, unused). PAIR (NG
+// 4): tile rows 0-63 are rows rowl.. of W, tile rows 64-127 the same rows of
+// W2 (SwiGLU's w1 and w3).
+template <int QT, int D16, int NG, bool PAIR = false>
 __device__ __forceinline__ void w_load(WReg &R, const MMat &W, const float *xcol, int ldx, int nb, int b, int rowl,
-                                       int tid) {
-    int r = rowl + ((tid >> 1) & (32 * NG - 1));
+                                       int tid, const MMat &W2 = MMat{}) {
+    const int tr = (tid >> 1) & (32 * NG - 1);
+    int r = rowl + (PAIR ? tr & 63 : tr);
     r = r < W.rows ? r : W.rows - 1;   // rows past the end re-read the last row (not stored)
     const size_t blk = (size_t)r * nb + b;
-    R.w = weight_frag<QT>(W.q + blk * (QT == ML_Q8_0 ? 32 : 16), tid & 1);
-    R.d = D16 ? (uint32_t)((const uint16_t *)W.d)[blk] : ((const uint32_t *)W.d)[blk];
+    const uint8_t *wq = PAIR && tr >= 64 ? W2.q : W.q;
+    const void *wd = PAIR && tr >= 64 ? W2.d : W.d;
+    R.w = weight_frag<QT>(wq + blk * (QT == ML_Q8_0 ? 32 : 16), tid & 1);
+    R.d = D16 ? (uint32_t)((const uint16_t *)wd)[blk] : ((const uint32_t *)wd)[blk];
     R.xs = xcol[(size_t)b * ldx + (tid & (MM_TT - 1))];
 }
 
@@ -190,7 +197,8 @@ __global__ void __launch_bounds__(256, 2) k_matmul(const MmArgs a) {
     const int local = (int)blockIdx.x - a.tile0[mi];
     const int rt = local / ntt, tt = local - rt * ntt;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int rowl = rt * 32 * NG, tokl = tt * MM_TT + 32 * wave;
+    constexpr bool PAIR = EPI == MM_SWIGLU;   // 64 rows of w1 and the same 64 of w3
+    const int rowl = rt * (PAIR ? 64 : 32 * NG), tokl = tt * MM_TT + 32 * wave;
     const int nb = a.K / KR_QK;
     const float *xcol = a.xdT + (size_t)tt * MM_TT;
 
@@ -209,9 +217,9 @@ __global__ void __launch_bounds__(256, 2) k_matmul(const MmArgs a) {
     if constexpr (NG == 4) {
         WReg R;
         XFrag x0, x1;
-        w_load<QT, D16, NG>(R, W, xcol, a.ldx, nb, 0, rowl, tid);
+        w_load<QT, D16, NG, PAIR>(R, W, xcol, a.ldx, nb, 0, rowl, tid, a.w[1]);
         w_store(L, 0, R, tid);
-        w_load<QT, D16, NG>(R, W, xcol, a.ldx, nb, 1 < bl ? 1 : bl, rowl, tid);
+        w_load<QT, D16, NG, PAIR>(R, W, xcol, a.ldx, nb, 1 < bl ? 1 : bl, rowl, tid, a.w[1]);
         x_load(x0, a, 0, tokl, lane);
         x_load(x1, a, 1 < bl ? 1 : bl, tokl, lane);
         __syncthreads();
@@ -219,12 +227,12 @@ __global__ void __launch_bounds__(256, 2) k_matmul(const MmArgs a) {
         for (int b = 0; b < nb; b += 2) {
             const int s1 = st == MM_ST - 1 ? 0 : st + 1, s2 = s1 == MM_ST - 1 ? 0 : s1 + 1;
             w_store(L, s1, R, tid);
-            w_load<QT, D16, NG>(R, W, xcol, a.ldx, nb, b + 2 < bl ? b + 2 : bl, rowl, tid);
+            w_load<QT, D16, NG, PAIR>(R, W, xcol, a.ldx, nb, b + 2 < bl ? b + 2 : bl, rowl, tid, a.w[1]);
             mm_step<D16, NG>(acc, x0, L, st, lane, 32 * wave);
             x_load(x0, a, b + 2 < bl ? b + 2 : bl, tokl, lane);
             __syncthreads();
             w_store(L, s2, R, tid);
-            w_load<QT, D16, NG>(R, W, xcol, a.ldx, nb, b + 3 < bl ? b + 3 : bl, rowl, tid);
+            w_load<QT, D16, NG, PAIR>(R, W, xcol, a.ldx, nb, b + 3 < bl ? b + 3 : bl, rowl, tid, a.w[1]);
             if (b + 1 < nb) mm_step<D16, NG>(acc, x1, L, s1, lane, 32 * wave);
             x_load(x1, a, b + 3 < bl ? b + 3 : bl, tokl, lane);
             __syncthreads();
@@ -244,18 +252,19 @@ __global__ void __launch_bounds__(256, 2) k_matmul(const MmArgs a) {
         XFrag x[MM_PD];
 #pragma unroll
         for (int j = 0; j < MM_PD; j++) {
-            w_load<QT, D16, NG>(R[j], W, xcol, a.ldx, nb, j < bl ? j : bl, rowl, tid);
+            w_load<QT, D16, NG, PAIR>(R[j], W, xcol, a.ldx, nb, j < bl ? j : bl, rowl, tid, a.w[1]);
             x_load(x[j], a, j < bl ? j : bl, tokl, lane);
         }
         w_store(L, 0, R[0], tid);
-        w_load<QT, D16, NG>(R[0], W, xcol, a.ldx, nb, MM_PD < bl ? MM_PD : bl, rowl, tid);
+        w_load<QT, D16, NG, PAIR>(R[0], W, xcol, a.ldx, nb, MM_PD < bl ? MM_PD : bl, rowl, tid, a.w[1]);
         __syncthreads();
         for (int b0 = 0; b0 < nb; b0 += MM_PD) {
 #pragma unroll
             for (int k = 0; k < MM_PD; k++) {
                 const int t = b0 + k, k1 = (k + 1) % MM_PD;
                 w_store(L, (k + 1) & 1, R[k1], tid);
-                w_load<QT, D16, NG>(R[k1], W, xcol, a.ldx, nb, t + 1 + MM_PD < bl ? t + 1 + MM_PD : bl, rowl, tid);
+                w_load<QT, D16, NG, PAIR>(R[k1], W, xcol, a.ldx, nb, t + 1 + MM_PD < bl ? t + 1 + MM_PD : bl, rowl,
+                                          tid, a.w[1]);
                 if (t < nb) mm_step<D16, NG>(acc, x[k], L, k & 1, lane, 32 * wave);
                 x_load(x[k], a, t + MM_PD < bl ? t + MM_PD : bl, tokl, lane);
                 __syncthreads();
@@ -264,6 +273,30 @@ __global__ void __launch_bounds__(256, 2) k_matmul(const MmArgs a) {
     }
 
     // epilogue: lane = one row (32 g + lane % 32), tokens 8 (r / 4) + 4 (lane / 32) + r % 4
+    if constexpr (PAIR) {
+        // h = silu(w1 x) * (w3 x) (k_scalar.c:96-98), then its Q8_0 in blocks
+        // of 32 rows (k_scalar.c:39-57): a block's 32 values are the 32 lanes
+        // of a half-wave (groups 0, 1: w1 rows; 2, 3: the same w3 rows)
+#pragma unroll
+        for (int g = 0; g < 2; g++) {
+            const int row = rowl + 32 * g + (lane & 31);
+            const bool bin = rowl + 32 * g < W.rows;   // rows % 32 == 0: whole blocks in or out
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int t = tokl + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                const float h1 = acc[g][r], h3 = acc[g + 2][r];
+                const float v = kr_fmul(kr_fdiv(h1, kr_fadd(1.0f, kr_expf(-h1))), h3);
+                int8_t q;
+                float d;
+                kr_quant_block32(v, &q, &d);
+                if (bin && t < a.T) {
+                    a.hq[(size_t)t * W.rows + row] = q;
+                    if ((lane & 31) == 0) a.hdT[(size_t)(row >> 5) * a.ldx + t] = d;
+                }
+            }
+        }
+        return;
+    }
     float *Y = mi == 0 ? a.y[0] : (mi == 1 ? a.y[1] : a.y[2]);
     const int ldy = mi == 0 ? a.ldy[0] : (mi == 1 ? a.ldy[1] : a.ldy[2]);
     const float *bias = mi == 0 ? a.bias[0] : (mi == 1 ? a.bias[1] : a.bias[2]);
@@ -305,13 +338,17 @@ void launch_mm(const MmArgs &a, const MMat &W) {
         return;
     }
     auto go = [&](auto kern) { hipLaunchKernelGGL(kern, dim3(grid), dim3(256), 0, kr_stream(), a); };
+    if (EPI == MM_SWIGLU && a.ng != 4) {
+        kr_fail(ML_E_SHAPE, "matmul: SwiGLU pairs take 128-row tiles", hipSuccess);
+        return;
+    }
     if (a.ng == 4) {
         if (W.type == ML_Q8_0) {
             if (W.d16) go(k_matmul<EPI, ML_Q8_0, 1, 4>); else go(k_matmul<EPI, ML_Q8_0, 0, 4>);
         } else {
             if (W.d16) go(k_matmul<EPI, ML_Q4_0, 1, 4>); else go(k_matmul<EPI, ML_Q4_0, 0, 4>);
         }
-    } else {
+    } else if constexpr (EPI != MM_SWIGLU) {
         if (W.type == ML_Q8_0) {
             if (W.d16) go(k_matmul<EPI, ML_Q8_0, 1, 1>); else go(k_matmul<EPI, ML_Q8_0, 0, 1>);
         } else {
@@ -393,6 +430,32 @@ __global__ void k_embed_batch(float *x, const MMat e, const int *tok, float scal
 }  // namespace
 
 // ---- C ABI ----
+
+extern "C" void krh_matmul_swiglu(int8_t *hq, float *hdT, const krh_mat *w1, const krh_mat *w3, const int8_t *xq,
+                                  const float *xdT, int ldx, int T) {
+    if (!hq || !hdT || w1->rows != w3->rows || w1->cols != w3->cols || w1->type != w3->type || w1->d16 != w3->d16 ||
+        w1->rows % KR_QK) {
+        kr_fail(ML_E_SHAPE, "matmul_swiglu: w1 and w3 of one shape, type and scale width, rows % 32 == 0",
+                hipSuccess);
+        return;
+    }
+    MmArgs a = {};
+    a.w[0] = to_mmat(w1);
+    a.w[1] = to_mmat(w3);
+    a.nmat = 1;
+    a.tile0[0] = 0;
+    const int ntt = (T + MM_TT - 1) / MM_TT;
+    a.ng = 4;
+    a.tile0[1] = (w1->rows + 63) / 64 * ntt;
+    a.xq = xq;
+    a.xdT = xdT;
+    a.ldx = ldx;
+    a.T = T;
+    a.K = w1->cols;
+    a.hq = hq;
+    a.hdT = hdT;
+    launch_mm<MM_SWIGLU>(a, a.w[0]);
+}
 
 extern "C" void krh_matmul(float *Y, int ldy, const krh_mat *W, const int8_t *xq, const float *xdT, int ldx, int T,
                            int accumulate) {

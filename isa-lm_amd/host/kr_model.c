@@ -606,6 +606,18 @@ static ml_status batch_buffers(kr_state *s, int with_logits) {
     return ML_OK;
 }
 
+/* whether a prompt step of T tokens takes the FFN as one launch
+ * (krh_matmul_swiglu: 64-row tiles of w1 and w3 together): from 3/4 of a
+ * tile per compute unit, where the single launch fills the device; shorter
+ * steps keep the separate products, whose 32-row tiles do. */
+static int swiglu_fused(const kr_state *s, const struct kr_dev_layer *D, int T) {
+    const ml_config *c = &s->m->cfg;
+    if (D->w1.type != D->w3.type || D->w1.d16 != D->w3.d16 || c->hidden_dim % 32) return 0;
+    const long tiles = (long)(c->hidden_dim + 63) / 64 * ((T + 127) / 128);
+    const int cus = krh_device_cus() > 0 ? krh_device_cus() : 256;
+    return 4 * tiles >= 3L * cus;
+}
+
 /* rmsnorm of rows rows of n floats in place, w shared, in launches of at
  * most KRH_ROWS_MAX rows (the per-head norms of a batch) */
 static void norm_rows(float *x, const float *w, int n, float eps, long rows) {
@@ -723,10 +735,17 @@ static ml_status prefill_step(kr_state *s, const int *tokens, int T, int p0, flo
         krh_quantize_q8_t(s->bxq, s->bxd, ldx, s->bao, c->q_dim, T);
         krh_matmul(s->bx, c->dim, &D->wo, s->bxq, s->bxd, ldx, T, 1);
         krh_rmsnorm_q8_t(s->bxq, s->bxd, ldx, NULL, s->bx, D->ffn_norm, c->dim, c->norm_eps, T);
-        krh_matmul(s->bh1, c->hidden_dim, &D->w1, s->bxq, s->bxd, ldx, T, 0);
-        krh_matmul(s->bh3, c->hidden_dim, &D->w3, s->bxq, s->bxd, ldx, T, 0);
-        krh_silu_quant(s->bxq, s->bxd, ldx, s->bh1, s->bh3, c->hidden_dim, T);
-        krh_matmul(s->bx, c->dim, &D->w2, s->bxq, s->bxd, ldx, T, 1);
+        if (swiglu_fused(s, D, T)) {   /* h's Q8_0 in bh1's space (4x what it needs) */
+            int8_t *hq = (int8_t *)s->bh1;
+            float *hd = (float *)((uint8_t *)s->bh1 + RUP((size_t)ldx * c->hidden_dim));
+            krh_matmul_swiglu(hq, hd, &D->w1, &D->w3, s->bxq, s->bxd, ldx, T);
+            krh_matmul(s->bx, c->dim, &D->w2, hq, hd, ldx, T, 1);
+        } else {
+            krh_matmul(s->bh1, c->hidden_dim, &D->w1, s->bxq, s->bxd, ldx, T, 0);
+            krh_matmul(s->bh3, c->hidden_dim, &D->w3, s->bxq, s->bxd, ldx, T, 0);
+            krh_silu_quant(s->bxq, s->bxd, ldx, s->bh1, s->bh3, c->hidden_dim, T);
+            krh_matmul(s->bx, c->dim, &D->w2, s->bxq, s->bxd, ldx, T, 1);
+        }
     }
     if (logits) {
         krh_rmsnorm_q8_t(s->bxq, s->bxd, ldx, NULL, s->bx, m->d_final_norm, c->dim, c->norm_eps, T);

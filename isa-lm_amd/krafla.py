@@ -178,6 +178,7 @@ for name, res, args in [
     ("krh_rmsnorm_q8_t", None, [_P, _P, C.c_int, _P, _P, _P, C.c_int, C.c_float, C.c_int]),
     ("krh_quantize_q8_t", None, [_P, _P, C.c_int, _P, C.c_int, C.c_int]),
     ("krh_matmul", None, [_P, C.c_int, C.POINTER(KrhMat), _P, _P, C.c_int, C.c_int, C.c_int]),
+    ("krh_matmul_swiglu", None, [_P, _P, C.POINTER(KrhMat), C.POINTER(KrhMat), _P, _P, C.c_int, C.c_int]),
     ("krh_matmul_qkv", None, [_P, _P, _P, C.POINTER(KrhMat), C.POINTER(KrhMat), C.POINTER(KrhMat), _P, _P, _P,
                               _P, _P, C.c_int, C.c_int, _P, _P, C.c_int, C.c_int]),
     ("krh_matmul_qkv_stage", None, [_P, _P, _P, C.POINTER(KrhMat), C.POINTER(KrhMat), C.POINTER(KrhMat), _P, _P,

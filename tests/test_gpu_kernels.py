@@ -604,6 +604,48 @@ def test_silu_quant(dev):
         assert np.array_equal(q[t], q0) and np.array_equal(bits(d[:, t]), bits(d0))
 
 
+@pytest.mark.parametrize("typ,d16", [(K.ML_Q8_0, 1), (K.ML_Q4_0, 1), (K.ML_Q8_0, 0)])
+@pytest.mark.parametrize("rows,cols,T", [(14336, 4096, 300), (4864, 896, 511), (768, 288, 37), (96, 64, 5),
+                                         (8192, 2048, 129)])
+def test_matmul_swiglu_matches_separate(dev, typ, d16, rows, cols, T):
+    """krh_matmul_swiglu (w1 and w3 tiles in one launch, SiLU and the Q8_0 of
+    h in its epilogue) gives the bits of two krh_matmul calls and
+    krh_silu_quant (both pinned to the oracle above): the quants and the
+    transposed scales of every token (96 rows: a half-empty last tile)"""
+    mats = [rand_mat(rows, cols, typ, d16) for _ in range(2)]
+    Ws = [dmat(dev, q, d, dh, rows, cols, typ, d16) for q, d, dh in mats]
+    X = f32(RNG.normal(0, 1, (T, cols)) * RNG.choice([1e-2, 1.0, 30.0], (T, 1)))
+    ldx = (T + 127) // 128 * 128
+    xq = np.zeros((ldx, cols), np.int8)
+    xd = np.zeros((T, cols // 32), np.float32)
+    for t in range(T):
+        xq[t], xd[t] = O.quantize(X[t])
+    xqb, xdb = dev.put(xq), dev.put(transposed_scales(xd, T, cols // 32, ldx))
+    g, u = dev.zeros(4 * ldx * rows), dev.zeros(4 * ldx * rows)
+    K.hip.krh_matmul(g.ptr, rows, C.byref(Ws[0]), xqb.ptr, xdb.ptr, ldx, T, 0)
+    K.hip.krh_matmul(u.ptr, rows, C.byref(Ws[1]), xqb.ptr, xdb.ptr, ldx, T, 0)
+    wq, wd = dev.zeros(ldx * rows), dev.zeros(4 * ldx * rows // 32)
+    K.hip.krh_silu_quant(wq.ptr, wd.ptr, ldx, g.ptr, u.ptr, rows, T)
+    hq, hd = dev.zeros(ldx * rows), dev.zeros(4 * ldx * rows // 32)
+    K.hip.krh_matmul_swiglu(hq.ptr, hd.ptr, C.byref(Ws[0]), C.byref(Ws[1]), xqb.ptr, xdb.ptr, ldx, T)
+    ok()
+    assert np.array_equal(hq.get(np.int8, ldx * rows).reshape(ldx, rows)[:T],
+                          wq.get(np.int8, ldx * rows).reshape(ldx, rows)[:T])
+    got_d = hd.get(np.float32, ldx * rows // 32).reshape(rows // 32, ldx)[:, :T]
+    want_d = wd.get(np.float32, ldx * rows // 32).reshape(rows // 32, ldx)[:, :T]
+    assert np.array_equal(bits(got_d), bits(want_d))
+
+
+def test_matmul_swiglu_rejects_mismatched_pairs(dev):
+    q, d, dh = rand_mat(64, 64, K.ML_Q8_0, 1)
+    W1 = dmat(dev, q, d, dh, 64, 64, K.ML_Q8_0, 1)
+    W3 = dmat(dev, q, d, dh, 64, 64, K.ML_Q8_0, 0)   # another scale width
+    buf = dev.zeros(4 * 128 * 64)
+    K.hip.krh_matmul_swiglu(buf.ptr, buf.ptr, C.byref(W1), C.byref(W3), buf.ptr, buf.ptr, 128, 5)
+    assert K.hip.krh_status() == K.ML_E_SHAPE
+    K.hip.krh_clear_error()
+
+
 # ---- rmsnorm fused into the consuming matvec ----
 
 def oracle_norm_q8(x, w, eps=1e-5):
