@@ -611,13 +611,17 @@ void launch_mv(MvArgs &a, const KMat &W) {
 
 // One workgroup per token; each thread keeps its float4 slices of x and w in
 // registers (n <= RN_MAX); see rmsnorm_q8_block.
+// V4: float4 slices of x and w per thread (n <= RN_THREADS * V4 * 4): 4 for
+// rows up to 4096 keep the kernel at a quarter of the registers of 16, so
+// four times the tokens are in flight (each token's ordered sum is latency)
+template <int V4>
 __global__ void __launch_bounds__(RN_THREADS) k_rmsnorm_q8(int8_t *q, float *d, int dld, float *xb, const float *x,
                                                            const float *w, int n, float eps, int norm) {
     const size_t t = blockIdx.x;
     // scales [t][n / 32], or transposed [n / 32][dld] when dld > 0
     extern __shared__ __align__(16) float rn_smem[];
-    rmsnorm_q8_block<RN_THREADS, RN_V4>(q + t * n, d + (dld > 0 ? t : t * (n / KR_QK)), dld > 0 ? (size_t)dld : 1,
-                                        xb ? xb + t * n : nullptr, x + t * n, w, n, eps, norm != 0, rn_smem);
+    rmsnorm_q8_block<RN_THREADS, V4>(q + t * n, d + (dld > 0 ? t : t * (n / KR_QK)), dld > 0 ? (size_t)dld : 1,
+                                     xb ? xb + t * n : nullptr, x + t * n, w, n, eps, norm != 0, rn_smem);
 }
 
 // Q8_0 of ntok rows of n floats, QZ_CHUNK values per workgroup: thread t
@@ -830,7 +834,12 @@ extern "C" void krh_rmsnorm_q8_t(int8_t *q, float *d, int dld, float *xb, const 
         kr_fail(ML_E_SHAPE, "rmsnorm shape", hipSuccess);
         return;
     }
-    hipLaunchKernelGGL(k_rmsnorm_q8, dim3(ntok), dim3(RN_THREADS), lds, kr_stream(), q, d, dld, xb, x, w, n, eps, 1);
+    if (n <= RN_THREADS * 4 * 4)
+        hipLaunchKernelGGL(k_rmsnorm_q8<4>, dim3(ntok), dim3(RN_THREADS), lds, kr_stream(), q, d, dld, xb, x, w, n,
+                           eps, 1);
+    else
+        hipLaunchKernelGGL(k_rmsnorm_q8<RN_V4>, dim3(ntok), dim3(RN_THREADS), lds, kr_stream(), q, d, dld, xb, x, w,
+                           n, eps, 1);
     kr_check_launch("rmsnorm_q8");
 }
 
