@@ -295,7 +295,7 @@ __host__ __device__ inline MvLds mv_lds(int K, int maxloc, int nbc, bool norm) {
 // are in flight): copied, quantized, or normalized first (rmsnorm's ordered
 // sum, k_scalar.c:59-64) and quantized.
 template <int EPI, int QT, int D16>
-__global__ void __launch_bounds__(MV_THREADS, 2) k_matvec(const MvArgs a) {
+__global__ void __launch_bounds__(MV_THREADS, 3) k_matvec(const MvArgs a) {
     extern __shared__ __align__(16) unsigned char smem[];
     const int K = a.K, nb = K / KR_QK, tid = threadIdx.x;
     const int ntiles = a.nmat == 1 ? a.tile0[1] : a.nmat == 2 ? a.tile0[2] : a.tile0[3];
@@ -556,9 +556,11 @@ __global__ void __launch_bounds__(MV_THREADS, 2) k_matvec(const MvArgs a) {
     }
 }
 
-// workgroups resident at once: two per compute unit of this device (512 on
-// an MI355X's 256 CUs)
-int mv_resident() { return 2 * (krh_device_cus() > 0 ? krh_device_cus() : 256); }
+// workgroups resident at once: three per compute unit of this device (768
+// on an MI355X's 256 CUs; the kernel's 166 VGPRs fit three waves a SIMD).
+// Two a CU streamed the 8B decode at 274.9 tok/s, three at 282.5: more
+// weight loads in flight, and more waves to cover each other's ordered sums
+int mv_resident() { return 3 * (krh_device_cus() > 0 ? krh_device_cus() : 256); }
 
 // Rows per tile (one wave's): the largest power of two (at most cap, even for
 // the RoPE pairs) that still gives every resident wave a tile; blocks per
