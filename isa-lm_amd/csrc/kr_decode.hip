@@ -50,22 +50,24 @@ struct MvArgs {
     const int *pos;
     int kv16;            // EPI_QKV: k and v rows are the F16 cache's (halves)
     float *keep;         // EPI_ADD: receives the product W x as well; EPI_SWIGLU: receives w3 x
-    // workgroup 0 stores the prologue's results when set (float inputs held
-    // in registers only): the normalized x (with nw) and its Q8_0 quants and
-    // scales, as the reference's separate rmsnorm and quantize_q8 calls
-    // leave them in memory
+    // workgroup 0 stores the prologue's results when set (float inputs):
+    // the normalized x (with nw) and its Q8_0 quants and scales, as the
+    // reference's separate rmsnorm and quantize_q8 calls leave them in memory
     float *keep_xb;
     int8_t *keep_xq;
     float *keep_xd;
 };
 
 constexpr int MV_THREADS = 256;
-constexpr int MV_NPT = 4;   // weight blocks per thread per work item
+constexpr int MV_NPT = 2;   // weight blocks per thread per work item
 constexpr int MV_DEPTH = 2;    // work items in flight per wave: a wave that issues more loads than the
                                // memory pipeline holds stalls at issue
-constexpr int MV_XQ_MAX = 16384;   // quantized activations up to this length are staged from registers
-constexpr int MV_XF_MAX = 8192;    // float activations up to this length are normalized and quantized from registers
-constexpr int MV_XF_PLAIN_MAX = 16384;   // float activations without a norm: quantized from registers up to this length
+// Activations held in registers by the prologue (longer ones are staged
+// through LDS from memory): sized so that the kernel fits 128 VGPRs, four
+// workgroups per CU
+constexpr int MV_XQ_MAX = 8192;   // quantized activations up to this length are staged from registers
+constexpr int MV_XF_MAX = 4096;    // float activations up to this length are normalized and quantized from registers
+constexpr int MV_XF_PLAIN_MAX = 4096;   // float activations without a norm: quantized from registers up to this length
 
 template <typename T> __device__ __forceinline__ T pick3(int i, T a, T b, T c) { return i == 0 ? a : (i == 1 ? b : c); }
 
@@ -125,9 +127,9 @@ __device__ __forceinline__ float4 kr_norm4(float4 x, float inv, float4 w) {
 
 // Q8_0 of K floats into LDS: each thread takes 4 consecutive values, 8
 // threads a 32-block. K % 32 == 0, x 16-byte aligned. With w: the rmsnorm
-// output (x * inv) * w is quantized.
+// output (x * inv) * w is quantized, and also stored into xb when it is set.
 __device__ __forceinline__ void quantize_to_lds(const float *x, int K, int8_t *xs, float *xds,
-                                                const float *w = nullptr, float inv = 1.0f) {
+                                                const float *w = nullptr, float inv = 1.0f, float *xb = nullptr) {
     constexpr int B = 4;   // float4 loads in flight per thread
     for (int base = 0; base < K; base += 4 * B * MV_THREADS) {
         float4 vs[B], ws[B];
@@ -142,7 +144,11 @@ __device__ __forceinline__ void quantize_to_lds(const float *x, int K, int8_t *x
 #pragma unroll
         for (int k = 0; k < B; k++) {
             const int i = base + 4 * (k * MV_THREADS + threadIdx.x);   // K % 32 == 0: 8-lane groups all in or all out
-            if (i < K) kr_quant4(w ? kr_norm4(vs[k], inv, ws[k]) : vs[k], i, xs, xds, 1);
+            if (i < K) {
+                const float4 o = w ? kr_norm4(vs[k], inv, ws[k]) : vs[k];
+                kr_quant4(o, i, xs, xds, 1);
+                if (xb) *(float4 *)(xb + i) = o;
+            }
         }
     }
 }
@@ -295,7 +301,7 @@ __host__ __device__ inline MvLds mv_lds(int K, int maxloc, int nbc, bool norm) {
 // are in flight): copied, quantized, or normalized first (rmsnorm's ordered
 // sum, k_scalar.c:59-64) and quantized.
 template <int EPI, int QT, int D16>
-__global__ void __launch_bounds__(MV_THREADS, 3) k_matvec(const MvArgs a) {
+__global__ void __launch_bounds__(MV_THREADS, 4) k_matvec(const MvArgs a) {
     extern __shared__ __align__(16) unsigned char smem[];
     const int K = a.K, nb = K / KR_QK, tid = threadIdx.x;
     const int ntiles = a.nmat == 1 ? a.tile0[1] : a.nmat == 2 ? a.tile0[2] : a.tile0[3];
@@ -422,7 +428,7 @@ __global__ void __launch_bounds__(MV_THREADS, 3) k_matvec(const MvArgs a) {
             __syncthreads();
             const float ss = kr_spec_sum<MV_THREADS>(sq, K, (unsigned char *)(sq + sc_terms_cap(K)));
             const float inv = kr_fdiv(1.0f, kr_fsqrt(kr_fadd(kr_fdiv(ss, (float)K), a.eps)));
-            quantize_to_lds(a.xf, K, xs, xds, a.nw, inv);
+            quantize_to_lds(a.xf, K, xs, xds, a.nw, inv, blockIdx.x == 0 ? a.keep_xb : nullptr);
         } else {
             quantize_to_lds(a.xf, K, xs, xds);
         }
@@ -556,11 +562,13 @@ __global__ void __launch_bounds__(MV_THREADS, 3) k_matvec(const MvArgs a) {
     }
 }
 
-// workgroups resident at once: three per compute unit of this device (768
-// on an MI355X's 256 CUs; the kernel's 166 VGPRs fit three waves a SIMD).
-// Two a CU streamed the 8B decode at 274.9 tok/s, three at 282.5: more
-// weight loads in flight, and more waves to cover each other's ordered sums
-int mv_resident() { return 3 * (krh_device_cus() > 0 ? krh_device_cus() : 256); }
+// workgroups resident at once: four per compute unit of this device (1024
+// on an MI355X's 256 CUs; the kernel fits 128 VGPRs, four waves a SIMD).
+// The 8B decode streamed at 274.9 tok/s with two a CU (4 blocks per lane
+// and item, 166 VGPRs), 282.5 with three, 284.1 with four (2 blocks per lane
+// and item, the activations of up to 4096 held in registers): more waves to
+// cover each other's ordered sums and loads
+int mv_resident() { return 4 * (krh_device_cus() > 0 ? krh_device_cus() : 256); }
 
 // Rows per tile (one wave's): the largest power of two (at most cap, even for
 // the RoPE pairs) that still gives every resident wave a tile; blocks per
@@ -872,9 +880,9 @@ extern "C" void krh_quantize_q8_rows(int8_t *q, size_t ldq, float *d, size_t ldd
     kr_check_launch("quantize_q8");
 }
 
-// the prologue results a launch also stores (MvArgs::keep_*): only for a
-// float input held in registers (K up to MV_XF_MAX with a norm,
-// MV_XF_PLAIN_MAX without), and the normalized x only with a norm
+// the prologue results a launch also stores (MvArgs::keep_*): for a float
+// input of any length (the register prologue and the one staged through LDS
+// both store them), the normalized x only with a norm
 struct MvKeep {
     float *xb;
     int8_t *xq;
@@ -883,9 +891,9 @@ struct MvKeep {
 
 static bool keep_ok(const MvKeep &k, const float *xf, const float *nw, int K) {
     if (!k.xb && !k.xq) return true;
-    const bool ok = xf && (k.xq != nullptr) == (k.xd != nullptr) && (!k.xb || nw) &&
-                    K <= (nw ? MV_XF_MAX : MV_XF_PLAIN_MAX) && !((uintptr_t)k.xq & 15) && !((uintptr_t)k.xb & 15);
-    if (!ok) kr_fail(ML_E_SHAPE, "matvec keep: a float input in registers, 16-byte aligned outputs", hipSuccess);
+    const bool ok = xf && (k.xq != nullptr) == (k.xd != nullptr) && (!k.xb || nw) && !((uintptr_t)k.xq & 15) &&
+                    !((uintptr_t)k.xb & 15);
+    if (!ok) kr_fail(ML_E_SHAPE, "matvec keep: a float input, 16-byte aligned outputs", hipSuccess);
     return ok;
 }
 

@@ -851,13 +851,16 @@ def test_matvec_fused_op_sequences(dev, rows, cols, typ, d16):
 
 @pytest.mark.parametrize("dim,nh,nkv,hd,typ,vtyp,bias,hidden", [(288, 6, 6, 48, K.ML_Q8_0, K.ML_Q8_0, 0, 768),
                                                                  (896, 14, 2, 64, K.ML_Q4_0, K.ML_Q8_0, 1, 4864),
-                                                                 (4096, 32, 8, 128, K.ML_Q8_0, K.ML_Q8_0, 0, 14336)])
+                                                                 (4096, 32, 8, 128, K.ML_Q8_0, K.ML_Q8_0, 0, 14336),
+                                                                 (5120, 40, 8, 128, K.ML_Q8_0, K.ML_Q8_0, 0, 13824)])
 def test_matvec_keep_prologues(dev, dim, nh, nkv, hd, typ, vtyp, bias, hidden):
     """the fused-norm and float-input launches that also store their
     prologue's results (the op-table binding's replacement of the reference's
     rmsnorm, quantize_q8 and products, model/transformer.c:270-293): xb, the
     Q8_0 of xb (or of x), and every product, bit for bit against the oracle's
-    rmsnorm, quantize, matvec, add, rope and silu_mul"""
+    rmsnorm, quantize, matvec, add, rope and silu_mul. Inputs longer than the
+    prologue keeps in registers (4864, 5120, 13824, 14336) take the prologue
+    staged through LDS, which stores the same results."""
     H = K.hip
     qd, kvd, pos = nh * hd, nkv * hd, 17
     x = f32(RNG.normal(0, 2, dim))
