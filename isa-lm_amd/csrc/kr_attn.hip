@@ -276,11 +276,12 @@ __global__ void __launch_bounds__(AT_THREADS) k_attn_scores_q8(float *att, const
 // between one batched read and one write (every load issued at once, from an
 // index clamped into the row); longer rows go AT_CHUNK at a time through LDS,
 // the sum continuing from chunk to chunk.
-constexpr int AT_CHUNK = 8192, AT_V = AT_CHUNK / AT_THREADS;
-__global__ void __launch_bounds__(AT_THREADS) k_attn_softmax(float *att, int max_seq, int window, const int *pos_p) {
+constexpr int SMX_THREADS = 1024;   // threads of the decode softmax: its loads, exponentials and stores spread wide
+constexpr int AT_CHUNK = 8192, AT_V = AT_CHUNK / SMX_THREADS;
+__global__ void __launch_bounds__(SMX_THREADS) k_attn_softmax(float *att, int max_seq, int window, const int *pos_p) {
     __shared__ __align__(16) float es[sc_terms_cap(AT_CHUNK)];
-    __shared__ __align__(16) unsigned char scr[sc_lds_bytes(AT_CHUNK, AT_THREADS)];
-    __shared__ float red[AT_THREADS / 64];
+    __shared__ __align__(16) unsigned char scr[sc_lds_bytes(AT_CHUNK, SMX_THREADS)];
+    __shared__ float red[SMX_THREADS / 64];
     __shared__ uint64_t xtab[32];   // expf's table
     int first, n;
     attn_range(pos_p, window, &first, &n);
@@ -295,37 +296,37 @@ __global__ void __launch_bounds__(AT_THREADS) k_attn_softmax(float *att, int max
         // live slot's index is clamped: repeats change no max
 #pragma unroll
         for (int k = 0; k < AT_V; k++)
-            if (k * AT_THREADS < n) v[k] = a[min(k * AT_THREADS + tid, n - 1)];
+            if (k * SMX_THREADS < n) v[k] = a[min(k * SMX_THREADS + tid, n - 1)];
 #pragma unroll
         for (int k = 0; k < AT_V; k++)
-            if (k * AT_THREADS < n) m = fmaxf(m, v[k]);
+            if (k * SMX_THREADS < n) m = fmaxf(m, v[k]);
     } else {
-        for (int t = tid; t < n; t += AT_THREADS) m = fmaxf(m, a[t]);
+        for (int t = tid; t < n; t += SMX_THREADS) m = fmaxf(m, a[t]);
     }
     for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
     if ((tid & 63) == 0) red[tid >> 6] = m;
     __syncthreads();
     float mx = red[0];
-    for (int k = 1; k < AT_THREADS / 64; k++) mx = fmaxf(mx, red[k]);
+    for (int k = 1; k < SMX_THREADS / 64; k++) mx = fmaxf(mx, red[k]);
     if (mx == -INFINITY) {   // every score -inf: the scalar loop's 1/n
-        for (int t = tid; t < n; t += AT_THREADS) a[t] = kr_fdiv(1.0f, (float)n);
+        for (int t = tid; t < n; t += SMX_THREADS) a[t] = kr_fdiv(1.0f, (float)n);
         return;
     }
     if (fits) {
         const int sh = sc_log_len(n);
 #pragma unroll
         for (int k = 0; k < AT_V; k++) {
-            if (k * AT_THREADS >= n) break;   // the rest of the slots are clamped repeats
-            const int t = k * AT_THREADS + tid;
+            if (k * SMX_THREADS >= n) break;   // the rest of the slots are clamped repeats
+            const int t = k * SMX_THREADS + tid;
             v[k] = kr_expf_tab(kr_fsub(v[k], mx), xtab);
             if (t < n) es[sc_at(t, sh)] = v[k];
         }
         __syncthreads();
-        const float inv = kr_fdiv(1.0f, kr_spec_sum<AT_THREADS>(es, n, scr));
+        const float inv = kr_fdiv(1.0f, kr_spec_sum<SMX_THREADS>(es, n, scr));
 #pragma unroll
         for (int k = 0; k < AT_V; k++) {
-            if (k * AT_THREADS >= n) break;
-            const int t = k * AT_THREADS + tid;
+            if (k * SMX_THREADS >= n) break;
+            const int t = k * SMX_THREADS + tid;
             if (t < n) a[t] = kr_fmul(v[k], inv);
         }
         return;
@@ -333,16 +334,16 @@ __global__ void __launch_bounds__(AT_THREADS) k_attn_softmax(float *att, int max
     float sum = 0.0f;
     for (int c0 = 0; c0 < n; c0 += AT_CHUNK) {
         const int cn = min(AT_CHUNK, n - c0), sh = sc_log_len(cn);
-        for (int t = tid; t < cn; t += AT_THREADS) {
+        for (int t = tid; t < cn; t += SMX_THREADS) {
             const float e = kr_expf_tab(kr_fsub(a[c0 + t], mx), xtab);
             es[sc_at(t, sh)] = e;
             a[c0 + t] = e;
         }
         __syncthreads();
-        sum = kr_spec_sum<AT_THREADS>(es, cn, scr, sum);   // ends with a barrier: es is free again
+        sum = kr_spec_sum<SMX_THREADS>(es, cn, scr, sum);   // ends with a barrier: es is free again
     }
     const float inv = kr_fdiv(1.0f, sum);
-    for (int t = tid; t < n; t += AT_THREADS) a[t] = kr_fmul(a[t], inv);
+    for (int t = tid; t < n; t += SMX_THREADS) a[t] = kr_fmul(a[t], inv);
 }
 
 // Batched (prefill) softmax, one row per wave and RW rows per workgroup:
@@ -1029,7 +1030,7 @@ static void attention(float *ao, float *att, const float *q, const KvView &kv, i
             hipLaunchKernelGGL(k_attn_softmax_rows<2>, dim3((nrows + 1) / 2), dim3(128), 2 * per_wave, kr_stream(),
                                att, n_heads, max_seq, window, pos, nrows, tcap, scr);
     } else {
-        hipLaunchKernelGGL(k_attn_softmax, dim3(n_heads, 1, ntok), dim3(AT_THREADS), 0, kr_stream(), att, max_seq,
+        hipLaunchKernelGGL(k_attn_softmax, dim3(n_heads, 1, ntok), dim3(SMX_THREADS), 0, kr_stream(), att, max_seq,
                            window, pos);
     }
     const int gp = group <= 1 ? 1 : group <= 2 ? 2 : group <= 4 ? 4 : group <= 8 ? 8 : 16;
