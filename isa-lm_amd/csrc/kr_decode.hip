@@ -67,7 +67,8 @@ constexpr int MV_DEPTH = 2;    // work items in flight per wave: a wave that iss
 // workgroups per CU
 constexpr int MV_XQ_MAX = 8192;   // quantized activations up to this length are staged from registers
 constexpr int MV_XF_MAX = 4096;    // float activations up to this length are normalized and quantized from registers
-constexpr int MV_XF_PLAIN_MAX = 4096;   // float activations without a norm: quantized from registers up to this length
+constexpr int MV_XF_PLAIN_MAX = 16384;  // float activations without a norm: quantized from registers up to this length,
+constexpr int MV_XF_PASS = 4096;        // in passes of this many
 
 template <typename T> __device__ __forceinline__ T pick3(int i, T a, T b, T c) { return i == 0 ? a : (i == 1 ? b : c); }
 
@@ -355,19 +356,32 @@ __global__ void __launch_bounds__(MV_THREADS, 4) k_matvec(const MvArgs a) {
 #pragma unroll
         for (int d = 0; d < MV_DEPTH - 1; d++) load_item(S[d], I[d]);
     } else if (!a.xq && !a.nw && K <= MV_XF_PLAIN_MAX) {
-        // a float activation without a norm (ao before wo, h before w2): its
+        // a float activation without a norm (ao before wo, h before w2), in
+        // passes of MV_XF_PASS floats held in registers: the first pass's
         // loads go out first, then the first item's weight loads, and the
-        // quantization waits on the activation alone
-        constexpr int XV = MV_XF_PLAIN_MAX / 4 / MV_THREADS;
+        // first quantization waits on the activation alone; later passes
+        // (h of more than MV_XF_PASS) follow
+        constexpr int XV = MV_XF_PASS / 4 / MV_THREADS;
         float4 xv[XV];
+        auto pass_load = [&](int base) {
 #pragma unroll
-        for (int k = 0; k < XV; k++) xv[k] = *(const float4 *)(a.xf + min(4 * (k * MV_THREADS + tid), K - 4));
+            for (int k = 0; k < XV; k++)
+                xv[k] = *(const float4 *)(a.xf + min(base + 4 * (k * MV_THREADS + tid), K - 4));
+        };
+        auto pass_quant = [&](int base) {
+#pragma unroll
+            for (int k = 0; k < XV; k++) {
+                const int i = base + 4 * (k * MV_THREADS + tid);   // K % 32 == 0: 8-lane groups all in or all out
+                if (i < K) kr_quant4(xv[k], i, xs, xds, 1);
+            }
+        };
+        pass_load(0);
 #pragma unroll
         for (int d = 0; d < MV_DEPTH - 1; d++) load_item(S[d], I[d]);
-#pragma unroll
-        for (int k = 0; k < XV; k++) {
-            const int i = 4 * (k * MV_THREADS + tid);   // K % 32 == 0: 8-lane groups all in or all out
-            if (i < K) kr_quant4(xv[k], i, xs, xds, 1);
+        pass_quant(0);
+        for (int base = MV_XF_PASS; base < K; base += MV_XF_PASS) {
+            pass_load(base);
+            pass_quant(base);
         }
     } else if (!a.xq && K <= MV_XF_MAX) {
         // a float activation (normalized first when nw is set), held in
