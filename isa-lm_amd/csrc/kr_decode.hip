@@ -588,7 +588,7 @@ int mv_resident() { return 4 * (krh_device_cus() > 0 ? krh_device_cus() : 256); 
 // the RoPE pairs) that still gives every resident wave a tile; blocks per
 // chunk: as many as MV_NPT slots per lane allow (a multiple of 4, for the
 // 16-byte term reads).
-constexpr int MV_MAX_LOC = 8;   // local rows per tile: a row's chunk then spans >= 32 blocks (1 KB of Q8_0)
+constexpr int MV_MAX_LOC = 8;   // local rows per tile: a row's chunk then spans >= MV_NPT * 8 blocks
 
 int mv_rows(int K, int total_rows, int local_per_row, int cap) {
     (void)K;
