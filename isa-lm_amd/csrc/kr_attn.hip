@@ -119,8 +119,9 @@ __global__ void __launch_bounds__(AT_THREADS) k_attn_scores(float *att, const fl
     attn_scores<KV_F32, TT>(att, q, kv, group, hd, kv_dim, max_seq, window, scale, pos_p);
 }
 
-// Batched (prefill) scores over the F32 cache without a window, a block of
-// AT_TB tokens at a time. Every token of the block attends from position 0,
+// Batched (prefill) scores over the F32 or F16 cache without a window, a
+// block of AT_TB tokens at a time (F16 rows widened exactly as the K tile is
+// staged). Every token of the block attends from position 0,
 // so one K tile of AT_T positions, staged once in LDS, serves the whole block
 // (the per-token kernel stages it again for every token). The queries of QB
 // tokens at a time follow in LDS; thread (position t, head j) runs the QB
@@ -130,8 +131,8 @@ __global__ void __launch_bounds__(AT_THREADS) k_attn_scores(float *att, const fl
 // * scale; a token stores only the positions it attends. HD: the head size
 // when it is 64 or 128, else 0 (any).
 constexpr int AT_TB = 16;
-template <int HD, int QB>
-__global__ void __launch_bounds__(AT_THREADS) k_attn_scores_blk(float *att, const float *q, const float *kc, int group,
+template <int HD, int QB, int KT>
+__global__ void __launch_bounds__(AT_THREADS) k_attn_scores_blk(float *att, const float *q, const KvView kv, int group,
                                                                 int hd_arg, int kv_dim, int max_seq, float scale,
                                                                 const int *pos_p, int ntok) {
     extern __shared__ __align__(16) float at_smem[];
@@ -144,7 +145,8 @@ __global__ void __launch_bounds__(AT_THREADS) k_attn_scores_blk(float *att, cons
     float *kt = at_smem, *qs = at_smem + AT_T * ks;   // K tile [AT_T][ks]; queries [QB][group][hd]
     for (int e = tid; e < nt * h4; e += AT_THREADS) {
         const int r = e / h4, c = e - r * h4;
-        *(float4 *)(kt + r * ks + 4 * c) = *(const float4 *)(kc + (size_t)(t0 + r) * kv_dim + (size_t)g * hd + 4 * c);
+        *(float4 *)(kt + r * ks + 4 * c) =
+            Kv4<KT>::wide(Kv4<KT>::load(kv.k, (size_t)(t0 + r) * kv_dim + (size_t)g * hd + 4 * c));
     }
     const int t = tid % AT_T, p = t0 + t;   // this thread's position (absolute: no window)
     const size_t qstride = (size_t)group * hd;   // floats between two tokens' queries in LDS
@@ -779,7 +781,10 @@ __device__ __forceinline__ void attn_mix_batch(float *ao, const float *att, cons
 // and a DPP row broadcast (row_newbcast) hands position t0 + k's weight to
 // every lane of the row as the multiply's operand. So a row of 16 lanes must
 // hold one head: DW >= 16. Tiles are double-buffered: tile k + 1 is stored
-// while tile k is read, the loads of tile k + 2 already in flight.
+// while tile k is read, the loads of tile k + 2 already in flight. F16 and Q8
+// cache rows are widened exactly as they are staged; over the Q8 cache a
+// lane's weight is a_t * dv_t (the row's scale, k_scalar.c:151) before the
+// broadcast, as in the per-token mix.
 constexpr int MK_W = 4, MK_T = 64, MK_TS = MK_T + 4;
 
 template <int K> __device__ __forceinline__ float row_bcast(float v) {
@@ -796,8 +801,8 @@ __device__ __forceinline__ void mk_quad(float &o, float a, float4 v) {
     o = kr_fadd(o, kr_fmul(row_bcast<4 * Q + 3>(a), v.w));
 }
 
-template <int DW>
-__global__ void __launch_bounds__(64 * MK_W) k_attn_mix_blk(float *ao, const float *att, const float *vc, int group,
+template <int DW, int KT>
+__global__ void __launch_bounds__(64 * MK_W) k_attn_mix_blk(float *ao, const float *att, const KvView kv, int group,
                                                             int hd, int kv_dim, int max_seq, const int *pos_p,
                                                             int ntok) {
     static_assert(DW >= 16, "a 16-lane row must hold one head");
@@ -812,35 +817,52 @@ __global__ void __launch_bounds__(64 * MK_W) k_attn_mix_blk(float *ao, const flo
     const int nmax = pos0 + min(z0 + MK_W, ntok);               // the block's last token's
     const int n_heads = gridDim.x * group, cw = min(DW, hd - c0), ntiles = (nmax + MK_T - 1) / MK_T;
     const float *arow = att + ((size_t)min(z, ntok - 1) * n_heads + (size_t)g * group + min(j, group - 1)) * max_seq;
-    const float *vbase = vc + (size_t)g * hd + c0;
+    const size_t vbase = (size_t)g * hd + c0;   // element offset of the chunk in a V row
     // staging slot of this thread in pass p: row p * RPP + srow, dims scol .. scol + 3
     const int srow = tid / QPR, scol = min(4 * (tid % QPR), cw - 4);
-    float4 sv[NP];
+    using VT = typename Kv4<KT>::T;
+    VT sv[NP];
     auto stage_load = [&](int tile) {
 #pragma unroll
         for (int p = 0; p < NP; p++)
-            sv[p] = *(const float4 *)(vbase + (size_t)min(tile * MK_T + p * RPP + srow, nmax - 1) * kv_dim + scol);
+            sv[p] = Kv4<KT>::load(kv.v, vbase + (size_t)min(tile * MK_T + p * RPP + srow, nmax - 1) * kv_dim + scol);
     };
     auto stage_store = [&](int buf) {
         float *V = vt[buf];
 #pragma unroll
         for (int p = 0; p < NP; p++) {
             const int r = p * RPP + srow, c = 4 * (tid % QPR);
-            V[(c + 0) * MK_TS + r] = sv[p].x;
-            V[(c + 1) * MK_TS + r] = sv[p].y;
-            V[(c + 2) * MK_TS + r] = sv[p].z;
-            V[(c + 3) * MK_TS + r] = sv[p].w;
+            const float4 x = Kv4<KT>::wide(sv[p]);
+            V[(c + 0) * MK_TS + r] = x.x;
+            V[(c + 1) * MK_TS + r] = x.y;
+            V[(c + 2) * MK_TS + r] = x.z;
+            V[(c + 3) * MK_TS + r] = x.w;
         }
     };
+    // the weights of a tile (Q8: and the rows' scales, multiplied in when
+    // the tile becomes the current one, so the loads stay in flight)
+    constexpr int NDQ = KT == KV_Q8 ? MK_T / 16 : 1;
+    float dnext[NDQ];
     auto a_load = [&](int tile, float *a) {
 #pragma unroll
-        for (int b = 0; b < MK_T / 16; b++) a[b] = arow[min(tile * MK_T + 16 * b + (lane & 15), max_seq - 1)];
+        for (int b = 0; b < MK_T / 16; b++) {
+            const int t = min(tile * MK_T + 16 * b + (lane & 15), max_seq - 1);
+            a[b] = arow[t];
+            if constexpr (KT == KV_Q8) dnext[b] = kv.vd[(size_t)t * kv.n_kv + g];
+        }
+    };
+    auto a_scale = [&](float *a) {
+        if constexpr (KT == KV_Q8) {
+#pragma unroll
+            for (int b = 0; b < MK_T / 16; b++) a[b] = kr_fmul(a[b], dnext[b]);
+        }
     };
     float o = 0.0f;
     float acur[MK_T / 16], anext[MK_T / 16];
     stage_load(0);
     stage_store(0);
     a_load(0, acur);
+    a_scale(acur);
     if (ntiles > 1) stage_load(1);
     __syncthreads();
     for (int k = 0; k < ntiles; k++) {
@@ -871,6 +893,7 @@ __global__ void __launch_bounds__(64 * MK_W) k_attn_mix_blk(float *ao, const flo
                 for (int i = 0; i < 16 && t0 + 16 * b + i < n; i++) o = kr_fadd(o, kr_fmul(w[i], V[16 * b + i]));
             }
         }
+        a_scale(anext);
 #pragma unroll
         for (int b = 0; b < MK_T / 16; b++) acur[b] = anext[b];
         kr_lds_order();
@@ -935,11 +958,11 @@ template <int KT, int DW>
 static void launch_mix(const dim3 &grid, int ntok, float *ao, const float *att, const KvView &kv, int group, int hd,
                        int kv_dim, int max_seq, int window, const int *pos) {
     const float *vc = (const float *)kv.v;
-    if constexpr (KT == KV_F32 && DW >= 16) {
+    if constexpr (DW >= 16) {
         if (ntok > 1 && window == 0) {   // prefill without a window: blocks of MK_W tokens share the V tiles
             const dim3 bgrid(grid.x, grid.y, (ntok + MK_W - 1) / MK_W);
-            hipLaunchKernelGGL(k_attn_mix_blk<DW>, bgrid, dim3(64 * MK_W), 0, kr_stream(), ao, att, vc, group, hd,
-                               kv_dim, max_seq, pos, ntok);
+            hipLaunchKernelGGL((k_attn_mix_blk<DW, KT>), bgrid, dim3(64 * MK_W), 0, kr_stream(), ao, att, kv, group,
+                               hd, kv_dim, max_seq, pos, ntok);
             return;
         }
     }
@@ -982,7 +1005,7 @@ static void attention(float *ao, float *att, const float *q, const KvView &kv, i
     if constexpr (KT == KV_Q8)
         hipLaunchKernelGGL(k_attn_scores_q8, sgrid, dim3(AT_THREADS), lds, kr_stream(), att, q, kv, group, head_dim,
                            kv_dim, max_seq, window, scale, pos);
-    else if constexpr (KT == KV_F32) {
+    else {
         // the queries of QB tokens beside the K tile, within 64 KB of LDS
         const size_t ktile = sizeof(float) * (size_t)AT_T * (head_dim + 4);
         const size_t qtok = sizeof(float) * (size_t)group * head_dim;
@@ -991,18 +1014,21 @@ static void attention(float *ao, float *att, const float *q, const KvView &kv, i
             const dim3 bgrid(n_kv_heads, (max_pos + AT_T) / AT_T, (ntok + AT_TB - 1) / AT_TB);
             const size_t blds = ktile + qb * qtok;
             auto go = [&](auto kern) {
-                hipLaunchKernelGGL(kern, bgrid, dim3(AT_THREADS), blds, kr_stream(), att, q, (const float *)kv.k,
-                                   group, head_dim, kv_dim, max_seq, scale, pos, ntok);
+                hipLaunchKernelGGL(kern, bgrid, dim3(AT_THREADS), blds, kr_stream(), att, q, kv, group, head_dim,
+                                   kv_dim, max_seq, scale, pos, ntok);
             };
             if (qb == 8) {
-                if (head_dim == 128) go(k_attn_scores_blk<128, 8>);
-                else if (head_dim == 64) go(k_attn_scores_blk<64, 8>);
-                else go(k_attn_scores_blk<0, 8>);
+                if (head_dim == 128) go(k_attn_scores_blk<128, 8, KT>);
+                else if (head_dim == 64) go(k_attn_scores_blk<64, 8, KT>);
+                else go(k_attn_scores_blk<0, 8, KT>);
             } else {
-                if (head_dim == 128) go(k_attn_scores_blk<128, 4>);
-                else if (head_dim == 64) go(k_attn_scores_blk<64, 4>);
-                else go(k_attn_scores_blk<0, 4>);
+                if (head_dim == 128) go(k_attn_scores_blk<128, 4, KT>);
+                else if (head_dim == 64) go(k_attn_scores_blk<64, 4, KT>);
+                else go(k_attn_scores_blk<0, 4, KT>);
             }
+        } else if (KT != KV_F32) {
+            hipLaunchKernelGGL((k_attn_scores_kv<KT>), sgrid, dim3(AT_THREADS), lds, kr_stream(), att, q, kv, group,
+                               head_dim, kv_dim, max_seq, window, scale, pos);
         } else if (ntok == 1) {   // decode: tiles of AT_TD positions
             const dim3 dgrid(n_kv_heads, (max_pos + AT_TD) / AT_TD, 1);
             hipLaunchKernelGGL(k_attn_scores<AT_TD>, dgrid, dim3(AT_THREADS), lds, kr_stream(), att, q,
@@ -1012,9 +1038,6 @@ static void attention(float *ao, float *att, const float *q, const KvView &kv, i
                                (const float *)kv.k, group, head_dim, kv_dim, max_seq, window, scale, pos);
         }
     }
-    else
-        hipLaunchKernelGGL((k_attn_scores_kv<KT>), sgrid, dim3(AT_THREADS), lds, kr_stream(), att, q, kv, group,
-                           head_dim, kv_dim, max_seq, window, scale, pos);
     if (cap > 0.0f) krh_softcap_att(att, n_heads, max_seq, window, pos, ntok, cap);   // ops/ops.c:141
     if (ntok > 1 && max_pos + 1 <= SM_WN) {   // prefill rows short enough for one wave each
         const int tcap = sc_terms_cap(max_pos + 1), scr = (sc_lds_bytes(max_pos + 1, 64) + 15) / 16 * 16;
