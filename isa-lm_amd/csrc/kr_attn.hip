@@ -196,6 +196,20 @@ __global__ void __launch_bounds__(AT_THREADS) k_attn_scores_kv(float *att, const
     attn_scores<KT, AT_T>(att, q, kv, group, hd, kv_dim, max_seq, window, scale, pos_p);
 }
 
+// One query head of hd floats as the Q8 rule does it for the score
+// (ops/ops.c:81-96): the max |x| from 0, one scale for the head, each value
+// trunc(x * 127 / max + copysign(0.5, x)); a head of zeros (max below the
+// rule's tiny) has scale 0 and zero quants. One wave; lane 0 writes the scale.
+__device__ __forceinline__ void q8_head(const float *x, int hd, int8_t *dst, float *dd, int lane) {
+    float m = 0.0f;
+    for (int i = lane; i < hd; i += 64) m = fmaxf(m, fabsf(x[i]));
+    for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+    const bool zero = m < KR_QUANT_TINY;
+    const float id = zero ? 0.0f : kr_fdiv(127.0f, m);
+    for (int i = lane; i < hd; i += 64) dst[i] = zero ? (int8_t)0 : (int8_t)kr_q8_elem(x[i], id);
+    if (lane == 0) *dd = zero ? 0.0f : kr_fdiv(m, 127.0f);
+}
+
 // Scores over the Q8 cache (ops/ops.c:171-173, k_scalar.c:137-146): each query
 // head of the group quantized with one scale (ops/ops.c:81-96; every
 // workgroup quantizes its group's heads itself, the same bits), then per
@@ -217,16 +231,7 @@ __global__ void __launch_bounds__(AT_THREADS) k_attn_scores_q8(float *att, const
     float *qd = at_smem;                            // [16] query scales
     int8_t *qs = (int8_t *)(at_smem + 16);          // [group][hd]
     int8_t *kt = qs + (group * hd + 15) / 16 * 16;  // [AT_T][ks]
-    for (int j = wave; j < group; j += AT_THREADS / 64) {
-        const float *qh = q + (size_t)(g * group + j) * hd;
-        float m = 0.0f;
-        for (int i = lane; i < hd; i += 64) m = fmaxf(m, fabsf(qh[i]));
-        for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
-        const bool zero = m < KR_QUANT_TINY;
-        const float id = zero ? 0.0f : kr_fdiv(127.0f, m);
-        for (int i = lane; i < hd; i += 64) qs[j * hd + i] = zero ? (int8_t)0 : (int8_t)kr_q8_elem(qh[i], id);
-        if (lane == 0) qd[j] = zero ? 0.0f : kr_fdiv(m, 127.0f);
-    }
+    for (int j = wave; j < group; j += AT_THREADS / 64) q8_head(q + (size_t)(g * group + j) * hd, hd, qs + j * hd, qd + j, lane);
     // store_kv folded into decode (model/transformer.c:198-203): the tile
     // holding the current position quantizes its KV head's K row (wave 0,
     // straight into the tile as well) and V row (wave 1) into the cache
@@ -269,6 +274,70 @@ __global__ void __launch_bounds__(AT_THREADS) k_attn_scores_q8(float *att, const
         for (int i = 0; i < hd; i += 4) sum = kr_dot4(*(const int *)(qh + i), *(const int *)(kr + i), sum);
         const float c = kr_fmul(qd[j], scale);
         att[(size_t)(g * group + j) * max_seq + t0 + t] = kr_fmul(kr_fmul((float)sum, c), dk);
+    }
+}
+
+// Batched (prefill) scores over the Q8 cache without a window, a block of
+// AT_TB tokens at a time: the int8 K tile of AT_T positions and its row
+// scales are staged once for the block; then, QB tokens at a time, the
+// workgroup quantizes those tokens' query heads of its group into LDS
+// (q8_head: the per-token kernel's bits) and thread (position t, head j)
+// runs the QB exact int32 dots against its K row in one pass, each finished
+// as in the per-token kernel: ((float)sum * (dq * scale)) * dk_t.
+template <int QB>
+__global__ void __launch_bounds__(AT_THREADS) k_attn_scores_blk_q8(float *att, const float *q, const KvView kv,
+                                                                   int group, int hd, int kv_dim, int max_seq,
+                                                                   float scale, const int *pos_p, int ntok) {
+    extern __shared__ __align__(16) float at_smem[];
+    const int g = blockIdx.x, t0 = blockIdx.y * AT_T, z0 = blockIdx.z * AT_TB, tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int pos0 = *pos_p, zn = min(AT_TB, ntok - z0);
+    const int nlast = pos0 + z0 + zn;   // positions the block's last token attends
+    if (t0 >= nlast) return;
+    const int nt = min(AT_T, nlast - t0), ks = hd + 4, n_heads = gridDim.x * group, h4 = hd / 4;
+    float *dks = at_smem;                                   // [AT_T] K row scales
+    float *qd = dks + AT_T;                                 // [QB][group] query head scales
+    int8_t *kt = (int8_t *)(qd + (QB * group + 3) / 4 * 4);   // [AT_T][ks]
+    int8_t *qs = kt + (AT_T * ks + 15) / 16 * 16;          // [QB][group][hd]
+    for (int e = tid; e < nt * h4; e += AT_THREADS) {
+        const int r = e / h4, c = e - r * h4;
+        *(int *)(kt + r * ks + 4 * c) =
+            *(const int *)((const int8_t *)kv.k + (size_t)(t0 + r) * kv_dim + (size_t)g * hd + 4 * c);
+    }
+    for (int r = tid; r < nt; r += AT_THREADS) dks[r] = kv.kd[(size_t)(t0 + r) * kv.n_kv + g];
+    const int t = tid % AT_T, p = t0 + t;   // this thread's position (absolute: no window)
+    for (int zb = 0; zb < zn; zb += QB) {
+        const int qn = min(QB, zn - zb);
+        __syncthreads();   // the last queries are read
+        for (int h = wave; h < qn * group; h += AT_THREADS / 64) {
+            const int zz = h / group, jj = h - zz * group;
+            q8_head(q + ((size_t)(z0 + zb + zz) * n_heads + (size_t)g * group + jj) * hd, hd, qs + (size_t)h * hd,
+                    qd + h, lane);
+        }
+        __syncthreads();
+        if (t >= nt) continue;
+        const int8_t *kr = kt + t * ks;
+        const float dk = dks[t];
+        for (int j = tid / AT_T; j < group; j += AT_THREADS / AT_T) {
+            // tokens zb + u, u < QB (slots past qn hold an earlier block's
+            // queries and are not stored)
+            int acc[QB];
+#pragma unroll
+            for (int u = 0; u < QB; u++) acc[u] = 0;
+            for (int i = 0; i < hd; i += 4) {
+                const int k4 = *(const int *)(kr + i);
+#pragma unroll
+                for (int u = 0; u < QB; u++) acc[u] = kr_dot4(*(const int *)(qs + ((size_t)u * group + j) * hd + i), k4, acc[u]);
+            }
+#pragma unroll
+            for (int u = 0; u < QB; u++) {
+                const int z = z0 + zb + u;
+                if (u < qn && p <= pos0 + z) {
+                    const float c = kr_fmul(qd[u * group + j], scale);
+                    att[((size_t)z * n_heads + (size_t)g * group + j) * max_seq + p] = kr_fmul(kr_fmul((float)acc[u], c), dk);
+                }
+            }
+        }
     }
 }
 
@@ -810,6 +879,7 @@ __global__ void __launch_bounds__(64 * MK_W) k_attn_mix_blk(float *ao, const flo
     constexpr int RPP = 64 * MK_W / QPR;        // rows the workgroup stages per pass
     constexpr int NP = MK_T / RPP;              // passes per tile
     __shared__ __align__(16) float vt[2][DW * MK_TS];
+    __shared__ float dvs[2][KT == KV_Q8 ? MK_T : 1];   // Q8: the tile's V row scales
     const int g = blockIdx.x, c0 = blockIdx.y * DW, z0 = blockIdx.z * MK_W, tid = threadIdx.x;
     const int wave = tid >> 6, lane = tid & 63, j = lane / DW, d = lane % DW;
     const int z = z0 + wave, pos0 = *pos_p;
@@ -822,10 +892,12 @@ __global__ void __launch_bounds__(64 * MK_W) k_attn_mix_blk(float *ao, const flo
     const int srow = tid / QPR, scol = min(4 * (tid % QPR), cw - 4);
     using VT = typename Kv4<KT>::T;
     VT sv[NP];
+    float sd = 0.0f;
     auto stage_load = [&](int tile) {
 #pragma unroll
         for (int p = 0; p < NP; p++)
             sv[p] = Kv4<KT>::load(kv.v, vbase + (size_t)min(tile * MK_T + p * RPP + srow, nmax - 1) * kv_dim + scol);
+        if (KT == KV_Q8 && tid < MK_T) sd = kv.vd[(size_t)min(tile * MK_T + tid, nmax - 1) * kv.n_kv + g];
     };
     auto stage_store = [&](int buf) {
         float *V = vt[buf];
@@ -838,53 +910,49 @@ __global__ void __launch_bounds__(64 * MK_W) k_attn_mix_blk(float *ao, const flo
             V[(c + 2) * MK_TS + r] = x.z;
             V[(c + 3) * MK_TS + r] = x.w;
         }
+        if (KT == KV_Q8 && tid < MK_T) dvs[buf][tid] = sd;
     };
-    // the weights of a tile (Q8: and the rows' scales, multiplied in when
-    // the tile becomes the current one, so the loads stay in flight)
-    constexpr int NDQ = KT == KV_Q8 ? MK_T / 16 : 1;
-    float dnext[NDQ];
+    // the weights of a tile, loaded two tiles ahead like V: one tile's adds
+    // are shorter than a load's round trip
     auto a_load = [&](int tile, float *a) {
 #pragma unroll
-        for (int b = 0; b < MK_T / 16; b++) {
-            const int t = min(tile * MK_T + 16 * b + (lane & 15), max_seq - 1);
-            a[b] = arow[t];
-            if constexpr (KT == KV_Q8) dnext[b] = kv.vd[(size_t)t * kv.n_kv + g];
-        }
-    };
-    auto a_scale = [&](float *a) {
-        if constexpr (KT == KV_Q8) {
-#pragma unroll
-            for (int b = 0; b < MK_T / 16; b++) a[b] = kr_fmul(a[b], dnext[b]);
-        }
+        for (int b = 0; b < MK_T / 16; b++) a[b] = arow[min(tile * MK_T + 16 * b + (lane & 15), max_seq - 1)];
     };
     float o = 0.0f;
-    float acur[MK_T / 16], anext[MK_T / 16];
+    float acur[MK_T / 16], anext[MK_T / 16], anext2[MK_T / 16];
     stage_load(0);
     stage_store(0);
     a_load(0, acur);
-    a_scale(acur);
+    a_load(min(1, ntiles - 1), anext);
     if (ntiles > 1) stage_load(1);
     __syncthreads();
     for (int k = 0; k < ntiles; k++) {
         const int buf = k & 1, t0 = k * MK_T;
         if (k + 1 < ntiles) stage_store(buf ^ 1);   // its last reader finished before the last barrier
-        a_load(min(k + 1, ntiles - 1), anext);
-        if (k + 2 < ntiles) stage_load(k + 2);
+        a_load(min(k + 2, ntiles - 1), anext2);
+        // unconditional (a clamped tile past the end is loaded and never
+        // stored): with a fixed count of loads behind them, the waits for
+        // the weights at the end of the step leave this load in flight
+        stage_load(min(k + 2, ntiles - 1));
         const float *V = vt[buf] + d * MK_TS;
+        float aw[MK_T / 16];   // the weights (Q8: a_t * dv_t)
+#pragma unroll
+        for (int b = 0; b < MK_T / 16; b++)
+            aw[b] = KT == KV_Q8 ? kr_fmul(acur[b], dvs[buf][KT == KV_Q8 ? 16 * b + (lane & 15) : 0]) : acur[b];
         if (t0 + MK_T <= n) {   // a full tile for this token
 #pragma unroll
             for (int b = 0; b < MK_T / 16; b++) {
                 const float4 v0 = *(const float4 *)(V + 16 * b), v1 = *(const float4 *)(V + 16 * b + 4);
                 const float4 v2 = *(const float4 *)(V + 16 * b + 8), v3 = *(const float4 *)(V + 16 * b + 12);
-                mk_quad<0>(o, acur[b], v0);
-                mk_quad<1>(o, acur[b], v1);
-                mk_quad<2>(o, acur[b], v2);
-                mk_quad<3>(o, acur[b], v3);
+                mk_quad<0>(o, aw[b], v0);
+                mk_quad<1>(o, aw[b], v1);
+                mk_quad<2>(o, aw[b], v2);
+                mk_quad<3>(o, aw[b], v3);
             }
         } else if (t0 < n) {    // the token's last tile: its live positions only
 #pragma unroll
             for (int b = 0; b < MK_T / 16; b++) {
-                const float ab = acur[b];
+                const float ab = aw[b];
                 float w[16];
                 w[0] = row_bcast<0>(ab); w[1] = row_bcast<1>(ab); w[2] = row_bcast<2>(ab); w[3] = row_bcast<3>(ab);
                 w[4] = row_bcast<4>(ab); w[5] = row_bcast<5>(ab); w[6] = row_bcast<6>(ab); w[7] = row_bcast<7>(ab);
@@ -893,9 +961,11 @@ __global__ void __launch_bounds__(64 * MK_W) k_attn_mix_blk(float *ao, const flo
                 for (int i = 0; i < 16 && t0 + 16 * b + i < n; i++) o = kr_fadd(o, kr_fmul(w[i], V[16 * b + i]));
             }
         }
-        a_scale(anext);
 #pragma unroll
-        for (int b = 0; b < MK_T / 16; b++) acur[b] = anext[b];
+        for (int b = 0; b < MK_T / 16; b++) {
+            acur[b] = anext[b];
+            anext[b] = anext2[b];
+        }
         kr_lds_order();
         __syncthreads();
     }
@@ -1002,9 +1072,27 @@ static void attention(float *ao, float *att, const float *q, const KvView &kv, i
         return;
     }
     const dim3 sgrid(n_kv_heads, (max_pos + AT_T) / AT_T, ntok);
-    if constexpr (KT == KV_Q8)
-        hipLaunchKernelGGL(k_attn_scores_q8, sgrid, dim3(AT_THREADS), lds, kr_stream(), att, q, kv, group, head_dim,
-                           kv_dim, max_seq, window, scale, pos);
+    if constexpr (KT == KV_Q8) {
+        // prefill: the K tile and the quantized queries of QB tokens in LDS
+        auto qlds = [&](int qb) {
+            return sizeof(float) * (AT_T + (size_t)(qb * group + 3) / 4 * 4) + (size_t)(AT_T * (head_dim + 4) + 15) / 16 * 16 +
+                   (size_t)qb * group * head_dim;
+        };
+        const int qb = qlds(16) <= 64 * 1024 ? 16 : qlds(8) <= 64 * 1024 ? 8 : qlds(4) <= 64 * 1024 ? 4 : 0;
+        if (ntok > 1 && window == 0 && qb) {
+            const dim3 bgrid(n_kv_heads, (max_pos + AT_T) / AT_T, (ntok + AT_TB - 1) / AT_TB);
+            auto go = [&](auto kern) {
+                hipLaunchKernelGGL(kern, bgrid, dim3(AT_THREADS), qlds(qb), kr_stream(), att, q, kv, group, head_dim,
+                                   kv_dim, max_seq, scale, pos, ntok);
+            };
+            if (qb == 16) go(k_attn_scores_blk_q8<16>);
+            else if (qb == 8) go(k_attn_scores_blk_q8<8>);
+            else go(k_attn_scores_blk_q8<4>);
+        } else {
+            hipLaunchKernelGGL(k_attn_scores_q8, sgrid, dim3(AT_THREADS), lds, kr_stream(), att, q, kv, group,
+                               head_dim, kv_dim, max_seq, window, scale, pos);
+        }
+    }
     else {
         // the queries of QB tokens beside the K tile, within 64 KB of LDS
         const size_t ktile = sizeof(float) * (size_t)AT_T * (head_dim + 4);
