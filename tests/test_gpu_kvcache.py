@@ -148,6 +148,20 @@ def test_attention_kv(dev, kv_type, nh, nkv, hd, pos, window):
 @pytest.mark.parametrize("nh,nkv,hd,pos0,T,window", [(6, 6, 48, 0, 40, 0), (32, 8, 128, 100, 70, 0),
                                                      (14, 2, 64, 3, 200, 0), (8, 2, 64, 10, 50, 7)])
 def test_attention_kv_batch(dev, kv_type, nh, nkv, hd, pos0, T, window):
+    """batched attention over F16 and Q8 caches against the oracle's per-token
+    attention"""
+    kv_batch_case(dev, kv_type, nh, nkv, hd, pos0, T, window)
+
+
+@pytest.mark.parametrize("nh,nkv,hd,pos0,T", [(32, 2, 256, 5, 40), (16, 2, 512, 0, 20)])
+def test_attention_kv_batch_q8_wide_groups(dev, nh, nkv, hd, pos0, T):
+    """the batched Q8 score kernel when a group's quantized queries leave room
+    for 8 (group 16, head 256) or 4 (group 8, head 512) tokens a pass; the F16
+    score tile of these heads does not fit in 64 KB of LDS"""
+    kv_batch_case(dev, K.ML_Q8_0, nh, nkv, hd, pos0, T, 0)
+
+
+def kv_batch_case(dev, kv_type, nh, nkv, hd, pos0, T, window):
     max_seq = 512
     kvd, qd = nkv * hd, nh * hd
     Q = f32(RNG.normal(0, 1, (T, qd)))
