@@ -189,11 +189,11 @@ __global__ void __launch_bounds__(AT_THREADS) k_attn_scores_blk(float *att, cons
     }
 }
 
-template <int KT>
+template <int KT, int TT>
 __global__ void __launch_bounds__(AT_THREADS) k_attn_scores_kv(float *att, const float *q, const KvView kv, int group,
                                                                int hd, int kv_dim, int max_seq, int window, float scale,
                                                                const int *pos_p) {
-    attn_scores<KT, AT_T>(att, q, kv, group, hd, kv_dim, max_seq, window, scale, pos_p);
+    attn_scores<KT, TT>(att, q, kv, group, hd, kv_dim, max_seq, window, scale, pos_p);
 }
 
 // One query head of hd floats as the Q8 rule does it for the score
@@ -1065,13 +1065,20 @@ static void attention(float *ao, float *att, const float *q, const KvView &kv, i
         return;
     }
     const int group = n_heads / n_kv_heads, kv_dim = n_kv_heads * head_dim;
-    const size_t lds = KT == KV_Q8 ? 64 + (size_t)(group * head_dim + 15) / 16 * 16 + (size_t)AT_T * (head_dim + 4)
-                                   : sizeof(float) * ((size_t)group * head_dim + (size_t)AT_T * (head_dim + 4));
-    if (lds > 64 * 1024) {
+    // the per-token score kernels' LDS: the group's queries and a K tile of
+    // tt positions. F32/F16 tiles of wide heads (Gemma's 256) take AT_TD
+    // positions; the int8 Q8 tile fits at AT_T up to heads of 512 and more.
+    auto tile_lds = [&](int tt) {
+        return KT == KV_Q8 ? 64 + (size_t)(group * head_dim + 15) / 16 * 16 + (size_t)tt * (head_dim + 4)
+                           : sizeof(float) * ((size_t)group * head_dim + (size_t)tt * (head_dim + 4));
+    };
+    const int tt = tile_lds(AT_T) <= 64 * 1024 ? AT_T : KT != KV_Q8 && tile_lds(AT_TD) <= 64 * 1024 ? AT_TD : 0;
+    if (!tt) {
         kr_fail(ML_E_SHAPE, "attention: head_dim too large for the score tile", hipSuccess);
         return;
     }
-    const dim3 sgrid(n_kv_heads, (max_pos + AT_T) / AT_T, ntok);
+    const size_t lds = tile_lds(tt);
+    const dim3 sgrid(n_kv_heads, (max_pos + tt) / tt, ntok);
     if constexpr (KT == KV_Q8) {
         // prefill: the K tile and the quantized queries of QB tokens in LDS
         auto qlds = [&](int qb) {
@@ -1115,11 +1122,15 @@ static void attention(float *ao, float *att, const float *q, const KvView &kv, i
                 else go(k_attn_scores_blk<0, 4, KT>);
             }
         } else if (KT != KV_F32) {
-            hipLaunchKernelGGL((k_attn_scores_kv<KT>), sgrid, dim3(AT_THREADS), lds, kr_stream(), att, q, kv, group,
-                               head_dim, kv_dim, max_seq, window, scale, pos);
-        } else if (ntok == 1) {   // decode: tiles of AT_TD positions
-            const dim3 dgrid(n_kv_heads, (max_pos + AT_TD) / AT_TD, 1);
-            hipLaunchKernelGGL(k_attn_scores<AT_TD>, dgrid, dim3(AT_THREADS), lds, kr_stream(), att, q,
+            if (tt == AT_T)
+                hipLaunchKernelGGL((k_attn_scores_kv<KT, AT_T>), sgrid, dim3(AT_THREADS), lds, kr_stream(), att, q, kv,
+                                   group, head_dim, kv_dim, max_seq, window, scale, pos);
+            else
+                hipLaunchKernelGGL((k_attn_scores_kv<KT, AT_TD>), sgrid, dim3(AT_THREADS), lds, kr_stream(), att, q,
+                                   kv, group, head_dim, kv_dim, max_seq, window, scale, pos);
+        } else if (ntok == 1 || tt == AT_TD) {   // decode (or a wide head): tiles of AT_TD positions
+            const dim3 dgrid(n_kv_heads, (max_pos + AT_TD) / AT_TD, ntok);
+            hipLaunchKernelGGL(k_attn_scores<AT_TD>, dgrid, dim3(AT_THREADS), tile_lds(AT_TD), kr_stream(), att, q,
                                (const float *)kv.k, group, head_dim, kv_dim, max_seq, window, scale, pos);
         } else {
             hipLaunchKernelGGL(k_attn_scores<AT_T>, sgrid, dim3(AT_THREADS), lds, kr_stream(), att, q,

@@ -44,6 +44,12 @@ VARIANTS["gelu_post_qk_gemma3"] = dict(K.CONFIGS["qwen05b_mixed"], dim=128, n_la
                                        hidden_dim=256, vocab=512, max_seq=96, std=0.1, act=K.ML_ACT_GELU_TANH,
                                        post_norms=1, qk_norm=1, final_softcap=8.0, rope_local_theta=1e4,
                                        layer_local=0b01, layer_sliding=0b01, sliding_window=5)
+# Gemma 2's 256-wide heads (two query heads sharing one KV head): the score
+# tiles of such heads take the kernels' narrower position tiles
+VARIANTS["gemma2_wide_heads"] = dict(K.CONFIGS["qwen05b_mixed"], dim=512, n_layers=2, n_heads=2, n_kv_heads=1,
+                                     hidden_dim=1024, vocab=512, max_seq=96, std=0.1, act=K.ML_ACT_GELU_TANH,
+                                     embed_scale=22.6, attn_softcap=50.0, final_softcap=30.0, sliding_window=6,
+                                     layer_sliding=0b01, qkv_bias=0)
 KV = {"f32": K.ML_F32, "f16": K.ML_F16, "q8": K.ML_Q8_0}
 
 
@@ -185,7 +191,7 @@ def test_family_model_matches_reference(name, kv, workdir):
 
 @pytest.mark.parametrize("kv", sorted(KV))
 @pytest.mark.parametrize("name", ["qk_norm_bias_gqa", "qk_post_norms_f16", "window_local_rope_layers",
-                                  "gelu_softcap_gemma2", "gelu_post_qk_gemma3"])
+                                  "gelu_softcap_gemma2", "gelu_post_qk_gemma3", "gemma2_wide_heads"])
 def test_family_batched_prefill(name, kv, workdir):
     """the families' batched prefill (token_stage's per-token stages as row
     launches, model/transformer.c:324-365) over a prompt that passes the

@@ -303,7 +303,8 @@ def test_matvec_float_input(dev, typ, d16, rows, cols):
                                                     (32, 8, 128, 2175, 0), (32, 8, 128, 2174, 0),
                                                   (32, 8, 128, 2303, 0), (32, 8, 64, 4000, 0), (8, 2, 64, 100, 7),
                                                   (16, 1, 64, 63, 0), (4, 2, 32, 64, 0), (12, 4, 96, 130, 0),
-                                                  (4, 2, 32, 9000, 0), (8, 2, 64, 12000, 9000)])
+                                                  (4, 2, 32, 9000, 0), (8, 2, 64, 12000, 9000), (8, 4, 256, 300, 0),
+                                                  (4, 1, 256, 200, 64)])
 def test_attention(dev, nh, nkv, hd, pos, window):
     max_seq = max(256, pos + 1)
     kvd, qd = nkv * hd, nh * hd
@@ -560,7 +561,8 @@ def test_matmul_qkv_matches_decode(dev, dim, nh, nkv, hd, typ, vtyp, bias):
 
 
 @pytest.mark.parametrize("nh,nkv,hd,pos0,T,window", [(6, 6, 48, 0, 40, 0), (32, 8, 128, 100, 70, 0),
-                                                     (14, 2, 64, 3, 200, 0), (8, 2, 64, 10, 50, 7)])
+                                                     (14, 2, 64, 3, 200, 0), (8, 2, 64, 10, 50, 7),
+                                                     (8, 4, 256, 5, 40, 0), (4, 1, 256, 100, 30, 64)])
 def test_attention_batch_matches_decode(dev, nh, nkv, hd, pos0, T, window):
     max_seq = 512
     kvd, qd = nkv * hd, nh * hd

@@ -123,7 +123,8 @@ def views(dev, kv_type, k, v, kd, vd, window):
 @pytest.mark.parametrize("kv_type", [K.ML_F16, K.ML_Q8_0])
 @pytest.mark.parametrize("nh,nkv,hd,pos,window", [(6, 6, 48, 0, 0), (14, 2, 64, 511, 0), (32, 8, 128, 2175, 0),
                                                   (32, 8, 128, 2303, 0), (8, 2, 64, 100, 7), (16, 1, 64, 63, 0),
-                                                  (12, 4, 96, 130, 0), (4, 2, 32, 9000, 0)])
+                                                  (12, 4, 96, 130, 0), (4, 2, 32, 9000, 0), (8, 4, 256, 300, 0),
+                                                  (4, 1, 256, 200, 64)])
 def test_attention_kv(dev, kv_type, nh, nkv, hd, pos, window):
     max_seq = max(256, pos + 1)
     kvd, qd = nkv * hd, nh * hd
@@ -146,7 +147,8 @@ def test_attention_kv(dev, kv_type, nh, nkv, hd, pos, window):
 
 @pytest.mark.parametrize("kv_type", [K.ML_F16, K.ML_Q8_0])
 @pytest.mark.parametrize("nh,nkv,hd,pos0,T,window", [(6, 6, 48, 0, 40, 0), (32, 8, 128, 100, 70, 0),
-                                                     (14, 2, 64, 3, 200, 0), (8, 2, 64, 10, 50, 7)])
+                                                     (14, 2, 64, 3, 200, 0), (8, 2, 64, 10, 50, 7),
+                                                     (8, 4, 256, 5, 40, 0), (4, 1, 256, 100, 30, 64)])
 def test_attention_kv_batch(dev, kv_type, nh, nkv, hd, pos0, T, window):
     """batched attention over F16 and Q8 caches against the oracle's per-token
     attention"""
