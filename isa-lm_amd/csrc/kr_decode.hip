@@ -301,8 +301,15 @@ __host__ __device__ inline MvLds mv_lds(int K, int maxloc, int nbc, bool norm) {
 // dots the workgroup stages the activation into LDS (while the first loads
 // are in flight): copied, quantized, or normalized first (rmsnorm's ordered
 // sum, k_scalar.c:59-64) and quantized.
+// workgroups of a launch resident on one CU: four (128 VGPRs, four waves a
+// SIMD), three for q|k|v, whose RoPE epilogue then keeps its state in
+// registers (at 128 the Q8 form spilled 16 bytes, reloaded in every step:
+// 8B decode 308.2 -> 309.7 tok/s without the spill). The q|k|v grid of the
+// 8B shape is 768 workgroups in any case (3,072 two-row tiles).
+constexpr int mv_wgs_per_cu(int epi) { return epi == EPI_QKV ? 3 : 4; }
+
 template <int EPI, int QT, int D16>
-__global__ void __launch_bounds__(MV_THREADS, 4) k_matvec(const MvArgs a) {
+__global__ void __launch_bounds__(MV_THREADS, mv_wgs_per_cu(EPI)) k_matvec(const MvArgs a) {
     extern __shared__ __align__(16) unsigned char smem[];
     const int K = a.K, nb = K / KR_QK, tid = threadIdx.x;
     const int ntiles = a.nmat == 1 ? a.tile0[1] : a.nmat == 2 ? a.tile0[2] : a.tile0[3];
@@ -577,12 +584,13 @@ __global__ void __launch_bounds__(MV_THREADS, 4) k_matvec(const MvArgs a) {
 }
 
 // workgroups resident at once: four per compute unit of this device (1024
-// on an MI355X's 256 CUs; the kernel fits 128 VGPRs, four waves a SIMD).
+// on an MI355X's 256 CUs; the kernel fits 128 VGPRs, four waves a SIMD),
+// three for q|k|v.
 // The 8B decode streamed at 274.9 tok/s with two a CU (4 blocks per lane
 // and item, 166 VGPRs), 282.5 with three, 284.1 with four (2 blocks per lane
 // and item, the activations of up to 4096 held in registers): more waves to
 // cover each other's ordered sums and loads
-int mv_resident() { return 4 * (krh_device_cus() > 0 ? krh_device_cus() : 256); }
+int mv_resident(int epi = EPI_STORE) { return mv_wgs_per_cu(epi) * (krh_device_cus() > 0 ? krh_device_cus() : 256); }
 
 // Rows per tile (one wave's): the largest power of two (at most cap, even for
 // the RoPE pairs) that still gives every resident wave a tile; blocks per
@@ -590,12 +598,12 @@ int mv_resident() { return 4 * (krh_device_cus() > 0 ? krh_device_cus() : 256); 
 // 16-byte term reads).
 constexpr int MV_MAX_LOC = 8;   // local rows per tile: a row's chunk then spans >= MV_NPT * 8 blocks
 
-int mv_rows(int K, int total_rows, int local_per_row, int cap) {
+int mv_rows(int K, int total_rows, int local_per_row, int cap, int epi = EPI_STORE) {
     (void)K;
     int R = cap / local_per_row;
     if (R * local_per_row > 64) R = 64 / local_per_row;
     if (R * local_per_row > MV_MAX_LOC) R = MV_MAX_LOC / local_per_row;
-    while (R > 2 && (total_rows + R - 1) / R < mv_resident() * MV_WAVES) R /= 2;
+    while (R > 2 && (total_rows + R - 1) / R < mv_resident(epi) * MV_WAVES) R /= 2;
     if (R > 1) R &= ~1;
     return R < 1 ? 1 : R;
 }
@@ -614,7 +622,7 @@ void launch_mv(MvArgs &a, const KMat &W) {
     const size_t lds = mv_lds(a.K, nloc, a.nbc, a.nw != nullptr).total;
     const int ntiles = a.tile0[a.nmat];
     const int wgs = (ntiles + MV_WAVES - 1) / MV_WAVES;
-    const int grid = wgs > mv_resident() ? mv_resident() : wgs;
+    const int grid = wgs > mv_resident(EPI) ? mv_resident(EPI) : wgs;
     if (a.K % KR_QK || lds > 64 * 1024 || grid <= 0 || nloc > 64 || nloc * a.nbc > MV_NPT * 64 ||
         (!a.xq && !a.xf)) {
         kr_fail(ML_E_SHAPE, "matvec shape", hipSuccess);
@@ -1007,7 +1015,7 @@ static void qkv(float *q, float *kc, float *vc, const krh_mat *wq, const krh_mat
     a.m[1] = to_kmat(wk);
     a.m[2] = to_kmat(wv);
     a.nmat = 3;
-    a.R = mv_rows(wq->cols, wq->rows + 2 * wk->rows, 1, 64);
+    a.R = mv_rows(wq->cols, wq->rows + 2 * wk->rows, 1, 64, EPI_QKV);
     a.tile0[0] = 0;
     a.tile0[1] = (wq->rows + a.R - 1) / a.R;
     a.tile0[2] = a.tile0[1] + (wk->rows + a.R - 1) / a.R;
