@@ -129,26 +129,28 @@ __global__ void __launch_bounds__(AT_THREADS) k_attn_scores(float *att, const fl
 // them all (QB independent chains: the LDS latency hides under them). Each
 // chain is the per-token kernel's: s = sum_i q_i k_i in index order, then
 // * scale; a token stores only the positions it attends. HD: the head size
-// when it is 64 or 128, else 0 (any).
+// when it is 64 or 128, else 0 (any). TP: positions per K tile, AT_T, or
+// AT_T / 2 for heads whose AT_T-position tile and queries exceed 64 KB of
+// LDS (Gemma's 256-wide heads).
 constexpr int AT_TB = 16;
-template <int HD, int QB, int KT>
+template <int HD, int QB, int KT, int TP = AT_T>
 __global__ void __launch_bounds__(AT_THREADS) k_attn_scores_blk(float *att, const float *q, const KvView kv, int group,
                                                                 int hd_arg, int kv_dim, int max_seq, float scale,
                                                                 const int *pos_p, int ntok) {
     extern __shared__ __align__(16) float at_smem[];
     const int hd = HD ? HD : hd_arg;
-    const int g = blockIdx.x, t0 = blockIdx.y * AT_T, z0 = blockIdx.z * AT_TB, tid = threadIdx.x;
+    const int g = blockIdx.x, t0 = blockIdx.y * TP, z0 = blockIdx.z * AT_TB, tid = threadIdx.x;
     const int pos0 = *pos_p, zn = min(AT_TB, ntok - z0);
     const int nlast = pos0 + z0 + zn;   // positions the block's last token attends
     if (t0 >= nlast) return;
-    const int nt = min(AT_T, nlast - t0), ks = hd + 4, h4 = hd / 4, n_heads = gridDim.x * group;
-    float *kt = at_smem, *qs = at_smem + AT_T * ks;   // K tile [AT_T][ks]; queries [QB][group][hd]
+    const int nt = min(TP, nlast - t0), ks = hd + 4, h4 = hd / 4, n_heads = gridDim.x * group;
+    float *kt = at_smem, *qs = at_smem + TP * ks;   // K tile [TP][ks]; queries [QB][group][hd]
     for (int e = tid; e < nt * h4; e += AT_THREADS) {
         const int r = e / h4, c = e - r * h4;
         *(float4 *)(kt + r * ks + 4 * c) =
             Kv4<KT>::wide(Kv4<KT>::load(kv.k, (size_t)(t0 + r) * kv_dim + (size_t)g * hd + 4 * c));
     }
-    const int t = tid % AT_T, p = t0 + t;   // this thread's position (absolute: no window)
+    const int t = tid % TP, p = t0 + t;   // this thread's position (absolute: no window)
     const size_t qstride = (size_t)group * hd;   // floats between two tokens' queries in LDS
     for (int zb = 0; zb < zn; zb += QB) {
         const int qn = min(QB, zn - zb), gh4 = group * h4;
@@ -160,7 +162,7 @@ __global__ void __launch_bounds__(AT_THREADS) k_attn_scores_blk(float *att, cons
         __syncthreads();
         if (t >= nt) continue;
         const float *kr = kt + t * ks;
-        for (int j = tid / AT_T; j < group; j += AT_THREADS / AT_T) {
+        for (int j = tid / TP; j < group; j += AT_THREADS / TP) {
             // tokens zb + u, u < QB (slots past qn read an earlier block's
             // queries and are not stored)
             const float *qh = qs + (size_t)j * hd;
@@ -1101,18 +1103,23 @@ static void attention(float *ao, float *att, const float *q, const KvView &kv, i
         }
     }
     else {
-        // the queries of QB tokens beside the K tile, within 64 KB of LDS
-        const size_t ktile = sizeof(float) * (size_t)AT_T * (head_dim + 4);
+        // the queries of QB tokens beside a K tile of tp positions, within
+        // 64 KB of LDS (tp = AT_T, or AT_T / 2 for wide heads)
         const size_t qtok = sizeof(float) * (size_t)group * head_dim;
-        const int qb = ktile + 8 * qtok <= 64 * 1024 ? 8 : ktile + 4 * qtok <= 64 * 1024 ? 4 : 0;
+        auto ktile = [&](int tp) { return sizeof(float) * (size_t)tp * (head_dim + 4); };
+        auto pick_qb = [&](int tp) { return ktile(tp) + 8 * qtok <= 64 * 1024 ? 8 : ktile(tp) + 4 * qtok <= 64 * 1024 ? 4 : 0; };
+        const int tp = pick_qb(AT_T) ? AT_T : AT_T / 2, qb = pick_qb(tp);
         if (ntok > 1 && window == 0 && qb) {   // prefill: blocks of AT_TB tokens share a K tile
-            const dim3 bgrid(n_kv_heads, (max_pos + AT_T) / AT_T, (ntok + AT_TB - 1) / AT_TB);
-            const size_t blds = ktile + qb * qtok;
+            const dim3 bgrid(n_kv_heads, (max_pos + tp) / tp, (ntok + AT_TB - 1) / AT_TB);
+            const size_t blds = ktile(tp) + qb * qtok;
             auto go = [&](auto kern) {
                 hipLaunchKernelGGL(kern, bgrid, dim3(AT_THREADS), blds, kr_stream(), att, q, kv, group, head_dim,
                                    kv_dim, max_seq, scale, pos, ntok);
             };
-            if (qb == 8) {
+            if (tp != AT_T) {
+                if (qb == 8) go(k_attn_scores_blk<0, 8, KT, AT_T / 2>);
+                else go(k_attn_scores_blk<0, 4, KT, AT_T / 2>);
+            } else if (qb == 8) {
                 if (head_dim == 128) go(k_attn_scores_blk<128, 8, KT>);
                 else if (head_dim == 64) go(k_attn_scores_blk<64, 8, KT>);
                 else go(k_attn_scores_blk<0, 8, KT>);
