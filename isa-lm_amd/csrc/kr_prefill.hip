@@ -214,7 +214,7 @@ __global__ void __launch_bounds__(256, 2) k_matmul(const MmArgs a) {
     // the prefetch. Only the odd tail's step is conditional; every thread
     // reaches every barrier.
     const int bl = nb - 1;
-    if constexpr (NG == 4) {
+    if constexpr (NG >= 2) {
         WReg R;
         XFrag x0, x1;
         w_load<QT, D16, NG, PAIR>(R, W, xcol, a.ldx, nb, 0, rowl, tid, a.w[1]);
@@ -349,6 +349,15 @@ void launch_mm(const MmArgs &a, const MMat &W) {
             if (W.d16) go(k_matmul<EPI, ML_Q4_0, 1, 4>); else go(k_matmul<EPI, ML_Q4_0, 0, 4>);
         }
     } else if constexpr (EPI != MM_SWIGLU) {
+        if (a.ng == 2) {
+            if (W.type == ML_Q8_0) {
+                if (W.d16) go(k_matmul<EPI, ML_Q8_0, 1, 2>); else go(k_matmul<EPI, ML_Q8_0, 0, 2>);
+            } else {
+                if (W.d16) go(k_matmul<EPI, ML_Q4_0, 1, 2>); else go(k_matmul<EPI, ML_Q4_0, 0, 2>);
+            }
+            kr_check_launch("matmul");
+            return;
+        }
         if (W.type == ML_Q8_0) {
             if (W.d16) go(k_matmul<EPI, ML_Q8_0, 1, 1>); else go(k_matmul<EPI, ML_Q8_0, 0, 1>);
         } else {
@@ -366,7 +375,9 @@ MMat to_mmat(const krh_mat *m) {
 int row_tiles(int rows, int ng) { return (rows + 32 * ng - 1) / (32 * ng); }
 
 // NG for a launch over these row counts and ntt token tiles: 4 when it has
-// at least 3/4 of a 128-row tile per CU, else 1. Measured (K = 4096, 256
+// at least 3/4 of a 128-row tile per CU, else 2 when it has half a 64-row
+// tile per CU (w1 and w3 at the reference's 128-token steps: its 8B prefill
+// through ml_run 5,674 -> 5,844 tok/s), else 1. Measured (K = 4096, 256
 // CUs): a 128-row tile does 4 times a 32-row tile's work in 1.9 times its
 // time, so from about 200 tiles, where the 32-row grid needs two rounds of
 // resident workgroups, the 128-row grid's one round is the shorter (14336
@@ -376,7 +387,8 @@ int row_tiles(int rows, int ng) { return (rows + 32 * ng - 1) / (32 * ng); }
 int pick_ng(int rows0, int rows1, int rows2, int ntt) {
     const int tiles = row_tiles(rows0, 4) + row_tiles(rows1, 4) + row_tiles(rows2, 4);
     const int cus = krh_device_cus() > 0 ? krh_device_cus() : 256;
-    return 4L * tiles * ntt >= 3L * cus ? 4 : 1;
+    const int tiles2 = row_tiles(rows0, 2) + row_tiles(rows1, 2) + row_tiles(rows2, 2);
+    return 4L * tiles * ntt >= 3L * cus ? 4 : 2L * tiles2 * ntt >= cus ? 2 : 1;
 }
 
 // ---- per-token work of a batched step ----

@@ -289,7 +289,9 @@ def oracle_matvec(q, dh, rows, cols, typ, xq, xd):
                                              (K.ML_Q8_0, 4096, 14336, 2047), (K.ML_Q4_0, 8192, 2048, 2048),
                                              (K.ML_Q8_0, 2048, 8192, 2048), (K.ML_Q4_0, 4864, 896, 511),
                                              # 128-row tiles from 3/4 of a tile per CU on: 336 and 192 tiles
-                                             (K.ML_Q8_0, 14336, 4096, 300), (K.ML_Q4_0, 4096, 4096, 700)])
+                                             (K.ML_Q8_0, 14336, 4096, 300), (K.ML_Q4_0, 4096, 4096, 700),
+                                             # 64-row tiles: a 128-token step of w1 (224 tiles)
+                                             (K.ML_Q8_0, 14336, 4096, 128), (K.ML_Q4_0, 14336, 4096, 128)])
 def test_matmul_prompt_lengths(dev, typ, rows, cols, T):
     """the prefill matmul over a whole prompt step: sampled tokens' rows
     bit-equal to the matvec (tests/test_kernels.c:146-189's rule)"""
