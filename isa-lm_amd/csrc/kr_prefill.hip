@@ -45,6 +45,7 @@ struct MmArgs {
     const float *rope_cos, *rope_sin;
     int head_dim, pos0;
     int ng;              // row groups per wave (the kernel's NG)
+    int tw;              // waves per workgroup (the kernel's TW): 32 TW tokens a workgroup
     int8_t *hq;          // MM_SWIGLU: h's Q8_0 quants [T][rows] and scales [rows / 32][ldx]
     float *hdT;
 };
@@ -95,11 +96,11 @@ struct WReg {
 constexpr int MM_ST = 3;   // LDS ring stages of the weight tile
 constexpr int MM_PD = 8;   // NG = 1: blocks of load lookahead (even: the LDS stage of step k is k % 2)
 
-template <int NG>
+template <int NG, int TT>
 struct MmLds {
     v4i w[MM_ST][32 * NG][2];     // [stage][row][half]
     uint32_t d[MM_ST][32 * NG];   // [stage][row] raw scale bits
-    float xs[MM_ST][MM_TT];       // [stage][token] the tokens' scales
+    float xs[MM_ST][TT];          // [stage][token] the tokens' scales
 };
 
 __device__ __forceinline__ void x_load(XFrag &f, const MmArgs &a, int b, int tokl, int lane) {
@@ -115,7 +116,7 @@ __device__ __forceinline__ void x_load(XFrag &f, const MmArgs &a, int b, int tok
 // token scale, threads 128.. the same as thread tid - 128, unused). PAIR (NG
 // 4): tile rows 0-63 are rows rowl.. of W, tile rows 64-127 the same rows of
 // W2 (SwiGLU's w1 and w3).
-template <int QT, int D16, int NG, bool PAIR = false>
+template <int QT, int D16, int NG, int TT, bool PAIR = false>
 __device__ __forceinline__ void w_load(WReg &R, const MMat &W, const float *xcol, int ldx, int nb, int b, int rowl,
                                        int tid, const MMat &W2 = MMat{}) {
     const int tr = (tid >> 1) & (32 * NG - 1);
@@ -126,12 +127,12 @@ __device__ __forceinline__ void w_load(WReg &R, const MMat &W, const float *xcol
     const void *wd = PAIR && tr >= 64 ? W2.d : W.d;
     R.w = weight_frag<QT>(wq + blk * (QT == ML_Q8_0 ? 32 : 16), tid & 1);
     R.d = D16 ? (uint32_t)((const uint16_t *)wd)[blk] : ((const uint32_t *)wd)[blk];
-    R.xs = xcol[(size_t)b * ldx + (tid & (MM_TT - 1))];
+    R.xs = xcol[(size_t)b * ldx + (tid & (TT - 1))];
 }
 
-template <int NG>
-__device__ __forceinline__ void w_store(MmLds<NG> &L, int st, const WReg &R, int tid) {
-    if (tid < MM_TT) L.xs[st][tid] = R.xs;
+template <int NG, int TT>
+__device__ __forceinline__ void w_store(MmLds<NG, TT> &L, int st, const WReg &R, int tid) {
+    if (tid < TT) L.xs[st][tid] = R.xs;
     if ((tid >> 1) >= 32 * NG) return;
     L.w[st][tid >> 1][tid & 1] = R.w;
     if ((tid & 1) == 0) L.d[st][tid >> 1] = R.d;
@@ -144,8 +145,8 @@ __device__ __forceinline__ void w_store(MmLds<NG> &L, int st, const WReg &R, int
 // tile's token scales (16 cross-lane shuffles of one loaded scale per lane
 // cost 3-6% more time). The weight fragments and scales come from the
 // workgroup's LDS tile as well.
-template <int D16, int NG>
-__device__ __forceinline__ void mm_step(float (&acc)[NG][16], const XFrag &f, const MmLds<NG> &L, int st, int lane,
+template <int D16, int NG, int TT>
+__device__ __forceinline__ void mm_step(float (&acc)[NG][16], const XFrag &f, const MmLds<NG, TT> &L, int st, int lane,
                                         int tokw) {
     const int ln = lane & 31, hf = lane >> 5;
     v4i wb[NG];
@@ -181,26 +182,28 @@ __device__ __forceinline__ void mm_step(float (&acc)[NG][16], const XFrag &f, co
     }
 }
 
-// Workgroup = 4 waves over a 32 NG-row x 128-token tile; wave w takes all
-// the tile's rows (NG row groups) and tokens 32 w .. 32 w + 31. The 256
+// Workgroup = TW waves (4, or 1 for short batches) over a 32 NG-row x
+// 32 TW-token tile; wave w takes all the tile's rows (NG row groups) and
+// tokens 32 w .. 32 w + 31. The 256
 // threads load each block's weight tile and its scales once (16 bytes and
 // one scale per thread) into an LDS ring of 3 stages: block b + 1 is stored
 // during step b into the stage step b - 2 read, and the barrier closing each
 // step orders those stores before step b + 1 reads them.
-template <int EPI, int QT, int D16, int NG>
-__global__ void __launch_bounds__(256, 2) k_matmul(const MmArgs a) {
-    __shared__ MmLds<NG> L;
+template <int EPI, int QT, int D16, int NG, int TW = 4>
+__global__ void __launch_bounds__(64 * TW, 2) k_matmul(const MmArgs a) {   // 2: waves per SIMD, at least
+    constexpr int TT = 32 * TW;   // tokens per workgroup
+    __shared__ MmLds<NG, TT> L;
     int mi = 0;
     while (mi + 1 < a.nmat && (int)blockIdx.x >= a.tile0[mi + 1]) mi++;
     const MMat W = mi == 0 ? a.w[0] : (mi == 1 ? a.w[1] : a.w[2]);
-    const int ntt = (a.T + MM_TT - 1) / MM_TT;
+    const int ntt = (a.T + TT - 1) / TT;
     const int local = (int)blockIdx.x - a.tile0[mi];
     const int rt = local / ntt, tt = local - rt * ntt;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     constexpr bool PAIR = EPI == MM_SWIGLU;   // 64 rows of w1 and the same 64 of w3
-    const int rowl = rt * (PAIR ? 64 : 32 * NG), tokl = tt * MM_TT + 32 * wave;
+    const int rowl = rt * (PAIR ? 64 : 32 * NG), tokl = tt * TT + 32 * wave;
     const int nb = a.K / KR_QK;
-    const float *xcol = a.xdT + (size_t)tt * MM_TT;
+    const float *xcol = a.xdT + (size_t)tt * TT;
 
     float acc[NG][16];
 #pragma unroll
@@ -217,9 +220,9 @@ __global__ void __launch_bounds__(256, 2) k_matmul(const MmArgs a) {
     if constexpr (NG >= 2) {
         WReg R;
         XFrag x0, x1;
-        w_load<QT, D16, NG, PAIR>(R, W, xcol, a.ldx, nb, 0, rowl, tid, a.w[1]);
+        w_load<QT, D16, NG, TT, PAIR>(R, W, xcol, a.ldx, nb, 0, rowl, tid, a.w[1]);
         w_store(L, 0, R, tid);
-        w_load<QT, D16, NG, PAIR>(R, W, xcol, a.ldx, nb, 1 < bl ? 1 : bl, rowl, tid, a.w[1]);
+        w_load<QT, D16, NG, TT, PAIR>(R, W, xcol, a.ldx, nb, 1 < bl ? 1 : bl, rowl, tid, a.w[1]);
         x_load(x0, a, 0, tokl, lane);
         x_load(x1, a, 1 < bl ? 1 : bl, tokl, lane);
         __syncthreads();
@@ -227,13 +230,13 @@ __global__ void __launch_bounds__(256, 2) k_matmul(const MmArgs a) {
         for (int b = 0; b < nb; b += 2) {
             const int s1 = st == MM_ST - 1 ? 0 : st + 1, s2 = s1 == MM_ST - 1 ? 0 : s1 + 1;
             w_store(L, s1, R, tid);
-            w_load<QT, D16, NG, PAIR>(R, W, xcol, a.ldx, nb, b + 2 < bl ? b + 2 : bl, rowl, tid, a.w[1]);
-            mm_step<D16, NG>(acc, x0, L, st, lane, 32 * wave);
+            w_load<QT, D16, NG, TT, PAIR>(R, W, xcol, a.ldx, nb, b + 2 < bl ? b + 2 : bl, rowl, tid, a.w[1]);
+            mm_step<D16, NG, TT>(acc, x0, L, st, lane, 32 * wave);
             x_load(x0, a, b + 2 < bl ? b + 2 : bl, tokl, lane);
             __syncthreads();
             w_store(L, s2, R, tid);
-            w_load<QT, D16, NG, PAIR>(R, W, xcol, a.ldx, nb, b + 3 < bl ? b + 3 : bl, rowl, tid, a.w[1]);
-            if (b + 1 < nb) mm_step<D16, NG>(acc, x1, L, s1, lane, 32 * wave);
+            w_load<QT, D16, NG, TT, PAIR>(R, W, xcol, a.ldx, nb, b + 3 < bl ? b + 3 : bl, rowl, tid, a.w[1]);
+            if (b + 1 < nb) mm_step<D16, NG, TT>(acc, x1, L, s1, lane, 32 * wave);
             x_load(x1, a, b + 3 < bl ? b + 3 : bl, tokl, lane);
             __syncthreads();
             st = s2;
@@ -252,20 +255,20 @@ __global__ void __launch_bounds__(256, 2) k_matmul(const MmArgs a) {
         XFrag x[MM_PD];
 #pragma unroll
         for (int j = 0; j < MM_PD; j++) {
-            w_load<QT, D16, NG, PAIR>(R[j], W, xcol, a.ldx, nb, j < bl ? j : bl, rowl, tid, a.w[1]);
+            w_load<QT, D16, NG, TT, PAIR>(R[j], W, xcol, a.ldx, nb, j < bl ? j : bl, rowl, tid, a.w[1]);
             x_load(x[j], a, j < bl ? j : bl, tokl, lane);
         }
         w_store(L, 0, R[0], tid);
-        w_load<QT, D16, NG, PAIR>(R[0], W, xcol, a.ldx, nb, MM_PD < bl ? MM_PD : bl, rowl, tid, a.w[1]);
+        w_load<QT, D16, NG, TT, PAIR>(R[0], W, xcol, a.ldx, nb, MM_PD < bl ? MM_PD : bl, rowl, tid, a.w[1]);
         __syncthreads();
         for (int b0 = 0; b0 < nb; b0 += MM_PD) {
 #pragma unroll
             for (int k = 0; k < MM_PD; k++) {
                 const int t = b0 + k, k1 = (k + 1) % MM_PD;
                 w_store(L, (k + 1) & 1, R[k1], tid);
-                w_load<QT, D16, NG, PAIR>(R[k1], W, xcol, a.ldx, nb, t + 1 + MM_PD < bl ? t + 1 + MM_PD : bl, rowl,
+                w_load<QT, D16, NG, TT, PAIR>(R[k1], W, xcol, a.ldx, nb, t + 1 + MM_PD < bl ? t + 1 + MM_PD : bl, rowl,
                                           tid, a.w[1]);
-                if (t < nb) mm_step<D16, NG>(acc, x[k], L, k & 1, lane, 32 * wave);
+                if (t < nb) mm_step<D16, NG, TT>(acc, x[k], L, k & 1, lane, 32 * wave);
                 x_load(x[k], a, t + MM_PD < bl ? t + MM_PD : bl, tokl, lane);
                 __syncthreads();
             }
@@ -333,11 +336,11 @@ __global__ void __launch_bounds__(256, 2) k_matmul(const MmArgs a) {
 template <int EPI>
 void launch_mm(const MmArgs &a, const MMat &W) {
     const int grid = a.tile0[a.nmat];
-    if (a.K % KR_QK || a.T <= 0 || grid <= 0 || a.ldx % MM_TT || a.T > a.ldx) {
+    if (a.K % KR_QK || a.T <= 0 || grid <= 0 || a.ldx % MM_TT || a.T > a.ldx || (a.tw != 4 && (a.tw != 1 || a.ng != 1))) {
         kr_fail(ML_E_SHAPE, "matmul shape", hipSuccess);
         return;
     }
-    auto go = [&](auto kern) { hipLaunchKernelGGL(kern, dim3(grid), dim3(256), 0, kr_stream(), a); };
+    auto go = [&](auto kern) { hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * a.tw), 0, kr_stream(), a); };
     if (EPI == MM_SWIGLU && a.ng != 4) {
         kr_fail(ML_E_SHAPE, "matmul: SwiGLU pairs take 128-row tiles", hipSuccess);
         return;
@@ -358,7 +361,13 @@ void launch_mm(const MmArgs &a, const MMat &W) {
             kr_check_launch("matmul");
             return;
         }
-        if (W.type == ML_Q8_0) {
+        if (a.tw == 1) {
+            if (W.type == ML_Q8_0) {
+                if (W.d16) go(k_matmul<EPI, ML_Q8_0, 1, 1, 1>); else go(k_matmul<EPI, ML_Q8_0, 0, 1, 1>);
+            } else {
+                if (W.d16) go(k_matmul<EPI, ML_Q4_0, 1, 1, 1>); else go(k_matmul<EPI, ML_Q4_0, 0, 1, 1>);
+            }
+        } else if (W.type == ML_Q8_0) {
             if (W.d16) go(k_matmul<EPI, ML_Q8_0, 1, 1>); else go(k_matmul<EPI, ML_Q8_0, 0, 1>);
         } else {
             if (W.d16) go(k_matmul<EPI, ML_Q4_0, 1, 1>); else go(k_matmul<EPI, ML_Q4_0, 0, 1>);
@@ -389,6 +398,15 @@ int pick_ng(int rows0, int rows1, int rows2, int ntt) {
     const int cus = krh_device_cus() > 0 ? krh_device_cus() : 256;
     const int tiles2 = row_tiles(rows0, 2) + row_tiles(rows1, 2) + row_tiles(rows2, 2);
     return 4L * tiles * ntt >= 3L * cus ? 4 : 2L * tiles2 * ntt >= cus ? 2 : 1;
+}
+
+// Waves per workgroup (TW) for an NG 1 launch whose grid of 128-token tiles
+// leaves CUs idle (fewer than two 32-row tiles per CU: the reference's
+// 128-token steps over wq, wk, wv, wo and w2): one wave and 32 tokens a
+// workgroup gives 4 times the workgroups. Else 4.
+int pick_tw(int ng, int grid128) {
+    const int cus = krh_device_cus() > 0 ? krh_device_cus() : 256;
+    return ng == 1 && grid128 < 2 * cus ? 1 : 4;
 }
 
 // ---- per-token work of a batched step ----
@@ -458,6 +476,7 @@ extern "C" void krh_matmul_swiglu(int8_t *hq, float *hdT, const krh_mat *w1, con
     a.tile0[0] = 0;
     const int ntt = (T + MM_TT - 1) / MM_TT;
     a.ng = 4;
+    a.tw = 4;
     a.tile0[1] = (w1->rows + 63) / 64 * ntt;
     a.xq = xq;
     a.xdT = xdT;
@@ -475,8 +494,10 @@ extern "C" void krh_matmul(float *Y, int ldy, const krh_mat *W, const int8_t *xq
     a.w[0] = to_mmat(W);
     a.nmat = 1;
     a.tile0[0] = 0;
-    const int ntt = (T + MM_TT - 1) / MM_TT;
-    a.ng = pick_ng(W->rows, 0, 0, ntt);
+    const int ntt128 = (T + MM_TT - 1) / MM_TT;
+    a.ng = pick_ng(W->rows, 0, 0, ntt128);
+    a.tw = pick_tw(a.ng, row_tiles(W->rows, a.ng) * ntt128);
+    const int ntt = (T + 32 * a.tw - 1) / (32 * a.tw);
     a.tile0[1] = row_tiles(W->rows, a.ng) * ntt;
     a.xq = xq;
     a.xdT = xdT;
@@ -499,7 +520,7 @@ static void matmul_qkv(float *q, float *kc, float *vc, const krh_mat *wq, const 
         kr_fail(ML_E_SHAPE, "matmul qkv shapes", hipSuccess);
         return;
     }
-    const int ntt = (T + MM_TT - 1) / MM_TT;
+    const int ntt128 = (T + MM_TT - 1) / MM_TT;
     MmArgs a = {};
     a.w[0] = to_mmat(wq);
     a.w[1] = to_mmat(wk);
@@ -523,7 +544,9 @@ static void matmul_qkv(float *q, float *kc, float *vc, const krh_mat *wq, const 
     a.rope_sin = rope_sin;
     a.head_dim = head_dim;
     a.pos0 = pos0;
-    a.ng = pick_ng(wq->rows, wk->rows, wv->rows, ntt);
+    a.ng = pick_ng(wq->rows, wk->rows, wv->rows, ntt128);
+    a.tw = pick_tw(a.ng, (row_tiles(wq->rows, a.ng) + 2 * row_tiles(wk->rows, a.ng)) * ntt128);
+    const int ntt = (T + 32 * a.tw - 1) / (32 * a.tw);
     a.tile0[0] = 0;
     a.tile0[1] = row_tiles(wq->rows, a.ng) * ntt;
     a.tile0[2] = a.tile0[1] + row_tiles(wk->rows, a.ng) * ntt;
