@@ -184,7 +184,7 @@ __device__ __forceinline__ void mm_step(float (&acc)[NG][16], const XFrag &f, co
 
 // Workgroup = TW waves (4, or 1 for short batches) over a 32 NG-row x
 // 32 TW-token tile; wave w takes all the tile's rows (NG row groups) and
-// tokens 32 w .. 32 w + 31. The 256
+// tokens 32 w .. 32 w + 31. The workgroup's
 // threads load each block's weight tile and its scales once (16 bytes and
 // one scale per thread) into an LDS ring of 3 stages: block b + 1 is stored
 // during step b into the stage step b - 2 read, and the barrier closing each
