@@ -55,6 +55,8 @@ typedef struct {
 static kh_range g_rg[KH_RANGES];
 static int g_nrg;
 static int *g_ints;                 /* device ints: [0] position, [1] token row, [2] zero */
+static int g_pos_set = -1;          /* the position g_ints[0] holds (-1: none yet) */
+static int g_row_set;               /* g_ints[1] holds 0 */
 static float *g_dT, *g_batt;        /* matmul scales, batched attention scratch */
 static size_t g_dT_n, g_batt_n;
 static const void *g_cls_q;         /* the classifier's quants (ml_model_pack) */
@@ -66,6 +68,14 @@ static int ready(void) {
     if (krh_init() != ML_OK) return 0;
     if (!g_ints && (g_ints = krh_alloc(3 * sizeof(int)))) krh_set_int(g_ints + 2, 0);
     return g_ints != NULL;
+}
+
+/* g_ints[0] = pos, written only when it changes: every layer of a token
+ * attends at one position, and the launches run in order on one stream */
+static void set_pos(int pos) {
+    if (pos == g_pos_set) return;
+    krh_set_int(g_ints, pos);
+    g_pos_set = pos;
 }
 
 static uint8_t *dev_addr(const void *p, size_t n) {
@@ -300,7 +310,10 @@ void ml_dequant_row(float *out, const ml_qtensor *W, int row) {
         mat_of(&c, W, row, row + 1, &m);
         float *o = arg(&c, out, sizeof(float) * (size_t)W->cols, 0, 1);
         if (!c.fail) {
-            krh_set_int(g_ints + 1, 0);
+            if (!g_row_set) {
+                krh_set_int(g_ints + 1, 0);
+                g_row_set = 1;
+            }
             krh_embed(o, &m, g_ints + 1, W == g_emb ? g_emb_scale : 1.0f);
         }
         done(&c);
@@ -596,7 +609,7 @@ void ml_attention(ml_pool *pool, float *out, const float *q, const ml_kv_layer *
     float *att = arg(&c, att_scratch, F((size_t)cfg->n_heads * cfg->max_seq), 0, 0);
     const ml_kv_layer d = dev_kv(&c, kv, cfg);
     if (!c.fail) {
-        krh_set_int(g_ints, pos);
+        set_pos(pos);
         krh_attention_kv_softcap(o, att, qv, &d, cfg->n_heads, cfg->n_kv_heads, cfg->head_dim, cfg->max_seq,
                                  cfg->attn_scale, g_ints, 1, cfg->max_seq - 1, cfg->attn_softcap);
     }
@@ -614,7 +627,7 @@ void ml_attention_batch(ml_pool *pool, float *out, const float *q, const ml_kv_l
     const float *qv = arg(&c, q, F((size_t)n * cfg->q_dim), 1, 0);
     const ml_kv_layer d = dev_kv(&c, kv, cfg);
     if (!c.fail && g_batt) {
-        krh_set_int(g_ints, pos0);
+        set_pos(pos0);
         krh_attention_kv_softcap(o, g_batt, qv, &d, cfg->n_heads, cfg->n_kv_heads, cfg->head_dim, cfg->max_seq,
                                  cfg->attn_scale, g_ints, n, pos0 + n - 1, cfg->attn_softcap);
     }
