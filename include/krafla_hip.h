@@ -212,6 +212,11 @@ void krh_store_kv(int kv_type, void *kc, void *vc, float *kd, float *vd, const f
  * 128 and >= T; xq must be readable for ldx rows. */
 void krh_matmul(float *Y, int ldy, const krh_mat *W, const int8_t *xq, const float *xdT, int ldx, int T,
                 int accumulate);
+/* krh_matmul over the scales as an ml_qbatch holds them, token rows
+ * xd[t * (W->cols / 32) + b] (ops/ops.c:75-79: ml_matmul's X->d, read in
+ * place, no transpose launch); xd is read for T rows only. */
+void krh_matmul_rows(float *Y, int ldy, const krh_mat *W, const int8_t *xq, const float *xd, int ldx, int T,
+                     int accumulate);
 /* The FFN's products and activation of a prompt step in one launch
  * (model/transformer.c:410-413: the w1 and w3 ml_matmul calls, then
  * TOK_DOWN_IN's act_mul and quantize_row_t, :353-355): per
@@ -342,8 +347,6 @@ void krh_quantize_q8_rows(int8_t *q, size_t ldq, float *d, size_t ldd, const flo
 void krh_softcap_rows(float *x, size_t ld, int rows, int n, float cap);    /* ops/ops.c:98-101, the C library's tanhf */
 /* *dst = value, in stream order (positions and token ids of op-table calls) */
 void krh_set_int(int *dst, int value);
-/* dT[b * ldx + t] = d[t * nb + b]: batch scales to krh_matmul's layout */
-void krh_transpose_scales(float *dT, int ldx, const float *d, int n, int nb);
 
 /* ---- synthetic data ---- */
 /* Random quantized matrix [rows][cols] on the device: normals of the host

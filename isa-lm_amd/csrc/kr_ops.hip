@@ -177,14 +177,6 @@ __global__ void k_softcap(float *x, size_t ld, int rows, int n, float cap) {
 
 __global__ void k_set_int(int *dst, int v) { *dst = v; }
 
-// dT[b * ldx + t] = d[t * nb + b]
-__global__ void k_transpose(float *dT, int ldx, const float *d, int n, int nb) {
-    const size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (e >= (size_t)n * nb) return;
-    const int t = (int)(e / nb), b = (int)(e % nb);
-    dT[(size_t)b * ldx + t] = d[e];
-}
-
 unsigned blocks(size_t n) { return (unsigned)((n + OP_T - 1) / OP_T); }
 
 }  // namespace
@@ -340,10 +332,4 @@ extern "C" void krh_softcap_rows(float *x, size_t ld, int rows, int n, float cap
 extern "C" void krh_set_int(int *dst, int value) {
     hipLaunchKernelGGL(k_set_int, dim3(1), dim3(1), 0, kr_stream(), dst, value);
     kr_check_launch("set_int");
-}
-extern "C" void krh_transpose_scales(float *dT, int ldx, const float *d, int n, int nb) {
-    const size_t e = (size_t)n * nb;
-    if (e == 0) return;
-    hipLaunchKernelGGL(k_transpose, dim3(blocks(e)), dim3(OP_T), 0, kr_stream(), dT, ldx, d, n, nb);
-    kr_check_launch("transpose_scales");
 }

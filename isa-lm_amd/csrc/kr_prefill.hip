@@ -36,8 +36,9 @@ struct MmArgs {
     int tile0[4];        // first workgroup of matrix i; tile0[nmat] = grid size
     int nmat;
     const int8_t *xq;    // [T][K] (rows up to the padded token count readable)
-    const float *xdT;    // [K / 32][ldx] activation scales, transposed
-    int ldx;             // token stride of xdT: T rounded up to MM_TT
+    const float *xdT;    // activation scale of block b of token t: xdT[b * xsb + t * xst]
+    int ldx;             // T rounded up to MM_TT: xq's readable rows
+    int xsb, xst;        // transposed [K / 32][ldx]: ldx and 1; token rows [T][K / 32]: 1 and K / 32
     int T, K;
     float *y[3];         // y[i][t * ldy[i] + r]
     int ldy[3];
@@ -112,12 +113,13 @@ __device__ __forceinline__ void x_load(XFrag &f, const MmArgs &a, int b, int tok
 // thread tid loads half tid % 2 of tile row (tid / 2) mod 32 NG (for NG < 4
 // the surplus threads repeat a row's load, which keeps every load
 // unconditional; only the first 64 NG store it)
-// (xcol: the workgroup's first token column of xdT; every thread loads a
-// token scale, threads 128.. the same as thread tid - 128, unused). PAIR (NG
+// (xcol: the scales of this thread's token, tid % TT of the workgroup's,
+// clamped to the last token; threads TT.. repeat thread tid % TT's load,
+// unused; xsb: the stride from block to block). PAIR (NG
 // 4): tile rows 0-63 are rows rowl.. of W, tile rows 64-127 the same rows of
 // W2 (SwiGLU's w1 and w3).
 template <int QT, int D16, int NG, int TT, bool PAIR = false>
-__device__ __forceinline__ void w_load(WReg &R, const MMat &W, const float *xcol, int ldx, int nb, int b, int rowl,
+__device__ __forceinline__ void w_load(WReg &R, const MMat &W, const float *xcol, int xsb, int nb, int b, int rowl,
                                        int tid, const MMat &W2 = MMat{}) {
     const int tr = (tid >> 1) & (32 * NG - 1);
     int r = rowl + (PAIR ? tr & 63 : tr);
@@ -127,7 +129,7 @@ __device__ __forceinline__ void w_load(WReg &R, const MMat &W, const float *xcol
     const void *wd = PAIR && tr >= 64 ? W2.d : W.d;
     R.w = weight_frag<QT>(wq + blk * (QT == ML_Q8_0 ? 32 : 16), tid & 1);
     R.d = D16 ? (uint32_t)((const uint16_t *)wd)[blk] : ((const uint32_t *)wd)[blk];
-    R.xs = xcol[(size_t)b * ldx + (tid & (TT - 1))];
+    R.xs = xcol[(size_t)b * xsb];
 }
 
 template <int NG, int TT>
@@ -203,7 +205,7 @@ __global__ void __launch_bounds__(64 * TW, 2) k_matmul(const MmArgs a) {   // 2:
     constexpr bool PAIR = EPI == MM_SWIGLU;   // 64 rows of w1 and the same 64 of w3
     const int rowl = rt * (PAIR ? 64 : 32 * NG), tokl = tt * TT + 32 * wave;
     const int nb = a.K / KR_QK;
-    const float *xcol = a.xdT + (size_t)tt * TT;
+    const float *xcol = a.xdT + (size_t)min(tt * TT + (tid & (TT - 1)), a.T - 1) * a.xst;
 
     float acc[NG][16];
 #pragma unroll
@@ -220,9 +222,9 @@ __global__ void __launch_bounds__(64 * TW, 2) k_matmul(const MmArgs a) {   // 2:
     if constexpr (NG >= 2) {
         WReg R;
         XFrag x0, x1;
-        w_load<QT, D16, NG, TT, PAIR>(R, W, xcol, a.ldx, nb, 0, rowl, tid, a.w[1]);
+        w_load<QT, D16, NG, TT, PAIR>(R, W, xcol, a.xsb, nb, 0, rowl, tid, a.w[1]);
         w_store(L, 0, R, tid);
-        w_load<QT, D16, NG, TT, PAIR>(R, W, xcol, a.ldx, nb, 1 < bl ? 1 : bl, rowl, tid, a.w[1]);
+        w_load<QT, D16, NG, TT, PAIR>(R, W, xcol, a.xsb, nb, 1 < bl ? 1 : bl, rowl, tid, a.w[1]);
         x_load(x0, a, 0, tokl, lane);
         x_load(x1, a, 1 < bl ? 1 : bl, tokl, lane);
         __syncthreads();
@@ -230,12 +232,12 @@ __global__ void __launch_bounds__(64 * TW, 2) k_matmul(const MmArgs a) {   // 2:
         for (int b = 0; b < nb; b += 2) {
             const int s1 = st == MM_ST - 1 ? 0 : st + 1, s2 = s1 == MM_ST - 1 ? 0 : s1 + 1;
             w_store(L, s1, R, tid);
-            w_load<QT, D16, NG, TT, PAIR>(R, W, xcol, a.ldx, nb, b + 2 < bl ? b + 2 : bl, rowl, tid, a.w[1]);
+            w_load<QT, D16, NG, TT, PAIR>(R, W, xcol, a.xsb, nb, b + 2 < bl ? b + 2 : bl, rowl, tid, a.w[1]);
             mm_step<D16, NG, TT>(acc, x0, L, st, lane, 32 * wave);
             x_load(x0, a, b + 2 < bl ? b + 2 : bl, tokl, lane);
             __syncthreads();
             w_store(L, s2, R, tid);
-            w_load<QT, D16, NG, TT, PAIR>(R, W, xcol, a.ldx, nb, b + 3 < bl ? b + 3 : bl, rowl, tid, a.w[1]);
+            w_load<QT, D16, NG, TT, PAIR>(R, W, xcol, a.xsb, nb, b + 3 < bl ? b + 3 : bl, rowl, tid, a.w[1]);
             if (b + 1 < nb) mm_step<D16, NG, TT>(acc, x1, L, s1, lane, 32 * wave);
             x_load(x1, a, b + 3 < bl ? b + 3 : bl, tokl, lane);
             __syncthreads();
@@ -255,18 +257,18 @@ __global__ void __launch_bounds__(64 * TW, 2) k_matmul(const MmArgs a) {   // 2:
         XFrag x[MM_PD];
 #pragma unroll
         for (int j = 0; j < MM_PD; j++) {
-            w_load<QT, D16, NG, TT, PAIR>(R[j], W, xcol, a.ldx, nb, j < bl ? j : bl, rowl, tid, a.w[1]);
+            w_load<QT, D16, NG, TT, PAIR>(R[j], W, xcol, a.xsb, nb, j < bl ? j : bl, rowl, tid, a.w[1]);
             x_load(x[j], a, j < bl ? j : bl, tokl, lane);
         }
         w_store(L, 0, R[0], tid);
-        w_load<QT, D16, NG, TT, PAIR>(R[0], W, xcol, a.ldx, nb, MM_PD < bl ? MM_PD : bl, rowl, tid, a.w[1]);
+        w_load<QT, D16, NG, TT, PAIR>(R[0], W, xcol, a.xsb, nb, MM_PD < bl ? MM_PD : bl, rowl, tid, a.w[1]);
         __syncthreads();
         for (int b0 = 0; b0 < nb; b0 += MM_PD) {
 #pragma unroll
             for (int k = 0; k < MM_PD; k++) {
                 const int t = b0 + k, k1 = (k + 1) % MM_PD;
                 w_store(L, (k + 1) & 1, R[k1], tid);
-                w_load<QT, D16, NG, TT, PAIR>(R[k1], W, xcol, a.ldx, nb, t + 1 + MM_PD < bl ? t + 1 + MM_PD : bl, rowl,
+                w_load<QT, D16, NG, TT, PAIR>(R[k1], W, xcol, a.xsb, nb, t + 1 + MM_PD < bl ? t + 1 + MM_PD : bl, rowl,
                                           tid, a.w[1]);
                 if (t < nb) mm_step<D16, NG, TT>(acc, x[k], L, k & 1, lane, 32 * wave);
                 x_load(x[k], a, t + MM_PD < bl ? t + MM_PD : bl, tokl, lane);
@@ -336,7 +338,7 @@ __global__ void __launch_bounds__(64 * TW, 2) k_matmul(const MmArgs a) {   // 2:
 template <int EPI>
 void launch_mm(const MmArgs &a, const MMat &W) {
     const int grid = a.tile0[a.nmat];
-    if (a.K % KR_QK || a.T <= 0 || grid <= 0 || a.ldx % MM_TT || a.T > a.ldx || (a.tw != 4 && (a.tw != 1 || a.ng != 1))) {
+    if (a.K % KR_QK || a.T <= 0 || grid <= 0 || a.ldx % MM_TT || a.T > a.ldx || a.xsb <= 0 || a.xst <= 0 || (a.tw != 4 && (a.tw != 1 || a.ng != 1))) {
         kr_fail(ML_E_SHAPE, "matmul shape", hipSuccess);
         return;
     }
@@ -481,6 +483,8 @@ extern "C" void krh_matmul_swiglu(int8_t *hq, float *hdT, const krh_mat *w1, con
     a.xq = xq;
     a.xdT = xdT;
     a.ldx = ldx;
+    a.xsb = ldx;
+    a.xst = 1;
     a.T = T;
     a.K = w1->cols;
     a.hq = hq;
@@ -488,8 +492,9 @@ extern "C" void krh_matmul_swiglu(int8_t *hq, float *hdT, const krh_mat *w1, con
     launch_mm<MM_SWIGLU>(a, a.w[0]);
 }
 
-extern "C" void krh_matmul(float *Y, int ldy, const krh_mat *W, const int8_t *xq, const float *xdT, int ldx, int T,
-                           int accumulate) {
+// one matrix over T tokens; the scales' strides say their layout
+static void matmul_one(float *Y, int ldy, const krh_mat *W, const int8_t *xq, const float *xd, int ldx, int T,
+                       int accumulate, int xsb, int xst) {
     MmArgs a = {};
     a.w[0] = to_mmat(W);
     a.nmat = 1;
@@ -500,14 +505,26 @@ extern "C" void krh_matmul(float *Y, int ldy, const krh_mat *W, const int8_t *xq
     const int ntt = (T + 32 * a.tw - 1) / (32 * a.tw);
     a.tile0[1] = row_tiles(W->rows, a.ng) * ntt;
     a.xq = xq;
-    a.xdT = xdT;
+    a.xdT = xd;
     a.ldx = ldx;
+    a.xsb = xsb;
+    a.xst = xst;
     a.T = T;
     a.K = W->cols;
     a.y[0] = Y;
     a.ldy[0] = ldy;
     if (accumulate) launch_mm<MM_ADD>(a, a.w[0]);
     else launch_mm<MM_STORE>(a, a.w[0]);
+}
+
+extern "C" void krh_matmul(float *Y, int ldy, const krh_mat *W, const int8_t *xq, const float *xdT, int ldx, int T,
+                           int accumulate) {
+    matmul_one(Y, ldy, W, xq, xdT, ldx, T, accumulate, ldx, 1);
+}
+
+extern "C" void krh_matmul_rows(float *Y, int ldy, const krh_mat *W, const int8_t *xq, const float *xd, int ldx,
+                                int T, int accumulate) {
+    matmul_one(Y, ldy, W, xq, xd, ldx, T, accumulate, 1, W->cols / KR_QK);
 }
 
 // k and v go to the F32 cache rows pos0 + t, or with stage set to the
@@ -528,6 +545,8 @@ static void matmul_qkv(float *q, float *kc, float *vc, const krh_mat *wq, const 
     a.xq = xq;
     a.xdT = xdT;
     a.ldx = ldx;
+    a.xsb = ldx;
+    a.xst = 1;
     a.T = T;
     a.K = wq->cols;
     // q rows [t][q_dim]; k and v straight into the cache rows pos0 + t

@@ -178,6 +178,7 @@ for name, res, args in [
     ("krh_rmsnorm_q8_t", None, [_P, _P, C.c_int, _P, _P, _P, C.c_int, C.c_float, C.c_int]),
     ("krh_quantize_q8_t", None, [_P, _P, C.c_int, _P, C.c_int, C.c_int]),
     ("krh_matmul", None, [_P, C.c_int, C.POINTER(KrhMat), _P, _P, C.c_int, C.c_int, C.c_int]),
+    ("krh_matmul_rows", None, [_P, C.c_int, C.POINTER(KrhMat), _P, _P, C.c_int, C.c_int, C.c_int]),
     ("krh_matmul_swiglu", None, [_P, _P, C.POINTER(KrhMat), C.POINTER(KrhMat), _P, _P, C.c_int, C.c_int]),
     ("krh_matmul_qkv", None, [_P, _P, _P, C.POINTER(KrhMat), C.POINTER(KrhMat), C.POINTER(KrhMat), _P, _P, _P,
                               _P, _P, C.c_int, C.c_int, _P, _P, C.c_int, C.c_int]),
@@ -213,7 +214,7 @@ for name, res, args in [
     ("krh_rmsnorm_matvec_qkv_keep", None, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, C.c_float, _P, _P, C.c_int,
                                            _P, _P, _P, _P]),
     ("krh_softcap_rows", None, [_P, C.c_size_t, C.c_int, C.c_int, C.c_float]),
-    ("krh_set_int", None, [_P, C.c_int]), ("krh_transpose_scales", None, [_P, C.c_int, _P, C.c_int, C.c_int]),
+    ("krh_set_int", None, [_P, C.c_int]),
     ("krh_gen_blocks", None, [_P, _P, C.c_uint64, C.c_int, C.c_int, C.c_int, C.c_int, C.c_float]),
 ]:
     hip.declare(name, res, args)

@@ -57,8 +57,8 @@ static int g_nrg;
 static int *g_ints;                 /* device ints: [0] position, [1] token row, [2] zero */
 static int g_pos_set = -1;          /* the position g_ints[0] holds (-1: none yet) */
 static int g_row_set;               /* g_ints[1] holds 0 */
-static float *g_dT, *g_batt;        /* matmul scales, batched attention scratch */
-static size_t g_dT_n, g_batt_n;
+static float *g_batt;               /* batched attention scratch */
+static size_t g_batt_n;
 static const void *g_cls_q;         /* the classifier's quants (ml_model_pack) */
 static const ml_qtensor *g_emb;     /* the embedding table and its row scale (ml_model_pack) */
 static float g_emb_scale = 1.0f;
@@ -497,13 +497,13 @@ void ml_matvec(ml_pool *pool, float *y, const ml_qtensor *W, const ml_qact *x) {
 }
 
 /* Y[t * ldy + r] = W x_t (ops/ops.c:51-79): the MFMA matmul over the batch,
- * each token's row the matvec's bit for bit */
+ * each token's row the matvec's bit for bit, reading the batch's scales in
+ * their token rows */
 void ml_matmul(ml_pool *pool, float *Y, int ldy, const ml_qtensor *W, const ml_qbatch *X) {
     (void)pool;
     const int n = X->n, k = X->k, nb = k / QK, ldx = (n + 127) / 128 * 128;
     if (n <= 0 || !ready()) return;
     q_flush();
-    g_dT = grow(g_dT, &g_dT_n, F((size_t)nb * ldx));
     kh_call c = { 0 };
     krh_mat m;
     mat_of(&c, W, 0, W->rows, &m);
@@ -521,12 +521,9 @@ void ml_matmul(ml_pool *pool, float *Y, int ldy, const ml_qtensor *W, const ml_q
     const float *xd = arg(&c, X->d, F((size_t)n * nb), 1, 0);
     /* in and out: rows of Y are ldy apart and the gaps are the caller's */
     float *yd = arg(&c, Y, F((size_t)(n - 1) * ldy + W->rows), 1, 1);
-    if (!c.fail && g_dT) {
-        krh_transpose_scales(g_dT, ldx, xd, n, nb);
-        krh_matmul(yd, ldy, &m, xq, g_dT, ldx, n, 0);
-    }
+    if (!c.fail) krh_matmul_rows(yd, ldy, &m, xq, xd, ldx, n, 0);
     done(&c);
-    if (c.fail || !g_dT) fail_call("cannot stage a buffer");
+    if (c.fail) fail_call("cannot stage a buffer");
 }
 
 void ml_quantize_row(int8_t *q, float *d, const float *x, int n) {

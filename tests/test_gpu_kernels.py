@@ -515,11 +515,17 @@ def test_matmul(dev, typ, d16, rows, cols, T):
                          dev.put(transposed_scales(xd, T, cols // 32, ldx)).ptr, ldx, T, acc)
         ok()
         got = yb.get(np.float32, T * rows).reshape(T, rows)
+        # the same product over the scales in token rows, sized exactly [T][nb]
+        yr = dev.put(y0)
+        K.hip.krh_matmul_rows(yr.ptr, rows, C.byref(W), dev.put(xq).ptr, dev.put(xd).ptr, ldx, T, acc)
+        ok()
+        got_rows = yr.get(np.float32, T * rows).reshape(T, rows)
         for t in range(T):
             want = oracle_matvec(q, d, rows, cols, typ, xq[t], xd[t])
             if acc:
                 want = (y0[t] + want).astype(np.float32)
             assert np.array_equal(bits(got[t]), bits(want)), (t, acc)
+            assert np.array_equal(bits(got_rows[t]), bits(want)), (t, acc, "rows")
 
 
 @pytest.mark.parametrize("dim,nh,nkv,hd,typ,vtyp,bias", [(288, 6, 6, 48, K.ML_Q8_0, K.ML_Q8_0, 0),
