@@ -8,8 +8,11 @@
  *                      model/transformer.c:163) uploads the arenas, after the
  *                      host has written the RoPE tables into them
  *   model/pack_model.c ml_model_pack*: uploads the mapped model file
- *   core/quant_ref.c   ml_dequant_row (device gather into the arena),
- *                      ml_quantize_row_q4 (host)
+ *   core/quant_ref.c   ml_dequant_row: a device gather when the output row
+ *                      has an HBM copy; host buffers go to the reference's
+ *                      own core/quant_ref.c, compiled beside this file with
+ *                      that one function renamed ml_dequant_row_host (its
+ *                      ml_quantize_row_q4 is used unchanged)
  *   core/isa_check.c   ml_isa_check: a gfx950 device or ML_E_ISA (exit 3)
  *   ops/ops.c          ml_matvec, ml_matmul (int8 MFMA), ml_attention(_batch),
  *                      ml_quantize_row, ml_softcap_rows
@@ -42,6 +45,9 @@
 #define KRAFLA_TYPES_H   /* the types come from the reference's core/ml.h */
 #include "krafla_hip.h"
 
+/* core/quant_ref.c's ml_dequant_row, compiled under this name */
+void ml_dequant_row_host(float *out, const ml_qtensor *W, int row);
+
 /* ---- address ranges with an HBM copy ---- */
 
 typedef struct {
@@ -59,9 +65,17 @@ static int g_pos_set = -1;          /* the position g_ints[0] holds (-1: none ye
 static int g_row_set;               /* g_ints[1] holds 0 */
 static float *g_batt;               /* batched attention scratch */
 static size_t g_batt_n;
-static const void *g_cls_q;         /* the classifier's quants (ml_model_pack) */
-static const ml_qtensor *g_emb;     /* the embedding table and its row scale (ml_model_pack) */
-static float g_emb_scale = 1.0f;
+/* each packed model's embedding table, its row scale and its classifier's
+ * quants (ml_model_pack): the scale applies to that model's rows only, and
+ * its classifier's products are not queued (the host reads the logits) */
+typedef struct {
+    const ml_qtensor *emb;
+    float emb_scale;
+    const void *cls_q;
+} kh_packed;
+#define KH_MODELS 16
+static kh_packed g_pk[KH_MODELS];
+static int g_npk;
 static int g_reported;
 
 static int ready(void) {
@@ -286,10 +300,25 @@ ml_status ml_model_pack(ml_model *m, ml_pool *pool) {
     } else if (krh_copy_h2d(d, h, n) != ML_OK) {   /* the same address may be a new file */
         return ML_E_IO;
     }
-    g_cls_q = m->wcls.q;
-    g_emb = &m->tok_emb;
-    g_emb_scale = m->cfg.embed_scale;
+    int k = 0;
+    while (k < g_npk && g_pk[k].emb != &m->tok_emb) k++;
+    if (k == KH_MODELS) return ML_E_NOMEM;
+    if (k == g_npk) g_npk++;
+    g_pk[k] = (kh_packed){ &m->tok_emb, m->cfg.embed_scale, m->wcls.q };
     return ML_OK;
+}
+
+/* the embedding scale of the packed model whose table W is (1 otherwise) */
+static float emb_scale_of(const ml_qtensor *W) {
+    for (int k = 0; k < g_npk; k++)
+        if (g_pk[k].emb == W) return g_pk[k].emb_scale;
+    return 1.0f;
+}
+
+static int is_classifier(const void *q) {
+    for (int k = 0; k < g_npk; k++)
+        if (g_pk[k].cls_q == q) return 1;
+    return 0;
 }
 
 ml_status ml_model_pack_cached(ml_model *m, ml_pool *pool, const char *path, const char **how) {
@@ -314,45 +343,12 @@ void ml_dequant_row(float *out, const ml_qtensor *W, int row) {
                 krh_set_int(g_ints + 1, 0);
                 g_row_set = 1;
             }
-            krh_embed(o, &m, g_ints + 1, W == g_emb ? g_emb_scale : 1.0f);
+            krh_embed(o, &m, g_ints + 1, emb_scale_of(W));
         }
         done(&c);
         return;
     }
-    /* a host buffer: the scalar rule (core/quant_ref.c:4-19) */
-    const int nb = W->cols / QK;
-    const float *d = W->d + (size_t)row * nb;
-    if (W->type == ML_Q8_0) {
-        const int8_t *q = W->q + (size_t)row * W->cols;
-        for (int i = 0; i < W->cols; i++) out[i] = q[i] * d[i / QK];
-        return;
-    }
-    const uint8_t *q = (const uint8_t *)W->q + (size_t)row * nb * (QK / 2);
-    for (int b = 0; b < nb; b++)
-        for (int j = 0; j < QK / 2; j++) {
-            const uint8_t v = q[b * (QK / 2) + j];
-            out[b * QK + j] = ((v & 0xF) - 8) * d[b];
-            out[b * QK + j + QK / 2] = ((v >> 4) - 8) * d[b];
-        }
-}
-
-/* host only (load-time and tools), the amax / 7 rule (core/quant_ref.c:21-38) */
-void ml_quantize_row_q4(int8_t *q, float *d, const float *x, int k) {
-    for (int b = 0; b < k / QK; b++) {
-        const float *xb = x + b * QK;
-        float amax = 0.0f;
-        for (int j = 0; j < QK; j++) amax = fmaxf(amax, fabsf(xb[j]));
-        if (amax < ML_QUANT_TINY) amax = 0.0f;
-        const float id = amax != 0.0f ? 7.0f / amax : 0.0f;
-        d[b] = amax / 7.0f;
-        uint8_t nib[QK];
-        for (int j = 0; j < QK; j++) {
-            float v = truncf(xb[j] * id + copysignf(0.5f, xb[j]));
-            v = fminf(fmaxf(v, -8.0f), 7.0f);
-            nib[j] = (uint8_t)((int)v + 8);
-        }
-        for (int j = 0; j < QK / 2; j++) q[b * (QK / 2) + j] = (int8_t)(nib[j] | (nib[j + QK / 2] << 4));
-    }
+    ml_dequant_row_host(out, W, row);   /* a host buffer: the reference's own rule */
 }
 
 /* ---- kernels/hip ---- */
@@ -362,7 +358,7 @@ void ml_quantize_row_q4(int8_t *q, float *d, const float *x, int k) {
 /* a product on arena buffers into the queue (not the classifier's: the host
  * reads the logits next) */
 static int queue_matvec(float *y, const ml_qtensor *W, const ml_qact *x, int r0, int r1) {
-    if (W->q == g_cls_q) return 0;
+    if (is_classifier(W->q)) return 0;
     const size_t nb = (size_t)W->cols / QK, rowq = W->type == ML_Q8_0 ? (size_t)W->cols : (size_t)W->cols / 2;
     const size_t nr = (size_t)(r1 - r0);
     const void *h[] = { y + r0, x->q, x->d, (const uint8_t *)W->q + (size_t)r0 * rowq,
@@ -384,7 +380,7 @@ static void matvec_rows(float *y, const ml_qtensor *W, const ml_qact *x, int r0,
     const float *xd = arg(&c, x->d, F(W->cols / QK), 1, 0);
     float *yd = arg(&c, y + r0, F(r1 - r0), 0, 1);
     if (!c.fail) krh_matvec(yd, &m, xq, xd, 0);
-    if (W->q == g_cls_q && !c.staged && yd && yd != (void *)(y + r0)) {
+    if (is_classifier(W->q) && !c.staged && yd && yd != (void *)(y + r0)) {
         /* the logits: the host reads them next (app/ml_run.c:388-392) */
         if (krh_copy_d2h(y + r0, yd, F(r1 - r0)) != ML_OK || krh_status() != ML_OK) {
             fail_call(krh_last_error());

@@ -163,14 +163,14 @@ def test_workload_matches_reference(name):
         shutil.rmtree(tmp, ignore_errors=True)
 
 
-@pytest.mark.parametrize("name", ["qwen05b_mixed", "llama1b_mixed"])
+@pytest.mark.parametrize("name", ["qwen05b_mixed", "llama1b_mixed", "llama8b_q8"])
 def test_route_workload_matches_reference(name):
     """the reference's own ml_run over this backend's op table
     (oracle/_ref/hip/ml_run: model/transformer.c and app/ml_run.c unchanged,
-    the per-token op queue batching and fusing their calls) on the full-size
-    model: the greedy ids the scalar build printed, and for the 0.5B shape
-    every teacher-forced position's --dump-logits row against the fixture's
-    hashes"""
+    built with 2048-token prefill steps, the per-token op queue batching and
+    fusing their calls) on the full-size model: the greedy ids the scalar
+    build printed, and for the 0.5B shape every teacher-forced position's
+    --dump-logits row against the fixture's hashes"""
     exe = os.path.join(O.REF_DIR, "hip", "ml_run")
     if not os.path.exists(exe):
         pytest.skip("oracle/_ref/hip not built (needs the reference sources at build time)")

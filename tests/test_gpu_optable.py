@@ -74,9 +74,10 @@ def test_ml_run_dump_logits(name, batch, workdir):
 
 def test_ml_bench_kernel_table():
     """ml_bench (no model) runs its kernel table on the hip kernels, staged
-    from host buffers"""
+    from host buffers (the build with the reference's default 128-token
+    batches, app/ml_bench.c:53-54)"""
     import subprocess
-    r = subprocess.run([os.path.join(O.REF_DIR, "hip", "ml_bench")], capture_output=True, text=True, timeout=600)
+    r = subprocess.run([os.path.join(O.REF_DIR, "hip128", "ml_bench")], capture_output=True, text=True, timeout=600)
     assert r.returncode == 0, r.stderr
     assert "ISA: hip" in r.stdout and "matvec_q8 -> ml_k_matvec_q8_hip" in r.stdout
 
@@ -112,22 +113,39 @@ def test_ml_run_kv_f16_refused(workdir):
     assert "F16 KV cache" in r.stderr
 
 
+@pytest.mark.parametrize("build", ["hip", "hip128"])
 @pytest.mark.parametrize("name", ["qk_norm_q4mix", "post_norm_gelu_window", "softcap_embed_scale",
                                   "llama3_rope_gqa_q4", "c1_q8"])
-def test_ml_run_long_prompt(name, workdir):
-    """A prompt over several batched prefill steps (128 tokens each,
-    model/transformer.h:48): the binding replays each step's per-token op
-    loops as row-batched launches; the --dump-logits bytes and the greedy ids
-    that follow match the scalar build's"""
+def test_ml_run_long_prompt(name, build, workdir):
+    """A prompt of up to 300 tokens: in one batched prefill step (hip:
+    ML_BATCH_MAX 2048), or over several of the reference's default 128-token
+    steps (hip128, model/transformer.h:48); the binding replays each step's
+    per-token op loops as row-batched launches; the --dump-logits bytes and
+    the greedy ids that follow match the scalar build's"""
     path = model(name, workdir)
     V, S = MODELS[name]["vocab"], MODELS[name]["max_seq"]
     n = min(300, S - 40)
     toks = [int(t) for t in np.random.default_rng(5).integers(1, V, n)]
-    a, b = path + ".scalar.long.logits", path + ".hip.long.logits"
+    a, b = path + ".scalar.long.logits", path + "." + build + ".long.logits"
     O.ref_ml_run(path, toks, n, dump=a)
-    O.ref_ml_run(path, toks, n, dump=b, isa="hip")
+    O.ref_ml_run(path, toks, n, dump=b, isa=build)
     x, y = np.fromfile(a, dtype=np.uint8), np.fromfile(b, dtype=np.uint8)
     assert x.size == n * V * 4 and np.array_equal(x, y)
     want, _ = O.ref_ml_run(path, toks, n + 32)
-    got, _ = O.ref_ml_run(path, toks, n + 32, isa="hip")
+    got, _ = O.ref_ml_run(path, toks, n + 32, isa=build)
     assert np.array_equal(got, want)
+
+
+def test_ml_run_batch_option(workdir):
+    """--batch up to the build's ML_BATCH_MAX (app/ml_run.c:274): the 2048
+    build takes --batch 2048 and 200, the 128 build refuses 129"""
+    import subprocess
+    path = model("qwen_like_q4mix", workdir)
+    toks = [int(t) for t in np.random.default_rng(6).integers(1, 512, 150)]
+    want, _ = O.ref_ml_run(path, toks, 158)
+    for b in ("2048", "200", "7"):
+        got, _ = O.ref_ml_run(path, toks, 158, isa="hip", extra=["--batch", b])
+        assert np.array_equal(got, want), b
+    r = subprocess.run([os.path.join(O.REF_DIR, "hip128", "ml_run"), path, "--tokens", "1,2", "-n", "3",
+                        "--batch", "129"], capture_output=True, text=True, timeout=300)
+    assert r.returncode != 0 and "--batch" in r.stderr
