@@ -56,12 +56,24 @@ struct MvArgs {
     float *keep_xb;
     int8_t *keep_xq;
     float *keep_xd;
+    int touch;           // touches ahead (set by launch_mv: every matrix below 4 GiB)
 };
 
 constexpr int MV_THREADS = 256;
 constexpr int MV_NPT = 2;   // weight blocks per thread per work item
 constexpr int MV_DEPTH = 2;    // work items in flight per wave: a wave that issues more loads than the
                                // memory pipeline holds stalls at issue
+#ifndef KR_MV_TOUCH
+#define KR_MV_TOUCH 2
+#endif
+// Items a wave touches ahead (the item MV_TOUCH after the one whose dots run;
+// 1: none): a 2-byte read per 128-byte line of an item's quants and per row
+// of its scales, so that the lines are in this XCD's L2 (and the Infinity
+// Cache) when the item's own loads go out, above all under a prologue, when
+// the register-loaded item is the only other memory traffic. 2 or 4; 4
+// (three items touched) was slower: a wave's loads return in order, so the
+// item loads wait behind touches further out.
+constexpr int MV_TOUCH = KR_MV_TOUCH;
 // Activations held in registers by the prologue (longer ones are staged
 // through LDS from memory): sized so that the kernel fits 128 VGPRs, four
 // workgroups per CU
@@ -118,6 +130,32 @@ __device__ __forceinline__ void kr_quant4(float4 v, int i, int8_t *q, float *d, 
     }
     *(int *)(q + i) = packed;
     if ((i & 31) == 0) d[(size_t)(i >> 5) * dstep] = dd;
+}
+
+// Q8_0 of the 16 values v = x[i..i+15] held by this lane (k_scalar.c:39-57):
+// a 32-block is two lanes' halves, lanes 2j and 2j + 1 (both must call
+// together; i % 32 == 16 in the odd one). The block max is exact in any
+// order; the two divisions are paid once per 16 values instead of per 4.
+// q[i..i+15] receive the values, d[i / 32] the scale.
+__device__ __forceinline__ void kr_quant16(const float4 (&v)[4], int i, int8_t *q, float *d) {
+    float m = 0.0f;   // seeded with 0 as the reference's loop is: NaNs never raise the max
+#pragma unroll
+    for (int k = 0; k < 4; k++)
+        m = fmaxf(fmaxf(m, fmaxf(fabsf(v[k].x), fabsf(v[k].y))), fmaxf(fabsf(v[k].z), fabsf(v[k].w)));
+    m = fmaxf(m, __uint_as_float((unsigned)__builtin_amdgcn_mov_dpp((int)__float_as_uint(m), 0xB1, 0xF, 0xF, false)));
+    int4 packed = make_int4(0, 0, 0, 0);
+    float dd = 0.0f;
+    if (!(m < KR_QUANT_TINY)) {
+        const float id = kr_fdiv(127.0f, m);
+        dd = kr_fdiv(m, 127.0f);
+        auto p4 = [&](float4 x) {
+            return (kr_q8_elem(x.x, id) & 0xff) | (kr_q8_elem(x.y, id) & 0xff) << 8 |
+                   (kr_q8_elem(x.z, id) & 0xff) << 16 | (int)((unsigned)kr_q8_elem(x.w, id) << 24);
+        };
+        packed = make_int4(p4(v[0]), p4(v[1]), p4(v[2]), p4(v[3]));
+    }
+    *(int4 *)(q + i) = packed;
+    if ((i & 31) == 0) d[i >> 5] = dd;
 }
 
 // the rmsnorm output (x * inv) * w (k_scalar.c:63)
@@ -264,6 +302,30 @@ __device__ __forceinline__ void mv_load(MvSlots &S, const MvArgs &a, const MvIte
     }
 }
 
+// One dword per lane from one of the item's lines (a touch: the value is not
+// used): lanes l < n / 4 read local block 4 l (a 128-byte line of Q8_0 quants,
+// half of one of Q4_0), the next lanes the first and the middle scale of each
+// local row. The local blocks map to rows and blocks as in mv_load. Offsets
+// are 32-bit: the launcher sets touch only when every matrix's quants and
+// scales stay below 4 GiB.
+// (a 2-byte read of the block's first quants or of the scale itself)
+template <int EPI, int QT, int D16>
+__device__ __forceinline__ int mv_touch(const MvArgs &a, const MvItem &it, int nb, int lane) {
+    const KMat W = pick3(it.mi, a.m[0], a.m[1], a.m[2]);
+    const KMat W2 = a.m[1];
+    const int n = max(it.nloc * it.nbc, 1), nql = (n + 3) >> 2;
+    const bool scale = lane >= nql;
+    const int sl = lane - nql;
+    int j = scale ? min(sl >> 1, max(it.nloc, 1) - 1) * it.nbc + (sl & 1) * (it.nbc >> 1) : 4 * lane;
+    j = min(j, n - 1);
+    const int lr = j / it.nbc, b = j - lr * it.nbc;
+    const bool second = EPI == EPI_SWIGLU && lr >= it.nr;
+    const unsigned blk = (unsigned)(it.row0 + (second ? lr - it.nr : lr)) * (unsigned)nb + (unsigned)(it.c0 + b);
+    const uint8_t *base = scale ? (const uint8_t *)(second ? W2.d : W.d) : (second ? W2.q : W.q);
+    const unsigned off = scale ? blk * (D16 ? 2u : 4u) : blk * (QT == ML_Q8_0 ? 32u : 16u);
+    return *(const uint16_t *)(base + off);   // 2 bytes: in bounds for every block and scale
+}
+
 // LDS layout of k_matvec (byte offsets, every region 16-byte aligned): the
 // Q8_0 activation and its scales, each wave's chunk terms (rows of ts floats:
 // a multiple of 4 plus 4, for 16-byte reads with a 4-bank shift between
@@ -301,12 +363,17 @@ __host__ __device__ inline MvLds mv_lds(int K, int maxloc, int nbc, bool norm) {
 // dots the workgroup stages the activation into LDS (while the first loads
 // are in flight): copied, quantized, or normalized first (rmsnorm's ordered
 // sum, k_scalar.c:59-64) and quantized.
-// workgroups of a launch resident on one CU: four (128 VGPRs, four waves a
-// SIMD), three for q|k|v, whose RoPE epilogue then keeps its state in
-// registers (at 128 the Q8 form spilled 16 bytes, reloaded in every step:
-// 8B decode 308.2 -> 309.7 tok/s without the spill). The q|k|v grid of the
-// 8B shape is 768 workgroups in any case (3,072 two-row tiles).
-constexpr int mv_wgs_per_cu(int epi) { return epi == EPI_QKV ? 3 : 4; }
+// workgroups of a launch resident on one CU: three (up to 168 VGPRs, three
+// waves a SIMD). With the prologue's Q8_0 in half-blocks per lane and one
+// item touched ahead, the 8B decode ran at 316.0 tok/s with four (128
+// VGPRs) and 319.3 with three; with the 4-value quantization and no
+// touches, four had been ahead (307.5 against 310.9 with three and
+// touches). The q|k|v grid of the 8B shape is 768 workgroups in any case
+// (3,072 two-row tiles).
+#ifndef KR_MV_WGS
+#define KR_MV_WGS 3
+#endif
+constexpr int mv_wgs_per_cu(int epi) { return epi == EPI_QKV ? 3 : KR_MV_WGS; }
 
 template <int EPI, int QT, int D16>
 __global__ void __launch_bounds__(MV_THREADS, mv_wgs_per_cu(EPI)) k_matvec(const MvArgs a) {
@@ -343,6 +410,24 @@ __global__ void __launch_bounds__(MV_THREADS, mv_wgs_per_cu(EPI)) k_matvec(const
     };
     MvSlots S[MV_DEPTH];
     MvItem I[MV_DEPTH];
+    // touches: item i + MV_TOUCH is touched in item i's step, into slot
+    // i % MV_TOUCH, whose value (item i's touch, older than item i's own
+    // loads, so already back when item i's dots have run) is folded into sink
+    // first; the prologue touches items 1 .. MV_TOUCH - 1
+    int tv[MV_TOUCH > 1 ? MV_TOUCH : 1] = {};
+    int sink = 0, ttile = gw, tchunk = 0;
+    auto touch_item = [&]() -> int {
+        MvItem it = mv_item<EPI>(a, min(ttile, ntiles - 1), ttile < ntiles ? tchunk : 0, nb);
+        next_item(ttile, tchunk);
+        return a.touch ? mv_touch<EPI, QT, D16>(a, it, nb, lane) : 0;
+    };
+    auto prime_touch = [&]() {
+        if (MV_TOUCH > 1) {
+            next_item(ttile, tchunk);
+#pragma unroll
+            for (int t = 1; t < MV_TOUCH; t++) tv[t] = touch_item();
+        }
+    };
     if (a.xq && K <= MV_XQ_MAX) {
         // a quantized activation (just written by the previous launch, so
         // not yet in this die's L2): it is read and stored to LDS before the
@@ -362,29 +447,30 @@ __global__ void __launch_bounds__(MV_THREADS, mv_wgs_per_cu(EPI)) k_matvec(const
             if (tid + k * MV_THREADS < nb) xds[tid + k * MV_THREADS] = xdv[k];
 #pragma unroll
         for (int d = 0; d < MV_DEPTH - 1; d++) load_item(S[d], I[d]);
+        prime_touch();
     } else if (!a.xq && !a.nw && K <= MV_XF_PLAIN_MAX) {
         // a float activation without a norm (ao before wo, h before w2), in
         // passes of MV_XF_PASS floats held in registers: the first pass's
         // loads go out first, then the first item's weight loads, and the
         // first quantization waits on the activation alone; later passes
         // (h of more than MV_XF_PASS) follow
-        constexpr int XV = MV_XF_PASS / 4 / MV_THREADS;
-        float4 xv[XV];
+        // thread t takes the 16 values base + 16 t .. + 15, half of a
+        // 32-block (kr_quant16)
+        static_assert(MV_XF_PASS == 16 * MV_THREADS, "a pass is one half-block per thread");
+        float4 xv[4];
         auto pass_load = [&](int base) {
+            const int i = min(base + 16 * tid, K - 16);
 #pragma unroll
-            for (int k = 0; k < XV; k++)
-                xv[k] = *(const float4 *)(a.xf + min(base + 4 * (k * MV_THREADS + tid), K - 4));
+            for (int k = 0; k < 4; k++) xv[k] = *(const float4 *)(a.xf + i + 4 * k);
         };
         auto pass_quant = [&](int base) {
-#pragma unroll
-            for (int k = 0; k < XV; k++) {
-                const int i = base + 4 * (k * MV_THREADS + tid);   // K % 32 == 0: 8-lane groups all in or all out
-                if (i < K) kr_quant4(xv[k], i, xs, xds, 1);
-            }
+            const int i = base + 16 * tid;   // K % 32 == 0: both halves of a block are in or out
+            if (i < K) kr_quant16(xv, i, xs, xds);
         };
         pass_load(0);
 #pragma unroll
         for (int d = 0; d < MV_DEPTH - 1; d++) load_item(S[d], I[d]);
+        prime_touch();
         pass_quant(0);
         for (int base = MV_XF_PASS; base < K; base += MV_XF_PASS) {
             pass_load(base);
@@ -394,49 +480,59 @@ __global__ void __launch_bounds__(MV_THREADS, mv_wgs_per_cu(EPI)) k_matvec(const
         // a float activation (normalized first when nw is set), held in
         // registers: its loads go out before the weight loads; the squares
         // and the quantization read the registers
-        constexpr int XV = MV_XF_MAX / 4 / MV_THREADS;
+        // thread t holds the 16 values 16 t .. 16 t + 15 (half of a
+        // 32-block, kr_quant16) and their norm weights
+        static_assert(MV_XF_MAX == 16 * MV_THREADS, "one half-block per thread");
+        constexpr int XV = 4;
         float4 xv[XV], wv[XV];
+        const int i0 = 16 * tid;
+        const bool live = i0 < K;   // K % 32 == 0: both halves of a block are live or not
+        {
+            const int i = min(i0, K - 16);
 #pragma unroll
-        for (int k = 0; k < XV; k++) {
-            const int i = min(4 * (k * MV_THREADS + tid), K - 4);
-            xv[k] = *(const float4 *)(a.xf + i);
-            if (a.nw) wv[k] = *(const float4 *)(a.nw + i);
+            for (int k = 0; k < XV; k++) {
+                xv[k] = *(const float4 *)(a.xf + i + 4 * k);
+                if (a.nw) wv[k] = *(const float4 *)(a.nw + i + 4 * k);
+            }
         }
         float inv = 1.0f;
         if (a.nw) {
             // the squares wait on x alone; the weight stream then runs under
             // the ordered sum
             const int sh = sc_log_len(K);
+            if (live) {
 #pragma unroll
-            for (int k = 0; k < XV; k++) {
-                const int i = 4 * (k * MV_THREADS + tid);
-                if (i < K)
-                    *(float4 *)(sq + sc_at(i, sh)) = make_float4(kr_fmul(xv[k].x, xv[k].x), kr_fmul(xv[k].y, xv[k].y),
-                                                      kr_fmul(xv[k].z, xv[k].z), kr_fmul(xv[k].w, xv[k].w));
+                for (int k = 0; k < XV; k++)   // 16 | chunk length: the 16 terms are contiguous in sq
+                    *(float4 *)(sq + sc_at(i0, sh) + 4 * k) =
+                        make_float4(kr_fmul(xv[k].x, xv[k].x), kr_fmul(xv[k].y, xv[k].y), kr_fmul(xv[k].z, xv[k].z),
+                                    kr_fmul(xv[k].w, xv[k].w));
             }
 #pragma unroll
             for (int d = 0; d < MV_DEPTH - 1; d++) load_item(S[d], I[d]);
+            prime_touch();
             __syncthreads();
             const float ss = kr_spec_sum<MV_THREADS>(sq, K, (unsigned char *)(sq + sc_terms_cap(K)));
             inv = kr_fdiv(1.0f, kr_fsqrt(kr_fadd(kr_fdiv(ss, (float)K), a.eps)));
         }
-        const bool kxb = a.keep_xb && blockIdx.x == 0;
+        if (live) {
+            float4 o[XV];
 #pragma unroll
-        for (int k = 0; k < XV; k++) {
-            const int i = 4 * (k * MV_THREADS + tid);   // K % 32 == 0: 8-lane groups all in or all out
-            if (i < K) {
-                const float4 o = a.nw ? kr_norm4(xv[k], inv, wv[k]) : xv[k];
-                kr_quant4(o, i, xs, xds, 1);
-                if (kxb) *(float4 *)(a.keep_xb + i) = o;
+            for (int k = 0; k < XV; k++) o[k] = a.nw ? kr_norm4(xv[k], inv, wv[k]) : xv[k];
+            kr_quant16(o, i0, xs, xds);
+            if (a.keep_xb && blockIdx.x == 0) {
+#pragma unroll
+                for (int k = 0; k < XV; k++) *(float4 *)(a.keep_xb + i0 + 4 * k) = o[k];
             }
         }
         if (!a.nw) {
 #pragma unroll
             for (int d = 0; d < MV_DEPTH - 1; d++) load_item(S[d], I[d]);
+            prime_touch();
         }
     } else {
 #pragma unroll
         for (int d = 0; d < MV_DEPTH - 1; d++) load_item(S[d], I[d]);
+        prime_touch();
         if (a.xq) {
             for (int i = tid; i < K / 16; i += MV_THREADS) ((int4 *)xs)[i] = ((const int4 *)a.xq)[i];
             for (int i = tid; i < nb; i += MV_THREADS) xds[i] = a.xd[i];
@@ -461,9 +557,10 @@ __global__ void __launch_bounds__(MV_THREADS, mv_wgs_per_cu(EPI)) k_matvec(const
     }
 
     float acc = 0.0f;   // row sum of lane < nloc
-    // one item: S[P] holds it; S[P - 1] receives the loads MV_DEPTH - 1 ahead
-    auto step = [&](auto P_) -> bool {
-        constexpr int P = decltype(P_)::value;
+    // one item (step P4 of an unrolled group of 2 or 4): S[P4 % MV_DEPTH] holds it;
+    // the slot before receives the loads MV_DEPTH - 1 ahead
+    auto step = [&](auto P4_) -> bool {
+        constexpr int P4 = decltype(P4_)::value, P = P4 % MV_DEPTH;
         const MvItem cur = I[P];
         load_item(S[(P + MV_DEPTH - 1) % MV_DEPTH], I[(P + MV_DEPTH - 1) % MV_DEPTH]);
         int ntile = tile, nchunk = chunk;
@@ -501,6 +598,11 @@ __global__ void __launch_bounds__(MV_THREADS, mv_wgs_per_cu(EPI)) k_matvec(const
                 lr += sr;
                 if (b >= cur.nbc) { b -= cur.nbc; lr++; }
             }
+        }
+        if (MV_TOUCH > 1) {
+            constexpr int TS = P4 % (MV_TOUCH > 1 ? MV_TOUCH : 1);
+            sink ^= tv[TS];
+            tv[TS] = touch_item();
         }
         kr_wave_sync();
         if (lane < cur.nloc) {
@@ -571,25 +673,27 @@ __global__ void __launch_bounds__(MV_THREADS, mv_wgs_per_cu(EPI)) k_matvec(const
         chunk = nchunk;
         return tile < ntiles;
     };
-    static_assert(MV_DEPTH == 2 || MV_DEPTH == 4, "the step loop is unrolled by 2 or 4");
+    static_assert(MV_DEPTH == 2, "the step loop is unrolled by 2 or 4");
+    static_assert(MV_TOUCH == 1 || MV_TOUCH == 2 || MV_TOUCH == 4, "touch slots divide the unrolled 4");
     if (gw >= ntiles) return;   // a wave with no tile (after the workgroup's one barrier)
-    if (MV_DEPTH == 2) {
-        while (step(std::integral_constant<int, 0>()) && step(std::integral_constant<int, 1>() )) {
+    if (MV_TOUCH == 4) {
+        while (step(std::integral_constant<int, 0>()) && step(std::integral_constant<int, 1>()) &&
+               step(std::integral_constant<int, 2>()) && step(std::integral_constant<int, 3>())) {
         }
     } else {
-        while (step(std::integral_constant<int, 0>()) && step(std::integral_constant<int, 1 % MV_DEPTH>()) &&
-               step(std::integral_constant<int, 2 % MV_DEPTH>()) && step(std::integral_constant<int, 3 % MV_DEPTH>())) {
+        while (step(std::integral_constant<int, 0>()) && step(std::integral_constant<int, 1>())) {
         }
+    }
+    if (MV_TOUCH > 1) {
+        // keeps the touches (their values are never otherwise used)
+#pragma unroll
+        for (int t = 0; t < MV_TOUCH; t++) sink ^= tv[t];
+        if (sink == 0x5bd1e995 && K < 0) a.y[0][0] = 0.0f;
     }
 }
 
-// workgroups resident at once: four per compute unit of this device (1024
-// on an MI355X's 256 CUs; the kernel fits 128 VGPRs, four waves a SIMD),
-// three for q|k|v.
-// The 8B decode streamed at 274.9 tok/s with two a CU (4 blocks per lane
-// and item, 166 VGPRs), 282.5 with three, 284.1 with four (2 blocks per lane
-// and item, the activations of up to 4096 held in registers): more waves to
-// cover each other's ordered sums and loads
+// workgroups resident at once: mv_wgs_per_cu per compute unit of this
+// device (768 on an MI355X's 256 CUs)
 int mv_resident(int epi = EPI_STORE) { return mv_wgs_per_cu(epi) * (krh_device_cus() > 0 ? krh_device_cus() : 256); }
 
 // Rows per tile (one wave's): the largest power of two (at most cap, even for
@@ -619,6 +723,9 @@ void launch_mv(MvArgs &a, const KMat &W) {
     const int nb = a.K / KR_QK;
     const int nloc = EPI == EPI_SWIGLU ? 2 * a.R : a.R;
     a.nbc = mv_chunk(nb, nloc);
+    a.touch = 1;
+    for (int i = 0; i < a.nmat; i++)
+        if ((size_t)a.m[i].rows * (size_t)a.K >= ((size_t)1 << 32) / 32 * 32) a.touch = 0;
     const size_t lds = mv_lds(a.K, nloc, a.nbc, a.nw != nullptr).total;
     const int ntiles = a.tile0[a.nmat];
     const int wgs = (ntiles + MV_WAVES - 1) / MV_WAVES;
