@@ -201,7 +201,12 @@ def committed_traffic():
 
 
 def matvec_microbench(K, iters=1000):
-    """GB/s of the plain matvec on the isolated shapes, resident and rotating"""
+    """GB/s of the plain matvec on the isolated shapes, resident and rotating:
+    the 1000 launches captured as one graph and replayed (the host issues
+    one graph launch, so the figure is the device's launches back to back,
+    each graph kernel node's own dispatch cost included), and the same
+    launches issued eagerly one by one from the host (eager_*: the host's
+    issue rate included)"""
     out = []
     x = np.empty(4096, dtype=np.float32)
     K.host.kr_gen_normal(x.ctypes.data, 4096, 9)
@@ -233,11 +238,26 @@ def matvec_microbench(K, iters=1000):
                     K.hip.krh_matvec(yb.ptr, C.byref(w), xq.ptr, xdb.ptr, 0)
                 K.hip.krh_timer_mark(t, 1)
                 ms = K.hip.krh_timer_ms(t)
+                res["eager_" + mode] = round(nbytes * iters / (ms * 1e-3) / 1e9, 1)
+                g = C.c_void_p()
+                K.check(K.hip.krh_graph_begin(), "graph capture")
+                for w in seq:
+                    K.hip.krh_matvec(yb.ptr, C.byref(w), xq.ptr, xdb.ptr, 0)
+                K.check(K.hip.krh_graph_end(C.byref(g)), "graph capture")
+                K.check(K.hip.krh_graph_launch(g), "graph launch")   # warm: the graph's first replay uploads it
+                K.hip.krh_timer_mark(t, 0)
+                K.check(K.hip.krh_graph_launch(g), "graph launch")
+                K.hip.krh_timer_mark(t, 1)
+                ms = K.hip.krh_timer_ms(t)
+                K.hip.krh_graph_free(g)
                 res[mode] = round(nbytes * iters / (ms * 1e-3) / 1e9, 1)
+                res[mode + "_us"] = round(ms * 1e3 / iters, 3)
             K.check(K.hip.krh_sync(), "matvec microbench")
             out.append({"shape": "%s %dx%d f16" % (tname, rows, cols), "bytes": nbytes,
                         "gbs_resident": res["resident"], "gbs_hbm_rotating": res["rotating"],
-                        "frac_hbm_rotating": round(res["rotating"] / HBM_PEAK_GBS, 3)})
+                        "us_per_launch_resident": res["resident_us"], "us_per_launch_rotating": res["rotating_us"],
+                        "frac_hbm_rotating": round(res["rotating"] / HBM_PEAK_GBS, 3),
+                        "eager_gbs_resident": res["eager_resident"], "eager_gbs_hbm_rotating": res["eager_rotating"]})
             for bq, bd in bufs:
                 bq.free()
                 bd.free()

@@ -372,6 +372,9 @@ void krh_block_dots(int32_t *s, const krh_mat *W, const int8_t *xq);
  * No counterpart in the reference: a self-check of the kernels' summation. */
 enum { KRH_ORDERED_SUM_MAX = 8192 };
 void krh_ordered_sum(float *out, const float *t, int n, float s0);
+/* The same computed by a workgroup of 1024 threads (the decode softmax's),
+ * n in [1, KRH_ORDERED_SUM_MAX]. */
+void krh_ordered_sum_1024(float *out, const float *t, int n, float s0);
 /* The same computed by one wave alone (the batched softmax's single-wave
  * mode), n in [1, KRH_ORDERED_SUM_WAVE_MAX]. */
 enum { KRH_ORDERED_SUM_WAVE_MAX = 4096 };

@@ -915,6 +915,14 @@ __global__ void __launch_bounds__(256) k_ordered_sum(float *out, const float *t,
     const float s = kr_spec_sum<256>(os_t, n, (unsigned char *)(os_t + sc_terms_cap(n)), s0);
     if (threadIdx.x == 0) *out = s;
 }
+// the same by 1024 threads, the decode softmax's workgroup
+__global__ void __launch_bounds__(1024) k_ordered_sum_1024(float *out, const float *t, int n, float s0) {
+    extern __shared__ __align__(16) float osk_t[];
+    for (int i = threadIdx.x; i < n; i += 1024) osk_t[sc_at(i, sc_log_len(n))] = t[i];
+    __syncthreads();
+    const float s = kr_spec_sum<1024>(osk_t, n, (unsigned char *)(osk_t + sc_terms_cap(n)), s0);
+    if (threadIdx.x == 0) *out = s;
+}
 // the single-wave mode, run by the second wave of the workgroup (its lanes
 // and LDS are not the workgroup's first)
 __global__ void __launch_bounds__(128) k_ordered_sum_wave(float *out, const float *t, int n, float s0) {
@@ -1284,6 +1292,15 @@ extern "C" void krh_ordered_sum(float *out, const float *t, int n, float s0) {
     kr_check_launch("ordered_sum");
 }
 
+extern "C" void krh_ordered_sum_1024(float *out, const float *t, int n, float s0) {
+    if (n < 1 || n > KRH_ORDERED_SUM_MAX) {
+        kr_fail(ML_E_SHAPE, "ordered_sum_1024 size", hipSuccess);
+        return;
+    }
+    const size_t lds = sizeof(float) * (size_t)sc_terms_cap(n) + sc_lds_bytes(n, 1024);
+    hipLaunchKernelGGL(k_ordered_sum_1024, dim3(1), dim3(1024), lds, kr_stream(), out, t, n, s0);
+    kr_check_launch("ordered_sum_1024");
+}
 extern "C" void krh_ordered_sum_wave(float *out, const float *t, int n, float s0) {
     if (n < 1 || n > KRH_ORDERED_SUM_WAVE_MAX) {
         kr_fail(ML_E_SHAPE, "ordered_sum_wave size", hipSuccess);

@@ -4,8 +4,10 @@
  * The file is mapped read-only and the model's tensors are views into it.
  * Loading runs in three stages:
  *   1. the 256-byte header through a table of per-field rules (offset, type,
- *      accepted range, status when outside it), then the rules that relate
- *      fields to each other (derived dimensions, the q8 mask, RoPE scaling);
+ *      accepted range, status when outside it) and the rules that relate
+ *      fields to each other (derived dimensions, the q8 mask, RoPE scaling),
+ *      in four phases that give a header with several faults the reference
+ *      loader's status;
  *   2. the per-layer flag bytes, when the header announces them;
  *   3. a plan of the body: every array the configuration implies, in file
  *      order, each with its byte size and the pointer it fills; one pass lays
@@ -35,41 +37,48 @@
 enum { FIELD_U32 = 0, FIELD_F32 = 1 };
 
 /* one header field's acceptance rule: lo < v (open) or lo <= v, and v < hi
- * (open) or v <= hi; a NaN passes no rule */
+ * (open) or v <= hi; a NaN passes no rule. phase: when it is checked. A
+ * header with several faults gets the status of the first fault in the
+ * reference's order, which interleaves field ranges with the rules between
+ * fields in four phases, each of one status:
+ *   1 the dimensions' ranges (ML_E_SHAPE),
+ *   2 the weight encoding: wtype, the q8 mask, qkv_bias (ML_E_FORMAT),
+ *   3 the derived dimensions: divisibility, head_dim, q_dim (ML_E_SHAPE),
+ *   4 everything else (ML_E_FORMAT). */
 typedef struct {
-    uint8_t off, kind, status, lo_open, hi_open;
+    uint8_t off, kind, status, lo_open, hi_open, phase;
     double lo, hi;
     const char *name;
 } field_rule;
 
-#define U32(off, lo, hi, st, name) { off, FIELD_U32, st, 0, 0, lo, hi, name }
-#define F32(off, lo_open, lo, hi, hi_open, name) { off, FIELD_F32, ML_E_FORMAT, lo_open, hi_open, lo, hi, name }
+#define U32(ph, off, lo, hi, st, name) { off, FIELD_U32, st, 0, 0, ph, lo, hi, name }
+#define F32(ph, off, lo_open, lo, hi, hi_open, name) { off, FIELD_F32, ML_E_FORMAT, lo_open, hi_open, ph, lo, hi, name }
 
 static const field_rule FIELD_RULES[] = {
-    U32(8, 1, LIM_DIM, ML_E_SHAPE, "dim"),
-    U32(12, 1, LIM_DIM, ML_E_SHAPE, "n_layers"),
-    U32(16, 1, LIM_DIM, ML_E_SHAPE, "n_heads"),
-    U32(20, 1, LIM_DIM, ML_E_SHAPE, "n_kv_heads"),
-    U32(24, 1, LIM_DIM, ML_E_SHAPE, "hidden_dim"),
-    U32(28, 3, LIM_TOKENS, ML_E_SHAPE, "vocab"),   /* ids 1 and 2 are BOS and EOS */
-    U32(32, 1, LIM_TOKENS, ML_E_SHAPE, "max_seq"),
-    F32(36, 1, 0.0, INFINITY, 0, "rope_theta"),
-    F32(40, 0, 0.0, INFINITY, 0, "norm_eps"),
-    U32(44, ML_Q8_0, ML_Q4_0, ML_E_FORMAT, "wtype"),
-    U32(52, ML_ROPE_NONE, ML_ROPE_YARN, ML_E_FORMAT, "rope_type"),
-    U32(76, 0, 1, ML_E_FORMAT, "qkv_bias"),
-    U32(80, 0, LIM_DIM, ML_E_SHAPE, "head_dim"),
-    U32(84, 0, 1, ML_E_FORMAT, "qk_norm"),
-    U32(92, 0, LIM_TOKENS, ML_E_FORMAT, "sliding_window"),
-    U32(96, 0, 1, ML_E_FORMAT, "layer_flags"),
-    F32(100, 0, 0.0, 1e30, 1, "rope_local_theta"),
-    U32(104, ML_ACT_SILU, ML_ACT_GELU_TANH, ML_E_FORMAT, "act"),
-    U32(108, 0, 1, ML_E_FORMAT, "post_norms"),
-    F32(112, 0, 0.0, 1e6, 1, "embed_scale"),
-    F32(116, 0, 0.0, 1e6, 1, "attn_scale"),
-    U32(120, 0, 1, ML_E_FORMAT, "scale_f16"),
-    F32(124, 0, 0.0, 1e6, 1, "attn_softcap"),
-    F32(128, 0, 0.0, 1e6, 1, "final_softcap"),
+    U32(1, 8, 1, LIM_DIM, ML_E_SHAPE, "dim"),
+    U32(1, 12, 1, LIM_DIM, ML_E_SHAPE, "n_layers"),
+    U32(1, 16, 1, LIM_DIM, ML_E_SHAPE, "n_heads"),
+    U32(1, 20, 1, LIM_DIM, ML_E_SHAPE, "n_kv_heads"),
+    U32(1, 24, 1, LIM_DIM, ML_E_SHAPE, "hidden_dim"),
+    U32(1, 28, 3, LIM_TOKENS, ML_E_SHAPE, "vocab"),   /* ids 1 and 2 are BOS and EOS */
+    U32(1, 32, 1, LIM_TOKENS, ML_E_SHAPE, "max_seq"),
+    U32(2, 44, ML_Q8_0, ML_Q4_0, ML_E_FORMAT, "wtype"),
+    U32(2, 76, 0, 1, ML_E_FORMAT, "qkv_bias"),
+    U32(3, 80, 0, LIM_DIM, ML_E_SHAPE, "head_dim"),
+    F32(4, 36, 1, 0.0, INFINITY, 0, "rope_theta"),
+    F32(4, 40, 0, 0.0, INFINITY, 0, "norm_eps"),
+    U32(4, 52, ML_ROPE_NONE, ML_ROPE_YARN, ML_E_FORMAT, "rope_type"),
+    U32(4, 84, 0, 1, ML_E_FORMAT, "qk_norm"),
+    U32(4, 92, 0, LIM_TOKENS, ML_E_FORMAT, "sliding_window"),
+    U32(4, 96, 0, 1, ML_E_FORMAT, "layer_flags"),
+    F32(4, 100, 0, 0.0, 1e30, 1, "rope_local_theta"),
+    U32(4, 104, ML_ACT_SILU, ML_ACT_GELU_TANH, ML_E_FORMAT, "act"),
+    U32(4, 108, 0, 1, ML_E_FORMAT, "post_norms"),
+    F32(4, 112, 0, 0.0, 1e6, 1, "embed_scale"),
+    F32(4, 116, 0, 0.0, 1e6, 1, "attn_scale"),
+    U32(4, 120, 0, 1, ML_E_FORMAT, "scale_f16"),
+    F32(4, 124, 0, 0.0, 1e6, 1, "attn_softcap"),
+    F32(4, 128, 0, 0.0, 1e6, 1, "final_softcap"),
 };
 #undef U32
 #undef F32
@@ -114,15 +123,21 @@ static int rope_params_ok(const ml_config *c) {
     }
 }
 
+/* the header's field ranges of one phase */
+static ml_status check_fields(const uint8_t *h, int phase) {
+    for (size_t i = 0; i < sizeof FIELD_RULES / sizeof FIELD_RULES[0]; i++) {
+        const field_rule *r = &FIELD_RULES[i];
+        if (r->phase != phase) continue;
+        const double v = field_value(h, r);
+        if (!field_ok(v, r)) return kr_seterr((ml_status)r->status, "header field %s = %g out of range", r->name, v);
+    }
+    return ML_OK;
+}
+
 ml_status kr_parse_header(ml_config *cfg, int *shared, const uint8_t *h) {
     memset(cfg, 0, sizeof *cfg);
     if (memcmp(h, "MLB1", 4) != 0) return kr_seterr(ML_E_FORMAT, "magic is not MLB1");
     if (le32(h, 4) != 1) return kr_seterr(ML_E_FORMAT, "version %u (1 expected)", le32(h, 4));
-    for (size_t i = 0; i < sizeof FIELD_RULES / sizeof FIELD_RULES[0]; i++) {
-        const field_rule *r = &FIELD_RULES[i];
-        const double v = field_value(h, r);
-        if (!field_ok(v, r)) return kr_seterr((ml_status)r->status, "header field %s = %g out of range", r->name, v);
-    }
     ml_config *c = cfg;
     c->dim = (int)le32(h, 8);
     c->n_layers = (int)le32(h, 12);
@@ -155,18 +170,26 @@ ml_status kr_parse_header(ml_config *cfg, int *shared, const uint8_t *h) {
     c->scale_f16 = (int)le32(h, 120);
     c->attn_softcap = lef(h, 124);
     c->final_softcap = lef(h, 128);
+    ml_status st;
 
-    /* rules between fields */
+    /* 1: the dimensions */
+    if ((st = check_fields(h, 1)) != ML_OK) return st;
+    /* 2: the weight encoding */
+    if ((st = check_fields(h, 2)) != ML_OK) return st;
     if ((c->q8_mask & ~(unsigned)ML_Q8M_ALL) || (c->wtype == ML_Q8_0 && c->q8_mask))
         return kr_seterr(ML_E_FORMAT, "q8_mask 0x%x with wtype %d", c->q8_mask, c->wtype);
+    /* 3: the derived dimensions */
     if (c->dim % QK || c->hidden_dim % QK) return kr_seterr(ML_E_SHAPE, "dim and hidden_dim must be multiples of 32");
     if (c->n_heads % c->n_kv_heads) return kr_seterr(ML_E_SHAPE, "n_kv_heads must divide n_heads");
+    if ((st = check_fields(h, 3)) != ML_OK) return st;
     if (!head_dim && c->dim % c->n_heads) return kr_seterr(ML_E_SHAPE, "n_heads must divide dim");
     c->head_dim = head_dim ? head_dim : c->dim / c->n_heads;
     if ((double)c->head_dim * c->n_heads > LIM_DIM) return kr_seterr(ML_E_SHAPE, "q_dim above 65536");
     c->q_dim = c->head_dim * c->n_heads;
     c->kv_dim = c->head_dim * c->n_kv_heads;
     if (c->head_dim % 2 || c->q_dim % QK) return kr_seterr(ML_E_SHAPE, "odd head_dim or q_dim not a multiple of 32");
+    /* 4: the rest */
+    if ((st = check_fields(h, 4)) != ML_OK) return st;
     if (c->rope_type != ML_ROPE_YARN && c->rope_attn_factor != 0.0f)
         return kr_seterr(ML_E_FORMAT, "rope_attn_factor without yarn scaling");
     if (!rope_params_ok(c)) return kr_seterr(ML_E_FORMAT, "RoPE scaling parameters of rope_type %d", c->rope_type);

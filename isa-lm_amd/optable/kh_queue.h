@@ -347,6 +347,11 @@ static int fuse_at(int i) {
 static int run_at(int i, int *T_out) {
     int best_m = 0, best_T = 0;
     for (int m = 1; m <= KH_PERIOD_MAX && i + 2 * m <= g_nq; m++) {
+        /* no run of period m can cover more calls than are left in whole
+         * periods: once the best covers that many, longer periods cannot
+         * beat it (a stage of T tokens would otherwise extend every multiple
+         * of its period over all T rows) */
+        if (best_m && m * ((g_nq - i) / m) <= best_m * best_T) break;
         if (!same_sig(&g_q[i], &g_q[i + m])) continue;
         int ok = 1;
         for (int k = 0; k < m && ok; k++) {

@@ -28,9 +28,13 @@
  * The embedding's scale (model/transformer.c:228-229, a host loop over the
  * row) is applied on the device by ml_dequant_row instead, so the host loop
  * only touches the arena's host copy, which nothing reads.
- * Supported: the F32 and Q8 KV caches, no --imatrix (the F16 cache's
- * conversion and the importance statistics read activations on the host:
- * model/transformer.c:195-197, :250-255). */
+ * KV caches: F32 and Q8 (store_kv quantizes through ml_quantize_row), and
+ * F16: store_kv converts K and V to halves in a host loop
+ * (model/transformer.c:195-197) from staging rows that live on the device
+ * here, so the attention call first converts this step's staging rows on
+ * the device (the halves ml_f32_to_f16 gives, core/ml.c:39-53) into the
+ * cache rows it reads; the host loop's copy is never read. No --imatrix
+ * (the importance statistics read activations on the host, :250-255). */
 #include <math.h>
 #include <stdio.h>
 #include <stdlib.h>
@@ -41,6 +45,7 @@
 #include "core/quant_ref.h"
 #include "core/threads.h"
 #include "model/pack_model.h"
+#include "model/transformer.h"   /* ML_BATCH_MAX: the staging rows of an F16 cache */
 #include "ops/ops.h"
 #define KRAFLA_TYPES_H   /* the types come from the reference's core/ml.h */
 #include "krafla_hip.h"
@@ -216,6 +221,16 @@ ml_status ml_isa_check(const char **missing) {
 /* ---- core/arena.c: the same bump allocator (core/arena.c:3-26) over
  * pinned host memory, with an HBM twin registered for translation ---- */
 
+/* the arenas' allocations in order (ml_state_init's F16 cache is kh, vh,
+ * then the staging rows kbuf, vbuf: model/transformer.c:114-117) */
+typedef struct {
+    const uint8_t *p;
+    size_t n;
+} kh_alloc;
+#define KH_ALLOCS 512
+static kh_alloc g_al[KH_ALLOCS];
+static int g_nal;
+
 ml_status ml_arena_init(ml_arena *a, size_t cap) {
     a->base = NULL;
     a->cap = a->off = 0;
@@ -237,11 +252,16 @@ void *ml_arena_alloc(ml_arena *a, size_t n) {
     if (need > a->cap - a->off) return NULL;
     void *p = a->base + a->off;
     a->off += need;
+    if (g_nal < KH_ALLOCS) g_al[g_nal++] = (kh_alloc){ p, n };
     return p;
 }
 
 void ml_arena_free(ml_arena *a) {
     if (a->base) {
+        int k = 0;
+        for (int i = 0; i < g_nal; i++)
+            if (!(g_al[i].p >= a->base && g_al[i].p < a->base + a->cap)) g_al[k++] = g_al[i];
+        g_nal = k;
         q_flush();
         krh_sync();
         uint8_t *d = dev_addr(a->base, 1);
@@ -554,15 +574,31 @@ int ml_attention_batch_heads(const ml_config *cfg, int nthreads) {
     return cfg->n_heads / cfg->n_kv_heads;
 }
 
-/* The F32 and Q8 caches. The F16 cache is converted by a host loop in
- * store_kv (model/transformer.c:195-197) from K and V rows that live on the
- * device here, so it cannot be served through this binding. */
+/* The F16 cache's staging rows: the two allocations after the ones holding
+ * the layer views kh and vh (model/transformer.c:114-117), each
+ * ML_BATCH_MAX rows of kv_dim floats. */
+static int f16_staging(const ml_kv_layer *kv, const ml_config *cfg, const float **kb, const float **vb) {
+    const size_t rows = F((size_t)ML_BATCH_MAX * cfg->kv_dim);
+    for (int i = 0; i + 3 < g_nal; i++) {
+        const uint8_t *h = (const uint8_t *)kv->kh;
+        if (!(h >= g_al[i].p && h < g_al[i].p + g_al[i].n)) continue;
+        const uint8_t *v = (const uint8_t *)kv->vh;
+        if (!(v >= g_al[i + 1].p && v < g_al[i + 1].p + g_al[i + 1].n) || g_al[i + 2].n != rows || g_al[i + 3].n != rows)
+            return 0;
+        *kb = (const float *)g_al[i + 2].p;
+        *vb = (const float *)g_al[i + 3].p;
+        return 1;
+    }
+    return 0;
+}
+
 static int attn_supported(const ml_kv_layer *kv, const ml_config *cfg) {
-    if (kv->kh || kv->vh) {
-        fail_call("the F16 KV cache is converted on the host by model/transformer.c (use --kv f32 or --kv q8)");
+    const float *kb, *vb;
+    if ((kv->kh || kv->vh) && !(kv->kh && kv->vh && f16_staging(kv, cfg, &kb, &vb))) {
+        fail_call("an F16 KV cache whose staging rows are not the state's (model/transformer.c:114-117)");
         return 0;
     }
-    if (!(kv->k && kv->v) && !(kv->kq && kv->vq && kv->kd && kv->vd)) {
+    if (!(kv->k && kv->v) && !(kv->kh && kv->vh) && !(kv->kq && kv->vq && kv->kd && kv->vd)) {
         fail_call("attention without KV cache rows");
         return 0;
     }
@@ -571,8 +607,22 @@ static int attn_supported(const ml_kv_layer *kv, const ml_config *cfg) {
     return 1;
 }
 
-/* the layer's cache as device pointers: F32 rows, or Q8 rows and their row
- * scales (written on the device by ml_quantize_row in store_kv) */
+/* F16 cache: store_kv's halves of this step's ntok staging rows into the
+ * cache rows at positions g_ints[0] + t, on the device; 0 when the call
+ * must not go on */
+static int f16_store(kh_call *c, const ml_kv_layer *kv, const ml_kv_layer *d, const ml_config *cfg, int ntok) {
+    const float *kb, *vb;
+    if (!kv->kh) return !c->fail;
+    if (c->fail || !f16_staging(kv, cfg, &kb, &vb)) return 0;
+    const float *kd = arg(c, kb, F((size_t)ntok * cfg->kv_dim), 1, 0);
+    const float *vd = arg(c, vb, F((size_t)ntok * cfg->kv_dim), 1, 0);
+    if (c->fail) return 0;
+    krh_store_kv(ML_F16, d->kh, d->vh, NULL, NULL, kd, vd, cfg->n_kv_heads, cfg->head_dim, g_ints, ntok);
+    return 1;
+}
+
+/* the layer's cache as device pointers: F32 rows, F16 rows, or Q8 rows and
+ * their row scales (written on the device by ml_quantize_row in store_kv) */
 static ml_kv_layer dev_kv(kh_call *c, const ml_kv_layer *kv, const ml_config *cfg) {
     const size_t n = (size_t)cfg->max_seq * cfg->kv_dim, ns = (size_t)cfg->max_seq * cfg->n_kv_heads;
     ml_kv_layer d;
@@ -581,6 +631,9 @@ static ml_kv_layer dev_kv(kh_call *c, const ml_kv_layer *kv, const ml_config *cf
     if (kv->k) {
         d.k = arg(c, kv->k, F(n), 1, 0);
         d.v = arg(c, kv->v, F(n), 1, 0);
+    } else if (kv->kh) {
+        d.kh = arg(c, kv->kh, 2 * n, 1, 0);
+        d.vh = arg(c, kv->vh, 2 * n, 1, 0);
     } else {
         d.kq = arg(c, kv->kq, n, 1, 0);
         d.vq = arg(c, kv->vq, n, 1, 0);
@@ -603,8 +656,9 @@ void ml_attention(ml_pool *pool, float *out, const float *q, const ml_kv_layer *
     const ml_kv_layer d = dev_kv(&c, kv, cfg);
     if (!c.fail) {
         set_pos(pos);
-        krh_attention_kv_softcap(o, att, qv, &d, cfg->n_heads, cfg->n_kv_heads, cfg->head_dim, cfg->max_seq,
-                                 cfg->attn_scale, g_ints, 1, cfg->max_seq - 1, cfg->attn_softcap);
+        if (f16_store(&c, kv, &d, cfg, 1))
+            krh_attention_kv_softcap(o, att, qv, &d, cfg->n_heads, cfg->n_kv_heads, cfg->head_dim, cfg->max_seq,
+                                     cfg->attn_scale, g_ints, 1, cfg->max_seq - 1, cfg->attn_softcap);
     }
     done(&c);
 }
@@ -621,8 +675,9 @@ void ml_attention_batch(ml_pool *pool, float *out, const float *q, const ml_kv_l
     const ml_kv_layer d = dev_kv(&c, kv, cfg);
     if (!c.fail && g_batt) {
         set_pos(pos0);
-        krh_attention_kv_softcap(o, g_batt, qv, &d, cfg->n_heads, cfg->n_kv_heads, cfg->head_dim, cfg->max_seq,
-                                 cfg->attn_scale, g_ints, n, pos0 + n - 1, cfg->attn_softcap);
+        if (f16_store(&c, kv, &d, cfg, n))
+            krh_attention_kv_softcap(o, g_batt, qv, &d, cfg->n_heads, cfg->n_kv_heads, cfg->head_dim, cfg->max_seq,
+                                     cfg->attn_scale, g_ints, n, pos0 + n - 1, cfg->attn_softcap);
     }
     done(&c);
 }

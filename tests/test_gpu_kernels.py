@@ -304,7 +304,11 @@ def test_matvec_float_input(dev, typ, d16, rows, cols):
                                                   (32, 8, 128, 2303, 0), (32, 8, 64, 4000, 0), (8, 2, 64, 100, 7),
                                                   (16, 1, 64, 63, 0), (4, 2, 32, 64, 0), (12, 4, 96, 130, 0),
                                                   (4, 2, 32, 9000, 0), (8, 2, 64, 12000, 9000), (8, 4, 256, 300, 0),
-                                                  (4, 1, 256, 200, 64)])
+                                                  (4, 1, 256, 200, 64),
+                                                  # the softmax inside the mix launch (rows of at most 4096
+                                                  # scores, groups of 1 to 4): at the limit, groups 1 and 2
+                                                  (32, 8, 128, 4095, 0), (8, 8, 64, 1000, 0), (8, 4, 64, 3000, 0),
+                                                  (6, 3, 64, 4095, 100)])
 def test_attention(dev, nh, nkv, hd, pos, window):
     max_seq = max(256, pos + 1)
     kvd, qd = nkv * hd, nh * hd
@@ -406,6 +410,25 @@ def test_ordered_sum(dev, case, n, s0):
     t = ordered_terms(case, n)
     out = dev.zeros(4)
     K.hip.krh_ordered_sum(out.ptr, dev.put(t).ptr, n, s0)
+    ok()
+    got = out.get(np.float32, 1)[0]
+    want = seq_sum_f32(t, s0)
+    if np.isnan(want):
+        assert np.isnan(got)
+    else:
+        assert bits(np.float32(got)) == bits(np.float32(want)), (got, want)
+
+
+@pytest.mark.parametrize("s0", [0.0, 1234.5678])
+@pytest.mark.parametrize("case", ORDERED_CASES)
+@pytest.mark.parametrize("n", [1, 5, 31, 33, 128, 129, 2047, 2048, 2049, 4096, 4097, 8192])
+def test_ordered_sum_1024(dev, case, n, s0):
+    """the ordered sum by a workgroup of 1024 threads (16 waves: the decode
+    softmax's form, k_attn_softmax): the sequential fp32 sum's bits on every
+    case"""
+    t = ordered_terms(case, n)
+    out = dev.zeros(4)
+    K.hip.krh_ordered_sum_1024(out.ptr, dev.put(t).ptr, n, s0)
     ok()
     got = out.get(np.float32, 1)[0]
     want = seq_sum_f32(t, s0)

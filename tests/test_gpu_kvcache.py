@@ -124,7 +124,7 @@ def views(dev, kv_type, k, v, kd, vd, window):
 @pytest.mark.parametrize("nh,nkv,hd,pos,window", [(6, 6, 48, 0, 0), (14, 2, 64, 511, 0), (32, 8, 128, 2175, 0),
                                                   (32, 8, 128, 2303, 0), (8, 2, 64, 100, 7), (16, 1, 64, 63, 0),
                                                   (12, 4, 96, 130, 0), (4, 2, 32, 9000, 0), (8, 4, 256, 300, 0),
-                                                  (4, 1, 256, 200, 64)])
+                                                  (4, 1, 256, 200, 64), (32, 8, 128, 4095, 0), (8, 8, 64, 1000, 0)])
 def test_attention_kv(dev, kv_type, nh, nkv, hd, pos, window):
     max_seq = max(256, pos + 1)
     kvd, qd = nkv * hd, nh * hd

@@ -103,14 +103,31 @@ def test_ml_run_kv_q8(name, batch, workdir):
     assert np.array_equal(got, want)
 
 
-def test_ml_run_kv_f16_refused(workdir):
-    """the F16 cache is converted by a host loop of model/transformer.c, which
-    this binding cannot serve: the run says so on stderr"""
-    import subprocess
-    path = model("c1_q8", workdir)
-    r = subprocess.run([os.path.join(O.REF_DIR, "hip", "ml_run"), path, "--tokens", "1,2,3", "-n", "3", "-T", "0",
-                        "--kv", "f16"], capture_output=True, text=True, timeout=300)
-    assert "F16 KV cache" in r.stderr
+@pytest.mark.parametrize("build", ["hip", "hip128"])
+@pytest.mark.parametrize("batch", [None, 1])
+@pytest.mark.parametrize("name", ["c1_q8", "llama3_rope_gqa_q4", "qwen_like_q4mix", "qk_norm_q4mix",
+                                  "post_norm_gelu_window"])
+def test_ml_run_kv_f16(name, batch, build, workdir):
+    """--kv f16 (app/ml_run.c:277-281): store_kv's host loop converts K and V
+    to halves (model/transformer.c:195-197) from staging rows that live on
+    the device; the binding converts them on the device before attention
+    reads the cache. The same --dump-logits bytes and greedy ids as the
+    scalar build's --kv f16, per token (--batch 1) and batched (one step, or
+    the 128-token steps of hip128 over a 150-token prompt)"""
+    path = model(name, workdir)
+    V, S = MODELS[name]["vocab"], MODELS[name]["max_seq"]
+    n = min(150, S - 40)
+    toks = [int(t) for t in np.random.default_rng(8).integers(1, V, n)]
+    a, b = path + ".scalar.f16.logits", path + "." + build + ".f16.logits"
+    ext = ["--kv", "f16"] + (["--batch", str(batch)] if batch else [])
+    O.ref_ml_run(path, toks, n, dump=a, extra=["--kv", "f16"])
+    O.ref_ml_run(path, toks, n, dump=b, isa=build, extra=ext)
+    x, y = np.fromfile(a, dtype=np.uint8), np.fromfile(b, dtype=np.uint8)
+    assert x.size == n * V * 4 and np.array_equal(x, y)
+    steps = min(S, 8 + 64)
+    want, _ = O.ref_ml_run(path, toks[:8], steps, extra=["--kv", "f16"])
+    got, _ = O.ref_ml_run(path, toks[:8], steps, isa=build, extra=ext)
+    assert np.array_equal(got, want)
 
 
 @pytest.mark.parametrize("build", ["hip", "hip128"])

@@ -156,6 +156,31 @@ def test_header_patches(bases, base):
     assert {OK, FORMAT, SHAPE} <= statuses
 
 
+@pytest.mark.parametrize("base", sorted(BASES))
+def test_header_two_faults(bases, base):
+    """two patched fields whose single faults give different statuses: the
+    reference interleaves field ranges with the rules between fields
+    (model/mlb.c:80-157), so the status is that of the first fault in its
+    order; every such pair of the single-field cases, applied together"""
+    d, data = bases
+    blob = data[base]
+    single = [(name, patch, check_same(d, "%s: %s" % (base, name), patch(blob)))
+              for name, patch in HEADER_CASES + ROPE_CASES]
+    bad = [(n, p, st) for n, p, st in single if st != OK]
+    pairs = 0
+    for i, (na, pa, sa) in enumerate(bad):
+        for nb, pb, sb in bad[i + 1:]:
+            if sa != sb:
+                check_same(d, "%s: %s + %s" % (base, na, nb), pb(pa(blob)))
+                pairs += 1
+    assert pairs > 100
+    # the examples that separate the orders: a SHAPE fault before a later
+    # FORMAT one, and a FORMAT fault before a later SHAPE one
+    assert check_same(d, base + ": dim 40, rope_theta 0", set_f32(set_u32(blob, 8, 40), 36, 0.0)) == SHAPE
+    if BASES[base]["wtype"] == K.ML_Q8_0:
+        assert check_same(d, base + ": q8_mask 1, head_dim 65537", set_u32(set_u32(blob, 72, 1), 80, 65537)) == FORMAT
+
+
 def align64(n):
     return (n + 63) // 64 * 64
 
