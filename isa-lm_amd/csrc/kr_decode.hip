@@ -30,6 +30,14 @@ KMat to_kmat(const krh_mat *m) {
 }
 
 enum { EPI_STORE = 0, EPI_ADD = 1, EPI_QKV = 2, EPI_SWIGLU = 3 };
+// weight type template argument: ML_Q8_0, ML_Q4_0, or QT_MIXED, the type of
+// each matrix read from its KMat at run time (q|k|v of a Q4 model with its
+// v in Q8: one launch and one prologue; an item lies in one matrix, so the
+// branch is uniform across the wave)
+constexpr int QT_MIXED = 7;
+template <int QT> __device__ __forceinline__ bool qt_is_q8(int type) {
+    return QT == QT_MIXED ? type == ML_Q8_0 : QT == ML_Q8_0;
+}
 
 struct MvArgs {
     KMat m[3];
@@ -287,7 +295,7 @@ __device__ __forceinline__ void mv_load(MvSlots &S, const MvArgs &a, const MvIte
         const void *d = second ? W2.d : W.d;
         const size_t blk = in ? (size_t)(it.row0 + (second ? lr - it.nr : lr)) * nb + it.c0 + b
                               : (size_t)it.row0 * nb + it.c0;
-        if (QT == ML_Q8_0) {
+        if (qt_is_q8<QT>(W.type)) {
             const int4 *p = (const int4 *)(q + blk * 32);
             S.w0[k] = p[0];
             S.w1[k] = p[1];
@@ -322,7 +330,7 @@ __device__ __forceinline__ int mv_touch(const MvArgs &a, const MvItem &it, int n
     const bool second = EPI == EPI_SWIGLU && lr >= it.nr;
     const unsigned blk = (unsigned)(it.row0 + (second ? lr - it.nr : lr)) * (unsigned)nb + (unsigned)(it.c0 + b);
     const uint8_t *base = scale ? (const uint8_t *)(second ? W2.d : W.d) : (second ? W2.q : W.q);
-    const unsigned off = scale ? blk * (D16 ? 2u : 4u) : blk * (QT == ML_Q8_0 ? 32u : 16u);
+    const unsigned off = scale ? blk * (D16 ? 2u : 4u) : blk * (qt_is_q8<QT>(W.type) ? 32u : 16u);
     return *(const uint16_t *)(base + off);   // 2 bytes: in bounds for every block and scale
 }
 
@@ -590,7 +598,10 @@ __global__ void __launch_bounds__(MV_THREADS, mv_wgs_per_cu(EPI)) k_matvec(const
             for (int k = 0; k < MV_NPT; k++) {
                 if (lane + k * 64 < n) {
                     const int bb = cur.c0 + b;
-                    const int sdot = block_dot<QT>(S[P].w0[k], S[P].w1[k], xs + bb * 32);
+                    const int sdot = QT != QT_MIXED ? block_dot<QT>(S[P].w0[k], S[P].w1[k], xs + bb * 32)
+                                     : qt_is_q8<QT>(pick3(cur.mi, a.m[0].type, a.m[1].type, a.m[2].type))
+                                         ? block_dot<ML_Q8_0>(S[P].w0[k], S[P].w1[k], xs + bb * 32)
+                                         : block_dot<ML_Q4_0>(S[P].w0[k], S[P].w1[k], xs + bb * 32);
                     const float sc = D16 ? kr_h2f((uint16_t)S[P].wd[k]) : __uint_as_float(S[P].wd[k]);
                     T[lr * ts + b] = kr_fmul(kr_fmul((float)sdot, sc), xds[bb]);
                 }
@@ -738,6 +749,19 @@ void launch_mv(MvArgs &a, const KMat &W) {
     auto go = [&](auto kern) {
         hipLaunchKernelGGL(kern, dim3(grid), dim3(MV_THREADS), lds, kr_stream(), a);
     };
+    bool mixed = false;
+    for (int i = 1; i < a.nmat; i++) mixed = mixed || a.m[i].type != a.m[0].type;
+    if constexpr (EPI == EPI_QKV) {
+        if (mixed) {
+            if (W.d16) go(k_matvec<EPI, QT_MIXED, 1>); else go(k_matvec<EPI, QT_MIXED, 0>);
+            kr_check_launch("matvec");
+            return;
+        }
+    }
+    if (mixed) {
+        kr_fail(ML_E_SHAPE, "matvec: matrices of one launch differ in type", hipSuccess);
+        return;
+    }
     if (W.type == ML_Q8_0) {
         if (W.d16) go(k_matvec<EPI, ML_Q8_0, 1>); else go(k_matvec<EPI, ML_Q8_0, 0>);
     } else {
@@ -1154,21 +1178,8 @@ static void qkv(float *q, float *kc, float *vc, const krh_mat *wq, const krh_mat
     a.pos = pos;
     a.kv16 = kv16;
     set_keep(a, kp);
-    // wq, wk and wv may differ in type (Q4 models keep wv in Q8): one launch
-    // per type run
-    if (wv->type == wq->type) {
-        launch_mv<EPI_QKV>(a, a.m[0]);
-        return;
-    }
-    MvArgs b = a;
-    b.nmat = 2;   // q and k
-    launch_mv<EPI_QKV>(b, b.m[0]);
-    MvArgs c = a;   // v alone, as matrix 2 of the same epilogue
-    c.tile0[0] = c.tile0[1] = c.tile0[2] = 0;
-    c.tile0[3] = (wv->rows + a.R - 1) / a.R;
-    c.m[0] = c.m[1] = c.m[2];
-    c.nmat = 3;
-    launch_mv<EPI_QKV>(c, c.m[2]);
+    // wv may be Q8 in a Q4 model: the launch then reads each matrix's type
+    launch_mv<EPI_QKV>(a, a.m[0]);
 }
 
 extern "C" void krh_matvec_qkv(float *q, float *kc, float *vc, const krh_mat *wq, const krh_mat *wk,
