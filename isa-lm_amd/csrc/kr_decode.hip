@@ -465,24 +465,32 @@ __global__ void __launch_bounds__(MV_THREADS, mv_wgs_per_cu(EPI)) k_matvec(const
         // thread t takes the 16 values base + 16 t .. + 15, half of a
         // 32-block (kr_quant16)
         static_assert(MV_XF_PASS == 16 * MV_THREADS, "a pass is one half-block per thread");
-        float4 xv[4];
-        auto pass_load = [&](int base) {
+        // Two passes' registers in turn: a pass's loads go out before the
+        // pass ahead of it is quantized (h of 14,336 floats: four load round
+        // trips in series otherwise).
+        float4 xa[4], xb[4];
+        auto pass_load = [&](float4 (&xv)[4], int base) {
             const int i = min(base + 16 * tid, K - 16);
 #pragma unroll
             for (int k = 0; k < 4; k++) xv[k] = *(const float4 *)(a.xf + i + 4 * k);
         };
-        auto pass_quant = [&](int base) {
+        auto pass_quant = [&](const float4 (&xv)[4], int base) {
             const int i = base + 16 * tid;   // K % 32 == 0: both halves of a block are in or out
             if (i < K) kr_quant16(xv, i, xs, xds);
         };
-        pass_load(0);
+        pass_load(xa, 0);
+        if (MV_XF_PASS < K) pass_load(xb, MV_XF_PASS);
 #pragma unroll
         for (int d = 0; d < MV_DEPTH - 1; d++) load_item(S[d], I[d]);
         prime_touch();
-        pass_quant(0);
-        for (int base = MV_XF_PASS; base < K; base += MV_XF_PASS) {
-            pass_load(base);
-            pass_quant(base);
+        pass_quant(xa, 0);
+        for (int base = MV_XF_PASS; base < K; base += 2 * MV_XF_PASS) {
+            if (base + MV_XF_PASS < K) pass_load(xa, base + MV_XF_PASS);
+            pass_quant(xb, base);
+            if (base + MV_XF_PASS < K) {
+                if (base + 2 * MV_XF_PASS < K) pass_load(xb, base + 2 * MV_XF_PASS);
+                pass_quant(xa, base + MV_XF_PASS);
+            }
         }
     } else if (!a.xq && K <= MV_XF_MAX) {
         // a float activation (normalized first when nw is set), held in
