@@ -82,6 +82,24 @@ def test_ml_bench_kernel_table():
     assert "ISA: hip" in r.stdout and "matvec_q8 -> ml_k_matvec_q8_hip" in r.stdout
 
 
+@pytest.mark.parametrize("build", ["hip", "hip128"])
+@pytest.mark.parametrize("kv", ["f32", "q8", "f16"])
+def test_ml_bench_model_mode(kv, build, workdir):
+    """ml_bench with a model (app/ml_bench.c:105-131): ml_prefill of 64
+    tokens, then 64 ml_forward steps with an inline argmax, through the op
+    table; it prints only rates, so the check is that the run completes on
+    the device and reports both"""
+    import re
+    import subprocess
+    path = model("qwen_like_q4mix", workdir)
+    r = subprocess.run([os.path.join(O.REF_DIR, build, "ml_bench"), path, "-n", "64", "--kv", kv],
+                       capture_output=True, text=True, timeout=600)
+    assert r.returncode == 0, r.stderr
+    m = re.search(r"model .*: prefill ([\d.]+) tok/s, decode ([\d.]+) tok/s \(64 tokens each", r.stdout)
+    assert m and float(m.group(1)) > 0 and float(m.group(2)) > 0, r.stdout
+    assert "error" not in r.stderr
+
+
 @pytest.mark.parametrize("batch", [None, 1])
 @pytest.mark.parametrize("name", ["c1_q8", "llama3_rope_gqa_q4", "qwen_like_q4mix"])
 def test_ml_run_kv_q8(name, batch, workdir):
