@@ -495,8 +495,14 @@ __global__ void __launch_bounds__(64 * RW) k_attn_softmax_rows(float *att, int n
 // way. One barrier per step hands tiles over: producers write tile s in step
 // s; the adder reads tile s into registers in step s + 1 and adds it in step
 // s + 2, so no add waits on an LDS read.
-constexpr int MX_T = 64, MX_TS = MX_T + 4;   // positions per tile; padded product row
-constexpr int MX_P = 2, MX_TH = MX_T / MX_P;   // producers; their positions per tile
+// Three producers and the adder: one wave per SIMD of the CU (a fourth
+// producer would share the adder's SIMD and slow its chain). The adder, not
+// the producers, is the slower side: a tile's 96 dependent adds and its 24
+// reads take about 800 cycles, the producers' products and loads 550-700.
+// Rows of MX_TS = 100 floats put a 16-lane group's 16-byte reads on 64
+// distinct banks.
+constexpr int MX_P = 3, MX_TH = 32;                  // producers; their positions per tile
+constexpr int MX_T = MX_P * MX_TH, MX_TS = MX_T + 4;   // positions per tile; padded product row
 
 __device__ __forceinline__ void kr_lds_order() { asm volatile("" ::: "memory"); }
 
@@ -535,6 +541,32 @@ __device__ __forceinline__ void attn_mix(float *ao, const float *att, const KvVi
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int j = lane / DW, d = lane % DW;
     const int ntiles = (n + MX_T - 1) / MX_T;
+    if (c0 >= hd) {
+        // a helper workgroup (grid rows past the head's dim chunks, decode
+        // only): it reads one 2-byte word of every 128-byte line of KV head
+        // g's V rows and of its query heads' weight rows, earliest positions
+        // first, so that they wait in the L2 of this XCD (workgroups are
+        // dealt to the 8 XCDs by linear id, so with 8 KV heads per launch
+        // row all of head g's workgroups share one) before the producers ask
+        constexpr int eb = KT == KV_F32 ? 4 : KT == KV_F16 ? 2 : 1;
+        const int lpr = (hd * eb + 127) / 128, nhelp = gridDim.y - (hd + DW - 1) / DW;
+        const int hi = (blockIdx.y - (hd + DW - 1) / DW) * (64 * (1 + MX_P)) + threadIdx.x, hn = nhelp * 64 * (1 + MX_P);
+        const unsigned char *vb = (const unsigned char *)kv.v + ((size_t)first * kv_dim + (size_t)g * hd) * eb;
+        const float *ab = att + (size_t)g * group * max_seq;
+        const int vl = n * lpr, al = (n * 4 + 127) / 128;   // V lines; weight-row lines per head
+        int sink = 0;
+        for (int i = hi; i < vl + group * al; i += hn) {
+            if (i < vl) {
+                const int t = i / lpr;
+                sink ^= *(const unsigned short *)(vb + (size_t)t * kv_dim * eb + (size_t)(i - t * lpr) * 128);
+            } else {
+                const int h = (i - vl) / al;
+                sink ^= *(const unsigned short *)((const unsigned char *)(ab + (size_t)h * max_seq) + (size_t)(i - vl - h * al) * 128);
+            }
+        }
+        if (sink == 0x5bd1 && max_seq < 0) ao[0] = 0.0f;   // keeps the reads (never true)
+        return;
+    }
     const int steps = (ntiles + 2 + MX_D - 1) / MX_D * MX_D;   // every wave runs as many barriers
     const size_t q_dim = (size_t)gridDim.x * group * hd;
 
@@ -1046,11 +1078,14 @@ static void launch_mix(const dim3 &grid, int ntok, float *ao, const float *att, 
             hipLaunchKernelGGL((k_attn_mix_batch_kv<DW, KT>), grid, dim3(64), 0, kr_stream(), ao, att, kv, group, hd,
                                kv_dim, max_seq, window, pos);
     } else {
+        // decode: helper rows fill the chip (about 256 workgroups in all)
+        const int rows = grid.x ? 256 / (int)grid.x : 0;
+        const dim3 hgrid(grid.x, rows > (int)grid.y ? rows : grid.y, 1);
         if constexpr (KT == KV_F32)
-            hipLaunchKernelGGL(k_attn_mix<DW>, grid, dim3(64 * (1 + MX_P)), 0, kr_stream(), ao, att, vc, group, hd,
+            hipLaunchKernelGGL(k_attn_mix<DW>, hgrid, dim3(64 * (1 + MX_P)), 0, kr_stream(), ao, att, vc, group, hd,
                                kv_dim, max_seq, window, pos);
         else
-            hipLaunchKernelGGL((k_attn_mix_kv<DW, KT>), grid, dim3(64 * (1 + MX_P)), 0, kr_stream(), ao, att, kv, group,
+            hipLaunchKernelGGL((k_attn_mix_kv<DW, KT>), hgrid, dim3(64 * (1 + MX_P)), 0, kr_stream(), ao, att, kv, group,
                                hd, kv_dim, max_seq, window, pos);
     }
 }
