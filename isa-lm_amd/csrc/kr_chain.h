@@ -227,15 +227,23 @@ __device__ __forceinline__ float kr_spec_sum(float *t, int n, unsigned char *lds
     float acc = 0.0f;
     unsigned sg = 0;
     if (c < C) {
+        // a lane's half chunk, 16 float4 reads at a time, all issued before
+        // their adds
         const float4 *h = (const float4 *)(tc + (L / 2) * p);
         float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
-        for (int k = 0; k < L / 8; k++) {
-            const float4 v = h[k];
-            sg |= __float_as_uint(v.x) | __float_as_uint(v.y) | __float_as_uint(v.z) | __float_as_uint(v.w);
-            a0 += v.x;
-            a1 += v.y;
-            a2 += v.z;
-            a3 += v.w;
+        for (int k0 = 0; k0 < L / 8; k0 += 16) {   // L / 8 is a multiple of 16 (L >= 128)
+            float4 v[16];
+#pragma unroll
+            for (int k = 0; k < 16; k++) v[k] = h[k0 + k];
+#pragma unroll
+            for (int k = 0; k < 16; k++) {
+                sg |= __float_as_uint(v[k].x) | __float_as_uint(v[k].y) | __float_as_uint(v[k].z) |
+                      __float_as_uint(v[k].w);
+                a0 += v[k].x;
+                a1 += v[k].y;
+                a2 += v[k].z;
+                a3 += v[k].w;
+            }
         }
         acc = (a0 + a1) + (a2 + a3);
     }
@@ -270,15 +278,25 @@ __device__ __forceinline__ float kr_spec_sum(float *t, int n, unsigned char *lds
         int mask = 0, nseg = 0;
         bool run = false;
         int *re = p ? re1 : re0;
-        // two register buffers in turn: block blk + 1's LDS reads are issued
-        // before block blk's adds and arrive under them (a copy out of one
-        // prefetch buffer let the compiler issue the reads after the adds,
-        // so every block waited out the LDS latency)
-        float4 ba[4], bb[4];
+        // the bits at which the odd chain (the pair's upper one: rounding is
+        // monotone in the start) leaves b's binade (the terms are >= 0, so
+        // the chain only grows); the even lanes and chunk 0 never test
+        auto lim = [&](unsigned bb) { return p && c > 0 ? (bb & 0xFF800000u) + 0x00800000u : 0xFFFFFFFFu; };
+        unsigned blim = lim(b);
+        // four register buffers in turn: block blk + 3's LDS reads are issued
+        // before block blk's adds, so three blocks of adds cover their
+        // latency (one block ahead, every block waited for its reads; a copy
+        // out of one prefetch buffer let the compiler issue the reads after
+        // the adds)
+        float4 ba[4], bb[4], bc[4], bd[4];
 #pragma unroll
-        for (int q = 0; q < 4; q++) ba[q] = ((const float4 *)tc)[q];
+        for (int q = 0; q < 4; q++) {
+            ba[q] = ((const float4 *)tc)[q];
+            bb[q] = ((const float4 *)(tc + SC_BLK))[q];
+            bc[q] = ((const float4 *)(tc + 2 * SC_BLK))[q];
+        }
         auto block = [&](int blk, const float4 (&cur)[4], float4 (&nxt)[4]) {
-            const float4 *nb4 = (const float4 *)(tc + min(blk + 1, NB - 1) * SC_BLK);
+            const float4 *nb4 = (const float4 *)(tc + min(blk + 3, NB - 1) * SC_BLK);
 #pragma unroll
             for (int q = 0; q < 4; q++) nxt[q] = nb4[q];
             __builtin_amdgcn_sched_barrier(0);
@@ -291,6 +309,11 @@ __device__ __forceinline__ float kr_spec_sum(float *t, int n, unsigned char *lds
                 s = kr_fadd(s, cur[q].w);
             }
             const unsigned sb = __float_as_uint(s);
+            // no odd chain of the wave left its binade: every pair's run goes on
+            if (__builtin_expect(__ballot(sb >= blim) == 0ull, 1)) {
+                run = true;
+                return;
+            }
             unsigned cr = (c > 0) && ((sb ^ b) >> 23) != 0;
             cr |= sc_quad<SC_QP_SWAP>(cr);
             const unsigned nbits = sc_quad<SC_QP_EVEN>(sb) & ~1u;
@@ -302,15 +325,18 @@ __device__ __forceinline__ float kr_spec_sum(float *t, int n, unsigned char *lds
                 }
                 mask |= 1 << blk;
                 b = nbits;
+                blim = lim(b);
                 s = __uint_as_float(nbits | (unsigned)p);
                 run = false;
             } else {
                 run = true;
             }
         };
-        for (int blk = 0; blk < NB; blk += 2) {   // NB = L / 16 is even (L >= 128)
-            block(blk, ba, bb);
+        for (int blk = 0; blk < NB; blk += 4) {   // NB = L / 16 is a multiple of 4 (L >= 128)
+            block(blk, ba, bd);
             block(blk + 1, bb, ba);
+            block(blk + 2, bc, bb);
+            block(blk + 3, bd, bc);
         }
         if (run) {
             if (p == 0) rb[c * SC_NSEG + nseg] = (int)b;
@@ -345,6 +371,15 @@ __device__ __forceinline__ float kr_spec_sum(float *t, int n, unsigned char *lds
                 // the chunk's first run (a run before its first marked block)
                 const bool pre = lane < cnt && cc > 0 && (m & 1) == 0;
                 const bool brk = lane < cnt && m != 0;
+                // each lane's chunk's first marked block, read before the
+                // serial pass (which then adds it from registers)
+                float4 mb[4];
+                {
+                    const int fbl = m ? __builtin_ctz((unsigned)m) : 0;
+                    const float4 *q = (const float4 *)(t + sc_at(cl * L + fbl * SC_BLK, sh));
+#pragma unroll
+                    for (int k = 0; k < 4; k++) mb[k] = q[k];
+                }
                 unsigned d0 = pre ? e0 - b : 0u, d1 = pre ? e1 - b - 1u : 0u;
                 const unsigned long long bm = __ballot(brk);
                 // segments start at lane 0 and after each chunk with marks;
@@ -372,7 +407,15 @@ __device__ __forceinline__ float kr_spec_sum(float *t, int n, unsigned char *lds
                         const int mk = (int)sc_lane((unsigned)m, k);
                         const int fb = __builtin_ctz((unsigned)mk);
                         const int i0 = (g0 + k) * L + fb * SC_BLK;
-                        sv = sc_uni(__float_as_uint(sc_blk16(t, sh, i0, __uint_as_float(sv))));
+                        float x = __uint_as_float(sv);   // every lane adds its own block; lane k's is the one
+#pragma unroll
+                        for (int q = 0; q < 4; q++) {
+                            x = kr_fadd(x, mb[q].x);
+                            x = kr_fadd(x, mb[q].y);
+                            x = kr_fadd(x, mb[q].z);
+                            x = kr_fadd(x, mb[q].w);
+                        }
+                        sv = sc_lane(__float_as_uint(x), k);
                         if ((mk & (mk - 1)) == 0) {   // one mark: at most one run after it
                             if (fb + 1 < NB) {
                                 unsigned end;
