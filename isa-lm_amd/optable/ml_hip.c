@@ -33,8 +33,12 @@
  * (model/transformer.c:195-197) from staging rows that live on the device
  * here, so the attention call first converts this step's staging rows on
  * the device (the halves ml_f32_to_f16 gives, core/ml.c:39-53) into the
- * cache rows it reads; the host loop's copy is never read. No --imatrix
- * (the importance statistics read activations on the host, :250-255). */
+ * cache rows it reads; the host loop's copy is never read.
+ * --imatrix: the importance statistics are host reads of each matrix input
+ * right after its Q8_0 quantization (model/transformer.c:250-255, :272-301,
+ * :399-421). With --imatrix on the command line, every ml_k_quantize_q8 call
+ * runs at once (not queued) and copies its float input back to the host
+ * copy, so the host loop reads the device's values. */
 #include <math.h>
 #include <stdio.h>
 #include <stdlib.h>
@@ -82,6 +86,25 @@ typedef struct {
 static kh_packed g_pk[KH_MODELS];
 static int g_npk;
 static int g_reported;
+
+/* whether this process's command line holds --imatrix (app/ml_run.c:276):
+ * then the inputs of the Q8_0 quantizations are copied back to the host */
+static int g_imat = -1;
+static int imatrix_on(void) {
+    if (g_imat < 0) {
+        g_imat = 0;
+        FILE *f = fopen("/proc/self/cmdline", "rb");
+        if (f) {
+            static char buf[1 << 16];
+            const size_t n = fread(buf, 1, sizeof buf - 1, f);
+            fclose(f);
+            buf[n] = 0;
+            for (size_t i = 0; i < n; i += strlen(buf + i) + 1)
+                if (!strcmp(buf + i, "--imatrix")) g_imat = 1;
+        }
+    }
+    return g_imat;
+}
 
 static int ready(void) {
     if (krh_init() != ML_OK) return 0;
@@ -419,13 +442,15 @@ void ml_k_quantize_q8_hip(ml_qact *out, const float *x, int k) {
     const void *h[] = { out->q, out->d, x };
     const size_t len[] = { (size_t)k, F(k / QK), F(k) };
     const int wr[] = { 1, 1, 0 };
-    if (q_push(QOP_QUANT_Q8, k, 0, 0, 0.0f, 3, h, len, wr)) return;
+    const int imat = imatrix_on();
+    if (!imat && q_push(QOP_QUANT_Q8, k, 0, 0, 0.0f, 3, h, len, wr)) return;
     q_flush();
     kh_call c = { 0 };
     const float *xd = arg(&c, x, F(k), 1, 0);
     int8_t *q = arg(&c, out->q, (size_t)k, 0, 1);
     float *d = arg(&c, out->d, F(k / QK), 0, 1);
     if (!c.fail) krh_quantize_q8(q, d, xd, k, 1);
+    if (imat && !c.fail && xd != x && krh_copy_d2h((float *)x, xd, F(k)) != ML_OK) fail_call(krh_last_error());
     done(&c);
 }
 

@@ -100,6 +100,29 @@ def test_ml_bench_model_mode(kv, build, workdir):
     assert "error" not in r.stderr
 
 
+@pytest.mark.parametrize("build", ["hip", "hip128"])
+@pytest.mark.parametrize("name", ["c1_q8", "qwen_like_q4mix", "llama3_rope_gqa_q4", "softcap_embed_scale"])
+def test_ml_run_imatrix(name, build, workdir):
+    """--imatrix (app/ml_run.c:104-170, model/transformer.c:250-255): the
+    importance file written over the op table equals the reference's byte
+    for byte (its float64 sums of every matrix input's squares, per channel,
+    through the batched prefill and the per-token decode), and a second run
+    adds to it as the reference's does"""
+    path = model(name, workdir)
+    V = MODELS[name]["vocab"]
+    prompt = [int(t) for t in np.random.default_rng(6).integers(1, V, 24)]
+    a, b = path + ".scalar.imat", path + "." + build + ".imat"
+    for f in (a, b):
+        if os.path.exists(f):
+            os.remove(f)
+    for rep in range(2):
+        want, _ = O.ref_ml_run(path, prompt, 48, extra=["--imatrix", a])
+        got, err = O.ref_ml_run(path, prompt, 48, isa=build, extra=["--imatrix", b])
+        assert np.array_equal(got, want)
+        x, y = np.fromfile(a, dtype=np.uint8), np.fromfile(b, dtype=np.uint8)
+        assert x.size > 40 and np.array_equal(x, y), rep
+
+
 @pytest.mark.parametrize("batch", [None, 1])
 @pytest.mark.parametrize("name", ["c1_q8", "llama3_rope_gqa_q4", "qwen_like_q4mix"])
 def test_ml_run_kv_q8(name, batch, workdir):
