@@ -506,10 +506,7 @@ __global__ void __launch_bounds__(MV_THREADS, mv_wgs_per_cu(EPI)) k_matvec(const
         {
             const int i = min(i0, K - 16);
 #pragma unroll
-            for (int k = 0; k < XV; k++) {
-                xv[k] = *(const float4 *)(a.xf + i + 4 * k);
-                if (a.nw) wv[k] = *(const float4 *)(a.nw + i + 4 * k);
-            }
+            for (int k = 0; k < XV; k++) xv[k] = *(const float4 *)(a.xf + i + 4 * k);
         }
         float inv = 1.0f;
         if (a.nw) {
@@ -522,6 +519,15 @@ __global__ void __launch_bounds__(MV_THREADS, mv_wgs_per_cu(EPI)) k_matvec(const
                     *(float4 *)(sq + sc_at(i0, sh) + 4 * k) =
                         make_float4(kr_fmul(xv[k].x, xv[k].x), kr_fmul(xv[k].y, xv[k].y), kr_fmul(xv[k].z, xv[k].z),
                                     kr_fmul(xv[k].w, xv[k].w));
+            }
+            // the norm weights go out once x is in (every workgroup reads x
+            // at once; the weights, needed only by the quantization, return
+            // under the ordered sum), ahead of the weight stream, whose
+            // loads return after them
+            {
+                const int i = min(i0, K - 16);
+#pragma unroll
+                for (int k = 0; k < XV; k++) wv[k] = *(const float4 *)(a.nw + i + 4 * k);
             }
 #pragma unroll
             for (int d = 0; d < MV_DEPTH - 1; d++) load_item(S[d], I[d]);
