@@ -567,7 +567,14 @@ __device__ __forceinline__ void attn_mix(float *ao, const float *att, const KvVi
         if (sink == 0x5bd1 && max_seq < 0) ao[0] = 0.0f;   // keeps the reads (never true)
         return;
     }
-    const int steps = (ntiles + 2 + MX_D - 1) / MX_D * MX_D;   // every wave runs as many barriers
+    // the producers' loop runs in groups of MX_D steps (one per register
+    // slot) and may stop after a third (or half) of a group: the step count
+    // is rounded up to MX_S steps (every wave runs as many barriers). Whole
+    // groups ran up to 4 empty steps past the end (the 0.5B shape at 550
+    // positions: 12 steps for 8); a test after every step measured no
+    // better than one per third.
+    constexpr int MX_S = MX_D % 3 == 0 ? MX_D / 3 : MX_D % 2 == 0 ? MX_D / 2 : MX_D;
+    const int steps = (ntiles + 2 + MX_S - 1) / MX_S * MX_S;
     const size_t q_dim = (size_t)gridDim.x * group * hd;
 
     if (wave == 0) {
@@ -672,6 +679,7 @@ __device__ __forceinline__ void attn_mix(float *ao, const float *att, const KvVi
     for (int s0 = 0; s0 < steps; s0 += MX_D) {
 #pragma unroll
         for (int u = 0; u < MX_D; u++) {
+            if (u > 0 && u % MX_S == 0 && s0 + u >= steps) break;   // a part group ends the loop
             const int s = s0 + u;   // tile s sits in slot u
             // fenced for the scheduler: a step's products wait on its own
             // slot's loads only
