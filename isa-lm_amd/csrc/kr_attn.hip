@@ -567,14 +567,16 @@ __device__ __forceinline__ void attn_mix(float *ao, const float *att, const KvVi
         if (sink == 0x5bd1 && max_seq < 0) ao[0] = 0.0f;   // keeps the reads (never true)
         return;
     }
-    // the producers' loop runs in groups of MX_D steps (one per register
-    // slot) and may stop after a third (or half) of a group: the step count
-    // is rounded up to MX_S steps (every wave runs as many barriers). Whole
-    // groups ran up to 4 empty steps past the end (the 0.5B shape at 550
-    // positions: 12 steps for 8); a test after every step measured no
-    // better than one per third.
+    // Steps with a barrier: one per tile the producers write, rounded up to
+    // MX_S (every wave runs as many barriers); the adder's last two steps
+    // (the last tile's read, the last adds) follow without one. The
+    // producers' loop runs in groups of MX_D steps (one per register slot)
+    // and may stop after a third (or half) of a group: whole groups ran up
+    // to 4 empty steps past the end (the 0.5B shape at 550 positions: 12
+    // steps for 8); a test after every step measured no better than one per
+    // third.
     constexpr int MX_S = MX_D % 3 == 0 ? MX_D / 3 : MX_D % 2 == 0 ? MX_D / 2 : MX_D;
-    const int steps = (ntiles + 2 + MX_S - 1) / MX_S * MX_S;
+    const int steps = (ntiles + MX_S - 1) / MX_S * MX_S;
     const size_t q_dim = (size_t)gridDim.x * group * hd;
 
     if (wave == 0) {
@@ -583,7 +585,7 @@ __device__ __forceinline__ void attn_mix(float *ao, const float *att, const KvVi
         // registers read in step s - 1, so every LDS read has a whole tile
         // of adds to arrive in
         float o = 0.0f;
-        auto step = [&](int s, float4 *cur, float4 *nxt) {
+        auto step = [&](int s, float4 *cur, float4 *nxt, bool bar = true) {
             if (s - 1 >= 0 && s - 1 < ntiles) {
                 const float *P = prod[(s - 1) % 3] + lane * MX_TS;
 #pragma unroll
@@ -605,13 +607,19 @@ __device__ __forceinline__ void attn_mix(float *ao, const float *att, const KvVi
                     for (int r = 0; r < nt; r++) o = kr_fadd(o, P[r]);
                 }
             }
-            kr_lds_order();
-            __syncthreads();
+            if (bar) {
+                kr_lds_order();
+                __syncthreads();
+            }
         };
         float4 ta[MX_T / 4], tb[MX_T / 4];
         for (int s = 0; s < steps; s += 2) {
             step(s, ta, tb);
             if (s + 1 < steps) step(s + 1, tb, ta);
+        }
+        for (int s = steps; s < steps + 2; s++) {   // the producers are done: no barrier
+            if (s & 1) step(s, tb, ta, false);
+            else step(s, ta, tb, false);
         }
         if (j < group && d < min(DW, hd - c0)) ao[blockIdx.z * q_dim + (size_t)(g * group + j) * hd + c0 + d] = o;
         return;
