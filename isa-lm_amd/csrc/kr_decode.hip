@@ -646,6 +646,13 @@ __global__ void __launch_bounds__(MV_THREADS, mv_wgs_per_cu(EPI)) k_matvec(const
                     acc = kr_fadd(acc, r[k].w);
                 }
             }
+            for (; j + 4 <= cur.nbc; j += 4) {   // under 32 left (a 896-wide row's 28): 16-byte reads
+                const float4 r = *(const float4 *)(p + j);
+                acc = kr_fadd(acc, r.x);
+                acc = kr_fadd(acc, r.y);
+                acc = kr_fadd(acc, r.z);
+                acc = kr_fadd(acc, r.w);
+            }
             for (; j < cur.nbc; j++) acc = kr_fadd(acc, p[j]);
         }
         if (nchunk == 0) {   // the tile's last chunk: epilogue
