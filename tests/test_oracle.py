@@ -479,6 +479,41 @@ def test_forward_matches_reference(name, workdir):
     om.close()
 
 
+LONG = {
+    # the decode and batched attention at the context lengths of the 1B
+    # workload (4,000-token prompt), on a one-layer model so the reference's
+    # scalar loop runs it in seconds; llama3 RoPE scaling from position 64
+    "long_gqa_q4mix": dict(K.CONFIGS["llama1b_mixed"], dim=64, n_layers=1, n_heads=4, n_kv_heads=2,
+                           hidden_dim=128, vocab=256, max_seq=4200, std=0.1, rope_orig_max_seq=64),
+    # one KV head for all query heads, a Q8 model with f16 scales
+    "long_mqa_q8": dict(K.CONFIGS["llama8b_q8"], dim=64, n_layers=1, n_heads=2, n_kv_heads=1,
+                        hidden_dim=96, vocab=200, max_seq=2200, std=0.1),
+}
+
+
+@needs_ref
+@pytest.mark.parametrize("name", sorted(LONG))
+def test_long_context_matches_reference(name, workdir):
+    """every prefill row's logits over a prompt of max_seq - 200 tokens, and
+    the ids of 100 decode steps after it (the per-token attention at those
+    positions, ops/ops.c:124-180), equal the reference's ml_run"""
+    path = os.path.join(workdir, name + ".mlb")
+    K.gen_mlb(path, **LONG[name])
+    om = O.OracleModel(path)
+    V, P = om.cfg.vocab, om.cfg.max_seq - 200
+    toks = [int(t) for t in np.random.default_rng(17).integers(1, V, P)]
+    dump = path + ".logits"
+    O.ref_ml_run(path, toks, len(toks), dump=dump)
+    want = np.fromfile(dump, dtype=np.float32).reshape(len(toks), V)
+    got = om.prefill(toks, 0, logits=True)
+    assert np.array_equal(bits(got), bits(want))
+    om.close()
+    om = O.OracleModel(path)
+    ids_ref, _ = O.ref_ml_run(path, toks, P + 100)
+    assert np.array_equal(om.generate(toks, P + 100), ids_ref)
+    om.close()
+
+
 def test_hip_ml_run_guard_without_gpu(workdir):
     """the ISA=hip build keeps the reference's guard contract
     (app/main_guard.c:8-15): without a gfx950 device it exits 3"""
