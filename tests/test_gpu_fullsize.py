@@ -206,8 +206,10 @@ def test_route_workload_matches_reference(name):
 # ---- 2. the batched kernels at the prompt lengths ----
 
 def sample_tokens(T):
+    """the tile and chunk edges, and 64 tokens spread evenly over the step"""
     picks = {0, 1, 62, 63, 64, 127, 128, 254, 255, 256, 257, 511, 512, 1023, T // 3, T // 2, T - 65, T - 64,
              T - 2, T - 1}
+    picks |= {i * T // 64 + i % 7 for i in range(64)}
     return sorted(t for t in picks if 0 <= t < T)
 
 
@@ -245,7 +247,8 @@ def views(dev, kv_type, k, v, kd, vd):
                                                  (14, 2, 64, 1000, 1024), (6, 6, 48, 300, 300)])
 def test_attention_batch_prompt_lengths(dev, kv_type, nh, nkv, hd, T, max_seq):
     """a whole prompt's attention in one batched launch from position 0 (the
-    last case ends at row max_seq - 1), every sampled token bit-equal to the
+    last case ends at row max_seq - 1), every token (every third and the
+    sampled ones over the Q8 cache, whose oracle is slower) bit-equal to the
     oracle's attention at its position"""
     kvd, qd = nkv * hd, nh * hd
     Q = f32(RNG.normal(0, 1, (T, qd)))
@@ -260,7 +263,8 @@ def test_attention_batch_prompt_lengths(dev, kv_type, nh, nkv, hd, T, max_seq):
     cfg = K.MlConfig(n_heads=nh, n_kv_heads=nkv, head_dim=hd, kv_dim=kvd, q_dim=qd, max_seq=max_seq,
                      attn_scale=scale)
     scratch_ = np.zeros(max_seq, np.float32)
-    for t in sample_tokens(T):
+    toks = range(T) if kv_type != K.ML_Q8_0 else sorted(set(range(0, T, 3)) | set(sample_tokens(T)))
+    for t in toks:
         out = np.zeros(qd, np.float32)
         qt = f32(Q[t])
         oracle.kro_attention(out.ctypes.data, qt.ctypes.data, C.byref(hview), scratch_.ctypes.data, C.byref(cfg), t)
