@@ -889,35 +889,42 @@ __device__ __forceinline__ void attn_mix_batch(float *ao, const float *att, cons
     if (j < group && d < cw) ao[(size_t)(g * group + j) * hd + c0 + d] = o;
 }
 
-// Batched (prefill) mix without a window, by blocks of MK_W tokens: a
-// workgroup per (KV head g, DW dims from c0, MK_W consecutive tokens), one
-// wave per token, lane = (head j of the group, dim d); each lane runs its chain
-// o += a_t * v_t,d over positions t in order (k_scalar.c:119-122), each
-// product rounded before its add. The block's waves share each V tile, staged
-// once in LDS as [dim][position] so one 16-byte read gives a lane 4
-// positions. The weights take no LDS: a lane holds its head's weights of 16
-// positions in one register (lane d of a 16-lane row holds position t0 + d),
-// and a DPP row broadcast (row_newbcast) hands position t0 + k's weight to
-// every lane of the row as the multiply's operand. So a row of 16 lanes must
-// hold one head: DW >= 16. Tiles are double-buffered: tile k + 1 is stored
-// while tile k is read, the loads of tile k + 2 already in flight. F16 and Q8
-// cache rows are widened exactly as they are staged; over the Q8 cache a
-// lane's weight is a_t * dv_t (the row's scale, k_scalar.c:151) before the
-// broadcast, as in the per-token mix.
-constexpr int MK_W = 4, MK_T = 64, MK_TS = MK_T + 4;
+// Batched (prefill) mix without a window, by blocks of MK_W x MK_U tokens: a
+// workgroup per (KV head g, DW dims from c0, MK_W MK_U consecutive tokens),
+// MK_U consecutive tokens per wave, lane = (head j of the group, dim d); each
+// lane runs its tokens' chains o += a_t * v_t,d over positions t in order
+// (k_scalar.c:119-122), each product rounded before its add. The block's waves
+// share each V tile, staged once in LDS as [dim][position] so one 16-byte read
+// gives a lane 4 positions, and each V value read serves the lane's MK_U
+// chains, whose adds interleave (a chain's next add need not wait for its
+// last). The weights take no LDS: a lane holds its head's weights of 16
+// positions in one register a token (lane d of a 16-lane row holds position
+// t0 + d), and a DPP row broadcast (row_newbcast) hands position t0 + k's
+// weight to every lane of the row as the multiply's operand. So a row of 16
+// lanes must hold one head: DW >= 16. Tiles are double-buffered: tile k + 1
+// is stored while tile k is read, the loads of tile k + 2 already in flight.
+// F16 and Q8 cache rows are widened exactly as they are staged; over the Q8
+// cache a lane's weight is a_t * dv_t (the row's scale, k_scalar.c:151)
+// before the broadcast, as in the per-token mix.
+constexpr int MK_W = 4, MK_U = 2, MK_T = 64, MK_TS = MK_T + 4;
 
 template <int K> __device__ __forceinline__ float row_bcast(float v) {
     return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x150 + K, 0xF, 0xF, false));
 }
 
-// o += a_{t0+4q+i} * v4.i for i < 4, positions t0 + 4q + i of a 16-position
-// block whose weights sit in a (lane k of each row: position t0 + k)
-template <int Q>
-__device__ __forceinline__ void mk_quad(float &o, float a, float4 v) {
-    o = kr_fadd(o, kr_fmul(row_bcast<4 * Q + 0>(a), v.x));
-    o = kr_fadd(o, kr_fmul(row_bcast<4 * Q + 1>(a), v.y));
-    o = kr_fadd(o, kr_fmul(row_bcast<4 * Q + 2>(a), v.z));
-    o = kr_fadd(o, kr_fmul(row_bcast<4 * Q + 3>(a), v.w));
+// o[u] += a_{t0+4q+i} * v4.i for i < 4 and every token u, positions
+// t0 + 4q + i of a 16-position block whose weights sit in a[u] (lane k of
+// each row: position t0 + k); the tokens' adds of one position go out together
+template <int Q, int U>
+__device__ __forceinline__ void mk_quad(float (&o)[U], const float (&a)[U], float4 v) {
+#pragma unroll
+    for (int u = 0; u < U; u++) o[u] = kr_fadd(o[u], kr_fmul(row_bcast<4 * Q + 0>(a[u]), v.x));
+#pragma unroll
+    for (int u = 0; u < U; u++) o[u] = kr_fadd(o[u], kr_fmul(row_bcast<4 * Q + 1>(a[u]), v.y));
+#pragma unroll
+    for (int u = 0; u < U; u++) o[u] = kr_fadd(o[u], kr_fmul(row_bcast<4 * Q + 2>(a[u]), v.z));
+#pragma unroll
+    for (int u = 0; u < U; u++) o[u] = kr_fadd(o[u], kr_fmul(row_bcast<4 * Q + 3>(a[u]), v.w));
 }
 
 template <int DW, int KT>
@@ -925,18 +932,24 @@ __global__ void __launch_bounds__(64 * MK_W) k_attn_mix_blk(float *ao, const flo
                                                             int hd, int kv_dim, int max_seq, const int *pos_p,
                                                             int ntok) {
     static_assert(DW >= 16, "a 16-lane row must hold one head");
+    constexpr int U = MK_U;
     constexpr int QPR = DW / 4;                 // float4 per staged row of DW dims
     constexpr int RPP = 64 * MK_W / QPR;        // rows the workgroup stages per pass
     constexpr int NP = MK_T / RPP;              // passes per tile
     __shared__ __align__(16) float vt[2][DW * MK_TS];
     __shared__ float dvs[2][KT == KV_Q8 ? MK_T : 1];   // Q8: the tile's V row scales
-    const int g = blockIdx.x, c0 = blockIdx.y * DW, z0 = blockIdx.z * MK_W, tid = threadIdx.x;
+    const int g = blockIdx.x, c0 = blockIdx.y * DW, z0 = blockIdx.z * MK_W * U, tid = threadIdx.x;
     const int wave = tid >> 6, lane = tid & 63, j = lane / DW, d = lane % DW;
-    const int z = z0 + wave, pos0 = *pos_p;
-    const int n = z < ntok ? pos0 + z + 1 : 0;                  // positions this wave's token attends
-    const int nmax = pos0 + min(z0 + MK_W, ntok);               // the block's last token's
+    const int zw = z0 + wave * U, pos0 = *pos_p;      // the wave's first token
+    const int nmax = pos0 + min(z0 + MK_W * U, ntok);   // positions the block's last token attends
     const int n_heads = gridDim.x * group, cw = min(DW, hd - c0), ntiles = (nmax + MK_T - 1) / MK_T;
-    const float *arow = att + ((size_t)min(z, ntok - 1) * n_heads + (size_t)g * group + min(j, group - 1)) * max_seq;
+    int n[U];   // positions token zw + u attends (0 past the last token)
+    const float *arow[U];
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+        n[u] = zw + u < ntok ? pos0 + zw + u + 1 : 0;
+        arow[u] = att + ((size_t)min(zw + u, ntok - 1) * n_heads + (size_t)g * group + min(j, group - 1)) * max_seq;
+    }
     const size_t vbase = (size_t)g * hd + c0;   // element offset of the chunk in a V row
     // staging slot of this thread in pass p: row p * RPP + srow, dims scol .. scol + 3
     const int srow = tid / QPR, scol = min(4 * (tid % QPR), cw - 4);
@@ -964,12 +977,16 @@ __global__ void __launch_bounds__(64 * MK_W) k_attn_mix_blk(float *ao, const flo
     };
     // the weights of a tile, loaded two tiles ahead like V: one tile's adds
     // are shorter than a load's round trip
-    auto a_load = [&](int tile, float *a) {
+    auto a_load = [&](int tile, float (&a)[U][MK_T / 16]) {
 #pragma unroll
-        for (int b = 0; b < MK_T / 16; b++) a[b] = arow[min(tile * MK_T + 16 * b + (lane & 15), max_seq - 1)];
+        for (int u = 0; u < U; u++)
+#pragma unroll
+            for (int b = 0; b < MK_T / 16; b++) a[u][b] = arow[u][min(tile * MK_T + 16 * b + (lane & 15), max_seq - 1)];
     };
-    float o = 0.0f;
-    float acur[MK_T / 16], anext[MK_T / 16], anext2[MK_T / 16];
+    float o[U];
+#pragma unroll
+    for (int u = 0; u < U; u++) o[u] = 0.0f;
+    float acur[U][MK_T / 16], anext[U][MK_T / 16], anext2[U][MK_T / 16];
     stage_load(0);
     stage_store(0);
     a_load(0, acur);
@@ -985,11 +1002,13 @@ __global__ void __launch_bounds__(64 * MK_W) k_attn_mix_blk(float *ao, const flo
         // the weights at the end of the step leave this load in flight
         stage_load(min(k + 2, ntiles - 1));
         const float *V = vt[buf] + d * MK_TS;
-        float aw[MK_T / 16];   // the weights (Q8: a_t * dv_t)
+        float aw[MK_T / 16][U];   // the weights (Q8: a_t * dv_t)
 #pragma unroll
         for (int b = 0; b < MK_T / 16; b++)
-            aw[b] = KT == KV_Q8 ? kr_fmul(acur[b], dvs[buf][KT == KV_Q8 ? 16 * b + (lane & 15) : 0]) : acur[b];
-        if (t0 + MK_T <= n) {   // a full tile for this token
+#pragma unroll
+            for (int u = 0; u < U; u++)
+                aw[b][u] = KT == KV_Q8 ? kr_fmul(acur[u][b], dvs[buf][KT == KV_Q8 ? 16 * b + (lane & 15) : 0]) : acur[u][b];
+        if (t0 + MK_T <= n[0]) {   // a full tile for every token of the wave (tokens past the last are not stored)
 #pragma unroll
             for (int b = 0; b < MK_T / 16; b++) {
                 const float4 v0 = *(const float4 *)(V + 16 * b), v1 = *(const float4 *)(V + 16 * b + 4);
@@ -999,27 +1018,166 @@ __global__ void __launch_bounds__(64 * MK_W) k_attn_mix_blk(float *ao, const flo
                 mk_quad<2>(o, aw[b], v2);
                 mk_quad<3>(o, aw[b], v3);
             }
-        } else if (t0 < n) {    // the token's last tile: its live positions only
+        } else {   // the last tiles: each token its live positions
 #pragma unroll
-            for (int b = 0; b < MK_T / 16; b++) {
-                const float ab = aw[b];
-                float w[16];
-                w[0] = row_bcast<0>(ab); w[1] = row_bcast<1>(ab); w[2] = row_bcast<2>(ab); w[3] = row_bcast<3>(ab);
-                w[4] = row_bcast<4>(ab); w[5] = row_bcast<5>(ab); w[6] = row_bcast<6>(ab); w[7] = row_bcast<7>(ab);
-                w[8] = row_bcast<8>(ab); w[9] = row_bcast<9>(ab); w[10] = row_bcast<10>(ab); w[11] = row_bcast<11>(ab);
-                w[12] = row_bcast<12>(ab); w[13] = row_bcast<13>(ab); w[14] = row_bcast<14>(ab); w[15] = row_bcast<15>(ab);
-                for (int i = 0; i < 16 && t0 + 16 * b + i < n; i++) o = kr_fadd(o, kr_fmul(w[i], V[16 * b + i]));
+            for (int u = 0; u < U; u++) {
+                if (t0 >= n[u]) continue;
+#pragma unroll
+                for (int b = 0; b < MK_T / 16; b++) {
+                    const float ab = aw[b][u];
+                    float w[16];
+                    w[0] = row_bcast<0>(ab); w[1] = row_bcast<1>(ab); w[2] = row_bcast<2>(ab); w[3] = row_bcast<3>(ab);
+                    w[4] = row_bcast<4>(ab); w[5] = row_bcast<5>(ab); w[6] = row_bcast<6>(ab); w[7] = row_bcast<7>(ab);
+                    w[8] = row_bcast<8>(ab); w[9] = row_bcast<9>(ab); w[10] = row_bcast<10>(ab); w[11] = row_bcast<11>(ab);
+                    w[12] = row_bcast<12>(ab); w[13] = row_bcast<13>(ab); w[14] = row_bcast<14>(ab); w[15] = row_bcast<15>(ab);
+                    for (int i = 0; i < 16 && t0 + 16 * b + i < n[u]; i++) o[u] = kr_fadd(o[u], kr_fmul(w[i], V[16 * b + i]));
+                }
             }
         }
 #pragma unroll
-        for (int b = 0; b < MK_T / 16; b++) {
-            acur[b] = anext[b];
-            anext[b] = anext2[b];
-        }
+        for (int u = 0; u < U; u++)
+#pragma unroll
+            for (int b = 0; b < MK_T / 16; b++) {
+                acur[u][b] = anext[u][b];
+                anext[u][b] = anext2[u][b];
+            }
         kr_lds_order();
         __syncthreads();
     }
-    if (z < ntok && j < group && d < cw) ao[(size_t)z * n_heads * hd + (size_t)(g * group + j) * hd + c0 + d] = o;
+    if (j < group && d < cw) {
+#pragma unroll
+        for (int u = 0; u < U; u++)
+            if (zw + u < ntok) ao[(size_t)(zw + u) * n_heads * hd + (size_t)(g * group + j) * hd + c0 + d] = o[u];
+    }
+}
+
+// Batched (prefill) mix without a window for heads of HD = 64 or 128 dims,
+// blocked in registers: the rows (token z, query head j) of KV head g,
+// numbered z * group + j, go to workgroups RB_R at a time (the longest
+// first), and lane (row group rg, dim group dg) of a workgroup owns the
+// 4 x HD / 16 outputs of rows 4 rg .. 4 rg + 3 and dims 64 k + 4 dg + i: one
+// chain o += a_t * v_t,d per output over positions t in order
+// (k_scalar.c:119-122), each product rounded before its add. Per tile of
+// RB_T positions the weights [row][position] (Q8: a_t * dv_t, the per-token
+// kernel's product) and the V rows [position][dim] (F16 widened, Q8 as its
+// int8 values) are staged in LDS; per 4 positions a lane reads its rows' 4
+// weights and, per position, its dims' V values, 16-byte reads that feed
+// every product they take part in (4 x HD / 16 chains a lane, 2 to 4 reads
+// for 64 to 128 multiplies and as many adds: no broadcasts of a weight
+// across lanes). In the tiles past some row's own positions a select leaves
+// those terms out of that row's sums, so no weight or V value there (rows of
+// later tokens, stale rows) reaches them. The next tile's loads are in flight
+// while a tile is summed.
+constexpr int RB_R = 64, RB_T = 64;
+template <int HD, int KT>
+__global__ void __launch_bounds__(256) k_attn_mix_rb(float *ao, const float *att, const KvView kv, int group,
+                                                     int kv_dim, int max_seq, const int *pos_p, int ntok) {
+    constexpr int DPL = HD / 16, NQ = DPL / 4;        // dims a lane, in NQ quads 64 apart
+    constexpr int AS = RB_T + 4;                      // weight row stride (floats)
+    constexpr int NA = RB_R * RB_T / 4 / 256;         // 4-weight loads a thread stages per tile
+    constexpr int NV = RB_T * HD / 4 / 256;           // 4-element V loads a thread stages per tile
+    __shared__ __align__(16) float as[RB_R * AS];
+    __shared__ __align__(16) float vs[RB_T * HD];
+    const int g = blockIdx.x, tid = threadIdx.x, wave = tid >> 6, dg = tid & 15, rg = tid >> 4;
+    const int nrow = ntok * group, R0 = (gridDim.y - 1 - blockIdx.y) * RB_R;
+    const int pos0 = *pos_p, n_heads = gridDim.x * group;
+    const int nlast = pos0 + (min(R0 + RB_R, nrow) - 1) / group + 1;   // positions the block's last row attends
+    const int ntl = (nlast + RB_T - 1) / RB_T;
+    const int zw = (R0 + 16 * wave) / group;   // the token of the wave's first row
+    typename Kv4<KT>::T vr[NV];
+    float4 ar[NA];
+    float dv[NA][4];   // Q8: the V row scales of the staged weights' positions
+    auto load = [&](int t0) {
+#pragma unroll
+        for (int u = 0; u < NV; u++) {
+            const int e = tid + 256 * u, p = e / (HD / 4), c4 = e % (HD / 4);
+            vr[u] = Kv4<KT>::load(kv.v, (size_t)min(t0 + p, nlast - 1) * kv_dim + (size_t)g * HD + 4 * c4);
+        }
+#pragma unroll
+        for (int u = 0; u < NA; u++) {
+            const int e = tid + 256 * u, rr = e / (RB_T / 4), q4 = e % (RB_T / 4);
+            const int R = min(R0 + rr, nrow - 1), z = R / group, j = R - z * group;
+            ar[u] = *(const float4 *)(att + ((size_t)z * n_heads + (size_t)g * group + j) * max_seq +
+                                      min(t0 + 4 * q4, max_seq - 4));
+            if (KT == KV_Q8) {
+#pragma unroll
+                for (int i = 0; i < 4; i++) dv[u][i] = kv.vd[(size_t)min(t0 + 4 * q4 + i, nlast - 1) * kv.n_kv + g];
+            }
+        }
+    };
+    float acc[4][DPL];
+#pragma unroll
+    for (int r = 0; r < 4; r++)
+#pragma unroll
+        for (int c = 0; c < DPL; c++) acc[r][c] = 0.0f;
+    load(0);
+    for (int ti = 0; ti < ntl; ti++) {
+        const int t0 = ti * RB_T;
+        __syncthreads();   // the last tile is read
+#pragma unroll
+        for (int u = 0; u < NV; u++) {
+            const int e = tid + 256 * u;
+            *(float4 *)(vs + 4 * e) = Kv4<KT>::wide(vr[u]);   // [position][dim]: e = p HD / 4 + c4
+        }
+#pragma unroll
+        for (int u = 0; u < NA; u++) {
+            const int e = tid + 256 * u, rr = e / (RB_T / 4), q4 = e % (RB_T / 4);
+            float4 a = ar[u];
+            if (KT == KV_Q8)
+                a = make_float4(kr_fmul(a.x, dv[u][0]), kr_fmul(a.y, dv[u][1]), kr_fmul(a.z, dv[u][2]),
+                                kr_fmul(a.w, dv[u][3]));
+            *(float4 *)(as + rr * AS + 4 * q4) = a;
+        }
+        __syncthreads();
+        if (ti + 1 < ntl) load(t0 + RB_T);
+        const float *ap = as + 4 * rg * AS, *vp = vs + 4 * dg;
+        auto run = [&](auto upto) {
+            constexpr bool UPTO = decltype(upto)::value;
+            int lim[4];   // UPTO: position t0 + k counts for row r iff k <= lim[r]
+            if (UPTO) {
+#pragma unroll
+                for (int r = 0; r < 4; r++) lim[r] = pos0 + (R0 + 4 * rg + r) / group - t0;
+            }
+#pragma unroll 2
+            for (int t = 0; t < RB_T; t += 4) {
+                float4 a[4];
+#pragma unroll
+                for (int r = 0; r < 4; r++) a[r] = *(const float4 *)(ap + r * AS + t);
+#pragma unroll
+                for (int k = 0; k < 4; k++) {
+                    float4 v[NQ];
+#pragma unroll
+                    for (int q = 0; q < NQ; q++) v[q] = *(const float4 *)(vp + (t + k) * HD + 64 * q);
+#pragma unroll
+                    for (int r = 0; r < 4; r++) {
+                        const float w = k == 0 ? a[r].x : k == 1 ? a[r].y : k == 2 ? a[r].z : a[r].w;
+                        const bool in = !UPTO || t + k <= lim[r];
+#pragma unroll
+                        for (int q = 0; q < NQ; q++) {
+                            const float4 x = v[q];
+                            float *o = acc[r] + 4 * q;
+                            o[0] = in ? kr_fadd(o[0], kr_fmul(w, x.x)) : o[0];
+                            o[1] = in ? kr_fadd(o[1], kr_fmul(w, x.y)) : o[1];
+                            o[2] = in ? kr_fadd(o[2], kr_fmul(w, x.z)) : o[2];
+                            o[3] = in ? kr_fadd(o[3], kr_fmul(w, x.w)) : o[3];
+                        }
+                    }
+                }
+            }
+        };
+        if (t0 + RB_T - 1 <= pos0 + zw) run(std::false_type{});   // every position counts for every row of the wave
+        else run(std::true_type{});
+    }
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        const int R = R0 + 4 * rg + r;
+        if (R >= nrow) continue;
+        const int z = R / group, j = R - z * group;
+        float *dst = ao + (size_t)z * n_heads * HD + (size_t)(g * group + j) * HD + 4 * dg;
+#pragma unroll
+        for (int q = 0; q < NQ; q++)
+            *(float4 *)(dst + 64 * q) = make_float4(acc[r][4 * q], acc[r][4 * q + 1], acc[r][4 * q + 2], acc[r][4 * q + 3]);
+    }
 }
 
 template <int DW>
@@ -1078,9 +1236,20 @@ template <int KT, int DW>
 static void launch_mix(const dim3 &grid, int ntok, float *ao, const float *att, const KvView &kv, int group, int hd,
                        int kv_dim, int max_seq, int window, const int *pos) {
     const float *vc = (const float *)kv.v;
+    if (ntok > 1 && window == 0 && (hd == 64 || hd == 128) && max_seq % 4 == 0) {
+        // prefill without a window, 64- or 128-dim heads: register-blocked rows
+        const dim3 rgrid(grid.x, (ntok * group + RB_R - 1) / RB_R, 1);
+        if (hd == 64)
+            hipLaunchKernelGGL((k_attn_mix_rb<64, KT>), rgrid, dim3(256), 0, kr_stream(), ao, att, kv, group, kv_dim,
+                               max_seq, pos, ntok);
+        else
+            hipLaunchKernelGGL((k_attn_mix_rb<128, KT>), rgrid, dim3(256), 0, kr_stream(), ao, att, kv, group, kv_dim,
+                               max_seq, pos, ntok);
+        return;
+    }
     if constexpr (DW >= 16) {
         if (ntok > 1 && window == 0) {   // prefill without a window: blocks of MK_W tokens share the V tiles
-            const dim3 bgrid(grid.x, grid.y, (ntok + MK_W - 1) / MK_W);
+            const dim3 bgrid(grid.x, grid.y, (ntok + MK_W * MK_U - 1) / (MK_W * MK_U));
             hipLaunchKernelGGL((k_attn_mix_blk<DW, KT>), bgrid, dim3(64 * MK_W), 0, kr_stream(), ao, att, kv, group,
                                hd, kv_dim, max_seq, pos, ntok);
             return;

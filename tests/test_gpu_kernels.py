@@ -591,7 +591,11 @@ def test_matmul_qkv_matches_decode(dev, dim, nh, nkv, hd, typ, vtyp, bias):
 
 @pytest.mark.parametrize("nh,nkv,hd,pos0,T,window", [(6, 6, 48, 0, 40, 0), (32, 8, 128, 100, 70, 0),
                                                      (14, 2, 64, 3, 200, 0), (8, 2, 64, 10, 50, 7),
-                                                     (8, 4, 256, 5, 40, 0), (4, 1, 256, 100, 30, 64)])
+                                                     (8, 4, 256, 5, 40, 0), (4, 1, 256, 100, 30, 64),
+                                                     # the MFMA kernels' groups 1, 2, 4 (4, 2, 1 row
+                                                     # blocks a workgroup), the last ending at row 511
+                                                     (8, 8, 64, 37, 90, 0), (16, 8, 128, 0, 33, 0),
+                                                     (32, 8, 64, 5, 100, 0), (8, 4, 64, 450, 62, 0)])
 def test_attention_batch_matches_decode(dev, nh, nkv, hd, pos0, T, window):
     max_seq = 512
     kvd, qd = nkv * hd, nh * hd
@@ -608,6 +612,37 @@ def test_attention_batch_matches_decode(dev, nh, nkv, hd, pos0, T, window):
     cfg = K.MlConfig(n_heads=nh, n_kv_heads=nkv, head_dim=hd, kv_dim=kvd, q_dim=qd, max_seq=max_seq,
                      attn_scale=scale)
     kvl = O.KvLayer(kc.ctypes.data, vc.ctypes.data, None, None, None, None, window, None, None)
+    scratch = np.zeros(max_seq, np.float32)
+    for t in range(T):
+        out = np.zeros(qd, np.float32)
+        qt = f32(Q[t])
+        oracle.kro_attention(out.ctypes.data, qt.ctypes.data, C.byref(kvl), scratch.ctypes.data, C.byref(cfg),
+                             pos0 + t)
+        assert np.array_equal(bits(got[t]), bits(out)), t
+
+
+@pytest.mark.parametrize("nh,nkv,hd", [(32, 8, 128), (8, 8, 64), (16, 8, 64)])
+def test_attention_batch_stale_rows(dev, nh, nkv, hd):
+    """cache rows past the last token's position and score rows past each
+    token's own position hold NaN (rows still to be written, stale scores):
+    the batched attention lets none of them reach a result"""
+    max_seq, pos0, T = 512, 40, 75
+    kvd, qd = nkv * hd, nh * hd
+    Q = f32(RNG.normal(0, 1, (T, qd)))
+    kc = f32(RNG.normal(0, 1, max_seq * kvd))
+    vc = f32(RNG.normal(0, 1, max_seq * kvd))
+    kc[(pos0 + T) * kvd:] = np.nan
+    vc[(pos0 + T) * kvd:] = np.nan
+    scale = float(np.float32(1.0) / np.sqrt(np.float32(hd)))
+    ao, att = dev.zeros(4 * T * qd), dev.put(np.full(T * nh * max_seq, np.nan, np.float32))
+    K.hip.krh_attention_batch(ao.ptr, att.ptr, dev.put(Q).ptr, dev.put(kc).ptr, dev.put(vc).ptr, nh, nkv, hd,
+                              max_seq, 0, scale, dev.put(np.array([pos0], np.int32)).ptr, T, pos0 + T - 1)
+    ok()
+    got = ao.get(np.float32, T * qd).reshape(T, qd)
+    assert not np.isnan(got).any()
+    cfg = K.MlConfig(n_heads=nh, n_kv_heads=nkv, head_dim=hd, kv_dim=kvd, q_dim=qd, max_seq=max_seq,
+                     attn_scale=scale)
+    kvl = O.KvLayer(kc.ctypes.data, vc.ctypes.data, None, None, None, None, 0, None, None)
     scratch = np.zeros(max_seq, np.float32)
     for t in range(T):
         out = np.zeros(qd, np.float32)

@@ -148,7 +148,8 @@ def test_attention_kv(dev, kv_type, nh, nkv, hd, pos, window):
 @pytest.mark.parametrize("kv_type", [K.ML_F16, K.ML_Q8_0])
 @pytest.mark.parametrize("nh,nkv,hd,pos0,T,window", [(6, 6, 48, 0, 40, 0), (32, 8, 128, 100, 70, 0),
                                                      (14, 2, 64, 3, 200, 0), (8, 2, 64, 10, 50, 7),
-                                                     (8, 4, 256, 5, 40, 0), (4, 1, 256, 100, 30, 64)])
+                                                     (8, 4, 256, 5, 40, 0), (4, 1, 256, 100, 30, 64),
+                                                     (16, 8, 64, 7, 45, 0), (8, 8, 128, 200, 70, 0)])
 def test_attention_kv_batch(dev, kv_type, nh, nkv, hd, pos0, T, window):
     """batched attention over F16 and Q8 caches against the oracle's per-token
     attention"""
