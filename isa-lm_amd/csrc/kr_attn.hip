@@ -191,6 +191,110 @@ __global__ void __launch_bounds__(AT_THREADS) k_attn_scores_blk(float *att, cons
     }
 }
 
+// Batched (prefill) scores without a window for heads of HD = 64 or 128
+// dims, blocked in registers: the rows (token z, query head j) of KV head g,
+// numbered z * group + j, go to workgroups RB_R at a time, each over a chunk
+// of RB_PC tiles of RB_T positions. The workgroup stages its rows' queries
+// in LDS once and each K tile in turn (F16 rows widened exactly), rows HD + 4
+// floats apart; lane (row group rg, position group pg) owns the scores of rows
+// 4 rg .. 4 rg + 3 at positions pg + 16 k (k < 4): per 4 dims it reads 4 query
+// and 4 K 16-byte values, which feed 64 multiplies and 64 adds, each of its
+// 16 sums s = sum_i q_i k_i in index order, then * scale, as in the per-token
+// kernel. A row stores only the positions its token attends. The next tile's
+// loads are in flight while a tile is summed.
+constexpr int RB_R = 64, RB_T = 64;   // rows of a register-blocked workgroup; positions of its tiles
+constexpr int RB_PC = 8;             // K tiles per scores workgroup
+template <int HD, int KT>
+__global__ void __launch_bounds__(256) k_attn_scores_rb(float *att, const float *q, const KvView kv, int group,
+                                                        int kv_dim, int max_seq, float scale, const int *pos_p,
+                                                        int ntok) {
+    constexpr int S = HD + 4;                     // LDS row stride (floats)
+    constexpr int NL = RB_T * HD / 4 / 256;       // 4-element K loads a thread stages per tile
+    constexpr int NQL = RB_R * HD / 4 / 256;      // query float4 a thread stages
+    __shared__ __align__(16) float qs[RB_R * S];
+    __shared__ __align__(16) float ks[RB_T * S];
+    const int g = blockIdx.x, tid = threadIdx.x, pg = tid & 15, rg = tid >> 4;
+    const int nrow = ntok * group, R0 = blockIdx.y * RB_R;
+    const int pos0 = *pos_p, n_heads = gridDim.x * group;
+    const int nlast = pos0 + (min(R0 + RB_R, nrow) - 1) / group + 1;   // positions the block's last row attends
+    const int p0 = blockIdx.z * RB_PC * RB_T;
+    if (p0 >= nlast) return;
+    const int ntl = min(RB_PC, (nlast - p0 + RB_T - 1) / RB_T);
+#pragma unroll
+    for (int u = 0; u < NQL; u++) {
+        const int e = tid + 256 * u, rr = e / (HD / 4), c4 = e % (HD / 4);
+        const int R = min(R0 + rr, nrow - 1), z = R / group, j = R - z * group;
+        *(float4 *)(qs + rr * S + 4 * c4) = *(const float4 *)(q + ((size_t)z * n_heads + (size_t)g * group + j) * HD + 4 * c4);
+    }
+    typename Kv4<KT>::T kr[NL];
+    auto load = [&](int t0) {
+#pragma unroll
+        for (int u = 0; u < NL; u++) {
+            const int e = tid + 256 * u, p = e / (HD / 4), c4 = e % (HD / 4);
+            kr[u] = Kv4<KT>::load(kv.k, (size_t)min(t0 + p, nlast - 1) * kv_dim + (size_t)g * HD + 4 * c4);
+        }
+    };
+    int zr[4];   // the tokens of the lane's rows (past the last row: -1)
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        const int R = R0 + 4 * rg + r;
+        zr[r] = R < nrow ? R / group : -1;
+    }
+    load(p0);
+    for (int ti = 0; ti < ntl; ti++) {
+        const int t0 = p0 + ti * RB_T;
+        __syncthreads();   // the last tile is read
+#pragma unroll
+        for (int u = 0; u < NL; u++) {
+            const int e = tid + 256 * u, p = e / (HD / 4), c4 = e % (HD / 4);
+            *(float4 *)(ks + p * S + 4 * c4) = Kv4<KT>::wide(kr[u]);
+        }
+        __syncthreads();
+        if (ti + 1 < ntl) load(t0 + RB_T);
+        float acc[4][4];
+#pragma unroll
+        for (int r = 0; r < 4; r++)
+#pragma unroll
+            for (int k = 0; k < 4; k++) acc[r][k] = 0.0f;
+        const float *qp = qs + 4 * rg * S, *kp = ks + pg * S;
+#pragma unroll 4
+        for (int i = 0; i < HD; i += 4) {
+            float4 a[4], b[4];
+#pragma unroll
+            for (int r = 0; r < 4; r++) a[r] = *(const float4 *)(qp + r * S + i);
+#pragma unroll
+            for (int k = 0; k < 4; k++) b[k] = *(const float4 *)(kp + 16 * k * S + i);
+#pragma unroll
+            for (int r = 0; r < 4; r++)
+#pragma unroll
+                for (int k = 0; k < 4; k++) acc[r][k] = kr_fadd(acc[r][k], kr_fmul(a[r].x, b[k].x));
+#pragma unroll
+            for (int r = 0; r < 4; r++)
+#pragma unroll
+                for (int k = 0; k < 4; k++) acc[r][k] = kr_fadd(acc[r][k], kr_fmul(a[r].y, b[k].y));
+#pragma unroll
+            for (int r = 0; r < 4; r++)
+#pragma unroll
+                for (int k = 0; k < 4; k++) acc[r][k] = kr_fadd(acc[r][k], kr_fmul(a[r].z, b[k].z));
+#pragma unroll
+            for (int r = 0; r < 4; r++)
+#pragma unroll
+                for (int k = 0; k < 4; k++) acc[r][k] = kr_fadd(acc[r][k], kr_fmul(a[r].w, b[k].w));
+        }
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            if (zr[r] < 0) continue;
+            const int R = R0 + 4 * rg + r, j = R - zr[r] * group;
+            float *dst = att + ((size_t)zr[r] * n_heads + (size_t)g * group + j) * max_seq;
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const int p = t0 + pg + 16 * k;
+                if (p <= pos0 + zr[r]) dst[p] = kr_fmul(acc[r][k], scale);
+            }
+        }
+    }
+}
+
 template <int KT, int TT>
 __global__ void __launch_bounds__(AT_THREADS) k_attn_scores_kv(float *att, const float *q, const KvView kv, int group,
                                                                int hd, int kv_dim, int max_seq, int window, float scale,
@@ -1068,7 +1172,6 @@ __global__ void __launch_bounds__(64 * MK_W) k_attn_mix_blk(float *ao, const flo
 // those terms out of that row's sums, so no weight or V value there (rows of
 // later tokens, stale rows) reaches them. The next tile's loads are in flight
 // while a tile is summed.
-constexpr int RB_R = 64, RB_T = 64;
 template <int HD, int KT>
 __global__ void __launch_bounds__(256) k_attn_mix_rb(float *ao, const float *att, const KvView kv, int group,
                                                      int kv_dim, int max_seq, const int *pos_p, int ntok) {
@@ -1329,7 +1432,15 @@ static void attention(float *ao, float *att, const float *q, const KvView &kv, i
         auto ktile = [&](int tp) { return sizeof(float) * (size_t)tp * (head_dim + 4); };
         auto pick_qb = [&](int tp) { return ktile(tp) + 8 * qtok <= 64 * 1024 ? 8 : ktile(tp) + 4 * qtok <= 64 * 1024 ? 4 : 0; };
         const int tp = pick_qb(AT_T) ? AT_T : AT_T / 2, qb = pick_qb(tp);
-        if (ntok > 1 && window == 0 && qb) {   // prefill: blocks of AT_TB tokens share a K tile
+        if (ntok > 1 && window == 0 && (head_dim == 64 || head_dim == 128)) {   // prefill: register-blocked rows
+            const dim3 rgrid(n_kv_heads, (ntok * group + RB_R - 1) / RB_R, (max_pos + RB_PC * RB_T) / (RB_PC * RB_T));
+            if (head_dim == 64)
+                hipLaunchKernelGGL((k_attn_scores_rb<64, KT>), rgrid, dim3(256), 0, kr_stream(), att, q, kv, group,
+                                   kv_dim, max_seq, scale, pos, ntok);
+            else
+                hipLaunchKernelGGL((k_attn_scores_rb<128, KT>), rgrid, dim3(256), 0, kr_stream(), att, q, kv, group,
+                                   kv_dim, max_seq, scale, pos, ntok);
+        } else if (ntok > 1 && window == 0 && qb) {   // prefill: blocks of AT_TB tokens share a K tile
             const dim3 bgrid(n_kv_heads, (max_pos + tp) / tp, (ntok + AT_TB - 1) / AT_TB);
             const size_t blds = ktile(tp) + qb * qtok;
             auto go = [&](auto kern) {
