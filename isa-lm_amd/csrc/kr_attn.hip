@@ -204,16 +204,19 @@ __global__ void __launch_bounds__(AT_THREADS) k_attn_scores_blk(float *att, cons
 // loads are in flight while a tile is summed.
 constexpr int RB_R = 64, RB_T = 64;   // rows of a register-blocked workgroup; positions of its tiles
 constexpr int RB_PC = 8;             // K tiles per scores workgroup
-template <int HD, int KT>
-__global__ void __launch_bounds__(256) k_attn_scores_rb(float *att, const float *q, const KvView kv, int group,
-                                                        int kv_dim, int max_seq, float scale, const int *pos_p,
-                                                        int ntok) {
+constexpr int RB_NT128 = 512;        // threads of the 128-dim heads' workgroups (4 outputs' rows a lane, LDS for 2
+                                     // workgroups a CU: 4 waves a SIMD; 256 threads gave 2 and measured the same)
+template <int HD, int KT, int NT>
+__global__ void __launch_bounds__(NT) k_attn_scores_rb(float *att, const float *q, const KvView kv, int group,
+                                                       int kv_dim, int max_seq, float scale, const int *pos_p,
+                                                       int ntok) {
     constexpr int S = HD + 4;                     // LDS row stride (floats)
-    constexpr int NL = RB_T * HD / 4 / 256;       // 4-element K loads a thread stages per tile
-    constexpr int NQL = RB_R * HD / 4 / 256;      // query float4 a thread stages
+    constexpr int NPG = NT / 16, PPL = RB_T / NPG;   // position groups; positions a lane (pg + NPG k)
+    constexpr int NL = RB_T * HD / 4 / NT;        // 4-element K loads a thread stages per tile
+    constexpr int NQL = RB_R * HD / 4 / NT;       // query float4 a thread stages
     __shared__ __align__(16) float qs[RB_R * S];
     __shared__ __align__(16) float ks[RB_T * S];
-    const int g = blockIdx.x, tid = threadIdx.x, pg = tid & 15, rg = tid >> 4;
+    const int g = blockIdx.x, tid = threadIdx.x, pg = tid % NPG, rg = tid / NPG;
     const int nrow = ntok * group, R0 = blockIdx.y * RB_R;
     const int pos0 = *pos_p, n_heads = gridDim.x * group;
     const int nlast = pos0 + (min(R0 + RB_R, nrow) - 1) / group + 1;   // positions the block's last row attends
@@ -222,7 +225,7 @@ __global__ void __launch_bounds__(256) k_attn_scores_rb(float *att, const float 
     const int ntl = min(RB_PC, (nlast - p0 + RB_T - 1) / RB_T);
 #pragma unroll
     for (int u = 0; u < NQL; u++) {
-        const int e = tid + 256 * u, rr = e / (HD / 4), c4 = e % (HD / 4);
+        const int e = tid + NT * u, rr = e / (HD / 4), c4 = e % (HD / 4);
         const int R = min(R0 + rr, nrow - 1), z = R / group, j = R - z * group;
         *(float4 *)(qs + rr * S + 4 * c4) = *(const float4 *)(q + ((size_t)z * n_heads + (size_t)g * group + j) * HD + 4 * c4);
     }
@@ -230,7 +233,7 @@ __global__ void __launch_bounds__(256) k_attn_scores_rb(float *att, const float 
     auto load = [&](int t0) {
 #pragma unroll
         for (int u = 0; u < NL; u++) {
-            const int e = tid + 256 * u, p = e / (HD / 4), c4 = e % (HD / 4);
+            const int e = tid + NT * u, p = e / (HD / 4), c4 = e % (HD / 4);
             kr[u] = Kv4<KT>::load(kv.k, (size_t)min(t0 + p, nlast - 1) * kv_dim + (size_t)g * HD + 4 * c4);
         }
     };
@@ -246,40 +249,40 @@ __global__ void __launch_bounds__(256) k_attn_scores_rb(float *att, const float 
         __syncthreads();   // the last tile is read
 #pragma unroll
         for (int u = 0; u < NL; u++) {
-            const int e = tid + 256 * u, p = e / (HD / 4), c4 = e % (HD / 4);
+            const int e = tid + NT * u, p = e / (HD / 4), c4 = e % (HD / 4);
             *(float4 *)(ks + p * S + 4 * c4) = Kv4<KT>::wide(kr[u]);
         }
         __syncthreads();
         if (ti + 1 < ntl) load(t0 + RB_T);
-        float acc[4][4];
+        float acc[4][PPL];
 #pragma unroll
         for (int r = 0; r < 4; r++)
 #pragma unroll
-            for (int k = 0; k < 4; k++) acc[r][k] = 0.0f;
+            for (int k = 0; k < PPL; k++) acc[r][k] = 0.0f;
         const float *qp = qs + 4 * rg * S, *kp = ks + pg * S;
 #pragma unroll 4
         for (int i = 0; i < HD; i += 4) {
-            float4 a[4], b[4];
+            float4 a[4], b[PPL];
 #pragma unroll
             for (int r = 0; r < 4; r++) a[r] = *(const float4 *)(qp + r * S + i);
 #pragma unroll
-            for (int k = 0; k < 4; k++) b[k] = *(const float4 *)(kp + 16 * k * S + i);
+            for (int k = 0; k < PPL; k++) b[k] = *(const float4 *)(kp + NPG * k * S + i);
 #pragma unroll
             for (int r = 0; r < 4; r++)
 #pragma unroll
-                for (int k = 0; k < 4; k++) acc[r][k] = kr_fadd(acc[r][k], kr_fmul(a[r].x, b[k].x));
+                for (int k = 0; k < PPL; k++) acc[r][k] = kr_fadd(acc[r][k], kr_fmul(a[r].x, b[k].x));
 #pragma unroll
             for (int r = 0; r < 4; r++)
 #pragma unroll
-                for (int k = 0; k < 4; k++) acc[r][k] = kr_fadd(acc[r][k], kr_fmul(a[r].y, b[k].y));
+                for (int k = 0; k < PPL; k++) acc[r][k] = kr_fadd(acc[r][k], kr_fmul(a[r].y, b[k].y));
 #pragma unroll
             for (int r = 0; r < 4; r++)
 #pragma unroll
-                for (int k = 0; k < 4; k++) acc[r][k] = kr_fadd(acc[r][k], kr_fmul(a[r].z, b[k].z));
+                for (int k = 0; k < PPL; k++) acc[r][k] = kr_fadd(acc[r][k], kr_fmul(a[r].z, b[k].z));
 #pragma unroll
             for (int r = 0; r < 4; r++)
 #pragma unroll
-                for (int k = 0; k < 4; k++) acc[r][k] = kr_fadd(acc[r][k], kr_fmul(a[r].w, b[k].w));
+                for (int k = 0; k < PPL; k++) acc[r][k] = kr_fadd(acc[r][k], kr_fmul(a[r].w, b[k].w));
         }
 #pragma unroll
         for (int r = 0; r < 4; r++) {
@@ -287,8 +290,8 @@ __global__ void __launch_bounds__(256) k_attn_scores_rb(float *att, const float 
             const int R = R0 + 4 * rg + r, j = R - zr[r] * group;
             float *dst = att + ((size_t)zr[r] * n_heads + (size_t)g * group + j) * max_seq;
 #pragma unroll
-            for (int k = 0; k < 4; k++) {
-                const int p = t0 + pg + 16 * k;
+            for (int k = 0; k < PPL; k++) {
+                const int p = t0 + pg + NPG * k;
                 if (p <= pos0 + zr[r]) dst[p] = kr_fmul(acc[r][k], scale);
             }
         }
@@ -1179,33 +1182,33 @@ __global__ void __launch_bounds__(64 * MK_W) k_attn_mix_blk(float *ao, const flo
 // those terms out of that row's sums, so no weight or V value there (rows of
 // later tokens, stale rows) reaches them. The next tile's loads are in flight
 // while a tile is summed.
-template <int HD, int KT>
-__global__ void __launch_bounds__(256) k_attn_mix_rb(float *ao, const float *att, const KvView kv, int group,
-                                                     int kv_dim, int max_seq, const int *pos_p, int ntok) {
-    constexpr int DPL = HD / 16, NQ = DPL / 4;        // dims a lane, in NQ quads 64 apart
+template <int HD, int KT, int NT>
+__global__ void __launch_bounds__(NT) k_attn_mix_rb(float *ao, const float *att, const KvView kv, int group,
+                                                    int kv_dim, int max_seq, const int *pos_p, int ntok) {
+    constexpr int NDG = NT / 16, DPL = HD / NDG, NQ = DPL / 4;   // dim groups; dims a lane, NQ quads 4 NDG apart
     constexpr int AS = RB_T + 4;                      // weight row stride (floats)
-    constexpr int NA = RB_R * RB_T / 4 / 256;         // 4-weight loads a thread stages per tile
-    constexpr int NV = RB_T * HD / 4 / 256;           // 4-element V loads a thread stages per tile
+    constexpr int NA = RB_R * RB_T / 4 / NT;          // 4-weight loads a thread stages per tile
+    constexpr int NV = RB_T * HD / 4 / NT;            // 4-element V loads a thread stages per tile
     __shared__ __align__(16) float as[RB_R * AS];
     __shared__ __align__(16) float vs[RB_T * HD];
-    const int g = blockIdx.x, tid = threadIdx.x, wave = tid >> 6, dg = tid & 15, rg = tid >> 4;
+    const int g = blockIdx.x, tid = threadIdx.x, wave = tid >> 6, dg = tid % NDG, rg = tid / NDG;
     const int nrow = ntok * group, R0 = (gridDim.y - 1 - blockIdx.y) * RB_R;
     const int pos0 = *pos_p, n_heads = gridDim.x * group;
     const int nlast = pos0 + (min(R0 + RB_R, nrow) - 1) / group + 1;   // positions the block's last row attends
     const int ntl = (nlast + RB_T - 1) / RB_T;
-    const int zw = (R0 + 16 * wave) / group;   // the token of the wave's first row
+    const int zw = (R0 + 4 * (64 / NDG) * wave) / group;   // the token of the wave's first row
     typename Kv4<KT>::T vr[NV];
     float4 ar[NA];
     float dv[NA][4];   // Q8: the V row scales of the staged weights' positions
     auto load = [&](int t0) {
 #pragma unroll
         for (int u = 0; u < NV; u++) {
-            const int e = tid + 256 * u, p = e / (HD / 4), c4 = e % (HD / 4);
+            const int e = tid + NT * u, p = e / (HD / 4), c4 = e % (HD / 4);
             vr[u] = Kv4<KT>::load(kv.v, (size_t)min(t0 + p, nlast - 1) * kv_dim + (size_t)g * HD + 4 * c4);
         }
 #pragma unroll
         for (int u = 0; u < NA; u++) {
-            const int e = tid + 256 * u, rr = e / (RB_T / 4), q4 = e % (RB_T / 4);
+            const int e = tid + NT * u, rr = e / (RB_T / 4), q4 = e % (RB_T / 4);
             const int R = min(R0 + rr, nrow - 1), z = R / group, j = R - z * group;
             ar[u] = *(const float4 *)(att + ((size_t)z * n_heads + (size_t)g * group + j) * max_seq +
                                       min(t0 + 4 * q4, max_seq - 4));
@@ -1226,12 +1229,12 @@ __global__ void __launch_bounds__(256) k_attn_mix_rb(float *ao, const float *att
         __syncthreads();   // the last tile is read
 #pragma unroll
         for (int u = 0; u < NV; u++) {
-            const int e = tid + 256 * u;
+            const int e = tid + NT * u;
             *(float4 *)(vs + 4 * e) = Kv4<KT>::wide(vr[u]);   // [position][dim]: e = p HD / 4 + c4
         }
 #pragma unroll
         for (int u = 0; u < NA; u++) {
-            const int e = tid + 256 * u, rr = e / (RB_T / 4), q4 = e % (RB_T / 4);
+            const int e = tid + NT * u, rr = e / (RB_T / 4), q4 = e % (RB_T / 4);
             float4 a = ar[u];
             if (KT == KV_Q8)
                 a = make_float4(kr_fmul(a.x, dv[u][0]), kr_fmul(a.y, dv[u][1]), kr_fmul(a.z, dv[u][2]),
@@ -1257,7 +1260,7 @@ __global__ void __launch_bounds__(256) k_attn_mix_rb(float *ao, const float *att
                 for (int k = 0; k < 4; k++) {
                     float4 v[NQ];
 #pragma unroll
-                    for (int q = 0; q < NQ; q++) v[q] = *(const float4 *)(vp + (t + k) * HD + 64 * q);
+                    for (int q = 0; q < NQ; q++) v[q] = *(const float4 *)(vp + (t + k) * HD + 4 * NDG * q);
 #pragma unroll
                     for (int r = 0; r < 4; r++) {
                         const float w = k == 0 ? a[r].x : k == 1 ? a[r].y : k == 2 ? a[r].z : a[r].w;
@@ -1286,7 +1289,7 @@ __global__ void __launch_bounds__(256) k_attn_mix_rb(float *ao, const float *att
         float *dst = ao + (size_t)z * n_heads * HD + (size_t)(g * group + j) * HD + 4 * dg;
 #pragma unroll
         for (int q = 0; q < NQ; q++)
-            *(float4 *)(dst + 64 * q) = make_float4(acc[r][4 * q], acc[r][4 * q + 1], acc[r][4 * q + 2], acc[r][4 * q + 3]);
+            *(float4 *)(dst + 4 * NDG * q) = make_float4(acc[r][4 * q], acc[r][4 * q + 1], acc[r][4 * q + 2], acc[r][4 * q + 3]);
     }
 }
 
@@ -1350,11 +1353,11 @@ static void launch_mix(const dim3 &grid, int ntok, float *ao, const float *att, 
         // prefill without a window, 64- or 128-dim heads: register-blocked rows
         const dim3 rgrid(grid.x, (ntok * group + RB_R - 1) / RB_R, 1);
         if (hd == 64)
-            hipLaunchKernelGGL((k_attn_mix_rb<64, KT>), rgrid, dim3(256), 0, kr_stream(), ao, att, kv, group, kv_dim,
-                               max_seq, pos, ntok);
+            hipLaunchKernelGGL((k_attn_mix_rb<64, KT, 256>), rgrid, dim3(256), 0, kr_stream(), ao, att, kv, group,
+                               kv_dim, max_seq, pos, ntok);
         else
-            hipLaunchKernelGGL((k_attn_mix_rb<128, KT>), rgrid, dim3(256), 0, kr_stream(), ao, att, kv, group, kv_dim,
-                               max_seq, pos, ntok);
+            hipLaunchKernelGGL((k_attn_mix_rb<128, KT, RB_NT128>), rgrid, dim3(RB_NT128), 0, kr_stream(), ao, att, kv,
+                               group, kv_dim, max_seq, pos, ntok);
         return;
     }
     if constexpr (DW >= 16) {
@@ -1442,11 +1445,11 @@ static void attention(float *ao, float *att, const float *q, const KvView &kv, i
         if (ntok > 1 && window == 0 && (head_dim == 64 || head_dim == 128)) {   // prefill: register-blocked rows
             const dim3 rgrid(n_kv_heads, (ntok * group + RB_R - 1) / RB_R, (max_pos + RB_PC * RB_T) / (RB_PC * RB_T));
             if (head_dim == 64)
-                hipLaunchKernelGGL((k_attn_scores_rb<64, KT>), rgrid, dim3(256), 0, kr_stream(), att, q, kv, group,
-                                   kv_dim, max_seq, scale, pos, ntok);
+                hipLaunchKernelGGL((k_attn_scores_rb<64, KT, 256>), rgrid, dim3(256), 0, kr_stream(), att, q, kv,
+                                   group, kv_dim, max_seq, scale, pos, ntok);
             else
-                hipLaunchKernelGGL((k_attn_scores_rb<128, KT>), rgrid, dim3(256), 0, kr_stream(), att, q, kv, group,
-                                   kv_dim, max_seq, scale, pos, ntok);
+                hipLaunchKernelGGL((k_attn_scores_rb<128, KT, RB_NT128>), rgrid, dim3(RB_NT128), 0, kr_stream(), att,
+                                   q, kv, group, kv_dim, max_seq, scale, pos, ntok);
         } else if (ntok > 1 && window == 0 && qb) {   // prefill: blocks of AT_TB tokens share a K tile
             const dim3 bgrid(n_kv_heads, (max_pos + tp) / tp, (ntok + AT_TB - 1) / AT_TB);
             const size_t blds = ktile(tp) + qb * qtok;
