@@ -243,6 +243,13 @@ void krh_matmul_qkv_stage(float *q, float *k, float *v, const krh_mat *wq, const
 void krh_attention_batch(float *ao, float *att, const float *q, const float *kc, const float *vc, int n_heads,
                          int n_kv_heads, int head_dim, int max_seq, int window, float scale, const int *pos0, int ntok,
                          int last_pos);
+/* The batched attention's choice of kernels (no counterpart in the
+ * reference): heads of 64 or 128 dims take the register-blocked score and
+ * mix kernels when their rows (token, query head) fill at least min_wg
+ * workgroups of 64 rows, and the per-token-block kernels below that
+ * (default 512). Tests lower it to run the register-blocked kernels on small
+ * shapes; the results are the same bits either way. Process-wide. */
+void krh_set_attn_rb_min(int min_wg);
 /* h = silu(g) * u per token (k_scalar.c:96-98), quantized to Q8_0 with
  * transposed scales dT[b * ldd + t] */
 void krh_silu_quant(int8_t *q, float *dT, int ldd, const float *g, const float *u, int n, int ntok);

@@ -204,6 +204,14 @@ __global__ void __launch_bounds__(AT_THREADS) k_attn_scores_blk(float *att, cons
 // loads are in flight while a tile is summed.
 constexpr int RB_R = 64, RB_T = 64;   // rows of a register-blocked workgroup; positions of its tiles
 constexpr int RB_PC = 8;             // K tiles per scores workgroup
+// the register-blocked kernels take 64- and 128-dim heads whose rows fill at
+// least 512 workgroups (two a CU): a 511-token prompt over 2 KV heads of 7
+// query heads gives 112, and there the per-token-block kernels measured twice
+// as fast (scores 45.6 against 21.6 us a layer, mix 51.2 against 28.5)
+static int g_rb_min_wg = 512;
+static bool rb_shape(int hd, int ntok, int group, int n_kv) {
+    return (hd == 64 || hd == 128) && (long)n_kv * ((ntok * group + RB_R - 1) / RB_R) >= g_rb_min_wg;
+}
 constexpr int RB_NT128 = 512;        // threads of the 128-dim heads' workgroups (4 outputs' rows a lane, LDS for 2
                                      // workgroups a CU: 4 waves a SIMD; 256 threads gave 2 and measured the same)
 template <int HD, int KT, int NT>
@@ -1349,7 +1357,7 @@ template <int KT, int DW>
 static void launch_mix(const dim3 &grid, int ntok, float *ao, const float *att, const KvView &kv, int group, int hd,
                        int kv_dim, int max_seq, int window, const int *pos) {
     const float *vc = (const float *)kv.v;
-    if (ntok > 1 && window == 0 && (hd == 64 || hd == 128) && max_seq % 4 == 0) {
+    if (ntok > 1 && window == 0 && rb_shape(hd, ntok, group, grid.x) && max_seq % 4 == 0) {
         // prefill without a window, 64- or 128-dim heads: register-blocked rows
         const dim3 rgrid(grid.x, (ntok * group + RB_R - 1) / RB_R, 1);
         if (hd == 64)
@@ -1442,7 +1450,7 @@ static void attention(float *ao, float *att, const float *q, const KvView &kv, i
         auto ktile = [&](int tp) { return sizeof(float) * (size_t)tp * (head_dim + 4); };
         auto pick_qb = [&](int tp) { return ktile(tp) + 8 * qtok <= 64 * 1024 ? 8 : ktile(tp) + 4 * qtok <= 64 * 1024 ? 4 : 0; };
         const int tp = pick_qb(AT_T) ? AT_T : AT_T / 2, qb = pick_qb(tp);
-        if (ntok > 1 && window == 0 && (head_dim == 64 || head_dim == 128)) {   // prefill: register-blocked rows
+        if (ntok > 1 && window == 0 && rb_shape(head_dim, ntok, group, n_kv_heads)) {   // prefill: register-blocked rows
             const dim3 rgrid(n_kv_heads, (ntok * group + RB_R - 1) / RB_R, (max_pos + RB_PC * RB_T) / (RB_PC * RB_T));
             if (head_dim == 64)
                 hipLaunchKernelGGL((k_attn_scores_rb<64, KT, 256>), rgrid, dim3(256), 0, kr_stream(), att, q, kv,
@@ -1570,6 +1578,8 @@ extern "C" void krh_attention_noalloc(float *ao, const float *q, const float *kc
     attention<KV_F32>(ao, g_scratch_ptr[dev], q, f32_view(kc, vc), n_heads, n_kv_heads, head_dim, max_seq, window,
                       scale, pos, 1, max_seq - 1);
 }
+
+extern "C" void krh_set_attn_rb_min(int min_wg) { g_rb_min_wg = min_wg < 0 ? 0 : min_wg; }
 
 extern "C" void krh_attention_batch(float *ao, float *att, const float *q, const float *kc, const float *vc,
                                     int n_heads, int n_kv_heads, int head_dim, int max_seq, int window, float scale,

@@ -186,6 +186,7 @@ for name, res, args in [
                                     _P, _P, _P, C.c_int, C.c_int, _P, _P, C.c_int, C.c_int]),
     ("krh_attention_batch", None, [_P, _P, _P, _P, _P, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_float,
                                    _P, C.c_int, C.c_int]),
+    ("krh_set_attn_rb_min", None, [C.c_int]),
     ("krh_silu_quant", None, [_P, _P, C.c_int, _P, _P, C.c_int, C.c_int]),
     ("krh_embed_batch", None, [_P, C.POINTER(KrhMat), _P, C.c_int, C.c_float]),
     ("krh_take_token", None, [_P, _P, _P]), ("krh_advance", None, [_P]),

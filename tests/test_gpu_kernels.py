@@ -1,5 +1,6 @@
 """Parity of each fused HIP kernel with the oracle, bit for bit, through the
 C ABI of libkrafla_hip.so. Needs a gfx950 device."""
+import contextlib
 import ctypes as C
 import os
 
@@ -596,7 +597,28 @@ def test_matmul_qkv_matches_decode(dev, dim, nh, nkv, hd, typ, vtyp, bias):
                                                      # blocks a workgroup), the last ending at row 511
                                                      (8, 8, 64, 37, 90, 0), (16, 8, 128, 0, 33, 0),
                                                      (32, 8, 64, 5, 100, 0), (8, 4, 64, 450, 62, 0)])
-def test_attention_batch_matches_decode(dev, nh, nkv, hd, pos0, T, window):
+@pytest.mark.parametrize("rb", [False, True])
+def test_attention_batch_matches_decode(dev, nh, nkv, hd, pos0, T, window, rb):
+    """rb: the register-blocked kernels forced on (64- and 128-dim heads; at
+    these sizes the launch would take the per-token-block kernels)"""
+    if rb and hd not in (64, 128):
+        pytest.skip("the register-blocked kernels take 64- and 128-dim heads")
+    with rb_forced(rb):
+        attention_batch_case(dev, nh, nkv, hd, pos0, T, window)
+
+
+@contextlib.contextmanager
+def rb_forced(on):
+    """the register-blocked prefill attention kernels for any size while on"""
+    if on:
+        K.hip.krh_set_attn_rb_min(0)
+    try:
+        yield
+    finally:
+        K.hip.krh_set_attn_rb_min(512)
+
+
+def attention_batch_case(dev, nh, nkv, hd, pos0, T, window):
     max_seq = 512
     kvd, qd = nkv * hd, nh * hd
     Q = f32(RNG.normal(0, 1, (T, qd)))
@@ -622,10 +644,17 @@ def test_attention_batch_matches_decode(dev, nh, nkv, hd, pos0, T, window):
 
 
 @pytest.mark.parametrize("nh,nkv,hd", [(32, 8, 128), (8, 8, 64), (16, 8, 64)])
-def test_attention_batch_stale_rows(dev, nh, nkv, hd):
+@pytest.mark.parametrize("rb", [False, True])
+def test_attention_batch_stale_rows(dev, nh, nkv, hd, rb):
     """cache rows past the last token's position and score rows past each
     token's own position hold NaN (rows still to be written, stale scores):
-    the batched attention lets none of them reach a result"""
+    the batched attention lets none of them reach a result (both kernel
+    choices)"""
+    with rb_forced(rb):
+        stale_rows_case(dev, nh, nkv, hd)
+
+
+def stale_rows_case(dev, nh, nkv, hd):
     max_seq, pos0, T = 512, 40, 75
     kvd, qd = nkv * hd, nh * hd
     Q = f32(RNG.normal(0, 1, (T, qd)))

@@ -150,10 +150,19 @@ def test_attention_kv(dev, kv_type, nh, nkv, hd, pos, window):
                                                      (14, 2, 64, 3, 200, 0), (8, 2, 64, 10, 50, 7),
                                                      (8, 4, 256, 5, 40, 0), (4, 1, 256, 100, 30, 64),
                                                      (16, 8, 64, 7, 45, 0), (8, 8, 128, 200, 70, 0)])
-def test_attention_kv_batch(dev, kv_type, nh, nkv, hd, pos0, T, window):
+@pytest.mark.parametrize("rb", [False, True])
+def test_attention_kv_batch(dev, kv_type, nh, nkv, hd, pos0, T, window, rb):
     """batched attention over F16 and Q8 caches against the oracle's per-token
-    attention"""
-    kv_batch_case(dev, kv_type, nh, nkv, hd, pos0, T, window)
+    attention; rb: the register-blocked kernels forced on (64- and 128-dim
+    heads; at these sizes the launch would take the per-token-block kernels)"""
+    if rb and hd not in (64, 128):
+        pytest.skip("the register-blocked kernels take 64- and 128-dim heads")
+    if rb:
+        K.hip.krh_set_attn_rb_min(0)
+    try:
+        kv_batch_case(dev, kv_type, nh, nkv, hd, pos0, T, window)
+    finally:
+        K.hip.krh_set_attn_rb_min(512)
 
 
 @pytest.mark.parametrize("nh,nkv,hd,pos0,T", [(32, 2, 256, 5, 40), (16, 2, 512, 0, 20)])
