@@ -379,6 +379,9 @@ void krh_block_dots(int32_t *s, const krh_mat *W, const int8_t *xq);
  * No counterpart in the reference: a self-check of the kernels' summation. */
 enum { KRH_ORDERED_SUM_MAX = 8192 };
 void krh_ordered_sum(float *out, const float *t, int n, float s0);
+/* The same with fewer reads in flight (256 threads; the prefill softmax's
+ * form for rows of 2049-4096 scores), n in [1, KRH_ORDERED_SUM_MAX]. */
+void krh_ordered_sum_lean(float *out, const float *t, int n, float s0);
 /* The same computed by a workgroup of 1024 threads (the decode softmax's),
  * n in [1, KRH_ORDERED_SUM_MAX]. */
 void krh_ordered_sum_1024(float *out, const float *t, int n, float s0);

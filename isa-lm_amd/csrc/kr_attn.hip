@@ -469,7 +469,7 @@ __global__ void __launch_bounds__(AT_THREADS) k_attn_scores_blk_q8(float *att, c
 // of up to 4096 scores take 256 (the ordered sum needs 4 waves, and a small
 // workgroup lets 8 rows share a CU's LDS and SIMDs).
 constexpr int SMX_THREADS = 1024, AT_CHUNK = 8192;   // the decode launch
-template <int NT, int CH>
+template <int NT, int CH, bool LEAN = false>
 __global__ void __launch_bounds__(NT) k_attn_softmax(float *att, int max_seq, int window, const int *pos_p) {
     constexpr int SMX_THREADS = NT, AT_CHUNK = CH, AT_V = CH / NT;
     __shared__ __align__(16) float es[sc_terms_cap(AT_CHUNK)];
@@ -515,7 +515,7 @@ __global__ void __launch_bounds__(NT) k_attn_softmax(float *att, int max_seq, in
             if (t < n) es[sc_at(t, sh)] = v[k];
         }
         __syncthreads();
-        const float inv = kr_fdiv(1.0f, kr_spec_sum<SMX_THREADS>(es, n, scr));
+        const float inv = kr_fdiv(1.0f, kr_spec_sum<SMX_THREADS, false, false, LEAN>(es, n, scr));
 #pragma unroll
         for (int k = 0; k < AT_V; k++) {
             if (k * SMX_THREADS >= n) break;
@@ -533,7 +533,7 @@ __global__ void __launch_bounds__(NT) k_attn_softmax(float *att, int max_seq, in
             a[c0 + t] = e;
         }
         __syncthreads();
-        sum = kr_spec_sum<SMX_THREADS>(es, cn, scr, sum);   // ends with a barrier: es is free again
+        sum = kr_spec_sum<SMX_THREADS, false, false, LEAN>(es, cn, scr, sum);   // ends with a barrier: es is free again
     }
     const float inv = kr_fdiv(1.0f, sum);
     for (int t = tid; t < n; t += SMX_THREADS) a[t] = kr_fmul(a[t], inv);
@@ -1497,8 +1497,9 @@ static void attention(float *ao, float *att, const float *q, const KvView &kv, i
     if (ntok > 1 && max_pos + 1 > SM_WN / 2 && max_pos + 1 <= 4096) {
         // prefill rows of 2049 to 4096 scores: a 256-thread workgroup each
         // (measured: 1B-shape 4000-token prompt 59.9k -> 61.7k tok/s; rows
-        // up to 2048 run faster one wave each)
-        hipLaunchKernelGGL((k_attn_softmax<256, 4096>), dim3(n_heads, 1, ntok), dim3(256), 0, kr_stream(), att,
+        // up to 2048 run faster one wave each), the ordered sum's lean form
+        // (90 VGPRs against 111: 5 waves a SIMD; 64.5k -> 65.5k)
+        hipLaunchKernelGGL((k_attn_softmax<256, 4096, true>), dim3(n_heads, 1, ntok), dim3(256), 0, kr_stream(), att,
                            max_seq, window, pos);
     } else if (ntok > 1 && max_pos + 1 <= SM_WN / 2) {   // prefill rows of up to 2048 scores: one wave each
         const int tcap = sc_terms_cap(max_pos + 1), scr = (sc_lds_bytes(max_pos + 1, 64) + 15) / 16 * 16;

@@ -200,7 +200,10 @@ __device__ __forceinline__ unsigned sc_rest(const float *t, int sh, int c, int m
 // starts are then not written), else 0. WAVE: the calling wave alone
 // (NT = 64) computes the sum, with wave syncs in place of barriers, for n of
 // at most SC_CPW chunks (4096 terms); the workgroup's other waves take no part.
-template <int NT, bool REC = false, bool WAVE = false>
+// LEAN: fewer reads in flight (4 float4 per estimate batch instead of 16, one
+// block of the chains read ahead instead of three): fewer registers, so more
+// workgroups share a CU where many sums run side by side
+template <int NT, bool REC = false, bool WAVE = false, bool LEAN = false>
 __device__ __forceinline__ float kr_spec_sum(float *t, int n, unsigned char *lds, float s0 = 0.0f,
                                              unsigned *cst = nullptr) {
     constexpr int NW = NT / 64;
@@ -231,12 +234,13 @@ __device__ __forceinline__ float kr_spec_sum(float *t, int n, unsigned char *lds
         // their adds
         const float4 *h = (const float4 *)(tc + (L / 2) * p);
         float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
-        for (int k0 = 0; k0 < L / 8; k0 += 16) {   // L / 8 is a multiple of 16 (L >= 128)
-            float4 v[16];
+        constexpr int EB = LEAN ? 4 : 16;
+        for (int k0 = 0; k0 < L / 8; k0 += EB) {   // L / 8 is a multiple of 16 (L >= 128)
+            float4 v[EB];
 #pragma unroll
-            for (int k = 0; k < 16; k++) v[k] = h[k0 + k];
+            for (int k = 0; k < EB; k++) v[k] = h[k0 + k];
 #pragma unroll
-            for (int k = 0; k < 16; k++) {
+            for (int k = 0; k < EB; k++) {
                 sg |= __float_as_uint(v[k].x) | __float_as_uint(v[k].y) | __float_as_uint(v[k].z) |
                       __float_as_uint(v[k].w);
                 a0 += v[k].x;
@@ -296,7 +300,7 @@ __device__ __forceinline__ float kr_spec_sum(float *t, int n, unsigned char *lds
             bc[q] = ((const float4 *)(tc + 2 * SC_BLK))[q];
         }
         auto block = [&](int blk, const float4 (&cur)[4], float4 (&nxt)[4]) {
-            const float4 *nb4 = (const float4 *)(tc + min(blk + 3, NB - 1) * SC_BLK);
+            const float4 *nb4 = (const float4 *)(tc + min(blk + (LEAN ? 1 : 3), NB - 1) * SC_BLK);
 #pragma unroll
             for (int q = 0; q < 4; q++) nxt[q] = nb4[q];
             __builtin_amdgcn_sched_barrier(0);
@@ -332,11 +336,18 @@ __device__ __forceinline__ float kr_spec_sum(float *t, int n, unsigned char *lds
                 run = true;
             }
         };
-        for (int blk = 0; blk < NB; blk += 4) {   // NB = L / 16 is a multiple of 4 (L >= 128)
-            block(blk, ba, bd);
-            block(blk + 1, bb, ba);
-            block(blk + 2, bc, bb);
-            block(blk + 3, bd, bc);
+        if constexpr (LEAN) {   // two buffers: block blk + 1's reads before block blk's adds
+            for (int blk = 0; blk < NB; blk += 2) {
+                block(blk, ba, bb);
+                block(blk + 1, bb, ba);
+            }
+        } else {
+            for (int blk = 0; blk < NB; blk += 4) {   // NB = L / 16 is a multiple of 4 (L >= 128)
+                block(blk, ba, bd);
+                block(blk + 1, bb, ba);
+                block(blk + 2, bc, bb);
+                block(blk + 3, bd, bc);
+            }
         }
         if (run) {
             if (p == 0) rb[c * SC_NSEG + nseg] = (int)b;

@@ -960,6 +960,14 @@ __global__ void __launch_bounds__(256) k_ordered_sum(float *out, const float *t,
     const float s = kr_spec_sum<256>(os_t, n, (unsigned char *)(os_t + sc_terms_cap(n)), s0);
     if (threadIdx.x == 0) *out = s;
 }
+// the same with fewer reads in flight (the long-row prefill softmax's form)
+__global__ void __launch_bounds__(256) k_ordered_sum_lean(float *out, const float *t, int n, float s0) {
+    extern __shared__ __align__(16) float osl_t[];
+    for (int i = threadIdx.x; i < n; i += 256) osl_t[sc_at(i, sc_log_len(n))] = t[i];
+    __syncthreads();
+    const float s = kr_spec_sum<256, false, false, true>(osl_t, n, (unsigned char *)(osl_t + sc_terms_cap(n)), s0);
+    if (threadIdx.x == 0) *out = s;
+}
 // the same by 1024 threads, the decode softmax's workgroup
 __global__ void __launch_bounds__(1024) k_ordered_sum_1024(float *out, const float *t, int n, float s0) {
     extern __shared__ __align__(16) float osk_t[];
@@ -1328,6 +1336,16 @@ extern "C" void krh_ordered_sum(float *out, const float *t, int n, float s0) {
     const size_t lds = sizeof(float) * (size_t)sc_terms_cap(n) + sc_lds_bytes(n, RN_THREADS);
     hipLaunchKernelGGL(k_ordered_sum, dim3(1), dim3(256), lds, kr_stream(), out, t, n, s0);
     kr_check_launch("ordered_sum");
+}
+
+extern "C" void krh_ordered_sum_lean(float *out, const float *t, int n, float s0) {
+    if (n < 1 || n > KRH_ORDERED_SUM_MAX) {
+        kr_fail(ML_E_SHAPE, "ordered_sum_lean size", hipSuccess);
+        return;
+    }
+    const size_t lds = sizeof(float) * (size_t)sc_terms_cap(n) + sc_lds_bytes(n, RN_THREADS);
+    hipLaunchKernelGGL(k_ordered_sum_lean, dim3(1), dim3(256), lds, kr_stream(), out, t, n, s0);
+    kr_check_launch("ordered_sum_lean");
 }
 
 extern "C" void krh_ordered_sum_1024(float *out, const float *t, int n, float s0) {

@@ -193,6 +193,7 @@ for name, res, args in [
     ("krh_math_batch", None, [C.c_int, _P, _P, _P, C.c_size_t]), ("krh_h2f_batch", None, [_P, _P, C.c_size_t]),
     ("krh_block_dots", None, [_P, C.POINTER(KrhMat), _P]), ("krh_ordered_sum", None, [_P, _P, C.c_int, C.c_float]),
     ("krh_ordered_sum_1024", None, [_P, _P, C.c_int, C.c_float]),
+    ("krh_ordered_sum_lean", None, [_P, _P, C.c_int, C.c_float]),
     ("krh_rmsnorm", None, [_P, _P, _P, C.c_int, C.c_float]), ("krh_add", None, [_P, _P, C.c_int]),
     ("krh_rope", None, [_P, _P, _P, _P, C.c_int, C.c_int, C.c_int]),
     ("krh_silu_mul", None, [_P, _P, C.c_int]), ("krh_gelu_mul", None, [_P, _P, C.c_int]),

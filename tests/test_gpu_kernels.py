@@ -441,6 +441,25 @@ def test_ordered_sum_1024(dev, case, n, s0):
 
 @pytest.mark.parametrize("s0", [0.0, 1234.5678])
 @pytest.mark.parametrize("case", ORDERED_CASES)
+@pytest.mark.parametrize("n", [1, 5, 31, 33, 128, 129, 2047, 2048, 2049, 3000, 4096, 4097, 8192])
+def test_ordered_sum_lean(dev, case, n, s0):
+    """the ordered sum with fewer reads in flight (one chain block read
+    ahead, estimates 4 reads at a time: the long-row prefill softmax's form):
+    the sequential fp32 sum's bits on every case"""
+    t = ordered_terms(case, n)
+    out = dev.zeros(4)
+    K.hip.krh_ordered_sum_lean(out.ptr, dev.put(t).ptr, n, s0)
+    ok()
+    got = out.get(np.float32, 1)[0]
+    want = seq_sum_f32(t, s0)
+    if np.isnan(want):
+        assert np.isnan(got)
+    else:
+        assert bits(np.float32(got)) == bits(np.float32(want)), (got, want)
+
+
+@pytest.mark.parametrize("s0", [0.0, 1234.5678])
+@pytest.mark.parametrize("case", ORDERED_CASES)
 @pytest.mark.parametrize("n", [1, 5, 31, 32, 33, 127, 128, 129, 2047, 2048, 2049, 4095, 4096])
 def test_ordered_sum_wave(dev, case, n, s0):
     """the single-wave mode of the ordered sum (the batched softmax's), run by
