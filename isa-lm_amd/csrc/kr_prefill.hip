@@ -386,9 +386,13 @@ MMat to_mmat(const krh_mat *m) {
 int row_tiles(int rows, int ng) { return (rows + 32 * ng - 1) / (32 * ng); }
 
 // NG for a launch over these row counts and ntt token tiles: 4 when it has
-// at least 3/4 of a 128-row tile per CU, else 2 when it has half a 64-row
-// tile per CU (w1 and w3 at the reference's 128-token steps: its 8B prefill
-// through ml_run 5,674 -> 5,844 tok/s), else 1. Measured (K = 4096, 256
+// at least two 128-row tiles per CU, else 2 when it has half a 64-row tile
+// per CU (w1 and w3 at the reference's 128-token steps: its 8B prefill
+// through ml_run 5,674 -> 5,844 tok/s), else 1. One 128-row tile per CU
+// leaves each SIMD one wave, which issues a VALU instruction only every 6.5
+// cycles or more: the 1B shape's wo and w2 (256 tiles at 2048 tokens) on
+// 64-row tiles took its 4000-token prefill from 65.4k-65.7k to 67.6k-67.8k
+// tok/s (the threshold was 3/4 of a tile per CU). Measured (K = 4096, 256
 // CUs): a 128-row tile does 4 times a 32-row tile's work in 1.9 times its
 // time, so from about 200 tiles, where the 32-row grid needs two rounds of
 // resident workgroups, the 128-row grid's one round is the shorter (14336
@@ -399,7 +403,7 @@ int pick_ng(int rows0, int rows1, int rows2, int ntt) {
     const int tiles = row_tiles(rows0, 4) + row_tiles(rows1, 4) + row_tiles(rows2, 4);
     const int cus = krh_device_cus() > 0 ? krh_device_cus() : 256;
     const int tiles2 = row_tiles(rows0, 2) + row_tiles(rows1, 2) + row_tiles(rows2, 2);
-    return 4L * tiles * ntt >= 3L * cus ? 4 : 2L * tiles2 * ntt >= cus ? 2 : 1;
+    return tiles * ntt >= 2L * cus ? 4 : 2L * tiles2 * ntt >= cus ? 2 : 1;
 }
 
 // Waves per workgroup (TW) for an NG 1 launch whose grid of 128-token tiles
