@@ -392,7 +392,8 @@ int row_tiles(int rows, int ng) { return (rows + 32 * ng - 1) / (32 * ng); }
 // leaves each SIMD one wave, which issues a VALU instruction only every 6.5
 // cycles or more: the 1B shape's wo and w2 (256 tiles at 2048 tokens) on
 // 64-row tiles took its 4000-token prefill from 65.4k-65.7k to 67.6k-67.8k
-// tok/s (the threshold was 3/4 of a tile per CU). Measured (K = 4096, 256
+// tok/s (the threshold was 3/4 of a tile per CU); 64-row tiles up to 3 or 4
+// tiles per CU took the 8B shape's from 21.6k-21.8k to 20.4k-20.5k. Measured (K = 4096, 256
 // CUs): a 128-row tile does 4 times a 32-row tile's work in 1.9 times its
 // time, so from about 200 tiles, where the 32-row grid needs two rounds of
 // resident workgroups, the 128-row grid's one round is the shorter (14336
