@@ -1205,6 +1205,7 @@ __global__ void __launch_bounds__(NT) k_attn_mix_rb(float *ao, const float *att,
     const int nlast = pos0 + (min(R0 + RB_R, nrow) - 1) / group + 1;   // positions the block's last row attends
     const int ntl = (nlast + RB_T - 1) / RB_T;
     const int zw = (R0 + 4 * (64 / NDG) * wave) / group;   // the token of the wave's first row
+    const int zlw = (min(R0 + 4 * (64 / NDG) * (wave + 1), nrow) - 1) / group;   // of its last (within the rows)
     typename Kv4<KT>::T vr[NV];
     float4 ar[NA];
     float dv[NA][4];   // Q8: the V row scales of the staged weights' positions
@@ -1252,42 +1253,49 @@ __global__ void __launch_bounds__(NT) k_attn_mix_rb(float *ao, const float *att,
         __syncthreads();
         if (ti + 1 < ntl) load(t0 + RB_T);
         const float *ap = as + 4 * rg * AS, *vp = vs + 4 * dg;
-        auto run = [&](auto upto) {
+        int lim[4];   // in a masked step: position t0 + k counts for row r iff k <= lim[r]
+#pragma unroll
+        for (int r = 0; r < 4; r++) lim[r] = pos0 + (R0 + 4 * rg + r) / group - t0;
+        // positions t .. t + 3 of the tile, every row's terms (UPTO: each
+        // row's up to its own position)
+        auto step = [&](int t, auto upto) {
             constexpr bool UPTO = decltype(upto)::value;
-            int lim[4];   // UPTO: position t0 + k counts for row r iff k <= lim[r]
-            if (UPTO) {
+            float4 a[4];
 #pragma unroll
-                for (int r = 0; r < 4; r++) lim[r] = pos0 + (R0 + 4 * rg + r) / group - t0;
-            }
-#pragma unroll 2
-            for (int t = 0; t < RB_T; t += 4) {
-                float4 a[4];
+            for (int r = 0; r < 4; r++) a[r] = *(const float4 *)(ap + r * AS + t);
 #pragma unroll
-                for (int r = 0; r < 4; r++) a[r] = *(const float4 *)(ap + r * AS + t);
+            for (int k = 0; k < 4; k++) {
+                float4 v[NQ];
 #pragma unroll
-                for (int k = 0; k < 4; k++) {
-                    float4 v[NQ];
+                for (int q = 0; q < NQ; q++) v[q] = *(const float4 *)(vp + (t + k) * HD + 4 * NDG * q);
 #pragma unroll
-                    for (int q = 0; q < NQ; q++) v[q] = *(const float4 *)(vp + (t + k) * HD + 4 * NDG * q);
+                for (int r = 0; r < 4; r++) {
+                    const float w = k == 0 ? a[r].x : k == 1 ? a[r].y : k == 2 ? a[r].z : a[r].w;
+                    const bool in = !UPTO || t + k <= lim[r];
 #pragma unroll
-                    for (int r = 0; r < 4; r++) {
-                        const float w = k == 0 ? a[r].x : k == 1 ? a[r].y : k == 2 ? a[r].z : a[r].w;
-                        const bool in = !UPTO || t + k <= lim[r];
-#pragma unroll
-                        for (int q = 0; q < NQ; q++) {
-                            const float4 x = v[q];
-                            float *o = acc[r] + 4 * q;
-                            o[0] = in ? kr_fadd(o[0], kr_fmul(w, x.x)) : o[0];
-                            o[1] = in ? kr_fadd(o[1], kr_fmul(w, x.y)) : o[1];
-                            o[2] = in ? kr_fadd(o[2], kr_fmul(w, x.z)) : o[2];
-                            o[3] = in ? kr_fadd(o[3], kr_fmul(w, x.w)) : o[3];
-                        }
+                    for (int q = 0; q < NQ; q++) {
+                        const float4 x = v[q];
+                        float *o = acc[r] + 4 * q;
+                        o[0] = in ? kr_fadd(o[0], kr_fmul(w, x.x)) : o[0];
+                        o[1] = in ? kr_fadd(o[1], kr_fmul(w, x.y)) : o[1];
+                        o[2] = in ? kr_fadd(o[2], kr_fmul(w, x.z)) : o[2];
+                        o[3] = in ? kr_fadd(o[3], kr_fmul(w, x.w)) : o[3];
                     }
                 }
             }
         };
-        if (t0 + RB_T - 1 <= pos0 + zw) run(std::false_type{});   // every position counts for every row of the wave
-        else run(std::true_type{});
+        if (t0 + RB_T - 1 <= pos0 + zw) {   // every position counts for every row of the wave
+#pragma unroll 2
+            for (int t = 0; t < RB_T; t += 4) step(t, std::false_type{});
+        } else {
+            // the tile that holds the wave's own positions: whole steps below
+            // its first row's position, masked steps up to its last row's
+            const int full = pos0 + zw - t0, any = pos0 + zlw - t0;
+            for (int t = 0; t < RB_T && t <= any; t += 4) {
+                if (t + 3 <= full) step(t, std::false_type{});
+                else step(t, std::true_type{});
+            }
+        }
     }
 #pragma unroll
     for (int r = 0; r < 4; r++) {
