@@ -140,8 +140,15 @@ __device__ __forceinline__ void w_store(MmLds<NG, TT> &L, int st, const WReg &R,
     if ((tid & 1) == 0) L.d[st][tid >> 1] = R.d;
 }
 
-// The MFMA of row group g + 1 is issued before the rescale of group g, so
-// its latency runs under that VALU work. The 16 token scales a lane needs
+// Row group g + 1's MFMA is issued after the whole rescale of group g: an
+// empty asm takes every rescaled value of group g as input and the MFMA's
+// weight operand as in-out, so only one 16-register result set is live.
+// Left to itself the compiler issues all NG MFMAs of a step together and
+// holds NG result sets (64 VGPRs at NG 4: 183 VGPRs, 2 waves per SIMD);
+// with one set the kernel takes 146 VGPRs and runs 3 waves per SIMD, whose
+// interleaving hides the MFMA latency the wave itself now waits out (8B-shape
+// prefill 22.0k -> 23.0k tok/s; an MFMA lookahead of half a group, or 4
+// waves per SIMD, spills). The 16 token scales a lane needs
 // (tokens 8 (r / 4) + 4 (lane / 32) + r % 4 of the wave's 32: the same for
 // the 32 lanes of a half-wave) are four 16-byte LDS broadcast reads of the
 // tile's token scales (16 cross-lane shuffles of one loaded scale per lane
@@ -171,16 +178,16 @@ __device__ __forceinline__ void mm_step(float (&acc)[NG][16], const XFrag &f, co
     v16i s = __builtin_amdgcn_mfma_i32_32x32x32_i8(f.xa, wb[0], v16i{}, 0, 0, 0);
 #pragma unroll
     for (int g = 0; g < NG; g++) {
-        v16i sn;
-        if (g + 1 < NG) sn = __builtin_amdgcn_mfma_i32_32x32x32_i8(f.xa, wb[g + 1], v16i{}, 0, 0, 0);
-        // keeps the next MFMA from being hoisted further: two result sets
-        // live instead of four
-        __builtin_amdgcn_sched_barrier(0);
         const float wd = D16 ? kr_h2f((uint16_t)wdr[g]) : __uint_as_float(wdr[g]);
 #pragma unroll
         for (int r = 0; r < 16; r++)
             acc[g][r] = kr_fadd(acc[g][r], kr_fmul(kr_fmul((float)s[r], wd), xd[r]));
-        if (g + 1 < NG) s = sn;
+        if (g + 1 < NG) {
+            v4i w = wb[g + 1];
+#pragma unroll
+            for (int r = 0; r < 16; r++) asm volatile("" : "+v"(w) : "v"(acc[g][r]));
+            s = __builtin_amdgcn_mfma_i32_32x32x32_i8(f.xa, w, v16i{}, 0, 0, 0);
+        }
     }
 }
 
@@ -192,7 +199,7 @@ __device__ __forceinline__ void mm_step(float (&acc)[NG][16], const XFrag &f, co
 // during step b into the stage step b - 2 read, and the barrier closing each
 // step orders those stores before step b + 1 reads them.
 template <int EPI, int QT, int D16, int NG, int TW = 4>
-__global__ void __launch_bounds__(64 * TW, 2) k_matmul(const MmArgs a) {   // 2: waves per SIMD, at least
+__global__ void __launch_bounds__(64 * TW, 3) k_matmul(const MmArgs a) {   // 3: waves per SIMD, at least
     constexpr int TT = 32 * TW;   // tokens per workgroup
     __shared__ MmLds<NG, TT> L;
     int mi = 0;
